@@ -1,0 +1,120 @@
+/*
+ * w4a16_hip.h -- C ABI of the MI355X (gfx950) W4A16 linear-layer library.
+ *
+ * FP16 activations [M, K] times packed INT4 weights [N, K/2] (two's complement
+ * nibbles, even k in the low nibble) with one FP16 scale per `group_size`
+ * weights along K, giving FP16 output [M, N]:
+ *
+ *     out[m][n] = fp16_rn( sum_k fp32(x[m][k]) * code[n][k] * fp32(scale[n][k / group_size]) )
+ *
+ * All pointers are device pointers; nothing here allocates, synchronises or
+ * keeps state between calls, so every entry point is safe inside HIP graph
+ * capture. Work is enqueued on `stream` (a hipStream_t; NULL = legacy stream).
+ *
+ * Return value: W4A16_OK (0) or one of the W4A16_ERR_* codes below;
+ * w4a16_last_error() returns the message of the most recent failure on the
+ * calling thread.
+ */
+#ifndef W4A16_HIP_H
+#define W4A16_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_OK 0
+#define W4A16_ERR_GROUP_SIZE 1       /* group_size <= 0, odd, or not a multiple of 32 (dequantize) */
+#define W4A16_ERR_SHAPE 2            /* inconsistent M/N/K/scale shapes */
+#define W4A16_ERR_ALIGNMENT 3        /* pointer alignment the entry point requires is not met */
+#define W4A16_ERR_NULL 4             /* NULL pointer with non-empty work */
+#define W4A16_ERR_CONFIG 5           /* bad environment selector or tuning argument */
+#define W4A16_ERR_LAUNCH 6           /* HIP reported an error at launch */
+#define W4A16_ERR_TOO_LARGE 7        /* a dimension exceeds what the kernels index */
+
+/* Kernel families, as reported by w4a16_plan_linear / accepted by w4a16_linear_f16_tuned. */
+#define W4A16_KERNEL_NONE 0          /* M*N == 0: nothing launched */
+#define W4A16_KERNEL_VALU 1          /* VALU dot2 GEMV, activations staged in LDS (M <= 8) */
+#define W4A16_KERNEL_MFMA 2          /* fp16 MFMA 16x16x32 tiles, M zero-padded to 16 (M <= 8) */
+#define W4A16_KERNEL_GENERIC 3       /* any M, any even group_size, any alignment */
+
+/*
+ * Fused W4A16 linear layer.
+ * Replaces int4_linear_cuda (reference csrc/int4_linear_kernel.cu:641-802),
+ * registered as torch op w4a16::linear (reference csrc/int4_linear.cpp:16-28).
+ * activations: fp16 [M, K] row-major; packed_weights: uint8 [N, K/2];
+ * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
+ * group_size == 128 with 16-byte aligned activations and weights and M <= 8
+ * takes the tuned kernels; anything else takes the generic kernel.
+ * Environment, read at every call: W4A16_DECODE = auto|valu|mfma selects the
+ * kernel family for M <= 8; W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per
+ * workgroup of the VALU kernel (any other value is W4A16_ERR_CONFIG).
+ */
+int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights,
+                     const void* scales, void* output, int64_t M, int64_t N,
+                     int64_t K, int64_t group_size, void* stream);
+
+/*
+ * Dequantize packed INT4 weights to fp16 [N, K]: out = fp16_rn(code * scale),
+ * bit-identical to reference w4a16/reference.py:6-46 followed by .to(float16).
+ * Replaces int4_dequantize_cuda (reference csrc/int4_linear_kernel.cu:805-867),
+ * registered as torch op w4a16::dequantize (reference csrc/int4_linear.cpp:20-23).
+ * Requires group_size a positive multiple of 32 and 16-byte aligned weights,
+ * as the reference does.
+ */
+int w4a16_dequantize_f16(const uint8_t* packed_weights, const void* scales,
+                         void* output, int64_t N, int64_t K, int64_t group_size,
+                         void* stream);
+
+/*
+ * Shape validator shared by the torch op and host-only tests. Arguments are
+ * the sizes the three tensors carry. Returns W4A16_OK or an error code whose
+ * w4a16_last_error() text matches the reference's TORCH_CHECK messages
+ * (reference csrc/int4_linear_kernel.cu:671-691).
+ */
+int w4a16_check_linear_shapes(int64_t act_rows, int64_t act_cols,
+                              int64_t packed_rows, int64_t packed_cols,
+                              int64_t scale_rows, int64_t scale_cols,
+                              int64_t group_size);
+
+/* Same for dequantize (reference csrc/int4_linear_kernel.cu:826-841). */
+int w4a16_check_dequantize_shapes(int64_t packed_rows, int64_t packed_cols,
+                                  int64_t scale_rows, int64_t scale_cols,
+                                  int64_t group_size, uint64_t packed_address);
+
+/*
+ * Which kernel and launch shape w4a16_linear_f16 would use for these
+ * arguments (reads the same environment selectors). Pointers are used only
+ * for their alignment. No reference counterpart: it exposes the dispatcher's
+ * choice (reference csrc/int4_linear_kernel.cu:706-798) to tests and benches.
+ */
+int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
+                      int64_t M, int64_t N, int64_t K, int64_t group_size,
+                      int* kernel, int* rows, int* splits, int* unroll);
+
+/*
+ * w4a16_linear_f16 with an explicit kernel family and launch shape, for
+ * tuning sweeps. kernel: W4A16_KERNEL_VALU (rows 1|2|4, splits 1..8,
+ * unroll 1|2), W4A16_KERNEL_MFMA (rows = 16-row blocks per wave 1|2|4,
+ * splits 1..8, unroll 1|2|4) or W4A16_KERNEL_GENERIC (other arguments
+ * ignored). The VALU and MFMA families need group_size 128, M <= 8 and
+ * 16-byte aligned activations and weights. No reference counterpart (the
+ * reference's W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
+ */
+int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,
+                           const void* scales, void* output, int64_t M, int64_t N,
+                           int64_t K, int64_t group_size, void* stream,
+                           int kernel, int rows, int splits, int unroll);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* w4a16_last_error(void);
+
+/* Library version string. */
+const char* w4a16_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_HIP_H */

@@ -1,0 +1,148 @@
+"""ctypes binding of the C ABI in ``include/w4a16_hip.h`` (``libw4a16_hip.so``).
+
+This is the binding a non-torch caller would write; the torch ops in
+``nibble_amd._C`` call the same entry points from C++. torch is imported
+first so that the library binds to the HIP runtime torch already loaded
+(both resolve the same ``libamdhip64.so.7`` soname).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads the process's HIP runtime before the library)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libw4a16_hip.so")
+
+W4A16_OK = 0
+W4A16_ERR_GROUP_SIZE = 1
+W4A16_ERR_SHAPE = 2
+W4A16_ERR_ALIGNMENT = 3
+W4A16_ERR_NULL = 4
+W4A16_ERR_CONFIG = 5
+W4A16_ERR_LAUNCH = 6
+W4A16_ERR_TOO_LARGE = 7
+
+KERNEL_NONE = 0
+KERNEL_VALU = 1
+KERNEL_MFMA = 2
+KERNEL_GENERIC = 3
+KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic"}
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes); every symbol declared in include/w4a16_hip.h
+SIGNATURES = {
+    "w4a16_linear_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "w4a16_dequantize_f16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "w4a16_check_linear_shapes": (ctypes.c_int, [_i64] * 7),
+    "w4a16_check_dequantize_shapes": (ctypes.c_int, [_i64] * 5 + [ctypes.c_uint64]),
+    "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip]),
+    "w4a16_linear_f16_tuned": (
+        ctypes.c_int,
+        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
+    ),
+    "w4a16_last_error": (ctypes.c_char_p, []),
+    "w4a16_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+class W4A16Error(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load ``libw4a16_hip.so`` (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+            )
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().w4a16_last_error().decode()
+
+
+def _raise_on(code: int) -> None:
+    if code != W4A16_OK:
+        raise W4A16Error(code, last_error())
+
+
+def _stream_ptr(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream)
+
+
+def linear_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None) -> None:
+    """Run ``w4a16_linear_f16`` on torch device tensors (no checks beyond the C ABI's)."""
+    m, k = activations.shape
+    n = packed_weights.shape[0]
+    _raise_on(
+        lib().w4a16_linear_f16(
+            activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
+            m, n, k, group_size, _stream_ptr(stream),
+        )
+    )
+
+
+def linear_f16_tuned(activations, packed_weights, scales, output, group_size, kernel, rows, splits, unroll,
+                     stream=None) -> None:
+    m, k = activations.shape
+    n = packed_weights.shape[0]
+    _raise_on(
+        lib().w4a16_linear_f16_tuned(
+            activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
+            m, n, k, group_size, _stream_ptr(stream), kernel, rows, splits, unroll,
+        )
+    )
+
+
+def dequantize_f16(packed_weights, scales, output, group_size: int = 128, stream=None) -> None:
+    n, kh = packed_weights.shape
+    _raise_on(
+        lib().w4a16_dequantize_f16(
+            packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(), n, 2 * kh, group_size,
+            _stream_ptr(stream),
+        )
+    )
+
+
+def plan_linear(act_ptr: int, packed_ptr: int, m: int, n: int, k: int, group_size: int = 128) -> dict:
+    """The dispatcher's choice for these sizes/alignments (host-only, no GPU needed)."""
+    out = [ctypes.c_int(0) for _ in range(4)]
+    _raise_on(
+        lib().w4a16_plan_linear(act_ptr, packed_ptr, m, n, k, group_size, *[ctypes.byref(v) for v in out])
+    )
+    kernel, rows, splits, unroll = (v.value for v in out)
+    return {"kernel": KERNEL_NAMES[kernel], "rows": rows, "splits": splits, "unroll": unroll}
+
+
+def check_linear_shapes(act_rows, act_cols, packed_rows, packed_cols, scale_rows, scale_cols, group_size):
+    code = lib().w4a16_check_linear_shapes(
+        act_rows, act_cols, packed_rows, packed_cols, scale_rows, scale_cols, group_size
+    )
+    return code, (last_error() if code else "")
+
+
+def check_dequantize_shapes(packed_rows, packed_cols, scale_rows, scale_cols, group_size, address=0):
+    code = lib().w4a16_check_dequantize_shapes(packed_rows, packed_cols, scale_rows, scale_cols, group_size,
+                                               address)
+    return code, (last_error() if code else "")

@@ -1,0 +1,353 @@
+// Host side of the W4A16 C ABI (include/w4a16_hip.h): validation, kernel
+// selection and launch on the caller's stream. Nothing here allocates device
+// memory or synchronises, so every entry point can run under HIP graph
+// capture.
+#include "w4a16_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <set>
+#include <string>
+
+#include "w4a16_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+    g_last_error = message;
+    return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kMaxLdsBytes = 160 * 1024;   // gfx950 LDS per workgroup
+constexpr int kDefaultLdsBytes = 64 * 1024;
+
+// Raise a kernel's dynamic-LDS limit above the 64 KiB default once.
+int ensure_lds(const void* kernel, int bytes) {
+    if (bytes <= kDefaultLdsBytes) return W4A16_OK;
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;  // (kernel, device)
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return fail(W4A16_ERR_LAUNCH, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({kernel, device})) return W4A16_OK;
+    const hipError_t e =
+        hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes);
+    if (e != hipSuccess)
+        return fail(W4A16_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    done.insert({kernel, device});
+    return W4A16_OK;
+}
+
+int check_launch() {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
+struct Plan {
+    int kernel = W4A16_KERNEL_NONE;
+    int rows = 0;    // VALU: output rows per workgroup; MFMA: 16-row blocks per wavefront
+    int splits = 0;  // wavefronts per workgroup splitting K
+    int unroll = 0;  // chunks (VALU) or groups (MFMA) in flight per wavefront step
+};
+
+int valu_lds_bytes(int64_t M, int64_t K, const Plan& p) {
+    return (int)(M * K * 2 + (int64_t)p.splits * p.rows * M * 4);
+}
+int mfma_lds_bytes(const Plan& p) { return p.splits > 1 ? p.splits * p.rows * 64 * 16 : 0; }
+
+// Environment selectors, read at every call (as reference
+// csrc/int4_linear_kernel.cu:464-491 does) so tests can switch them.
+int read_env(int* family, int* rows_per_wave) {
+    *family = 0;  // auto
+    const char* d = std::getenv("W4A16_DECODE");
+    if (d != nullptr && d[0] != '\0') {
+        if (std::strcmp(d, "auto") == 0) *family = 0;
+        else if (std::strcmp(d, "valu") == 0) *family = W4A16_KERNEL_VALU;
+        else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
+        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, or mfma");
+    }
+    *rows_per_wave = 0;
+    const char* r = std::getenv("W4A16_ROWS_PER_WARP");
+    if (r != nullptr) {
+        const int v = std::atoi(r);
+        if (!(v == 1 || v == 2 || v == 4)) return fail(W4A16_ERR_CONFIG, "W4A16_ROWS_PER_WARP must be 1, 2, or 4");
+        *rows_per_wave = v;
+    }
+    return W4A16_OK;
+}
+
+int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+Plan plan_valu(int64_t M, int64_t N, int64_t K, int rows) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_VALU;
+    p.rows = rows ? rows : 2;
+    const int64_t chunks = K / 32;
+    p.splits = clampi((int)(chunks / 128), 1, 8);
+    p.unroll = (chunks >= 2 * 64 * p.splits) ? 2 : 1;
+    (void)M;
+    (void)N;
+    return p;
+}
+
+Plan plan_mfma(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_MFMA;
+    p.rows = 2;
+    const int64_t groups = K / 128;
+    p.splits = clampi((int)(groups / 4), 1, 8);
+    p.unroll = 2;
+    (void)M;
+    (void)N;
+    return p;
+}
+
+int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
+    int family = 0, rows = 0;
+    const int rc = read_env(&family, &rows);
+    if (rc != W4A16_OK) return rc;
+    if (M * N == 0) {
+        *out = Plan();
+        return W4A16_OK;
+    }
+    const bool tuned = G == 128 && M <= 8 && aligned16(act) && aligned16(packed);
+    if (!tuned) {
+        Plan p;
+        p.kernel = W4A16_KERNEL_GENERIC;
+        p.rows = 4;
+        p.splits = 1;
+        p.unroll = 1;
+        *out = p;
+        return W4A16_OK;
+    }
+    if (family == 0) family = (M == 1) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
+    if (family == W4A16_KERNEL_VALU) {
+        Plan p = plan_valu(M, N, K, rows);
+        if (valu_lds_bytes(M, K, p) <= kMaxLdsBytes) {
+            *out = p;
+            return W4A16_OK;
+        }
+        // activations do not fit in LDS: the MFMA kernel reads them from memory
+    }
+    *out = plan_mfma(M, N, K);
+    return W4A16_OK;
+}
+
+template <int M>
+int launch_valu_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                  w4a16::f16* o, int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    const void* fn = nullptr;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int) = nullptr;
+#define W4A16_PICK(R, U) \
+    if (p.rows == R && p.unroll == U) kern = gemv_valu<M, R, U>;
+    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(4, 1) W4A16_PICK(4, 2)
+#undef W4A16_PICK
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "VALU kernel: rows must be 1, 2, or 4 and unroll 1 or 2");
+    fn = reinterpret_cast<const void*>(kern);
+    const int lds = valu_lds_bytes(M, K, p);
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "VALU kernel: M*K activations do not fit in LDS");
+    int rc = ensure_lds(fn, lds);
+    if (rc != W4A16_OK) return rc;
+    const int blocks = (N + p.rows - 1) / p.rows;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K);
+    return check_launch();
+}
+
+int launch_valu(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                w4a16::f16* o, int N, int K, hipStream_t stream) {
+    switch (M) {
+        case 1: return launch_valu_m<1>(p, x, w, s, o, N, K, stream);
+        case 2: return launch_valu_m<2>(p, x, w, s, o, N, K, stream);
+        case 3: return launch_valu_m<3>(p, x, w, s, o, N, K, stream);
+        case 4: return launch_valu_m<4>(p, x, w, s, o, N, K, stream);
+        case 5: return launch_valu_m<5>(p, x, w, s, o, N, K, stream);
+        case 6: return launch_valu_m<6>(p, x, w, s, o, N, K, stream);
+        case 7: return launch_valu_m<7>(p, x, w, s, o, N, K, stream);
+        case 8: return launch_valu_m<8>(p, x, w, s, o, N, K, stream);
+        default: return fail(W4A16_ERR_CONFIG, "VALU kernel needs 1 <= M <= 8");
+    }
+}
+
+int launch_mfma(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                w4a16::f16* o, int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
+#define W4A16_PICK(RB, U) \
+    if (p.rows == RB && p.unroll == U) kern = gemv_mfma<RB, U>;
+    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4)
+    W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4)
+    W4A16_PICK(4, 1) W4A16_PICK(4, 2) W4A16_PICK(4, 4)
+#undef W4A16_PICK
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "MFMA kernel: rows must be 1, 2, or 4 and unroll 1, 2, or 4");
+    if (M < 1 || M > 8) return fail(W4A16_ERR_CONFIG, "MFMA kernel needs 1 <= M <= 8");
+    const int lds = mfma_lds_bytes(p);
+    const int blocks = (N + 16 * p.rows - 1) / (16 * p.rows);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, M, N, K);
+    return check_launch();
+}
+
+int launch_generic(int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s, w4a16::f16* o,
+                   int N, int K, int G, hipStream_t stream) {
+    const int blocks = (N + 3) / 4;
+    hipLaunchKernelGGL(w4a16::linear_generic, dim3(blocks), dim3(256), 0, stream, x, w, s, o, M, N, K, G);
+    return check_launch();
+}
+
+int check_scalar_args(int64_t M, int64_t N, int64_t K, int64_t G) {
+    if (G <= 0) return fail(W4A16_ERR_GROUP_SIZE, "group_size must be greater than zero");
+    if (G % 2 != 0) return fail(W4A16_ERR_GROUP_SIZE, "group_size must be even because each byte contains two weights");
+    if (M < 0 || N < 0 || K < 0) return fail(W4A16_ERR_SHAPE, "M, N and K must be non-negative");
+    if (K % G != 0) return fail(W4A16_ERR_SHAPE, "K must be divisible by group_size");
+    if (M > INT32_MAX || N > INT32_MAX || K > (int64_t)1 << 30)
+        return fail(W4A16_ERR_TOO_LARGE, "M, N or K exceeds the kernels' 32-bit indexing");
+    return W4A16_OK;
+}
+
+int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* scales, void* out,
+             int64_t M, int64_t N, int64_t K, int64_t G, void* stream) {
+    using w4a16::f16;
+    const f16* x = static_cast<const f16*>(act);
+    const f16* s = static_cast<const f16*>(scales);
+    f16* o = static_cast<f16*>(out);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (p.kernel) {
+        case W4A16_KERNEL_NONE: return W4A16_OK;
+        case W4A16_KERNEL_VALU: return launch_valu(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_MFMA: return launch_mfma(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
+        default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
+    }
+}
+
+int check_pointers(const void* act, const void* packed, const void* scales, const void* out) {
+    if (act == nullptr || packed == nullptr || scales == nullptr || out == nullptr)
+        return fail(W4A16_ERR_NULL, "activations, packed_weights, scales and output must be non-NULL");
+    if ((reinterpret_cast<uintptr_t>(act) & 1u) || (reinterpret_cast<uintptr_t>(scales) & 1u) ||
+        (reinterpret_cast<uintptr_t>(out) & 1u))
+        return fail(W4A16_ERR_ALIGNMENT, "fp16 buffers must be 2-byte aligned");
+    return W4A16_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* w4a16_last_error(void) { return g_last_error.c_str(); }
+
+const char* w4a16_version(void) { return "w4a16-hip 0.1.0 (gfx950)"; }
+
+int w4a16_check_linear_shapes(int64_t act_rows, int64_t act_cols, int64_t packed_rows,
+                              int64_t packed_cols, int64_t scale_rows, int64_t scale_cols,
+                              int64_t group_size) {
+    if (group_size <= 0) return fail(W4A16_ERR_GROUP_SIZE, "group_size must be greater than zero");
+    if (group_size % 2 != 0)
+        return fail(W4A16_ERR_GROUP_SIZE, "group_size must be even because each byte contains two weights");
+    if (act_rows < 0 || act_cols < 0 || packed_rows < 0 || packed_cols < 0 || scale_rows < 0 || scale_cols < 0)
+        return fail(W4A16_ERR_SHAPE, "tensor sizes must be non-negative");
+    if (packed_cols * 2 != act_cols)
+        return fail(W4A16_ERR_SHAPE, "packed_weights and activations must describe the same K dimension");
+    if (act_cols % group_size != 0) return fail(W4A16_ERR_SHAPE, "K must be divisible by group_size");
+    if (scale_rows != packed_rows || scale_cols != act_cols / group_size)
+        return fail(W4A16_ERR_SHAPE, "scales must have shape [N, K / group_size]");
+    return W4A16_OK;
+}
+
+int w4a16_check_dequantize_shapes(int64_t packed_rows, int64_t packed_cols, int64_t scale_rows,
+                                  int64_t scale_cols, int64_t group_size, uint64_t packed_address) {
+    if (group_size <= 0 || group_size % 32 != 0)
+        return fail(W4A16_ERR_GROUP_SIZE, "dequantize needs group_size to be a positive multiple of 32");
+    if (packed_address % 16 != 0) return fail(W4A16_ERR_ALIGNMENT, "packed_weights must be 16-byte aligned");
+    if (packed_rows < 0 || packed_cols < 0 || scale_rows < 0 || scale_cols < 0)
+        return fail(W4A16_ERR_SHAPE, "tensor sizes must be non-negative");
+    const int64_t K = packed_cols * 2;
+    if (K % group_size != 0) return fail(W4A16_ERR_SHAPE, "K must be divisible by group_size");
+    if (scale_rows != packed_rows || scale_cols != K / group_size)
+        return fail(W4A16_ERR_SHAPE, "scales must have shape [N, K / group_size]");
+    return W4A16_OK;
+}
+
+int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N,
+                      int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll) {
+    int rc = check_scalar_args(M, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    Plan p;
+    rc = make_plan(activations, packed_weights, M, N, K, group_size, &p);
+    if (rc != W4A16_OK) return rc;
+    if (kernel) *kernel = p.kernel;
+    if (rows) *rows = p.rows;
+    if (splits) *splits = p.splits;
+    if (unroll) *unroll = p.unroll;
+    return W4A16_OK;
+}
+
+int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
+                     void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream) {
+    int rc = check_scalar_args(M, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    Plan p;
+    rc = make_plan(activations, packed_weights, M, N, K, group_size, &p);
+    if (rc != W4A16_OK) return rc;
+    if (p.kernel == W4A16_KERNEL_NONE) return W4A16_OK;
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
+}
+
+int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights, const void* scales,
+                           void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream,
+                           int kernel, int rows, int splits, int unroll) {
+    int rc = check_scalar_args(M, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    if (M * N == 0) return W4A16_OK;
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    Plan p;
+    p.kernel = kernel;
+    p.rows = rows;
+    p.splits = splits;
+    p.unroll = unroll;
+    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA) {
+        if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
+        if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
+    } else if (kernel != W4A16_KERNEL_GENERIC) {
+        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _MFMA or _GENERIC");
+    }
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
+}
+
+int w4a16_dequantize_f16(const uint8_t* packed_weights, const void* scales, void* output, int64_t N,
+                         int64_t K, int64_t group_size, void* stream) {
+    if (N < 0 || K < 0 || K % 2 != 0) return fail(W4A16_ERR_SHAPE, "N and K must be non-negative and K even");
+    int rc = w4a16_check_dequantize_shapes(N, K / 2, N, group_size > 0 ? K / group_size : 0, group_size,
+                                           reinterpret_cast<uintptr_t>(packed_weights));
+    if (rc != W4A16_OK) return rc;
+    const int64_t chunks = N * K / 32;
+    if (chunks == 0) return W4A16_OK;
+    if (packed_weights == nullptr || scales == nullptr || output == nullptr)
+        return fail(W4A16_ERR_NULL, "packed_weights, scales and output must be non-NULL");
+    if (reinterpret_cast<uintptr_t>(output) & 15u) return fail(W4A16_ERR_ALIGNMENT, "output must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(scales) & 1u) return fail(W4A16_ERR_ALIGNMENT, "scales must be 2-byte aligned");
+    if (K / 32 > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "K too large");
+    const int64_t blocks = (chunks + 255) / 256;
+    if (blocks > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "too many chunks for one launch");
+    hipLaunchKernelGGL(w4a16::dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), packed_weights, static_cast<const w4a16::f16*>(scales),
+                       static_cast<w4a16::f16*>(output), chunks, (int)(K / 32), (int)(group_size / 32),
+                       (int)(K / group_size));
+    return check_launch();
+}
+
+}  // extern "C"

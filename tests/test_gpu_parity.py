@@ -1,0 +1,148 @@
+"""GPU parity of the HIP kernels, called through the C ABI (ctypes), against
+the CPU oracle. Bar: |err| <= 1e-2 (1 + |ref|) for the linear layer, bit
+identity for dequantize."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nibble_amd import _lib
+from tests._cases import assert_parity, expected, make_case
+
+pytestmark = pytest.mark.gpu
+
+VALU, MFMA, GENERIC = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC
+
+
+def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, group_size=128):
+    xd, pd, sd = x.to(dev), packed.to(dev), scales.to(dev)
+    out = torch.full((x.shape[0], packed.shape[0]), float("nan"), dtype=torch.float16, device=dev)
+    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} M={x.shape[0]} "
+          f"K={x.shape[1]} N={packed.shape[0]}", flush=True)
+    _lib.linear_f16_tuned(xd, pd, sd, out, group_size, kernel, rows, splits, unroll)
+    torch.cuda.synchronize()
+    return out
+
+
+def _run_default(dev, x, packed, scales, group_size=128):
+    xd, pd, sd = x.to(dev), packed.to(dev), scales.to(dev)
+    out = torch.full((x.shape[0], packed.shape[0]), float("nan"), dtype=torch.float16, device=dev)
+    print(f"[case] default M={x.shape[0]} K={x.shape[1]} N={packed.shape[0]} G={group_size}", flush=True)
+    _lib.linear_f16(xd, pd, sd, out, group_size)
+    torch.cuda.synchronize()
+    return out
+
+
+# ---- shapes from the reference's GPU tests and the benchmark configs ----
+SHAPES_M1 = [(256, 8), (256, 7), (1024, 13), (2048, 2048), (2048, 5632), (5632, 2048)]
+
+
+@pytest.mark.parametrize("k,n", SHAPES_M1)
+def test_default_dispatch_m1(gpu, k, n):
+    x, p, s = make_case(1, k, n, seed=k + n)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n}")
+
+
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 6, 7, 8])
+def test_default_dispatch_small_batch(gpu, m):
+    x, p, s = make_case(m, 2048, 2048, seed=m)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m}")
+
+
+@pytest.mark.parametrize("m", [2, 8])
+def test_small_batch_n7(gpu, m):
+    x, p, s = make_case(m, 256, 7, seed=7)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m} N=7")
+
+
+@pytest.mark.parametrize("kernel", [VALU, MFMA])
+@pytest.mark.parametrize("rows", [1, 2, 4])
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("unroll", [1, 2])
+@pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200)])
+def test_tuned_variants_m1(gpu, kernel, rows, splits, unroll, k, n):
+    x, p, s = make_case(1, k, n, seed=3)
+    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"kernel={kernel} rows={rows} splits={splits} unroll={unroll}")
+
+
+@pytest.mark.parametrize("kernel", [VALU, MFMA])
+@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("rows,splits,unroll", [(1, 1, 1), (2, 4, 2), (4, 2, 1)])
+def test_tuned_variants_batch(gpu, kernel, m, rows, splits, unroll):
+    x, p, s = make_case(m, 2048, 300, seed=m)
+    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
+
+
+@pytest.mark.parametrize("kernel", [VALU, MFMA, GENERIC])
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_all_nibble_values(gpu, kernel, m):
+    # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
+    x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
+    out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
+    assert_parity(out, expected(x, p, s), f"all nibbles kernel={kernel} M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 9, 16])
+@pytest.mark.parametrize("group_size", [32, 64, 128, 6])
+def test_generic_kernel_any_group(gpu, m, group_size):
+    k = 384 if group_size != 6 else 396
+    x, p, s = make_case(m, k, 19, seed=group_size, group_size=group_size)
+    out = _run_default(gpu, x, p, s, group_size)
+    assert_parity(out, expected(x, p, s, group_size), f"generic M={m} G={group_size}")
+
+
+def test_misaligned_activations_take_generic(gpu):
+    x, p, s = make_case(1, 2048, 96, seed=5)
+    buf = torch.empty(2048 + 1, dtype=torch.float16, device=gpu)
+    buf[1:] = x.to(gpu)[0]
+    xd = buf[1:].view(1, 2048)
+    assert xd.data_ptr() % 16 != 0
+    plan = _lib.plan_linear(xd.data_ptr(), 0, 1, 96, 2048)
+    assert plan["kernel"] == "generic"
+    out = torch.empty((1, 96), dtype=torch.float16, device=gpu)
+    _lib.linear_f16(xd, p.to(gpu), s.to(gpu), out)
+    torch.cuda.synchronize()
+    assert_parity(out, expected(x, p, s), "misaligned")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("m", [1, 8])
+def test_large_8b_shapes(gpu, k, n, m):
+    x, p, s = make_case(m, k, n, seed=1, device="cuda")
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("group_size", [32, 64, 128])
+@pytest.mark.parametrize("k,n", [(256, 8), (2048, 2048), (2048, 5632), (5632, 2048)])
+def test_dequantize_bit_identical(gpu, group_size, k, n):
+    _, p, s = make_case(1, k, n, seed=k, group_size=group_size)
+    out = torch.empty((n, k), dtype=torch.float16, device=gpu)
+    _lib.dequantize_f16(p.to(gpu), s.to(gpu), out, group_size)
+    torch.cuda.synchronize()
+    ref = oracle.dequantize_f16(p.numpy(), s.numpy(), group_size)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_dequantize_all_codes_all_finite_scales(gpu):
+    # every finite fp16 scale bit pattern (incl. subnormals, +-0) x all 16 codes;
+    # products overflow to inf for large scales and land on fp16 subnormals for
+    # tiny ones
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = bits[np.isfinite(bits.view(np.float16))]
+    n = finite.size                      # 63490 rows of one 32-wide group
+    codes_row = np.array([0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE] * 2, dtype=np.uint8)
+    packed = np.tile(codes_row, (n, 1))  # K = 32: codes 0,1,..,7,-8,..,-1 twice
+    scales = finite.view(np.float16).reshape(n, 1)
+    out = torch.empty((n, 32), dtype=torch.float16, device=gpu)
+    _lib.dequantize_f16(torch.from_numpy(packed).to(gpu), torch.from_numpy(scales.copy()).to(gpu), out, 32)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    ref = oracle.dequantize_f16(packed, scales, 32).view(np.uint16)
+    # NaN payloads are not part of the contract; scales here are finite, so
+    # 0 * finite never makes NaN
+    assert np.array_equal(got, ref)
