@@ -1,0 +1,319 @@
+"""Benchmark of the MI355X W4A16 linear layer (one GPU).
+
+Metric: INT4 GEMV us & % of HBM peak per layer (M=1); decode
+tok/s, 1.1B Llama.
+
+Workload of the headline line (`value`, configs[1]): the two MLP layer shapes
+at M = 1 -- up/gate K=2048 N=5632 and down K=5632 N=2048 -- group size 128,
+fp16 activations ~N(0,1), weights ~N(0,0.02) fp32 quantized RTN absmax, each
+shape with 64 rotated weight copies (762 MB together) so no layer runs from
+the 256 MB Infinity Cache. One step = one call of each shape on its next
+copy. Steps are recorded in a HIP graph and replayed; W warm-up steps are
+replayed untimed, then exactly K steps are timed with events on the replay
+stream between two synchronisations. `value` = algorithmic bytes moved by
+the K steps / elapsed time (GB/s), with algorithmic bytes per call
+N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 (reference scripts/profile_kernel.py:310-323).
+
+Also reported: per-layer us / GB/s / % of the 8 TB/s HBM peak for each shape
+(graph replay, 100 calls), a measured device copy bandwidth, end-to-end greedy
+decode tokens/s of the random-init 1.1B Llama-architecture model (configs[4],
+decode step in a HIP graph), and the CPU oracle's time for the same layers on
+the host cores (`cpu_baseline`; a reported baseline, not a target).
+
+usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the M=1 GEMV on the two configs[1] shapes (mean),
+# from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
+# each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
+# reads half the bytes on this part, WRITE_SIZE is exact).
+MEASURED_TRAFFIC_BYTES = 6154349
+
+
+def payload_bytes(m: int, n: int, k: int, group: int = 128) -> int:
+    return n * k // 2 + n * (k // group) * 2 + m * k * 2 + m * n * 2
+
+
+def make_layer(k: int, n: int, copies: int, device, seed: int = 0):
+    import torch
+
+    from nibble_amd.quantization import quantize_and_pack_weights
+
+    gen = torch.Generator(device=device).manual_seed(seed)
+    w = torch.randn((n, k), device=device, generator=gen) * 0.02
+    packed, scales = quantize_and_pack_weights(w, 128)
+    del w
+    return [packed.clone() for _ in range(copies)], [scales.clone() for _ in range(copies)]
+
+
+def capture(fn, count: int):
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn(0)  # warm any lazy state outside the capture
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(count):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def time_graph(graph, reps: int = 1) -> float:
+    """Seconds for `reps` replays, events on the replay (current) stream."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3
+
+
+def per_layer(op, copies: int, calls: int = 100, samples: int = 20) -> float:
+    """Median microseconds per call over `samples` replays of a `calls`-call graph."""
+    graph = capture(lambda i: op(i % copies), calls)
+    for _ in range(3):
+        graph.replay()
+    times = sorted(time_graph(graph) / calls * 1e6 for _ in range(samples))
+    return times[len(times) // 2]
+
+
+def copy_bandwidth(device) -> float:
+    """Device-to-device copy of 1 GiB (read + write bytes / time), GB/s."""
+    import torch
+
+    a = torch.empty(1 << 28, dtype=torch.float32, device=device)
+    b = torch.empty_like(a)
+    graph = capture(lambda i: b.copy_(a), 5)
+    graph.replay()
+    t = min(time_graph(graph) for _ in range(3))
+    del a, b
+    return 2 * (1 << 30) * 5 / t / 1e9
+
+
+def cpu_baseline(shapes, budget_s: float = 12.0) -> dict:
+    """The CPU oracle (C restatement of reference w4a16/reference.py:49-80:
+    full fp32 dequantize + fp32 matmul + fp16 cast) on the host cores, on a
+    bounded sample of the same layers (M = 1, one weight copy per shape)."""
+    import numpy as np
+
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    layers = []
+    for k, n in shapes:
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        packed, scales = oracle.quantize_and_pack(w, 128)
+        x = rng.standard_normal((1, k)).astype(np.float16)
+        layers.append((x, packed, scales, payload_bytes(1, n, k)))
+    for x, p, s, _ in layers:  # warm-up
+        oracle.linear(x, p, s, 128, threads=threads)
+    calls, total_bytes = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        for x, p, s, nbytes in layers:
+            oracle.linear(x, p, s, 128, threads=threads)
+            calls += 1
+            total_bytes += nbytes
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": round(total_bytes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{calls} single-token calls alternating up (2048x5632) and down (5632x2048) "
+                  f"in {elapsed:.1f} s, 1 weight copy per shape",
+        "us_per_call": round(elapsed / calls * 1e6, 1),
+    }
+
+
+def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 16) -> dict:
+    """greedy decode on the random-init 1.1B Llama, decode step in a HIP graph."""
+    import torch
+
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(max_seq_len=prompt_len + new_tokens)
+    model = LlamaDecoder(cfg, device=device, seed=0)
+    gen = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=gen).to(device)
+    model.prefill(prompt)
+    model.capture()
+    decode_s, prefill_s = [], []
+    for _ in range(runs + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill(prompt)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(new_tokens - 1):
+            model.replay()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        prefill_s.append(t1 - t0)
+        decode_s.append(t2 - t1)
+    decode_s, prefill_s = sorted(decode_s[1:]), sorted(prefill_s[1:])
+    med = decode_s[len(decode_s) // 2]
+    return {
+        "decode_tok_s": round((new_tokens - 1) / med, 1),
+        "ms_per_token": round(med / (new_tokens - 1) * 1e3, 3),
+        "prefill_ms": round(prefill_s[len(prefill_s) // 2] * 1e3, 3),
+        "linear_layers": len(model.linear_layers()),
+        "packed_weight_bytes_per_token": model.packed_bytes(),
+        "model": "random-init Llama 22L h2048 i5632 32q/4kv hd64 vocab32000, INT4 g128 on all 155 linears",
+        "prompt_tokens": prompt_len,
+        "new_tokens": new_tokens,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--counter-pass", action="store_true",
+                    help="eager launches only, for rocprofv3 --pmc: 50 calls of each MLP shape on rotated "
+                         "copies, then 5 elementwise negations of a 256 MiB fp32 buffer into another "
+                         "(256 MiB read + 256 MiB written each: the byte-count calibration); no JSON")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import nibble_amd
+    from nibble_amd import _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    if not nibble_amd.cuda_extension_available():
+        raise RuntimeError(f"W4A16 HIP extension not loaded: {nibble_amd.cuda.extension_load_error()}")
+    device = torch.device("cuda:0")
+    torch.manual_seed(0)
+
+    copies = 64
+    shapes = [(2048, 5632), (5632, 2048)]  # (K, N): up/gate and down
+    layers = [make_layer(k, n, copies, device, seed=i) for i, (k, n) in enumerate(shapes)]
+    xs = [torch.randn((1, k), device=device).to(torch.float16) for k, _ in shapes]
+    outs = [torch.empty((1, n), device=device, dtype=torch.float16) for _, n in shapes]
+
+    def call(j: int, i: int) -> None:
+        packed, scales = layers[j]
+        torch.ops.w4a16.linear(xs[j], packed[i % copies], scales[i % copies], 128)
+
+    def call_raw(j: int, i: int) -> None:
+        packed, scales = layers[j]
+        _lib.linear_f16(xs[j], packed[i % copies], scales[i % copies], outs[j])
+
+    if args.counter_pass:
+        for i in range(50):
+            call_raw(0, i)
+            call_raw(1, i)
+        a = torch.ones(1 << 26, dtype=torch.float32, device=device)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        print("counter pass done", flush=True)
+        return 0
+
+    # ---- headline: K timed steps (one call of each MLP shape per step) ----
+    def step(i: int) -> None:
+        call_raw(0, i)
+        call_raw(1, i)
+
+    warm = capture(step, max(args.warmup, 1))
+    timed = capture(step, args.steps)
+    warm.replay()
+    torch.cuda.synchronize()
+    elapsed = time_graph(timed)
+    step_bytes = sum(payload_bytes(1, n, k) for k, n in shapes)
+    value = step_bytes * args.steps / elapsed / 1e9
+
+    # ---- per-layer and the dominant kernel's roofline ----
+    layer_rows = {}
+    for j, (k, n) in enumerate(shapes):
+        us = per_layer(lambda i, j=j: call_raw(j, i), copies)
+        gbs = payload_bytes(1, n, k) / us / 1e3
+        plan = _lib.plan_linear(xs[j].data_ptr(), layers[j][0][0].data_ptr(), 1, n, k)
+        layer_rows[f"K{k}xN{n}"] = {"us": round(us, 3), "GBps": round(gbs, 1),
+                                    "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": plan}
+    # torch-op path (drop-in API) for the same shapes, for comparison with the raw C ABI
+    op_us = {f"K{k}xN{n}": round(per_layer(lambda i, j=j: call(j, i), copies), 3) for j, (k, n) in enumerate(shapes)}
+
+    achieved = step_bytes / (elapsed / args.steps) / 1e9  # = value; per-launch average over the two shapes
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "traffic": MEASURED_TRAFFIC_BYTES,
+        "kernel": "w4a16::gemv_valu<1,2,*> (M=1 VALU GEMV)",
+        "bytes_per_launch": step_bytes // 2,
+        "us_per_launch": round(elapsed / args.steps / 2 * 1e6, 3),
+    }
+
+    line = {
+        "metric": "INT4 GEMV µs & % of HBM peak per layer (M=1); decode tok/s, 1.1B Llama",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes x f16 -> f32 accumulate",
+        "data": "synthetic (weights ~N(0,0.02) fp32 RTN-quantized to INT4 g128, activations ~N(0,1) fp16)",
+        "config": {
+            "workload": "configs[1]: M=1 MLP layers K2048xN5632 + K5632xN2048, group 128, 64 rotated copies each",
+            "step": "one call of each shape on its next weight copy, HIP-graph replay",
+            "parallelism": "single GPU",
+        },
+        "layers_us": layer_rows,
+        "torch_op_us": op_us,
+        "roofline": roofline,
+    }
+    line["copy_GBps"] = round(copy_bandwidth(device), 1)
+    if not args.no_decode:
+        del layers
+        torch.cuda.empty_cache()
+        line["decode"] = decode_tok_s(device)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(shapes)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -38,6 +38,7 @@ extern "C" {
 #define W4A16_KERNEL_VALU 1          /* VALU dot2 GEMV, activations staged in LDS (M <= 8) */
 #define W4A16_KERNEL_MFMA 2          /* fp16 MFMA 16x16x32 tiles, M zero-padded to 16 (M <= 8) */
 #define W4A16_KERNEL_GENERIC 3       /* any M, any even group_size, any alignment */
+#define W4A16_KERNEL_DIAG 4          /* M = 1 on fp16 MFMA, group dots on the 16x16 diagonal */
 
 /*
  * Fused W4A16 linear layer.
@@ -49,7 +50,7 @@ extern "C" {
  * takes the tuned kernels; anything else takes the generic kernel.
  * Environment, read at every call: W4A16_DECODE = auto|valu|mfma selects the
  * kernel family for M <= 8; W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per
- * workgroup of the VALU kernel (any other value is W4A16_ERR_CONFIG).
+ * wavefront of the VALU kernel (any other value is W4A16_ERR_CONFIG).
  */
 int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights,
                      const void* scales, void* output, int64_t M, int64_t N,
@@ -91,21 +92,29 @@ int w4a16_check_dequantize_shapes(int64_t packed_rows, int64_t packed_cols,
  */
 int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
                       int64_t M, int64_t N, int64_t K, int64_t group_size,
-                      int* kernel, int* rows, int* splits, int* unroll);
+                      int* kernel, int* rows, int* splits, int* unroll,
+                      int* max_blocks);
 
 /*
  * w4a16_linear_f16 with an explicit kernel family and launch shape, for
- * tuning sweeps. kernel: W4A16_KERNEL_VALU (rows 1|2|4, splits 1..8,
- * unroll 1|2), W4A16_KERNEL_MFMA (rows = 16-row blocks per wave 1|2|4,
- * splits 1..8, unroll 1|2|4) or W4A16_KERNEL_GENERIC (other arguments
- * ignored). The VALU and MFMA families need group_size 128, M <= 8 and
- * 16-byte aligned activations and weights. No reference counterpart (the
- * reference's W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
+ * tuning sweeps.
+ *   W4A16_KERNEL_VALU: rows = output rows per wavefront task (1|2|4),
+ *     splits = wavefronts per workgroup (1..4), unroll = chunks in flight per
+ *     row (1|2|4|8; 8 needs rows <= 2), max_blocks = grid cap (0 = none).
+ *   W4A16_KERNEL_MFMA: rows = 16-row blocks per wavefront (1|2|4),
+ *     splits = wavefronts splitting K (1..8), unroll = groups in flight (1|2|4).
+ *   W4A16_KERNEL_DIAG (M = 1 only): rows = output rows per wavefront task
+ *     (1|2|4), splits = wavefronts per workgroup (1..4), unroll = 1 KiB spans
+ *     in flight per row (1|2|4; 4 needs rows <= 2), max_blocks = grid cap.
+ *   W4A16_KERNEL_GENERIC: other arguments ignored.
+ * The VALU and MFMA families need group_size 128, M <= 8 and 16-byte aligned
+ * activations and weights. No reference counterpart (the reference's
+ * W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
  */
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,
                            const void* scales, void* output, int64_t M, int64_t N,
                            int64_t K, int64_t group_size, void* stream,
-                           int kernel, int rows, int splits, int unroll);
+                           int kernel, int rows, int splits, int unroll, int max_blocks);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* w4a16_last_error(void);

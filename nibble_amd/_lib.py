@@ -29,7 +29,9 @@ KERNEL_NONE = 0
 KERNEL_VALU = 1
 KERNEL_MFMA = 2
 KERNEL_GENERIC = 3
-KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic"}
+KERNEL_DIAG = 4
+KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic",
+                KERNEL_DIAG: "diag"}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -41,10 +43,10 @@ SIGNATURES = {
     "w4a16_dequantize_f16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "w4a16_check_linear_shapes": (ctypes.c_int, [_i64] * 7),
     "w4a16_check_dequantize_shapes": (ctypes.c_int, [_i64] * 5 + [ctypes.c_uint64]),
-    "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip]),
+    "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip, _ip]),
     "w4a16_linear_f16_tuned": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int],
+        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp] + [ctypes.c_int] * 5,
     ),
     "w4a16_last_error": (ctypes.c_char_p, []),
     "w4a16_version": (ctypes.c_char_p, []),
@@ -104,13 +106,13 @@ def linear_f16(activations, packed_weights, scales, output, group_size: int = 12
 
 
 def linear_f16_tuned(activations, packed_weights, scales, output, group_size, kernel, rows, splits, unroll,
-                     stream=None) -> None:
+                     max_blocks=0, stream=None) -> None:
     m, k = activations.shape
     n = packed_weights.shape[0]
     _raise_on(
         lib().w4a16_linear_f16_tuned(
             activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
-            m, n, k, group_size, _stream_ptr(stream), kernel, rows, splits, unroll,
+            m, n, k, group_size, _stream_ptr(stream), kernel, rows, splits, unroll, max_blocks,
         )
     )
 
@@ -127,12 +129,13 @@ def dequantize_f16(packed_weights, scales, output, group_size: int = 128, stream
 
 def plan_linear(act_ptr: int, packed_ptr: int, m: int, n: int, k: int, group_size: int = 128) -> dict:
     """The dispatcher's choice for these sizes/alignments (host-only, no GPU needed)."""
-    out = [ctypes.c_int(0) for _ in range(4)]
+    out = [ctypes.c_int(0) for _ in range(5)]
     _raise_on(
         lib().w4a16_plan_linear(act_ptr, packed_ptr, m, n, k, group_size, *[ctypes.byref(v) for v in out])
     )
-    kernel, rows, splits, unroll = (v.value for v in out)
-    return {"kernel": KERNEL_NAMES[kernel], "rows": rows, "splits": splits, "unroll": unroll}
+    kernel, rows, splits, unroll, max_blocks = (v.value for v in out)
+    return {"kernel": KERNEL_NAMES[kernel], "rows": rows, "splits": splits, "unroll": unroll,
+            "max_blocks": max_blocks}
 
 
 def check_linear_shapes(act_rows, act_cols, packed_rows, packed_cols, scale_rows, scale_cols, group_size):

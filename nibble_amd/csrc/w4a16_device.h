@@ -30,8 +30,8 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
 // weight 2j in its low nibble and 2j+1 in its high nibble, two's complement,
 // so nibble i of a little-endian 32-bit word is weight i of that word.
 //
-// XOR with 0x8 turns a two's-complement nibble s into the offset value s+8 in
-// [0, 15]. OR-ing a 4-bit value v into the mantissa of binary16 1024.0
+// Flipping bit 3 turns a two's-complement nibble s into the offset value
+// s+8 in [0, 15]. OR-ing a 4-bit value v into the mantissa of binary16 1024.0
 // (0x6400, exponent 2^10, unit last place 1) gives exactly 1024 + v; placed
 // one nibble higher it gives 1024 + 16 v. One packed f16 add or fma then
 // recovers s exactly:
@@ -49,16 +49,20 @@ struct Codes8 {
 };
 
 __device__ __forceinline__ Codes8 unpack8(uint32_t word) {
-    const uint32_t u = word ^ 0x88888888u;
-    const uint32_t v = u >> 8;
+    // v_bitop3 computes (word & mask) ^ c in one instruction; c = the 0x6400
+    // magic OR the nibble's bit-3 flip (two's complement -> offset binary),
+    // which never overlaps the mask bits.
+    const uint32_t v = word >> 8;
     const f16x2 bias_lo = {(f16)-1032.0f, (f16)-1032.0f};
     const f16x2 mul_hi = {(f16)0.0625f, (f16)0.0625f};
     const f16x2 bias_hi = {(f16)-72.0f, (f16)-72.0f};
     Codes8 c;
-    c.p[0] = as_f16x2((u & 0x000F000Fu) | 0x64006400u) + bias_lo;
-    c.p[1] = __builtin_elementwise_fma(as_f16x2((u & 0x00F000F0u) | 0x64006400u), mul_hi, bias_hi);
-    c.p[2] = as_f16x2((v & 0x000F000Fu) | 0x64006400u) + bias_lo;
-    c.p[3] = __builtin_elementwise_fma(as_f16x2((v & 0x00F000F0u) | 0x64006400u), mul_hi, bias_hi);
+    c.p[0] = as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x000F000Fu, 0x64086408u, 0x6A)) + bias_lo;
+    c.p[1] = __builtin_elementwise_fma(
+        as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x00F000F0u, 0x64806480u, 0x6A)), mul_hi, bias_hi);
+    c.p[2] = as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x000F000Fu, 0x64086408u, 0x6A)) + bias_lo;
+    c.p[3] = __builtin_elementwise_fma(
+        as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x00F000F0u, 0x64806480u, 0x6A)), mul_hi, bias_hi);
     return c;
 }
 

@@ -55,13 +55,15 @@ int check_launch() {
 
 struct Plan {
     int kernel = W4A16_KERNEL_NONE;
-    int rows = 0;    // VALU: output rows per workgroup; MFMA: 16-row blocks per wavefront
-    int splits = 0;  // wavefronts per workgroup splitting K
-    int unroll = 0;  // chunks (VALU) or groups (MFMA) in flight per wavefront step
+    int rows = 0;        // VALU: output rows per wavefront task; MFMA: 16-row blocks per wavefront
+    int splits = 0;      // VALU: wavefronts per workgroup; MFMA: wavefronts splitting K
+    int unroll = 0;      // chunks (VALU) or groups (MFMA) in flight per row per step
+    int max_blocks = 0;  // VALU: grid cap (0 = one task per wavefront)
 };
 
 int valu_lds_bytes(int64_t M, int64_t K, const Plan& p) {
-    return (int)(M * K * 2 + (int64_t)p.splits * p.rows * M * 4);
+    (void)p;
+    return (int)(M * K * 2);
 }
 int mfma_lds_bytes(const Plan& p) { return p.splits > 1 ? p.splits * p.rows * 64 * 16 : 0; }
 
@@ -88,13 +90,23 @@ int read_env(int* family, int* rows_per_wave) {
 
 int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
+// Launch shape of the VALU kernel, from the sweeps over the benchmark shapes
+// (K 2048..28672, N 2048..28672): 2 rows per wavefront task, 4 wavefronts
+// per workgroup, grid capped at 1024 workgroups (several tasks per
+// wavefront), one chunk per row in flight when K is a multiple of 2048 up to
+// 8192, otherwise enough to cover the row's ragged or long tail.
 Plan plan_valu(int64_t M, int64_t N, int64_t K, int rows) {
     Plan p;
     p.kernel = W4A16_KERNEL_VALU;
+    const int64_t per_lane = (K / 32 + 63) / 64;  // chunks per lane per row
+    if (K % 2048 == 0 && per_lane <= 4)
+        p.unroll = 1;
+    else
+        p.unroll = per_lane <= 4 ? 4 : 8;
     p.rows = rows ? rows : 2;
-    const int64_t chunks = K / 32;
-    p.splits = clampi((int)(chunks / 128), 1, 8);
-    p.unroll = (chunks >= 2 * 64 * p.splits) ? 2 : 1;
+    if (p.rows == 4 && p.unroll == 8) p.unroll = 4;
+    p.splits = 4;
+    p.max_blocks = 1024;
     (void)M;
     (void)N;
     return p;
@@ -147,20 +159,24 @@ template <int M>
 int launch_valu_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
                   w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
-    const void* fn = nullptr;
-    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int) = nullptr;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
 #define W4A16_PICK(R, U) \
     if (p.rows == R && p.unroll == U) kern = gemv_valu<M, R, U>;
-    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(4, 1) W4A16_PICK(4, 2)
+    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4) W4A16_PICK(1, 8)
+    W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4) W4A16_PICK(2, 8)
+    W4A16_PICK(4, 1) W4A16_PICK(4, 2) W4A16_PICK(4, 4)
 #undef W4A16_PICK
-    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "VALU kernel: rows must be 1, 2, or 4 and unroll 1 or 2");
-    fn = reinterpret_cast<const void*>(kern);
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, "VALU kernel: rows must be 1, 2, or 4 and unroll 1, 2, 4, or 8 (8 needs rows <= 2)");
+    if (p.splits < 1 || p.splits > 4) return fail(W4A16_ERR_CONFIG, "VALU kernel: 1..4 wavefronts per workgroup");
     const int lds = valu_lds_bytes(M, K, p);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "VALU kernel: M*K activations do not fit in LDS");
-    int rc = ensure_lds(fn, lds);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
     if (rc != W4A16_OK) return rc;
-    const int blocks = (N + p.rows - 1) / p.rows;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K);
+    const int tasks = (N + p.rows - 1) / p.rows;
+    int blocks = (tasks + p.splits - 1) / p.splits;
+    if (p.max_blocks > 0 && blocks > p.max_blocks) blocks = p.max_blocks;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K, tasks);
     return check_launch();
 }
 
@@ -177,6 +193,32 @@ int launch_valu(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, con
         case 8: return launch_valu_m<8>(p, x, w, s, o, N, K, stream);
         default: return fail(W4A16_ERR_CONFIG, "VALU kernel needs 1 <= M <= 8");
     }
+}
+
+int launch_diag(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                w4a16::f16* o, int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    if (M != 1) return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel needs M == 1");
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
+#define W4A16_PICK(R, U) \
+    if (p.rows == R && p.unroll == U) kern = gemv_diag<R, U>;
+    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4)
+    W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4)
+    W4A16_PICK(4, 1) W4A16_PICK(4, 2)
+#undef W4A16_PICK
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: rows 1, 2, 4 and unroll 1, 2, 4 (4 needs rows <= 2)");
+    if (p.splits < 1 || p.splits > 4) return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: 1..4 wavefronts per workgroup");
+    const int spans = (K / 32 + 63) / 64;
+    const int lds = spans * 64 * 64;
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: activations do not fit in LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int tasks = (N + p.rows - 1) / p.rows;
+    int blocks = (tasks + p.splits - 1) / p.splits;
+    if (p.max_blocks > 0 && blocks > p.max_blocks) blocks = p.max_blocks;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K, tasks);
+    return check_launch();
 }
 
 int launch_mfma(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
@@ -225,6 +267,7 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_NONE: return W4A16_OK;
         case W4A16_KERNEL_VALU: return launch_valu(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA: return launch_mfma(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_DIAG: return launch_diag(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -278,7 +321,8 @@ int w4a16_check_dequantize_shapes(int64_t packed_rows, int64_t packed_cols, int6
 }
 
 int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N,
-                      int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll) {
+                      int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll,
+                      int* max_blocks) {
     int rc = check_scalar_args(M, N, K, group_size);
     if (rc != W4A16_OK) return rc;
     Plan p;
@@ -288,6 +332,7 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, in
     if (rows) *rows = p.rows;
     if (splits) *splits = p.splits;
     if (unroll) *unroll = p.unroll;
+    if (max_blocks) *max_blocks = p.max_blocks;
     return W4A16_OK;
 }
 
@@ -306,7 +351,7 @@ int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights, con
 
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights, const void* scales,
                            void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream,
-                           int kernel, int rows, int splits, int unroll) {
+                           int kernel, int rows, int splits, int unroll, int max_blocks) {
     int rc = check_scalar_args(M, N, K, group_size);
     if (rc != W4A16_OK) return rc;
     if (M * N == 0) return W4A16_OK;
@@ -317,13 +362,14 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.rows = rows;
     p.splits = splits;
     p.unroll = unroll;
-    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA) {
+    p.max_blocks = max_blocks;
+    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG) {
         if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
-        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _MFMA or _GENERIC");
+        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _MFMA, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
 }

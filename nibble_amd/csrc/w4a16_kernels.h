@@ -16,52 +16,162 @@ namespace w4a16 {
 // ---------------------------------------------------------------------------
 // VALU GEMV (M = 1..8 activation rows, template), G = 128.
 //
-// Workgroup = S wavefronts (blockDim = 64 S) on R consecutive output rows.
-// The activations are staged once per workgroup in LDS, permuted to the
-// unpack8 pair order and laid out unit-major: unit q (8 halves) of chunk c of
-// activation row m lives at xs[(m*4 + q) * C + c], so the 64 lanes of a
-// wavefront reading unit q of 64 consecutive chunks hit 64 consecutive
-// 16-byte slots.
-// Thread t handles chunks t, t + 64 S, ... of every one of the R rows: each
-// chunk is one 16-byte load per row, decoded once and dotted with the M
-// activation rows by v_dot2_f32_f16 (fp16 products, fp32 accumulation). The
-// chunk dot is scaled by its group's scale in fp32 (reference
-// csrc/int4_linear_kernel.cu:390 scales per-lane chunk partials the same way).
-// Reduction: DPP within each wavefront, LDS across the S wavefronts.
-// Rows past N re-read row N-1 and are not stored (keeps every access in
-// bounds and every wavefront on the same path).
+// Work unit ("task"): R consecutive output rows, handled by one wavefront over
+// the whole of K. Lane l takes chunks l, l + 64, l + 128, ... of each of the
+// R rows, U chunks per row per step, so every load instruction reads 1 KiB of
+// contiguous weights. Each 16-byte chunk is decoded once (unpack8) and dotted
+// with the M activation rows by v_dot2_f32_f16 (fp16 products, fp32 sums);
+// the chunk dot is scaled by its group's fp32 scale (the reference's kernel
+// scales per-chunk partials the same way, csrc/int4_linear_kernel.cu:390).
+// The row sum is a DPP wavefront reduction; lane 0 stores it.
+//
+// A workgroup of W wavefronts stages the activations once in LDS, permuted to
+// the unpack8 pair order and unit-major (unit q of chunk c of activation row m
+// at xs[(m*4 + q) * C + c]: lanes reading consecutive chunks hit consecutive
+// 16-byte slots), then each wavefront walks its (task, step) sequence --
+// tasks blockIdx.x*W + wave, + gridDim.x*W -- with two register buffers: the
+// loads of the next step are in flight while the current step computes. The
+// first step's loads are issued before the activation staging. Task and row
+// indices are wavefront-uniform (scalar registers), so each load is a scalar
+// row base plus a per-lane 32-bit offset. Rows past N re-read row N-1 and are
+// not stored.
 // ---------------------------------------------------------------------------
+// Copy the M activation rows into LDS, permuted to the unpack8 pair order,
+// unit-major: unit q (8 halves) of chunk c of row m goes to xs[(m*4 + q)*C + c].
+// Loads are issued in batches of 8 per thread before any is waited on, so the
+// whole copy costs about one L2 round trip instead of one per unit.
+template <int M>
+__device__ __forceinline__ void stage_activations(const f16* __restrict__ x, u32x4* xs, int K, int C) {
+    constexpr int kBatch = 8;
+    const int units_per_row = K >> 3;
+    const int total = M * units_per_row;
+    const int T = blockDim.x;
+    for (int base = threadIdx.x; base < total; base += kBatch * T) {
+        u32x4 a[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = base + j * T;
+            if (i < total) a[j] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = base + j * T;
+            if (i < total) {
+                const int m = i / units_per_row;
+                const int u = i - m * units_per_row;
+                xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(a[j]);
+            }
+        }
+    }
+}
+
 template <int M, int R, int U>
-__global__ void __launch_bounds__(512)
+struct ValuStep {
+    u32x4 w[U][R];
+    f16 s[U][R];
+};
+
+template <int M, int R, int U>
+__device__ __forceinline__ void valu_load(ValuStep<M, R, U>& b, const uint8_t* __restrict__ w,
+                                          const f16* __restrict__ scales, int task, int step, int lane,
+                                          int N, int C, int G, uint32_t row_bytes) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(task * R + r, N - 1);
+        const uint8_t* wrow = w + (size_t)n * row_bytes;                 // wavefront-uniform
+        const uint8_t* srow = reinterpret_cast<const uint8_t*>(scales + (size_t)n * G);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = (step * U + u) * 64 + lane;
+            if (c < C) {
+                // unsigned 32-bit per-lane byte offsets: scalar base + vector offset addressing
+                const uint32_t c32 = (uint32_t)c;
+                b.w[u][r] = load_stream(reinterpret_cast<const u32x4*>(wrow + c32 * 16u));
+                b.s[u][r] = *reinterpret_cast<const f16*>(srow + (c32 >> 2) * 2u);
+            }
+        }
+    }
+}
+
+template <int M, int R, int U>
+__device__ __forceinline__ void valu_compute(const ValuStep<M, R, U>& b, const u32x4* xs, float (&acc)[R][M],
+                                             int step, int lane, int C) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c = (step * U + u) * 64 + lane;
+        if (c < C) {
+            float d[R][M];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < M; ++m) d[r][m] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                u32x4 xa[M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) xa[m] = xs[(m * 4 + q) * C + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const Codes8 cw = unpack8(b.w[u][r][q]);
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].x), cw.p[0], d[r][m], false);
+                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].y), cw.p[1], d[r][m], false);
+                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].z), cw.p[2], d[r][m], false);
+                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].w), cw.p[3], d[r][m], false);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float s = (float)b.s[u][r];
+#pragma unroll
+                for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fmaf(d[r][m], s, acc[r][m]);
+            }
+        }
+    }
+}
+
+template <int M, int R>
+__device__ __forceinline__ void valu_finish(float (&acc)[R][M], f16* __restrict__ out, int task, int lane, int N) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float v = wave_sum(acc[r][m]);
+            acc[r][m] = 0.0f;
+            if (lane == 0 && task * R + r < N) out[(size_t)m * N + task * R + r] = (f16)v;
+        }
+    }
+}
+
+template <int M, int R, int U>
+__global__ void __launch_bounds__(256)
 gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
-          const f16* __restrict__ scales, f16* __restrict__ out, int N, int K) {
+          const f16* __restrict__ scales, f16* __restrict__ out, int N, int K, int num_tasks) {
     extern __shared__ __align__(16) uint8_t smem[];
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
 
-    const int T = blockDim.x;
-    const int tid = threadIdx.x;
-    const int C = K >> 5;   // chunks per row
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int C = K >> 5;   // 16-byte chunks per row
     const int G = K >> 7;   // groups per row
+    const int steps = (C + 64 * U - 1) / (64 * U);
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
 
-    // Stage activations (16 B per unit, permuted).
-    const int units_per_row = K >> 3;
-    for (int i = tid; i < M * units_per_row; i += T) {
-        const int m = i / units_per_row;
-        const int j = i - m * units_per_row;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
-        xs[(m * 4 + (j & 3)) * C + (j >> 2)] = permute8(a);
-    }
+    const int task0 = blockIdx.x * W + wave;
+    const int task_stride = gridDim.x * W;
+    const int my_tasks = task0 < num_tasks ? (num_tasks - 1 - task0) / task_stride + 1 : 0;
+    const int units = my_tasks * steps;
+
+    ValuStep<M, R, U> buf0, buf1;
+    // (task, step) of the unit in buf0; buf1 holds the one after it
+    int task = task0, step = 0;
+    if (units > 0) valu_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
+
+    stage_activations<M>(x, xs, K, C);
     __syncthreads();
-
-    const int n0 = blockIdx.x * R;
-    const u32x4* wrow[R];
-    const f16* srow[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int n = min(n0 + r, N - 1);
-        wrow[r] = reinterpret_cast<const u32x4*>(w + (size_t)n * (size_t)(K >> 1));
-        srow[r] = scales + (size_t)n * G;
-    }
 
     float acc[R][M];
 #pragma unroll
@@ -69,72 +179,187 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
-    for (int c0 = tid; c0 < C; c0 += U * T) {
-        u32x4 wv[U][R];
-        f16 sv[U][R];
+    for (int u = 0; u < units; u += 2) {
+        // next unit -> buf1
+        int task1 = task, step1 = step + 1;
+        if (step1 == steps) { step1 = 0; task1 += task_stride; }
+        if (u + 1 < units) valu_load(buf1, w, scales, task1, step1, lane, N, C, G, row_bytes);
+        valu_compute(buf0, xs, acc, step, lane, C);
+        if (step == steps - 1) valu_finish(acc, out, task, lane, N);
+        if (u + 1 >= units) break;
+        // unit after that -> buf0
+        task = task1;
+        step = step1 + 1;
+        if (step == steps) { step = 0; task += task_stride; }
+        if (u + 2 < units) valu_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
+        valu_compute(buf1, xs, acc, step1, lane, C);
+        if (step1 == steps - 1) valu_finish(acc, out, task1, lane, N);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M = 1 GEMV on the matrix cores ("diagonal MFMA"), G = 128.
+//
+// A wavefront reads a row in 1 KiB spans (64 lanes x 16 bytes = 64 chunks =
+// 16 groups) like the VALU kernel, but lane l = 16q + j takes chunk 4j + q of
+// the span, so the four lanes j, 16+j, 32+j, 48+j hold the four chunks of
+// group j. With B = the lane's unpacked codes (column j = l%16, k-block q)
+// and A = the matching activations (row i = l%16, same k-block), the four
+// v_mfma_f32_16x16x32_f16 of one span (one per 32-bit word of the chunk)
+// leave D[j][j] = sum over group j of x * code: the diagonal is the 16 group
+// dots, exactly accumulated in fp32 (off-diagonal entries are unused). Every
+// lane holds column j = l%16, so scaling all of D by the lane's group scale
+// scales the diagonal correctly. The decode costs 9 VALU operations per 8
+// weights and the products move to the matrix cores.
+// D[i][j] sits in lane 16(i/4) + j, register i%4: the diagonal is lane l's
+// register l%4 when (l%16)/4 == l/16.
+// Activations are staged once per workgroup in LDS with chunk c of span s at
+// slot s*64 + 16(c%4) + (c%64)/4 (unit-major, zero padded to whole spans),
+// so lane l reads slot s*64 + l: conflict-free and already in A layout.
+// Task/step/double-buffer structure as in the VALU kernel.
+// ---------------------------------------------------------------------------
+template <int R, int U>
+struct DiagStep {
+    u32x4 w[U][R];
+    f16 s[U][R];
+};
+
+__device__ __forceinline__ int diag_chunk(int lane) { return 4 * (lane & 15) + (lane >> 4); }
+
+template <int R, int U>
+__device__ __forceinline__ void diag_load(DiagStep<R, U>& b, const uint8_t* __restrict__ w,
+                                          const f16* __restrict__ scales, int task, int step, int lane,
+                                          int N, int C, int G, uint32_t row_bytes) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(task * R + r, N - 1);
+        const uint8_t* wrow = w + (size_t)n * row_bytes;
+        const uint8_t* srow = reinterpret_cast<const uint8_t*>(scales + (size_t)n * G);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int c = c0 + u * T;
+            const int span = step * U + u;
+            const int c = span * 64 + diag_chunk(lane);
             if (c < C) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    wv[u][r] = load_stream(wrow[r] + c);
-                    sv[u][r] = srow[r][c >> 2];
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int c = c0 + u * T;
-            if (c < C) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    u32x4 xa[M];
-#pragma unroll
-                    for (int m = 0; m < M; ++m) xa[m] = xs[(m * 4 + q) * C + c];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const Codes8 cw = unpack8(wv[u][r][q]);
-                        const float s = (float)sv[u][r];
-#pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            float d = 0.0f;
-                            d = __builtin_amdgcn_fdot2(as_f16x2(xa[m].x), cw.p[0], d, false);
-                            d = __builtin_amdgcn_fdot2(as_f16x2(xa[m].y), cw.p[1], d, false);
-                            d = __builtin_amdgcn_fdot2(as_f16x2(xa[m].z), cw.p[2], d, false);
-                            d = __builtin_amdgcn_fdot2(as_f16x2(xa[m].w), cw.p[3], d, false);
-                            acc[r][m] = __builtin_fmaf(d, s, acc[r][m]);
-                        }
-                    }
-                }
+                const uint32_t c32 = (uint32_t)c;
+                b.w[u][r] = load_stream(reinterpret_cast<const u32x4*>(wrow + c32 * 16u));
+                b.s[u][r] = *reinterpret_cast<const f16*>(srow + (c32 >> 2) * 2u);
+            } else {
+                b.w[u][r] = (u32x4){0u, 0u, 0u, 0u};   // all codes 0
+                b.s[u][r] = (f16)0.0f;
             }
         }
     }
+}
 
-    const int S = T >> 6;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    float* red = reinterpret_cast<float*>(smem + (size_t)M * K * 2);
+template <int R, int U>
+__device__ __forceinline__ void diag_compute(const DiagStep<R, U>& b, const u32x4* xs, f32x4 (&acc)[R],
+                                             int step, int lane, int spans) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int u = 0; u < U; ++u) {
+        const int span = step * U + u;
+        if (span < spans) {
+            f16x8 a[4];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float v = wave_sum(acc[r][m]);
-            if (S == 1) {
-                if (lane == 0 && n0 + r < N) out[(size_t)m * N + n0 + r] = (f16)v;
-            } else if (lane == 0) {
-                red[wave * (R * M) + r * M + m] = v;
+            for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(f16x8, xs[(t * spans + span) * 64 + lane]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const Codes8 cw = unpack8(b.w[u][r][t]);
+                    const f16x8 bt = __builtin_bit_cast(
+                        f16x8, (u32x4){as_u32(cw.p[0]), as_u32(cw.p[1]), as_u32(cw.p[2]), as_u32(cw.p[3])});
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bt, d, 0, 0, 0);
+                }
+                acc[r] = d * (float)b.s[u][r] + acc[r];
             }
         }
-    if (S > 1) {
-        __syncthreads();
-        if (tid < R * M) {
-            const int r = tid / M;
-            const int m = tid - r * M;
-            float v = 0.0f;
-            for (int s = 0; s < S; ++s) v += red[s * (R * M) + tid];
-            if (n0 + r < N) out[(size_t)m * N + n0 + r] = (f16)v;
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void diag_finish(f32x4 (&acc)[R], f16* __restrict__ out, int task, int lane, int N) {
+    const bool on_diag = ((lane & 15) >> 2) == (lane >> 4);
+    const int e = lane & 3;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float d = e == 0 ? acc[r][0] : e == 1 ? acc[r][1] : e == 2 ? acc[r][2] : acc[r][3];
+        const float v = wave_sum(on_diag ? d : 0.0f);
+        acc[r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        if (lane == 0 && task * R + r < N) out[task * R + r] = (f16)v;
+    }
+}
+
+// Activations into LDS in the diagonal-MFMA A layout (see above).
+__device__ __forceinline__ void stage_activations_diag(const f16* __restrict__ x, u32x4* xs, int K, int spans) {
+    constexpr int kBatch = 8;
+    const int units = K >> 3;            // real 16-byte units
+    const int total = spans * 64 * 4;    // padded
+    const int T = blockDim.x;
+    for (int base = threadIdx.x; base < total; base += kBatch * T) {
+        u32x4 a[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = base + j * T;
+            a[j] = (u32x4){0u, 0u, 0u, 0u};
+            if (i < units) a[j] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
         }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = base + j * T;
+            if (i < total) {
+                const int c = i >> 2, t = i & 3;
+                const int span = c >> 6, cl = c & 63;
+                xs[(t * spans + span) * 64 + 16 * (cl & 3) + (cl >> 2)] = permute8(a[j]);
+            }
+        }
+    }
+}
+
+template <int R, int U>
+__global__ void __launch_bounds__(256)
+gemv_diag(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+          const f16* __restrict__ scales, f16* __restrict__ out, int N, int K, int num_tasks) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);
+
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int C = K >> 5;
+    const int G = K >> 7;
+    const int spans = (C + 63) >> 6;
+    const int steps = (spans + U - 1) / U;
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+
+    const int task0 = blockIdx.x * W + wave;
+    const int task_stride = gridDim.x * W;
+    const int my_tasks = task0 < num_tasks ? (num_tasks - 1 - task0) / task_stride + 1 : 0;
+    const int units = my_tasks * steps;
+
+    DiagStep<R, U> buf0, buf1;
+    int task = task0, step = 0;
+    if (units > 0) diag_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
+    stage_activations_diag(x, xs, K, spans);
+    __syncthreads();
+
+    f32x4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int u = 0; u < units; u += 2) {
+        int task1 = task, step1 = step + 1;
+        if (step1 == steps) { step1 = 0; task1 += task_stride; }
+        if (u + 1 < units) diag_load(buf1, w, scales, task1, step1, lane, N, C, G, row_bytes);
+        diag_compute(buf0, xs, acc, step, lane, spans);
+        if (step == steps - 1) diag_finish(acc, out, task, lane, N);
+        if (u + 1 >= units) break;
+        task = task1;
+        step = step1 + 1;
+        if (step == steps) { step = 0; task += task_stride; }
+        if (u + 2 < units) diag_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
+        diag_compute(buf1, xs, acc, step1, lane, spans);
+        if (step1 == steps - 1) diag_finish(acc, out, task1, lane, N);
     }
 }
 

@@ -1,0 +1,222 @@
+"""A random-init Llama-architecture decoder whose linear layers are
+``QuantizedLinear`` -- the caller that the end-to-end decode measurement
+(tokens/s) exercises.
+
+The reference measures decode on HuggingFace TinyLlama-1.1B with a static KV
+cache and CUDA graphs (reference ``scripts/generate.py:260-365``); checkpoints
+cannot be fetched here, so this module builds the same architecture offline:
+22 layers, hidden 2048, intermediate 5632, 32 query / 4 key-value heads of
+dim 64, vocab 32000, RMSNorm, rotary position embedding, SiLU-gated MLP.
+All 155 linear layers (q, k, v, o, gate, up, down per layer, and lm_head)
+hold INT4 group-128 weights quantized from N(0, 0.02).
+
+Decode (one token, M = 1) runs the fused HIP GEMV for every linear layer;
+prefill (M = prompt length > 8) runs the HIP dequantize kernel + hipBLASLt.
+``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
+lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
+graph, so generating a token is one ``graph.replay()``.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from nibble_amd.linear import QuantizedLinear
+from nibble_amd.quantization import quantize_and_pack_weights
+
+
+@dataclass
+class LlamaConfig:
+    vocab_size: int = 32000
+    hidden_size: int = 2048
+    intermediate_size: int = 5632
+    num_layers: int = 22
+    num_heads: int = 32
+    num_kv_heads: int = 4
+    head_dim: int = 64
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    max_seq_len: int = 64
+    group_size: int = 128
+    init_std: float = 0.02
+
+    @property
+    def num_linear_layers(self) -> int:
+        return self.num_layers * 7 + 1
+
+
+def _quantized(out_features: int, in_features: int, cfg: LlamaConfig, device, gen) -> QuantizedLinear:
+    weight = torch.randn((out_features, in_features), device=device, generator=gen) * cfg.init_std
+    packed, scales = quantize_and_pack_weights(weight, cfg.group_size)
+    return QuantizedLinear(packed, scales, group_size=cfg.group_size)
+
+
+class RMSNorm(torch.nn.Module):
+    def __init__(self, dim: int, eps: float, device) -> None:
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(dim, dtype=torch.float16, device=device), requires_grad=False)
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(torch.float16)
+
+
+class Block(torch.nn.Module):
+    def __init__(self, cfg: LlamaConfig, device, gen) -> None:
+        super().__init__()
+        h, kv = cfg.hidden_size, cfg.num_kv_heads * cfg.head_dim
+        self.cfg = cfg
+        self.input_norm = RMSNorm(h, cfg.rms_norm_eps, device)
+        self.q_proj = _quantized(h, h, cfg, device, gen)
+        self.k_proj = _quantized(kv, h, cfg, device, gen)
+        self.v_proj = _quantized(kv, h, cfg, device, gen)
+        self.o_proj = _quantized(h, h, cfg, device, gen)
+        self.post_norm = RMSNorm(h, cfg.rms_norm_eps, device)
+        self.gate_proj = _quantized(cfg.intermediate_size, h, cfg, device, gen)
+        self.up_proj = _quantized(cfg.intermediate_size, h, cfg, device, gen)
+        self.down_proj = _quantized(h, cfg.intermediate_size, cfg, device, gen)
+
+    def forward(self, x, cos, sin, positions, k_cache, v_cache, mask):
+        """x [T, H] fp16; positions [T] int64 (cache slots to write);
+        k_cache / v_cache [kv_heads, S, head_dim]; mask [T, S] additive fp32."""
+        cfg = self.cfg
+        t = x.shape[0]
+        h = self.input_norm(x)
+        q = self.q_proj(h).view(t, cfg.num_heads, cfg.head_dim)
+        k = self.k_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
+        v = self.v_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
+        q = _rope(q, cos, sin)
+        k = _rope(k, cos, sin)
+        k_cache.index_copy_(1, positions, k.transpose(0, 1).contiguous())
+        v_cache.index_copy_(1, positions, v.transpose(0, 1).contiguous())
+        group = cfg.num_heads // cfg.num_kv_heads
+        # attention in fp32 on contiguous operands
+        kf = k_cache.float().repeat_interleave(group, dim=0)            # [heads, S, d]
+        vf = v_cache.float().repeat_interleave(group, dim=0)
+        qf = q.float().transpose(0, 1).contiguous()                     # [heads, T, d]
+        scores = torch.matmul(qf, kf.transpose(1, 2).contiguous()) / math.sqrt(cfg.head_dim) + mask
+        attn = torch.matmul(torch.softmax(scores, dim=-1), vf)          # [heads, T, d]
+        attn = attn.transpose(0, 1).reshape(t, cfg.hidden_size).to(torch.float16)
+        x = x + self.o_proj(attn)
+        h = self.post_norm(x)
+        x = x + self.down_proj(F.silu(self.gate_proj(h)) * self.up_proj(h))
+        return x
+
+
+def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding, half-split convention; x [T, heads, d], cos/sin [T, d/2]."""
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half].float(), x[..., half:].float()
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+
+class LlamaDecoder(torch.nn.Module):
+    """Random-init Llama with INT4 linear layers, a static KV cache and greedy decode."""
+
+    def __init__(self, cfg: LlamaConfig, device: str | torch.device = "cuda", seed: int = 0) -> None:
+        super().__init__()
+        self.cfg = cfg
+        device = torch.device(device)
+        gen = torch.Generator(device=device).manual_seed(seed)
+        self.embed = torch.nn.Parameter(
+            (torch.randn((cfg.vocab_size, cfg.hidden_size), device=device, generator=gen) * cfg.init_std).to(
+                torch.float16
+            ),
+            requires_grad=False,
+        )
+        self.layers = torch.nn.ModuleList([Block(cfg, device, gen) for _ in range(cfg.num_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device)
+        self.lm_head = _quantized(cfg.vocab_size, cfg.hidden_size, cfg, device, gen)
+        inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, device=device).float() / cfg.head_dim))
+        angles = torch.outer(torch.arange(cfg.max_seq_len, device=device).float(), inv_freq)
+        self.register_buffer("cos", angles.cos(), persistent=False)
+        self.register_buffer("sin", angles.sin(), persistent=False)
+        shape = (cfg.num_layers, cfg.num_kv_heads, cfg.max_seq_len, cfg.head_dim)
+        self.register_buffer("k_cache", torch.zeros(shape, dtype=torch.float16, device=device), persistent=False)
+        self.register_buffer("v_cache", torch.zeros(shape, dtype=torch.float16, device=device), persistent=False)
+        self.slots = torch.arange(cfg.max_seq_len, device=device)
+        # static decode-step state (graph inputs/outputs)
+        self.token = torch.zeros((1,), dtype=torch.int64, device=device)
+        self.position = torch.zeros((1,), dtype=torch.int64, device=device)
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    def linear_layers(self) -> list[QuantizedLinear]:
+        return [m for m in self.modules() if isinstance(m, QuantizedLinear)]
+
+    def packed_bytes(self) -> int:
+        return sum(m.packed_weights.numel() + m.scales.numel() * 2 for m in self.linear_layers())
+
+    def _forward(self, tokens: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+        """tokens [T], positions [T] -> logits of the last position [vocab] fp16."""
+        x = self.embed[tokens]
+        cos, sin = self.cos[positions], self.sin[positions]
+        # additive mask: slot s visible to query t iff s <= positions[t]
+        mask = torch.where(self.slots.unsqueeze(0) <= positions.unsqueeze(1), 0.0, float("-inf"))
+        for i, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, positions, self.k_cache[i], self.v_cache[i], mask)
+        return self.lm_head(self.norm(x[-1:]))[0]
+
+    @torch.inference_mode()
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        """Run the prompt (int64 [T]); sets the next token and position; returns it."""
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+        positions = torch.arange(prompt.numel(), device=prompt.device)
+        logits = self._forward(prompt, positions)
+        self.token.copy_(torch.argmax(logits).view(1))
+        self.position.fill_(prompt.numel())
+        return self.token.clone()
+
+    def _step(self) -> None:
+        logits = self._forward(self.token, self.position)
+        self.token.copy_(torch.argmax(logits).view(1))
+        self.position.add_(1)
+
+    @torch.inference_mode()
+    def step(self) -> torch.Tensor:
+        """One eager decode step; returns the new token."""
+        self._step()
+        return self.token.clone()
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        """Record one decode step in a HIP graph (after a warm-up eager step
+        on a side stream so lazy initialisation is not captured). The KV cache
+        and position are restored afterwards."""
+        saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone())
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            self._step()
+        torch.cuda.current_stream().wait_stream(stream)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize()
+        self.k_cache.copy_(saved[0])
+        self.v_cache.copy_(saved[1])
+        self.token.copy_(saved[2])
+        self.position.copy_(saved[3])
+
+    def replay(self) -> None:
+        assert self.graph is not None, "call capture() first"
+        self.graph.replay()
+
+    @torch.inference_mode()
+    def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True) -> torch.Tensor:
+        """Greedy decode: prefill, then new_tokens - 1 decode steps."""
+        out = [self.prefill(prompt)]
+        for _ in range(new_tokens - 1):
+            if use_graph:
+                self.replay()
+                out.append(self.token.clone())
+            else:
+                out.append(self.step())
+        return torch.cat(out)

@@ -1,0 +1,159 @@
+"""Host-only checks of the C ABI (no GPU): the library loads, exports every
+symbol include/w4a16_hip.h declares, validates shapes with the reference's
+messages, and routes calls as the reference's dispatcher does
+(reference csrc/int4_linear_kernel.cu:641-802)."""
+
+from __future__ import annotations
+
+import os
+import re
+
+import pytest
+import torch
+
+from nibble_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "w4a16_hip.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(w4a16_\w+)\s*\(", text, re.M)))
+
+
+def test_header_symbols_exported():
+    names = declared_functions()
+    assert len(names) >= 8, names
+    lib = _lib.lib()
+    for name in names:
+        assert hasattr(lib, name), f"{name} not exported by libw4a16_hip.so"
+    assert set(names) == set(_lib.SIGNATURES), "ctypes binding out of sync with the header"
+
+
+def test_version():
+    assert b"gfx950" in _lib.lib().w4a16_version()
+
+
+@pytest.mark.parametrize(
+    "shape,code,message",
+    [
+        ((1, 256, 8, 128, 8, 2, 128), _lib.W4A16_OK, ""),
+        ((1, 256, 8, 128, 8, 2, 0), _lib.W4A16_ERR_GROUP_SIZE, "group_size must be greater than zero"),
+        ((1, 256, 8, 128, 8, 2, 7), _lib.W4A16_ERR_GROUP_SIZE, "group_size must be even"),
+        ((1, 256, 8, 64, 8, 2, 128), _lib.W4A16_ERR_SHAPE, "same K dimension"),
+        ((1, 200, 8, 100, 8, 2, 128), _lib.W4A16_ERR_SHAPE, "K must be divisible by group_size"),
+        ((1, 256, 8, 128, 8, 3, 128), _lib.W4A16_ERR_SHAPE, "scales must have shape [N, K / group_size]"),
+        ((1, 256, 8, 128, 7, 2, 128), _lib.W4A16_ERR_SHAPE, "scales must have shape [N, K / group_size]"),
+    ],
+)
+def test_check_linear_shapes(shape, code, message):
+    got, msg = _lib.check_linear_shapes(*shape)
+    assert got == code
+    assert message in msg
+
+
+def test_check_dequantize_shapes():
+    assert _lib.check_dequantize_shapes(8, 128, 8, 2, 128, 0)[0] == _lib.W4A16_OK
+    code, msg = _lib.check_dequantize_shapes(8, 48, 8, 2, 48, 0)
+    assert code == _lib.W4A16_ERR_GROUP_SIZE and "multiple of 32" in msg
+    code, msg = _lib.check_dequantize_shapes(8, 128, 8, 2, 128, 8)
+    assert code == _lib.W4A16_ERR_ALIGNMENT and "16-byte aligned" in msg
+    code, msg = _lib.check_dequantize_shapes(8, 128, 8, 4, 128, 0)
+    assert code == _lib.W4A16_ERR_SHAPE
+
+
+ALIGNED = 1 << 20
+
+
+@pytest.mark.parametrize(
+    "m,k,g,act,kernel",
+    [
+        (1, 2048, 128, ALIGNED, "valu"),       # decode
+        (4, 2048, 128, ALIGNED, "mfma"),       # small batch
+        (8, 2048, 128, ALIGNED, "mfma"),
+        (9, 2048, 128, ALIGNED, "generic"),    # above the small-batch range
+        (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128
+        (1, 2048, 128, ALIGNED + 2, "generic"),  # activations not 16-byte aligned
+        (0, 2048, 128, ALIGNED, "none"),       # empty
+    ],
+)
+def test_plan_routing(monkeypatch, m, k, g, act, kernel):
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    assert _lib.plan_linear(act, ALIGNED, m, 64, k, g)["kernel"] == kernel
+
+
+def test_plan_misaligned_weights_take_generic():
+    assert _lib.plan_linear(ALIGNED, ALIGNED + 8, 1, 64, 2048, 128)["kernel"] == "generic"
+
+
+def test_env_selectors(monkeypatch):
+    monkeypatch.setenv("W4A16_DECODE", "mfma")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma"
+    monkeypatch.setenv("W4A16_DECODE", "valu")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "valu"
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "4")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["rows"] == 4
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "3")
+    with pytest.raises(_lib.W4A16Error, match="W4A16_ROWS_PER_WARP must be 1, 2, or 4"):
+        _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")
+    monkeypatch.setenv("W4A16_DECODE", "v9")
+    with pytest.raises(_lib.W4A16Error, match="W4A16_DECODE"):
+        _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+
+
+def test_valu_falls_back_to_mfma_when_activations_exceed_lds(monkeypatch):
+    monkeypatch.setenv("W4A16_DECODE", "valu")
+    # M=8, K=14336 -> 229 KiB of activations, more than the 160 KiB of LDS
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 14336, 128)["kernel"] == "mfma"
+
+
+def test_scalar_argument_errors():
+    lib = _lib.lib()
+    assert lib.w4a16_linear_f16(None, None, None, None, 1, 8, 256, 0, None) == _lib.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_f16(None, None, None, None, 1, 8, 200, 128, None) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_linear_f16(None, None, None, None, 1, 8, 256, 128, None) == _lib.W4A16_ERR_NULL
+    # empty work: nothing to launch, NULL pointers allowed
+    assert lib.w4a16_linear_f16(None, None, None, None, 0, 8, 256, 128, None) == _lib.W4A16_OK
+    assert lib.w4a16_dequantize_f16(None, None, None, 8, 256, 48, None) == _lib.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 8, 256, 128, None,
+                                      _lib.KERNEL_VALU, 3, 1, 1, 0) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 8, 256, 64, None,
+                                      _lib.KERNEL_MFMA, 1, 1, 1, 0) == _lib.W4A16_ERR_CONFIG
+
+
+def test_torch_op_schemas_match_reference():
+    import nibble_amd  # noqa: F401  (registers the ops)
+
+    assert str(torch.ops.w4a16.linear.default._schema) == (
+        "w4a16::linear(Tensor activations, Tensor packed_weights, Tensor scales, int group_size) -> Tensor")
+    assert str(torch.ops.w4a16.dequantize.default._schema) == (
+        "w4a16::dequantize(Tensor packed_weights, Tensor scales, int group_size) -> Tensor")
+
+
+def test_torch_op_rejects_cpu_tensors():
+    import nibble_amd
+
+    assert nibble_amd.cuda_extension_available()
+    x = torch.zeros((1, 256), dtype=torch.float16)
+    p = torch.zeros((8, 128), dtype=torch.uint8)
+    s = torch.ones((8, 2), dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        nibble_amd.linear_cuda(x, p, s, 128)
+    with pytest.raises(RuntimeError):
+        nibble_amd.dequantize_cuda(p, s, 128)
+
+
+def test_fake_kernels_give_shapes():
+    import nibble_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty((3, 256), dtype=torch.float16, device="cuda")
+        p = torch.empty((8, 128), dtype=torch.uint8, device="cuda")
+        s = torch.empty((8, 2), dtype=torch.float16, device="cuda")
+        y = torch.ops.w4a16.linear(x, p, s, 128)
+        w = torch.ops.w4a16.dequantize(p, s, 128)
+    assert tuple(y.shape) == (3, 8) and y.dtype == torch.float16
+    assert tuple(w.shape) == (8, 256) and w.dtype == torch.float16

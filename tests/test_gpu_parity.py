@@ -14,15 +14,15 @@ from tests._cases import assert_parity, expected, make_case
 
 pytestmark = pytest.mark.gpu
 
-VALU, MFMA, GENERIC = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC
+VALU, MFMA, GENERIC, DIAG = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC, _lib.KERNEL_DIAG
 
 
-def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, group_size=128):
+def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
     xd, pd, sd = x.to(dev), packed.to(dev), scales.to(dev)
     out = torch.full((x.shape[0], packed.shape[0]), float("nan"), dtype=torch.float16, device=dev)
-    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} M={x.shape[0]} "
-          f"K={x.shape[1]} N={packed.shape[0]}", flush=True)
-    _lib.linear_f16_tuned(xd, pd, sd, out, group_size, kernel, rows, splits, unroll)
+    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} max_blocks={max_blocks} "
+          f"M={x.shape[0]} K={x.shape[1]} N={packed.shape[0]}", flush=True)
+    _lib.linear_f16_tuned(xd, pd, sd, out, group_size, kernel, rows, splits, unroll, max_blocks)
     torch.cuda.synchronize()
     return out
 
@@ -58,29 +58,66 @@ def test_small_batch_n7(gpu, m):
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m} N=7")
 
 
-@pytest.mark.parametrize("kernel", [VALU, MFMA])
-@pytest.mark.parametrize("rows", [1, 2, 4])
-@pytest.mark.parametrize("splits", [1, 3, 8])
-@pytest.mark.parametrize("unroll", [1, 2])
-@pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200)])
-def test_tuned_variants_m1(gpu, kernel, rows, splits, unroll, k, n):
+VALU_VARIANTS = [
+    (rows, waves, unroll, cap)
+    for rows in (1, 2, 4)
+    for waves in (1, 4)
+    for unroll in (1, 2, 4, 8)
+    for cap in (0, 3)
+    if not (rows == 4 and unroll == 8)
+]
+MFMA_VARIANTS = [(rows, splits, unroll, 0) for rows in (1, 2, 4) for splits in (1, 3, 8) for unroll in (1, 2, 4)]
+
+
+@pytest.mark.parametrize("rows,splits,unroll,cap", VALU_VARIANTS)
+@pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200), (14336, 40)])
+def test_valu_variants_m1(gpu, rows, splits, unroll, cap, k, n):
     x, p, s = make_case(1, k, n, seed=3)
-    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
-    assert_parity(out, expected(x, p, s), f"kernel={kernel} rows={rows} splits={splits} unroll={unroll}")
+    out = _run_tuned(gpu, x, p, s, VALU, rows, splits, unroll, cap)
+    assert_parity(out, expected(x, p, s), f"valu rows={rows} waves={splits} unroll={unroll} cap={cap}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, MFMA])
+DIAG_VARIANTS = [
+    (rows, waves, unroll, cap)
+    for rows in (1, 2, 4)
+    for waves in (1, 4)
+    for unroll in (1, 2, 4)
+    for cap in (0, 3)
+    if not (rows == 4 and unroll == 4)
+]
+
+
+@pytest.mark.parametrize("rows,splits,unroll,cap", DIAG_VARIANTS)
+@pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200), (14336, 40), (2048, 64)])
+def test_diag_variants_m1(gpu, rows, splits, unroll, cap, k, n):
+    x, p, s = make_case(1, k, n, seed=5)
+    out = _run_tuned(gpu, x, p, s, DIAG, rows, splits, unroll, cap)
+    assert_parity(out, expected(x, p, s), f"diag rows={rows} waves={splits} unroll={unroll} cap={cap}")
+
+
+@pytest.mark.parametrize("rows,splits,unroll,cap", MFMA_VARIANTS)
+@pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200)])
+def test_mfma_variants_m1(gpu, rows, splits, unroll, cap, k, n):
+    x, p, s = make_case(1, k, n, seed=3)
+    out = _run_tuned(gpu, x, p, s, MFMA, rows, splits, unroll, cap)
+    assert_parity(out, expected(x, p, s), f"mfma rows={rows} splits={splits} unroll={unroll}")
+
+
+@pytest.mark.parametrize("kernel,rows,splits,unroll,cap",
+                         [(VALU, 1, 1, 1, 0), (VALU, 2, 4, 2, 0), (VALU, 4, 2, 1, 5), (VALU, 2, 4, 8, 0),
+                          (MFMA, 1, 1, 1, 0), (MFMA, 2, 4, 2, 0), (MFMA, 4, 2, 1, 0)])
 @pytest.mark.parametrize("m", [1, 2, 5, 8])
-@pytest.mark.parametrize("rows,splits,unroll", [(1, 1, 1), (2, 4, 2), (4, 2, 1)])
-def test_tuned_variants_batch(gpu, kernel, m, rows, splits, unroll):
+def test_tuned_variants_batch(gpu, kernel, rows, splits, unroll, cap, m):
     x, p, s = make_case(m, 2048, 300, seed=m)
-    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
+    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
     assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, MFMA, GENERIC])
+@pytest.mark.parametrize("kernel", [VALU, MFMA, GENERIC, DIAG])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_all_nibble_values(gpu, kernel, m):
+    if kernel == DIAG and m != 1:
+        pytest.skip("the diagonal MFMA kernel is M = 1 only")
     # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
     x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
     out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
@@ -110,9 +147,10 @@ def test_misaligned_activations_take_generic(gpu):
     assert_parity(out, expected(x, p, s), "misaligned")
 
 
-@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (8192, 28672),
+                                 (28672, 8192)])
 @pytest.mark.parametrize("m", [1, 8])
-def test_large_8b_shapes(gpu, k, n, m):
+def test_large_shapes(gpu, k, n, m):
     x, p, s = make_case(m, k, n, seed=1, device="cuda")
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n}")
 
