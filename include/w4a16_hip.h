@@ -39,6 +39,7 @@ extern "C" {
 #define W4A16_KERNEL_MFMA 2          /* fp16 MFMA 16x16x32 tiles, M zero-padded to 16 (M <= 8) */
 #define W4A16_KERNEL_GENERIC 3       /* any M, any even group_size, any alignment */
 #define W4A16_KERNEL_DIAG 4          /* M = 1 on fp16 MFMA, group dots on the 16x16 diagonal */
+#define W4A16_KERNEL_VALU_OFFSET 5   /* VALU kernel, decode without f16 fix-ups, per-chunk offset correction */
 
 /*
  * Fused W4A16 linear layer.
@@ -48,7 +49,7 @@ extern "C" {
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
  * takes the tuned kernels; anything else takes the generic kernel.
- * Environment, read at every call: W4A16_DECODE = auto|valu|mfma selects the
+ * Environment, read at every call: W4A16_DECODE = auto|valu|valu_offset|mfma selects the
  * kernel family for M <= 8; W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per
  * wavefront of the VALU kernel (any other value is W4A16_ERR_CONFIG).
  */
@@ -103,6 +104,7 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     row (1|2|4|8; 8 needs rows <= 2), max_blocks = grid cap (0 = none).
  *   W4A16_KERNEL_MFMA: rows = 16-row blocks per wavefront (1|2|4),
  *     splits = wavefronts splitting K (1..8), unroll = groups in flight (1|2|4).
+ *   W4A16_KERNEL_VALU_OFFSET (M = 1 only): as W4A16_KERNEL_VALU.
  *   W4A16_KERNEL_DIAG (M = 1 only): rows = output rows per wavefront task
  *     (1|2|4), splits = wavefronts per workgroup (1..4), unroll = 1 KiB spans
  *     in flight per row (1|2|4; 4 needs rows <= 2), max_blocks = grid cap.

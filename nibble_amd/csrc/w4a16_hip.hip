@@ -62,8 +62,8 @@ struct Plan {
 };
 
 int valu_lds_bytes(int64_t M, int64_t K, const Plan& p) {
-    (void)p;
-    return (int)(M * K * 2);
+    const int64_t sums = p.kernel == W4A16_KERNEL_VALU_OFFSET ? M * (K / 32) * 8 : 0;
+    return (int)(M * K * 2 + sums);
 }
 int mfma_lds_bytes(const Plan& p) { return p.splits > 1 ? p.splits * p.rows * 64 * 16 : 0; }
 
@@ -75,8 +75,9 @@ int read_env(int* family, int* rows_per_wave) {
     if (d != nullptr && d[0] != '\0') {
         if (std::strcmp(d, "auto") == 0) *family = 0;
         else if (std::strcmp(d, "valu") == 0) *family = W4A16_KERNEL_VALU;
+        else if (std::strcmp(d, "valu_offset") == 0) *family = W4A16_KERNEL_VALU_OFFSET;
         else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
-        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, or mfma");
+        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, or mfma");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -112,15 +113,17 @@ Plan plan_valu(int64_t M, int64_t N, int64_t K, int rows) {
     return p;
 }
 
+// Launch shape of the MFMA kernel, from the M = 2..8 sweeps: one 16-row
+// block per wavefront and 8 wavefronts splitting K, except wide layers with
+// short rows (N >= 8192, K <= 4096), which take 2 blocks and 4 wavefronts.
 Plan plan_mfma(int64_t M, int64_t N, int64_t K) {
     Plan p;
     p.kernel = W4A16_KERNEL_MFMA;
-    p.rows = 2;
-    const int64_t groups = K / 128;
-    p.splits = clampi((int)(groups / 4), 1, 8);
-    p.unroll = 2;
+    const bool wide = N >= 8192 && K <= 4096;
+    p.rows = wide ? 2 : 1;
+    p.splits = wide ? 4 : 8;
+    p.unroll = 1;
     (void)M;
-    (void)N;
     return p;
 }
 
@@ -142,9 +145,14 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         *out = p;
         return W4A16_OK;
     }
-    if (family == 0) family = (M == 1) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
-    if (family == W4A16_KERNEL_VALU) {
+    // Measured crossover (M = 1..8 on the benchmark shapes): the VALU kernel
+    // wins while M dot2 passes per decoded word stay cheap (M <= 2, or M <= 4
+    // with K <= 8192); beyond that the MFMA kernel's cost does not grow with M.
+    if (family == 0) family = (M <= 2 || (M <= 4 && K <= 8192)) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
+    if (family == W4A16_KERNEL_VALU_OFFSET && M != 1) family = W4A16_KERNEL_VALU;
+    if (family == W4A16_KERNEL_VALU || family == W4A16_KERNEL_VALU_OFFSET) {
         Plan p = plan_valu(M, N, K, rows);
+        p.kernel = family;
         if (valu_lds_bytes(M, K, p) <= kMaxLdsBytes) {
             *out = p;
             return W4A16_OK;
@@ -155,13 +163,13 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     return W4A16_OK;
 }
 
-template <int M>
+template <int M, bool OFFSET>
 int launch_valu_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
                   w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
     void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
 #define W4A16_PICK(R, U) \
-    if (p.rows == R && p.unroll == U) kern = gemv_valu<M, R, U>;
+    if (p.rows == R && p.unroll == U) kern = gemv_valu<M, R, U, OFFSET>;
     W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4) W4A16_PICK(1, 8)
     W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4) W4A16_PICK(2, 8)
     W4A16_PICK(4, 1) W4A16_PICK(4, 2) W4A16_PICK(4, 4)
@@ -180,17 +188,20 @@ int launch_valu_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4
     return check_launch();
 }
 
+template <bool OFFSET>
 int launch_valu(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
                 w4a16::f16* o, int N, int K, hipStream_t stream) {
+    if (OFFSET && M != 1) return fail(W4A16_ERR_CONFIG, "the offset-decode VALU kernel is built for M == 1 only");
+    if (OFFSET) return launch_valu_m<1, true>(p, x, w, s, o, N, K, stream);
     switch (M) {
-        case 1: return launch_valu_m<1>(p, x, w, s, o, N, K, stream);
-        case 2: return launch_valu_m<2>(p, x, w, s, o, N, K, stream);
-        case 3: return launch_valu_m<3>(p, x, w, s, o, N, K, stream);
-        case 4: return launch_valu_m<4>(p, x, w, s, o, N, K, stream);
-        case 5: return launch_valu_m<5>(p, x, w, s, o, N, K, stream);
-        case 6: return launch_valu_m<6>(p, x, w, s, o, N, K, stream);
-        case 7: return launch_valu_m<7>(p, x, w, s, o, N, K, stream);
-        case 8: return launch_valu_m<8>(p, x, w, s, o, N, K, stream);
+        case 1: return launch_valu_m<1, false>(p, x, w, s, o, N, K, stream);
+        case 2: return launch_valu_m<2, false>(p, x, w, s, o, N, K, stream);
+        case 3: return launch_valu_m<3, false>(p, x, w, s, o, N, K, stream);
+        case 4: return launch_valu_m<4, false>(p, x, w, s, o, N, K, stream);
+        case 5: return launch_valu_m<5, false>(p, x, w, s, o, N, K, stream);
+        case 6: return launch_valu_m<6, false>(p, x, w, s, o, N, K, stream);
+        case 7: return launch_valu_m<7, false>(p, x, w, s, o, N, K, stream);
+        case 8: return launch_valu_m<8, false>(p, x, w, s, o, N, K, stream);
         default: return fail(W4A16_ERR_CONFIG, "VALU kernel needs 1 <= M <= 8");
     }
 }
@@ -227,11 +238,12 @@ int launch_mfma(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, con
     void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
 #define W4A16_PICK(RB, U) \
     if (p.rows == RB && p.unroll == U) kern = gemv_mfma<RB, U>;
-    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4)
-    W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4)
+    W4A16_PICK(1, 1) W4A16_PICK(1, 2) W4A16_PICK(1, 4) W4A16_PICK(1, 8)
+    W4A16_PICK(2, 1) W4A16_PICK(2, 2) W4A16_PICK(2, 4) W4A16_PICK(2, 8)
     W4A16_PICK(4, 1) W4A16_PICK(4, 2) W4A16_PICK(4, 4)
 #undef W4A16_PICK
-    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "MFMA kernel: rows must be 1, 2, or 4 and unroll 1, 2, or 4");
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, "MFMA kernel: rows 1, 2, or 4 and unroll 1, 2, 4, or 8 (8 needs rows <= 2)");
     if (M < 1 || M > 8) return fail(W4A16_ERR_CONFIG, "MFMA kernel needs 1 <= M <= 8");
     const int lds = mfma_lds_bytes(p);
     const int blocks = (N + 16 * p.rows - 1) / (16 * p.rows);
@@ -265,7 +277,8 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (p.kernel) {
         case W4A16_KERNEL_NONE: return W4A16_OK;
-        case W4A16_KERNEL_VALU: return launch_valu(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_VALU: return launch_valu<false>(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_VALU_OFFSET: return launch_valu<true>(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA: return launch_mfma(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_DIAG: return launch_diag(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
@@ -363,13 +376,14 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG) {
+    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
+        kernel == W4A16_KERNEL_VALU_OFFSET) {
         if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
-        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _MFMA, _DIAG or _GENERIC");
+        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _MFMA, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
 }

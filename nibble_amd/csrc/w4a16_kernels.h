@@ -40,8 +40,11 @@ namespace w4a16 {
 // unit-major: unit q (8 halves) of chunk c of row m goes to xs[(m*4 + q)*C + c].
 // Loads are issued in batches of 8 per thread before any is waited on, so the
 // whole copy costs about one L2 round trip instead of one per unit.
-template <int M>
-__device__ __forceinline__ void stage_activations(const f16* __restrict__ x, u32x4* xs, int K, int C) {
+// With SUMS, also store per chunk the fp32 sums of its even-k and odd-k
+// activations (float2 at sums[m*C + c]) for the offset decode.
+template <int M, bool SUMS>
+__device__ __forceinline__ void stage_activations(const f16* __restrict__ x, u32x4* xs, float2* sums, int K,
+                                                  int C) {
     constexpr int kBatch = 8;
     const int units_per_row = K >> 3;
     const int total = M * units_per_row;
@@ -56,10 +59,26 @@ __device__ __forceinline__ void stage_activations(const f16* __restrict__ x, u32
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
             const int i = base + j * T;
-            if (i < total) {
-                const int m = i / units_per_row;
-                const int u = i - m * units_per_row;
-                xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(a[j]);
+            const int m = M == 1 ? 0 : i / units_per_row;
+            const int u = i - m * units_per_row;
+            if (i < total) xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(a[j]);
+            if (SUMS) {
+                // even k = low halves, odd k = high halves of the 4 words
+                const f16x2 one = {(f16)1.0f, (f16)1.0f};
+                float ev = 0.0f, od = 0.0f;
+                if (i < total) {
+                    const f16x2 w0 = as_f16x2(a[j].x), w1 = as_f16x2(a[j].y), w2 = as_f16x2(a[j].z),
+                                w3 = as_f16x2(a[j].w);
+                    ev = ((float)w0.x + (float)w1.x) + ((float)w2.x + (float)w3.x);
+                    od = ((float)w0.y + (float)w1.y) + ((float)w2.y + (float)w3.y);
+                }
+                (void)one;
+                // the 4 units of a chunk sit in 4 consecutive lanes (T is a multiple of 64, base % 4 == tid % 4)
+                ev += dpp<0xB1>(ev);
+                od += dpp<0xB1>(od);
+                ev += dpp<0x4E>(ev);
+                od += dpp<0x4E>(od);
+                if (i < total && (u & 3) == 0) sums[m * C + (u >> 2)] = make_float2(ev, od);
             }
         }
     }
@@ -93,18 +112,36 @@ __device__ __forceinline__ void valu_load(ValuStep<M, R, U>& b, const uint8_t* _
     }
 }
 
-template <int M, int R, int U>
-__device__ __forceinline__ void valu_compute(const ValuStep<M, R, U>& b, const u32x4* xs, float (&acc)[R][M],
-                                             int step, int lane, int C) {
+// Decode without f16 fix-ups for the offset path: pairs (0,4) (2,6) as
+// 1024 + v and pairs (1,5) (3,7) as 1024 + 16 v, v = s + 8.
+__device__ __forceinline__ Codes8 unpack8_offset(uint32_t word) {
+    const uint32_t v = word >> 8;
+    Codes8 c;
+    c.p[0] = as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x000F000Fu, 0x64086408u, 0x6A));
+    c.p[1] = as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x00F000F0u, 0x64806480u, 0x6A));
+    c.p[2] = as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x000F000Fu, 0x64086408u, 0x6A));
+    c.p[3] = as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x00F000F0u, 0x64806480u, 0x6A));
+    return c;
+}
+
+// One step of U chunks per row. Exact path: unpack8 (codes exact in f16),
+// dot2 into one fp32 sum per chunk. Offset path (OFFSET): dot2 of the
+// un-fixed values into an even-k sum E = sum x (1024 + v) and an odd-k sum
+// O = sum x (1024 + 16 v); with v = s + 8 the chunk dot is
+//   E - 1032 * Sx_even + (O - 1152 * Sx_odd) / 16,
+// where Sx_even / Sx_odd are the chunk's activation sums staged in LDS.
+template <int M, int R, int U, bool OFFSET>
+__device__ __forceinline__ void valu_compute(const ValuStep<M, R, U>& b, const u32x4* xs, const float2* sums,
+                                             float (&acc)[R][M], int step, int lane, int C) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int c = (step * U + u) * 64 + lane;
         if (c < C) {
-            float d[R][M];
+            float d[R][M], e[R][M];
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int m = 0; m < M; ++m) d[r][m] = 0.0f;
+                for (int m = 0; m < M; ++m) d[r][m] = e[r][m] = 0.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 u32x4 xa[M];
@@ -112,21 +149,41 @@ __device__ __forceinline__ void valu_compute(const ValuStep<M, R, U>& b, const u
                 for (int m = 0; m < M; ++m) xa[m] = xs[(m * 4 + q) * C + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const Codes8 cw = unpack8(b.w[u][r][q]);
+                    const Codes8 cw = OFFSET ? unpack8_offset(b.w[u][r][q]) : unpack8(b.w[u][r][q]);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
-                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].x), cw.p[0], d[r][m], false);
-                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].y), cw.p[1], d[r][m], false);
-                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].z), cw.p[2], d[r][m], false);
-                        d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].w), cw.p[3], d[r][m], false);
+                        if (OFFSET) {
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].x), cw.p[0], d[r][m], false);
+                            e[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].y), cw.p[1], e[r][m], false);
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].z), cw.p[2], d[r][m], false);
+                            e[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].w), cw.p[3], e[r][m], false);
+                        } else {
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].x), cw.p[0], d[r][m], false);
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].y), cw.p[1], d[r][m], false);
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].z), cw.p[2], d[r][m], false);
+                            d[r][m] = __builtin_amdgcn_fdot2(as_f16x2(xa[m].w), cw.p[3], d[r][m], false);
+                        }
                     }
                 }
+            }
+            float2 sx[M];
+            if (OFFSET) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) sx[m] = sums[m * C + c];
             }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const float s = (float)b.s[u][r];
 #pragma unroll
-                for (int m = 0; m < M; ++m) acc[r][m] = __builtin_fmaf(d[r][m], s, acc[r][m]);
+                for (int m = 0; m < M; ++m) {
+                    float dot = d[r][m];
+                    if (OFFSET) {
+                        dot = __builtin_fmaf(-1032.0f, sx[m].x, dot);
+                        const float odd = __builtin_fmaf(-1152.0f, sx[m].y, e[r][m]);
+                        dot = __builtin_fmaf(odd, 0.0625f, dot);
+                    }
+                    acc[r][m] = __builtin_fmaf(dot, s, acc[r][m]);
+                }
             }
         }
     }
@@ -145,12 +202,13 @@ __device__ __forceinline__ void valu_finish(float (&acc)[R][M], f16* __restrict_
     }
 }
 
-template <int M, int R, int U>
+template <int M, int R, int U, bool OFFSET>
 __global__ void __launch_bounds__(256)
 gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
           const f16* __restrict__ scales, f16* __restrict__ out, int N, int K, int num_tasks) {
     extern __shared__ __align__(16) uint8_t smem[];
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
+    float2* sums = reinterpret_cast<float2*>(smem + (size_t)M * K * 2);   // OFFSET only
 
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -168,9 +226,14 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     ValuStep<M, R, U> buf0, buf1;
     // (task, step) of the unit in buf0; buf1 holds the one after it
     int task = task0, step = 0;
+    // The first two units' weights are requested before the activation
+    // staging, so the staging latency overlaps the weight stream.
+    int task1 = task, step1 = step + 1;
+    if (step1 == steps) { step1 = 0; task1 += task_stride; }
     if (units > 0) valu_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
+    if (units > 1) valu_load(buf1, w, scales, task1, step1, lane, N, C, G, row_bytes);
 
-    stage_activations<M>(x, xs, K, C);
+    stage_activations<M, OFFSET>(x, xs, sums, K, C);
     __syncthreads();
 
     float acc[R][M];
@@ -180,20 +243,22 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
     for (int u = 0; u < units; u += 2) {
-        // next unit -> buf1
-        int task1 = task, step1 = step + 1;
-        if (step1 == steps) { step1 = 0; task1 += task_stride; }
-        if (u + 1 < units) valu_load(buf1, w, scales, task1, step1, lane, N, C, G, row_bytes);
-        valu_compute(buf0, xs, acc, step, lane, C);
+        // buf0 holds unit u = (task, step), buf1 unit u+1 = (task1, step1)
+        valu_compute<M, R, U, OFFSET>(buf0, xs, sums, acc, step, lane, C);
         if (step == steps - 1) valu_finish(acc, out, task, lane, N);
         if (u + 1 >= units) break;
-        // unit after that -> buf0
+        // unit u+2 -> buf0
         task = task1;
         step = step1 + 1;
         if (step == steps) { step = 0; task += task_stride; }
         if (u + 2 < units) valu_load(buf0, w, scales, task, step, lane, N, C, G, row_bytes);
-        valu_compute(buf1, xs, acc, step1, lane, C);
+        valu_compute<M, R, U, OFFSET>(buf1, xs, sums, acc, step1, lane, C);
         if (step1 == steps - 1) valu_finish(acc, out, task1, lane, N);
+        // unit u+3 -> buf1
+        task1 = task;
+        step1 = step + 1;
+        if (step1 == steps) { step1 = 0; task1 += task_stride; }
+        if (u + 3 < units) valu_load(buf1, w, scales, task1, step1, lane, N, C, G, row_bytes);
     }
 }
 
@@ -203,16 +268,24 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 // A wavefront reads a row in 1 KiB spans (64 lanes x 16 bytes = 64 chunks =
 // 16 groups) like the VALU kernel, but lane l = 16q + j takes chunk 4j + q of
 // the span, so the four lanes j, 16+j, 32+j, 48+j hold the four chunks of
-// group j. With B = the lane's unpacked codes (column j = l%16, k-block q)
+// group j. With B = the lane's decoded codes (column j = l%16, k-block q)
 // and A = the matching activations (row i = l%16, same k-block), the four
 // v_mfma_f32_16x16x32_f16 of one span (one per 32-bit word of the chunk)
-// leave D[j][j] = sum over group j of x * code: the diagonal is the 16 group
-// dots, exactly accumulated in fp32 (off-diagonal entries are unused). Every
-// lane holds column j = l%16, so scaling all of D by the lane's group scale
-// scales the diagonal correctly. The decode costs 9 VALU operations per 8
-// weights and the products move to the matrix cores.
-// D[i][j] sits in lane 16(i/4) + j, register i%4: the diagonal is lane l's
-// register l%4 when (l%16)/4 == l/16.
+// leave D[j][j] = the dot product of group j: the diagonal holds the span's
+// 16 group dots (off-diagonal entries are unused). D[i][j] sits in lane
+// 16(i/4) + j, register i%4, so the diagonal is lane l's register l%4 when
+// (l%16)/4 == l/16.
+//
+// Decode without fix-ups: every nibble is placed one position up in the
+// mantissa of binary16 1024 (unpack8_x16), giving 1024 + 16 v exactly with
+// v = s + 8. Then sum x (1024 + 16 v) = 16 sum x s + 1152 sum x, and the
+// second term is removed by starting each row's MFMA chain from
+// -1152 sum x, computed once per span by four MFMAs against the constant
+// B = -1152 (exact in binary16) and shared by the R rows. D = 16 * dot then
+// takes the lane's group scale and a final exact 1/16. Products are exact
+// in fp32 and the sums accumulate in fp32; the offset costs at most the
+// rounding of an fp32 sum of magnitude ~1152 |sum x| per group.
+//
 // Activations are staged once per workgroup in LDS with chunk c of span s at
 // slot s*64 + 16(c%4) + (c%64)/4 (unit-major, zero padded to whole spans),
 // so lane l reads slot s*64 + l: conflict-free and already in A layout.
@@ -225,6 +298,17 @@ struct DiagStep {
 };
 
 __device__ __forceinline__ int diag_chunk(int lane) { return 4 * (lane & 15) + (lane >> 4); }
+
+// All eight nibbles of a word as 1024 + 16 v (v = nibble ^ 8), pair order
+// (0,4) (1,5) (2,6) (3,7) as in unpack8: 3 shifts + 4 v_bitop3, no f16 math.
+__device__ __forceinline__ u32x4 unpack8_x16(uint32_t word) {
+    u32x4 o;
+    o.x = __builtin_amdgcn_bitop3_b32(word << 4, 0x00F000F0u, 0x64806480u, 0x6A);
+    o.y = __builtin_amdgcn_bitop3_b32(word, 0x00F000F0u, 0x64806480u, 0x6A);
+    o.z = __builtin_amdgcn_bitop3_b32(word >> 4, 0x00F000F0u, 0x64806480u, 0x6A);
+    o.w = __builtin_amdgcn_bitop3_b32(word >> 8, 0x00F000F0u, 0x64806480u, 0x6A);
+    return o;
+}
 
 template <int R, int U>
 __device__ __forceinline__ void diag_load(DiagStep<R, U>& b, const uint8_t* __restrict__ w,
@@ -244,7 +328,7 @@ __device__ __forceinline__ void diag_load(DiagStep<R, U>& b, const uint8_t* __re
                 b.w[u][r] = load_stream(reinterpret_cast<const u32x4*>(wrow + c32 * 16u));
                 b.s[u][r] = *reinterpret_cast<const f16*>(srow + (c32 >> 2) * 2u);
             } else {
-                b.w[u][r] = (u32x4){0u, 0u, 0u, 0u};   // all codes 0
+                b.w[u][r] = (u32x4){0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};   // all codes 0
                 b.s[u][r] = (f16)0.0f;
             }
         }
@@ -254,6 +338,8 @@ __device__ __forceinline__ void diag_load(DiagStep<R, U>& b, const uint8_t* __re
 template <int R, int U>
 __device__ __forceinline__ void diag_compute(const DiagStep<R, U>& b, const u32x4* xs, f32x4 (&acc)[R],
                                              int step, int lane, int spans) {
+    const f16x8 neg_offset = {(f16)-1152.0f, (f16)-1152.0f, (f16)-1152.0f, (f16)-1152.0f,
+                              (f16)-1152.0f, (f16)-1152.0f, (f16)-1152.0f, (f16)-1152.0f};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int span = step * U + u;
@@ -261,17 +347,20 @@ __device__ __forceinline__ void diag_compute(const DiagStep<R, U>& b, const u32x
             f16x8 a[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) a[t] = __builtin_bit_cast(f16x8, xs[(t * spans + span) * 64 + lane]);
+            // -1152 * (sum of each group's activations) on the diagonal
+            f32x4 base = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) base = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], neg_offset, base, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+                f16x8 bt[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const Codes8 cw = unpack8(b.w[u][r][t]);
-                    const f16x8 bt = __builtin_bit_cast(
-                        f16x8, (u32x4){as_u32(cw.p[0]), as_u32(cw.p[1]), as_u32(cw.p[2]), as_u32(cw.p[3])});
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bt, d, 0, 0, 0);
-                }
-                acc[r] = d * (float)b.s[u][r] + acc[r];
+                for (int t = 0; t < 4; ++t) bt[t] = __builtin_bit_cast(f16x8, unpack8_x16(b.w[u][r][t]));
+                f32x4 d = base;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], bt[t], d, 0, 0, 0);
+                const float s = (float)b.s[u][r];
+                acc[r] = d * s + acc[r];
             }
         }
     }
@@ -284,13 +373,14 @@ __device__ __forceinline__ void diag_finish(f32x4 (&acc)[R], f16* __restrict__ o
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float d = e == 0 ? acc[r][0] : e == 1 ? acc[r][1] : e == 2 ? acc[r][2] : acc[r][3];
-        const float v = wave_sum(on_diag ? d : 0.0f);
+        const float v = wave_sum(on_diag ? d : 0.0f) * 0.0625f;   // D carried 16 x the dot
         acc[r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         if (lane == 0 && task * R + r < N) out[task * R + r] = (f16)v;
     }
 }
 
-// Activations into LDS in the diagonal-MFMA A layout (see above).
+// Activations into LDS in the diagonal-MFMA A layout (see above); padding
+// beyond K is zero, so padded chunks contribute nothing.
 __device__ __forceinline__ void stage_activations_diag(const f16* __restrict__ x, u32x4* xs, int K, int spans) {
     constexpr int kBatch = 8;
     const int units = K >> 3;            // real 16-byte units
@@ -379,8 +469,10 @@ gemv_diag(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 // 16x16 product is scaled by the per-lane (= per-column n) fp32 scale and
 // accumulated in fp32.
 // Wavefront = RB blocks of 16 rows sharing the A fragments; workgroup = S
-// wavefronts splitting the groups of K (wave w takes groups w, w+S, ...),
-// reduced through LDS at the end. Activation rows m >= M and rows past N
+// wavefronts splitting the groups of K (wave w takes groups w, w+S, ..., U
+// of them in flight per step, so the S wavefronts of a workgroup read
+// adjacent 64-byte pieces of each row at the same time), reduced through LDS
+// at the end. Activation rows m >= M and rows past N
 // follow the same path with zero A / clamped rows and are not stored.
 // ---------------------------------------------------------------------------
 template <int RB, int U>
@@ -389,7 +481,7 @@ gemv_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
           const f16* __restrict__ scales, f16* __restrict__ out, int M, int N, int K) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int S = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int col = lane & 15;      // n within a 16-row block; also activation row for A
     const int kq = lane >> 4;       // which 32-weight quarter of a group

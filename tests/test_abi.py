@@ -69,7 +69,10 @@ ALIGNED = 1 << 20
     "m,k,g,act,kernel",
     [
         (1, 2048, 128, ALIGNED, "valu"),       # decode
-        (4, 2048, 128, ALIGNED, "mfma"),       # small batch
+        (2, 2048, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
+        (4, 2048, 128, ALIGNED, "valu"),
+        (4, 14336, 128, ALIGNED, "mfma"),      # small batch, long rows -> MFMA
+        (5, 2048, 128, ALIGNED, "mfma"),
         (8, 2048, 128, ALIGNED, "mfma"),
         (9, 2048, 128, ALIGNED, "generic"),    # above the small-batch range
         (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128

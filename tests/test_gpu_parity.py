@@ -15,6 +15,7 @@ from tests._cases import assert_parity, expected, make_case
 pytestmark = pytest.mark.gpu
 
 VALU, MFMA, GENERIC, DIAG = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC, _lib.KERNEL_DIAG
+VOFF = _lib.KERNEL_VALU_OFFSET
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -66,14 +67,16 @@ VALU_VARIANTS = [
     for cap in (0, 3)
     if not (rows == 4 and unroll == 8)
 ]
-MFMA_VARIANTS = [(rows, splits, unroll, 0) for rows in (1, 2, 4) for splits in (1, 3, 8) for unroll in (1, 2, 4)]
+MFMA_VARIANTS = [(rows, splits, unroll, 0) for rows in (1, 2, 4) for splits in (1, 3, 8) for unroll in (1, 2, 4, 8)
+                 if not (rows == 4 and unroll == 8)]
 
 
+@pytest.mark.parametrize("kernel", [VALU, VOFF])
 @pytest.mark.parametrize("rows,splits,unroll,cap", VALU_VARIANTS)
 @pytest.mark.parametrize("k,n", [(256, 7), (1024, 13), (5632, 200), (14336, 40)])
-def test_valu_variants_m1(gpu, rows, splits, unroll, cap, k, n):
+def test_valu_variants_m1(gpu, kernel, rows, splits, unroll, cap, k, n):
     x, p, s = make_case(1, k, n, seed=3)
-    out = _run_tuned(gpu, x, p, s, VALU, rows, splits, unroll, cap)
+    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
     assert_parity(out, expected(x, p, s), f"valu rows={rows} waves={splits} unroll={unroll} cap={cap}")
 
 
@@ -105,23 +108,56 @@ def test_mfma_variants_m1(gpu, rows, splits, unroll, cap, k, n):
 
 @pytest.mark.parametrize("kernel,rows,splits,unroll,cap",
                          [(VALU, 1, 1, 1, 0), (VALU, 2, 4, 2, 0), (VALU, 4, 2, 1, 5), (VALU, 2, 4, 8, 0),
+                          (VOFF, 1, 1, 1, 0), (VOFF, 2, 4, 2, 0), (VOFF, 4, 2, 1, 5), (VOFF, 2, 4, 8, 0),
                           (MFMA, 1, 1, 1, 0), (MFMA, 2, 4, 2, 0), (MFMA, 4, 2, 1, 0)])
 @pytest.mark.parametrize("m", [1, 2, 5, 8])
 def test_tuned_variants_batch(gpu, kernel, rows, splits, unroll, cap, m):
     x, p, s = make_case(m, 2048, 300, seed=m)
+    if kernel == VOFF and m != 1:
+        with pytest.raises(_lib.W4A16Error, match="M == 1 only"):
+            _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
+        return
     out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
     assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, MFMA, GENERIC, DIAG])
+@pytest.mark.parametrize("kernel", [VALU, VOFF, MFMA, GENERIC, DIAG])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_all_nibble_values(gpu, kernel, m):
-    if kernel == DIAG and m != 1:
-        pytest.skip("the diagonal MFMA kernel is M = 1 only")
+    if kernel in (DIAG, VOFF) and m != 1:
+        pytest.skip("the diagonal MFMA and offset-decode VALU kernels are M = 1 only")
     # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
     x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
     out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
     assert_parity(out, expected(x, p, s), f"all nibbles kernel={kernel} M={m}")
+
+
+def _stress_activations(kind: str, m: int, k: int) -> torch.Tensor:
+    gen = torch.Generator().manual_seed(17)
+    if kind == "constant":        # every group sum large and one-signed
+        return torch.full((m, k), 60.0).to(torch.float16)
+    if kind == "outliers":        # N(0,1) with 1% channels at +-300
+        x = torch.randn((m, k), generator=gen)
+        idx = torch.randperm(k, generator=gen)[: k // 100]
+        x[:, idx] = 300.0 * torch.sign(torch.randn((m, idx.numel()), generator=gen))
+        return x.to(torch.float16)
+    if kind == "cancel":          # +c then -c within each group: sum x per group = 0, sum |x| large
+        x = torch.full((m, k), 40.0)
+        x[:, 1::2] = -40.0
+        return x.to(torch.float16)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kernel,rows,splits,unroll", [(VALU, 2, 4, 1), (VOFF, 2, 4, 1), (VOFF, 1, 4, 8),
+                                                       (DIAG, 2, 4, 1), (DIAG, 1, 4, 2),
+                                                       (MFMA, 2, 4, 1), (GENERIC, 1, 1, 1)])
+@pytest.mark.parametrize("kind", ["constant", "outliers", "cancel"])
+def test_precision_stress(gpu, kernel, rows, splits, unroll, kind):
+    m = 1 if kernel in (DIAG, VOFF) else 4
+    _, p, s = make_case(m, 4096, 96, seed=21)
+    x = _stress_activations(kind, m, 4096)
+    out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"stress {kind} kernel={kernel}")
 
 
 @pytest.mark.parametrize("m", [1, 3, 9, 16])
