@@ -40,7 +40,16 @@ HBM_PEAK_GBPS = 8000.0
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
 # reads half the bytes on this part, WRITE_SIZE is exact).
-MEASURED_TRAFFIC_BYTES = 6154349
+MEASURED_TRAFFIC_BYTES = 6071434
+
+
+def _kernel_name(plan: dict) -> str:
+    """Template instance the C ABI launches for a plan (w4a16_kernels.h)."""
+    if plan["kernel"] == "oneshot":
+        return f"w4a16::gemv_oneshot<1,{plan['rows']},{plan['unroll']},{plan['splits']}>"
+    if plan["kernel"] == "valu":
+        return f"w4a16::gemv_valu<1,{plan['rows']},{plan['unroll']},false>"
+    return f"w4a16 {plan['kernel']} kernel"
 
 
 def payload_bytes(m: int, n: int, k: int, group: int = 128) -> int:
@@ -277,7 +286,7 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBPS, 4),
         "traffic": MEASURED_TRAFFIC_BYTES,
-        "kernel": "w4a16::gemv_valu<1,2,*> (M=1 VALU GEMV)",
+        "kernel": " + ".join(_kernel_name(r["kernel"]) for r in layer_rows.values()),
         "bytes_per_launch": step_bytes // 2,
         "us_per_launch": round(elapsed / args.steps / 2 * 1e6, 3),
     }

@@ -40,6 +40,7 @@ extern "C" {
 #define W4A16_KERNEL_GENERIC 3       /* any M, any even group_size, any alignment */
 #define W4A16_KERNEL_DIAG 4          /* M = 1 on fp16 MFMA, group dots on the 16x16 diagonal */
 #define W4A16_KERNEL_VALU_OFFSET 5   /* VALU kernel, decode without f16 fix-ups, per-chunk offset correction */
+#define W4A16_KERNEL_ONESHOT 6       /* VALU GEMV, every weight of a wavefront's rows requested at once (M <= 4) */
 
 /*
  * Fused W4A16 linear layer.
@@ -108,6 +109,10 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *   W4A16_KERNEL_DIAG (M = 1 only): rows = output rows per wavefront task
  *     (1|2|4), splits = wavefronts per workgroup (1..4), unroll = 1 KiB spans
  *     in flight per row (1|2|4; 4 needs rows <= 2), max_blocks = grid cap.
+ *   W4A16_KERNEL_ONESHOT (M <= 4): rows = output rows per wavefront (1|2),
+ *     splits = wavefronts per workgroup (4|8), unroll = 1 KiB loads per row
+ *     per lane (0 = the smallest that covers K; else >= ceil(K / 2048) and
+ *     one of 1..8, 10, 12, 14, 16), max_blocks ignored.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 and 16-byte aligned
  * activations and weights. No reference counterpart (the reference's

@@ -31,8 +31,10 @@ KERNEL_MFMA = 2
 KERNEL_GENERIC = 3
 KERNEL_DIAG = 4
 KERNEL_VALU_OFFSET = 5
+KERNEL_ONESHOT = 6
 KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic",
-                KERNEL_DIAG: "diag", KERNEL_VALU_OFFSET: "valu_offset"}
+                KERNEL_DIAG: "diag", KERNEL_VALU_OFFSET: "valu_offset",
+                KERNEL_ONESHOT: "oneshot"}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

@@ -57,7 +57,7 @@ struct Plan {
     int kernel = W4A16_KERNEL_NONE;
     int rows = 0;        // VALU: output rows per wavefront task; MFMA: 16-row blocks per wavefront
     int splits = 0;      // VALU: wavefronts per workgroup; MFMA: wavefronts splitting K
-    int unroll = 0;      // chunks (VALU) or groups (MFMA) in flight per row per step
+    int unroll = 0;      // chunks (VALU) or groups (MFMA) in flight per row per step; one-shot: loads per row
     int max_blocks = 0;  // VALU: grid cap (0 = one task per wavefront)
 };
 
@@ -77,7 +77,8 @@ int read_env(int* family, int* rows_per_wave) {
         else if (std::strcmp(d, "valu") == 0) *family = W4A16_KERNEL_VALU;
         else if (std::strcmp(d, "valu_offset") == 0) *family = W4A16_KERNEL_VALU_OFFSET;
         else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
-        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, or mfma");
+        else if (std::strcmp(d, "oneshot") == 0) *family = W4A16_KERNEL_ONESHOT;
+        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, oneshot, or mfma");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -88,8 +89,6 @@ int read_env(int* family, int* rows_per_wave) {
     }
     return W4A16_OK;
 }
-
-int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // Launch shape of the VALU kernel, from the sweeps over the benchmark shapes
 // (K 2048..28672, N 2048..28672): 2 rows per wavefront task, 4 wavefronts
@@ -127,6 +126,39 @@ Plan plan_mfma(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
+// Instantiated loads-per-row values of the one-shot kernel; a row of C
+// chunks runs on the smallest L with 64 L >= C.
+constexpr int kOneshotLoads[] = {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 14, 16};
+
+int oneshot_loads(int64_t K) {
+    const int64_t need = (K / 32 + 63) / 64;
+    for (int l : kOneshotLoads)
+        if (l >= need) return l;
+    return 0;  // row too long for the one-shot kernel
+}
+
+// Launch shape of the one-shot kernel, from the M = 1..4 sweeps over the
+// benchmark shapes: at M = 1, two rows per wavefront and 4 wavefronts per
+// workgroup when a row is 2, 4 or >= 12 loads (K 4096, 8192, 28672), else
+// one row and 8 wavefronts; M >= 2 always one row and 8 wavefronts (more
+// rows per workgroup share each staged copy of the activations).
+Plan plan_oneshot(int64_t M, int64_t K, int rows) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_ONESHOT;
+    p.unroll = oneshot_loads(K);
+    const bool pair = M == 1 && (p.unroll == 2 || p.unroll == 4 || p.unroll >= 12);
+    if (rows > 0)
+        p.rows = rows >= 2 ? 2 : 1;   // W4A16_ROWS_PER_WARP=4 runs as 2 rows in this kernel
+    else
+        p.rows = pair ? 2 : 1;
+    p.splits = pair ? 4 : 8;
+    return p;
+}
+
+bool oneshot_fits(int64_t M, int64_t K) {
+    return M >= 1 && M <= 4 && oneshot_loads(K) > 0 && M * K * 2 <= kMaxLdsBytes;
+}
+
 int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
     int family = 0, rows = 0;
     const int rc = read_env(&family, &rows);
@@ -148,8 +180,26 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // Measured crossover (M = 1..8 on the benchmark shapes): the VALU kernel
     // wins while M dot2 passes per decoded word stay cheap (M <= 2, or M <= 4
     // with K <= 8192); beyond that the MFMA kernel's cost does not grow with M.
-    if (family == 0) family = (M <= 2 || (M <= 4 && K <= 8192)) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
+    // An explicit W4A16_ROWS_PER_WARP (an A/B switch, as in the reference)
+    // keeps auto on the looped VALU kernel whose rows it sets.
+    // One-shot: every M = 1 row that fits; for M = 2..4 only small layers
+    // (K, N <= 5632), because each workgroup re-stages M*K activations, which
+    // on large layers outweighs the weights it streams.
+    if (family == 0) {
+        const bool small = K <= 5632 && N <= 5632;
+        if (rows == 0 && oneshot_fits(M, K) && (M == 1 || small))
+            family = W4A16_KERNEL_ONESHOT;
+        else
+            family = (M <= 2 || (M <= 4 && K <= 8192)) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
+    }
     if (family == W4A16_KERNEL_VALU_OFFSET && M != 1) family = W4A16_KERNEL_VALU;
+    if (family == W4A16_KERNEL_ONESHOT) {
+        if (oneshot_fits(M, K)) {
+            *out = plan_oneshot(M, K, rows);
+            return W4A16_OK;
+        }
+        family = M <= 8 ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;   // rows too long or M > 4
+    }
     if (family == W4A16_KERNEL_VALU || family == W4A16_KERNEL_VALU_OFFSET) {
         Plan p = plan_valu(M, N, K, rows);
         p.kernel = family;
@@ -203,6 +253,49 @@ int launch_valu(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, con
         case 7: return launch_valu_m<7, false>(p, x, w, s, o, N, K, stream);
         case 8: return launch_valu_m<8, false>(p, x, w, s, o, N, K, stream);
         default: return fail(W4A16_ERR_CONFIG, "VALU kernel needs 1 <= M <= 8");
+    }
+}
+
+template <int M>
+int launch_oneshot_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                     w4a16::f16* o, int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int) = nullptr;
+#define W4A16_PICK_L(R, L, W) \
+    if (p.rows == R && p.unroll == L && p.splits == W) kern = gemv_oneshot<M, R, L, W>;
+#define W4A16_PICK(R, W)                                                                                  \
+    W4A16_PICK_L(R, 1, W) W4A16_PICK_L(R, 2, W) W4A16_PICK_L(R, 3, W) W4A16_PICK_L(R, 4, W)             \
+    W4A16_PICK_L(R, 5, W) W4A16_PICK_L(R, 6, W) W4A16_PICK_L(R, 7, W) W4A16_PICK_L(R, 8, W)             \
+    W4A16_PICK_L(R, 10, W) W4A16_PICK_L(R, 12, W) W4A16_PICK_L(R, 14, W) W4A16_PICK_L(R, 16, W)
+    W4A16_PICK(1, 4) W4A16_PICK(1, 8) W4A16_PICK(2, 4) W4A16_PICK(2, 8)
+#undef W4A16_PICK
+#undef W4A16_PICK_L
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG,
+                    "one-shot kernel: rows 1 or 2, splits 4 or 8, unroll one of 1..8, 10, 12, 14, 16");
+    const int lds = M * K * 2;
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "one-shot kernel: M*K activations do not fit in LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int waves = (N + p.rows - 1) / p.rows;
+    const int blocks = (waves + p.splits - 1) / p.splits;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K);
+    return check_launch();
+}
+
+int launch_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s, w4a16::f16* o,
+                   int N, int K, hipStream_t stream) {
+    const int need = oneshot_loads(K);
+    if (need == 0) return fail(W4A16_ERR_CONFIG, "one-shot kernel: K exceeds 16 loads of 1 KiB per row (K > 32768)");
+    if (p.unroll == 0) p.unroll = need;
+    if (p.unroll < (K / 32 + 63) / 64)
+        return fail(W4A16_ERR_CONFIG, "one-shot kernel: unroll (loads per row) too small for K");
+    switch (M) {
+        case 1: return launch_oneshot_m<1>(p, x, w, s, o, N, K, stream);
+        case 2: return launch_oneshot_m<2>(p, x, w, s, o, N, K, stream);
+        case 3: return launch_oneshot_m<3>(p, x, w, s, o, N, K, stream);
+        case 4: return launch_oneshot_m<4>(p, x, w, s, o, N, K, stream);
+        default: return fail(W4A16_ERR_CONFIG, "one-shot kernel needs 1 <= M <= 4");
     }
 }
 
@@ -281,6 +374,7 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_VALU_OFFSET: return launch_valu<true>(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA: return launch_mfma(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_DIAG: return launch_diag(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_ONESHOT: return launch_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -377,13 +471,14 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.unroll = unroll;
     p.max_blocks = max_blocks;
     if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
-        kernel == W4A16_KERNEL_VALU_OFFSET) {
+        kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT) {
         if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
-        return fail(W4A16_ERR_CONFIG, "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _MFMA, _DIAG or _GENERIC");
+        return fail(W4A16_ERR_CONFIG,
+                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
 }

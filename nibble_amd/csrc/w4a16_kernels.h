@@ -263,6 +263,143 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------
+// One-shot VALU GEMV (M = 1..4 activation rows, template), G = 128.
+//
+// Every wavefront owns R consecutive output rows and requests ALL of their
+// weights at once: a row is L = ceil(C / 64) loads of 1 KiB (lane l takes
+// chunks l, l + 64, ...; lanes past C idle on the last one), so a wavefront
+// has R * L loads in flight and the whole matrix is requested within the
+// first few hundred cycles of the launch. There is no loop and no second
+// round of tasks: the grid has ceil(N / R) wavefronts.
+//
+// Order of requests, which matters because a wavefront's loads return in
+// issue order: first the workgroup's share of the activations (contiguous
+// 16-byte units, so they come back first), then the scales, then the
+// weights. The activations are permuted to the unpack8 pair order and
+// written to LDS unit-major (unit q of chunk c of row m at
+// xs[(m*4 + q) * C + c], conflict-free for lanes reading consecutive
+// chunks); after one barrier each wavefront consumes its weights in the
+// order they arrive. Decode and arithmetic are those of gemv_valu (exact
+// codes, v_dot2_f32_f16 per chunk, fp32 scale per chunk, DPP row sum).
+// ---------------------------------------------------------------------------
+template <int M, int R, int L, int W>
+__global__ void __launch_bounds__(64 * W)
+gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+             const f16* __restrict__ scales, f16* __restrict__ out, int N, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);
+    const int C = K >> 5;
+    const int G = K >> 7;
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * W + wave) * R;
+
+    // 1. activations: units i = m * 4C + u, u = 4c + q. Up to kFirst units
+    // per thread are requested ahead of the weights; any rest (large M * K)
+    // is copied after them. Every request is unconditional (indices past
+    // the end are clamped to the last element and their data is dropped):
+    // branches around loads would make the compiler wait for all
+    // outstanding loads at each join.
+    constexpr int T = 64 * W;
+    constexpr int kPer = (M * 4 * 64 * L + T - 1) / T;
+    constexpr int kFirst = kPer < 8 ? kPer : 8;
+    const int units = M * 4 * C;
+    const int units_per_row = 4 * C;
+    u32x4 a[kFirst];
+#pragma unroll
+    for (int p = 0; p < kFirst; ++p) {
+        const int i = min((int)threadIdx.x + p * T, units - 1);
+        a[p] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
+    }
+
+    // 2. scales and weights of this wavefront's rows (rows past N re-read
+    // N-1 and are not stored; chunks past C re-read chunk C-1 and are not used)
+    uint32_t sv[R][L];   // fp16 bits, one per register (no packing, no early wait)
+    u32x4 wv[R][L];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(row0 + r, N - 1);
+        const uint16_t* srow = reinterpret_cast<const uint16_t*>(scales) + (size_t)n * G;
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const int c = min(j * 64 + lane, C - 1);
+            sv[r][j] = srow[c >> 2];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(row0 + r, N - 1);
+        const uint8_t* wrow = w + (size_t)n * row_bytes;   // wavefront-uniform
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const uint32_t c = (uint32_t)min(j * 64 + lane, C - 1);
+            wv[r][j] = load_stream(reinterpret_cast<const u32x4*>(wrow + c * 16u));
+        }
+    }
+    // keep every request above ahead of the first wait below
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. activations into LDS
+#pragma unroll
+    for (int p = 0; p < kFirst; ++p) {
+        const int i = threadIdx.x + p * T;
+        if (i < units) {
+            const int m = M == 1 ? 0 : i / units_per_row;
+            const int u = i - m * units_per_row;
+            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(a[p]);
+        }
+    }
+    if (kPer > kFirst) {
+        for (int i = threadIdx.x + kFirst * T; i < units; i += T) {
+            const int m = M == 1 ? 0 : i / units_per_row;
+            const int u = i - m * units_per_row;
+            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(*reinterpret_cast<const u32x4*>(x + (size_t)i * 8));
+        }
+    }
+    __syncthreads();
+    if (row0 >= N) return;
+
+    // 4. dot products, row by row in arrival order. Straight-line code (no
+    // branch per chunk, so each chunk waits only for its own load): lanes
+    // past C compute on the clamped chunk and select 0.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+            const int c = j * 64 + lane;
+            const int cc = min(c, C - 1);
+            float d[M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) d[m] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const Codes8 cw = unpack8(wv[r][j][q]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const u32x4 xv = xs[(m * 4 + q) * C + cc];
+                    d[m] = __builtin_amdgcn_fdot2(as_f16x2(xv.x), cw.p[0], d[m], false);
+                    d[m] = __builtin_amdgcn_fdot2(as_f16x2(xv.y), cw.p[1], d[m], false);
+                    d[m] = __builtin_amdgcn_fdot2(as_f16x2(xv.z), cw.p[2], d[m], false);
+                    d[m] = __builtin_amdgcn_fdot2(as_f16x2(xv.w), cw.p[3], d[m], false);
+                }
+            }
+            const float s = (float)__builtin_bit_cast(f16, (uint16_t)sv[r][j]);
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[m] = __builtin_fmaf(c < C ? d[m] : 0.0f, s, acc[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float v = wave_sum(acc[m]);
+            if (lane == 0 && row0 + r < N) out[(size_t)m * N + row0 + r] = (f16)v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // M = 1 GEMV on the matrix cores ("diagonal MFMA"), G = 128.
 //
 // A wavefront reads a row in 1 KiB spans (64 lanes x 16 bytes = 64 chunks =

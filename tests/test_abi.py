@@ -68,9 +68,12 @@ ALIGNED = 1 << 20
 @pytest.mark.parametrize(
     "m,k,g,act,kernel",
     [
-        (1, 2048, 128, ALIGNED, "valu"),       # decode
-        (2, 2048, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
-        (4, 2048, 128, ALIGNED, "valu"),
+        (1, 2048, 128, ALIGNED, "oneshot"),    # decode
+        (1, 32768, 128, ALIGNED, "oneshot"),   # 16 loads of 1 KiB per row
+        (1, 34816, 128, ALIGNED, "valu"),      # rows too long for the one-shot kernel
+        (2, 2048, 128, ALIGNED, "oneshot"),    # small batch on a small layer
+        (4, 2048, 128, ALIGNED, "oneshot"),
+        (2, 8192, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
         (4, 14336, 128, ALIGNED, "mfma"),      # small batch, long rows -> MFMA
         (5, 2048, 128, ALIGNED, "mfma"),
         (8, 2048, 128, ALIGNED, "mfma"),
@@ -88,6 +91,24 @@ def test_plan_routing(monkeypatch, m, k, g, act, kernel):
 
 def test_plan_misaligned_weights_take_generic():
     assert _lib.plan_linear(ALIGNED, ALIGNED + 8, 1, 64, 2048, 128)["kernel"] == "generic"
+
+
+def test_oneshot_plan_shapes(monkeypatch):
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    # (K, rows, waves per workgroup, loads per row)
+    for k, rows, splits, loads in [(2048, 1, 8, 1), (4096, 2, 4, 2), (5632, 1, 8, 3), (8192, 2, 4, 4),
+                                   (14336, 1, 8, 7), (18432, 1, 8, 10), (28672, 2, 4, 14), (32768, 2, 4, 16),
+                                   (256, 1, 8, 1)]:
+        plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
+        assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "valu"      # M > 1, large N
+    monkeypatch.setenv("W4A16_DECODE", "oneshot")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "oneshot"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 5, 64, 2048, 128)["kernel"] == "valu"     # M > 4
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 32768, 128)["kernel"] == "mfma"    # no LDS room: MFMA
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "4")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["rows"] == 2
 
 
 def test_env_selectors(monkeypatch):

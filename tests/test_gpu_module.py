@@ -34,7 +34,7 @@ def test_op_matches_oracle(gpu, m, k, n):
     assert_parity(out, expected(x, p, s), f"op M={m} K={k} N={n}")
 
 
-@pytest.mark.parametrize("decode", ["auto", "valu", "mfma"])
+@pytest.mark.parametrize("decode", ["auto", "valu", "oneshot", "mfma"])
 @pytest.mark.parametrize("rows_per_warp", ["1", "2", "4"])
 def test_env_selected_kernels(gpu, monkeypatch, decode, rows_per_warp):
     monkeypatch.setenv("W4A16_DECODE", decode)

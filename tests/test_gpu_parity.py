@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 
 VALU, MFMA, GENERIC, DIAG = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC, _lib.KERNEL_DIAG
 VOFF = _lib.KERNEL_VALU_OFFSET
+ONESHOT = _lib.KERNEL_ONESHOT
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -106,8 +107,48 @@ def test_mfma_variants_m1(gpu, rows, splits, unroll, cap, k, n):
     assert_parity(out, expected(x, p, s), f"mfma rows={rows} splits={splits} unroll={unroll}")
 
 
+# K values: one partial load (256), whole loads (2048, 32768 = 16 loads), a
+# ragged last load (5632: 176 chunks), 7 loads (14336) and 9 chunks-of-64
+# rounded up to the 10-load instantiation (18432).
+@pytest.mark.parametrize("rows,splits", [(1, 4), (2, 4), (1, 8), (2, 8)])
+@pytest.mark.parametrize("k,n", [(256, 7), (2048, 13), (5632, 40), (14336, 21), (18432, 9), (32768, 5)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_oneshot_variants(gpu, m, rows, splits, k, n):
+    x, p, s = make_case(m, k, n, seed=m * 31 + k + n)
+    if m * k * 2 > 160 * 1024:
+        with pytest.raises(_lib.W4A16Error, match="do not fit in LDS"):
+            _run_tuned(gpu, x, p, s, ONESHOT, rows, splits, 0)
+        return
+    out = _run_tuned(gpu, x, p, s, ONESHOT, rows, splits, 0)
+    assert_parity(out, expected(x, p, s), f"oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
+
+
+@pytest.mark.parametrize("unroll", [2, 4, 8, 16])
+def test_oneshot_more_loads_than_needed(gpu, unroll):
+    # lanes past the row's last chunk idle on every extra load
+    x, p, s = make_case(1, 1024, 33, seed=unroll)
+    out = _run_tuned(gpu, x, p, s, ONESHOT, 1, 4, unroll)
+    assert_parity(out, expected(x, p, s), f"oneshot unroll={unroll}")
+
+
+def test_oneshot_rejects_short_unroll_and_long_rows(gpu):
+    x, p, s = make_case(1, 4096, 8, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="too small"):
+        _run_tuned(gpu, x, p, s, ONESHOT, 1, 4, 1)
+    with pytest.raises(_lib.W4A16Error, match="rows 1 or 2"):
+        _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
+    x, p, s = make_case(1, 34816, 3, seed=4)
+    with pytest.raises(_lib.W4A16Error, match="K > 32768"):
+        _run_tuned(gpu, x, p, s, ONESHOT, 1, 8, 0)
+    # the default plan falls back to the looped VALU kernel for such rows
+    plan = _lib.plan_linear(16, 16, 1, 3, 34816)
+    assert plan["kernel"] == "valu"
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), "M=1 K=34816 default")
+
+
 @pytest.mark.parametrize("kernel,rows,splits,unroll,cap",
-                         [(VALU, 1, 1, 1, 0), (VALU, 2, 4, 2, 0), (VALU, 4, 2, 1, 5), (VALU, 2, 4, 8, 0),
+                         [(ONESHOT, 1, 4, 0, 0), (ONESHOT, 2, 8, 0, 0),
+                          (VALU, 1, 1, 1, 0), (VALU, 2, 4, 2, 0), (VALU, 4, 2, 1, 5), (VALU, 2, 4, 8, 0),
                           (VOFF, 1, 1, 1, 0), (VOFF, 2, 4, 2, 0), (VOFF, 4, 2, 1, 5), (VOFF, 2, 4, 8, 0),
                           (MFMA, 1, 1, 1, 0), (MFMA, 2, 4, 2, 0), (MFMA, 4, 2, 1, 0)])
 @pytest.mark.parametrize("m", [1, 2, 5, 8])
@@ -117,18 +158,27 @@ def test_tuned_variants_batch(gpu, kernel, rows, splits, unroll, cap, m):
         with pytest.raises(_lib.W4A16Error, match="M == 1 only"):
             _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
         return
+    if kernel == ONESHOT and m > 4:
+        with pytest.raises(_lib.W4A16Error, match="1 <= M <= 4"):
+            _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
+        return
     out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, cap)
     assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, VOFF, MFMA, GENERIC, DIAG])
+@pytest.mark.parametrize("kernel", [VALU, VOFF, ONESHOT, MFMA, GENERIC, DIAG])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_all_nibble_values(gpu, kernel, m):
     if kernel in (DIAG, VOFF) and m != 1:
         pytest.skip("the diagonal MFMA and offset-decode VALU kernels are M = 1 only")
+    if kernel == ONESHOT and m > 4:
+        pytest.skip("the one-shot kernel is built for M <= 4")
     # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
     x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
-    out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
+    if kernel == ONESHOT:
+        out = _run_tuned(gpu, x, p, s, kernel, 2, 4, 0)
+    else:
+        out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
     assert_parity(out, expected(x, p, s), f"all nibbles kernel={kernel} M={m}")
 
 
@@ -149,6 +199,7 @@ def _stress_activations(kind: str, m: int, k: int) -> torch.Tensor:
 
 
 @pytest.mark.parametrize("kernel,rows,splits,unroll", [(VALU, 2, 4, 1), (VOFF, 2, 4, 1), (VOFF, 1, 4, 8),
+                                                       (ONESHOT, 2, 4, 0), (ONESHOT, 1, 8, 0),
                                                        (DIAG, 2, 4, 1), (DIAG, 1, 4, 2),
                                                        (MFMA, 2, 4, 1), (GENERIC, 1, 1, 1)])
 @pytest.mark.parametrize("kind", ["constant", "outliers", "cancel"])
