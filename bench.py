@@ -160,7 +160,9 @@ def cpu_baseline(shapes, budget_s: float = 12.0) -> dict:
 
 
 def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 16) -> dict:
-    """greedy decode on the random-init 1.1B Llama, decode step in a HIP graph."""
+    """greedy decode on the random-init 1.1B Llama, decode step in a
+    HIP graph: the fused step (5 launches per layer) and, on the same weights,
+    the step as separate torch ops around QuantizedLinear."""
     import torch
 
     from nibble_amd.llama import LlamaConfig, LlamaDecoder
@@ -169,27 +171,37 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     model = LlamaDecoder(cfg, device=device, seed=0)
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=gen).to(device)
-    model.prefill(prompt)
-    model.capture()
-    decode_s, prefill_s = [], []
-    for _ in range(runs + 1):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
+
+    def timed(fused: bool):
+        model.fused = fused
         model.prefill(prompt)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(new_tokens - 1):
-            model.replay()
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        prefill_s.append(t1 - t0)
-        decode_s.append(t2 - t1)
-    decode_s, prefill_s = sorted(decode_s[1:]), sorted(prefill_s[1:])
-    med = decode_s[len(decode_s) // 2]
+        model.capture()
+        decode_s, prefill_s = [], []
+        for _ in range(runs + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            model.prefill(prompt)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(new_tokens - 1):
+                model.replay()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            prefill_s.append(t1 - t0)
+            decode_s.append(t2 - t1)
+        decode_s, prefill_s = sorted(decode_s[1:]), sorted(prefill_s[1:])
+        return decode_s[len(decode_s) // 2], prefill_s[len(prefill_s) // 2]
+
+    unfused_s, _ = timed(False)
+    med, prefill = timed(True)
     return {
         "decode_tok_s": round((new_tokens - 1) / med, 1),
         "ms_per_token": round(med / (new_tokens - 1) * 1e3, 3),
-        "prefill_ms": round(prefill_s[len(prefill_s) // 2] * 1e3, 3),
+        "weight_GBps": round(model.packed_bytes() * (new_tokens - 1) / med / 1e9, 1),
+        "step": "fused: RMSNorm+qkv GEMV, rotary+KV append+attention, o GEMV+residual, "
+                "RMSNorm+gate|up GEMV+SiLU*up, down GEMV+residual per layer; RMSNorm+lm_head GEMV, argmax",
+        "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
+        "prefill_ms": round(prefill * 1e3, 3),
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),
         "model": "random-init Llama 22L h2048 i5632 32q/4kv hd64 vocab32000, INT4 g128 on all 155 linears",

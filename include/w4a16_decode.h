@@ -1,0 +1,88 @@
+/*
+ * W4A16 decode-step extensions for gfx950 (MI355X): the fused GEMV variants
+ * and the small kernels that, together with the W4A16 linear layer, run one
+ * greedy-decode step of a Llama-architecture model in 5 launches per layer.
+ *
+ * Reference interfaces they replace (chris320211/Nibble): the reference runs
+ * its end-to-end decode (scripts/generate.py:260-305, HF generate with a
+ * static cache under CUDA graphs) through Hugging Face's Llama modules, whose
+ * RMSNorm, rotary embedding, attention, SiLU-gated MLP, residual adds and
+ * argmax are separate eager kernels around its w4a16::linear calls
+ * (w4a16/linear.py:154-200). These entry points fuse those operations into
+ * the GEMV's prologue / epilogue or into one kernel each; they have no
+ * one-to-one counterpart in the reference's C++ (csrc/ holds only the
+ * linear and dequantize ops).
+ *
+ * Conventions are those of w4a16_hip.h: device pointers, a hipStream_t
+ * passed as void*, W4A16_OK or a W4A16_ERR_* code whose message
+ * w4a16_last_error returns, nothing allocated or synchronised
+ * (graph-capturable).
+ */
+#ifndef W4A16_DECODE_H
+#define W4A16_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * One activation row (M = 1) through an INT4 linear layer with the decode
+ * step's neighbouring element-wise work fused in:
+ *   norm_weight != NULL: RMSNorm the row first (fp32 mean of squares,
+ *     x * rsqrt(mean + eps) * norm_weight, rounded to fp16);
+ *   paired == 0: output[n] = fp16(W[n] . x') (+ residual[n] in fp16 when
+ *     residual != NULL; residual may alias output);
+ *   paired != 0: W is [gate; up] with N rows (N even) and
+ *     output[i] = fp16(silu(fp16(W[i] . x')) * fp16(W[i + N/2] . x')),
+ *     i < N/2 (residual must be NULL).
+ * Needs group_size 128, K a multiple of 128 up to 16384, and 16-byte aligned
+ * activations, norm_weight and packed_weights.
+ * Replaces (reference): Llama RMSNorm + q/k/v or gate/up QuantizedLinear
+ * calls (w4a16/linear.py:154-200) + act_fn(gate) * up + residual add.
+ */
+int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float eps,
+                         const uint8_t* packed_weights, const void* scales,
+                         const void* residual, void* output, int64_t N, int64_t K,
+                         int64_t group_size, int paired, void* stream);
+
+/*
+ * Attention of one new token at position *position (device int64):
+ * qkv = [q (num_heads x 64) | k (num_kv_heads x 64) | v (num_kv_heads x 64)]
+ * fp16; rotary embedding (half-split, cos / sin tables [max_seq_len, 32]
+ * fp32) on q and k; k and v appended to the caches [num_kv_heads,
+ * max_seq_len, 64] fp16 at the position; output [num_heads x 64] fp16 =
+ * softmax(q k^T / 8) v over cache slots 0..position. head_dim must be 64.
+ * A position outside [0, max_seq_len) writes NaN and leaves the caches alone.
+ * Replaces (reference): HF LlamaAttention's rotary embedding, static-cache
+ * update and sdpa call in the decode loop of scripts/generate.py:260-305.
+ */
+int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache,
+                               const float* cos_table, const float* sin_table,
+                               const int64_t* position, void* output,
+                               int64_t num_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t max_seq_len, void* stream);
+
+/*
+ * Greedy token: *token = first index of the maximum of logits[0..n) (fp16);
+ * if position != NULL, *position += 1.
+ * Replaces (reference): the greedy pick of HF generate(do_sample=False),
+ * scripts/generate.py:286-293.
+ */
+int w4a16_argmax_f16(const void* logits, int64_t n, int64_t* token, int64_t* position,
+                     void* stream);
+
+/*
+ * output[0..hidden) = table[*token, :] (fp16 [vocab, hidden]); a token
+ * outside [0, vocab) gives zeros.
+ * Replaces (reference): the embedding lookup of the decode step.
+ */
+int w4a16_embedding_f16(const void* table, int64_t vocab, int64_t hidden,
+                        const int64_t* token, void* output, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16_DECODE_H */

@@ -55,6 +55,17 @@ SIGNATURES = {
     "w4a16_version": (ctypes.c_char_p, []),
 }
 
+# every symbol declared in include/w4a16_decode.h
+DECODE_SIGNATURES = {
+    "w4a16_gemv_fused_f16": (
+        ctypes.c_int,
+        [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp],
+    ),
+    "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
+    "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
+    "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+}
+
 _lib = None
 
 
@@ -73,7 +84,7 @@ def lib() -> ctypes.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
             )
         handle = ctypes.CDLL(LIB_PATH)
-        for name, (restype, argtypes) in SIGNATURES.items():
+        for name, (restype, argtypes) in {**SIGNATURES, **DECODE_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = restype
             fn.argtypes = argtypes
@@ -152,3 +163,48 @@ def check_dequantize_shapes(packed_rows, packed_cols, scale_rows, scale_cols, gr
     code = lib().w4a16_check_dequantize_shapes(packed_rows, packed_cols, scale_rows, scale_cols, group_size,
                                                address)
     return code, (last_error() if code else "")
+
+
+# ---------------------------------------------------------------- decode step --
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def gemv_fused_f16(activations, packed_weights, scales, output, norm_weight=None, eps: float = 1e-5,
+                   residual=None, paired: bool = False, group_size: int = 128, stream=None) -> None:
+    """``w4a16_gemv_fused_f16``: one activation row (1-D or [1, K] fp16) through
+    an INT4 layer with optional RMSNorm prologue, residual add, or paired
+    [gate; up] SiLU-multiply epilogue."""
+    k = activations.shape[-1]
+    n = packed_weights.shape[0]
+    _raise_on(
+        lib().w4a16_gemv_fused_f16(
+            activations.data_ptr(), _ptr(norm_weight), float(eps), packed_weights.data_ptr(), scales.data_ptr(),
+            _ptr(residual), output.data_ptr(), n, k, group_size, int(bool(paired)), _stream_ptr(stream),
+        )
+    )
+
+
+def decode_attention_f16(qkv, k_cache, v_cache, cos_table, sin_table, position, output, num_heads: int,
+                         num_kv_heads: int, head_dim: int = 64, stream=None) -> None:
+    """``w4a16_decode_attention_f16`` on one layer's caches [kv_heads, S, head_dim]."""
+    _raise_on(
+        lib().w4a16_decode_attention_f16(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+            position.data_ptr(), output.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2],
+            _stream_ptr(stream),
+        )
+    )
+
+
+def argmax_f16(logits, token, position=None, stream=None) -> None:
+    """``w4a16_argmax_f16``: token <- argmax(logits); position += 1 when given."""
+    _raise_on(lib().w4a16_argmax_f16(logits.data_ptr(), logits.numel(), token.data_ptr(), _ptr(position),
+                                     _stream_ptr(stream)))
+
+
+def embedding_f16(table, token, output, stream=None) -> None:
+    """``w4a16_embedding_f16``: output <- table[token]."""
+    vocab, hidden = table.shape
+    _raise_on(lib().w4a16_embedding_f16(table.data_ptr(), vocab, hidden, token.data_ptr(), output.data_ptr(),
+                                        _stream_ptr(stream)))

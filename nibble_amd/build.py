@@ -46,10 +46,36 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(lines), flush=True)
 
 
+HIP_SOURCES = ["w4a16_hip.hip", "w4a16_decode.hip"]
+
+
 def build_hip(verbose: bool = False) -> str:
+    """Compile every HIP source to an object (in parallel), then link the library."""
     out = os.path.join(HERE, "libw4a16_hip.so")
-    src = os.path.join(CSRC, "w4a16_hip.hip")
-    _run([os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, f"-I{INCLUDE}", "-o", out, src], verbose)
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs, procs = [], []
+    for name in HIP_SOURCES:
+        obj = os.path.join(CSRC, os.path.splitext(name)[0] + ".o")
+        cmd = [hipcc, *compile_flags, f"-I{INCLUDE}", "-c", "-o", obj, os.path.join(CSRC, name)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    failed = None
+    for cmd, proc in procs:
+        text = proc.communicate()[0]
+        lines = [ln for ln in text.splitlines() if "packed-fp32-ops" not in ln]
+        if proc.returncode != 0:
+            sys.stderr.write("\n".join(lines) + "\n")
+            failed = failed or f"build step failed ({proc.returncode}): {cmd[-1]}"
+        elif verbose and lines:
+            print("\n".join(lines), flush=True)
+    if failed:
+        raise RuntimeError(failed)
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out, *objs], verbose)
+    for obj in objs:
+        os.remove(obj)
     return out
 
 

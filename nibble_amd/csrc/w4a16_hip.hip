@@ -3,6 +3,7 @@
 // memory or synchronises, so every entry point can run under HIP graph
 // capture.
 #include "w4a16_hip.h"
+#include "w4a16_decode.h"
 
 #include <hip/hip_runtime.h>
 
@@ -260,9 +261,9 @@ template <int M>
 int launch_oneshot_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
                      w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
-    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int) = nullptr;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, GemvFusion) = nullptr;
 #define W4A16_PICK_L(R, L, W) \
-    if (p.rows == R && p.unroll == L && p.splits == W) kern = gemv_oneshot<M, R, L, W>;
+    if (p.rows == R && p.unroll == L && p.splits == W) kern = gemv_oneshot<M, R, L, W, false, false>;
 #define W4A16_PICK(R, W)                                                                                  \
     W4A16_PICK_L(R, 1, W) W4A16_PICK_L(R, 2, W) W4A16_PICK_L(R, 3, W) W4A16_PICK_L(R, 4, W)             \
     W4A16_PICK_L(R, 5, W) W4A16_PICK_L(R, 6, W) W4A16_PICK_L(R, 7, W) W4A16_PICK_L(R, 8, W)             \
@@ -279,7 +280,7 @@ int launch_oneshot_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const
     if (rc != W4A16_OK) return rc;
     const int waves = (N + p.rows - 1) / p.rows;
     const int blocks = (waves + p.splits - 1) / p.splits;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K, GemvFusion{});
     return check_launch();
 }
 
@@ -297,6 +298,38 @@ int launch_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w
         case 4: return launch_oneshot_m<4>(p, x, w, s, o, N, K, stream);
         default: return fail(W4A16_ERR_CONFIG, "one-shot kernel needs 1 <= M <= 4");
     }
+}
+
+// Fused M = 1 variants (RMSNorm prologue / residual / paired SiLU epilogue).
+// Rows of up to 8 loads (K <= 16384); launch shape: paired rows need R = 2
+// (4 wavefronts per workgroup), the others take the one-shot plan.
+template <bool NORM, bool PAIRED>
+int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* norm_w, float eps,
+                   const uint8_t* w, const w4a16::f16* s, const w4a16::f16* resid, w4a16::f16* o, int N, int K,
+                   hipStream_t stream) {
+    using namespace w4a16;
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, GemvFusion) = nullptr;
+#define W4A16_PICK_L(RR, LL, WW) \
+    if (R == RR && L == LL && W == WW) kern = gemv_oneshot<1, RR, LL, WW, NORM, PAIRED>;
+#define W4A16_PICK(RR, WW)                                                                               \
+    W4A16_PICK_L(RR, 1, WW) W4A16_PICK_L(RR, 2, WW) W4A16_PICK_L(RR, 3, WW) W4A16_PICK_L(RR, 4, WW)   \
+    W4A16_PICK_L(RR, 5, WW) W4A16_PICK_L(RR, 6, WW) W4A16_PICK_L(RR, 7, WW) W4A16_PICK_L(RR, 8, WW)
+    if constexpr (PAIRED) {
+        W4A16_PICK(2, 4)
+    } else {
+        W4A16_PICK(1, 8) W4A16_PICK(2, 4)
+    }
+#undef W4A16_PICK
+#undef W4A16_PICK_L
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "fused GEMV: no kernel for this launch shape");
+    const int lds = K * 2 + 64;   // activations + per-wavefront partial sums of squares
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int tasks = PAIRED ? N / 2 : (N + R - 1) / R;
+    const int blocks = (tasks + W - 1) / W;
+    GemvFusion fz{norm_w, eps, resid};
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * W), lds, stream, x, w, s, o, N, K, fz);
+    return check_launch();
 }
 
 int launch_diag(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
@@ -391,6 +424,10 @@ int check_pointers(const void* act, const void* packed, const void* scales, cons
 
 }  // namespace
 
+namespace w4a16_internal {
+void set_last_error(const std::string& message) { g_last_error = message; }
+}  // namespace w4a16_internal
+
 extern "C" {
 
 const char* w4a16_last_error(void) { return g_last_error.c_str(); }
@@ -481,6 +518,45 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
+}
+
+int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float eps,
+                         const uint8_t* packed_weights, const void* scales, const void* residual, void* output,
+                         int64_t N, int64_t K, int64_t group_size, int paired, void* stream) {
+    int rc = check_scalar_args(1, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    if (group_size != 128) return fail(W4A16_ERR_GROUP_SIZE, "fused GEMV needs group_size 128");
+    if (K == 0 || K > 16384) return fail(W4A16_ERR_SHAPE, "fused GEMV needs 0 < K <= 16384");
+    if (paired && (N % 2 != 0)) return fail(W4A16_ERR_SHAPE, "paired fused GEMV needs an even number of rows");
+    if (paired && residual != nullptr) return fail(W4A16_ERR_CONFIG, "paired fused GEMV takes no residual");
+    if (N == 0) return W4A16_OK;
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    if (!aligned16(activations) || !aligned16(packed_weights) || (norm_weight && !aligned16(norm_weight)))
+        return fail(W4A16_ERR_ALIGNMENT, "fused GEMV needs 16-byte aligned activations, norm_weight and weights");
+    if (residual && (reinterpret_cast<uintptr_t>(residual) & 1u))
+        return fail(W4A16_ERR_ALIGNMENT, "residual must be 2-byte aligned");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "eps must be non-negative");
+    using w4a16::f16;
+    const int L = oneshot_loads(K);
+    int R = 2, W = 4;
+    if (!paired) {
+        const Plan p = plan_oneshot(1, K, 0);
+        R = p.rows;
+        W = p.splits;
+    }
+    const f16* x = static_cast<const f16*>(activations);
+    const f16* nw = static_cast<const f16*>(norm_weight);
+    const f16* sc = static_cast<const f16*>(scales);
+    const f16* res = static_cast<const f16*>(residual);
+    f16* o = static_cast<f16*>(output);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int n = (int)N, k = (int)K;
+    if (paired)
+        return nw ? launch_fused_t<true, true>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st)
+                  : launch_fused_t<false, true>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st);
+    return nw ? launch_fused_t<true, false>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st)
+              : launch_fused_t<false, false>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st);
 }
 
 int w4a16_dequantize_f16(const uint8_t* packed_weights, const void* scales, void* output, int64_t N,

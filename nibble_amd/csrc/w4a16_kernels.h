@@ -265,12 +265,12 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 // ---------------------------------------------------------------------------
 // One-shot VALU GEMV (M = 1..4 activation rows, template), G = 128.
 //
-// Every wavefront owns R consecutive output rows and requests ALL of their
-// weights at once: a row is L = ceil(C / 64) loads of 1 KiB (lane l takes
-// chunks l, l + 64, ...; lanes past C idle on the last one), so a wavefront
-// has R * L loads in flight and the whole matrix is requested within the
-// first few hundred cycles of the launch. There is no loop and no second
-// round of tasks: the grid has ceil(N / R) wavefronts.
+// Every wavefront owns R output rows and requests ALL of their weights at
+// once: a row is L = ceil(C / 64) loads of 1 KiB (lane l takes chunks l,
+// l + 64, ...; lanes past C re-read the row's last chunk and drop it), so a
+// wavefront has R * L loads in flight and the whole matrix is requested
+// within the first few hundred cycles of the launch. There is no loop and no
+// second round of tasks: the grid has ceil(N / R) wavefronts.
 //
 // Order of requests, which matters because a wavefront's loads return in
 // issue order: first the workgroup's share of the activations (contiguous
@@ -281,11 +281,31 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 // chunks); after one barrier each wavefront consumes its weights in the
 // order they arrive. Decode and arithmetic are those of gemv_valu (exact
 // codes, v_dot2_f32_f16 per chunk, fp32 scale per chunk, DPP row sum).
+//
+// Fused decode-step variants (M = 1 only; the plain op passes an empty
+// GemvFusion and NORM = PAIRED = false):
+//   NORM (norm_weight): the activation row is RMS-normalised while it is staged,
+//     y = fp16((fp32(x) * rsqrt(mean(x^2) + eps)) * fp32(norm_weight)),
+//     the fp32 operation order of an RMSNorm that returns fp16;
+//   residual: out[n] = fp16(fp32(residual[n]) + fp32(fp16(dot))), the fp16
+//     "x + linear(a)" of a residual stream (residual may alias out: each
+//     row is read and written by the same lane);
+//   PAIRED (R = 2): wavefront i owns rows i and i + N/2 of a [gate; up]
+//     weight pair and stores out[i] = fp16(silu(g) * u) with g, u, silu(g)
+//     each rounded to fp16 first, as fp16 tensors would be.
 // ---------------------------------------------------------------------------
-template <int M, int R, int L, int W>
+struct GemvFusion {
+    const f16* norm_weight;   // nullptr: no RMSNorm prologue
+    float eps;
+    const f16* residual;      // nullptr: no residual add
+};
+
+template <int M, int R, int L, int W, bool NORM, bool PAIRED>
 __global__ void __launch_bounds__(64 * W)
 gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
-             const f16* __restrict__ scales, f16* __restrict__ out, int N, int K) {
+             const f16* __restrict__ scales, f16* out, int N, int K, GemvFusion fz) {
+    static_assert(!PAIRED || (M == 1 && R == 2), "paired rows are an M = 1, R = 2 layout");
+    static_assert(!NORM || M == 1, "the RMSNorm prologue normalises one activation row");
     extern __shared__ __align__(16) uint8_t smem[];
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
     const int C = K >> 5;
@@ -293,7 +313,12 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     const uint32_t row_bytes = (uint32_t)(K >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * W + wave) * R;
+    const int task = blockIdx.x * W + wave;
+    // row r of this wavefront, and the number of valid tasks
+    const int half = N >> 1;
+    const int row0 = PAIRED ? task : task * R;
+    const int row_step = PAIRED ? half : 1;
+    const bool valid = PAIRED ? task < half : row0 < N;
 
     // 1. activations: units i = m * 4C + u, u = 4c + q. Up to kFirst units
     // per thread are requested ahead of the weights; any rest (large M * K)
@@ -306,11 +331,20 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     constexpr int kFirst = kPer < 8 ? kPer : 8;
     const int units = M * 4 * C;
     const int units_per_row = 4 * C;
+    static_assert(!NORM || kPer == kFirst, "the RMSNorm prologue holds the whole row in registers");
     u32x4 a[kFirst];
+    u32x4 nw[NORM ? kFirst : 1];
 #pragma unroll
     for (int p = 0; p < kFirst; ++p) {
         const int i = min((int)threadIdx.x + p * T, units - 1);
         a[p] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
+    }
+    if (NORM) {
+#pragma unroll
+        for (int p = 0; p < kFirst; ++p) {
+            const int i = min((int)threadIdx.x + p * T, units - 1);
+            nw[p] = *reinterpret_cast<const u32x4*>(fz.norm_weight + (size_t)i * 8);
+        }
     }
 
     // 2. scales and weights of this wavefront's rows (rows past N re-read
@@ -319,7 +353,7 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     u32x4 wv[R][L];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int n = min(row0 + r, N - 1);
+        const int n = min(row0 + r * row_step, N - 1);
         const uint16_t* srow = reinterpret_cast<const uint16_t*>(scales) + (size_t)n * G;
 #pragma unroll
         for (int j = 0; j < L; ++j) {
@@ -329,7 +363,7 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int n = min(row0 + r, N - 1);
+        const int n = min(row0 + r * row_step, N - 1);
         const uint8_t* wrow = w + (size_t)n * row_bytes;   // wavefront-uniform
 #pragma unroll
         for (int j = 0; j < L; ++j) {
@@ -340,7 +374,40 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     // keep every request above ahead of the first wait below
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. activations into LDS
+    // 3. activations into LDS (RMS-normalised first when asked)
+    if (NORM) {
+        float* partial = reinterpret_cast<float*>(smem + (size_t)M * K * 2);   // W floats after xs
+        float ss = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kFirst; ++p) {
+            const int i = threadIdx.x + p * T;
+            if (i < units) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f16x2 h = as_f16x2(a[p][e]);
+                    ss = __builtin_fmaf((float)h.x, (float)h.x, ss);
+                    ss = __builtin_fmaf((float)h.y, (float)h.y, ss);
+                }
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) partial[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int v = 0; v < W; ++v) total += partial[v];
+        const float inv = 1.0f / __builtin_sqrtf(total / (float)K + fz.eps);
+#pragma unroll
+        for (int p = 0; p < kFirst; ++p) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 h = as_f16x2(a[p][e]);
+                const f16x2 g = as_f16x2(nw[NORM ? p : 0][e]);
+                const f16x2 y = {(f16)(((float)h.x * inv) * (float)g.x), (f16)(((float)h.y * inv) * (float)g.y)};
+                a[p][e] = as_u32(y);
+            }
+        }
+    }
 #pragma unroll
     for (int p = 0; p < kFirst; ++p) {
         const int i = threadIdx.x + p * T;
@@ -358,11 +425,12 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         }
     }
     __syncthreads();
-    if (row0 >= N) return;
+    if (!valid) return;
 
     // 4. dot products, row by row in arrival order. Straight-line code (no
     // branch per chunk, so each chunk waits only for its own load): lanes
     // past C compute on the clamped chunk and select 0.
+    float rowsum[R][M];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float acc[M];
@@ -393,9 +461,20 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const float v = wave_sum(acc[m]);
-            if (lane == 0 && row0 + r < N) out[(size_t)m * N + row0 + r] = (f16)v;
+            rowsum[r][m] = wave_sum(acc[m]);
+            if (!PAIRED && lane == 0 && row0 + r < N) {
+                const int n = row0 + r;
+                f16 v = (f16)rowsum[r][m];
+                if (fz.residual != nullptr) v = (f16)((float)fz.residual[n] + (float)v);
+                out[(size_t)m * N + n] = v;
+            }
         }
+    }
+    if (PAIRED && lane == 0) {
+        const float g = (float)(f16)rowsum[0][0];
+        const float u = (float)(f16)rowsum[R - 1][0];
+        const float act = (float)(f16)(g / (1.0f + expf(-g)));
+        out[task] = (f16)(act * u);
     }
 }
 

@@ -10,8 +10,18 @@ dim 64, vocab 32000, RMSNorm, rotary position embedding, SiLU-gated MLP.
 All 155 linear layers (q, k, v, o, gate, up, down per layer, and lm_head)
 hold INT4 group-128 weights quantized from N(0, 0.02).
 
-Decode (one token, M = 1) runs the fused HIP GEMV for every linear layer;
-prefill (M = prompt length > 8) runs the HIP dequantize kernel + hipBLASLt.
+Decode (one token, M = 1) runs the fused step of ``include/w4a16_decode.h``
+by default: per layer, (1) RMSNorm + q|k|v GEMV over the concatenated
+projection, (2) rotary embedding + KV-cache append + attention, (3) o GEMV +
+residual, (4) RMSNorm + gate|up GEMV with the SiLU-multiply epilogue, (5)
+down GEMV + residual; then RMSNorm + lm_head GEMV and the greedy argmax,
+which also advances the position: 5 launches per layer. The q/k/v and
+gate/up weights live in one buffer each, and every ``QuantizedLinear`` keeps
+a contiguous view of its rows, so state-dict keys and layouts are those of
+the per-layer modules. ``fused=False`` runs the same step as separate torch
+ops around ``QuantizedLinear`` (the reference-shaped decoder).
+
+Prefill (M = prompt length > 8) runs the HIP dequantize kernel + hipBLASLt.
 ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.
@@ -25,6 +35,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from nibble_amd import _lib
 from nibble_amd.linear import QuantizedLinear
 from nibble_amd.quantization import quantize_and_pack_weights
 
@@ -109,6 +120,20 @@ class Block(torch.nn.Module):
         return x
 
 
+def _concat_rows(modules: list[QuantizedLinear]) -> tuple[torch.Tensor, torch.Tensor]:
+    """Move the modules' packed weights and scales into one buffer each (rows
+    stacked in order) and point every module at a contiguous view of its rows."""
+    packed = torch.cat([m.packed_weights for m in modules])
+    scales = torch.cat([m.scales for m in modules])
+    row = 0
+    for m in modules:
+        n = m.out_features
+        m.packed_weights = packed[row: row + n]
+        m.scales = scales[row: row + n]
+        row += n
+    return packed, scales
+
+
 def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """Rotary embedding, half-split convention; x [T, heads, d], cos/sin [T, d/2]."""
     half = x.shape[-1] // 2
@@ -120,10 +145,15 @@ def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor
 class LlamaDecoder(torch.nn.Module):
     """Random-init Llama with INT4 linear layers, a static KV cache and greedy decode."""
 
-    def __init__(self, cfg: LlamaConfig, device: str | torch.device = "cuda", seed: int = 0) -> None:
+    def __init__(self, cfg: LlamaConfig, device: str | torch.device = "cuda", seed: int = 0,
+                 fused: bool = True) -> None:
         super().__init__()
         self.cfg = cfg
         device = torch.device(device)
+        # The fused step is HIP-only (CPU runs the torch ops) and built for
+        # head_dim 64 and rows of K <= 16384.
+        self.fused = (fused and device.type == "cuda" and cfg.head_dim == 64
+                      and max(cfg.hidden_size, cfg.intermediate_size) <= 16384)
         gen = torch.Generator(device=device).manual_seed(seed)
         self.embed = torch.nn.Parameter(
             (torch.randn((cfg.vocab_size, cfg.hidden_size), device=device, generator=gen) * cfg.init_std).to(
@@ -146,6 +176,15 @@ class LlamaDecoder(torch.nn.Module):
         self.token = torch.zeros((1,), dtype=torch.int64, device=device)
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
+        # fused-step weights (views keep the per-module state-dict entries) and work buffers
+        self.qkv = [_concat_rows([b.q_proj, b.k_proj, b.v_proj]) for b in self.layers]
+        self.gate_up = [_concat_rows([b.gate_proj, b.up_proj]) for b in self.layers]
+        h, kv = cfg.hidden_size, cfg.num_kv_heads * cfg.head_dim
+        self.x_buf = torch.zeros((h,), dtype=torch.float16, device=device)
+        self.qkv_buf = torch.zeros((h + 2 * kv,), dtype=torch.float16, device=device)
+        self.attn_buf = torch.zeros((cfg.num_heads * cfg.head_dim,), dtype=torch.float16, device=device)
+        self.mlp_buf = torch.zeros((cfg.intermediate_size,), dtype=torch.float16, device=device)
+        self.logits = torch.zeros((cfg.vocab_size,), dtype=torch.float16, device=device)
 
     def linear_layers(self) -> list[QuantizedLinear]:
         return [m for m in self.modules() if isinstance(m, QuantizedLinear)]
@@ -175,9 +214,33 @@ class LlamaDecoder(torch.nn.Module):
         return self.token.clone()
 
     def _step(self) -> None:
+        if self.fused:
+            self._step_fused()
+            return
         logits = self._forward(self.token, self.position)
+        self.logits.copy_(logits)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.add_(1)
+
+    def _step_fused(self) -> None:
+        """One decode step as 5 launches per layer (include/w4a16_decode.h)."""
+        cfg = self.cfg
+        x = self.x_buf
+        _lib.embedding_f16(self.embed, self.token, x)
+        for i, b in enumerate(self.layers):
+            qkv_w, qkv_s = self.qkv[i]
+            gu_w, gu_s = self.gate_up[i]
+            _lib.gemv_fused_f16(x, qkv_w, qkv_s, self.qkv_buf, norm_weight=b.input_norm.weight,
+                                eps=b.input_norm.eps)
+            _lib.decode_attention_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.cos, self.sin,
+                                      self.position, self.attn_buf, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
+            _lib.gemv_fused_f16(self.attn_buf, b.o_proj.packed_weights, b.o_proj.scales, x, residual=x)
+            _lib.gemv_fused_f16(x, gu_w, gu_s, self.mlp_buf, norm_weight=b.post_norm.weight, eps=b.post_norm.eps,
+                                paired=True)
+            _lib.gemv_fused_f16(self.mlp_buf, b.down_proj.packed_weights, b.down_proj.scales, x, residual=x)
+        _lib.gemv_fused_f16(x, self.lm_head.packed_weights, self.lm_head.scales, self.logits,
+                            norm_weight=self.norm.weight, eps=self.norm.eps)
+        _lib.argmax_f16(self.logits, self.token, self.position)
 
     @torch.inference_mode()
     def step(self) -> torch.Tensor:

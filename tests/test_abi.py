@@ -13,21 +13,50 @@ import torch
 
 from nibble_amd import _lib
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "w4a16_hip.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include")
+HEADER = os.path.join(INCLUDE, "w4a16_hip.h")
+DECODE_HEADER = os.path.join(INCLUDE, "w4a16_decode.h")
 
 
-def declared_functions() -> list[str]:
-    text = open(HEADER).read()
+def declared_functions(header: str = HEADER) -> list[str]:
+    text = open(header).read()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(w4a16_\w+)\s*\(", text, re.M)))
 
 
-def test_header_symbols_exported():
-    names = declared_functions()
-    assert len(names) >= 8, names
+@pytest.mark.parametrize("header,table,minimum", [(HEADER, "SIGNATURES", 8), (DECODE_HEADER, "DECODE_SIGNATURES", 4)])
+def test_header_symbols_exported(header, table, minimum):
+    names = declared_functions(header)
+    assert len(names) >= minimum, names
     lib = _lib.lib()
     for name in names:
         assert hasattr(lib, name), f"{name} not exported by libw4a16_hip.so"
-    assert set(names) == set(_lib.SIGNATURES), "ctypes binding out of sync with the header"
+    assert set(names) == set(getattr(_lib, table)), "ctypes binding out of sync with the header"
+
+
+def test_decode_entry_points_validate_before_launch():
+    """Argument checks of include/w4a16_decode.h return codes without touching a GPU."""
+    lib = _lib.lib()
+    a = 1 << 20   # an aligned stand-in address; nothing is launched on these paths
+    # fused GEMV: group size, K range, odd paired rows, residual with paired, alignment
+    assert lib.w4a16_gemv_fused_f16(a, 0, 1e-5, a, a, 0, a, 8, 256, 64, 0, 0) == _lib.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_gemv_fused_f16(a, 0, 1e-5, a, a, 0, a, 8, 32768, 128, 0, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_gemv_fused_f16(a, 0, 1e-5, a, a, 0, a, 7, 256, 128, 1, 0) == _lib.W4A16_ERR_SHAPE
+    assert "even" in _lib.last_error()
+    assert lib.w4a16_gemv_fused_f16(a, 0, 1e-5, a, a, a, a, 8, 256, 128, 1, 0) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_gemv_fused_f16(a + 2, 0, 1e-5, a, a, 0, a, 8, 256, 128, 0, 0) == _lib.W4A16_ERR_ALIGNMENT
+    assert lib.w4a16_gemv_fused_f16(a, 0, -1.0, a, a, 0, a, 8, 256, 128, 0, 0) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_gemv_fused_f16(0, 0, 1e-5, a, a, 0, a, 8, 256, 128, 0, 0) == _lib.W4A16_ERR_NULL
+    # attention: head_dim, head grouping, sequence length, NULL pointers
+    args = [a] * 7
+    assert lib.w4a16_decode_attention_f16(*args, 32, 4, 128, 64, 0) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_decode_attention_f16(*args, 30, 4, 64, 64, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_decode_attention_f16(*args, 32, 4, 64, 0, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_decode_attention_f16(0, *args[1:], 32, 4, 64, 64, 0) == _lib.W4A16_ERR_NULL
+    # argmax / embedding
+    assert lib.w4a16_argmax_f16(a, 0, a, 0, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_argmax_f16(0, 10, a, 0, 0) == _lib.W4A16_ERR_NULL
+    assert lib.w4a16_embedding_f16(a, 0, 64, a, a, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_embedding_f16(a, 10, 64, 0, a, 0) == _lib.W4A16_ERR_NULL
 
 
 def test_version():

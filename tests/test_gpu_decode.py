@@ -1,0 +1,241 @@
+"""GPU tests of the decode-step entry points (include/w4a16_decode.h), called
+through the C ABI, and of the Llama decoder's fused step.
+
+References: the fused GEMV against the CPU oracle applied to the torch-fp32
+RMSNorm of the row (bar |err| <= 1e-2 (1 + |ref|), with the residual add and
+SiLU-multiply done on fp16-rounded values as fp16 tensors would); attention
+against a float64 torch restatement of rotary embedding + masked softmax
+attention (|err| <= 2e-3 + 1e-2 |ref|, fp16 output); argmax and embedding
+exactly."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nibble_amd import _lib
+from tests._cases import assert_parity, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _rms_norm_f16(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (xf * w.float()).to(torch.float16)
+
+
+def _linear_ref(x16: torch.Tensor, p: torch.Tensor, s: torch.Tensor) -> np.ndarray:
+    return oracle.linear(x16.cpu().numpy().reshape(1, -1), p.cpu().numpy(), s.cpu().numpy(), 128)[0]
+
+
+def _f16(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("k,n", [(256, 7), (2048, 64), (2048, 2560), (5632, 300), (16384, 33)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemv_fused_plain_and_norm(gpu, k, n, norm):
+    x, p, s = make_case(1, k, n, seed=k + n)
+    gen = torch.Generator().manual_seed(k)
+    w = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16)
+    xin = _rms_norm_f16(x, w, 1e-5) if norm else x
+    ref = _linear_ref(xin, p, s)
+    out = torch.full((n,), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] fused norm={norm} K={k} N={n}", flush=True)
+    _lib.gemv_fused_f16(x.to(gpu), p.to(gpu), s.to(gpu), out, norm_weight=w.to(gpu) if norm else None, eps=1e-5)
+    torch.cuda.synchronize()
+    assert_parity(out.view(1, n), ref.reshape(1, n), f"fused norm={norm} K={k} N={n}")
+
+
+@pytest.mark.parametrize("alias", [False, True])
+@pytest.mark.parametrize("k,n", [(2048, 2048), (5632, 2048), (256, 9)])
+def test_gemv_fused_residual(gpu, k, n, alias):
+    x, p, s = make_case(1, k, n, seed=3 * k + n)
+    resid = torch.randn((n,), generator=torch.Generator().manual_seed(n)).to(torch.float16)
+    ref = _f16(resid.float().numpy() + _f16(_linear_ref(x, p, s)))
+    r = resid.to(gpu)
+    out = r if alias else torch.full((n,), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] fused residual alias={alias} K={k} N={n}", flush=True)
+    _lib.gemv_fused_f16(x.to(gpu), p.to(gpu), s.to(gpu), out, residual=r)
+    torch.cuda.synchronize()
+    assert_parity(out.view(1, n), ref.reshape(1, n), f"residual alias={alias}")
+
+
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("k,half", [(2048, 5632), (256, 5), (4096, 64)])
+def test_gemv_fused_paired_silu(gpu, k, half, norm):
+    x, p, s = make_case(1, k, 2 * half, seed=k + half)
+    w = (1.0 + 0.25 * torch.randn((k,), generator=torch.Generator().manual_seed(7))).to(torch.float16)
+    xin = _rms_norm_f16(x, w, 1e-6) if norm else x
+    y = _f16(_linear_ref(xin, p, s))
+    g, u = y[:half].astype(np.float64), y[half:].astype(np.float64)
+    ref = _f16(_f16(g / (1.0 + np.exp(-g))) * u)
+    out = torch.full((half,), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] fused paired norm={norm} K={k} N/2={half}", flush=True)
+    _lib.gemv_fused_f16(x.to(gpu), p.to(gpu), s.to(gpu), out, norm_weight=w.to(gpu) if norm else None, eps=1e-6,
+                        paired=True)
+    torch.cuda.synchronize()
+    assert_parity(out.view(1, half), ref.reshape(1, half), f"paired norm={norm}")
+
+
+def test_gemv_fused_rejects(gpu):
+    x, p, s = make_case(1, 256, 7, seed=1)
+    out = torch.empty((7,), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="even number of rows"):
+        _lib.gemv_fused_f16(x.to(gpu), p.to(gpu), s.to(gpu), out, paired=True)
+    xd = torch.empty((257,), dtype=torch.float16, device=gpu)[1:]
+    with pytest.raises(_lib.W4A16Error, match="16-byte aligned"):
+        _lib.gemv_fused_f16(xd, p.to(gpu), s.to(gpu), out)
+
+
+# ------------------------------------------------------------ attention ----
+def _rope64(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    x1, x2 = x[..., :32].double(), x[..., 32:].double()
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1)
+
+
+def _tables(S: int, theta: float = 10000.0):
+    inv = 1.0 / (theta ** (torch.arange(0, 64, 2).float() / 64))
+    ang = torch.outer(torch.arange(S).float(), inv)
+    return ang.cos(), ang.sin()
+
+
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
+@pytest.mark.parametrize("pos", [0, 1, 17, 63, 64, 127])
+def test_decode_attention(gpu, heads, kv, pos):
+    S = 128
+    gen = torch.Generator().manual_seed(pos * 31 + heads)
+    qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    cos, sin = _tables(S)
+    # reference (float64 on fp16-rounded rotary outputs, as the cache stores them)
+    c, s_ = cos[pos].double(), sin[pos].double()
+    q = _rope64(qkv[: heads * 64].view(heads, 64), c, s_).to(torch.float16).double()
+    k_new = _rope64(qkv[heads * 64: (heads + kv) * 64].view(kv, 64), c, s_).to(torch.float16)
+    v_new = qkv[(heads + kv) * 64:].view(kv, 64)
+    kc, vc = k_cache.clone(), v_cache.clone()
+    kc[:, pos], vc[:, pos] = k_new, v_new
+    group = heads // kv
+    kf = kc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    vf = vc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    scores = torch.einsum("hd,hsd->hs", q, kf) / math.sqrt(64)
+    ref = torch.einsum("hs,hsd->hd", torch.softmax(scores, dim=-1), vf).reshape(-1)
+
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = torch.full((heads * 64,), float("nan"), dtype=torch.float16, device=gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] attention heads={heads} kv={kv} pos={pos}", flush=True)
+    _lib.decode_attention_f16(qkv.to(gpu), kd, vd, cos.to(gpu), sin.to(gpu), position, out, heads, kv)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    assert float(err.max()) <= float((2e-3 + 1e-2 * ref.abs()).max()), float(err.max())
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs())
+    # the cache gained exactly slot `pos` (rotary k within one fp16 ulp, v exact); other slots untouched
+    kg, vg = kd.cpu(), vd.cpu()
+    others = [t for t in range(S) if t != pos]
+    assert torch.equal(kg[:, others], k_cache[:, others]) and torch.equal(vg[:, others], v_cache[:, others])
+    assert torch.equal(vg[:, pos], v_new)
+    assert torch.allclose(kg[:, pos].float(), k_new.float(), rtol=2 ** -10, atol=2 ** -14)
+
+
+def test_decode_attention_position_out_of_range(gpu):
+    S, heads, kv = 16, 8, 2
+    qkv = torch.randn(((heads + 2 * kv) * 64,)).to(torch.float16).to(gpu)
+    kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+    vd = torch.zeros_like(kd)
+    cos, sin = _tables(S)
+    out = torch.zeros((heads * 64,), dtype=torch.float16, device=gpu)
+    for bad in (S, -1):
+        position = torch.tensor([bad], dtype=torch.int64, device=gpu)
+        _lib.decode_attention_f16(qkv, kd, vd, cos.to(gpu), sin.to(gpu), position, out, heads, kv)
+        torch.cuda.synchronize()
+        assert torch.isnan(out).all()
+        assert not kd.any() and not vd.any()
+
+
+# ------------------------------------------------------- argmax, embedding ----
+@pytest.mark.parametrize("n", [1, 1000, 32000, 50257])
+def test_argmax_first_maximum_and_position(gpu, n):
+    gen = torch.Generator().manual_seed(n)
+    logits = torch.randn((n,), generator=gen).to(torch.float16)
+    if n > 10:
+        top = float(logits.max())
+        logits[n // 3] = top + 1.0
+        logits[n // 2] = top + 1.0        # tie: the first index wins
+    token = torch.full((1,), -5, dtype=torch.int64, device=gpu)
+    position = torch.tensor([41], dtype=torch.int64, device=gpu)
+    _lib.argmax_f16(logits.to(gpu), token, position)
+    torch.cuda.synchronize()
+    assert int(token) == int(torch.argmax(logits))
+    assert int(position) == 42
+    _lib.argmax_f16(logits.to(gpu), token)   # no position
+    torch.cuda.synchronize()
+    assert int(token) == int(torch.argmax(logits))
+
+
+def test_embedding_gather(gpu):
+    table = torch.randn((100, 2048)).to(torch.float16).to(gpu)
+    out = torch.empty((2048,), dtype=torch.float16, device=gpu)
+    for t in (0, 57, 99):
+        _lib.embedding_f16(table, torch.tensor([t], device=gpu), out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, table[t])
+    _lib.embedding_f16(table, torch.tensor([100], device=gpu), out)
+    torch.cuda.synchronize()
+    assert not out.any()
+
+
+# ----------------------------------------------------------- fused decoder ----
+def _small_cfg():
+    from nibble_amd.llama import LlamaConfig
+
+    return LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1280, num_layers=2, num_heads=8,
+                       num_kv_heads=2, head_dim=64, max_seq_len=32)
+
+
+def test_fused_step_matches_torch_step(gpu):
+    """One decode step from the same state: fused kernels vs the torch-op step
+    around QuantizedLinear (same weights). Bar on the logits:
+    |err| <= 2e-2 (1 + |ref|)."""
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(_small_cfg(), device=gpu, seed=0)
+    assert model.fused
+    prompt = torch.randint(0, 512, (12,), generator=torch.Generator().manual_seed(1)).to(gpu)
+    model.prefill(prompt)
+    state = (model.k_cache.clone(), model.v_cache.clone(), model.token.clone(), model.position.clone())
+    with torch.inference_mode():
+        model.fused = False
+        model.step()
+        ref_logits, ref_k = model.logits.clone(), model.k_cache.clone()
+        model.k_cache.copy_(state[0]); model.v_cache.copy_(state[1])
+        model.token.copy_(state[2]); model.position.copy_(state[3])
+        model.fused = True
+        model.step()
+    torch.cuda.synchronize()
+    got, ref = model.logits.float().cpu(), ref_logits.float().cpu()
+    assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
+    assert int(model.position) == int(state[3]) + 1
+    # the new cache slot holds the same k (rotary within fp16 rounding)
+    p = int(state[3])
+    assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
+
+
+def test_fused_decode_graph_matches_eager(gpu):
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(_small_cfg(), device=gpu, seed=2)
+    prompt = torch.randint(0, 512, (10,), generator=torch.Generator().manual_seed(3)).to(gpu)
+    eager = model.generate(prompt, 10, use_graph=False)
+    model.prefill(prompt)
+    model.capture()
+    for _ in range(2):
+        assert torch.equal(model.generate(prompt, 10, use_graph=True), eager)

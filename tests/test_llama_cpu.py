@@ -31,3 +31,27 @@ def test_kv_cache_decode_equals_full_recompute():
         nxt = m.prefill(seq)
         assert int(nxt) == int(toks[i])
         seq = torch.cat([seq, nxt])
+
+
+def test_fused_weight_buffers_keep_state_dict_layout():
+    """q|k|v and gate|up rows live in one buffer each; every module's
+    packed_weights / scales is a contiguous view of its own rows, so the
+    state dict keeps the per-module keys and shapes."""
+    cfg = _tiny()
+    m = LlamaDecoder(cfg, device="cpu", seed=1)
+    sd = m.state_dict()
+    kv = cfg.num_kv_heads * cfg.head_dim
+    for i, b in enumerate(m.layers):
+        assert sd[f"layers.{i}.q_proj.packed_weights"].shape == (cfg.hidden_size, cfg.hidden_size // 2)
+        assert sd[f"layers.{i}.k_proj.packed_weights"].shape == (kv, cfg.hidden_size // 2)
+        assert sd[f"layers.{i}.up_proj.scales"].shape == (cfg.intermediate_size, cfg.hidden_size // 128)
+        qkv_w, qkv_s = m.qkv[i]
+        gu_w, gu_s = m.gate_up[i]
+        assert qkv_w.shape[0] == cfg.hidden_size + 2 * kv and gu_w.shape[0] == 2 * cfg.intermediate_size
+        for mod in (b.q_proj, b.k_proj, b.v_proj, b.gate_proj, b.up_proj):
+            assert mod.packed_weights.is_contiguous() and mod.scales.is_contiguous()
+        assert b.k_proj.packed_weights.data_ptr() == qkv_w[cfg.hidden_size:].data_ptr()
+        assert b.v_proj.scales.data_ptr() == qkv_s[cfg.hidden_size + kv:].data_ptr()
+        assert b.up_proj.packed_weights.data_ptr() == gu_w[cfg.intermediate_size:].data_ptr()
+        assert torch.equal(torch.cat([b.gate_proj.packed_weights, b.up_proj.packed_weights]), gu_w)
+    assert not m.fused   # the fused step runs on GPUs only
