@@ -15,12 +15,15 @@ the K steps / elapsed time (GB/s), with algorithmic bytes per call
 N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 (reference scripts/profile_kernel.py:310-323).
 
 Also reported: per-layer us / GB/s / % of the 8 TB/s HBM peak for each shape
-(graph replay, 100 calls), a measured device copy bandwidth, end-to-end greedy
-decode tokens/s of the random-init 1.1B Llama-architecture model (configs[4],
-decode step in a HIP graph), and the CPU oracle's time for the same layers on
-the host cores (`cpu_baseline`; a reported baseline, not a target).
+(graph replay, 100 calls), the configs[2] small-batch table (M = 1, 2, 4, 8
+on 2048x2048, 2048x5632, 5632x2048, next to fp16 hipBLASLt on the dequantized
+weights) and the configs[3] large-layer table (M = 1, 8), a measured device
+copy bandwidth, end-to-end greedy decode tokens/s of the random-init 1.1B
+Llama-architecture model (configs[4], decode step in a HIP graph), and the
+CPU oracle's time for the same layers on the host cores (`cpu_baseline`; a
+reported baseline, not a target).
 
-usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables]
 """
 
 from __future__ import annotations
@@ -210,6 +213,57 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
+def _copies(nbytes: int, floor_bytes: int = 512 << 20) -> int:
+    """Rotated copies so the working set is >= 2x the 256 MiB Infinity Cache."""
+    return max(2, -(-floor_bytes // nbytes))
+
+
+def layer_tables(device) -> dict:
+    """M in {1, 2, 4, 8} on the three small-batch shapes, each next
+    to an fp16 hipBLASLt GEMM (F.linear) on the dequantized weights; configs[3]:
+    the 8B- and 70B-class shapes at M in {1, 8}. Per-layer time = median of
+    graph replays of 100 calls over rotated weight copies."""
+    import torch
+    import torch.nn.functional as F
+
+    from nibble_amd import _lib
+
+    def rows_for(shapes, ms, with_fp16: bool, samples: int):
+        rows = []
+        for k, n in shapes:
+            copies = _copies(n * k // 2)
+            packed, scales = make_layer(k, n, copies, device, seed=k + n)
+            w16 = []
+            if with_fp16:
+                c16 = _copies(2 * n * k)
+                w16 = [torch.ops.w4a16.dequantize(packed[i % copies], scales[i % copies], 128) for i in range(c16)]
+            base_us = None
+            for m in ms:
+                x = torch.randn((m, k), device=device).to(torch.float16)
+                out = torch.empty((m, n), device=device, dtype=torch.float16)
+                us = per_layer(lambda i: _lib.linear_f16(x, packed[i], scales[i], out), copies, samples=samples)
+                plan = _lib.plan_linear(x.data_ptr(), packed[0].data_ptr(), m, n, k)
+                gbs = payload_bytes(m, n, k) / us / 1e3
+                row = {"K": k, "N": n, "M": m, "us": round(us, 3), "GBps": round(gbs, 1),
+                       "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": plan["kernel"]}
+                if m == 1:
+                    base_us = us
+                else:
+                    row["vs_M1"] = round(us / base_us, 3)
+                if w16:
+                    row["fp16_hipblaslt_us"] = round(
+                        per_layer(lambda i: F.linear(x, w16[i]), len(w16), samples=samples), 3)
+                rows.append(row)
+            del packed, scales, w16
+            torch.cuda.empty_cache()
+        return rows
+
+    small = rows_for([(2048, 2048), (2048, 5632), (5632, 2048)], (1, 2, 4, 8), True, 10)
+    large = rows_for([(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (8192, 28672), (28672, 8192)],
+                     (1, 8), False, 5)
+    return {"configs2_small_batch": small, "configs3_large": large}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,6 +271,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-tables", action="store_true", help="skip the configs[2] / configs[3] per-layer tables")
     ap.add_argument("--counter-pass", action="store_true",
                     help="eager launches only, for rocprofv3 --pmc: 50 calls of each MLP shape on rotated "
                          "copies, then 5 elementwise negations of a 256 MiB fp32 buffer into another "
@@ -326,6 +381,8 @@ def main() -> int:
         "roofline": roofline,
     }
     line["copy_GBps"] = round(copy_bandwidth(device), 1)
+    if not args.no_tables:
+        line["layers"] = layer_tables(device)
     if not args.no_decode:
         del layers
         torch.cuda.empty_cache()

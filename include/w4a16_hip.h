@@ -41,6 +41,7 @@ extern "C" {
 #define W4A16_KERNEL_DIAG 4          /* M = 1 on fp16 MFMA, group dots on the 16x16 diagonal */
 #define W4A16_KERNEL_VALU_OFFSET 5   /* VALU kernel, decode without f16 fix-ups, per-chunk offset correction */
 #define W4A16_KERNEL_ONESHOT 6       /* VALU GEMV, every weight of a wavefront's rows requested at once (M <= 4) */
+#define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 8, K <= 8192) */
 
 /*
  * Fused W4A16 linear layer.
@@ -113,6 +114,11 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splits = wavefronts per workgroup (4|8), unroll = 1 KiB loads per row
  *     per lane (0 = the smallest that covers K; else >= ceil(K / 2048) and
  *     one of 1..8, 10, 12, 14, 16), max_blocks ignored.
+ *   W4A16_KERNEL_MFMA_ONESHOT (K <= 8192, M*K*2 + K/2 + 16 KiB of LDS):
+ *     rows = 16-row blocks per workgroup (1|2), splits = wavefronts
+ *     splitting K (4|8), unroll = groups per wavefront (0 = ceil(K / 128 /
+ *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
+ *     1..8 with 8), max_blocks ignored.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 and 16-byte aligned
  * activations and weights. No reference counterpart (the reference's

@@ -79,7 +79,10 @@ int read_env(int* family, int* rows_per_wave) {
         else if (std::strcmp(d, "valu_offset") == 0) *family = W4A16_KERNEL_VALU_OFFSET;
         else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
         else if (std::strcmp(d, "oneshot") == 0) *family = W4A16_KERNEL_ONESHOT;
-        else return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, oneshot, or mfma");
+        else if (std::strcmp(d, "mfma_oneshot") == 0) *family = W4A16_KERNEL_MFMA_ONESHOT;
+        else
+            return fail(W4A16_ERR_CONFIG,
+                        "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, or mfma_oneshot");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -160,6 +163,36 @@ bool oneshot_fits(int64_t M, int64_t K) {
     return M >= 1 && M <= 4 && oneshot_loads(K) > 0 && M * K * 2 <= kMaxLdsBytes;
 }
 
+// One-shot MFMA kernel (rows up to 8192 weights, activations within LDS).
+// Launch shape from the M = 3..8 sweeps: 4 or 8 wavefronts split K; two
+// 16-row blocks per workgroup (one staged copy of the activations serves 32
+// rows) where N leaves enough workgroups to fill the chip.
+constexpr int kMfmaOneshotMaxGroups = 64;
+
+bool mfma_oneshot_fits(int64_t M, int64_t K) {
+    const int64_t G = K / 128;
+    return M >= 1 && M <= 8 && G >= 1 && G <= kMfmaOneshotMaxGroups &&
+           M * K * 2 + G * 64 + 2 * 8 * 1024 <= kMaxLdsBytes;
+}
+
+Plan plan_mfma_oneshot(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_MFMA_ONESHOT;
+    if (K <= 2048) {            // 2048 x 2048, 2048 x 5632
+        p.splits = 4;
+        p.rows = N >= 4096 ? 2 : 1;
+    } else if (K <= 4096) {     // 4096 x 4096 vs 4096 x 14336
+        p.splits = N >= 8192 ? 4 : 8;
+        p.rows = N >= 8192 ? 2 : 1;
+    } else {                    // 8192 x 8192, 8192 x 28672
+        p.splits = 8;
+        p.rows = (M >= 5 && N >= 8192) ? 2 : 1;
+    }
+    p.unroll = (int)((K / 128 + p.splits - 1) / p.splits);
+    if (p.unroll > 8) p.unroll = (p.unroll + 1) & ~1;
+    return p;
+}
+
 int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
     int family = 0, rows = 0;
     const int rc = read_env(&family, &rows);
@@ -183,15 +216,34 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // with K <= 8192); beyond that the MFMA kernel's cost does not grow with M.
     // An explicit W4A16_ROWS_PER_WARP (an A/B switch, as in the reference)
     // keeps auto on the looped VALU kernel whose rows it sets.
-    // One-shot: every M = 1 row that fits; for M = 2..4 only small layers
-    // (K, N <= 5632), because each workgroup re-stages M*K activations, which
-    // on large layers outweighs the weights it streams.
+    // Measured routing (M = 1..8 sweeps over the benchmark shapes):
+    //   M = 1: one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
+    //   M >= 3: one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
+    //   small layers (K, N <= 5632; each workgroup re-stages M*K activations,
+    //   which on large layers outweighs the weights it streams), one-shot
+    //   MFMA up to K = 8192 when N >= 4096 gives it enough row blocks;
+    //   otherwise the looped VALU kernel for M = 1, M = 2 (K <= 16384) or
+    //   M <= 4 (K <= 4096), else the looped MFMA kernel.
     if (family == 0) {
         const bool small = K <= 5632 && N <= 5632;
-        if (rows == 0 && oneshot_fits(M, K) && (M == 1 || small))
+        if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
             family = W4A16_KERNEL_ONESHOT;
+        else if (M >= 3 && K <= 4096 && mfma_oneshot_fits(M, K))
+            family = W4A16_KERNEL_MFMA_ONESHOT;
+        else if (rows == 0 && M <= 4 && small && oneshot_fits(M, K))
+            family = W4A16_KERNEL_ONESHOT;
+        else if (M >= 3 && N >= 4096 && mfma_oneshot_fits(M, K))
+            family = W4A16_KERNEL_MFMA_ONESHOT;
         else
-            family = (M <= 2 || (M <= 4 && K <= 8192)) ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;
+            family = (M == 1 || (M == 2 && K <= 16384) || (M <= 4 && K <= 4096)) ? W4A16_KERNEL_VALU
+                                                                                   : W4A16_KERNEL_MFMA;
+    }
+    if (family == W4A16_KERNEL_MFMA_ONESHOT) {
+        if (mfma_oneshot_fits(M, K)) {
+            *out = plan_mfma_oneshot(M, N, K);
+            return W4A16_OK;
+        }
+        family = W4A16_KERNEL_MFMA;   // rows too long for the staged activations
     }
     if (family == W4A16_KERNEL_VALU_OFFSET && M != 1) family = W4A16_KERNEL_VALU;
     if (family == W4A16_KERNEL_ONESHOT) {
@@ -332,6 +384,44 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* n
     return check_launch();
 }
 
+int launch_mfma_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s, w4a16::f16* o,
+                        int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    if (M < 1 || M > 8) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel needs 1 <= M <= 8");
+    const int G = K / 128;
+    if (G < 1 || G > kMfmaOneshotMaxGroups)
+        return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel: K must be a multiple of 128 up to 8192");
+    if (p.splits != 4 && p.splits != 8) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel: splits must be 4 or 8");
+    if (p.unroll == 0) {
+        p.unroll = (G + p.splits - 1) / p.splits;
+        if (p.unroll > 8) p.unroll = (p.unroll + 1) & ~1;   // instantiated: 1..8, 10, 12, 14, 16
+    }
+    if (p.unroll * p.splits < G) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel: unroll * splits must cover K / 128");
+    void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, int) = nullptr;
+#define W4A16_PICK(SK, SN, GPW) \
+    if (p.splits == SK && p.rows == SN && p.unroll == GPW) kern = gemv_mfma_oneshot<SK, SN, GPW>;
+#define W4A16_PICK8(SK, SN)                                                                               \
+    W4A16_PICK(SK, SN, 1) W4A16_PICK(SK, SN, 2) W4A16_PICK(SK, SN, 3) W4A16_PICK(SK, SN, 4)             \
+    W4A16_PICK(SK, SN, 5) W4A16_PICK(SK, SN, 6) W4A16_PICK(SK, SN, 7) W4A16_PICK(SK, SN, 8)
+#define W4A16_PICK16(SK, SN)                                                                              \
+    W4A16_PICK8(SK, SN) W4A16_PICK(SK, SN, 10) W4A16_PICK(SK, SN, 12) W4A16_PICK(SK, SN, 14)            \
+    W4A16_PICK(SK, SN, 16)
+    W4A16_PICK16(4, 1) W4A16_PICK16(4, 2) W4A16_PICK8(8, 1) W4A16_PICK8(8, 2)
+#undef W4A16_PICK16
+#undef W4A16_PICK8
+#undef W4A16_PICK
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG,
+                    "one-shot MFMA kernel: rows 1 or 2, unroll 1..8, 10, 12, 14, 16 with 4 splits or 1..8 with 8");
+    const int lds = M * K * 2 + G * 64 + p.splits * p.rows * 64 * 16;
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel: activations do not fit in LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int blocks = (N + 16 * p.rows - 1) / (16 * p.rows);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits * p.rows), lds, stream, x, w, s, o, M, N, K);
+    return check_launch();
+}
+
 int launch_diag(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
                 w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
@@ -408,6 +498,7 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_MFMA: return launch_mfma(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_DIAG: return launch_diag(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_ONESHOT: return launch_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_MFMA_ONESHOT: return launch_mfma_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -508,14 +599,15 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.unroll = unroll;
     p.max_blocks = max_blocks;
     if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
-        kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT) {
+        kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT ||
+        kernel == W4A16_KERNEL_MFMA_ONESHOT) {
         if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
-                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _DIAG or _GENERIC");
+                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
 }

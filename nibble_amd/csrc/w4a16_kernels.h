@@ -789,6 +789,165 @@ gemv_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------
+// One-shot MFMA kernel for small batches (runtime M = 1..8), G = 128.
+//
+// Workgroup = SK x SN wavefronts: SN blocks of 16 output rows, each block's
+// groups split over SK wavefronts (wavefront kw takes groups kw, kw + SK, ...,
+// GPW of them, so at any step the SK wavefronts read adjacent 64-byte pieces
+// of each row). MFMA layout as in gemv_mfma: lane l = 16 q + c supplies row
+// n0 + c's chunk q of a group as B (word t -> MFMA t) and activation row c's
+// matching 8 k values as A; D[4 q + e][c] lands in lane l, register e.
+//
+// Differences from gemv_mfma, each measured on the small-batch benchmark shapes:
+//   * every weight and scale load of a wavefront is issued up front
+//     (straight-line, clamped addresses), after the workgroup's activation
+//     units, which return first;
+//   * the activations are staged once per workgroup in LDS in A order
+//     (unit (g, t, q) of row m at xs[((g*4 + t)*4 + q)*M + m]), and each
+//     group's four A fragments are read one group ahead of its MFMAs;
+//   * offset decode: B holds the codes without f16 fix-ups (1024 + v for
+//     pos-0 nibbles, 1024 + 16 v for pos-1 nibbles, v = s + 8) and A the
+//     activations with pos-1 halves pre-scaled by 1/16 (exact unless
+//     subnormal), so the dot carries 1032 * sum(x pos-0) + 72 * sum(x pos-1)
+//     on top of sum x*s. That bias depends only on the activations: it is
+//     computed while staging (base[g][m], fp32) and each group's MFMA chain
+//     starts from -base instead of 0. Products are exact; the sums are fp32
+//     with a larger magnitude than sum x*s alone (the precision of the
+//     offset decode, within the 1e-2 (1 + |ref|) bar with ~10x margin);
+//   * the D rows of activation rows >= M read duplicated rows and are never
+//     stored, so no lane selects zeros.
+// Partial sums of the SK wavefronts are reduced through LDS.
+// ---------------------------------------------------------------------------
+template <int SK, int SN, int GPW>
+__global__ void __launch_bounds__(64 * SK * SN)
+gemv_mfma_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+                  f16* __restrict__ out, int M, int N, int K) {
+    constexpr int S = SK * SN;
+    constexpr int T = 64 * S;
+    constexpr int kFirst = 8;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int G = K >> 7;
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);                               // M*K*2 bytes
+    float* base = reinterpret_cast<float*>(smem + (size_t)M * K * 2);          // [G][16] fp32
+    f32x4* red = reinterpret_cast<f32x4*>(smem + (size_t)M * K * 2 + (size_t)G * 64);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15, q = lane >> 4;
+    const int kw = wave % SK, nb = wave / SK;
+    const int n0 = (blockIdx.x * SN + nb) * 16;
+    const int n = min(n0 + col, N - 1);
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+
+    // 1. activation units (8 halves): i = m * K/8 + uk
+    const int upr = K >> 3;
+    const int units = M * upr;
+    u32x4 a[kFirst];
+#pragma unroll
+    for (int p = 0; p < kFirst; ++p) {
+        const int i = min((int)threadIdx.x + p * T, units - 1);
+        a[p] = *reinterpret_cast<const u32x4*>(x + (size_t)i * 8);
+    }
+    // 2. scales and weights: groups kw + SK j (clamped; j past G is dropped)
+    const uint16_t* srow = reinterpret_cast<const uint16_t*>(scales) + (size_t)n * G;
+    const uint8_t* wrow = w + (size_t)n * row_bytes + q * 16;
+    uint32_t sv[GPW];
+    u32x4 wv[GPW];
+#pragma unroll
+    for (int j = 0; j < GPW; ++j) sv[j] = srow[min(kw + SK * j, G - 1)];
+#pragma unroll
+    for (int j = 0; j < GPW; ++j)
+        wv[j] = load_stream(reinterpret_cast<const u32x4*>(wrow + (uint32_t)min(kw + SK * j, G - 1) * 64u));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. stage A fragments and the per-(group, row) bias
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 b0 = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 b1 = {(f16)1152.0f, (f16)1152.0f};
+    auto put = [&](int i, u32x4 v, bool valid) {
+        const int m = i / upr;
+        const int uk = i - m * upr;
+        const int g = uk >> 4, qq = (uk >> 2) & 3, t = uk & 3;
+        u32x4 pv = permute8(v);
+        pv.y = as_u32(as_f16x2(pv.y) * sixteenth);
+        pv.w = as_u32(as_f16x2(pv.w) * sixteenth);
+        float c = 0.0f;
+        c = __builtin_amdgcn_fdot2(as_f16x2(pv.x), b0, c, false);
+        c = __builtin_amdgcn_fdot2(as_f16x2(pv.y), b1, c, false);
+        c = __builtin_amdgcn_fdot2(as_f16x2(pv.z), b0, c, false);
+        c = __builtin_amdgcn_fdot2(as_f16x2(pv.w), b1, c, false);
+        // the 16 units of (m, g) sit in 16 consecutive lanes (a DPP row):
+        // after the mirrors every lane of the row holds the row sum
+        c += dpp<0xB1>(c);
+        c += dpp<0x4E>(c);
+        c += dpp<0x141>(c);
+        c += dpp<0x140>(c);
+        if (valid) {
+            xs[((g * 4 + t) * 4 + qq) * M + m] = pv;
+            if ((uk & 15) == 0) base[g * 16 + m] = -c;
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < kFirst; ++p) {
+        const int i = threadIdx.x + p * T;
+        put(min(i, units - 1), a[p], i < units);
+    }
+    // rest of a large M*K (requested after the weights): whole rows of lanes
+    for (int i0 = threadIdx.x + kFirst * T; i0 < ((units + T - 1) / T) * T; i0 += T) {
+        const int i = min(i0, units - 1);
+        put(i, *reinterpret_cast<const u32x4*>(x + (size_t)i * 8), i0 < units);
+    }
+    __syncthreads();
+
+    // 4. groups: fragments of group j+1 read while group j runs on the MFMAs
+    const int arow = col % M;
+    auto fetch = [&](u32x4 (&av)[4], f32x4& bv, int j) {
+        const int g = min(kw + SK * j, G - 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) av[t] = xs[((g * 4 + t) * 4 + q) * M + arow];
+        bv = *reinterpret_cast<const f32x4*>(base + g * 16 + ((4 * q) & 7));
+    };
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4 A0[4], A1[4];
+    f32x4 B0, B1;
+    fetch(A0, B0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < GPW; ++j) {
+        u32x4 (&cur)[4] = (j & 1) ? A1 : A0;
+        u32x4 (&nxt)[4] = (j & 1) ? A0 : A1;
+        f32x4& cb = (j & 1) ? B1 : B0;
+        f32x4& nbv = (j & 1) ? B0 : B1;
+        if (j + 1 < GPW) fetch(nxt, nbv, j + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 d = cb;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const Codes8 cw = unpack8_offset(wv[j][t]);
+            const f16x8 bt = __builtin_bit_cast(
+                f16x8, (u32x4){as_u32(cw.p[0]), as_u32(cw.p[1]), as_u32(cw.p[2]), as_u32(cw.p[3])});
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[t]), bt, d, 0, 0, 0);
+        }
+        const float sc = (kw + SK * j) < G ? (float)__builtin_bit_cast(f16, (uint16_t)sv[j]) : 0.0f;
+        acc = d * sc + acc;
+    }
+
+    // 5. reduce the SK partial tiles of this row block, store rows m < M
+    if (SK > 1) {
+        red[wave * 64 + lane] = acc;
+        __syncthreads();
+        if (kw != 0) return;
+#pragma unroll
+        for (int s2 = 1; s2 < SK; ++s2) acc += red[(wave + s2) * 64 + lane];
+    }
+    const int nn = n0 + col;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = q * 4 + e;
+        if (m < M && nn < N) out[(size_t)m * N + nn] = (f16)acc[e];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic kernel: any M, any even G with K % G == 0, any pointer alignment
 // (fp16 data needs only its natural 2-byte alignment). One wavefront per
 // output row; lanes stride over the packed bytes; activation rows in tiles of

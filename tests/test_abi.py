@@ -100,12 +100,19 @@ ALIGNED = 1 << 20
         (1, 2048, 128, ALIGNED, "oneshot"),    # decode
         (1, 32768, 128, ALIGNED, "oneshot"),   # 16 loads of 1 KiB per row
         (1, 34816, 128, ALIGNED, "valu"),      # rows too long for the one-shot kernel
-        (2, 2048, 128, ALIGNED, "oneshot"),    # small batch on a small layer
-        (4, 2048, 128, ALIGNED, "oneshot"),
+        (2, 2048, 128, ALIGNED, "oneshot"),    # M = 2 up to K = 5632
+        (2, 5632, 128, ALIGNED, "oneshot"),
+        (4, 2048, 128, ALIGNED, "mfma_oneshot"),
+        (4, 5632, 128, ALIGNED, "oneshot"),    # small layer beyond the staged-MFMA rows
         (2, 8192, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
+        (2, 28672, 128, ALIGNED, "mfma"),      # very long rows
+        (4, 8192, 128, ALIGNED, "mfma"),           # N = 64: too few row blocks for the staged kernel
+        (8, 8192, 128, ALIGNED, "mfma"),
+        (8, 8320, 128, ALIGNED, "mfma"),           # beyond the staged-MFMA rows
         (4, 14336, 128, ALIGNED, "mfma"),      # small batch, long rows -> MFMA
-        (5, 2048, 128, ALIGNED, "mfma"),
-        (8, 2048, 128, ALIGNED, "mfma"),
+        (5, 2048, 128, ALIGNED, "mfma_oneshot"),   # small batch, rows up to 4096 weights
+        (8, 4096, 128, ALIGNED, "mfma_oneshot"),
+        (8, 5632, 128, ALIGNED, "mfma"),           # K > 4096 with few rows: looped MFMA
         (9, 2048, 128, ALIGNED, "generic"),    # above the small-batch range
         (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128
         (1, 2048, 128, ALIGNED + 2, "generic"),  # activations not 16-byte aligned
@@ -122,6 +129,21 @@ def test_plan_misaligned_weights_take_generic():
     assert _lib.plan_linear(ALIGNED, ALIGNED + 8, 1, 64, 2048, 128)["kernel"] == "generic"
 
 
+def test_mfma_oneshot_plan_shapes(monkeypatch):
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    for m, n, k, rows, splits, unroll in [(8, 2048, 2048, 1, 4, 4), (8, 5632, 2048, 2, 4, 4),
+                                          (8, 14336, 4096, 2, 4, 8), (8, 4096, 4096, 1, 8, 4),
+                                          (3, 8192, 8192, 1, 8, 8), (8, 28672, 8192, 2, 8, 8),
+                                          (3, 64, 128, 1, 4, 1), (5, 100, 1152, 1, 4, 3)]:
+        plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+        assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
+            ("mfma_oneshot", rows, splits, unroll), (m, n, k)
+    monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma_oneshot"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 8320, 128)["kernel"] == "mfma"   # rows too long
+
+
 def test_oneshot_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
@@ -131,7 +153,8 @@ def test_oneshot_plan_shapes(monkeypatch):
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "valu"      # M > 1, large N
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 14336, 128)["kernel"] == "mfma"     # M > 2, long rows
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "oneshot"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 5, 64, 2048, 128)["kernel"] == "valu"     # M > 4

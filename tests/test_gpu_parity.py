@@ -17,6 +17,7 @@ pytestmark = pytest.mark.gpu
 VALU, MFMA, GENERIC, DIAG = _lib.KERNEL_VALU, _lib.KERNEL_MFMA, _lib.KERNEL_GENERIC, _lib.KERNEL_DIAG
 VOFF = _lib.KERNEL_VALU_OFFSET
 ONESHOT = _lib.KERNEL_ONESHOT
+MFMA_OS = _lib.KERNEL_MFMA_ONESHOT
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -123,6 +124,29 @@ def test_oneshot_variants(gpu, m, rows, splits, k, n):
     assert_parity(out, expected(x, p, s), f"oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
 
 
+# one-shot MFMA: every (rows, splits) shape, K from one group to 32 groups
+# (partial last step when splits do not divide K / 128), ragged N
+@pytest.mark.parametrize("rows,splits", [(1, 4), (2, 4), (1, 8), (2, 8)])
+@pytest.mark.parametrize("k,n", [(128, 7), (256, 40), (1152, 33), (2048, 2048), (3968, 21), (4096, 100),
+                                 (4224, 9), (6144, 33), (8192, 64)])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+def test_mfma_oneshot_variants(gpu, m, rows, splits, k, n):
+    x, p, s = make_case(m, k, n, seed=m * 13 + k + n)
+    out = _run_tuned(gpu, x, p, s, MFMA_OS, rows, splits, 0)
+    assert_parity(out, expected(x, p, s), f"mfma_oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
+
+
+def test_mfma_oneshot_rejects(gpu):
+    x, p, s = make_case(2, 8320, 8, seed=2)
+    with pytest.raises(_lib.W4A16Error, match="up to 8192"):
+        _run_tuned(gpu, x, p, s, MFMA_OS, 1, 4, 0)
+    x, p, s = make_case(2, 2048, 8, seed=2)
+    with pytest.raises(_lib.W4A16Error, match="cover K"):
+        _run_tuned(gpu, x, p, s, MFMA_OS, 1, 4, 2)
+    with pytest.raises(_lib.W4A16Error, match="splits must be 4 or 8"):
+        _run_tuned(gpu, x, p, s, MFMA_OS, 1, 2, 0)
+
+
 @pytest.mark.parametrize("unroll", [2, 4, 8, 16])
 def test_oneshot_more_loads_than_needed(gpu, unroll):
     # lanes past the row's last chunk idle on every extra load
@@ -147,7 +171,7 @@ def test_oneshot_rejects_short_unroll_and_long_rows(gpu):
 
 
 @pytest.mark.parametrize("kernel,rows,splits,unroll,cap",
-                         [(ONESHOT, 1, 4, 0, 0), (ONESHOT, 2, 8, 0, 0),
+                         [(ONESHOT, 1, 4, 0, 0), (ONESHOT, 2, 8, 0, 0), (MFMA_OS, 2, 4, 0, 0), (MFMA_OS, 1, 8, 0, 0),
                           (VALU, 1, 1, 1, 0), (VALU, 2, 4, 2, 0), (VALU, 4, 2, 1, 5), (VALU, 2, 4, 8, 0),
                           (VOFF, 1, 1, 1, 0), (VOFF, 2, 4, 2, 0), (VOFF, 4, 2, 1, 5), (VOFF, 2, 4, 8, 0),
                           (MFMA, 1, 1, 1, 0), (MFMA, 2, 4, 2, 0), (MFMA, 4, 2, 1, 0)])
@@ -166,7 +190,7 @@ def test_tuned_variants_batch(gpu, kernel, rows, splits, unroll, cap, m):
     assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, VOFF, ONESHOT, MFMA, GENERIC, DIAG])
+@pytest.mark.parametrize("kernel", [VALU, VOFF, ONESHOT, MFMA, MFMA_OS, GENERIC, DIAG])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_all_nibble_values(gpu, kernel, m):
     if kernel in (DIAG, VOFF) and m != 1:
@@ -175,7 +199,7 @@ def test_all_nibble_values(gpu, kernel, m):
         pytest.skip("the one-shot kernel is built for M <= 4")
     # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
     x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
-    if kernel == ONESHOT:
+    if kernel in (ONESHOT, MFMA_OS):
         out = _run_tuned(gpu, x, p, s, kernel, 2, 4, 0)
     else:
         out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
@@ -200,6 +224,7 @@ def _stress_activations(kind: str, m: int, k: int) -> torch.Tensor:
 
 @pytest.mark.parametrize("kernel,rows,splits,unroll", [(VALU, 2, 4, 1), (VOFF, 2, 4, 1), (VOFF, 1, 4, 8),
                                                        (ONESHOT, 2, 4, 0), (ONESHOT, 1, 8, 0),
+                                                       (MFMA_OS, 1, 4, 0), (MFMA_OS, 2, 8, 0),
                                                        (DIAG, 2, 4, 1), (DIAG, 1, 4, 2),
                                                        (MFMA, 2, 4, 1), (GENERIC, 1, 1, 1)])
 @pytest.mark.parametrize("kind", ["constant", "outliers", "cancel"])
