@@ -1,7 +1,8 @@
 /*
  * W4A16 decode-step extensions for gfx950 (MI355X): the fused GEMV variants
  * and the small kernels that, together with the W4A16 linear layer, run one
- * greedy-decode step of a Llama-architecture model in 5 launches per layer.
+ * greedy-decode step of a Llama-architecture model in 5 launches per layer
+ * plus 2.
  *
  * Reference interfaces they replace (chris320211/Nibble): the reference runs
  * its end-to-end decode (scripts/generate.py:260-305, HF generate with a
@@ -72,6 +73,17 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache,
  */
 int w4a16_argmax_f16(const void* logits, int64_t n, int64_t* token, int64_t* position,
                      void* stream);
+
+/*
+ * w4a16_argmax_f16, then output[0..hidden) = table[*token, :] (fp16 [vocab,
+ * hidden], vocab >= n): the next step's embedding gathered by the same
+ * launch, so a decode step needs no separate gather.
+ * Replaces (reference): the greedy pick plus the next step's embedding
+ * lookup (scripts/generate.py:286-293).
+ */
+int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_t* position,
+                           const void* table, int64_t vocab, int64_t hidden, void* output,
+                           void* stream);
 
 /*
  * output[0..hidden) = table[*token, :] (fp16 [vocab, hidden]); a token

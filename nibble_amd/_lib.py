@@ -64,6 +64,7 @@ DECODE_SIGNATURES = {
     ),
     "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
+    "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
 }
 
@@ -202,6 +203,14 @@ def argmax_f16(logits, token, position=None, stream=None) -> None:
     """``w4a16_argmax_f16``: token <- argmax(logits); position += 1 when given."""
     _raise_on(lib().w4a16_argmax_f16(logits.data_ptr(), logits.numel(), token.data_ptr(), _ptr(position),
                                      _stream_ptr(stream)))
+
+
+def argmax_embed_f16(logits, token, position, table, output, stream=None) -> None:
+    """``w4a16_argmax_embed_f16``: token <- argmax(logits); position += 1;
+    output <- table[token] (the next step's input row)."""
+    vocab, hidden = table.shape
+    _raise_on(lib().w4a16_argmax_embed_f16(logits.data_ptr(), logits.numel(), token.data_ptr(), _ptr(position),
+                                           table.data_ptr(), vocab, hidden, output.data_ptr(), _stream_ptr(stream)))
 
 
 def embedding_f16(table, token, output, stream=None) -> None:

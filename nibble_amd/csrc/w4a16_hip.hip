@@ -353,8 +353,10 @@ int launch_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w
 }
 
 // Fused M = 1 variants (RMSNorm prologue / residual / paired SiLU epilogue).
-// Rows of up to 8 loads (K <= 16384); launch shape: paired rows need R = 2
-// (4 wavefronts per workgroup), the others take the one-shot plan.
+// Rows of up to 8 loads (K <= 16384). Launch shapes from the decode-layer
+// sweeps: paired rows R = 2 with 8 wavefronts per workgroup; very wide
+// layers (N >= 16384, the lm_head) 4 rows per wavefront; the other RMSNorm
+// layers (q|k|v) 2 rows and 8 wavefronts; residual layers 1 row and 8.
 template <bool NORM, bool PAIRED>
 int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* norm_w, float eps,
                    const uint8_t* w, const w4a16::f16* s, const w4a16::f16* resid, w4a16::f16* o, int N, int K,
@@ -367,9 +369,9 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* n
     W4A16_PICK_L(RR, 1, WW) W4A16_PICK_L(RR, 2, WW) W4A16_PICK_L(RR, 3, WW) W4A16_PICK_L(RR, 4, WW)   \
     W4A16_PICK_L(RR, 5, WW) W4A16_PICK_L(RR, 6, WW) W4A16_PICK_L(RR, 7, WW) W4A16_PICK_L(RR, 8, WW)
     if constexpr (PAIRED) {
-        W4A16_PICK(2, 4)
+        W4A16_PICK(2, 8)
     } else {
-        W4A16_PICK(1, 8) W4A16_PICK(2, 4)
+        W4A16_PICK(1, 8) W4A16_PICK(2, 8) W4A16_PICK(4, 4)
     }
 #undef W4A16_PICK
 #undef W4A16_PICK_L
@@ -631,11 +633,18 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
     if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "eps must be non-negative");
     using w4a16::f16;
     const int L = oneshot_loads(K);
-    int R = 2, W = 4;
+    int R = 2, W = 8;
     if (!paired) {
-        const Plan p = plan_oneshot(1, K, 0);
-        R = p.rows;
-        W = p.splits;
+        if (N >= 16384) {
+            R = 4;
+            W = 4;
+        } else if (norm_weight != nullptr) {
+            R = 2;
+            W = 8;
+        } else {
+            R = 1;
+            W = 8;
+        }
     }
     const f16* x = static_cast<const f16*>(activations);
     const f16* nw = static_cast<const f16*>(norm_weight);

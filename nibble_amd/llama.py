@@ -211,6 +211,8 @@ class LlamaDecoder(torch.nn.Module):
         logits = self._forward(prompt, positions)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.fill_(prompt.numel())
+        if self.fused:
+            _lib.embedding_f16(self.embed, self.token, self.x_buf)   # the first decode step's input
         return self.token.clone()
 
     def _step(self) -> None:
@@ -223,10 +225,11 @@ class LlamaDecoder(torch.nn.Module):
         self.position.add_(1)
 
     def _step_fused(self) -> None:
-        """One decode step as 5 launches per layer (include/w4a16_decode.h)."""
+        """One decode step as 5 launches per layer plus 2 (include/w4a16_decode.h).
+        x_buf holds the current token's embedding on entry (prefill gathers the
+        first one); the final argmax gathers the next token's."""
         cfg = self.cfg
         x = self.x_buf
-        _lib.embedding_f16(self.embed, self.token, x)
         for i, b in enumerate(self.layers):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
@@ -240,7 +243,7 @@ class LlamaDecoder(torch.nn.Module):
             _lib.gemv_fused_f16(self.mlp_buf, b.down_proj.packed_weights, b.down_proj.scales, x, residual=x)
         _lib.gemv_fused_f16(x, self.lm_head.packed_weights, self.lm_head.scales, self.logits,
                             norm_weight=self.norm.weight, eps=self.norm.eps)
-        _lib.argmax_f16(self.logits, self.token, self.position)
+        _lib.argmax_embed_f16(self.logits, self.token, self.position, self.embed, x)
 
     @torch.inference_mode()
     def step(self) -> torch.Tensor:
@@ -252,8 +255,9 @@ class LlamaDecoder(torch.nn.Module):
     def capture(self) -> None:
         """Record one decode step in a HIP graph (after a warm-up eager step
         on a side stream so lazy initialisation is not captured). The KV cache
-        and position are restored afterwards."""
-        saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone())
+        position and the fused step's input row are restored afterwards."""
+        saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone(),
+                 self.x_buf.clone())
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
@@ -267,6 +271,7 @@ class LlamaDecoder(torch.nn.Module):
         self.v_cache.copy_(saved[1])
         self.token.copy_(saved[2])
         self.position.copy_(saved[3])
+        self.x_buf.copy_(saved[4])
 
     def replay(self) -> None:
         assert self.graph is not None, "call capture() first"

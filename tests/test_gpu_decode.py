@@ -106,9 +106,9 @@ def _tables(S: int, theta: float = 10000.0):
 
 
 @pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
-@pytest.mark.parametrize("pos", [0, 1, 17, 63, 64, 127])
+@pytest.mark.parametrize("pos", [0, 1, 17, 63, 64, 127, 200, 511])
 def test_decode_attention(gpu, heads, kv, pos):
-    S = 128
+    S = 512
     gen = torch.Generator().manual_seed(pos * 31 + heads)
     qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
     k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
@@ -179,6 +179,26 @@ def test_argmax_first_maximum_and_position(gpu, n):
     _lib.argmax_f16(logits.to(gpu), token)   # no position
     torch.cuda.synchronize()
     assert int(token) == int(torch.argmax(logits))
+
+
+def test_argmax_embed_gathers_next_row(gpu):
+    vocab, hidden = 1000, 2048
+    table = torch.randn((vocab, hidden)).to(torch.float16).to(gpu)
+    logits = torch.randn((vocab,)).to(torch.float16)
+    logits[777] = 50.0
+    token = torch.zeros((1,), dtype=torch.int64, device=gpu)
+    position = torch.tensor([3], dtype=torch.int64, device=gpu)
+    out = torch.zeros((hidden,), dtype=torch.float16, device=gpu)
+    _lib.argmax_embed_f16(logits.to(gpu), token, position, table, out)
+    torch.cuda.synchronize()
+    assert int(token) == 777 and int(position) == 4
+    assert torch.equal(out, table[777])
+    # misaligned logits take the scalar path
+    buf = torch.empty((vocab + 1,), dtype=torch.float16, device=gpu)
+    buf[1:] = logits.to(gpu)
+    _lib.argmax_embed_f16(buf[1:], token, None, table, out)
+    torch.cuda.synchronize()
+    assert int(token) == 777
 
 
 def test_embedding_gather(gpu):
