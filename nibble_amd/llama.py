@@ -61,6 +61,10 @@ class LlamaConfig:
 
 
 def _quantized(out_features: int, in_features: int, cfg: LlamaConfig, device, gen) -> QuantizedLinear:
+    """Random N(0, init_std) weights quantized RTN to INT4, or (gen is None)
+    uninitialised packed storage for a later load_state_dict."""
+    if gen is None:
+        return QuantizedLinear.empty(out_features, in_features, group_size=cfg.group_size, device=device)
     weight = torch.randn((out_features, in_features), device=device, generator=gen) * cfg.init_std
     packed, scales = quantize_and_pack_weights(weight, cfg.group_size)
     return QuantizedLinear(packed, scales, group_size=cfg.group_size)
@@ -146,21 +150,26 @@ class LlamaDecoder(torch.nn.Module):
     """Random-init Llama with INT4 linear layers, a static KV cache and greedy decode."""
 
     def __init__(self, cfg: LlamaConfig, device: str | torch.device = "cuda", seed: int = 0,
-                 fused: bool = True) -> None:
+                 fused: bool = True, init: str = "random") -> None:
+        """init="random": N(0, init_std) weights (seeded); init="empty":
+        uninitialised storage for load_state_dict (e.g. from
+        nibble_amd.model_checkpoint.decoder_from_checkpoint)."""
         super().__init__()
+        if init not in ("random", "empty"):
+            raise ValueError("init must be 'random' or 'empty'")
         self.cfg = cfg
         device = torch.device(device)
         # The fused step is HIP-only (CPU runs the torch ops) and built for
         # head_dim 64 and rows of K <= 16384.
         self.fused = (fused and device.type == "cuda" and cfg.head_dim == 64
                       and max(cfg.hidden_size, cfg.intermediate_size) <= 16384)
-        gen = torch.Generator(device=device).manual_seed(seed)
-        self.embed = torch.nn.Parameter(
-            (torch.randn((cfg.vocab_size, cfg.hidden_size), device=device, generator=gen) * cfg.init_std).to(
-                torch.float16
-            ),
-            requires_grad=False,
-        )
+        gen = torch.Generator(device=device).manual_seed(seed) if init == "random" else None
+        if gen is None:
+            table = torch.empty((cfg.vocab_size, cfg.hidden_size), dtype=torch.float16, device=device)
+        else:
+            table = (torch.randn((cfg.vocab_size, cfg.hidden_size), device=device, generator=gen)
+                     * cfg.init_std).to(torch.float16)
+        self.embed = torch.nn.Parameter(table, requires_grad=False)
         self.layers = torch.nn.ModuleList([Block(cfg, device, gen) for _ in range(cfg.num_layers)])
         self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device)
         self.lm_head = _quantized(cfg.vocab_size, cfg.hidden_size, cfg, device, gen)

