@@ -195,7 +195,8 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
         decode_s, prefill_s = sorted(decode_s[1:]), sorted(prefill_s[1:])
         return decode_s[len(decode_s) // 2], prefill_s[len(prefill_s) // 2]
 
-    unfused_s, _ = timed(False)
+    unfused_s, prefill_eager = timed(False)
+    model.capture_prefill(prompt_len)
     med, prefill = timed(True)
     return {
         "decode_tok_s": round((new_tokens - 1) / med, 1),
@@ -205,6 +206,9 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
                 "RMSNorm+gate|up GEMV+SiLU*up, down GEMV+residual per layer; RMSNorm+lm_head GEMV, argmax",
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
+        "prefill_eager_ms": round(prefill_eager * 1e3, 3),
+        "prefill": "16-token prompt: W4A16 op (one-shot MFMA kernel, M=16) for q|k|v, o, gate|up; dequantize + "
+                   "hipBLASLt for down (K=5632); torch ops between; prefill_ms replays it as one HIP graph",
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),
         "model": "random-init Llama 22L h2048 i5632 32q/4kv hd64 vocab32000, INT4 g128 on all 155 linears",

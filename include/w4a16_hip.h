@@ -41,7 +41,7 @@ extern "C" {
 #define W4A16_KERNEL_DIAG 4          /* M = 1 on fp16 MFMA, group dots on the 16x16 diagonal */
 #define W4A16_KERNEL_VALU_OFFSET 5   /* VALU kernel, decode without f16 fix-ups, per-chunk offset correction */
 #define W4A16_KERNEL_ONESHOT 6       /* VALU GEMV, every weight of a wavefront's rows requested at once (M <= 4) */
-#define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 8, K <= 8192) */
+#define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 16, K <= 8192) */
 
 /*
  * Fused W4A16 linear layer.
@@ -50,10 +50,14 @@ extern "C" {
  * activations: fp16 [M, K] row-major; packed_weights: uint8 [N, K/2];
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
- * takes the tuned kernels; anything else takes the generic kernel.
- * Environment, read at every call: W4A16_DECODE = auto|valu|valu_offset|mfma selects the
- * kernel family for M <= 8; W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per
- * wavefront of the VALU kernel (any other value is W4A16_ERR_CONFIG).
+ * takes the tuned kernels, and M = 9..16 the one-shot MFMA kernel when its
+ * activations fit in LDS (M*K*2 bytes, K <= 4096 at M = 16); anything else
+ * takes the generic kernel (the reference routes every M > 8 to its naive
+ * kernel).
+ * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
+ * valu_offset|mfma|mfma_oneshot selects the kernel family for M <= 8;
+ * W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront of the VALU
+ * kernels (any other value is W4A16_ERR_CONFIG).
  */
 int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights,
                      const void* scales, void* output, int64_t M, int64_t N,
@@ -120,8 +124,8 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
  *     1..8 with 8), max_blocks ignored.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
- * The VALU and MFMA families need group_size 128, M <= 8 and 16-byte aligned
- * activations and weights. No reference counterpart (the reference's
+ * The VALU and MFMA families need group_size 128, M <= 8 (16 for
+ * W4A16_KERNEL_MFMA_ONESHOT) and 16-byte aligned activations and weights. No reference counterpart (the reference's
  * W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
  */
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,

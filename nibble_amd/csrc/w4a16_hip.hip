@@ -171,7 +171,7 @@ constexpr int kMfmaOneshotMaxGroups = 64;
 
 bool mfma_oneshot_fits(int64_t M, int64_t K) {
     const int64_t G = K / 128;
-    return M >= 1 && M <= 8 && G >= 1 && G <= kMfmaOneshotMaxGroups &&
+    return M >= 1 && M <= 16 && G >= 1 && G <= kMfmaOneshotMaxGroups &&
            M * K * 2 + G * 64 + 2 * 8 * 1024 <= kMaxLdsBytes;
 }
 
@@ -201,7 +201,15 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         *out = Plan();
         return W4A16_OK;
     }
-    const bool tuned = G == 128 && M <= 8 && aligned16(act) && aligned16(packed);
+    const bool aligned = G == 128 && aligned16(act) && aligned16(packed);
+    // M = 9..16 (a short prompt) is one MFMA tile: the one-shot MFMA kernel
+    // when the activations fit in LDS, else the generic kernel as before.
+    if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_ONESHOT) &&
+        mfma_oneshot_fits(M, K)) {
+        *out = plan_mfma_oneshot(M, N, K);
+        return W4A16_OK;
+    }
+    const bool tuned = aligned && M <= 8;
     if (!tuned) {
         Plan p;
         p.kernel = W4A16_KERNEL_GENERIC;
@@ -389,7 +397,7 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* n
 int launch_mfma_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s, w4a16::f16* o,
                         int N, int K, hipStream_t stream) {
     using namespace w4a16;
-    if (M < 1 || M > 8) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel needs 1 <= M <= 8");
+    if (M < 1 || M > 16) return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel needs 1 <= M <= 16");
     const int G = K / 128;
     if (G < 1 || G > kMfmaOneshotMaxGroups)
         return fail(W4A16_ERR_CONFIG, "one-shot MFMA kernel: K must be a multiple of 128 up to 8192");
@@ -603,9 +611,11 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
         kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT ||
         kernel == W4A16_KERNEL_MFMA_ONESHOT) {
-        if (group_size != 128 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+        const int64_t max_m = kernel == W4A16_KERNEL_MFMA_ONESHOT ? 16 : 8;
+        if (group_size != 128 || M > max_m || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
-                        "VALU and MFMA kernels need group_size 128, M <= 8 and 16-byte aligned activations and weights");
+                        "VALU and MFMA kernels need group_size 128, M <= 8 (16 for the one-shot MFMA kernel) and "
+                        "16-byte aligned activations and weights");
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,

@@ -789,7 +789,8 @@ gemv_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------
-// One-shot MFMA kernel for small batches (runtime M = 1..8), G = 128.
+// One-shot MFMA kernel for small batches (runtime M = 1..16, one MFMA tile
+// of activation rows), G = 128.
 //
 // Workgroup = SK x SN wavefronts: SN blocks of 16 output rows, each block's
 // groups split over SK wavefronts (wavefront kw takes groups kw, kw + SK, ...,
@@ -904,7 +905,7 @@ gemv_mfma_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w, cons
         const int g = min(kw + SK * j, G - 1);
 #pragma unroll
         for (int t = 0; t < 4; ++t) av[t] = xs[((g * 4 + t) * 4 + q) * M + arow];
-        bv = *reinterpret_cast<const f32x4*>(base + g * 16 + ((4 * q) & 7));
+        bv = *reinterpret_cast<const f32x4*>(base + g * 16 + 4 * q);
     };
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     u32x4 A0[4], A1[4];

@@ -21,8 +21,11 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill (M = prompt length > 8) runs the HIP dequantize kernel + hipBLASLt.
-``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
+Prefill of a prompt of up to 16 tokens runs the W4A16 op itself (its
+one-shot MFMA kernel; q|k|v and gate|up as one op each) where the
+activations fit its LDS, and dequantize + hipBLASLt elsewhere (the 5632-wide
+down projection); ``capture_prefill(T)`` records a T-token prefill in a HIP
+graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.
 """
@@ -96,16 +99,44 @@ class Block(torch.nn.Module):
         self.gate_proj = _quantized(cfg.intermediate_size, h, cfg, device, gen)
         self.up_proj = _quantized(cfg.intermediate_size, h, cfg, device, gen)
         self.down_proj = _quantized(h, cfg.intermediate_size, cfg, device, gen)
+        # concatenated q|k|v and gate|up storage (set by LlamaDecoder)
+        self.qkv_packed = self.qkv_scales = self.gu_packed = self.gu_scales = None
+        self.native_prefill = True
+
+    def _native(self, x: torch.Tensor, packed: torch.Tensor) -> bool:
+        """Whether the W4A16 op itself (not dequantize + hipBLASLt) is the fast
+        path for these rows: GPU rows the op routes to a tuned kernel
+        (M <= 16 within the one-shot MFMA kernel's LDS)."""
+        if not (self.native_prefill and x.is_cuda and x.shape[0] <= 16):
+            return False
+        plan = _lib.plan_linear(x.data_ptr(), packed.data_ptr(), x.shape[0], packed.shape[0], x.shape[1],
+                                self.cfg.group_size)
+        return plan["kernel"] != "generic"
+
+    def _linear(self, mod: QuantizedLinear, x: torch.Tensor) -> torch.Tensor:
+        if self._native(x, mod.packed_weights):
+            return torch.ops.w4a16.linear(x, mod.packed_weights, mod.scales, self.cfg.group_size)
+        return mod(x)
 
     def forward(self, x, cos, sin, positions, k_cache, v_cache, mask):
         """x [T, H] fp16; positions [T] int64 (cache slots to write);
-        k_cache / v_cache [kv_heads, S, head_dim]; mask [T, S] additive fp32."""
+        k_cache / v_cache [kv_heads, S, head_dim]; mask [T, S] additive fp32.
+        With native_prefill on a GPU, short prompts run q|k|v and gate|up as
+        one W4A16 op each over the concatenated weights; otherwise every
+        projection is its QuantizedLinear."""
         cfg = self.cfg
         t = x.shape[0]
+        kv = cfg.num_kv_heads * cfg.head_dim
         h = self.input_norm(x)
-        q = self.q_proj(h).view(t, cfg.num_heads, cfg.head_dim)
-        k = self.k_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
-        v = self.v_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
+        if self.qkv_packed is not None and self._native(h, self.qkv_packed):
+            qkv = torch.ops.w4a16.linear(h, self.qkv_packed, self.qkv_scales, cfg.group_size)
+            q = qkv[:, : cfg.hidden_size].reshape(t, cfg.num_heads, cfg.head_dim)
+            k = qkv[:, cfg.hidden_size: cfg.hidden_size + kv].reshape(t, cfg.num_kv_heads, cfg.head_dim)
+            v = qkv[:, cfg.hidden_size + kv:].reshape(t, cfg.num_kv_heads, cfg.head_dim)
+        else:
+            q = self.q_proj(h).view(t, cfg.num_heads, cfg.head_dim)
+            k = self.k_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
+            v = self.v_proj(h).view(t, cfg.num_kv_heads, cfg.head_dim)
         q = _rope(q, cos, sin)
         k = _rope(k, cos, sin)
         k_cache.index_copy_(1, positions, k.transpose(0, 1).contiguous())
@@ -118,9 +149,14 @@ class Block(torch.nn.Module):
         scores = torch.matmul(qf, kf.transpose(1, 2).contiguous()) / math.sqrt(cfg.head_dim) + mask
         attn = torch.matmul(torch.softmax(scores, dim=-1), vf)          # [heads, T, d]
         attn = attn.transpose(0, 1).reshape(t, cfg.hidden_size).to(torch.float16)
-        x = x + self.o_proj(attn)
+        x = x + self._linear(self.o_proj, attn)
         h = self.post_norm(x)
-        x = x + self.down_proj(F.silu(self.gate_proj(h)) * self.up_proj(h))
+        if self.gu_packed is not None and self._native(h, self.gu_packed):
+            gu = torch.ops.w4a16.linear(h, self.gu_packed, self.gu_scales, cfg.group_size)
+            mlp = F.silu(gu[:, : cfg.intermediate_size]) * gu[:, cfg.intermediate_size:]
+        else:
+            mlp = F.silu(self.gate_proj(h)) * self.up_proj(h)
+        x = x + self._linear(self.down_proj, mlp)
         return x
 
 
@@ -185,9 +221,14 @@ class LlamaDecoder(torch.nn.Module):
         self.token = torch.zeros((1,), dtype=torch.int64, device=device)
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
+        self.prefill_graph: torch.cuda.CUDAGraph | None = None
+        self.prefill_tokens: torch.Tensor | None = None
+        self.prefill_positions: torch.Tensor | None = None
         # fused-step weights (views keep the per-module state-dict entries) and work buffers
         self.qkv = [_concat_rows([b.q_proj, b.k_proj, b.v_proj]) for b in self.layers]
         self.gate_up = [_concat_rows([b.gate_proj, b.up_proj]) for b in self.layers]
+        for b, (qw, qs), (gw, gs) in zip(self.layers, self.qkv, self.gate_up):
+            b.qkv_packed, b.qkv_scales, b.gu_packed, b.gu_scales = qw, qs, gw, gs
         h, kv = cfg.hidden_size, cfg.num_kv_heads * cfg.head_dim
         self.x_buf = torch.zeros((h,), dtype=torch.float16, device=device)
         self.qkv_buf = torch.zeros((h + 2 * kv,), dtype=torch.float16, device=device)
@@ -211,18 +252,47 @@ class LlamaDecoder(torch.nn.Module):
             x = layer(x, cos, sin, positions, self.k_cache[i], self.v_cache[i], mask)
         return self.lm_head(self.norm(x[-1:]))[0]
 
-    @torch.inference_mode()
-    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
-        """Run the prompt (int64 [T]); sets the next token and position; returns it."""
+    def _prefill(self, prompt: torch.Tensor, positions: torch.Tensor) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()
-        positions = torch.arange(prompt.numel(), device=prompt.device)
         logits = self._forward(prompt, positions)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.fill_(prompt.numel())
         if self.fused:
             _lib.embedding_f16(self.embed, self.token, self.x_buf)   # the first decode step's input
+
+    @torch.inference_mode()
+    def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
+        """Run the prompt (int64 [T]); sets the next token and position; returns
+        it. A prompt of the length captured by capture_prefill replays that graph."""
+        if self.prefill_graph is not None and prompt.numel() == self.prefill_tokens.numel():
+            self.prefill_tokens.copy_(prompt)
+            self.prefill_graph.replay()
+        else:
+            self._prefill(prompt, torch.arange(prompt.numel(), device=prompt.device))
         return self.token.clone()
+
+    @torch.inference_mode()
+    def capture_prefill(self, prompt_len: int) -> None:
+        """Record prefill of a prompt_len-token prompt in a HIP graph (the
+        prompt is copied into a static buffer before each replay). Resets the
+        KV cache, token and position like a prefill does."""
+        device = self.token.device
+        # Every tensor the graph reads must outlive it: the token and position
+        # buffers are attributes (a local allocated before the capture would be
+        # freed on return and its memory reused under the recorded kernels).
+        self.prefill_tokens = torch.zeros((prompt_len,), dtype=torch.int64, device=device)
+        self.prefill_positions = torch.arange(prompt_len, device=device)
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            self._prefill(self.prefill_tokens, self.prefill_positions)   # warm-up outside the capture
+        torch.cuda.current_stream().wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._prefill(self.prefill_tokens, self.prefill_positions)
+        torch.cuda.synchronize()
+        self.prefill_graph = graph
 
     def _step(self) -> None:
         if self.fused:

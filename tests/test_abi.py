@@ -113,7 +113,10 @@ ALIGNED = 1 << 20
         (5, 2048, 128, ALIGNED, "mfma_oneshot"),   # small batch, rows up to 4096 weights
         (8, 4096, 128, ALIGNED, "mfma_oneshot"),
         (8, 5632, 128, ALIGNED, "mfma"),           # K > 4096 with few rows: looped MFMA
-        (9, 2048, 128, ALIGNED, "generic"),    # above the small-batch range
+        (9, 2048, 128, ALIGNED, "mfma_oneshot"),   # a short prompt: one MFMA tile of rows
+        (16, 4096, 128, ALIGNED, "mfma_oneshot"),
+        (16, 5632, 128, ALIGNED, "generic"),       # activations beyond LDS
+        (17, 2048, 128, ALIGNED, "generic"),       # above one tile
         (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128
         (1, 2048, 128, ALIGNED + 2, "generic"),  # activations not 16-byte aligned
         (0, 2048, 128, ALIGNED, "none"),       # empty

@@ -285,3 +285,33 @@ def test_checkpoint_into_fused_decoder(gpu, tmp_path):
     dec.prefill(prompt)
     dec.capture()
     assert torch.equal(dec.generate(prompt, 6, use_graph=True), eager)
+
+
+def test_native_and_graphed_prefill(gpu):
+    """Prefill with the W4A16 op for the short prompt (one-shot MFMA kernel,
+    fused q|k|v and gate|up) matches the dequantize + hipBLASLt module path
+    (logits |err| <= 2e-2 (1 + |ref|), same next token), and the graphed
+    prefill reproduces the eager one exactly."""
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(_small_cfg(), device=gpu, seed=7)
+    prompt = torch.randint(0, 512, (16,), generator=torch.Generator().manual_seed(8)).to(gpu)
+    positions = torch.arange(16, device=gpu)
+    with torch.inference_mode():
+        for b in model.layers:
+            b.native_prefill = False
+        model.k_cache.zero_(); model.v_cache.zero_()
+        ref = model._forward(prompt, positions).float()
+        for b in model.layers:
+            b.native_prefill = True
+        model.k_cache.zero_(); model.v_cache.zero_()
+        got = model._forward(prompt, positions).float()
+    assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
+    eager_tok = model.prefill(prompt)
+    k_eager, x_eager = model.k_cache.clone(), model.x_buf.clone()
+    model.capture_prefill(16)
+    other = torch.randint(0, 512, (16,), generator=torch.Generator().manual_seed(9)).to(gpu)
+    model.prefill(other)                       # a replay on different tokens in between
+    assert torch.equal(model.prefill(prompt), eager_tok)
+    assert torch.equal(model.k_cache, k_eager) and torch.equal(model.x_buf, x_eager)
+    assert int(model.position) == 16

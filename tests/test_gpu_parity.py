@@ -129,11 +129,23 @@ def test_oneshot_variants(gpu, m, rows, splits, k, n):
 @pytest.mark.parametrize("rows,splits", [(1, 4), (2, 4), (1, 8), (2, 8)])
 @pytest.mark.parametrize("k,n", [(128, 7), (256, 40), (1152, 33), (2048, 2048), (3968, 21), (4096, 100),
                                  (4224, 9), (6144, 33), (8192, 64)])
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 11, 16])
 def test_mfma_oneshot_variants(gpu, m, rows, splits, k, n):
+    if m * k * 2 + (k // 128) * 64 + splits * rows * 1024 > 160 * 1024:
+        x, p, s = make_case(m, k, n, seed=1)
+        with pytest.raises(_lib.W4A16Error, match="do not fit in LDS"):
+            _run_tuned(gpu, x, p, s, MFMA_OS, rows, splits, 0)
+        return
     x, p, s = make_case(m, k, n, seed=m * 13 + k + n)
     out = _run_tuned(gpu, x, p, s, MFMA_OS, rows, splits, 0)
     assert_parity(out, expected(x, p, s), f"mfma_oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7)])
+def test_default_dispatch_short_prompt(gpu, m, k, n):
+    x, p, s = make_case(m, k, n, seed=m + k)
+    assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "mfma_oneshot"
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"prompt M={m} K={k} N={n}")
 
 
 def test_mfma_oneshot_rejects(gpu):
