@@ -142,15 +142,15 @@ int oneshot_loads(int64_t K) {
 }
 
 // Launch shape of the one-shot kernel, from the M = 1..4 sweeps over the
-// benchmark shapes: at M = 1, two rows per wavefront and 4 wavefronts per
-// workgroup when a row is 2, 4 or >= 12 loads (K 4096, 8192, 28672), else
-// one row and 8 wavefronts; M >= 2 always one row and 8 wavefronts (more
-// rows per workgroup share each staged copy of the activations).
+// benchmark shapes (offset decode): at M = 1, two rows per wavefront and 4
+// wavefronts per workgroup when a row is 2 or >= 12 loads (K 4096, 28672),
+// else one row and 8 wavefronts; M >= 2 always one row and 8 wavefronts
+// (more rows per workgroup share each staged copy of the activations).
 Plan plan_oneshot(int64_t M, int64_t K, int rows) {
     Plan p;
     p.kernel = W4A16_KERNEL_ONESHOT;
     p.unroll = oneshot_loads(K);
-    const bool pair = M == 1 && (p.unroll == 2 || p.unroll == 4 || p.unroll >= 12);
+    const bool pair = M == 1 && (p.unroll == 2 || p.unroll >= 12);
     if (rows > 0)
         p.rows = rows >= 2 ? 2 : 1;   // W4A16_ROWS_PER_WARP=4 runs as 2 rows in this kernel
     else
@@ -159,8 +159,15 @@ Plan plan_oneshot(int64_t M, int64_t K, int rows) {
     return p;
 }
 
+// LDS of the one-shot kernel: M*K fp16 activations, one fp32 offset bias per
+// 32-weight chunk of each activation row, and (RMSNorm prologue) one fp32
+// partial sum of squares per wavefront.
+int64_t oneshot_lds_bytes(int64_t M, int64_t K, bool norm) {
+    return M * K * 2 + M * (K / 32) * 4 + (norm ? 64 : 0);
+}
+
 bool oneshot_fits(int64_t M, int64_t K) {
-    return M >= 1 && M <= 4 && oneshot_loads(K) > 0 && M * K * 2 <= kMaxLdsBytes;
+    return M >= 1 && M <= 4 && oneshot_loads(K) > 0 && oneshot_lds_bytes(M, K, false) <= kMaxLdsBytes;
 }
 
 // One-shot MFMA kernel (rows up to 8192 weights, activations within LDS).
@@ -334,7 +341,7 @@ int launch_oneshot_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
                     "one-shot kernel: rows 1 or 2, splits 4 or 8, unroll one of 1..8, 10, 12, 14, 16");
-    const int lds = M * K * 2;
+    const int lds = (int)oneshot_lds_bytes(M, K, false);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "one-shot kernel: M*K activations do not fit in LDS");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
     if (rc != W4A16_OK) return rc;
@@ -384,7 +391,7 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* n
 #undef W4A16_PICK
 #undef W4A16_PICK_L
     if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "fused GEMV: no kernel for this launch shape");
-    const int lds = K * 2 + 64;   // activations + per-wavefront partial sums of squares
+    const int lds = (int)oneshot_lds_bytes(1, K, true);
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
     if (rc != W4A16_OK) return rc;
     const int tasks = PAIRED ? N / 2 : (N + R - 1) / R;

@@ -279,8 +279,18 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 // written to LDS unit-major (unit q of chunk c of row m at
 // xs[(m*4 + q) * C + c], conflict-free for lanes reading consecutive
 // chunks); after one barrier each wavefront consumes its weights in the
-// order they arrive. Decode and arithmetic are those of gemv_valu (exact
-// codes, v_dot2_f32_f16 per chunk, fp32 scale per chunk, DPP row sum).
+// order they arrive.
+//
+// Offset decode (unpack8_offset: one v_bitop3 per pair, no f16 fix-ups):
+// even-k codes arrive as 1024 + v and odd-k codes as 1024 + 16 v, v = s + 8.
+// The staged activations carry the odd-k halves pre-scaled by 1/16 (exact
+// for normal fp16), so each product is x s plus an offset 1032 x (even k)
+// or 72 x (odd k). Staging also stores, per chunk c of activation row m,
+// bias[m][c] = -(1032 sum_even x + 1152 sum_odd x/16) in fp32 (one quad of
+// lanes per chunk, DPP quad sum), and every chunk dot starts its
+// v_dot2_f32_f16 chain from that bias, so the chunk sum is sum x s up to
+// fp32 rounding of sums of magnitude ~1032 |x| (relative error ~1e-3 or
+// less on the outputs). Then the fp32 scale per chunk and a DPP row sum.
 //
 // Fused decode-step variants (M = 1 only; the plain op passes an empty
 // GemvFusion and NORM = PAIRED = false):
@@ -294,6 +304,27 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 //     weight pair and stores out[i] = fp16(silu(g) * u) with g, u, silu(g)
 //     each rounded to fp16 first, as fp16 tensors would be.
 // ---------------------------------------------------------------------------
+// One 16-byte activation unit for the offset decode: permuted to the
+// unpack8 pair order with the odd-k pairs (.y, .w) scaled by 1/16; `bias`
+// receives -(1032 sum_even x + 1152 sum_odd x/16) summed over the unit's DPP
+// quad (the four units of one 32-weight chunk). Every lane of the wavefront
+// must execute it (DPP), and the four lanes of a quad must hold the four
+// units of one chunk.
+__device__ __forceinline__ u32x4 stage_offset(u32x4 a, float& bias) {
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    u32x4 v = permute8(a);
+    const f16x2 e0 = as_f16x2(v.x), e1 = as_f16x2(v.z);
+    const f16x2 o0 = as_f16x2(v.y) * sixteenth, o1 = as_f16x2(v.w) * sixteenth;
+    v.y = as_u32(o0);
+    v.w = as_u32(o1);
+    float part = 1032.0f * (((float)e0.x + (float)e0.y) + ((float)e1.x + (float)e1.y)) +
+                 1152.0f * (((float)o0.x + (float)o0.y) + ((float)o1.x + (float)o1.y));
+    part += dpp<0xB1>(part);   // quad_perm [1,0,3,2]
+    part += dpp<0x4E>(part);   // quad_perm [2,3,0,1]
+    bias = -part;
+    return v;
+}
+
 struct GemvFusion {
     const f16* norm_weight;   // nullptr: no RMSNorm prologue
     float eps;
@@ -310,6 +341,7 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
     const int C = K >> 5;
     const int G = K >> 7;
+    float* cbias = reinterpret_cast<float*>(smem + (size_t)M * K * 2);   // [M][C], after xs
     const uint32_t row_bytes = (uint32_t)(K >> 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -374,9 +406,10 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     // keep every request above ahead of the first wait below
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. activations into LDS (RMS-normalised first when asked)
+    // 3. activations into LDS (RMS-normalised first when asked), with the
+    // per-chunk offset bias
     if (NORM) {
-        float* partial = reinterpret_cast<float*>(smem + (size_t)M * K * 2);   // W floats after xs
+        float* partial = cbias + M * C;   // W floats after the biases
         float ss = 0.0f;
 #pragma unroll
         for (int p = 0; p < kFirst; ++p) {
@@ -408,20 +441,29 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
             }
         }
     }
+    // unit i = (m, chunk c, quarter q) with q = i % 4: the four lanes of a
+    // DPP quad hold one chunk (T and 4C are multiples of 4), so the quad sum
+    // is that chunk's bias and every quad is wholly inside or past `units`
 #pragma unroll
     for (int p = 0; p < kFirst; ++p) {
         const int i = threadIdx.x + p * T;
+        float bias;
+        const u32x4 v = stage_offset(a[p], bias);
         if (i < units) {
             const int m = M == 1 ? 0 : i / units_per_row;
             const int u = i - m * units_per_row;
-            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(a[p]);
+            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = v;
+            if ((u & 3) == 0) cbias[m * C + (u >> 2)] = bias;
         }
     }
     if (kPer > kFirst) {
         for (int i = threadIdx.x + kFirst * T; i < units; i += T) {
             const int m = M == 1 ? 0 : i / units_per_row;
             const int u = i - m * units_per_row;
-            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = permute8(*reinterpret_cast<const u32x4*>(x + (size_t)i * 8));
+            float bias;
+            const u32x4 v = stage_offset(*reinterpret_cast<const u32x4*>(x + (size_t)i * 8), bias);
+            xs[(m * 4 + (u & 3)) * C + (u >> 2)] = v;
+            if ((u & 3) == 0) cbias[m * C + (u >> 2)] = bias;
         }
     }
     __syncthreads();
@@ -442,10 +484,10 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
             const int cc = min(c, C - 1);
             float d[M];
 #pragma unroll
-            for (int m = 0; m < M; ++m) d[m] = 0.0f;
+            for (int m = 0; m < M; ++m) d[m] = cbias[m * C + cc];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const Codes8 cw = unpack8(wv[r][j][q]);
+                const Codes8 cw = unpack8_offset(wv[r][j][q]);
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const u32x4 xv = xs[(m * 4 + q) * C + cc];

@@ -151,7 +151,7 @@ def test_oneshot_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     # (K, rows, waves per workgroup, loads per row)
-    for k, rows, splits, loads in [(2048, 1, 8, 1), (4096, 2, 4, 2), (5632, 1, 8, 3), (8192, 2, 4, 4),
+    for k, rows, splits, loads in [(2048, 1, 8, 1), (4096, 2, 4, 2), (5632, 1, 8, 3), (8192, 1, 8, 4),
                                    (14336, 1, 8, 7), (18432, 1, 8, 10), (28672, 2, 4, 14), (32768, 2, 4, 16),
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
