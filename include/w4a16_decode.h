@@ -66,6 +66,30 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache,
                                int64_t head_dim, int64_t max_seq_len, void* stream);
 
 /*
+ * Attention of one new token fused with the o projection and the residual
+ * add, for positions below 64 (one chunk of cache slots):
+ *   attn = softmax(q k^T / 8) v as w4a16_decode_attention_f16 (same qkv
+ *     layout, caches and append), except that cos / sin of
+ *     position * inv_freq[i] (inv_freq: 32 fp32, i < 32) are computed in
+ *     the kernel instead of read from tables;
+ *   residual[n] = fp16(residual[n] + fp16(o_packed[n] . attn)), n < hidden,
+ *     with the o projection [hidden, num_heads * 64] INT4 group 128.
+ * Needs head_dim 64, num_kv_heads 1, 2, 4 or 8, num_heads / num_kv_heads <= 16,
+ * num_heads * 64 <= 4096, group_size 128, 16-byte aligned qkv, caches and
+ * o_packed. A position outside [0, min(max_seq_len, 64)) writes NaN to every
+ * residual row and leaves the caches alone.
+ * Replaces (reference): HF LlamaAttention (rotary, static-cache update,
+ * sdpa) + o_proj QuantizedLinear + residual add of one decoder layer in the
+ * decode loop of scripts/generate.py:260-305 (w4a16/linear.py:154-200 for
+ * the o_proj call).
+ */
+int w4a16_attention_o_f16(const void* qkv, void* k_cache, void* v_cache, const float* inv_freq,
+                          const int64_t* position, const uint8_t* o_packed, const void* o_scales,
+                          void* residual, int64_t num_heads, int64_t num_kv_heads,
+                          int64_t head_dim, int64_t max_seq_len, int64_t hidden,
+                          int64_t group_size, void* stream);
+
+/*
  * Greedy token: *token = first index of the maximum of logits[0..n) (fp16);
  * if position != NULL, *position += 1.
  * Replaces (reference): the greedy pick of HF generate(do_sample=False),

@@ -63,6 +63,7 @@ DECODE_SIGNATURES = {
         [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp],
     ),
     "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
+    "w4a16_attention_o_f16": (ctypes.c_int, [_vp] * 8 + [_i64] * 6 + [_vp]),
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
@@ -195,6 +196,20 @@ def decode_attention_f16(qkv, k_cache, v_cache, cos_table, sin_table, position, 
             qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
             position.data_ptr(), output.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2],
             _stream_ptr(stream),
+        )
+    )
+
+
+def attention_o_f16(qkv, k_cache, v_cache, inv_freq, position, o_packed, o_scales, residual, num_heads: int,
+                    num_kv_heads: int, head_dim: int = 64, group_size: int = 128, stream=None) -> None:
+    """``w4a16_attention_o_f16``: one layer's attention of the new token (caches
+    [kv_heads, S, head_dim], position < 64) fused with the o projection;
+    residual [hidden] += o(attn) in fp16."""
+    _raise_on(
+        lib().w4a16_attention_o_f16(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), inv_freq.data_ptr(), position.data_ptr(),
+            o_packed.data_ptr(), o_scales.data_ptr(), residual.data_ptr(), num_heads, num_kv_heads, head_dim,
+            k_cache.shape[-2], residual.numel(), group_size, _stream_ptr(stream),
         )
     )
 

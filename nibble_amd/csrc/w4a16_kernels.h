@@ -112,17 +112,6 @@ __device__ __forceinline__ void valu_load(ValuStep<M, R, U>& b, const uint8_t* _
     }
 }
 
-// Decode without f16 fix-ups for the offset path: pairs (0,4) (2,6) as
-// 1024 + v and pairs (1,5) (3,7) as 1024 + 16 v, v = s + 8.
-__device__ __forceinline__ Codes8 unpack8_offset(uint32_t word) {
-    const uint32_t v = word >> 8;
-    Codes8 c;
-    c.p[0] = as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x000F000Fu, 0x64086408u, 0x6A));
-    c.p[1] = as_f16x2(__builtin_amdgcn_bitop3_b32(word, 0x00F000F0u, 0x64806480u, 0x6A));
-    c.p[2] = as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x000F000Fu, 0x64086408u, 0x6A));
-    c.p[3] = as_f16x2(__builtin_amdgcn_bitop3_b32(v, 0x00F000F0u, 0x64806480u, 0x6A));
-    return c;
-}
 
 // One step of U chunks per row. Exact path: unpack8 (codes exact in f16),
 // dot2 into one fp32 sum per chunk. Offset path (OFFSET): dot2 of the
@@ -304,26 +293,6 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 //     weight pair and stores out[i] = fp16(silu(g) * u) with g, u, silu(g)
 //     each rounded to fp16 first, as fp16 tensors would be.
 // ---------------------------------------------------------------------------
-// One 16-byte activation unit for the offset decode: permuted to the
-// unpack8 pair order with the odd-k pairs (.y, .w) scaled by 1/16; `bias`
-// receives -(1032 sum_even x + 1152 sum_odd x/16) summed over the unit's DPP
-// quad (the four units of one 32-weight chunk). Every lane of the wavefront
-// must execute it (DPP), and the four lanes of a quad must hold the four
-// units of one chunk.
-__device__ __forceinline__ u32x4 stage_offset(u32x4 a, float& bias) {
-    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
-    u32x4 v = permute8(a);
-    const f16x2 e0 = as_f16x2(v.x), e1 = as_f16x2(v.z);
-    const f16x2 o0 = as_f16x2(v.y) * sixteenth, o1 = as_f16x2(v.w) * sixteenth;
-    v.y = as_u32(o0);
-    v.w = as_u32(o1);
-    float part = 1032.0f * (((float)e0.x + (float)e0.y) + ((float)e1.x + (float)e1.y)) +
-                 1152.0f * (((float)o0.x + (float)o0.y) + ((float)o1.x + (float)o1.y));
-    part += dpp<0xB1>(part);   // quad_perm [1,0,3,2]
-    part += dpp<0x4E>(part);   // quad_perm [2,3,0,1]
-    bias = -part;
-    return v;
-}
 
 struct GemvFusion {
     const f16* norm_weight;   // nullptr: no RMSNorm prologue

@@ -15,7 +15,11 @@ by default: per layer, (1) RMSNorm + q|k|v GEMV over the concatenated
 projection, (2) rotary embedding + KV-cache append + attention, (3) o GEMV +
 residual, (4) RMSNorm + gate|up GEMV with the SiLU-multiply epilogue, (5)
 down GEMV + residual; then RMSNorm + lm_head GEMV and the greedy argmax,
-which also advances the position: 5 launches per layer. The q/k/v and
+which also advances the position: 5 launches per layer. While the position
+is below 64 (and the head layout allows it), (2) and (3) are one launch
+(``w4a16_attention_o_f16``: every o-projection workgroup recomputes the
+one-chunk attention on the matrix cores), so a step is 4 launches per layer;
+the host tracks the position to pick that step. The q/k/v and
 gate/up weights live in one buffer each, and every ``QuantizedLinear`` keeps
 a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
@@ -186,10 +190,12 @@ class LlamaDecoder(torch.nn.Module):
     """Random-init Llama with INT4 linear layers, a static KV cache and greedy decode."""
 
     def __init__(self, cfg: LlamaConfig, device: str | torch.device = "cuda", seed: int = 0,
-                 fused: bool = True, init: str = "random") -> None:
+                 fused: bool = True, init: str = "random", fuse_attention_o: bool = True) -> None:
         """init="random": N(0, init_std) weights (seeded); init="empty":
         uninitialised storage for load_state_dict (e.g. from
-        nibble_amd.model_checkpoint.decoder_from_checkpoint)."""
+        nibble_amd.model_checkpoint.decoder_from_checkpoint).
+        fuse_attention_o=False keeps attention and the o GEMV as two launches
+        at every position."""
         super().__init__()
         if init not in ("random", "empty"):
             raise ValueError("init must be 'random' or 'empty'")
@@ -199,6 +205,11 @@ class LlamaDecoder(torch.nn.Module):
         # head_dim 64 and rows of K <= 16384.
         self.fused = (fused and device.type == "cuda" and cfg.head_dim == 64
                       and max(cfg.hidden_size, cfg.intermediate_size) <= 16384)
+        # attention + o projection as one launch (positions < 64): head layouts
+        # the kernel supports
+        self.attn_o = (self.fused and fuse_attention_o and cfg.num_kv_heads in (1, 2, 4, 8)
+                       and cfg.num_heads % cfg.num_kv_heads == 0 and cfg.num_heads // cfg.num_kv_heads <= 16
+                       and cfg.num_heads * cfg.head_dim <= 4096 and cfg.group_size == 128)
         gen = torch.Generator(device=device).manual_seed(seed) if init == "random" else None
         if gen is None:
             table = torch.empty((cfg.vocab_size, cfg.hidden_size), dtype=torch.float16, device=device)
@@ -213,6 +224,7 @@ class LlamaDecoder(torch.nn.Module):
         angles = torch.outer(torch.arange(cfg.max_seq_len, device=device).float(), inv_freq)
         self.register_buffer("cos", angles.cos(), persistent=False)
         self.register_buffer("sin", angles.sin(), persistent=False)
+        self.register_buffer("inv_freq", inv_freq, persistent=False)
         shape = (cfg.num_layers, cfg.num_kv_heads, cfg.max_seq_len, cfg.head_dim)
         self.register_buffer("k_cache", torch.zeros(shape, dtype=torch.float16, device=device), persistent=False)
         self.register_buffer("v_cache", torch.zeros(shape, dtype=torch.float16, device=device), persistent=False)
@@ -221,6 +233,8 @@ class LlamaDecoder(torch.nn.Module):
         self.token = torch.zeros((1,), dtype=torch.int64, device=device)
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
+        self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
+        self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
         self.prefill_tokens: torch.Tensor | None = None
         self.prefill_positions: torch.Tensor | None = None
@@ -270,6 +284,7 @@ class LlamaDecoder(torch.nn.Module):
             self.prefill_graph.replay()
         else:
             self._prefill(prompt, torch.arange(prompt.numel(), device=prompt.device))
+        self.host_position = prompt.numel()
         return self.token.clone()
 
     @torch.inference_mode()
@@ -294,19 +309,26 @@ class LlamaDecoder(torch.nn.Module):
         torch.cuda.synchronize()
         self.prefill_graph = graph
 
-    def _step(self) -> None:
+    def short_step(self) -> bool:
+        """Whether the next step (at host_position) takes the attention + o
+        launch, which covers positions below 64."""
+        return self.attn_o and self.host_position < min(64, self.cfg.max_seq_len)
+
+    def _step(self, short: bool | None = None) -> None:
         if self.fused:
-            self._step_fused()
+            self._step_fused(self.short_step() if short is None else short)
             return
         logits = self._forward(self.token, self.position)
         self.logits.copy_(logits)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.add_(1)
 
-    def _step_fused(self) -> None:
-        """One decode step as 5 launches per layer plus 2 (include/w4a16_decode.h).
-        x_buf holds the current token's embedding on entry (prefill gathers the
-        first one); the final argmax gathers the next token's."""
+    def _step_fused(self, short: bool = False) -> None:
+        """One decode step as 5 launches per layer plus 2 (include/w4a16_decode.h),
+        4 per layer when `short` (attention + o projection in one launch; the
+        position must then be below 64). x_buf holds the current token's
+        embedding on entry (prefill gathers the first one); the final argmax
+        gathers the next token's."""
         cfg = self.cfg
         x = self.x_buf
         for i, b in enumerate(self.layers):
@@ -314,9 +336,15 @@ class LlamaDecoder(torch.nn.Module):
             gu_w, gu_s = self.gate_up[i]
             _lib.gemv_fused_f16(x, qkv_w, qkv_s, self.qkv_buf, norm_weight=b.input_norm.weight,
                                 eps=b.input_norm.eps)
-            _lib.decode_attention_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.cos, self.sin,
-                                      self.position, self.attn_buf, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
-            _lib.gemv_fused_f16(self.attn_buf, b.o_proj.packed_weights, b.o_proj.scales, x, residual=x)
+            if short:
+                _lib.attention_o_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.inv_freq, self.position,
+                                     b.o_proj.packed_weights, b.o_proj.scales, x, cfg.num_heads, cfg.num_kv_heads,
+                                     cfg.head_dim, cfg.group_size)
+            else:
+                _lib.decode_attention_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.cos, self.sin,
+                                          self.position, self.attn_buf, cfg.num_heads, cfg.num_kv_heads,
+                                          cfg.head_dim)
+                _lib.gemv_fused_f16(self.attn_buf, b.o_proj.packed_weights, b.o_proj.scales, x, residual=x)
             _lib.gemv_fused_f16(x, gu_w, gu_s, self.mlp_buf, norm_weight=b.post_norm.weight, eps=b.post_norm.eps,
                                 paired=True)
             _lib.gemv_fused_f16(self.mlp_buf, b.down_proj.packed_weights, b.down_proj.scales, x, residual=x)
@@ -328,33 +356,56 @@ class LlamaDecoder(torch.nn.Module):
     def step(self) -> torch.Tensor:
         """One eager decode step; returns the new token."""
         self._step()
+        self.host_position += 1
         return self.token.clone()
 
-    @torch.inference_mode()
-    def capture(self) -> None:
-        """Record one decode step in a HIP graph (after a warm-up eager step
-        on a side stream so lazy initialisation is not captured). The KV cache
-        position and the fused step's input row are restored afterwards."""
-        saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone(),
-                 self.x_buf.clone())
+    def _capture_step(self, short: bool) -> torch.cuda.CUDAGraph:
+        """A decode step in a HIP graph, after a warm-up eager step on a side
+        stream so lazy initialisation is not captured."""
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
-            self._step()
+            self._step(short)
         torch.cuda.current_stream().wait_stream(stream)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._step()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._step(short)
         torch.cuda.synchronize()
-        self.k_cache.copy_(saved[0])
-        self.v_cache.copy_(saved[1])
-        self.token.copy_(saved[2])
-        self.position.copy_(saved[3])
-        self.x_buf.copy_(saved[4])
+        return graph
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        """Record the decode step in HIP graphs: the general one and, when the
+        attention + o launch applies, the step for positions below 64. The KV
+        cache, position and the fused step's input row are restored afterwards
+        (capturing runs steps)."""
+        saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone(),
+                 self.x_buf.clone())
+
+        def restore():
+            self.k_cache.copy_(saved[0])
+            self.v_cache.copy_(saved[1])
+            self.token.copy_(saved[2])
+            self.position.copy_(saved[3])
+            self.x_buf.copy_(saved[4])
+
+        self.graph = self._capture_step(False)
+        restore()
+        if self.attn_o:
+            # the warm-up step must see a position the short step accepts
+            self.position.fill_(min(self.host_position, min(64, self.cfg.max_seq_len) - 1))
+            self.graph_short = self._capture_step(True)
+            restore()
+        torch.cuda.synchronize()
 
     def replay(self) -> None:
+        """One decode step: the captured graph for the current position."""
         assert self.graph is not None, "call capture() first"
-        self.graph.replay()
+        if self.graph_short is not None and self.short_step():
+            self.graph_short.replay()
+        else:
+            self.graph.replay()
+        self.host_position += 1
 
     @torch.inference_mode()
     def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True) -> torch.Tensor:

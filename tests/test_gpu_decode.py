@@ -161,6 +161,134 @@ def test_decode_attention_position_out_of_range(gpu):
         assert not kd.any() and not vd.any()
 
 
+# ------------------------------------------------ attention + o projection ----
+def _inv_freq(theta: float = 10000.0) -> torch.Tensor:
+    return 1.0 / (theta ** (torch.arange(0, 64, 2).float() / 64))
+
+
+def _attention_ref(qkv, k_cache, v_cache, pos, heads, kv):
+    """float64 attention of the new token with cos / sin of the fp32 angle
+    pos * inv_freq (as the kernel forms it); returns (attn [heads*64] float64,
+    rotated k_new fp16, v_new fp16)."""
+    ang = (torch.tensor(float(pos)) * _inv_freq()).double()
+    c, s_ = ang.cos(), ang.sin()
+    q = _rope64(qkv[: heads * 64].view(heads, 64), c, s_).to(torch.float16).double()
+    k_new = _rope64(qkv[heads * 64: (heads + kv) * 64].view(kv, 64), c, s_).to(torch.float16)
+    v_new = qkv[(heads + kv) * 64:].view(kv, 64)
+    kc, vc = k_cache.clone(), v_cache.clone()
+    kc[:, pos], vc[:, pos] = k_new, v_new
+    group = heads // kv
+    kf = kc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    vf = vc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    scores = torch.einsum("hd,hsd->hs", q, kf) / math.sqrt(64)
+    attn = torch.einsum("hs,hsd->hd", torch.softmax(scores, dim=-1), vf).reshape(-1)
+    return attn, k_new, v_new
+
+
+_DIAG = 7 * float(torch.tensor(1.0 / 7.0, dtype=torch.float16))   # code 7 x fp16(1/7)
+
+
+def _identity_o(n: int):
+    """INT4 packing of _DIAG times the n x n identity (code 7, every scale
+    fp16(1/7): the magnitudes of a real layer, where the offset decode's fp32
+    rounding is ~1e-3 of a chunk's activations times the scale)."""
+    codes = torch.zeros((n, n), dtype=torch.int8)
+    codes[torch.arange(n), torch.arange(n)] = 7
+    lo, hi = codes[:, 0::2].to(torch.uint8) & 0xF, codes[:, 1::2].to(torch.uint8) & 0xF
+    return lo | (hi << 4), torch.full((n, n // 128), 1.0 / 7.0, dtype=torch.float16)
+
+
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 2), (4, 1), (64, 8), (16, 1)])
+@pytest.mark.parametrize("pos,S", [(0, 48), (1, 48), (17, 48), (47, 48), (63, 64), (40, 512), (63, 512)])
+def test_attention_o_identity_projection(gpu, heads, kv, pos, S):
+    """With o = _DIAG x identity and a zero residual the output is the
+    attention row itself times _DIAG (rounded to fp16): the bar of the
+    attention test, |err| <= 2e-3 + 1e-2 |ref|; slots past the position hold
+    NaN, which must not leak in; the cache gains exactly slot pos."""
+    gen = torch.Generator().manual_seed(pos * 131 + heads + S)
+    qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    k_cache[:, pos + 1:] = float("nan")
+    v_cache[:, pos + 1:] = float("nan")
+    ref, k_new, v_new = _attention_ref(qkv, k_cache, v_cache, pos, heads, kv)
+    ref = ref * _DIAG
+    n = heads * 64
+    op, os_ = _identity_o(n)
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    resid = torch.zeros((n,), dtype=torch.float16, device=gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] attention_o identity heads={heads} kv={kv} pos={pos} S={S}", flush=True)
+    _lib.attention_o_f16(qkv.to(gpu), kd, vd, _inv_freq().to(gpu), position, op.to(gpu), os_.to(gpu), resid,
+                         heads, kv)
+    torch.cuda.synchronize()
+    got = resid.double().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs()), float(err.max())
+    kg, vg = kd.cpu(), vd.cpu()
+    others = [t for t in range(S) if t != pos]
+    assert torch.equal(kg[:, others].isnan(), k_cache[:, others].isnan())
+    fin = [t for t in others if t < pos]
+    assert torch.equal(kg[:, fin], k_cache[:, fin]) and torch.equal(vg[:, fin], v_cache[:, fin])
+    assert torch.equal(vg[:, pos], v_new)
+    assert torch.allclose(kg[:, pos].float(), k_new.float(), rtol=2 ** -10, atol=2 ** -14)
+
+
+@pytest.mark.parametrize("heads,kv,hidden", [(32, 4, 2048), (8, 2, 300), (64, 8, 1000)])
+@pytest.mark.parametrize("pos", [5, 47])
+def test_attention_o_projection_and_residual(gpu, heads, kv, hidden, pos):
+    """Random INT4 o projection (CPU oracle on the fp16-rounded attention row)
+    plus a residual: out = fp16(resid + fp16(o . attn)), |err| <= 1e-2 (1 + |ref|)."""
+    S = 48
+    gen = torch.Generator().manual_seed(pos + hidden)
+    qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    attn, _, _ = _attention_ref(qkv, k_cache, v_cache, pos, heads, kv)
+    _, op, os_ = make_case(1, heads * 64, hidden, seed=hidden)
+    resid = torch.randn((hidden,), generator=gen).to(torch.float16)
+    ref = _f16(resid.float().numpy() + _f16(_linear_ref(attn.to(torch.float16), op, os_)))
+    out = resid.to(gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] attention_o projection heads={heads} kv={kv} hidden={hidden} pos={pos}", flush=True)
+    _lib.attention_o_f16(qkv.to(gpu), k_cache.to(gpu), v_cache.to(gpu), _inv_freq().to(gpu), position, op.to(gpu),
+                         os_.to(gpu), out, heads, kv)
+    torch.cuda.synchronize()
+    assert_parity(out.view(1, hidden), ref.reshape(1, hidden), f"attention_o heads={heads} hidden={hidden}")
+
+
+def test_attention_o_position_out_of_range(gpu):
+    heads, kv = 8, 2
+    qkv = torch.randn(((heads + 2 * kv) * 64,)).to(torch.float16).to(gpu)
+    op, os_ = _identity_o(heads * 64)
+    op, os_ = op.to(gpu), os_.to(gpu)
+    for S, bad in ((48, 48), (48, -1), (128, 64), (128, 100)):
+        kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+        vd = torch.zeros_like(kd)
+        resid = torch.zeros((heads * 64,), dtype=torch.float16, device=gpu)
+        position = torch.tensor([bad], dtype=torch.int64, device=gpu)
+        print(f"[case] attention_o out of range S={S} pos={bad}", flush=True)
+        _lib.attention_o_f16(qkv, kd, vd, _inv_freq().to(gpu), position, op, os_, resid, heads, kv)
+        torch.cuda.synchronize()
+        assert torch.isnan(resid).all()
+        assert not kd.any() and not vd.any()
+
+
+def test_attention_o_rejects(gpu):
+    t = torch.zeros((4096,), dtype=torch.float16, device=gpu)
+    cache = torch.zeros((3, 16, 64), dtype=torch.float16, device=gpu)
+    pos = torch.zeros((1,), dtype=torch.int64, device=gpu)
+    inv = _inv_freq().to(gpu)
+    w = torch.zeros((64, 64), dtype=torch.uint8, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="num_kv_heads"):
+        _lib.attention_o_f16(t, cache, cache, inv, pos, w, t, t[:64], 6, 3)
+    with pytest.raises(_lib.W4A16Error, match="head_dim"):
+        _lib.attention_o_f16(t, cache, cache, inv, pos, w, t, t[:64], 4, 2, head_dim=128)
+    with pytest.raises(_lib.W4A16Error, match="at most 16"):
+        _lib.attention_o_f16(t, cache, cache, inv, pos, w, t, t[:64], 34, 2)
+
+
 # ------------------------------------------------------- argmax, embedding ----
 @pytest.mark.parametrize("n", [1, 1000, 32000, 50257])
 def test_argmax_first_maximum_and_position(gpu, n):
@@ -247,6 +375,51 @@ def test_fused_step_matches_torch_step(gpu):
     # the new cache slot holds the same k (rotary within fp16 rounding)
     p = int(state[3])
     assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
+
+
+def test_attention_o_step_matches_two_launch_step(gpu):
+    """From the same state, the step with attention + o as one launch and the
+    step with separate attention and o GEMV launches agree (logits
+    |err| <= 2e-2 (1 + |ref|), same new token, same cache slot within fp16
+    rounding)."""
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(_small_cfg(), device=gpu, seed=4)
+    assert model.attn_o
+    prompt = torch.randint(0, 512, (20,), generator=torch.Generator().manual_seed(9)).to(gpu)
+    model.prefill(prompt)
+    state = (model.k_cache.clone(), model.v_cache.clone(), model.token.clone(), model.position.clone(),
+             model.x_buf.clone())
+    with torch.inference_mode():
+        model._step(short=False)
+        ref_logits, ref_k, ref_tok = model.logits.clone(), model.k_cache.clone(), model.token.clone()
+        for t, s in zip((model.k_cache, model.v_cache, model.token, model.position, model.x_buf), state):
+            t.copy_(s)
+        model._step(short=True)
+    torch.cuda.synchronize()
+    got, ref = model.logits.float().cpu(), ref_logits.float().cpu()
+    assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
+    assert torch.equal(model.token, ref_tok)
+    p = int(state[3])
+    assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
+
+
+def test_decode_graphs_across_position_64(gpu):
+    """Generation that crosses position 64 switches from the attention + o
+    graph to the general one; graph replays equal eager decode (which switches
+    at the same step)."""
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1280, num_layers=2, num_heads=8,
+                      num_kv_heads=2, head_dim=64, max_seq_len=96)
+    model = LlamaDecoder(cfg, device=gpu, seed=11)
+    prompt = torch.randint(0, 512, (58,), generator=torch.Generator().manual_seed(12)).to(gpu)
+    eager = model.generate(prompt, 12, use_graph=False)
+    model.prefill(prompt)
+    model.capture()
+    assert model.graph_short is not None
+    assert torch.equal(model.generate(prompt, 12, use_graph=True), eager)
+    assert model.host_position == 58 + 11 and int(model.position) == 58 + 11
 
 
 def test_fused_decode_graph_matches_eager(gpu):
