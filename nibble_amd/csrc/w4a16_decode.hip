@@ -19,7 +19,8 @@
 namespace w4a16 {
 
 // ---------------------------------------------------------------------------
-// Attention of one new token, one wavefront per query head (head_dim 64).
+// Attention of one new token, one workgroup of WA wavefronts per query head
+// (head_dim 64).
 //
 // Inputs: qkv = [q (H x 64) | k (KV x 64) | v (KV x 64)] fp16 from the fused
 // QKV projection; caches [KV, S, 64] fp16; cos / sin [S, 32] fp32 tables;
@@ -30,40 +31,68 @@ namespace w4a16 {
 //      query head of each KV group writes k and v to slot p, and every head
 //      uses its own copy of slot p (never the cache line another workgroup
 //      is writing);
-//   2. slots 0..p in chunks of 64: lane t holds slot c0 + t's key row (8
-//      16-byte loads, all requested before any is used) and its score
-//      q.k / 8 in fp32; the chunk's value rows go to LDS (coalesced 16-byte
-//      loads); an online softmax (running max, rescaled sum and output)
-//      folds the chunk in, and lane d accumulates sum_t prob_t v_t[d];
-//   3. out[d] = acc / sum, rounded to fp16.
-// Slots past p are masked (weight exactly 0, as exp(-inf) is). A position
-// outside [0, S) writes NaN to the head's output and touches no cache slot.
+//   2. slots 0..p in chunks of 64, wavefront w taking chunks w, w + WA, ...:
+//      lane t holds slot c0 + t's key row (8 16-byte loads, requested before
+//      any is used) and its score q.k / 8 in fp32; the chunk's value rows go
+//      to the wavefront's LDS tile (coalesced 16-byte loads, rows past p
+//      zeroed); an online softmax (running max, rescaled sum and output; DPP
+//      reductions) folds the chunk in, and lane d accumulates
+//      sum_t prob_t v_t[d]. The next chunk's rows are requested before the
+//      current chunk's reductions;
+//   3. the WA partial states (max m_w, sum l_w, output o_w) combine as
+//      out[d] = sum_w o_w[d] e^(m_w - M) / sum_w l_w e^(m_w - M), rounded to
+//      fp16 (a wavefront with no chunk has l_w = 0 and drops out).
+// Slots past p get weight exactly 0. A position outside [0, S) writes NaN
+// to the head's output and touches no cache slot. Every load that does not
+// depend on the position (cache rows of each wavefront's first chunk, q, k,
+// v) is requested before the position arrives.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(64)
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    // LDS operations of one wavefront complete in order; this only keeps the
+    // compiler from moving LDS accesses across the point
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int WA>
+__global__ void __launch_bounds__(64 * WA)
 decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
                  const float* __restrict__ cos_table, const float* __restrict__ sin_table,
                  const int64_t* __restrict__ position, f16* __restrict__ out, int num_heads, int num_kv, int S) {
     constexpr int D = 64;
-    __shared__ float qs[D];
-    __shared__ float probs[64];
-    __shared__ __align__(16) f16 vt[64 * D];   // value rows of the current chunk
+    __shared__ __align__(16) float qs_all[WA][D];
+    __shared__ __align__(16) f16 knew_all[WA][D];
+    __shared__ __align__(16) f16 vnew_all[WA][D];
+    __shared__ __align__(16) float probs[WA][64];
+    __shared__ __align__(16) f16 vt[WA][64 * D];
+    __shared__ float wmax[WA], wsum[WA];
+    __shared__ float wacc[WA][D];
 
+    const int64_t p64 = position[0];
+    __builtin_amdgcn_sched_barrier(0);
     const int hq = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int group = num_heads / num_kv;
     const int hk = hq / group;
-    const int64_t p64 = position[0];
-    if (p64 < 0 || p64 >= S) {
-        out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
-        return;
-    }
-    const int p = (int)p64;
     const f16* kc = k_cache + (size_t)hk * S * D;
     const f16* vc = v_cache + (size_t)hk * S * D;
 
-    // first chunk's cache rows, requested before the rotary work
-    auto load_k = [&](u32x4 (&kr)[8], int t) {
-        const u32x4* row = reinterpret_cast<const u32x4*>(kc + (size_t)min(t, S - 1) * D);
+    auto load_k = [&](u32x4 (&kr)[8], int c0) {
+        const u32x4* row = reinterpret_cast<const u32x4*>(kc + (size_t)min(c0 + lane, S - 1) * D);
 #pragma unroll
         for (int e = 0; e < 8; ++e) kr[e] = row[e];
     };
@@ -76,39 +105,46 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
         }
     };
     u32x4 kr[8], vr[8];
-    load_k(kr, lane);
-    load_v(vr, 0);
-
-    const float c = cos_table[(size_t)p * (D / 2) + (lane & 31)];
-    const float s = sin_table[(size_t)p * (D / 2) + (lane & 31)];
+    int c0 = 64 * wave;
+    load_k(kr, c0);
+    load_v(vr, c0);
     const f16* q = qkv + (size_t)hq * D;
     const f16* k = qkv + (size_t)num_heads * D + (size_t)hk * D;
     const f16* v = qkv + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
-    const float qa = (float)q[lane], qb = (float)q[lane ^ 32];
-    const float ka = (float)k[lane], kb = (float)k[lane ^ 32];
+    const f16 qa16 = q[lane], qb16 = q[lane ^ 32], ka16 = k[lane], kb16 = k[lane ^ 32];
+    const f16 v16 = v[lane];
+    __builtin_amdgcn_sched_barrier(0);
+
+    const bool valid = p64 >= 0 && p64 < S;
+    const int p = valid ? (int)p64 : 0;
+    const float c = cos_table[(size_t)p * (D / 2) + (lane & 31)];
+    const float s = sin_table[(size_t)p * (D / 2) + (lane & 31)];
+    const float qa = (float)qa16, qb = (float)qb16, ka = (float)ka16, kb = (float)kb16;
     const float qr = lane < 32 ? qa * c - qb * s : qa * c + qb * s;
     const float kro = lane < 32 ? ka * c - kb * s : ka * c + kb * s;
-    const f16 q16 = (f16)qr, k16 = (f16)kro, v16 = v[lane];
+    const f16 q16 = (f16)qr, k16 = (f16)kro;
+    // every wavefront keeps its own copy (no branch the loads above could sink into)
+    float* qs = qs_all[wave];
+    f16* knew = knew_all[wave];
+    f16* vnew = vnew_all[wave];
     qs[lane] = (float)q16;
-    if (hq % group == 0) {
+    knew[lane] = k16;
+    vnew[lane] = v16;
+    if (valid && wave == 0 && hq % group == 0) {
         k_cache[((size_t)hk * S + p) * D + lane] = k16;
         v_cache[((size_t)hk * S + p) * D + lane] = v16;
     }
-    // slot p's key row for the lane that scores it: gathered from the lanes
-    __shared__ __align__(16) f16 knew[D];
-    knew[lane] = k16;
-    __syncthreads();
+    wave_lds_sync();
+    if (!valid) {
+        if (wave == 0) out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
+        return;
+    }
 
     float run_max = -__builtin_inff(), run_sum = 0.0f, acc = 0.0f;
-    for (int c0 = 0; c0 <= p; c0 += 64) {
+    f16* my_vt = vt[wave];
+    float* my_probs = probs[wave];
+    for (; c0 <= p; c0 += 64 * WA) {
         const int t = c0 + lane;
-        // this chunk's value rows into LDS (slot p patched with the new v)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int row = (lane >> 3) + 8 * i;
-            reinterpret_cast<u32x4*>(vt + row * D)[lane & 7] = vr[i];
-        }
-        // score of slot t
         float dot = 0.0f;
         if (t == p) {
 #pragma unroll
@@ -124,32 +160,66 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
                 }
             }
         }
-        const float score = t <= p ? dot / 8.0f : -__builtin_inff();
-        // next chunk's rows requested before this chunk's reductions
-        if (c0 + 64 <= p) {
-            load_k(kr, t + 64);
-            load_v(vr, c0 + 64);
+        const float score = t <= p ? dot * 0.125f : -__builtin_inff();
+        // value rows of the chunk to LDS: rows past p zeroed, slot p from vnew
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int row = (lane >> 3) + 8 * i;
+            const int slot = c0 + row;
+            u32x4 val = vr[i];
+            if (slot == p) val = reinterpret_cast<const u32x4*>(vnew)[lane & 7];
+            if (slot > p) val = (u32x4){0u, 0u, 0u, 0u};
+            reinterpret_cast<u32x4*>(my_vt + row * D)[lane & 7] = val;
         }
-        float cmax = score;
-        for (int off = 32; off >= 1; off >>= 1) cmax = fmaxf(cmax, __shfl_xor(cmax, off));
+        // next chunk's rows requested before this chunk's reductions
+        const int next = c0 + 64 * WA;
+        if (next <= p) {
+            load_k(kr, next);
+            load_v(vr, next);
+        }
+        const float cmax = wave_max(score);
         const float new_max = fmaxf(run_max, cmax);
         const float pr = t <= p ? expf(score - new_max) : 0.0f;
-        float psum = pr;
-        for (int off = 32; off >= 1; off >>= 1) psum += __shfl_xor(psum, off);
+        const float psum = wave_sum(pr);
         const float rescale = expf(run_max - new_max);   // 0 on the first chunk
-        probs[lane] = pr;
-        __syncthreads();
-        if (p - c0 < 64) vt[(p - c0) * D + lane] = v16;   // slot p from registers, not the cache
-        __syncthreads();
+        my_probs[lane] = pr;
+        wave_lds_sync();
         float part = 0.0f;
-        const int rows = min(64, p - c0 + 1);
-        for (int r = 0; r < rows; ++r) part = __builtin_fmaf(probs[r], (float)vt[r * D + lane], part);
+#pragma unroll
+        for (int r4 = 0; r4 < 16; ++r4) {
+            const f32x4 pp = reinterpret_cast<const f32x4*>(my_probs)[r4];
+            part = __builtin_fmaf(pp.x, (float)my_vt[(4 * r4 + 0) * D + lane], part);
+            part = __builtin_fmaf(pp.y, (float)my_vt[(4 * r4 + 1) * D + lane], part);
+            part = __builtin_fmaf(pp.z, (float)my_vt[(4 * r4 + 2) * D + lane], part);
+            part = __builtin_fmaf(pp.w, (float)my_vt[(4 * r4 + 3) * D + lane], part);
+        }
+        wave_lds_sync();
         acc = acc * rescale + part;
         run_sum = run_sum * rescale + psum;
         run_max = new_max;
-        __syncthreads();
     }
-    out[(size_t)hq * D + lane] = (f16)(acc / run_sum);
+    if (WA == 1) {
+        out[(size_t)hq * D + lane] = (f16)(acc / run_sum);
+        return;
+    }
+    if (lane == 0) {
+        wmax[wave] = run_max;
+        wsum[wave] = run_sum;
+    }
+    wacc[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float m = wmax[0];
+#pragma unroll
+    for (int w = 1; w < WA; ++w) m = fmaxf(m, wmax[w]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WA; ++w) {
+        const float f = wsum[w] > 0.0f ? expf(wmax[w] - m) : 0.0f;
+        num = __builtin_fmaf(wacc[w][lane], f, num);
+        den = __builtin_fmaf(wsum[w], f, den);
+    }
+    out[(size_t)hq * D + lane] = (f16)(num / den);
 }
 
 // ---------------------------------------------------------------------------
@@ -263,14 +333,6 @@ embedding_kernel(const f16* __restrict__ table, int64_t vocab, int hidden, const
 // outside [0, min(S, 64)) makes every attention value NaN (so the residual
 // stream turns NaN) and touches no cache slot.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void wave_lds_sync() {
-    // LDS operations of one wavefront complete in order; this only keeps the
-    // compiler from moving LDS accesses across the point
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 constexpr int kAttnOSlots = 64;
 constexpr int kVStride = 72;   // V tile row stride in halves (144 bytes: conflict-free 16-byte stores)
 
@@ -557,11 +619,17 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache, co
         return fail(W4A16_ERR_SHAPE, "attention: max_seq_len must be in 1..16384");
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(qkv, 2) || !aligned(output, 2))
         return fail(W4A16_ERR_ALIGNMENT, "attention: caches must be 16-byte aligned, fp16 buffers 2-byte aligned");
-    hipLaunchKernelGGL(w4a16::decode_attention, dim3((unsigned)num_heads), dim3(64), 0,
-                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
-                       static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
-                       position, static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads,
-                       (int)max_seq_len);
+    // wavefronts per head: one chunk of 64 slots each at a time; short caches
+    // keep one wavefront (a second would only re-read the same chunk)
+    const int WA = max_seq_len <= 64 ? 1 : max_seq_len <= 256 ? 4 : 8;
+    void (*kern)(const w4a16::f16*, w4a16::f16*, w4a16::f16*, const float*, const float*, const int64_t*,
+                 w4a16::f16*, int, int, int) = WA == 1   ? w4a16::decode_attention<1>
+                                                : WA == 4 ? w4a16::decode_attention<4>
+                                                          : w4a16::decode_attention<8>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)num_heads), dim3(64 * WA), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),
+                       static_cast<w4a16::f16*>(v_cache), cos_table, sin_table, position,
+                       static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
     return check_launch();
 }
 
