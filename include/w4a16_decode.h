@@ -1,8 +1,8 @@
 /*
  * W4A16 decode-step extensions for gfx950 (MI355X): the fused GEMV variants
  * and the small kernels that, together with the W4A16 linear layer, run one
- * greedy-decode step of a Llama-architecture model in 5 launches per layer
- * plus 2.
+ * greedy-decode step of a Llama-architecture model in 4 or 5 launches per
+ * layer plus 2.
  *
  * Reference interfaces they replace (chris320211/Nibble): the reference runs
  * its end-to-end decode (scripts/generate.py:260-305, HF generate with a
@@ -47,6 +47,37 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
                          const uint8_t* packed_weights, const void* scales,
                          const void* residual, void* output, int64_t N, int64_t K,
                          int64_t group_size, int paired, void* stream);
+
+/*
+ * The lm_head GEMV with the greedy argmax in its epilogue: logits[n] =
+ * fp16(W[n] . x') as w4a16_gemv_fused_f16 (norm_weight optional; logits may
+ * be NULL when the caller does not need them), then in the same launch
+ * *token = first index of the maximum logit (a NaN counts as the maximum,
+ * -0 as +0, as torch.argmax), *position += 1 when position != NULL, and
+ * emb_out[0..hidden) = table[*token, :] when table / emb_out are given
+ * (vocab >= N). Each workgroup publishes its best (logit, index) in the
+ * workspace and the last one to arrive finishes the reduction.
+ * workspace: device memory of at least w4a16_gemv_argmax_workspace_bytes(N)
+ * bytes, 16-byte aligned, zero-filled once before its first use; every call
+ * leaves its counters at zero again, so it is reused as is (also under graph
+ * capture). Calls that share a workspace must not run concurrently.
+ * Needs group_size 128, 0 < K <= 16384 (multiple of 128), 16-byte aligned
+ * activations, norm_weight and packed_weights.
+ * Cost on MI355X: each workgroup's device-scope release / acquire fences
+ * write back and invalidate its XCD's L2 while the other workgroups stream
+ * weights, ~30 ns per workgroup in series (61 us for a 32000 x 2048 lm_head
+ * against 8.8 us + 6.8 us for w4a16_gemv_fused_f16 + w4a16_argmax_embed_f16),
+ * so that pair stays the decode step's choice.
+ * Replaces (reference): lm_head QuantizedLinear (w4a16/linear.py:154-200)
+ * + the greedy pick of HF generate(do_sample=False) and the next step's
+ * embedding lookup (scripts/generate.py:286-293).
+ */
+int64_t w4a16_gemv_argmax_workspace_bytes(int64_t N);
+int w4a16_gemv_argmax_f16(const void* activations, const void* norm_weight, float eps,
+                          const uint8_t* packed_weights, const void* scales, void* logits,
+                          int64_t N, int64_t K, int64_t group_size, int64_t* token,
+                          int64_t* position, const void* table, int64_t vocab, int64_t hidden,
+                          void* emb_out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Attention of one new token at position *position (device int64):

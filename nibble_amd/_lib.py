@@ -64,6 +64,11 @@ DECODE_SIGNATURES = {
     ),
     "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
     "w4a16_attention_o_f16": (ctypes.c_int, [_vp] * 8 + [_i64] * 6 + [_vp]),
+    "w4a16_gemv_argmax_workspace_bytes": (_i64, [_i64]),
+    "w4a16_gemv_argmax_f16": (
+        ctypes.c_int,
+        [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp],
+    ),
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
@@ -210,6 +215,28 @@ def attention_o_f16(qkv, k_cache, v_cache, inv_freq, position, o_packed, o_scale
             qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), inv_freq.data_ptr(), position.data_ptr(),
             o_packed.data_ptr(), o_scales.data_ptr(), residual.data_ptr(), num_heads, num_kv_heads, head_dim,
             k_cache.shape[-2], residual.numel(), group_size, _stream_ptr(stream),
+        )
+    )
+
+
+def gemv_argmax_workspace_bytes(n: int) -> int:
+    """Bytes of the workspace ``gemv_argmax_f16`` needs for an N-row layer."""
+    return int(lib().w4a16_gemv_argmax_workspace_bytes(n))
+
+
+def gemv_argmax_f16(x, packed, scales, token, workspace, logits=None, norm_weight=None, eps: float = 1e-6,
+                    position=None, table=None, emb_out=None, group_size: int = 128, stream=None) -> None:
+    """``w4a16_gemv_argmax_f16``: logits = W x' (RMSNorm first when norm_weight is
+    given), token <- argmax, position += 1, emb_out <- table[token]; one launch.
+    ``workspace``: a zeroed device tensor of at least
+    ``gemv_argmax_workspace_bytes(N)`` bytes, reused across calls."""
+    n, k = packed.shape[0], packed.shape[1] * 2
+    vocab, hidden = (table.shape if table is not None else (0, 0))
+    _raise_on(
+        lib().w4a16_gemv_argmax_f16(
+            x.data_ptr(), _ptr(norm_weight), eps, packed.data_ptr(), scales.data_ptr(), _ptr(logits), n, k,
+            group_size, token.data_ptr(), _ptr(position), _ptr(table), vocab, hidden, _ptr(emb_out),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_ptr(stream),
         )
     )
 

@@ -372,14 +372,13 @@ int launch_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w
 // sweeps: paired rows R = 2 with 8 wavefronts per workgroup; very wide
 // layers (N >= 16384, the lm_head) 4 rows per wavefront; the other RMSNorm
 // layers (q|k|v) 2 rows and 8 wavefronts; residual layers 1 row and 8.
-template <bool NORM, bool PAIRED>
-int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* norm_w, float eps,
-                   const uint8_t* w, const w4a16::f16* s, const w4a16::f16* resid, w4a16::f16* o, int N, int K,
-                   hipStream_t stream) {
+template <bool NORM, bool PAIRED, bool ARGMAX = false>
+int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::GemvFusion& fz, const uint8_t* w,
+                   const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
     void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, GemvFusion) = nullptr;
 #define W4A16_PICK_L(RR, LL, WW) \
-    if (R == RR && L == LL && W == WW) kern = gemv_oneshot<1, RR, LL, WW, NORM, PAIRED>;
+    if (R == RR && L == LL && W == WW) kern = gemv_oneshot<1, RR, LL, WW, NORM, PAIRED, ARGMAX>;
 #define W4A16_PICK(RR, WW)                                                                               \
     W4A16_PICK_L(RR, 1, WW) W4A16_PICK_L(RR, 2, WW) W4A16_PICK_L(RR, 3, WW) W4A16_PICK_L(RR, 4, WW)   \
     W4A16_PICK_L(RR, 5, WW) W4A16_PICK_L(RR, 6, WW) W4A16_PICK_L(RR, 7, WW) W4A16_PICK_L(RR, 8, WW)
@@ -396,9 +395,33 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::f16* n
     if (rc != W4A16_OK) return rc;
     const int tasks = PAIRED ? N / 2 : (N + R - 1) / R;
     const int blocks = (tasks + W - 1) / W;
-    GemvFusion fz{norm_w, eps, resid};
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * W), lds, stream, x, w, s, o, N, K, fz);
     return check_launch();
+}
+
+// Launch shape of the fused M = 1 GEMV: paired rows (2, 8); very wide
+// layers (lm_head) 4 rows x 4 wavefronts; RMSNorm rows 2 x 8; else 1 x 8.
+void fused_shape(bool paired, bool norm, int64_t N, int& R, int& W) {
+    R = 2;
+    W = 8;
+    if (paired) return;
+    if (N >= 16384) {
+        R = 4;
+        W = 4;
+    } else if (!norm) {
+        R = 1;
+    }
+}
+
+// Workspace of the argmax epilogue: 9 counters on separate 128-byte lines,
+// then one 8-byte key per workgroup.
+constexpr int64_t kArgmaxCounterBytes = 9 * 128;
+
+int64_t argmax_workspace_bytes(int64_t N) {
+    int R, W;
+    fused_shape(false, true, N, R, W);
+    const int64_t blocks = (N + (int64_t)R * W - 1) / ((int64_t)R * W);
+    return kArgmaxCounterBytes + 8 * blocks;
 }
 
 int launch_mfma_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s, w4a16::f16* o,
@@ -650,31 +673,73 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
     if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "eps must be non-negative");
     using w4a16::f16;
     const int L = oneshot_loads(K);
-    int R = 2, W = 8;
-    if (!paired) {
-        if (N >= 16384) {
-            R = 4;
-            W = 4;
-        } else if (norm_weight != nullptr) {
-            R = 2;
-            W = 8;
-        } else {
-            R = 1;
-            W = 8;
-        }
-    }
+    int R, W;
+    fused_shape(paired != 0, norm_weight != nullptr, N, R, W);
     const f16* x = static_cast<const f16*>(activations);
     const f16* nw = static_cast<const f16*>(norm_weight);
     const f16* sc = static_cast<const f16*>(scales);
-    const f16* res = static_cast<const f16*>(residual);
     f16* o = static_cast<f16*>(output);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n = (int)N, k = (int)K;
+    w4a16::GemvFusion fz{};
+    fz.norm_weight = nw;
+    fz.eps = eps;
+    fz.residual = static_cast<const f16*>(residual);
     if (paired)
-        return nw ? launch_fused_t<true, true>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st)
-                  : launch_fused_t<false, true>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st);
-    return nw ? launch_fused_t<true, false>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st)
-              : launch_fused_t<false, false>(L, R, W, x, nw, eps, packed_weights, sc, res, o, n, k, st);
+        return nw ? launch_fused_t<true, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
+                  : launch_fused_t<false, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
+    return nw ? launch_fused_t<true, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
+              : launch_fused_t<false, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
+}
+
+int64_t w4a16_gemv_argmax_workspace_bytes(int64_t N) { return N <= 0 ? 0 : argmax_workspace_bytes(N); }
+
+int w4a16_gemv_argmax_f16(const void* activations, const void* norm_weight, float eps,
+                          const uint8_t* packed_weights, const void* scales, void* logits, int64_t N, int64_t K,
+                          int64_t group_size, int64_t* token, int64_t* position, const void* table, int64_t vocab,
+                          int64_t hidden, void* emb_out, void* workspace, int64_t workspace_bytes, void* stream) {
+    int rc = check_scalar_args(1, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    if (group_size != 128) return fail(W4A16_ERR_GROUP_SIZE, "GEMV argmax needs group_size 128");
+    if (K == 0 || K > 16384) return fail(W4A16_ERR_SHAPE, "GEMV argmax needs 0 < K <= 16384");
+    if (N == 0 || N > INT32_MAX - 1) return fail(W4A16_ERR_SHAPE, "GEMV argmax needs 1 <= N < 2^31 - 1");
+    rc = check_pointers(activations, packed_weights, scales, token);
+    if (rc != W4A16_OK) return rc;
+    if (workspace == nullptr) return fail(W4A16_ERR_NULL, "GEMV argmax needs its workspace");
+    if ((table == nullptr) != (emb_out == nullptr))
+        return fail(W4A16_ERR_NULL, "GEMV argmax: table and emb_out must both be given or both be NULL");
+    if (table && (vocab < N || hidden <= 0 || hidden > INT32_MAX / 2))
+        return fail(W4A16_ERR_SHAPE, "GEMV argmax: the embedding table needs vocab >= N and a positive hidden size");
+    if (workspace_bytes < argmax_workspace_bytes(N))
+        return fail(W4A16_ERR_SHAPE, "GEMV argmax: workspace smaller than w4a16_gemv_argmax_workspace_bytes(N)");
+    if (!aligned16(activations) || !aligned16(packed_weights) || (norm_weight && !aligned16(norm_weight)) ||
+        !aligned16(workspace))
+        return fail(W4A16_ERR_ALIGNMENT, "GEMV argmax needs 16-byte aligned activations, norm_weight, weights "
+                                         "and workspace");
+    if (logits && (reinterpret_cast<uintptr_t>(logits) & 1u))
+        return fail(W4A16_ERR_ALIGNMENT, "logits must be 2-byte aligned");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "eps must be non-negative");
+    using w4a16::f16;
+    int R, W;
+    fused_shape(false, true, N, R, W);
+    w4a16::GemvFusion fz{};
+    fz.norm_weight = static_cast<const f16*>(norm_weight);
+    fz.eps = eps;
+    fz.counters = static_cast<uint32_t*>(workspace);
+    fz.partials = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + kArgmaxCounterBytes);
+    fz.token = token;
+    fz.position = position;
+    fz.table = static_cast<const f16*>(table);
+    fz.vocab = vocab;
+    fz.hidden = (int)hidden;
+    fz.emb_out = static_cast<f16*>(emb_out);
+    const int L = oneshot_loads(K);
+    const f16* x = static_cast<const f16*>(activations);
+    const f16* sc = static_cast<const f16*>(scales);
+    f16* o = static_cast<f16*>(logits);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return norm_weight ? launch_fused_t<true, false, true>(L, R, W, x, fz, packed_weights, sc, o, (int)N, (int)K, st)
+                       : launch_fused_t<false, false, true>(L, R, W, x, fz, packed_weights, sc, o, (int)N, (int)K, st);
 }
 
 int w4a16_dequantize_f16(const uint8_t* packed_weights, const void* scales, void* output, int64_t N,

@@ -291,20 +291,114 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 //     row is read and written by the same lane);
 //   PAIRED (R = 2): wavefront i owns rows i and i + N/2 of a [gate; up]
 //     weight pair and stores out[i] = fp16(silu(g) * u) with g, u, silu(g)
-//     each rounded to fp16 first, as fp16 tensors would be.
+//     each rounded to fp16 first, as fp16 tensors would be;
+//   ARGMAX: the rows' fp16 logits (stored when out != nullptr) feed a greedy
+//     argmax over all N rows in the kernel's tail (argmax_tail).
 // ---------------------------------------------------------------------------
 
 struct GemvFusion {
     const f16* norm_weight;   // nullptr: no RMSNorm prologue
     float eps;
     const f16* residual;      // nullptr: no residual add
+    // greedy argmax epilogue (ARGMAX; see argmax_tail)
+    uint32_t* counters;       // arrival counters, zero on entry and on return
+    uint64_t* partials;       // one (logit, index) key per workgroup
+    int64_t* token;
+    int64_t* position;        // nullptr: not advanced
+    const f16* table;         // nullptr: no embedding gather
+    int64_t vocab;
+    int hidden;
+    f16* emb_out;
 };
 
-template <int M, int R, int L, int W, bool NORM, bool PAIRED>
+// Order-preserving key of an fp16 logit at index n: larger logit first,
+// then smaller index (torch.argmax's first maximum); -0 counts as +0 and any
+// NaN as the largest value, as torch.argmax treats them.
+__device__ __forceinline__ uint64_t argmax_key(float v, int n) {
+    v = v + 0.0f;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t ord = v != v ? 0xFFFFFFFFu : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+    return ((uint64_t)ord << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)n);
+}
+
+// Greedy argmax over all workgroups' rows in the GEMV's tail: each workgroup
+// publishes its best key, and the last workgroup to arrive (two-level
+// counters: one per slot blockIdx % 8, which spreads the arrivals over eight
+// cache lines, then one over the slots; device-scope atomics and fences)
+// reduces the keys, writes the token, advances the position, gathers the
+// token's embedding row and returns the counters to zero for the next call.
+// Two calls sharing counters must not overlap.
+template <int R, int W>
+__device__ __forceinline__ void argmax_tail(const float (&rowsum)[R], int row0, int N, const GemvFusion& fz,
+                                            int wave, int lane) {
+    __shared__ uint64_t wbest[W];
+    __shared__ int last;
+    __shared__ int64_t chosen;
+    uint64_t best = 0;   // below every key
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint64_t key = argmax_key((float)(f16)rowsum[r], row0 + r);
+        if (row0 + r < N && key > best) best = key;
+    }
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = wbest[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) b = wbest[w] > b ? wbest[w] : b;
+        __hip_atomic_store(&fz.partials[blockIdx.x], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence();
+        const unsigned x = blockIdx.x & 7u;
+        const unsigned in_slot = (gridDim.x + 7u - x) / 8u;
+        const unsigned slots = gridDim.x < 8u ? gridDim.x : 8u;
+        int is_last = 0;
+        if (atomicAdd(&fz.counters[32u * (1u + x)], 1u) == in_slot - 1u) {
+            __threadfence();
+            is_last = atomicAdd(&fz.counters[0], 1u) == slots - 1u;
+        }
+        last = is_last;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    uint64_t b = 0;
+    for (int i = threadIdx.x; i < (int)gridDim.x; i += 64 * W) {
+        const uint64_t v = __hip_atomic_load(&fz.partials[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        b = v > b ? v : b;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = (uint64_t)__shfl_xor((unsigned long long)b, off);
+        b = o > b ? o : b;
+    }
+    if (lane == 0) wbest[wave] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t k = wbest[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) k = wbest[w] > k ? wbest[w] : k;
+        const int64_t t = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFu));
+        fz.token[0] = t;
+        chosen = t;
+        if (fz.position != nullptr) fz.position[0] += 1;
+        __hip_atomic_store(&fz.counters[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            __hip_atomic_store(&fz.counters[32 * (1 + s)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (fz.emb_out == nullptr) return;
+    __syncthreads();
+    const int64_t t = chosen;
+    for (int i = threadIdx.x; i < fz.hidden; i += 64 * W)
+        fz.emb_out[i] = (t >= 0 && t < fz.vocab) ? fz.table[t * fz.hidden + i] : (f16)0.0f;
+}
+
+template <int M, int R, int L, int W, bool NORM, bool PAIRED, bool ARGMAX = false>
 __global__ void __launch_bounds__(64 * W)
 gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
              const f16* __restrict__ scales, f16* out, int N, int K, GemvFusion fz) {
     static_assert(!PAIRED || (M == 1 && R == 2), "paired rows are an M = 1, R = 2 layout");
+    static_assert(!ARGMAX || (M == 1 && !PAIRED), "the argmax epilogue is an M = 1 plain-row layout");
     static_assert(!NORM || M == 1, "the RMSNorm prologue normalises one activation row");
     extern __shared__ __align__(16) uint8_t smem[];
     u32x4* xs = reinterpret_cast<u32x4*>(smem);
@@ -436,7 +530,7 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         }
     }
     __syncthreads();
-    if (!valid) return;
+    if (!valid && !ARGMAX) return;   // the argmax tail needs every wavefront at its barriers
 
     // 4. dot products, row by row in arrival order. Straight-line code (no
     // branch per chunk, so each chunk waits only for its own load): lanes
@@ -473,7 +567,7 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             rowsum[r][m] = wave_sum(acc[m]);
-            if (!PAIRED && lane == 0 && row0 + r < N) {
+            if (!PAIRED && lane == 0 && row0 + r < N && (!ARGMAX || out != nullptr)) {
                 const int n = row0 + r;
                 f16 v = (f16)rowsum[r][m];
                 if (fz.residual != nullptr) v = (f16)((float)fz.residual[n] + (float)v);
@@ -486,6 +580,12 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
         const float u = (float)(f16)rowsum[R - 1][0];
         const float act = (float)(f16)(g / (1.0f + expf(-g)));
         out[task] = (f16)(act * u);
+    }
+    if constexpr (ARGMAX) {
+        float rs[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) rs[r] = rowsum[r][0];
+        argmax_tail<R, W>(rs, row0, N, fz, wave, lane);
     }
 }
 

@@ -15,7 +15,8 @@ by default: per layer, (1) RMSNorm + q|k|v GEMV over the concatenated
 projection, (2) rotary embedding + KV-cache append + attention, (3) o GEMV +
 residual, (4) RMSNorm + gate|up GEMV with the SiLU-multiply epilogue, (5)
 down GEMV + residual; then RMSNorm + lm_head GEMV and the greedy argmax,
-which also advances the position: 5 launches per layer. While the position
+which also advances the position and gathers the next token's embedding: 5
+launches per layer plus 2. While the position
 is below 64 (and the head layout allows it), (2) and (3) are one launch
 (``w4a16_attention_o_f16``: every o-projection workgroup recomputes the
 one-chunk attention on the matrix cores), so a step is 4 launches per layer;
@@ -348,6 +349,9 @@ class LlamaDecoder(torch.nn.Module):
             _lib.gemv_fused_f16(x, gu_w, gu_s, self.mlp_buf, norm_weight=b.post_norm.weight, eps=b.post_norm.eps,
                                 paired=True)
             _lib.gemv_fused_f16(self.mlp_buf, b.down_proj.packed_weights, b.down_proj.scales, x, residual=x)
+        # RMSNorm + lm_head GEMV, then greedy argmax + position += 1 + the next
+        # token's embedding into x_buf. Two launches: the single-launch form
+        # (w4a16_gemv_argmax_f16) pays one device-scope fence per workgroup.
         _lib.gemv_fused_f16(x, self.lm_head.packed_weights, self.lm_head.scales, self.logits,
                             norm_weight=self.norm.weight, eps=self.norm.eps)
         _lib.argmax_embed_f16(self.logits, self.token, self.position, self.embed, x)

@@ -289,6 +289,73 @@ def test_attention_o_rejects(gpu):
         _lib.attention_o_f16(t, cache, cache, inv, pos, w, t, t[:64], 34, 2)
 
 
+# ------------------------------------------------------- lm_head + argmax ----
+@pytest.mark.parametrize("k,n", [(256, 1), (256, 7), (2048, 1000), (2048, 32000), (1024, 50257)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemv_argmax(gpu, k, n, norm):
+    """Logits bit-identical to the fused GEMV's (same arithmetic), token =
+    torch.argmax of them, position + 1, embedding row gathered; three calls in
+    a row (the workspace counters must return to zero)."""
+    x, p, s = make_case(1, k, n, seed=k + 7 * n)
+    gen = torch.Generator().manual_seed(n)
+    w = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16).to(gpu)
+    xg, pg, sg = x.to(gpu).view(-1), p.to(gpu), s.to(gpu)
+    ref_logits = torch.empty((n,), dtype=torch.float16, device=gpu)
+    _lib.gemv_fused_f16(xg, pg, sg, ref_logits, norm_weight=w if norm else None, eps=1e-5)
+    table = torch.randn((n, 96), generator=gen).to(torch.float16).to(gpu)
+    ws = torch.zeros(((_lib.gemv_argmax_workspace_bytes(n) + 7) // 8,), dtype=torch.int64, device=gpu)
+    token = torch.full((1,), -5, dtype=torch.int64, device=gpu)
+    position = torch.tensor([10], dtype=torch.int64, device=gpu)
+    for call in range(3):
+        logits = torch.full((n,), float("nan"), dtype=torch.float16, device=gpu)
+        emb = torch.zeros((96,), dtype=torch.float16, device=gpu)
+        print(f"[case] gemv_argmax K={k} N={n} norm={norm} call {call}", flush=True)
+        _lib.gemv_argmax_f16(xg, pg, sg, token, ws, logits=logits, norm_weight=w if norm else None, eps=1e-5,
+                             position=position, table=table, emb_out=emb)
+        torch.cuda.synchronize()
+        assert torch.equal(logits, ref_logits)
+        t = int(torch.argmax(ref_logits.float()))
+        assert int(token) == t and int(position) == 11 + call
+        assert torch.equal(emb, table[t])
+        assert not ws[: (9 * 128) // 8].any()   # counters back at zero
+
+
+def test_gemv_argmax_ties_and_no_logits(gpu):
+    """Equal maxima in rows far apart: the first index wins (torch.argmax), also
+    when the logits are not stored."""
+    from nibble_amd.quantization import pack_int4
+
+    k, n = 512, 20000
+    x, p, s = make_case(1, k, n, seed=3)
+    # rows 123, 777, 5000, 19999: codes 7 sign(x) and the largest scale, so
+    # they share a logit far above every other row
+    codes = torch.where(x[0] > 0, 7, -7).to(torch.int8).view(1, k)
+    for r in (123, 777, 5000, 19999):
+        p[r] = pack_int4(codes)[0]
+        s[r] = s.max()
+    xg, pg, sg = x.to(gpu).view(-1), p.to(gpu), s.to(gpu)
+    logits = torch.empty((n,), dtype=torch.float16, device=gpu)
+    _lib.gemv_fused_f16(xg, pg, sg, logits)
+    assert float(logits.max()) == float(logits[123]) == float(logits[19999])
+    ws = torch.zeros(((_lib.gemv_argmax_workspace_bytes(n) + 7) // 8,), dtype=torch.int64, device=gpu)
+    token = torch.zeros((1,), dtype=torch.int64, device=gpu)
+    _lib.gemv_argmax_f16(xg, pg, sg, token, ws)
+    torch.cuda.synchronize()
+    assert int(token) == int(torch.argmax(logits.float())) == 123
+
+
+def test_gemv_argmax_rejects(gpu):
+    x, p, s = make_case(1, 256, 64, seed=1)
+    xg, pg, sg = x.to(gpu).view(-1), p.to(gpu), s.to(gpu)
+    token = torch.zeros((1,), dtype=torch.int64, device=gpu)
+    small = torch.zeros((4,), dtype=torch.int64, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="workspace"):
+        _lib.gemv_argmax_f16(xg, pg, sg, token, small)
+    ws = torch.zeros((1024,), dtype=torch.int64, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="both be given"):
+        _lib.gemv_argmax_f16(xg, pg, sg, token, ws, table=torch.zeros((64, 8), dtype=torch.float16, device=gpu))
+
+
 # ------------------------------------------------------- argmax, embedding ----
 @pytest.mark.parametrize("n", [1, 1000, 32000, 50257])
 def test_argmax_first_maximum_and_position(gpu, n):
