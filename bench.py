@@ -43,7 +43,7 @@ HBM_PEAK_GBPS = 8000.0
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
 # reads half the bytes on this part, WRITE_SIZE is exact).
-MEASURED_TRAFFIC_BYTES = 6074304
+MEASURED_TRAFFIC_BYTES = 6070301
 
 
 def _kernel_name(plan: dict) -> str:
