@@ -42,6 +42,7 @@ extern "C" {
 #define W4A16_KERNEL_VALU_OFFSET 5   /* VALU kernel, decode without f16 fix-ups, per-chunk offset correction */
 #define W4A16_KERNEL_ONESHOT 6       /* VALU GEMV, every weight of a wavefront's rows requested at once (M <= 4) */
 #define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 16, K <= 8192) */
+#define W4A16_KERNEL_MFMA_PAIR 8     /* fp16 MFMA on 8 rows x 2 groups, loads up front (2 <= M <= 8, staged M*K in LDS) */
 
 /*
  * Fused W4A16 linear layer.
@@ -55,7 +56,7 @@ extern "C" {
  * takes the generic kernel (the reference routes every M > 8 to its naive
  * kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
- * valu_offset|mfma|mfma_oneshot selects the kernel family for M <= 8;
+ * valu_offset|mfma|mfma_oneshot|mfma_pair selects the kernel family for M <= 8;
  * W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront of the VALU
  * kernels (any other value is W4A16_ERR_CONFIG).
  */
@@ -123,9 +124,17 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splitting K (4|8), unroll = groups per wavefront (0 = ceil(K / 128 /
  *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
  *     1..8 with 8), max_blocks ignored.
+ *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 8): splits = wavefronts splitting the
+ *     K / 256 group pairs (2|4|8), max_blocks = 8-row-block wavefronts per
+ *     workgroup (1|2|4|8, splits * max_blocks <= 16), rows = 8-row blocks
+ *     per wavefront (1), unroll = group pairs per wavefront (0 = ceil(K /
+ *     256 / splits); else 1..8 with splits * unroll >= ceil(K / 256));
+ *     staged activations, biases and reduction
+ *     within 160 KiB of LDS (K <= 8192 at M = 8, 16384 at M <= 4).
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
- * W4A16_KERNEL_MFMA_ONESHOT) and 16-byte aligned activations and weights. No reference counterpart (the reference's
+ * W4A16_KERNEL_MFMA_ONESHOT, 2..8 for W4A16_KERNEL_MFMA_PAIR) and 16-byte
+ * aligned activations and weights. No reference counterpart (the reference's
  * W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
  */
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,

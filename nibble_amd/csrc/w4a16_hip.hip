@@ -17,6 +17,13 @@
 
 #include "w4a16_kernels.h"
 
+namespace w4a16_internal {
+// w4a16_pair.hip: the paired-group MFMA kernel for M = 2..8
+int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int rb, int gpw);
+int launch_mfma_pair(int sk, int sn, int rb, int gpw, int M, const void* x, const uint8_t* w, const void* s,
+                     void* o, int N, int K, hipStream_t stream);
+}  // namespace w4a16_internal
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -80,9 +87,10 @@ int read_env(int* family, int* rows_per_wave) {
         else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
         else if (std::strcmp(d, "oneshot") == 0) *family = W4A16_KERNEL_ONESHOT;
         else if (std::strcmp(d, "mfma_oneshot") == 0) *family = W4A16_KERNEL_MFMA_ONESHOT;
+        else if (std::strcmp(d, "mfma_pair") == 0) *family = W4A16_KERNEL_MFMA_PAIR;
         else
             return fail(W4A16_ERR_CONFIG,
-                        "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, or mfma_oneshot");
+                        "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, mfma_oneshot, or mfma_pair");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -200,6 +208,53 @@ Plan plan_mfma_oneshot(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
+// Paired-group MFMA kernel (M = 2..8, w4a16_pair.h). Plan fields: splits =
+// SK wavefronts splitting the K / 256 group pairs, max_blocks = SN row-block
+// wavefronts per workgroup, rows = 8-row blocks per wavefront, unroll = pairs
+// per wavefront. Launch shape from the M = 4 and M = 8 sweeps over the
+// benchmark shapes: SK = 4 on short rows of narrow layers and 2 on wide ones
+// (up to 8 pairs: N <= 4096; 9..16 pairs: N < 8192), 8 for 17..24 pairs, 4
+// up to 32, 8 beyond; a workgroup takes the largest of 8, 16, 32, 64 rows
+// that leaves >= 176 workgroups, at most 16 wavefronts, except that M <= 4
+// layers with over 512 such workgroups run two 8-wavefront workgroups per
+// CU (each stages its activations while the other streams weights).
+Plan plan_mfma_pair(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_MFMA_PAIR;
+    const int64_t pairs = (K / 128 + 1) / 2;
+    int sk;
+    if (pairs <= 8)
+        sk = N <= 4096 ? 4 : 2;
+    else if (pairs <= 16)
+        sk = N >= 8192 ? 2 : 4;
+    else if (pairs <= 24)
+        sk = 8;
+    else if (pairs <= 32)
+        sk = 4;
+    else
+        sk = 8;
+    const int gpw = (int)((pairs + sk - 1) / sk);
+    int rows = 8;
+    while (rows < 64 && N / (2 * rows) >= 176) rows *= 2;
+    int sn = rows / 8;
+    while (sk * sn > 16) sn /= 2;
+    if (M <= 4 && sk * sn == 16 && N / (4 * sn) > 512 &&
+        2 * w4a16_internal::mfma_pair_lds_bytes(M, K, sk, sn / 2, 1, gpw) <= kMaxLdsBytes)
+        sn /= 2;
+    p.splits = sk;
+    p.max_blocks = sn;
+    p.rows = 1;
+    p.unroll = gpw;
+    return p;
+}
+
+bool mfma_pair_fits(int64_t M, int64_t N, int64_t K) {
+    if (M < 2 || M > 8 || K < 128 || K % 128 != 0 || K > 16384) return false;
+    const Plan p = plan_mfma_pair(M, N, K);
+    return p.unroll <= 8 &&
+           w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
+}
+
 int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
     int family = 0, rows = 0;
     const int rc = read_env(&family, &rows);
@@ -233,7 +288,9 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // keeps auto on the looped VALU kernel whose rows it sets.
     // Measured routing (M = 1..8 sweeps over the benchmark shapes):
     //   M = 1: one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
-    //   M >= 3: one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
+    //   M >= 3: the paired-group MFMA kernel wherever its activations fit in
+    //   LDS (K <= 8192 at M = 8, 16384 at M <= 4); beyond that as before:
+    //   one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
     //   small layers (K, N <= 5632; each workgroup re-stages M*K activations,
     //   which on large layers outweighs the weights it streams), one-shot
     //   MFMA up to K = 8192 when N >= 4096 gives it enough row blocks;
@@ -243,6 +300,8 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         const bool small = K <= 5632 && N <= 5632;
         if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
             family = W4A16_KERNEL_ONESHOT;
+        else if (rows == 0 && M >= 3 && mfma_pair_fits(M, N, K))
+            family = W4A16_KERNEL_MFMA_PAIR;
         else if (M >= 3 && K <= 4096 && mfma_oneshot_fits(M, K))
             family = W4A16_KERNEL_MFMA_ONESHOT;
         else if (rows == 0 && M <= 4 && small && oneshot_fits(M, K))
@@ -252,6 +311,13 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         else
             family = (M == 1 || (M == 2 && K <= 16384) || (M <= 4 && K <= 4096)) ? W4A16_KERNEL_VALU
                                                                                    : W4A16_KERNEL_MFMA;
+    }
+    if (family == W4A16_KERNEL_MFMA_PAIR) {
+        if (mfma_pair_fits(M, N, K)) {
+            *out = plan_mfma_pair(M, N, K);
+            return W4A16_OK;
+        }
+        family = W4A16_KERNEL_MFMA;   // M = 1 or activations too long for LDS
     }
     if (family == W4A16_KERNEL_MFMA_ONESHOT) {
         if (mfma_oneshot_fits(M, K)) {
@@ -539,6 +605,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_DIAG: return launch_diag(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_ONESHOT: return launch_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA_ONESHOT: return launch_mfma_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_MFMA_PAIR:
+            return w4a16_internal::launch_mfma_pair(p.splits, p.max_blocks, p.rows, p.unroll, (int)M, x, packed, s,
+                                                    o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -557,6 +626,7 @@ int check_pointers(const void* act, const void* packed, const void* scales, cons
 
 namespace w4a16_internal {
 void set_last_error(const std::string& message) { g_last_error = message; }
+int ensure_lds(const void* kernel, int bytes) { return ::ensure_lds(kernel, bytes); }
 }  // namespace w4a16_internal
 
 extern "C" {
@@ -638,7 +708,12 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
+    if (kernel == W4A16_KERNEL_MFMA_PAIR) {
+        if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "the paired MFMA kernel needs group_size 128, 2 <= M <= 8 and 16-byte aligned activations "
+                        "and weights");
+    } else if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
         kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT ||
         kernel == W4A16_KERNEL_MFMA_ONESHOT) {
         const int64_t max_m = kernel == W4A16_KERNEL_MFMA_ONESHOT ? 16 : 8;
@@ -649,7 +724,8 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
-                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _DIAG or _GENERIC");
+                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, _DIAG "
+                    "or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
 }

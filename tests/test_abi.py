@@ -102,17 +102,21 @@ ALIGNED = 1 << 20
         (1, 34816, 128, ALIGNED, "valu"),      # rows too long for the one-shot kernel
         (2, 2048, 128, ALIGNED, "oneshot"),    # M = 2 up to K = 5632
         (2, 5632, 128, ALIGNED, "oneshot"),
-        (4, 2048, 128, ALIGNED, "mfma_oneshot"),
-        (4, 5632, 128, ALIGNED, "oneshot"),    # small layer beyond the staged-MFMA rows
+        (3, 2048, 128, ALIGNED, "mfma_pair"),  # M >= 3: paired-group MFMA wherever M*K fits in LDS
+        (4, 2048, 128, ALIGNED, "mfma_pair"),
+        (4, 5632, 128, ALIGNED, "mfma_pair"),
         (2, 8192, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
         (2, 28672, 128, ALIGNED, "mfma"),      # very long rows
-        (4, 8192, 128, ALIGNED, "mfma"),           # N = 64: too few row blocks for the staged kernel
-        (8, 8192, 128, ALIGNED, "mfma"),
-        (8, 8320, 128, ALIGNED, "mfma"),           # beyond the staged-MFMA rows
-        (4, 14336, 128, ALIGNED, "mfma"),      # small batch, long rows -> MFMA
-        (5, 2048, 128, ALIGNED, "mfma_oneshot"),   # small batch, rows up to 4096 weights
-        (8, 4096, 128, ALIGNED, "mfma_oneshot"),
-        (8, 5632, 128, ALIGNED, "mfma"),           # K > 4096 with few rows: looped MFMA
+        (4, 8192, 128, ALIGNED, "mfma_pair"),
+        (8, 8192, 128, ALIGNED, "mfma_pair"),
+        (8, 8320, 128, ALIGNED, "mfma"),           # M*K beyond LDS at M = 8
+        (4, 14336, 128, ALIGNED, "mfma_pair"),     # M <= 4 stages up to K = 16384
+        (4, 16384, 128, ALIGNED, "mfma_pair"),
+        (4, 16512, 128, ALIGNED, "mfma"),          # beyond 8 pairs per wavefront
+        (4, 28672, 128, ALIGNED, "mfma"),
+        (5, 2048, 128, ALIGNED, "mfma_pair"),
+        (8, 4096, 128, ALIGNED, "mfma_pair"),
+        (8, 5632, 128, ALIGNED, "mfma_pair"),
         (9, 2048, 128, ALIGNED, "mfma_oneshot"),   # a short prompt: one MFMA tile of rows
         (16, 4096, 128, ALIGNED, "mfma_oneshot"),
         (16, 5632, 128, ALIGNED, "generic"),       # activations beyond LDS
@@ -132,8 +136,30 @@ def test_plan_misaligned_weights_take_generic():
     assert _lib.plan_linear(ALIGNED, ALIGNED + 8, 1, 64, 2048, 128)["kernel"] == "generic"
 
 
-def test_mfma_oneshot_plan_shapes(monkeypatch):
+def test_mfma_pair_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    # (M, N, K) -> (splits, row-block wavefronts per workgroup, unroll)
+    for m, n, k, splits, blocks, unroll in [(8, 2048, 2048, 4, 1, 2), (8, 5632, 2048, 2, 4, 4),
+                                            (8, 4096, 4096, 4, 2, 4), (8, 14336, 4096, 2, 8, 8),
+                                            (8, 2048, 5632, 8, 1, 3), (8, 8192, 8192, 4, 4, 8),
+                                            (8, 28672, 8192, 4, 4, 8), (4, 28672, 8192, 4, 2, 8),
+                                            (4, 8192, 8192, 4, 4, 8), (3, 6000, 14336, 8, 2, 7),
+                                            (6, 64, 128, 4, 1, 1)]:
+        plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+        assert (plan["kernel"], plan["splits"], plan["max_blocks"], plan["rows"], plan["unroll"]) == \
+            ("mfma_pair", splits, blocks, 1, unroll), (m, n, k)
+    monkeypatch.setenv("W4A16_DECODE", "mfma_pair")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 64, 2048, 128)["kernel"] == "mfma_pair"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma"   # M = 1
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 8320, 128)["kernel"] == "mfma"   # beyond LDS
+    monkeypatch.delenv("W4A16_DECODE")
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # an explicit VALU row count keeps auto off it
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] != "mfma_pair"
+
+
+def test_mfma_oneshot_plan_shapes(monkeypatch):
+    monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     for m, n, k, rows, splits, unroll in [(8, 2048, 2048, 1, 4, 4), (8, 5632, 2048, 2, 4, 4),
                                           (8, 14336, 4096, 2, 4, 8), (8, 4096, 4096, 1, 8, 4),
@@ -142,7 +168,6 @@ def test_mfma_oneshot_plan_shapes(monkeypatch):
         plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
             ("mfma_oneshot", rows, splits, unroll), (m, n, k)
-    monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma_oneshot"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 8320, 128)["kernel"] == "mfma"   # rows too long
 
@@ -156,7 +181,7 @@ def test_oneshot_plan_shapes(monkeypatch):
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 14336, 128)["kernel"] == "mfma"     # M > 2, long rows
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 28672, 128)["kernel"] == "mfma"     # M > 2, long rows
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "oneshot"
