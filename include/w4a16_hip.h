@@ -124,13 +124,16 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splitting K (4|8), unroll = groups per wavefront (0 = ceil(K / 128 /
  *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
  *     1..8 with 8), max_blocks ignored.
- *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 8): splits = wavefronts splitting the
- *     K / 256 group pairs (2|4|8), max_blocks = 8-row-block wavefronts per
- *     workgroup (1|2|4|8, splits * max_blocks <= 16), rows = 8-row blocks
- *     per wavefront (1), unroll = group pairs per wavefront (0 = ceil(K /
- *     256 / splits); else 1..8 with splits * unroll >= ceil(K / 256));
- *     staged activations, biases and reduction
- *     within 160 KiB of LDS (K <= 8192 at M = 8, 16384 at M <= 4).
+ *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 8, K <= 32768): splits = wavefronts
+ *     splitting the K / 256 group pairs (2|4|8), max_blocks = 8-row-block
+ *     wavefronts per workgroup (1|2|4|8, splits * max_blocks <= 16), unroll =
+ *     group pairs per wavefront (0 = ceil(K / 256 / splits); else with
+ *     splits * unroll >= ceil(K / 256)), rows = group pairs of activations
+ *     staged in LDS at a time (0 = automatic; splits * unroll = whole rows:
+ *     unroll 1..8; 8 = double-buffered chunks: splits 4 with max_blocks
+ *     1|2|4 and unroll 7|8, or splits 8 with max_blocks 1|2 and unroll
+ *     3..8|10|12|14|16);
+ *     staged activations, biases and reduction within 160 KiB of LDS.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..8 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

@@ -18,9 +18,12 @@
 #include "w4a16_kernels.h"
 
 namespace w4a16_internal {
-// w4a16_pair.hip: the paired-group MFMA kernel for M = 2..8
-int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int rb, int gpw);
-int launch_mfma_pair(int sk, int sn, int rb, int gpw, int M, const void* x, const uint8_t* w, const void* s,
+// w4a16_pair.hip: the paired-group MFMA kernel for M = 2..8 (chunk = staged
+// group pairs per chunk, 0 = the launcher's choice)
+int mfma_pair_auto_chunk(int64_t M, int sk, int sn, int gpw);
+bool mfma_pair_instantiated(int64_t M, int sk, int sn, int chunk, int gpw);
+int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int gpw);
+int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream);
 }  // namespace w4a16_internal
 
@@ -210,14 +213,19 @@ Plan plan_mfma_oneshot(int64_t M, int64_t N, int64_t K) {
 
 // Paired-group MFMA kernel (M = 2..8, w4a16_pair.h). Plan fields: splits =
 // SK wavefronts splitting the K / 256 group pairs, max_blocks = SN row-block
-// wavefronts per workgroup, rows = 8-row blocks per wavefront, unroll = pairs
-// per wavefront. Launch shape from the M = 4 and M = 8 sweeps over the
+// wavefronts per workgroup (one 8-row block each), rows = group pairs staged
+// per chunk (splits * unroll: whole rows), unroll = pairs per wavefront. Launch shape from the M = 4 and M = 8 sweeps over the
 // benchmark shapes: SK = 4 on short rows of narrow layers and 2 on wide ones
 // (up to 8 pairs: N <= 4096; 9..16 pairs: N < 8192), 8 for 17..24 pairs, 4
-// up to 32, 8 beyond; a workgroup takes the largest of 8, 16, 32, 64 rows
+// up to 32, 8 beyond (10, 12, 14 or 16 pairs per wavefront past 8); rows
+// longer than 16 pairs whose staging would pass 80 KiB go in 8-pair chunks,
+// which lets two workgroups share a CU (M = 8: 14336 x 4096 12.8 us, 28672 x
+// 8192 46.3 us against 16.9 and 57.9 with the looped MFMA kernel); a
+// workgroup takes the largest of 8, 16, 32, 64 rows
 // that leaves >= 176 workgroups, at most 16 wavefronts, except that M <= 4
 // layers with over 512 such workgroups run two 8-wavefront workgroups per
-// CU (each stages its activations while the other streams weights).
+// CU when those stage whole rows (each stages its activations while the
+// other streams weights).
 Plan plan_mfma_pair(int64_t M, int64_t N, int64_t K) {
     Plan p;
     p.kernel = W4A16_KERNEL_MFMA_PAIR;
@@ -233,25 +241,27 @@ Plan plan_mfma_pair(int64_t M, int64_t N, int64_t K) {
         sk = 4;
     else
         sk = 8;
-    const int gpw = (int)((pairs + sk - 1) / sk);
+    int gpw = (int)((pairs + sk - 1) / sk);
+    if (gpw > 8) gpw = (gpw + 1) & ~1;   // chunked instantiations: 10, 12, 14, 16
     int rows = 8;
     while (rows < 64 && N / (2 * rows) >= 176) rows *= 2;
     int sn = rows / 8;
     while (sk * sn > 16) sn /= 2;
     if (M <= 4 && sk * sn == 16 && N / (4 * sn) > 512 &&
-        2 * w4a16_internal::mfma_pair_lds_bytes(M, K, sk, sn / 2, 1, gpw) <= kMaxLdsBytes)
+        w4a16_internal::mfma_pair_auto_chunk(M, sk, sn / 2, gpw) == sk * gpw &&
+        2 * w4a16_internal::mfma_pair_lds_bytes(M, K, sk, sn / 2, 0, gpw) <= kMaxLdsBytes)
         sn /= 2;
     p.splits = sk;
     p.max_blocks = sn;
-    p.rows = 1;
+    p.rows = w4a16_internal::mfma_pair_auto_chunk(M, sk, sn, gpw);
     p.unroll = gpw;
     return p;
 }
 
 bool mfma_pair_fits(int64_t M, int64_t N, int64_t K) {
-    if (M < 2 || M > 8 || K < 128 || K % 128 != 0 || K > 16384) return false;
+    if (M < 2 || M > 8 || K < 128 || K % 128 != 0 || K > 32768) return false;
     const Plan p = plan_mfma_pair(M, N, K);
-    return p.unroll <= 8 &&
+    return w4a16_internal::mfma_pair_instantiated(M, p.splits, p.max_blocks, p.rows, p.unroll) &&
            w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
 }
 
@@ -288,8 +298,8 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // keeps auto on the looped VALU kernel whose rows it sets.
     // Measured routing (M = 1..8 sweeps over the benchmark shapes):
     //   M = 1: one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
-    //   M >= 3: the paired-group MFMA kernel wherever its activations fit in
-    //   LDS (K <= 8192 at M = 8, 16384 at M <= 4); beyond that as before:
+    //   M >= 3: the paired-group MFMA kernel up to K = 32768 (activations
+    //   staged whole or in chunks); beyond that as before:
     //   one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
     //   small layers (K, N <= 5632; each workgroup re-stages M*K activations,
     //   which on large layers outweighs the weights it streams), one-shot

@@ -17,6 +17,7 @@ int ensure_lds(const void* kernel, int bytes);     // w4a16_hip.hip: raise the d
 namespace {
 
 constexpr int kMaxLdsBytes = 160 * 1024;
+constexpr int kChunkPairs = 8;   // group pairs per staged chunk (K = 2048 per chunk)
 
 int fail(int code, const char* message) {
     w4a16_internal::set_last_error(message);
@@ -25,24 +26,24 @@ int fail(int code, const char* message) {
 
 using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int);
 
-// Instantiated shapes: SK in {2, 4, 8} wavefronts splitting K, SN in {1, 2,
-// 4, 8} row-block wavefronts with SK * SN <= 16, one 8-row block per
-// wavefront, 1..8 group pairs per wavefront, 4 or 8 row slots.
+// Instantiated shapes, whole rows staged (chunk = splits * unroll pairs):
+// SK in {2, 4, 8} wavefronts splitting K, SN in {1, 2, 4, 8} row-block
+// wavefronts with SK * SN <= 16, one 8-row block per wavefront, 1..8 group
+// pairs per wavefront, 4 or 8 row slots.
 template <int MS>
-Kern pick(int sk, int sn, int rb, int gpw) {
+Kern pick_whole(int sk, int sn, int gpw) {
     using namespace w4a16;
-    if (rb != 1) return nullptr;
 #define W4A16_G(SK, SN)                                                                                        \
     if (sk == SK && sn == SN) {                                                                                \
         switch (gpw) {                                                                                         \
-            case 1: return gemv_mfma_pair<SK, SN, 1, 1, MS>;                                                   \
-            case 2: return gemv_mfma_pair<SK, SN, 1, 2, MS>;                                                   \
-            case 3: return gemv_mfma_pair<SK, SN, 1, 3, MS>;                                                   \
-            case 4: return gemv_mfma_pair<SK, SN, 1, 4, MS>;                                                   \
-            case 5: return gemv_mfma_pair<SK, SN, 1, 5, MS>;                                                   \
-            case 6: return gemv_mfma_pair<SK, SN, 1, 6, MS>;                                                   \
-            case 7: return gemv_mfma_pair<SK, SN, 1, 7, MS>;                                                   \
-            case 8: return gemv_mfma_pair<SK, SN, 1, 8, MS>;                                                   \
+            case 1: return gemv_mfma_pair<SK, SN, 1, 1, MS, SK * 1>;                                           \
+            case 2: return gemv_mfma_pair<SK, SN, 1, 2, MS, SK * 2>;                                           \
+            case 3: return gemv_mfma_pair<SK, SN, 1, 3, MS, SK * 3>;                                           \
+            case 4: return gemv_mfma_pair<SK, SN, 1, 4, MS, SK * 4>;                                           \
+            case 5: return gemv_mfma_pair<SK, SN, 1, 5, MS, SK * 5>;                                           \
+            case 6: return gemv_mfma_pair<SK, SN, 1, 6, MS, SK * 6>;                                           \
+            case 7: return gemv_mfma_pair<SK, SN, 1, 7, MS, SK * 7>;                                           \
+            case 8: return gemv_mfma_pair<SK, SN, 1, 8, MS, SK * 8>;                                           \
             default: return nullptr;                                                                           \
         }                                                                                                      \
     }
@@ -53,18 +54,84 @@ Kern pick(int sk, int sn, int rb, int gpw) {
     return nullptr;
 }
 
+// Chunked staging (two buffers of kChunkPairs pairs): SK = 4 with SN in {1,
+// 2, 4} and 7 or 8 pairs per wavefront, or SK = 8 with SN in {1, 2} and
+// 3..8, 10, 12, 14 or 16.
+template <int MS>
+Kern pick_chunked(int sk, int sn, int gpw) {
+    using namespace w4a16;
+    constexpr int C = kChunkPairs;
+#define W4A16_G4(SN)                                                                                           \
+    if (sk == 4 && sn == SN) {                                                                                 \
+        if (gpw == 7) return gemv_mfma_pair<4, SN, 1, 7, MS, C>;                                               \
+        if (gpw == 8) return gemv_mfma_pair<4, SN, 1, 8, MS, C>;                                               \
+        return nullptr;                                                                                        \
+    }
+#define W4A16_G8(SN)                                                                                           \
+    if (sk == 8 && sn == SN) {                                                                                 \
+        switch (gpw) {                                                                                         \
+            case 3: return gemv_mfma_pair<8, SN, 1, 3, MS, C>;                                                 \
+            case 4: return gemv_mfma_pair<8, SN, 1, 4, MS, C>;                                                 \
+            case 5: return gemv_mfma_pair<8, SN, 1, 5, MS, C>;                                                 \
+            case 6: return gemv_mfma_pair<8, SN, 1, 6, MS, C>;                                                 \
+            case 7: return gemv_mfma_pair<8, SN, 1, 7, MS, C>;                                                 \
+            case 8: return gemv_mfma_pair<8, SN, 1, 8, MS, C>;                                                 \
+            case 10: return gemv_mfma_pair<8, SN, 1, 10, MS, C>;                                               \
+            case 12: return gemv_mfma_pair<8, SN, 1, 12, MS, C>;                                               \
+            case 14: return gemv_mfma_pair<8, SN, 1, 14, MS, C>;                                               \
+            case 16: return gemv_mfma_pair<8, SN, 1, 16, MS, C>;                                               \
+            default: return nullptr;                                                                           \
+        }                                                                                                      \
+    }
+    W4A16_G4(1) W4A16_G4(2) W4A16_G4(4) W4A16_G8(1) W4A16_G8(2)
+#undef W4A16_G4
+#undef W4A16_G8
+    return nullptr;
+}
+
+// Staged pairs per chunk when the caller leaves it to the launcher: whole
+// rows up to 16 pairs (K <= 4096) or while the workgroup's LDS stays within
+// half of the CU's (two workgroups per CU), else kChunkPairs. Measured at M
+// = 4 and 8: 8-pair chunks beat whole rows from K = 5632 (M = 8: 5632 x 2048
+// 5.6 against 6.2 us, 8192 x 8192 12.3 against 13.7) and beat 16-pair chunks
+// on the longest rows (M = 4, 28672 x 8192: 39.6 against 56.1 us).
+int auto_chunk(int64_t M, int sk, int sn, int gpw) {
+    const int64_t pairs = (int64_t)sk * gpw;
+    if (pairs <= 16 || w4a16::pair_lds_bytes(M, pairs, pairs, (int64_t)sk * sn, 1) <= kMaxLdsBytes / 2)
+        return (int)pairs;
+    return kChunkPairs;
+}
+
 }  // namespace
 
 namespace w4a16_internal {
 
-int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int rb, int gpw) {
-    (void)K;
-    return w4a16::pair_lds_bytes(M, (int64_t)sk * gpw, (int64_t)sk * sn, rb);
+int mfma_pair_auto_chunk(int64_t M, int sk, int sn, int gpw) { return auto_chunk(M, sk, sn, gpw); }
+
+Kern pick(int64_t M, int sk, int sn, int chunk, int gpw) {
+    if (chunk == sk * gpw) return M <= 4 ? pick_whole<4>(sk, sn, gpw) : pick_whole<8>(sk, sn, gpw);
+    if (chunk == kChunkPairs) return M <= 4 ? pick_chunked<4>(sk, sn, gpw) : pick_chunked<8>(sk, sn, gpw);
+    return nullptr;
 }
 
-// Launch gemv_mfma_pair<sk, sn, rb, gpw> over [M, K] x [N, K]^T. The caller
-// has checked pointers, group size 128 and 16-byte alignment.
-int launch_mfma_pair(int sk, int sn, int rb, int gpw, int M, const void* x, const uint8_t* w, const void* s,
+bool mfma_pair_instantiated(int64_t M, int sk, int sn, int chunk, int gpw) {
+    if (chunk == 0) chunk = auto_chunk(M, sk, sn, gpw);
+    return pick(M, sk, sn, chunk, gpw) != nullptr;
+}
+
+// chunk: staged pairs per chunk, 0 = auto_chunk
+int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int gpw) {
+    (void)K;
+    const int64_t pairs = (int64_t)sk * gpw;
+    if (chunk == 0) chunk = auto_chunk(M, sk, sn, gpw);
+    return w4a16::pair_lds_bytes(M, pairs, chunk, (int64_t)sk * sn, 1);
+}
+
+// Launch gemv_mfma_pair over [M, K] x [N, K]^T: sk wavefronts splitting the
+// pairs, sn row-block wavefronts per workgroup, gpw pairs per wavefront,
+// `chunk` staged pairs per chunk (0 = auto_chunk; sk * gpw = whole rows).
+// The caller has checked pointers, group size 128 and 16-byte alignment.
+int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream) {
     if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel needs 2 <= M <= 8");
     if (K < 128 || K % 128 != 0) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel: K must be a positive multiple of 128");
@@ -73,16 +140,20 @@ int launch_mfma_pair(int sk, int sn, int rb, int gpw, int M, const void* x, cons
     if (gpw == 0 && sk > 0) gpw = (pairs + sk - 1) / sk;   // the fewest pairs per wavefront that cover K
     if (gpw < 1 || (int64_t)sk * gpw < pairs)
         return fail(W4A16_ERR_CONFIG, "paired MFMA kernel: splits * unroll must cover the K / 256 group pairs");
-    const Kern kern = M <= 4 ? pick<4>(sk, sn, rb, gpw) : pick<8>(sk, sn, rb, gpw);
+    if (sk != 2 && sk != 4 && sk != 8) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel: splits 2, 4 or 8");
+    if (chunk == 0) chunk = auto_chunk(M, sk, sn, gpw);
+    const Kern kern = pick(M, sk, sn, chunk, gpw);
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
-                    "paired MFMA kernel: splits 2, 4 or 8, wavefront blocks 1, 2, 4 or 8 with splits * blocks "
-                    "<= 16, rows 1, unroll 1..8");
-    const int64_t lds = mfma_pair_lds_bytes(M, K, sk, sn, rb, gpw);
+                    "paired MFMA kernel: no instantiation for this shape (whole rows, rows = splits * unroll: "
+                    "splits 2, 4 or 8, blocks 1, 2, 4 or 8 with splits * blocks <= 16, unroll 1..8; chunks, rows = "
+                    "8: splits 4 with blocks 1, 2 or 4 and unroll 7 or 8, or splits 8 with blocks 1 or 2 and "
+                    "unroll 3..8, 10, 12, 14 or 16)");
+    const int64_t lds = w4a16::pair_lds_bytes(M, (int64_t)sk * gpw, chunk, (int64_t)sk * sn, 1);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel: activations do not fit in LDS");
     const int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
     if (rc != W4A16_OK) return rc;
-    const int rows = 8 * rb * sn;
+    const int rows = 8 * sn;
     const int blocks = (N + rows - 1) / rows;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream,
                        static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),

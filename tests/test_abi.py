@@ -109,11 +109,12 @@ ALIGNED = 1 << 20
         (2, 28672, 128, ALIGNED, "mfma"),      # very long rows
         (4, 8192, 128, ALIGNED, "mfma_pair"),
         (8, 8192, 128, ALIGNED, "mfma_pair"),
-        (8, 8320, 128, ALIGNED, "mfma"),           # M*K beyond LDS at M = 8
-        (4, 14336, 128, ALIGNED, "mfma_pair"),     # M <= 4 stages up to K = 16384
+        (8, 8320, 128, ALIGNED, "mfma_pair"),      # rows past LDS: staged in chunks
+        (4, 14336, 128, ALIGNED, "mfma_pair"),
         (4, 16384, 128, ALIGNED, "mfma_pair"),
-        (4, 16512, 128, ALIGNED, "mfma"),          # beyond 8 pairs per wavefront
-        (4, 28672, 128, ALIGNED, "mfma"),
+        (8, 28672, 128, ALIGNED, "mfma_pair"),
+        (8, 32768, 128, ALIGNED, "mfma_pair"),
+        (8, 32896, 128, ALIGNED, "mfma"),          # beyond 16 pairs per wavefront
         (5, 2048, 128, ALIGNED, "mfma_pair"),
         (8, 4096, 128, ALIGNED, "mfma_pair"),
         (8, 5632, 128, ALIGNED, "mfma_pair"),
@@ -139,20 +140,24 @@ def test_plan_misaligned_weights_take_generic():
 def test_mfma_pair_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
-    # (M, N, K) -> (splits, row-block wavefronts per workgroup, unroll)
-    for m, n, k, splits, blocks, unroll in [(8, 2048, 2048, 4, 1, 2), (8, 5632, 2048, 2, 4, 4),
-                                            (8, 4096, 4096, 4, 2, 4), (8, 14336, 4096, 2, 8, 8),
-                                            (8, 2048, 5632, 8, 1, 3), (8, 8192, 8192, 4, 4, 8),
-                                            (8, 28672, 8192, 4, 4, 8), (4, 28672, 8192, 4, 2, 8),
-                                            (4, 8192, 8192, 4, 4, 8), (3, 6000, 14336, 8, 2, 7),
-                                            (6, 64, 128, 4, 1, 1)]:
+    # (M, N, K) -> (splits, row-block wavefronts per workgroup, unroll, staged pairs per chunk)
+    for m, n, k, splits, blocks, unroll, chunk in [
+            (8, 2048, 2048, 4, 1, 2, 8), (8, 5632, 2048, 2, 4, 4, 8), (8, 4096, 4096, 4, 2, 4, 16),
+            (8, 14336, 4096, 2, 8, 8, 16),                     # whole rows up to 16 pairs
+            (8, 2048, 5632, 8, 1, 3, 8), (8, 8192, 8192, 4, 4, 8, 8), (8, 28672, 8192, 4, 4, 8, 8),
+            (8, 4096, 14336, 8, 2, 7, 8), (8, 8192, 28672, 8, 2, 14, 8), (5, 300, 16512, 8, 1, 10, 8),
+            (4, 28672, 8192, 4, 2, 8, 32),                     # two whole-row workgroups per CU
+            (4, 8192, 8192, 4, 4, 8, 8), (4, 2048, 5632, 8, 1, 3, 24), (3, 6000, 14336, 8, 2, 7, 8),
+            (6, 64, 128, 4, 1, 1, 4)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
-        assert (plan["kernel"], plan["splits"], plan["max_blocks"], plan["rows"], plan["unroll"]) == \
-            ("mfma_pair", splits, blocks, 1, unroll), (m, n, k)
+        assert (plan["kernel"], plan["splits"], plan["max_blocks"], plan["unroll"], plan["rows"]) == \
+            ("mfma_pair", splits, blocks, unroll, chunk), (m, n, k)
     monkeypatch.setenv("W4A16_DECODE", "mfma_pair")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 64, 2048, 128)["kernel"] == "mfma_pair"
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 2, 64, 32768, 128)
+    assert (plan["kernel"], plan["splits"], plan["unroll"], plan["rows"]) == ("mfma_pair", 8, 16, 8)
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma"   # M = 1
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 8320, 128)["kernel"] == "mfma"   # beyond LDS
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 32896, 128)["kernel"] == "mfma"   # too long
     monkeypatch.delenv("W4A16_DECODE")
     monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # an explicit VALU row count keeps auto off it
     assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] != "mfma_pair"
@@ -181,7 +186,7 @@ def test_oneshot_plan_shapes(monkeypatch):
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 28672, 128)["kernel"] == "mfma"     # M > 2, long rows
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 34816, 128)["kernel"] == "mfma"     # M > 2, long rows
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "oneshot"

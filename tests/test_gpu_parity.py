@@ -142,62 +142,87 @@ def test_mfma_oneshot_variants(gpu, m, rows, splits, k, n):
     assert_parity(out, expected(x, p, s), f"mfma_oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
 
 
-def _pair_lds(m, k, splits, blocks):
-    pairs = (k // 128 + 1) // 2
-    unroll = -(-pairs // splits)
+def _pair_lds(m, staged, chunk, splits, blocks):
     slots = 4 if m <= 4 else 8
-    staged = splits * unroll
-    return staged * 16 * 2 * slots * 16 + staged * 128 + splits * blocks * 1024
+    buffers = 2 if chunk < staged else 1
+    return buffers * (chunk * 16 * 2 * slots * 16 + chunk * 128) + splits * blocks * 1024
 
 
-# paired-group MFMA: every (splits, blocks) class, odd group counts (a half
-# pair zero-filled), splits * unroll past the last pair (padding pairs),
-# ragged N, both row-slot widths (M <= 4 and M > 4), K up to LDS
+# paired-group MFMA, whole rows staged (rows = splits * unroll): every
+# (splits, blocks) class, odd group counts (a half pair zero-filled), splits *
+# unroll past the last pair (padding pairs), ragged N, both row-slot widths
+# (M <= 4 and M > 4), K up to LDS
 @pytest.mark.parametrize("splits,blocks", [(2, 1), (4, 2), (8, 1), (2, 8), (4, 4), (8, 2)])
 @pytest.mark.parametrize("k,n", [(128, 7), (384, 9), (1152, 33), (2048, 2048), (3968, 21), (5632, 100),
                                  (8192, 64), (16384, 24)])
 @pytest.mark.parametrize("m", [2, 3, 4, 6, 8])
-def test_mfma_pair_variants(gpu, m, splits, blocks, k, n):
+def test_mfma_pair_whole(gpu, m, splits, blocks, k, n):
     pairs = (k // 128 + 1) // 2
-    if -(-pairs // splits) > 8 or _pair_lds(m, k, splits, blocks) > 160 * 1024:
+    unroll = -(-pairs // splits)
+    staged = splits * unroll
+    if unroll > 8 or _pair_lds(m, staged, staged, splits, blocks) > 160 * 1024:
         x, p, s = make_case(m, k, n, seed=1)
-        with pytest.raises(_lib.W4A16Error, match="cover the K / 256|do not fit in LDS|unroll 1..8"):
-            _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, splits, 0, blocks)
+        with pytest.raises(_lib.W4A16Error, match="no instantiation|do not fit in LDS"):
+            _run_tuned(gpu, x, p, s, MFMA_PAIR, staged, splits, unroll, blocks)
         return
     x, p, s = make_case(m, k, n, seed=m * 17 + k + n)
-    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, splits, 0, blocks)
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, staged, splits, unroll, blocks)
     assert_parity(out, expected(x, p, s), f"mfma_pair M={m} splits={splits} blocks={blocks} K={k} N={n}")
 
 
+# chunked staging (rows = 8 pairs per chunk, two buffers): every
+# instantiated (splits, blocks, unroll) class, odd group counts, padding
+# pairs and a partial last chunk, rows up to K = 32768, ragged N
+@pytest.mark.parametrize("splits,blocks,k", [(4, 1, 7168), (4, 4, 8192), (4, 2, 6400), (8, 1, 5632), (8, 2, 5760),
+                                             (8, 1, 8192), (8, 2, 14336), (8, 1, 16512), (8, 2, 28672),
+                                             (8, 1, 32768)])
+@pytest.mark.parametrize("m", [2, 4, 5, 8])
+def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
+    n = 37
+    pairs = (k // 128 + 1) // 2
+    unroll = -(-pairs // splits)
+    if unroll > 8:
+        unroll += unroll % 2
+    assert _pair_lds(m, splits * unroll, 8, splits, blocks) <= 160 * 1024
+    x, p, s = make_case(m, k, n, seed=m * 7 + k + blocks)
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 8, splits, unroll, blocks)
+    assert_parity(out, expected(x, p, s), f"mfma_pair chunked M={m} splits={splits} blocks={blocks} K={k}")
+
+
 @pytest.mark.parametrize("m,k,n", [(3, 2048, 5632), (5, 4096, 4096), (7, 5632, 2048), (8, 8192, 1000),
-                                   (4, 14336, 300)])
+                                   (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
+                                   (5, 8320, 77)])
 def test_default_dispatch_mfma_pair(gpu, m, k, n):
     x, p, s = make_case(m, k, n, seed=m + k + n)
     assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "mfma_pair"
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"pair default M={m} K={k} N={n}")
 
 
-def test_mfma_pair_more_pairs_than_needed(gpu):
-    # splits * unroll = 24 pairs for the 2 of K = 512: padding pairs read zeros, weight 0
+@pytest.mark.parametrize("rows", [0, 24, 8])
+def test_mfma_pair_more_pairs_than_needed(gpu, rows):
+    # splits * unroll = 24 pairs for the 2 of K = 512: padding pairs read
+    # zeros and weigh 0, staged whole (24) or in chunks (8, and 0 = auto)
     x, p, s = make_case(5, 512, 40, seed=5)
-    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, 8, 3, 1)
-    assert_parity(out, expected(x, p, s), "mfma_pair padded")
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, rows, 8, 3, 1)
+    assert_parity(out, expected(x, p, s), f"mfma_pair padded rows={rows}")
 
 
 def test_mfma_pair_rejects(gpu):
     x, p, s = make_case(1, 2048, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="2 <= M <= 8"):
-        _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, 4, 0, 1)
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 1)
     x, p, s = make_case(4, 2048, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="cover the K / 256"):
-        _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, 2, 1, 1)
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 2, 1, 1)
     with pytest.raises(_lib.W4A16Error, match="splits 2, 4 or 8"):
-        _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, 4, 0, 8)   # 32 wavefronts
-    with pytest.raises(_lib.W4A16Error, match="splits 2, 4 or 8"):
-        _run_tuned(gpu, x, p, s, MFMA_PAIR, 2, 4, 0, 1)   # two blocks per wavefront
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 3, 0, 1)
+    with pytest.raises(_lib.W4A16Error, match="no instantiation"):
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 8)   # 32 wavefronts
+    with pytest.raises(_lib.W4A16Error, match="no instantiation"):
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 2, 4, 0, 1)   # 2-pair chunks
     x, p, s = make_case(8, 8320, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="do not fit in LDS"):
-        _run_tuned(gpu, x, p, s, MFMA_PAIR, 1, 8, 0, 1)
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 40, 8, 5, 1)  # whole rows of 40 pairs
 
 
 @pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7)])
