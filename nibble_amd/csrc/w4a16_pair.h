@@ -41,9 +41,10 @@ namespace w4a16 {
 // offset from a per-lane base (no clamps).
 //
 // Chunks (C pairs < SK * GPW): rows too long for LDS are staged C pairs at a
-// time into two alternating buffers. Every weight load is still issued up
-// front; chunk c + 1's activation loads are issued before chunk c's MFMAs
-// and written to the other buffer after them, one barrier per chunk.
+// time into two alternating buffers, one barrier per chunk: chunk c + 1 is
+// written to the other buffer after chunk c's MFMAs. Loads are requested
+// chunk by chunk (activations, then that chunk's scales and weights), the
+// first LA chunks up front and chunk c + LA when chunk c starts.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int pair_row_slots(int M) { return M <= 4 ? 4 : 8; }
 
@@ -57,7 +58,7 @@ __host__ __device__ constexpr int64_t pair_lds_bytes(int64_t M, int64_t pairs, i
            waves * rb * 64 * 16;
 }
 
-template <int SK, int SN, int RB, int GPW, int MS, int C>
+template <int SK, int SN, int RB, int GPW, int MS, int C, int LA = 64>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
                f16* __restrict__ out, int M, int N, int K) {
@@ -66,6 +67,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     constexpr int LS = 2 * MS;                 // units per line
     constexpr int P = SK * GPW;                // pairs the workgroup steps over
     static_assert(C % SK == 0 && C <= P, "a chunk is a whole number of steps");
+    static_assert(LA >= 1, "at least the first chunk is requested up front");
     constexpr int NC = (P + C - 1) / C;        // chunks
     constexpr int NB = NC > 1 ? 2 : 1;         // staging buffers
     constexpr int JPC = C / SK;                // steps per chunk
@@ -132,30 +134,47 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         }
     };
 
-    // 1. chunk 0's activations, then every weight and scale (clamped
-    // addresses; groups past K weighted 0 below)
-    u32x4 a[UPT];
-    load_chunk(a, 0);
+    // 1. loads, chunk by chunk in the order they are consumed: a chunk's
+    // activations, then its steps' scales and weights (clamped addresses;
+    // groups past K weighted 0 below). The first LA chunks are requested up
+    // front and chunk c + LA at the start of chunk c, so a chunk's
+    // activations never queue behind weights of much later chunks (a
+    // wavefront's loads return in issue order).
     const uint16_t* sbase = reinterpret_cast<const uint16_t*>(scales);
+    u32x4 a[NC][UPT];
     uint32_t sv[GPW][RB];
     u32x4 wv[GPW][RB];
+    auto issue = [&](int cc) {
+        load_chunk(a[cc], cc);
+        __builtin_amdgcn_sched_barrier(0);   // keep the activations ahead of the weights
 #pragma unroll
-    for (int j = 0; j < GPW; ++j)
+        for (int jl = 0; jl < JPC; ++jl) {
+            const int j = cc * JPC + jl;
+            if (j < GPW) {
 #pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const int n = min(n0 + 8 * b + brow, N - 1);
-            sv[j][b] = sbase[(size_t)n * G + min(group(j, bhalf), G - 1)];
+                for (int b = 0; b < RB; ++b) {
+                    const int n = min(n0 + 8 * b + brow, N - 1);
+                    sv[j][b] = sbase[(size_t)n * G + min(group(j, bhalf), G - 1)];
+                }
+            }
         }
 #pragma unroll
-    for (int j = 0; j < GPW; ++j)
+        for (int jl = 0; jl < JPC; ++jl) {
+            const int j = cc * JPC + jl;
+            if (j < GPW) {
 #pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            const int n = min(n0 + 8 * b + brow, N - 1);
-            wv[j][b] = load_stream(reinterpret_cast<const u32x4*>(
-                w + (size_t)n * row_bytes + (uint32_t)min(group(j, bhalf), G - 1) * 64u + q * 16));
+                for (int b = 0; b < RB; ++b) {
+                    const int n = min(n0 + 8 * b + brow, N - 1);
+                    wv[j][b] = load_stream(reinterpret_cast<const u32x4*>(
+                        w + (size_t)n * row_bytes + (uint32_t)min(group(j, bhalf), G - 1) * 64u + q * 16));
+                }
+            }
         }
+    };
+#pragma unroll
+    for (int cc = 0; cc < NC && cc < LA; ++cc) issue(cc);
     __builtin_amdgcn_sched_barrier(0);
-    put_chunk(a, 0, 0);
+    put_chunk(a[0], 0, 0);
     __syncthreads();
 
     // 2. chunks of pairs: A fragments of step j+1 read while step j runs on
@@ -175,7 +194,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         const int buf = c % NB;
         const u32x4* xb = xs + buf * XS;
         const float* bb = base + buf * C * 32;
-        if (c + 1 < NC) load_chunk(a, c + 1);
+        if (c + LA < NC) issue(c + LA);
         auto fetch = [&](u32x4 (&av)[4], f32x4& bv, int jl) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) av[t] = xb[jl * SK * 16 * LS + toff[t]];
@@ -214,7 +233,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             }
         }
         if (c + 1 < NC) {
-            put_chunk(a, c + 1, (c + 1) % NB);
+            put_chunk(a[c + 1], c + 1, (c + 1) % NB);
             __syncthreads();
         }
     }
