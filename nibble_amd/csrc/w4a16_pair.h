@@ -40,6 +40,10 @@ namespace w4a16 {
 // staged as zeros (weight 0), so the fragment reads of every step are a fixed
 // offset from a per-lane base (no clamps).
 //
+// MB: the per-(group, row) bias comes from 4 more MFMAs per step (A against
+// the constant -(1032, 1032, 1152, 1152, ...), shared by the RB blocks)
+// instead of staging dot products and an LDS table.
+//
 // Chunks (C pairs < SK * GPW): rows too long for LDS are staged C pairs at a
 // time into two alternating buffers, one barrier per chunk: chunk c + 1 is
 // written to the other buffer after chunk c's MFMAs. Loads are requested
@@ -58,7 +62,7 @@ __host__ __device__ constexpr int64_t pair_lds_bytes(int64_t M, int64_t pairs, i
            waves * rb * 64 * 16;
 }
 
-template <int SK, int SN, int RB, int GPW, int MS, int C, int LA = 64>
+template <int SK, int SN, int RB, int GPW, int MS, int C, int LA = 64, bool MB = false>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
                f16* __restrict__ out, int M, int N, int K) {
@@ -118,18 +122,20 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             pv.w = as_u32(as_f16x2(pv.w) * sixteenth);
             if (zero) pv = (u32x4){0u, 0u, 0u, 0u};
             float cs = 0.0f;
-            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.x), b0, cs, false);
-            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.y), b1, cs, false);
-            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.z), b0, cs, false);
-            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.w), b1, cs, false);
-            // the 16 units of (m, g) sit in 16 consecutive lanes (a DPP row)
-            cs += dpp<0xB1>(cs);
-            cs += dpp<0x4E>(cs);
-            cs += dpp<0x141>(cs);
-            cs += dpp<0x140>(cs);
+            if (!MB) {
+                cs = __builtin_amdgcn_fdot2(as_f16x2(pv.x), b0, cs, false);
+                cs = __builtin_amdgcn_fdot2(as_f16x2(pv.y), b1, cs, false);
+                cs = __builtin_amdgcn_fdot2(as_f16x2(pv.z), b0, cs, false);
+                cs = __builtin_amdgcn_fdot2(as_f16x2(pv.w), b1, cs, false);
+                // the 16 units of (m, g) sit in 16 consecutive lanes (a DPP row)
+                cs += dpp<0xB1>(cs);
+                cs += dpp<0x4E>(cs);
+                cs += dpp<0x141>(cs);
+                cs += dpp<0x140>(cs);
+            }
             if (m < M) {
                 xb[(((gl >> 1) * 4 + t) * 4 + qq) * LS + ((m + MS * (gl & 1) + 4 * qq + t) & (LS - 1))] = pv;
-                if ((ul & 15) == 0) bb[gl * 16 + m] = -cs;
+                if (!MB && (ul & 15) == 0) bb[gl * 16 + m] = -cs;
             }
         }
     };
@@ -198,11 +204,11 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         auto fetch = [&](u32x4 (&av)[4], f32x4& bv, int jl) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) av[t] = xb[jl * SK * 16 * LS + toff[t]];
-            bv = *reinterpret_cast<const f32x4*>(bb + jl * SK * 32 + boff);
+            if (!MB) bv = *reinterpret_cast<const f32x4*>(bb + jl * SK * 32 + boff);
         };
         const int steps = (c + 1) * JPC <= GPW ? JPC : GPW - c * JPC;
         u32x4 A0[4], A1[4];
-        f32x4 B0, B1;
+        f32x4 B0 = {0.0f, 0.0f, 0.0f, 0.0f}, B1 = {0.0f, 0.0f, 0.0f, 0.0f};
         fetch(A0, B0, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -216,6 +222,19 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
                 if (jl + 1 < steps) fetch(nxt, nbv, jl + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 const bool in_range = group(j, bhalf) < G;
+                if (MB) {
+                    // the bias rows on the matrix cores: A against the
+                    // constant -(1032, 1032, 1152, 1152, ...) of the offset
+                    // decode (exact products, fp32 sums)
+                    const f16x8 cneg = {(f16)-1032.0f, (f16)-1032.0f, (f16)-1152.0f, (f16)-1152.0f,
+                                        (f16)-1032.0f, (f16)-1032.0f, (f16)-1152.0f, (f16)-1152.0f};
+                    f32x4 db = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        db = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[t]), cneg, db, 0, 0,
+                                                                    0);
+                    cb = db;
+                }
 #pragma unroll
                 for (int b = 0; b < RB; ++b) {
                     f32x4 d = cb;
