@@ -280,6 +280,9 @@ def main() -> int:
                     help="eager launches only, for rocprofv3 --pmc: 50 calls of each MLP shape on rotated "
                          "copies, then 5 elementwise negations of a 256 MiB fp32 buffer into another "
                          "(256 MiB read + 256 MiB written each: the byte-count calibration); no JSON")
+    ap.add_argument("--layer-pass", type=int, nargs=5, metavar=("M", "K", "N", "COPIES", "CALLS"),
+                    help="eager launches only, for rocprofv3 --pmc: CALLS default-dispatch calls of one "
+                         "[M, K] x [N, K] layer on COPIES rotated weight copies; no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -298,6 +301,18 @@ def main() -> int:
         raise RuntimeError(f"W4A16 HIP extension not loaded: {nibble_amd.cuda.extension_load_error()}")
     device = torch.device("cuda:0")
     torch.manual_seed(0)
+
+    if args.layer_pass:
+        m, k, n, lcopies, calls = args.layer_pass
+        packed, scales = make_layer(k, n, lcopies, device, seed=0)
+        x = torch.randn((m, k), device=device).to(torch.float16)
+        out = torch.empty((m, n), device=device, dtype=torch.float16)
+        torch.cuda.synchronize()
+        for i in range(calls):
+            _lib.linear_f16(x, packed[i % lcopies], scales[i % lcopies], out)
+        torch.cuda.synchronize()
+        print("layer pass done", flush=True)
+        return 0
 
     copies = 64
     shapes = [(2048, 5632), (5632, 2048)]  # (K, N): up/gate and down
