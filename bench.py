@@ -207,8 +207,9 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),
-        "prefill": "16-token prompt: W4A16 op (one-shot MFMA kernel, M=16) for q|k|v, o, gate|up; dequantize + "
-                   "hipBLASLt for down (K=5632); torch ops between; prefill_ms replays it as one HIP graph",
+        "prefill": "16-token prompt: W4A16 op for every projection (one-shot MFMA kernel, M=16, for q|k|v, o, "
+                   "gate|up; the paired MFMA kernel over two 8-row halves for down, K=5632); torch ops between; "
+                   "prefill_ms replays it as one HIP graph",
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),
         "model": "random-init Llama 22L h2048 i5632 32q/4kv hd64 vocab32000, INT4 g128 on all 155 linears",

@@ -52,7 +52,8 @@ extern "C" {
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
  * takes the tuned kernels, and M = 9..16 the one-shot MFMA kernel when its
- * activations fit in LDS (M*K*2 bytes, K <= 4096 at M = 16); anything else
+ * activations fit in LDS (M*K*2 bytes, K <= 4096 at M = 16), else the
+ * paired MFMA kernel over two halves of the rows (K <= 32768); anything else
  * takes the generic kernel (the reference routes every M > 8 to its naive
  * kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
@@ -124,7 +125,9 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splitting K (4|8), unroll = groups per wavefront (0 = ceil(K / 128 /
  *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
  *     1..8 with 8), max_blocks ignored.
- *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 8, K <= 32768): splits = wavefronts
+ *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 16, K <= 32768; M > 8 runs as two
+ *     launches over rows [0, ceil(M/2)) and the rest, each choosing its
+ *     own staging chunk, rows ignored): splits = wavefronts
  *     splitting the K / 256 group pairs (2|4|8), max_blocks = 8-row-block
  *     wavefronts per workgroup (1|2|4|8, splits * max_blocks <= 16), unroll =
  *     group pairs per wavefront (0 = ceil(K / 256 / splits); else with
@@ -136,7 +139,7 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     staged activations, biases and reduction within 160 KiB of LDS.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
- * W4A16_KERNEL_MFMA_ONESHOT, 2..8 for W4A16_KERNEL_MFMA_PAIR) and 16-byte
+ * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte
  * aligned activations and weights. No reference counterpart (the reference's
  * W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
  */

@@ -259,10 +259,33 @@ Plan plan_mfma_pair(int64_t M, int64_t N, int64_t K) {
 }
 
 bool mfma_pair_fits(int64_t M, int64_t N, int64_t K) {
+    if (M > 8 && M <= 16) {   // two launches over rows [0, ceil(M/2)) and the rest
+        const int64_t m1 = (M + 1) / 2;
+        return mfma_pair_fits(m1, N, K) && mfma_pair_fits(M - m1, N, K);
+    }
     if (M < 2 || M > 8 || K < 128 || K % 128 != 0 || K > 32768) return false;
     const Plan p = plan_mfma_pair(M, N, K);
     return w4a16_internal::mfma_pair_instantiated(M, p.splits, p.max_blocks, p.rows, p.unroll) &&
            w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
+}
+
+// M = 9..16 on the paired kernel: two launches, rows [0, m1) and [m1, M) with
+// m1 = ceil(M/2) (each half 4..8 rows), each with its own launch shape unless
+// the caller fixed one; the weights are streamed twice.
+int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16* x, const uint8_t* w,
+                          const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t st) {
+    if (M <= 8)
+        return w4a16_internal::launch_mfma_pair(p.splits, p.max_blocks, p.rows, p.unroll, M, x, w, s, o, N, K, st);
+    const int m1 = (M + 1) / 2;
+    const int ms[2] = {m1, M - m1};
+    for (int h = 0; h < 2; ++h) {
+        const Plan q = own_plans ? plan_mfma_pair(ms[h], N, K) : p;
+        const int64_t row0 = h == 0 ? 0 : m1;
+        const int rc = w4a16_internal::launch_mfma_pair(q.splits, q.max_blocks, own_plans ? q.rows : 0, q.unroll,
+                                                        ms[h], x + row0 * K, w, s, o + row0 * N, N, K, st);
+        if (rc != W4A16_OK) return rc;
+    }
+    return W4A16_OK;
 }
 
 int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
@@ -275,10 +298,16 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     }
     const bool aligned = G == 128 && aligned16(act) && aligned16(packed);
     // M = 9..16 (a short prompt) is one MFMA tile: the one-shot MFMA kernel
-    // when the activations fit in LDS, else the generic kernel as before.
+    // when the activations fit in LDS, else the paired kernel over two halves
+    // of the rows (K up to 32768), else the generic kernel.
     if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_ONESHOT) &&
         mfma_oneshot_fits(M, K)) {
         *out = plan_mfma_oneshot(M, N, K);
+        return W4A16_OK;
+    }
+    if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_PAIR) &&
+        mfma_pair_fits(M, N, K)) {
+        *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
     const bool tuned = aligned && M <= 8;
@@ -601,7 +630,7 @@ int check_scalar_args(int64_t M, int64_t N, int64_t K, int64_t G) {
 }
 
 int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* scales, void* out,
-             int64_t M, int64_t N, int64_t K, int64_t G, void* stream) {
+             int64_t M, int64_t N, int64_t K, int64_t G, void* stream, bool own_plans = true) {
     using w4a16::f16;
     const f16* x = static_cast<const f16*>(act);
     const f16* s = static_cast<const f16*>(scales);
@@ -616,8 +645,7 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_ONESHOT: return launch_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA_ONESHOT: return launch_mfma_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA_PAIR:
-            return w4a16_internal::launch_mfma_pair(p.splits, p.max_blocks, p.rows, p.unroll, (int)M, x, packed, s,
-                                                    o, (int)N, (int)K, st);
+            return launch_mfma_pair_rows(p, own_plans, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -719,9 +747,9 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.unroll = unroll;
     p.max_blocks = max_blocks;
     if (kernel == W4A16_KERNEL_MFMA_PAIR) {
-        if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+        if (group_size != 128 || M < 2 || M > 16 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
-                        "the paired MFMA kernel needs group_size 128, 2 <= M <= 8 and 16-byte aligned activations "
+                        "the paired MFMA kernel needs group_size 128, 2 <= M <= 16 and 16-byte aligned activations "
                         "and weights");
     } else if (kernel == W4A16_KERNEL_VALU || kernel == W4A16_KERNEL_MFMA || kernel == W4A16_KERNEL_DIAG ||
         kernel == W4A16_KERNEL_VALU_OFFSET || kernel == W4A16_KERNEL_ONESHOT ||
@@ -737,7 +765,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, _DIAG "
                     "or _GENERIC");
     }
-    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
 }
 
 int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float eps,

@@ -26,10 +26,11 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill of a prompt of up to 16 tokens runs the W4A16 op itself (its
-one-shot MFMA kernel; q|k|v and gate|up as one op each) where the
-activations fit its LDS, and dequantize + hipBLASLt elsewhere (the 5632-wide
-down projection); ``capture_prefill(T)`` records a T-token prefill in a HIP
+Prefill of a prompt of up to 16 tokens runs the W4A16 op itself (q|k|v and
+gate|up as one op each; the op takes its one-shot MFMA kernel where the
+activations fit that kernel's LDS and the paired MFMA kernel over two halves
+of the rows elsewhere, as for the 5632-wide down projection), and dequantize
++ hipBLASLt for longer prompts; ``capture_prefill(T)`` records a T-token prefill in a HIP
 graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.
@@ -111,7 +112,7 @@ class Block(torch.nn.Module):
     def _native(self, x: torch.Tensor, packed: torch.Tensor) -> bool:
         """Whether the W4A16 op itself (not dequantize + hipBLASLt) is the fast
         path for these rows: GPU rows the op routes to a tuned kernel
-        (M <= 16 within the one-shot MFMA kernel's LDS)."""
+        (M <= 16, K up to 32768)."""
         if not (self.native_prefill and x.is_cuda and x.shape[0] <= 16):
             return False
         plan = _lib.plan_linear(x.data_ptr(), packed.data_ptr(), x.shape[0], packed.shape[0], x.shape[1],

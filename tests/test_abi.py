@@ -120,7 +120,9 @@ ALIGNED = 1 << 20
         (8, 5632, 128, ALIGNED, "mfma_pair"),
         (9, 2048, 128, ALIGNED, "mfma_oneshot"),   # a short prompt: one MFMA tile of rows
         (16, 4096, 128, ALIGNED, "mfma_oneshot"),
-        (16, 5632, 128, ALIGNED, "generic"),       # activations beyond LDS
+        (16, 5632, 128, ALIGNED, "mfma_pair"),     # beyond the one-shot kernel's LDS: two paired launches
+        (9, 28672, 128, ALIGNED, "mfma_pair"),
+        (16, 34816, 128, ALIGNED, "generic"),      # beyond the paired kernel's rows
         (17, 2048, 128, ALIGNED, "generic"),       # above one tile
         (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128
         (1, 2048, 128, ALIGNED + 2, "generic"),  # activations not 16-byte aligned

@@ -191,7 +191,9 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
 
 @pytest.mark.parametrize("m,k,n", [(3, 2048, 5632), (5, 4096, 4096), (7, 5632, 2048), (8, 8192, 1000),
                                    (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
-                                   (5, 8320, 77)])
+                                   (5, 8320, 77),
+                                   # M = 9..16 past the one-shot MFMA kernel's LDS: two launches
+                                   (16, 5632, 2048), (9, 28672, 100), (13, 8192, 77)])
 def test_default_dispatch_mfma_pair(gpu, m, k, n):
     x, p, s = make_case(m, k, n, seed=m + k + n)
     assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "mfma_pair"
@@ -207,9 +209,20 @@ def test_mfma_pair_more_pairs_than_needed(gpu, rows):
     assert_parity(out, expected(x, p, s), f"mfma_pair padded rows={rows}")
 
 
+@pytest.mark.parametrize("m", [9, 11, 16])
+def test_mfma_pair_two_halves_tuned(gpu, m):
+    # one launch shape for both halves (rows [0, ceil(m/2)) and the rest)
+    x, p, s = make_case(m, 2048, 300, seed=m)
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 2)
+    assert_parity(out, expected(x, p, s), f"mfma_pair two halves M={m}")
+
+
 def test_mfma_pair_rejects(gpu):
     x, p, s = make_case(1, 2048, 8, seed=2)
-    with pytest.raises(_lib.W4A16Error, match="2 <= M <= 8"):
+    with pytest.raises(_lib.W4A16Error, match="2 <= M <= 16"):
+        _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 1)
+    x, p, s = make_case(17, 2048, 8, seed=2)
+    with pytest.raises(_lib.W4A16Error, match="2 <= M <= 16"):
         _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 1)
     x, p, s = make_case(4, 2048, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="cover the K / 256"):
