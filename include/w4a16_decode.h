@@ -148,6 +148,41 @@ int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_
 int w4a16_embedding_f16(const void* table, int64_t vocab, int64_t hidden,
                         const int64_t* token, void* output, void* stream);
 
+/*
+ * Prefill of a T-token prompt: the element-wise work between its W4A16
+ * projections, one launch each (replaces the torch ops of HF LlamaModel's
+ * prefill forward around the reference's w4a16::linear / dequantize calls,
+ * scripts/generate.py:260-305 with w4a16/linear.py:154-200).
+ *
+ * RMSNorm of `rows` rows of `hidden` fp16: output[r] = fp16((fp32(x[r]) *
+ * inv) * fp32(weight)), inv = 1 / sqrt(mean(x[r]^2) + eps) in fp32 (the
+ * arithmetic of w4a16_gemv_fused_f16's prologue).
+ */
+int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output, int64_t rows, int64_t hidden,
+                      void* stream);
+
+/*
+ * output[r, i] = fp16(fp16(silu(g)) * u) for g = gate_up[r, i] and u =
+ * gate_up[r, inter + i] (rows of [gate | up], 2 * inter wide; the roundings
+ * of silu(g) * u on fp16 tensors).
+ */
+int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t inter, void* stream);
+
+/*
+ * Attention of `tokens` new tokens at cache slots start .. start + tokens - 1:
+ * qkv rows [q (num_heads x 64) | k (num_kv_heads x 64) | v] fp16 as for
+ * w4a16_decode_attention_f16; rotary embedding (cos / sin tables [max_seq_len,
+ * 32] fp32) on q and k rounded to fp16; k and v appended to the caches; query t
+ * attends to slots 0 .. start + t (slots below start read from the caches):
+ * output[t] = softmax(q k^T / 8) v, [tokens, num_heads * 64] fp16.
+ * Needs head_dim 64, tokens <= 64, start + tokens <= min(max_seq_len, 256),
+ * 16-byte aligned caches.
+ */
+int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
+                                const float* sin_table, int64_t start, int64_t tokens, void* output,
+                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

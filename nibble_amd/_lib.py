@@ -74,6 +74,10 @@ DECODE_SIGNATURES = {
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
+    "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
+    "w4a16_prefill_attention_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                                   _i64, _vp]),
 }
 
 _lib = None
@@ -262,3 +266,29 @@ def embedding_f16(table, token, output, stream=None) -> None:
     vocab, hidden = table.shape
     _raise_on(lib().w4a16_embedding_f16(table.data_ptr(), vocab, hidden, token.data_ptr(), output.data_ptr(),
                                         _stream_ptr(stream)))
+
+
+def rmsnorm_f16(x, weight, eps: float, output, stream=None) -> None:
+    """``w4a16_rmsnorm_f16`` over the rows of x [rows, hidden]."""
+    rows, hidden = x.shape
+    _raise_on(lib().w4a16_rmsnorm_f16(x.data_ptr(), weight.data_ptr(), float(eps), output.data_ptr(), rows, hidden,
+                                      _stream_ptr(stream)))
+
+
+def silu_mul_f16(gate_up, output, stream=None) -> None:
+    """``w4a16_silu_mul_f16``: output [rows, inter] <- silu(gate) * up of gate_up [rows, 2 * inter]."""
+    rows, width = gate_up.shape
+    _raise_on(lib().w4a16_silu_mul_f16(gate_up.data_ptr(), output.data_ptr(), rows, width // 2, _stream_ptr(stream)))
+
+
+def prefill_attention_f16(qkv, k_cache, v_cache, cos_table, sin_table, start: int, output, num_heads: int,
+                          num_kv_heads: int, head_dim: int = 64, stream=None) -> None:
+    """``w4a16_prefill_attention_f16`` for the qkv rows [tokens, ...] at slots
+    start .. start + tokens - 1 of one layer's caches [kv_heads, S, head_dim]."""
+    _raise_on(
+        lib().w4a16_prefill_attention_f16(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+            start, qkv.shape[0], output.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2],
+            _stream_ptr(stream),
+        )
+    )

@@ -579,6 +579,149 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Prefill: the element-wise work around the W4A16 projections of a T-token
+// prompt, each as one launch.
+// ---------------------------------------------------------------------------
+
+// out[r] = fp16((fp32(x[r]) * inv) * fp32(w)), inv = 1 / sqrt(mean(x[r]^2) +
+// eps) in fp32: the decode step's RMSNorm, one workgroup per row.
+__global__ void __launch_bounds__(256)
+rmsnorm_rows_kernel(const f16* __restrict__ x, const f16* __restrict__ w, float eps, f16* __restrict__ out,
+                    int hidden) {
+    __shared__ float partial[4];
+    const f16* xr = x + (size_t)blockIdx.x * hidden;
+    f16* orow = out + (size_t)blockIdx.x * hidden;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < hidden; i += 256) {
+        const float v = (float)xr[i];
+        ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)hidden + eps);
+    for (int i = threadIdx.x; i < hidden; i += 256) orow[i] = (f16)(((float)xr[i] * inv) * (float)w[i]);
+}
+
+// out[r, i] = fp16(fp16(silu(g)) * u), g = gate_up[r, i], u = gate_up[r, inter + i]:
+// the roundings of torch's silu(g) * u on fp16 tensors.
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const f16* __restrict__ gate_up, f16* __restrict__ out, int rows, int inter) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * inter) return;
+    const int64_t r = i / inter, c = i - r * inter;
+    const float g = (float)gate_up[r * 2 * inter + c];
+    const float u = (float)gate_up[r * 2 * inter + inter + c];
+    const f16 sg = (f16)(g / (1.0f + __expf(-g)));
+    out[i] = (f16)((float)sg * u);
+}
+
+// Prefill attention of T new tokens at cache slots start .. start + T - 1,
+// one workgroup of 4 wavefronts per query head. qkv rows (stride
+// (num_heads + 2 num_kv) * 64) hold [q | k | v] as the decode step's; q and
+// k get the rotary embedding of their slot in fp32, rounded to fp16; the
+// workgroup of the group's first query head appends k and v to the caches.
+// Attention: query t sees slots 0 .. start + t (slots below start from the
+// caches), softmax(q k^T / 8) v in fp32 with an online softmax over 64-slot
+// chunks, one query per wavefront at a time; output [T, num_heads * 64] fp16.
+// LDS: q [T][64] fp32, k and v [start + T][kRow] fp16 (rows padded to 72
+// halves, so a wavefront reading 64 rows spreads over the banks).
+constexpr int kPrefillRow = 72;
+constexpr int kPrefillMaxSlots = 256;   // start + tokens: 90 KiB of LDS at 64 tokens
+
+__global__ void __launch_bounds__(256)
+prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
+                         const float* __restrict__ cos_table, const float* __restrict__ sin_table, int start,
+                         int T, f16* __restrict__ out, int num_heads, int num_kv, int S) {
+    constexpr int D = 64;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int NK = start + T;
+    float* qs = reinterpret_cast<float*>(smem);                            // [T][64]
+    f16* ks = reinterpret_cast<f16*>(smem + (size_t)T * D * 4);          // [NK][kPrefillRow]
+    f16* vs = ks + (size_t)NK * kPrefillRow;                               // [NK][kPrefillRow]
+    __shared__ __align__(16) float probs[4][64];
+    const int hq = blockIdx.x;
+    const int group = num_heads / num_kv;
+    const int hk = hq / group;
+    const bool writer = hq % group == 0;
+    const int row_stride = (num_heads + 2 * num_kv) * D;
+
+    // earlier slots from the caches (16 bytes per thread and step)
+    for (int i = threadIdx.x; i < start * 8; i += 256) {
+        const int srow = i >> 3, c = i & 7;
+        const size_t g = ((size_t)hk * S + srow) * D;
+        reinterpret_cast<u32x4*>(ks + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(k_cache + g)[c];
+        reinterpret_cast<u32x4*>(vs + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(v_cache + g)[c];
+    }
+    // the new tokens: rotary q and k, v as is
+    for (int i = threadIdx.x; i < T * D; i += 256) {
+        const int t = i / D, d = i - t * D;
+        const int slot = start + t;
+        const f16* row = qkv + (size_t)t * row_stride;
+        const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
+        const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
+        const f16* q = row + (size_t)hq * D;
+        const f16* k = row + (size_t)num_heads * D + (size_t)hk * D;
+        const f16* v = row + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
+        const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
+        const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
+        const f16 qr = (f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
+        const f16 kr = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
+        const f16 vv = v[d];
+        qs[t * D + d] = (float)qr;
+        ks[slot * kPrefillRow + d] = kr;
+        vs[slot * kPrefillRow + d] = vv;
+        if (writer) {
+            k_cache[((size_t)hk * S + slot) * D + d] = kr;
+            v_cache[((size_t)hk * S + slot) * D + d] = vv;
+        }
+    }
+    __syncthreads();
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* my_probs = probs[wave];
+    for (int t = wave; t < T; t += 4) {
+        const int last = start + t;   // highest visible slot
+        const float* qrow = qs + t * D;
+        float run_max = -__builtin_inff(), run_sum = 0.0f, acc = 0.0f;
+        for (int c0 = 0; c0 <= last; c0 += 64) {
+            const int slot = c0 + lane;
+            float dot = 0.0f;
+            if (slot <= last) {
+                const u32x4* krow = reinterpret_cast<const u32x4*>(ks + slot * kPrefillRow);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const u32x4 kk = krow[e];
+#pragma unroll
+                    for (int w2 = 0; w2 < 4; ++w2) {
+                        const f16x2 h = as_f16x2(kk[w2]);
+                        dot = __builtin_fmaf(qrow[e * 8 + 2 * w2], (float)h.x, dot);
+                        dot = __builtin_fmaf(qrow[e * 8 + 2 * w2 + 1], (float)h.y, dot);
+                    }
+                }
+            }
+            const float score = slot <= last ? dot * 0.125f : -__builtin_inff();
+            const float new_max = fmaxf(run_max, wave_max(score));
+            const float pr = slot <= last ? __expf(score - new_max) : 0.0f;
+            const float psum = wave_sum(pr);
+            const float rescale = __expf(run_max - new_max);   // 0 on the first chunk
+            my_probs[lane] = pr;
+            wave_lds_sync();
+            float part = 0.0f;
+            const int n = min(64, last + 1 - c0);
+            for (int r = 0; r < n; ++r) part = __builtin_fmaf(my_probs[r], (float)vs[(c0 + r) * kPrefillRow + lane], part);
+            wave_lds_sync();
+            acc = acc * rescale + part;
+            run_sum = run_sum * rescale + psum;
+            run_max = new_max;
+        }
+        out[(size_t)t * num_heads * D + (size_t)hq * D + lane] = (f16)(acc / run_sum);
+    }
+}
+
 }  // namespace w4a16
 
 namespace w4a16_internal {
@@ -707,6 +850,66 @@ int w4a16_embedding_f16(const void* table, int64_t vocab, int64_t hidden, const 
     hipLaunchKernelGGL(w4a16::embedding_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const w4a16::f16*>(table), vocab, (int)hidden, token,
                        static_cast<w4a16::f16*>(output));
+    return check_launch();
+}
+
+int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output, int64_t rows, int64_t hidden,
+                      void* stream) {
+    if (rows == 0) return W4A16_OK;
+    if (!x || !weight || !output) return fail(W4A16_ERR_NULL, "rmsnorm: every pointer must be non-NULL");
+    if (rows < 0 || rows > INT32_MAX || hidden <= 0 || hidden > INT32_MAX)
+        return fail(W4A16_ERR_SHAPE, "rmsnorm: rows must be non-negative and hidden positive");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "rmsnorm: eps must be non-negative");
+    if (!aligned(x, 2) || !aligned(weight, 2) || !aligned(output, 2))
+        return fail(W4A16_ERR_ALIGNMENT, "rmsnorm: fp16 buffers must be 2-byte aligned");
+    hipLaunchKernelGGL(w4a16::rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(x),
+                       static_cast<const w4a16::f16*>(weight), eps, static_cast<w4a16::f16*>(output), (int)hidden);
+    return check_launch();
+}
+
+int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t inter, void* stream) {
+    if (rows == 0) return W4A16_OK;
+    if (!gate_up || !output) return fail(W4A16_ERR_NULL, "silu_mul: every pointer must be non-NULL");
+    if (rows < 0 || inter <= 0 || rows * inter > (int64_t)INT32_MAX * 128)
+        return fail(W4A16_ERR_SHAPE, "silu_mul: rows must be non-negative and inter positive");
+    if (!aligned(gate_up, 2) || !aligned(output, 2))
+        return fail(W4A16_ERR_ALIGNMENT, "silu_mul: fp16 buffers must be 2-byte aligned");
+    const int64_t blocks = (rows * inter + 255) / 256;
+    hipLaunchKernelGGL(w4a16::silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(gate_up),
+                       static_cast<w4a16::f16*>(output), (int)rows, (int)inter);
+    return check_launch();
+}
+
+int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
+                                const float* sin_table, int64_t start, int64_t tokens, void* output,
+                                int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len,
+                                void* stream) {
+    if (tokens == 0) return W4A16_OK;
+    if (!qkv || !k_cache || !v_cache || !cos_table || !sin_table || !output)
+        return fail(W4A16_ERR_NULL, "prefill attention: every pointer must be non-NULL");
+    if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "prefill attention: head_dim must be 64");
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
+        return fail(W4A16_ERR_SHAPE, "prefill attention: num_heads must be a positive multiple of num_kv_heads");
+    if (tokens < 0 || tokens > 64 || start < 0 || start + tokens > w4a16::kPrefillMaxSlots ||
+        start + tokens > max_seq_len)
+        return fail(W4A16_ERR_SHAPE,
+                    "prefill attention: needs 0 <= tokens <= 64 and start + tokens <= min(max_seq_len, 256)");
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(qkv, 2) || !aligned(output, 2))
+        return fail(W4A16_ERR_ALIGNMENT, "prefill attention: caches must be 16-byte aligned, qkv and output 2-byte");
+    const int nk = (int)(start + tokens);
+    const size_t lds = (size_t)tokens * 64 * 4 + (size_t)2 * nk * w4a16::kPrefillRow * 2;
+    const void* kern = reinterpret_cast<const void*>(w4a16::prefill_attention_kernel);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
+    }
+    hipLaunchKernelGGL(w4a16::prefill_attention_kernel, dim3((unsigned)num_heads), dim3(256), lds,
+                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                       static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
+                       (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads,
+                       (int)max_seq_len);
     return check_launch();
 }
 

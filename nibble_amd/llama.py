@@ -238,6 +238,7 @@ class LlamaDecoder(torch.nn.Module):
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
+        self.fuse_prefill = True   # prompts of <= 16 tokens: fused prefill (see fused_prefill)
         self.prefill_tokens: torch.Tensor | None = None
         self.prefill_positions: torch.Tensor | None = None
         # fused-step weights (views keep the per-module state-dict entries) and work buffers
@@ -268,14 +269,54 @@ class LlamaDecoder(torch.nn.Module):
             x = layer(x, cos, sin, positions, self.k_cache[i], self.v_cache[i], mask)
         return self.lm_head(self.norm(x[-1:]))[0]
 
+    def fused_prefill(self, tokens: int) -> bool:
+        """Whether a prompt of `tokens` tokens takes the fused prefill: the W4A16
+        op for every projection (M <= 16) and one launch for each RMSNorm,
+        attention and SiLU-multiply."""
+        return (self.fused and self.fuse_prefill and 1 <= tokens <= 16
+                and tokens <= min(self.cfg.max_seq_len, 256))
+
     def _prefill(self, prompt: torch.Tensor, positions: torch.Tensor) -> None:
         self.k_cache.zero_()
         self.v_cache.zero_()
+        if self.fused_prefill(prompt.numel()):
+            self._prefill_fused(prompt)
+            return
         logits = self._forward(prompt, positions)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.fill_(prompt.numel())
         if self.fused:
             _lib.embedding_f16(self.embed, self.token, self.x_buf)   # the first decode step's input
+
+    def _prefill_fused(self, prompt: torch.Tensor) -> None:
+        """The prompt (cache slots 0 .. T-1) with the decode step's roundings:
+        per layer RMSNorm, q|k|v op, rotary + KV append + causal attention, o
+        op + residual, RMSNorm, gate|up op, SiLU * up, down op + residual; then
+        RMSNorm + lm_head GEMV and the greedy argmax, which also gathers the
+        first decode step's input row."""
+        cfg = self.cfg
+        t = prompt.numel()
+        g = cfg.group_size
+        x = self.embed[prompt]
+        h = torch.empty_like(x)
+        attn = torch.empty((t, cfg.num_heads * cfg.head_dim), dtype=torch.float16, device=x.device)
+        mlp = torch.empty((t, cfg.intermediate_size), dtype=torch.float16, device=x.device)
+        for i, b in enumerate(self.layers):
+            qkv_w, qkv_s = self.qkv[i]
+            gu_w, gu_s = self.gate_up[i]
+            _lib.rmsnorm_f16(x, b.input_norm.weight, b.input_norm.eps, h)
+            qkv = torch.ops.w4a16.linear(h, qkv_w, qkv_s, g)
+            _lib.prefill_attention_f16(qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, attn,
+                                       cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
+            x = x + torch.ops.w4a16.linear(attn, b.o_proj.packed_weights, b.o_proj.scales, g)
+            _lib.rmsnorm_f16(x, b.post_norm.weight, b.post_norm.eps, h)
+            gu = torch.ops.w4a16.linear(h, gu_w, gu_s, g)
+            _lib.silu_mul_f16(gu, mlp)
+            x = x + torch.ops.w4a16.linear(mlp, b.down_proj.packed_weights, b.down_proj.scales, g)
+        _lib.gemv_fused_f16(x[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits,
+                            norm_weight=self.norm.weight, eps=self.norm.eps)
+        _lib.argmax_embed_f16(self.logits, self.token, None, self.embed, self.x_buf)
+        self.position.fill_(t)
 
     @torch.inference_mode()
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:

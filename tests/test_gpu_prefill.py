@@ -1,0 +1,171 @@
+"""GPU tests of the prefill launches (include/w4a16_decode.h: RMSNorm rows,
+SiLU * up, prefill attention) against float64 / torch restatements, and of
+the decoder's fused prefill against its torch-op prefill."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nibble_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+ULP = 2.0 ** -10   # one fp16 unit in the last place, relative
+
+
+def _tables(S: int, theta: float = 10000.0):
+    inv = 1.0 / (theta ** (torch.arange(0, 64, 2).float() / 64))
+    ang = torch.outer(torch.arange(S).float(), inv)
+    return ang.cos(), ang.sin()
+
+
+def _rope64(x: torch.Tensor, c: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    x1, x2 = x[..., :32].double(), x[..., 32:].double()
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1)
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 2048), (16, 2048), (7, 5632), (3, 100)])
+def test_rmsnorm_rows(gpu, rows, hidden):
+    gen = torch.Generator().manual_seed(rows * 7 + hidden)
+    x = (3.0 * torch.randn((rows, hidden), generator=gen)).to(torch.float16)
+    w = (1.0 + 0.5 * torch.randn((hidden,), generator=gen)).to(torch.float16)
+    eps = 1e-5
+    xd = x.double()
+    ref = (xd * torch.rsqrt(xd.pow(2).mean(dim=-1, keepdim=True) + eps)) * w.double()
+    out = torch.full((rows, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] rmsnorm rows={rows} hidden={hidden}", flush=True)
+    _lib.rmsnorm_f16(x.to(gpu), w.to(gpu), eps, out)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    # one fp16 rounding of a value within fp32 error of the exact one
+    assert torch.all((got - ref).abs() <= ULP * ref.abs() + 2 ** -24), float((got - ref).abs().max())
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 5632), (16, 5632), (5, 77)])
+def test_silu_mul(gpu, rows, inter):
+    gen = torch.Generator().manual_seed(rows + inter)
+    gu = (4.0 * torch.randn((rows, 2 * inter), generator=gen)).to(torch.float16)
+    g, u = gu[:, :inter].double(), gu[:, inter:].double()
+    silu16 = (g / (1 + torch.exp(-g))).to(torch.float16).double()
+    ref = silu16 * u
+    out = torch.full((rows, inter), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] silu_mul rows={rows} inter={inter}", flush=True)
+    _lib.silu_mul_f16(gu.to(gpu), out)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    # silu(g) within one fp16 ulp of the exact rounding, then one more rounding
+    assert torch.all((got - ref).abs() <= 3 * ULP * ref.abs() + 2 ** -20), float((got - ref).abs().max())
+    # and against torch's own fp16 ops on the same tensors
+    torch_ref = (F.silu(gu[:, :inter].to(gpu)) * gu[:, inter:].to(gpu)).double().cpu()
+    assert torch.all((got - torch_ref).abs() <= 2 * ULP * torch_ref.abs() + 2 ** -20)
+
+
+def _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv):
+    """float64 restatement: rotary q / k rounded to fp16, causal softmax attention."""
+    t = qkv.shape[0]
+    slots = torch.arange(start, start + t)
+    c, s = cos[slots].double().unsqueeze(1), sin[slots].double().unsqueeze(1)
+    q = _rope64(qkv[:, : heads * 64].view(t, heads, 64), c, s).to(torch.float16)
+    k_new = _rope64(qkv[:, heads * 64: (heads + kv) * 64].view(t, kv, 64), c, s).to(torch.float16)
+    v_new = qkv[:, (heads + kv) * 64:].view(t, kv, 64)
+    kc, vc = k_cache.clone(), v_cache.clone()
+    kc[:, start: start + t] = k_new.transpose(0, 1)
+    vc[:, start: start + t] = v_new.transpose(0, 1)
+    group = heads // kv
+    nk = start + t
+    kf = kc.double().repeat_interleave(group, 0)[:, :nk]            # [heads, nk, 64]
+    vf = vc.double().repeat_interleave(group, 0)[:, :nk]
+    qd = q.double().transpose(0, 1)                                  # [heads, t, 64]
+    scores = torch.matmul(qd, kf.transpose(1, 2)) / math.sqrt(64)   # [heads, t, nk]
+    mask = torch.arange(nk).unsqueeze(0) > (start + torch.arange(t)).unsqueeze(1)
+    scores = scores.masked_fill(mask, float("-inf"))
+    out = torch.matmul(torch.softmax(scores, dim=-1), vf)           # [heads, t, 64]
+    return out.transpose(0, 1).reshape(t, heads * 64), kc, vc, k_new, v_new
+
+
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
+@pytest.mark.parametrize("tokens,start", [(1, 0), (5, 0), (16, 0), (64, 0), (16, 7), (64, 192)])
+def test_prefill_attention(gpu, heads, kv, tokens, start):
+    S = 256
+    gen = torch.Generator().manual_seed(tokens * 13 + start + heads)
+    qkv = torch.randn((tokens, (heads + 2 * kv) * 64), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    cos, sin = _tables(S)
+    ref, kc_ref, vc_ref, k_new, v_new = _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv)
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = torch.full((tokens, heads * 64), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] prefill attention heads={heads} kv={kv} tokens={tokens} start={start}", flush=True)
+    _lib.prefill_attention_f16(qkv.to(gpu), kd, vd, cos.to(gpu), sin.to(gpu), start, out, heads, kv)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs()), float(err.max())
+    # caches: slots start .. start + tokens - 1 replaced (v exact, rotary k within an fp16 ulp), others untouched
+    kg, vg = kd.cpu(), vd.cpu()
+    new = slice(start, start + tokens)
+    others = [s for s in range(S) if not start <= s < start + tokens]
+    assert torch.equal(kg[:, others], k_cache[:, others]) and torch.equal(vg[:, others], v_cache[:, others])
+    assert torch.equal(vg[:, new], v_new.transpose(0, 1))
+    assert torch.allclose(kg[:, new].float(), k_new.transpose(0, 1).float(), rtol=ULP, atol=2 ** -14)
+
+
+def test_prefill_attention_rejects(gpu):
+    heads, kv, S = 8, 2, 64
+    kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+    vd = torch.zeros_like(kd)
+    cos, sin = _tables(S)
+    cos, sin = cos.to(gpu), sin.to(gpu)
+    for tokens, start in [(65, 0), (10, 60)]:
+        qkv = torch.zeros((tokens, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
+        out = torch.zeros((tokens, heads * 64), dtype=torch.float16, device=gpu)
+        with pytest.raises(_lib.W4A16Error, match="tokens"):
+            _lib.prefill_attention_f16(qkv, kd, vd, cos, sin, start, out, heads, kv)
+    qkv = torch.zeros((4, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
+    out = torch.zeros((4, heads * 64), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="head_dim"):
+        _lib.prefill_attention_f16(qkv, kd, vd, cos, sin, 0, out, heads, kv, head_dim=128)
+    with pytest.raises(_lib.W4A16Error, match="multiple"):
+        _lib.prefill_attention_f16(qkv, kd, vd, cos, sin, 0, out, 7, 2)
+    assert not kd.any() and not vd.any()
+
+
+def _small_cfg():
+    from nibble_amd.llama import LlamaConfig
+
+    return LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1280, num_layers=2, num_heads=8,
+                       num_kv_heads=2, head_dim=64, max_seq_len=32)
+
+
+@pytest.mark.parametrize("tokens", [1, 9, 16])
+def test_fused_prefill_matches_torch_prefill(gpu, tokens):
+    """The fused prefill against the torch-op prefill of the same model and
+    prompt: logits of the last token within 2e-2 (1 + |ref|), KV caches within
+    fp16 roundings; the graphed fused prefill reproduces the eager one exactly."""
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(_small_cfg(), device=gpu, seed=11)
+    prompt = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(tokens)).to(gpu)
+    assert model.fused_prefill(tokens)
+    with torch.inference_mode():
+        model.k_cache.zero_(); model.v_cache.zero_()
+        ref = model._forward(prompt, torch.arange(tokens, device=gpu)).float()
+        k_ref, v_ref = model.k_cache.clone().float(), model.v_cache.clone().float()
+    tok = model.prefill(prompt)
+    got = model.logits.float()
+    assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
+    assert torch.allclose(model.k_cache.float(), k_ref, rtol=1e-2, atol=1e-2)
+    assert torch.allclose(model.v_cache.float(), v_ref, rtol=1e-2, atol=1e-2)
+    assert int(model.position) == tokens
+    assert torch.equal(model.x_buf, model.embed[tok[0]])
+    logits_eager, k_eager = model.logits.clone(), model.k_cache.clone()
+    model.capture_prefill(tokens)
+    other = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(99)).to(gpu)
+    model.prefill(other)
+    assert torch.equal(model.prefill(prompt), tok)
+    assert torch.equal(model.logits, logits_eager) and torch.equal(model.k_cache, k_eager)
