@@ -43,6 +43,7 @@ extern "C" {
 #define W4A16_KERNEL_ONESHOT 6       /* VALU GEMV, every weight of a wavefront's rows requested at once (M <= 4) */
 #define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 16, K <= 8192) */
 #define W4A16_KERNEL_MFMA_PAIR 8     /* fp16 MFMA on 8 rows x 2 groups, loads up front (2 <= M <= 8, staged M*K in LDS) */
+#define W4A16_KERNEL_STREAM 9        /* VALU GEMV, resident workgroups streaming rows along K (M = 1, K <= 32768) */
 
 /*
  * Fused W4A16 linear layer.
@@ -57,7 +58,8 @@ extern "C" {
  * takes the generic kernel (the reference routes every M > 8 to its naive
  * kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
- * valu_offset|mfma|mfma_oneshot|mfma_pair selects the kernel family for M <= 8;
+ * valu_offset|mfma|mfma_oneshot|mfma_pair|stream selects the kernel family
+ * for M <= 8;
  * W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront of the VALU
  * kernels (any other value is W4A16_ERR_CONFIG).
  */
@@ -137,6 +139,11 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     1|2|4 and unroll 7|8, or splits 8 with max_blocks 1|2 and unroll
  *     3..8|10|12|14|16);
  *     staged activations, biases and reduction within 160 KiB of LDS.
+ *   W4A16_KERNEL_STREAM (M = 1, K <= 32768): rows = output rows per
+ *     wavefront task (2|4 with unroll 2|3|4, 8 with unroll 2), splits =
+ *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
+ *     (at most ceil(K / 2048)),
+ *     max_blocks = grid (0 = the workgroups resident on the device at once).
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

@@ -25,6 +25,11 @@ bool mfma_pair_instantiated(int64_t M, int sk, int sn, int chunk, int gpw);
 int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int gpw);
 int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream);
+// w4a16_stream.hip: the streaming M = 1 kernel for long rows
+int64_t stream_lds_bytes(int64_t K);
+bool stream_instantiated(int rows, int waves, int depth, int64_t K);
+int launch_stream(int rows, int waves, int depth, int max_blocks, const void* x, const uint8_t* w, const void* s,
+                  void* o, int N, int K, hipStream_t stream);
 }  // namespace w4a16_internal
 
 namespace {
@@ -91,9 +96,10 @@ int read_env(int* family, int* rows_per_wave) {
         else if (std::strcmp(d, "oneshot") == 0) *family = W4A16_KERNEL_ONESHOT;
         else if (std::strcmp(d, "mfma_oneshot") == 0) *family = W4A16_KERNEL_MFMA_ONESHOT;
         else if (std::strcmp(d, "mfma_pair") == 0) *family = W4A16_KERNEL_MFMA_PAIR;
+        else if (std::strcmp(d, "stream") == 0) *family = W4A16_KERNEL_STREAM;
         else
-            return fail(W4A16_ERR_CONFIG,
-                        "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, mfma_oneshot, or mfma_pair");
+            return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, mfma_oneshot, "
+                                          "mfma_pair, or stream");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -258,6 +264,43 @@ Plan plan_mfma_pair(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
+// Streaming M = 1 kernel (w4a16_stream.h). Plan fields: rows = output rows
+// per task, splits = wavefronts per workgroup, unroll = 1 KiB steps per row
+// in flight, max_blocks = grid (0 = the workgroups resident at once). Launch
+// shape from the sweep over K 11008..28672, N 2048..28672: 4 rows, 4
+// wavefronts and 2 steps in flight on rows past 16384 (28672 x 8192: 20.4
+// us, 2 workgroups per CU), else 2 rows, 8 wavefronts and 3 steps (14336 x
+// 4096: 7.25 us, 16384 x 8192: 13.9 us).
+Plan plan_stream(int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_STREAM;
+    const bool longest = K > 16384;
+    p.rows = longest ? 4 : 2;
+    p.splits = longest ? 4 : 8;
+    p.unroll = longest ? 2 : 3;
+    const int64_t steps = (K / 32 + 63) / 64;   // 1 KiB loads per row
+    if (p.unroll > steps) p.unroll = (int)steps;
+    p.max_blocks = 0;
+    (void)N;
+    return p;
+}
+
+bool stream_fits(int64_t K) {
+    const Plan p = plan_stream(0, K);
+    return K % 128 == 0 && p.unroll >= 2 &&
+           w4a16_internal::stream_instantiated(p.rows, p.splits, p.unroll, K) &&
+           w4a16_internal::stream_lds_bytes(K) <= kMaxLdsBytes;
+}
+
+// M = 1 layers with rows from kStreamMinK weights and at least
+// kStreamMinN rows run the streaming kernel (measured against the one-shot
+// kernel: 28672 x 8192 20.4 against 30.8 us, 14336 x 4096 7.25 against 7.76;
+// the one-shot kernel keeps 11008 x 4096, 16384 x 2048 and 8192 x 28672,
+// where its single round of loads covers the layer or the streaming grid
+// would leave CUs idle).
+constexpr int64_t kStreamMinK = 14336;
+constexpr int64_t kStreamMinN = 4096;
+
 bool mfma_pair_fits(int64_t M, int64_t N, int64_t K) {
     if (M > 8 && M <= 16) {   // two launches over rows [0, ceil(M/2)) and the rest
         const int64_t m1 = (M + 1) / 2;
@@ -326,7 +369,8 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // An explicit W4A16_ROWS_PER_WARP (an A/B switch, as in the reference)
     // keeps auto on the looped VALU kernel whose rows it sets.
     // Measured routing (M = 1..8 sweeps over the benchmark shapes):
-    //   M = 1: one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
+    //   M = 1: streaming VALU for long rows of wide layers (K >= 14336,
+    //   N >= 4096), else one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
     //   M >= 3: the paired-group MFMA kernel up to K = 32768 (activations
     //   staged whole or in chunks); beyond that as before:
     //   one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
@@ -337,7 +381,9 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     //   M <= 4 (K <= 4096), else the looped MFMA kernel.
     if (family == 0) {
         const bool small = K <= 5632 && N <= 5632;
-        if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
+        if (rows == 0 && M == 1 && K >= kStreamMinK && N >= kStreamMinN && stream_fits(K))
+            family = W4A16_KERNEL_STREAM;
+        else if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
             family = W4A16_KERNEL_ONESHOT;
         else if (rows == 0 && M >= 3 && mfma_pair_fits(M, N, K))
             family = W4A16_KERNEL_MFMA_PAIR;
@@ -350,6 +396,13 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         else
             family = (M == 1 || (M == 2 && K <= 16384) || (M <= 4 && K <= 4096)) ? W4A16_KERNEL_VALU
                                                                                    : W4A16_KERNEL_MFMA;
+    }
+    if (family == W4A16_KERNEL_STREAM) {
+        if (M == 1 && stream_fits(K)) {
+            *out = plan_stream(N, K);
+            return W4A16_OK;
+        }
+        family = oneshot_fits(M, K) ? W4A16_KERNEL_ONESHOT : W4A16_KERNEL_VALU;   // M > 1 or rows too short
     }
     if (family == W4A16_KERNEL_MFMA_PAIR) {
         if (mfma_pair_fits(M, N, K)) {
@@ -646,6 +699,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_MFMA_ONESHOT: return launch_mfma_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA_PAIR:
             return launch_mfma_pair_rows(p, own_plans, (int)M, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_STREAM:
+            return w4a16_internal::launch_stream(p.rows, p.splits, p.unroll, p.max_blocks, x, packed, s, o, (int)N,
+                                                 (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -746,7 +802,12 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_MFMA_PAIR) {
+    if (kernel == W4A16_KERNEL_STREAM) {
+        if (group_size != 128 || M != 1 || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "the streaming kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
+                        "weights");
+    } else if (kernel == W4A16_KERNEL_MFMA_PAIR) {
         if (group_size != 128 || M < 2 || M > 16 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "the paired MFMA kernel needs group_size 128, 2 <= M <= 16 and 16-byte aligned activations "
@@ -762,8 +823,8 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
         if (splits < 1 || splits > 8) return fail(W4A16_ERR_CONFIG, "splits must be in 1..8");
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
-                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, _DIAG "
-                    "or _GENERIC");
+                    "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
+                    "_STREAM, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
 }

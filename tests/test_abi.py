@@ -98,7 +98,8 @@ ALIGNED = 1 << 20
     "m,k,g,act,kernel",
     [
         (1, 2048, 128, ALIGNED, "oneshot"),    # decode
-        (1, 32768, 128, ALIGNED, "oneshot"),   # 16 loads of 1 KiB per row
+        (1, 11008, 128, ALIGNED, "oneshot"),
+        (1, 32768, 128, ALIGNED, "oneshot"),   # 16 loads of 1 KiB per row (N = 64: too few rows to stream)
         (1, 34816, 128, ALIGNED, "valu"),      # rows too long for the one-shot kernel
         (2, 2048, 128, ALIGNED, "oneshot"),    # M = 2 up to K = 5632
         (2, 5632, 128, ALIGNED, "oneshot"),
@@ -133,6 +134,34 @@ def test_plan_routing(monkeypatch, m, k, g, act, kernel):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     assert _lib.plan_linear(act, ALIGNED, m, 64, k, g)["kernel"] == kernel
+
+
+@pytest.mark.parametrize("n,k,kernel,rows,splits,unroll", [
+    (8192, 28672, "stream", 4, 4, 2), (4096, 14336, "stream", 2, 8, 3), (8192, 16384, "stream", 2, 8, 3),
+    (4096, 32768, "stream", 4, 4, 2), (4096, 16512, "stream", 4, 4, 2),
+    (4096, 11008, "oneshot", 1, 8, 6), (2048, 16384, "oneshot", 1, 8, 8), (28672, 8192, "oneshot", 1, 8, 4),
+    (4096, 34816, "valu", 2, 4, 8),
+])
+def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
+    """M = 1: long rows of wide layers stream; shorter rows, narrow layers
+    and rows past 32768 keep their kernels."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
+    assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == (kernel, rows, splits, unroll)
+    if kernel == "stream":
+        assert plan["max_blocks"] == 0
+        monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # an explicit VALU row count keeps auto off it
+        assert _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)["kernel"] != "stream"
+
+
+def test_stream_env_selector(monkeypatch):
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    monkeypatch.setenv("W4A16_DECODE", "stream")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 4096, 128)["kernel"] == "stream"     # any N
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "oneshot"    # one step per row
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 64, 4096, 128)["kernel"] == "oneshot"    # M > 1
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 34816, 128)["kernel"] == "valu"      # rows too long
 
 
 def test_plan_misaligned_weights_take_generic():

@@ -19,6 +19,7 @@ VOFF = _lib.KERNEL_VALU_OFFSET
 ONESHOT = _lib.KERNEL_ONESHOT
 MFMA_OS = _lib.KERNEL_MFMA_ONESHOT
 MFMA_PAIR = _lib.KERNEL_MFMA_PAIR
+STREAM = _lib.KERNEL_STREAM
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -238,6 +239,54 @@ def test_mfma_pair_rejects(gpu):
         _run_tuned(gpu, x, p, s, MFMA_PAIR, 40, 8, 5, 1)  # whole rows of 40 pairs
 
 
+STREAM_SHAPES = [(2, 4, 2), (2, 8, 4), (4, 4, 3), (4, 8, 2), (4, 4, 4), (8, 4, 2), (8, 8, 2), (2, 4, 3)]
+
+
+@pytest.mark.parametrize("rows,waves,depth", STREAM_SHAPES)
+@pytest.mark.parametrize("k,n", [(8192, 7), (16384, 40), (16512, 9), (18432, 33), (28672, 21), (32768, 5)])
+def test_stream_variants(gpu, rows, waves, depth, k, n):
+    """Streaming kernel (M = 1): every instantiated shape on short and ragged
+    rows (16512 = 8 full steps + 4 chunks), both activation-unit counts
+    (K <= 16384 and above) and N not a multiple of the rows per task."""
+    x, p, s = make_case(1, k, n, seed=k + n + rows)
+    got = _run_tuned(gpu, x, p, s, STREAM, rows, waves, depth)
+    assert_parity(got, expected(x, p, s), f"stream {rows}/{waves}/{depth} K={k} N={n}")
+
+
+@pytest.mark.parametrize("rows,waves,depth,cap", [(4, 4, 3, 1), (2, 8, 4, 3), (8, 4, 2, 2), (4, 8, 2, 5)])
+@pytest.mark.parametrize("k,n", [(8192, 203), (16512, 77)])
+def test_stream_many_tasks_per_wavefront(gpu, rows, waves, depth, cap, k, n):
+    """A small grid cap gives each wavefront many tasks, so the ring of
+    in-flight steps crosses from one task's rows to the next (and the
+    peeled tail starts inside a task)."""
+    x, p, s = make_case(1, k, n, seed=k * 3 + n + cap)
+    got = _run_tuned(gpu, x, p, s, STREAM, rows, waves, depth, max_blocks=cap)
+    assert_parity(got, expected(x, p, s), f"stream cap {cap} {rows}/{waves}/{depth} K={k} N={n}")
+
+
+@pytest.mark.parametrize("k,n", [(16384, 64), (28672, 100), (32768, 33)])
+def test_default_dispatch_long_rows_m1(gpu, k, n):
+    x, p, s = make_case(1, k, n, seed=k + 2 * n)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n}")
+
+
+def test_stream_rejects(gpu):
+    x, p, s = make_case(2, 4096, 16, seed=5)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    out = torch.zeros((2, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="M == 1"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, STREAM, 4, 4, 2, 0)
+    out1 = torch.zeros((1, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="exceeds"):   # 4096 = 2 steps of 1 KiB per row
+        _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 4, 4, 3, 0)
+    with pytest.raises(_lib.W4A16Error, match="rows 8 with unroll 2"):
+        _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 8, 4, 3, 0)
+    with pytest.raises(_lib.W4A16Error, match="splits"):
+        _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 4, 2, 2, 0)
+    torch.cuda.synchronize()
+    assert not out.any() and not out1.any()
+
+
 @pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7)])
 def test_default_dispatch_short_prompt(gpu, m, k, n):
     x, p, s = make_case(m, k, n, seed=m + k)
@@ -299,17 +348,20 @@ def test_tuned_variants_batch(gpu, kernel, rows, splits, unroll, cap, m):
     assert_parity(out, expected(x, p, s), f"kernel={kernel} M={m}")
 
 
-@pytest.mark.parametrize("kernel", [VALU, VOFF, ONESHOT, MFMA, MFMA_OS, GENERIC, DIAG])
+@pytest.mark.parametrize("kernel", [VALU, VOFF, ONESHOT, MFMA, MFMA_OS, GENERIC, DIAG, STREAM])
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_all_nibble_values(gpu, kernel, m):
-    if kernel in (DIAG, VOFF) and m != 1:
-        pytest.skip("the diagonal MFMA and offset-decode VALU kernels are M = 1 only")
+    if kernel in (DIAG, VOFF, STREAM) and m != 1:
+        pytest.skip("the diagonal MFMA, offset-decode VALU and streaming kernels are M = 1 only")
     if kernel == ONESHOT and m > 4:
         pytest.skip("the one-shot kernel is built for M <= 4")
     # random bytes: all 16 codes (incl. -8) in both nibbles of every byte position
     x, p, s = make_case(m, 1024, 64, seed=11, all_nibbles=True)
     if kernel in (ONESHOT, MFMA_OS):
         out = _run_tuned(gpu, x, p, s, kernel, 2, 4, 0)
+    elif kernel == STREAM:
+        x, p, s = make_case(m, 4096, 64, seed=11, all_nibbles=True)   # two steps of 1 KiB per row
+        out = _run_tuned(gpu, x, p, s, kernel, 4, 4, 2)
     else:
         out = _run_tuned(gpu, x, p, s, kernel, 2, 2, 2)
     assert_parity(out, expected(x, p, s), f"all nibbles kernel={kernel} M={m}")
@@ -335,10 +387,10 @@ def _stress_activations(kind: str, m: int, k: int) -> torch.Tensor:
                                                        (ONESHOT, 2, 4, 0), (ONESHOT, 1, 8, 0),
                                                        (MFMA_OS, 1, 4, 0), (MFMA_OS, 2, 8, 0),
                                                        (DIAG, 2, 4, 1), (DIAG, 1, 4, 2),
-                                                       (MFMA, 2, 4, 1), (GENERIC, 1, 1, 1)])
+                                                       (MFMA, 2, 4, 1), (GENERIC, 1, 1, 1), (STREAM, 4, 4, 2)])
 @pytest.mark.parametrize("kind", ["constant", "outliers", "cancel"])
 def test_precision_stress(gpu, kernel, rows, splits, unroll, kind):
-    m = 1 if kernel in (DIAG, VOFF) else 4
+    m = 1 if kernel in (DIAG, VOFF, STREAM) else 4
     _, p, s = make_case(m, 4096, 96, seed=21)
     x = _stress_activations(kind, m, 4096)
     out = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll)
