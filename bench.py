@@ -221,6 +221,49 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
+def prefill_long(device, prompt_len: int = 64, runs: int = 5) -> dict:
+    """A 64-token prompt on the random-init 1.1B Llama, each path recorded in
+    a HIP graph: the fused prefill (every projection on the W4A16 op, which
+    runs its GEMM at M = 64) against the reference's prefill path (every
+    projection as dequantize + hipBLASLt inside QuantizedLinear, torch ops
+    around them)."""
+    import torch
+
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    model = LlamaDecoder(LlamaConfig(max_seq_len=prompt_len), device=device, seed=0)
+    gen = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, model.cfg.vocab_size, (prompt_len,), generator=gen).to(device)
+
+    def timed() -> float:
+        model.capture_prefill(prompt_len)
+        ts = []
+        for _ in range(runs + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            model.prefill(prompt)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        ts = sorted(ts[1:])
+        return ts[len(ts) // 2]
+
+    model.fused = True
+    fused = timed()
+    model.fused = False
+    for b in model.layers:
+        b.native_prefill = False
+    dequant = timed()
+    del model
+    torch.cuda.empty_cache()
+    return {
+        "prefill64_ms": round(fused * 1e3, 3),
+        "prefill64_dequant_ms": round(dequant * 1e3, 3),
+        "prefill64": f"{prompt_len}-token prompt, one HIP graph each: the fused prefill (W4A16 GEMM for q|k|v, o, "
+                     "gate|up, down at M=64) against dequantize + hipBLASLt for every projection with torch ops "
+                     "around them (the reference's prefill path)",
+    }
+
+
 def _copies(nbytes: int, floor_bytes: int = 512 << 20) -> int:
     """Rotated copies so the working set is >= 2x the 256 MiB Infinity Cache."""
     return max(2, -(-floor_bytes // nbytes))
@@ -410,6 +453,7 @@ def main() -> int:
         del layers
         torch.cuda.empty_cache()
         line["decode"] = decode_tok_s(device)
+        line["decode"].update(prefill_long(device))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(shapes)
     print(json.dumps(line), flush=True)

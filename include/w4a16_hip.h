@@ -44,6 +44,7 @@ extern "C" {
 #define W4A16_KERNEL_MFMA_ONESHOT 7  /* fp16 MFMA, loads up front, activations staged in LDS (M <= 16, K <= 8192) */
 #define W4A16_KERNEL_MFMA_PAIR 8     /* fp16 MFMA on 8 rows x 2 groups, loads up front (2 <= M <= 8, staged M*K in LDS) */
 #define W4A16_KERNEL_STREAM 9        /* VALU GEMV, resident workgroups streaming rows along K (M = 1, K <= 32768) */
+#define W4A16_KERNEL_GEMM 10         /* fp16 MFMA GEMM on weights decoded in registers (M > 16, prompts) */
 
 /*
  * Fused W4A16 linear layer.
@@ -52,11 +53,11 @@ extern "C" {
  * activations: fp16 [M, K] row-major; packed_weights: uint8 [N, K/2];
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
- * takes the tuned kernels, and M = 9..16 the one-shot MFMA kernel when its
+ * takes the tuned kernels, M = 9..16 the one-shot MFMA kernel when its
  * activations fit in LDS (M*K*2 bytes, K <= 4096 at M = 16), else the
- * paired MFMA kernel over two halves of the rows (K <= 32768); anything else
- * takes the generic kernel (the reference routes every M > 8 to its naive
- * kernel).
+ * paired MFMA kernel over two halves of the rows (K <= 32768), and M > 16
+ * the W4A16 GEMM (operands below 4 GiB); anything else takes the generic
+ * kernel (the reference routes every M > 8 to its naive kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
  * valu_offset|mfma|mfma_oneshot|mfma_pair|stream selects the kernel family
  * for M <= 8;
@@ -144,6 +145,10 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
  *     (at most ceil(K / 2048)),
  *     max_blocks = grid (0 = the workgroups resident on the device at once).
+ *   W4A16_KERNEL_GEMM (any M; every operand below 4 GiB): rows = 16-row
+ *     activation tiles per wavefront (1|2|4), max_blocks = 16-row weight
+ *     tiles per wavefront (1|2|4), splits = wavefronts splitting K (2|4|8;
+ *     not 8 with rows = max_blocks = 4), unroll ignored.
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

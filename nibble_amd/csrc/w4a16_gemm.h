@@ -1,0 +1,198 @@
+// W4A16 GEMM for prompts (M > 16 activation rows) on gfx950, group size 128.
+//
+// out[m][n] = fp16( sum_k x[m][k] * W[n][k] ), W[n][k] = fp16_rn(code * scale)
+// decoded in registers: the B operand of every MFMA is bit-identical to what
+// w4a16_dequantize_f16 writes, so the result is the reference's prefill path
+// (dequantize, then an fp16 GEMM with fp32 accumulation) without the fp16
+// weight round trip through HBM (0.5 byte per weight read instead of 0.5
+// read + 2 written + 2 read).
+//
+// v_mfma_f32_16x16x32_f16 tiles: D[m][n] over 16 activation rows x 16 weight
+// rows. Within a 128-weight group, step t (0..3) of lane l = 16 q + c takes
+// k = 32 q + 8 t .. + 7 (the MFMA needs the same k set for its A and B
+// lanes, not a particular order): lane (q, c) then reads its whole share of
+// the group's weights for row c as ONE 16-byte load (bytes 16 q .. 16 q + 15
+// of the row's 64-byte group), word t of which is step t; its A fragment of
+// step t is the 16 contiguous bytes x[m][128 g + 32 q + 8 t ..], loaded
+// straight from memory in natural order (no staging, no permutation).
+//
+// Decode of one word (8 weights, nibble i = weight i): per byte, v_perm puts
+// the byte in both halves, v_bitop3 keeps the low nibble in the low half and
+// the high nibble 4 bits up in the high half, flips bit 3 (two's complement
+// to offset binary) and ORs in the binary16 1024.0 pattern; one packed fma
+// (x {1, 1/16}, - {1032, 72}) gives the exact codes and one packed multiply
+// by the group scale rounds code * scale once (RNE), as the dequantize kernel
+// does. 16 VALU per 8 weights, shared by the MT activation tiles.
+//
+// Workgroup = SK wavefronts splitting the K / 128 groups (wavefront kw takes
+// groups kw, kw + SK, ...); each wavefront computes MT x RB tiles (16 MT
+// activation rows, 16 RB weight rows), so each A fragment feeds RB MFMAs and
+// each decoded B fragment feeds MT. Loads of the next group are issued before
+// the current group's MFMAs (two register buffers). The SK partial tiles are
+// summed through LDS in a fixed order (deterministic) and stored as fp16.
+//
+// Grid: nbp * mblocks workgroups, nbp = the weight-row blocks rounded up to a
+// multiple of 8. Workgroup b runs on XCD b % 8 (round-robin dispatch); it
+// takes weight block 8 (s / mblocks) + b % 8 and activation block s % mblocks
+// (s = b / 8), so every activation block of one weight block runs on the same
+// XCD, one after another, and re-reads those weights from that XCD's L2.
+// Workgroups past the last weight block return at once.
+#pragma once
+
+#include "w4a16_device.h"
+
+namespace w4a16 {
+
+// LDS of gemm_w4a16: the partial tiles of wavefronts 1 .. SK - 1.
+__host__ __device__ constexpr int64_t gemm_lds_bytes(int mt, int rb, int sk) {
+    return (int64_t)(sk - 1) * mt * rb * 64 * 16;
+}
+
+template <int MT, int RB>
+struct GemmGroup {
+    u32x4 a[MT][4];   // A fragments of the 4 steps, per activation tile
+    u32x4 w[RB];      // 32 packed weights per lane, per weight tile
+    uint32_t s[RB];   // fp16 bits of the group scale
+};
+
+template <int MT, int RB, int SK>
+__global__ void __launch_bounds__(64 * SK)
+gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+           f16* __restrict__ out, int M, int N, int K, int nblocks) {
+    const int b = blockIdx.x;
+    const int mblocks = (int)gridDim.x / ((nblocks + 7) & ~7);
+    const int s = b >> 3;
+    const int nbk = 8 * (s / mblocks) + (b & 7);
+    const int mbk = s % mblocks;
+    if (nbk >= nblocks) return;   // padding workgroup: whole workgroup, before any barrier
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    f32x4* red = reinterpret_cast<f32x4*>(smem);   // [SK - 1][MT][RB][64]
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int G = K >> 7;
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+    const int n0 = nbk * 16 * RB;
+    const int m0 = mbk * 16 * MT;
+    const int ng = wave < G ? (G - 1 - wave) / SK + 1 : 0;   // groups of this wavefront
+
+    // per-lane 32-bit byte offsets (the host checks that every buffer is
+    // below 4 GiB); rows past the end re-read the last row and are not stored
+    const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scales);
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(x);
+    uint32_t wrow[RB], srow[RB], xrow[MT];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const uint32_t n = (uint32_t)min(n0 + 16 * r + c, N - 1);
+        wrow[r] = n * row_bytes + 16u * q;
+        srow[r] = n * (uint32_t)G * 2u;
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const uint32_t m = (uint32_t)min(m0 + 16 * t + c, M - 1);
+        xrow[t] = (m * (uint32_t)K + 32u * q) * 2u;
+    }
+
+    auto load = [&](GemmGroup<MT, RB>& buf, int j) {
+        const uint32_t g = (uint32_t)(wave + SK * j);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) buf.s[r] = *reinterpret_cast<const uint16_t*>(sbase + srow[r] + g * 2u);
+#pragma unroll
+        for (int r = 0; r < RB; ++r) buf.w[r] = *reinterpret_cast<const u32x4*>(w + wrow[r] + g * 64u);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                buf.a[t][st] = *reinterpret_cast<const u32x4*>(xbase + xrow[t] + g * 256u + 16u * st);
+    };
+
+    f32x4 acc[MT][RB];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[t][r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const GemmGroup<MT, RB>& buf) {
+        const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+        const f16x2 off = {(f16)-1032.0f, (f16)-72.0f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const f16 sc = __builtin_bit_cast(f16, (uint16_t)buf.s[r]);
+                const f16x2 sc2 = {sc, sc};
+                const uint32_t word = buf.w[r][st];
+                f16x2 p[4];
+#pragma unroll
+                for (int by = 0; by < 4; ++by) {
+                    // byte `by` in both halves, low nibble low, high nibble 4 bits up
+                    const uint32_t sel = (0x0Cu << 24) | ((uint32_t)by << 16) | (0x0Cu << 8) | (uint32_t)by;
+                    const uint32_t v = __builtin_amdgcn_bitop3_b32(perm(word, word, sel), 0x00F0000Fu,
+                                                                   0x64806408u, 0x6A);
+                    p[by] = __builtin_elementwise_fma(as_f16x2(v), mul, off) * sc2;
+                }
+                const f16x8 bt = __builtin_bit_cast(
+                    f16x8, (u32x4){as_u32(p[0]), as_u32(p[1]), as_u32(p[2]), as_u32(p[3])});
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, buf.a[t][st]), bt,
+                                                                       acc[t][r], 0, 0, 0);
+            }
+        }
+    };
+
+    // groups j = 0 .. ng - 1, two register buffers; the loop's tail is
+    // peeled so no load sits behind a branch inside it
+    if (ng > 0) {
+        GemmGroup<MT, RB> b0, b1;
+        load(b0, 0);
+        int j = 0;
+        for (; j + 2 < ng; j += 2) {
+            load(b1, j + 1);
+            compute(b0);
+            load(b0, j + 2);
+            compute(b1);
+        }
+        if (j + 1 < ng) {
+            load(b1, j + 1);
+            compute(b0);
+            compute(b1);
+        } else {
+            compute(b0);
+        }
+    }
+
+    // SK partial tiles: wavefronts 1.. write, wavefront 0 sums in order 0..SK-1
+    if (SK > 1) {
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < RB; ++r) red[(((wave - 1) * MT + t) * RB + r) * 64 + lane] = acc[t][r];
+        }
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int kw = 1; kw < SK; ++kw) acc[t][r] += red[(((kw - 1) * MT + t) * RB + r) * 64 + lane];
+    }
+    // D rows 4 q .. 4 q + 3 (activation rows), column c (weight row)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int n = n0 + 16 * r + c;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + 16 * t + 4 * q + e;
+                if (m < M && n < N) out[(size_t)m * N + n] = (f16)acc[t][r][e];
+            }
+        }
+    }
+}
+
+}  // namespace w4a16

@@ -1,0 +1,94 @@
+// Launcher of the W4A16 GEMM for prompts (w4a16_gemm.h) and its
+// instantiations, in a translation unit of their own. Called by the
+// dispatcher in w4a16_hip.hip.
+#include "w4a16_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "w4a16_gemm.h"
+
+namespace w4a16_internal {
+void set_last_error(const std::string& message);   // w4a16_hip.hip
+int ensure_lds(const void* kernel, int bytes);     // w4a16_hip.hip: raise the dynamic-LDS limit once
+}  // namespace w4a16_internal
+
+namespace {
+
+int fail(int code, const std::string& message) {
+    w4a16_internal::set_last_error(message);
+    return code;
+}
+
+using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int, int);
+
+// Instantiated shapes: MT in {1, 2, 4} activation tiles and RB in {1, 2, 4}
+// weight tiles per wavefront, SK in {2, 4, 8} wavefronts splitting K, except
+// MT = RB = 4 with 8 wavefronts (its 16 tiles spill within the 256 VGPRs of
+// a 512-thread workgroup).
+template <int MT, int RB>
+Kern pick_sk(int sk) {
+    using namespace w4a16;
+    if (sk == 2) return gemm_w4a16<MT, RB, 2>;
+    if (sk == 4) return gemm_w4a16<MT, RB, 4>;
+    if constexpr (MT * RB < 16) {
+        if (sk == 8) return gemm_w4a16<MT, RB, 8>;
+    }
+    return nullptr;
+}
+
+template <int MT>
+Kern pick_rb(int rb, int sk) {
+    if (rb == 1) return pick_sk<MT, 1>(sk);
+    if (rb == 2) return pick_sk<MT, 2>(sk);
+    if (rb == 4) return pick_sk<MT, 4>(sk);
+    return nullptr;
+}
+
+Kern pick(int mt, int rb, int sk) {
+    if (mt == 1) return pick_rb<1>(rb, sk);
+    if (mt == 2) return pick_rb<2>(rb, sk);
+    if (mt == 4) return pick_rb<4>(rb, sk);
+    return nullptr;
+}
+
+}  // namespace
+
+namespace w4a16_internal {
+
+bool gemm_instantiated(int mt, int rb, int sk) { return pick(mt, rb, sk) != nullptr; }
+
+// Every byte offset the kernel forms fits in 32 bits.
+bool gemm_fits(int64_t M, int64_t N, int64_t K) {
+    const int64_t lim = (int64_t)1 << 32;
+    return K % 128 == 0 && K > 0 && N * (K / 2) < lim && M * K * 2 < lim && N * (K / 128) * 2 < lim;
+}
+
+// Launch gemm_w4a16 over [M, K] x [N, K]^T: mt activation tiles and rb
+// weight tiles of 16 rows per wavefront, sk wavefronts splitting K. The
+// caller has checked pointers, group size 128 and 16-byte alignment.
+int launch_gemm(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N, int K,
+                hipStream_t stream) {
+    if (M < 1 || N < 1 || !gemm_fits(M, N, K))
+        return fail(W4A16_ERR_CONFIG, "GEMM kernel: K must be a positive multiple of 128 and every operand below 4 GiB");
+    const Kern kern = pick(mt, rb, sk);
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, "GEMM kernel: rows (activation tiles) 1, 2 or 4, max_blocks (weight tiles) 1, 2 "
+                                      "or 4, splits 2, 4 or 8 (not 8 with rows = max_blocks = 4)");
+    const int lds = (int)w4a16::gemm_lds_bytes(mt, rb, sk);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int nblocks = (N + 16 * rb - 1) / (16 * rb);
+    const int mblocks = (M + 16 * mt - 1) / (16 * mt);
+    const int64_t grid = (int64_t)((nblocks + 7) & ~7) * mblocks;
+    if (grid > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "GEMM kernel: too many workgroups");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * sk), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, N, K, nblocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
+}  // namespace w4a16_internal

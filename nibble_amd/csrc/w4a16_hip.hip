@@ -30,6 +30,11 @@ int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
 int launch_stream(int rows, int waves, int depth, int max_blocks, const void* x, const uint8_t* w, const void* s,
                   void* o, int N, int K, hipStream_t stream);
+// w4a16_gemm.hip: the W4A16 GEMM for prompts (M > 16)
+bool gemm_instantiated(int mt, int rb, int sk);
+bool gemm_fits(int64_t M, int64_t N, int64_t K);
+int launch_gemm(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N, int K,
+                hipStream_t stream);
 }  // namespace w4a16_internal
 
 namespace {
@@ -292,6 +297,50 @@ bool stream_fits(int64_t K) {
            w4a16_internal::stream_lds_bytes(K) <= kMaxLdsBytes;
 }
 
+// W4A16 GEMM (w4a16_gemm.h) for M > 16. Plan fields: rows = MT activation
+// tiles of 16 rows per wavefront, max_blocks = RB weight tiles of 16 rows
+// per wavefront, splits = SK wavefronts splitting K, unroll unused. Launch
+// shape from the sweep over M 32..256 and the 1.1B / 8B layer shapes: the
+// first of (MT, RB) = (4, 4), (2, 4), (4, 2), (2, 2), (1, 4), (1, 2), (2, 1),
+// (1, 1) with MT <= ceil(M / 16) that leaves at least 160 workgroups (the
+// most workgroups otherwise); 2 wavefronts splitting K for tiles of 8 or 16
+// MFMA blocks, else 4 (2 on rows of fewer than 8 groups).
+Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_GEMM;
+    static const int kShapes[8][2] = {{4, 4}, {2, 4}, {4, 2}, {2, 2}, {1, 4}, {1, 2}, {2, 1}, {1, 1}};
+    const int64_t mtiles = (M + 15) / 16;
+    int64_t best = -1;
+    for (const auto& sh : kShapes) {
+        const int mt = sh[0], rb = sh[1];
+        if (mt > mtiles) continue;
+        const int64_t wgs = ((N + 16 * rb - 1) / (16 * rb)) * ((M + 16 * mt - 1) / (16 * mt));
+        if (wgs >= 160) {
+            p.rows = mt;
+            p.max_blocks = rb;
+            best = wgs;
+            break;
+        }
+        if (wgs > best) {
+            best = wgs;
+            p.rows = mt;
+            p.max_blocks = rb;
+        }
+    }
+    p.splits = (K / 128 < 8 || p.rows * p.max_blocks >= 8) ? 2 : 4;
+    p.unroll = 0;
+    return p;
+}
+
+// Largest M the dispatcher sends to the GEMM kernel.
+constexpr int64_t kGemmMaxM = 1 << 20;
+
+bool gemm_fits(int64_t M, int64_t N, int64_t K) {
+    const Plan p = plan_gemm(M, N, K);
+    return M > 16 && M <= kGemmMaxM && w4a16_internal::gemm_fits(M, N, K) &&
+           w4a16_internal::gemm_instantiated(p.rows, p.max_blocks, p.splits);
+}
+
 // M = 1 layers with rows from kStreamMinK weights and at least
 // kStreamMinN rows run the streaming kernel (measured against the one-shot
 // kernel: 28672 x 8192 20.4 against 30.8 us, 14336 x 4096 7.25 against 7.76;
@@ -351,6 +400,11 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_PAIR) &&
         mfma_pair_fits(M, N, K)) {
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
+        return W4A16_OK;
+    }
+    // M > 16 (a prompt): the W4A16 GEMM
+    if (aligned && M > 16 && gemm_fits(M, N, K)) {
+        *out = plan_gemm(M, N, K);
         return W4A16_OK;
     }
     const bool tuned = aligned && M <= 8;
@@ -702,6 +756,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_STREAM:
             return w4a16_internal::launch_stream(p.rows, p.splits, p.unroll, p.max_blocks, x, packed, s, o, (int)N,
                                                  (int)K, st);
+        case W4A16_KERNEL_GEMM:
+            return w4a16_internal::launch_gemm(p.rows, p.max_blocks, p.splits, (int)M, x, packed, s, o, (int)N, (int)K,
+                                               st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -802,7 +859,11 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_STREAM) {
+    if (kernel == W4A16_KERNEL_GEMM) {
+        if (group_size != 128 || M > INT32_MAX || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "the GEMM kernel needs group_size 128 and 16-byte aligned activations and weights");
+    } else if (kernel == W4A16_KERNEL_STREAM) {
         if (group_size != 128 || M != 1 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "the streaming kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
@@ -824,7 +885,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_STREAM, _DIAG or _GENERIC");
+                    "_STREAM, _GEMM, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
 }

@@ -26,12 +26,15 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill of a prompt of up to 16 tokens runs the W4A16 op itself (q|k|v and
-gate|up as one op each; the op takes its one-shot MFMA kernel where the
-activations fit that kernel's LDS and the paired MFMA kernel over two halves
-of the rows elsewhere, as for the 5632-wide down projection), and dequantize
-+ hipBLASLt for longer prompts; ``capture_prefill(T)`` records a T-token prefill in a HIP
-graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
+Prefill of a prompt of up to 64 tokens runs the W4A16 op itself for every
+projection (q|k|v and gate|up as one op each; up to 16 tokens the op takes
+its one-shot MFMA kernel where the activations fit that kernel's LDS and the
+paired MFMA kernel over two halves of the rows elsewhere, as for the
+5632-wide down projection; beyond 16 its W4A16 GEMM) with one launch each
+for the RMSNorms, the rotary + KV append + causal attention and the
+SiLU-multiply; longer prompts run torch ops around the same op (the GEMM up
+to 256 rows, dequantize + hipBLASLt beyond). ``capture_prefill(T)`` records
+a T-token prefill in a HIP graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.
 """
@@ -47,6 +50,15 @@ import torch.nn.functional as F
 from nibble_amd import _lib
 from nibble_amd.linear import QuantizedLinear
 from nibble_amd.quantization import quantize_and_pack_weights
+
+# Longest prompt the fused prefill takes (w4a16_prefill_attention_f16 holds
+# at most 64 new tokens).
+FUSED_PREFILL_MAX_TOKENS = 64
+# Most rows a prefill projection sends to the W4A16 op in the torch-op
+# prefill; more rows take dequantize + hipBLASLt. Measured on the 1.1B and 8B
+# layer shapes: the op's GEMM is 1.2-3x faster than dequantize + hipBLASLt
+# from 32 to 256 rows, except 4096 x 14336 at 256 rows (90.7 against 80.7 us).
+NATIVE_PREFILL_MAX_ROWS = 256
 
 
 @dataclass
@@ -111,9 +123,9 @@ class Block(torch.nn.Module):
 
     def _native(self, x: torch.Tensor, packed: torch.Tensor) -> bool:
         """Whether the W4A16 op itself (not dequantize + hipBLASLt) is the fast
-        path for these rows: GPU rows the op routes to a tuned kernel
-        (M <= 16, K up to 32768)."""
-        if not (self.native_prefill and x.is_cuda and x.shape[0] <= 16):
+        path for these rows: GPU rows (at most NATIVE_PREFILL_MAX_ROWS) that
+        the op routes to a tuned kernel or its GEMM."""
+        if not (self.native_prefill and x.is_cuda and x.shape[0] <= NATIVE_PREFILL_MAX_ROWS):
             return False
         plan = _lib.plan_linear(x.data_ptr(), packed.data_ptr(), x.shape[0], packed.shape[0], x.shape[1],
                                 self.cfg.group_size)
@@ -127,8 +139,9 @@ class Block(torch.nn.Module):
     def forward(self, x, cos, sin, positions, k_cache, v_cache, mask):
         """x [T, H] fp16; positions [T] int64 (cache slots to write);
         k_cache / v_cache [kv_heads, S, head_dim]; mask [T, S] additive fp32.
-        With native_prefill on a GPU, short prompts run q|k|v and gate|up as
-        one W4A16 op each over the concatenated weights; otherwise every
+        With native_prefill on a GPU, prompts of up to NATIVE_PREFILL_MAX_ROWS
+        tokens run q|k|v and gate|up as one W4A16 op each over the
+        concatenated weights (and o, down as the op); otherwise every
         projection is its QuantizedLinear."""
         cfg = self.cfg
         t = x.shape[0]
@@ -238,7 +251,7 @@ class LlamaDecoder(torch.nn.Module):
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
-        self.fuse_prefill = True   # prompts of <= 16 tokens: fused prefill (see fused_prefill)
+        self.fuse_prefill = True   # prompts of <= 64 tokens: fused prefill (see fused_prefill)
         self.prefill_tokens: torch.Tensor | None = None
         self.prefill_positions: torch.Tensor | None = None
         # fused-step weights (views keep the per-module state-dict entries) and work buffers
@@ -271,9 +284,10 @@ class LlamaDecoder(torch.nn.Module):
 
     def fused_prefill(self, tokens: int) -> bool:
         """Whether a prompt of `tokens` tokens takes the fused prefill: the W4A16
-        op for every projection (M <= 16) and one launch for each RMSNorm,
-        attention and SiLU-multiply."""
-        return (self.fused and self.fuse_prefill and 1 <= tokens <= 16
+        op for every projection and one launch for each RMSNorm, attention and
+        SiLU-multiply (1 <= tokens <= FUSED_PREFILL_MAX_TOKENS, within the
+        cache and the attention launch's 256 slots)."""
+        return (self.fused and self.fuse_prefill and 1 <= tokens <= FUSED_PREFILL_MAX_TOKENS
                 and tokens <= min(self.cfg.max_seq_len, 256))
 
     def _prefill(self, prompt: torch.Tensor, positions: torch.Tensor) -> None:

@@ -124,7 +124,10 @@ ALIGNED = 1 << 20
         (16, 5632, 128, ALIGNED, "mfma_pair"),     # beyond the one-shot kernel's LDS: two paired launches
         (9, 28672, 128, ALIGNED, "mfma_pair"),
         (16, 34816, 128, ALIGNED, "generic"),      # beyond the paired kernel's rows
-        (17, 2048, 128, ALIGNED, "generic"),       # above one tile
+        (17, 2048, 128, ALIGNED, "gemm"),          # prompts above one tile: the W4A16 GEMM
+        (64, 5632, 128, ALIGNED, "gemm"),
+        (300, 34816, 128, ALIGNED, "gemm"),
+        (17, 2048, 128, ALIGNED + 2, "generic"),   # misaligned prompt
         (1, 2048, 64, ALIGNED, "generic"),     # group size other than 128
         (1, 2048, 128, ALIGNED + 2, "generic"),  # activations not 16-byte aligned
         (0, 2048, 128, ALIGNED, "none"),       # empty
@@ -153,6 +156,22 @@ def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
         assert plan["max_blocks"] == 0
         monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # an explicit VALU row count keeps auto off it
         assert _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)["kernel"] != "stream"
+
+
+@pytest.mark.parametrize("m,n,k,rows,blocks,splits", [
+    # best shapes of the M = 32..256 sweep on the 1.1B / 8B layers
+    (32, 2560, 2048, 1, 2, 4), (32, 2048, 2048, 1, 1, 4), (32, 11264, 2048, 2, 4, 2), (32, 14336, 4096, 2, 4, 2),
+    (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (64, 11264, 2048, 4, 4, 2), (64, 4096, 14336, 2, 2, 4),
+    (128, 2560, 2048, 2, 4, 2), (128, 14336, 4096, 4, 4, 2), (256, 2048, 2048, 2, 4, 2), (256, 4096, 14336, 4, 4, 2),
+    (17, 64, 256, 1, 1, 2),     # few workgroups whatever the shape: the most; short rows: 2 wavefronts
+])
+def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
+    """M > 16: the largest tile (activation tiles within ceil(M / 16)) that
+    leaves >= 160 workgroups; 2 wavefronts splitting K for 8+ MFMA blocks per
+    wavefront or rows of fewer than 8 groups, else 4."""
+    monkeypatch.setenv("W4A16_DECODE", "valu")   # the selector covers M <= 8 only
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+    assert (plan["kernel"], plan["rows"], plan["max_blocks"], plan["splits"]) == ("gemm", rows, blocks, splits)
 
 
 def test_stream_env_selector(monkeypatch):

@@ -527,16 +527,20 @@ def test_checkpoint_into_fused_decoder(gpu, tmp_path):
     assert torch.equal(dec.generate(prompt, 6, use_graph=True), eager)
 
 
-def test_native_and_graphed_prefill(gpu):
-    """Prefill with the W4A16 op for the short prompt (one-shot MFMA kernel,
-    fused q|k|v and gate|up) matches the dequantize + hipBLASLt module path
-    (logits |err| <= 2e-2 (1 + |ref|), same next token), and the graphed
-    prefill reproduces the eager one exactly."""
+@pytest.mark.parametrize("tokens", [16, 40])
+def test_native_and_graphed_prefill(gpu, tokens):
+    """Torch-op prefill with the W4A16 op for the projections (16 tokens: the
+    one-shot MFMA kernel; 40: the GEMM; fused q|k|v and gate|up) matches the
+    dequantize + hipBLASLt module path (logits |err| <= 2e-2 (1 + |ref|)),
+    and the graphed prefill reproduces the eager one exactly."""
+    from dataclasses import replace
+
     from nibble_amd.llama import LlamaDecoder
 
-    model = LlamaDecoder(_small_cfg(), device=gpu, seed=7)
-    prompt = torch.randint(0, 512, (16,), generator=torch.Generator().manual_seed(8)).to(gpu)
-    positions = torch.arange(16, device=gpu)
+    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=64), device=gpu, seed=7)
+    model.fuse_prefill = False   # prefill() takes the torch-op path checked here
+    prompt = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(8)).to(gpu)
+    positions = torch.arange(tokens, device=gpu)
     with torch.inference_mode():
         for b in model.layers:
             b.native_prefill = False
@@ -549,9 +553,9 @@ def test_native_and_graphed_prefill(gpu):
     assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
     eager_tok = model.prefill(prompt)
     k_eager, x_eager = model.k_cache.clone(), model.x_buf.clone()
-    model.capture_prefill(16)
-    other = torch.randint(0, 512, (16,), generator=torch.Generator().manual_seed(9)).to(gpu)
+    model.capture_prefill(tokens)
+    other = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(9)).to(gpu)
     model.prefill(other)                       # a replay on different tokens in between
     assert torch.equal(model.prefill(prompt), eager_tok)
     assert torch.equal(model.k_cache, k_eager) and torch.equal(model.x_buf, x_eager)
-    assert int(model.position) == 16
+    assert int(model.position) == tokens

@@ -20,6 +20,7 @@ ONESHOT = _lib.KERNEL_ONESHOT
 MFMA_OS = _lib.KERNEL_MFMA_ONESHOT
 MFMA_PAIR = _lib.KERNEL_MFMA_PAIR
 STREAM = _lib.KERNEL_STREAM
+GEMM = _lib.KERNEL_GEMM
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -237,6 +238,59 @@ def test_mfma_pair_rejects(gpu):
     x, p, s = make_case(8, 8320, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="do not fit in LDS"):
         _run_tuned(gpu, x, p, s, MFMA_PAIR, 40, 8, 5, 1)  # whole rows of 40 pairs
+
+
+GEMM_SHAPES = [(1, 1, 2), (2, 1, 4), (4, 1, 8), (1, 2, 4), (2, 2, 8), (4, 2, 2), (1, 4, 8), (2, 4, 4), (4, 4, 2),
+               (4, 4, 4)]
+
+
+@pytest.mark.parametrize("rows,blocks,splits", GEMM_SHAPES)
+@pytest.mark.parametrize("m,k,n", [(17, 2048, 200), (64, 384, 33), (100, 5632, 48), (3, 1152, 100)])
+def test_gemm_variants(gpu, rows, blocks, splits, m, k, n):
+    """The GEMM's instantiated tilings on ragged M and N (tiles past the
+    end), K of 3..44 groups (wavefronts with no group when splits > K / 128)."""
+    x, p, s = make_case(m, k, n, seed=m * 5 + k + n + rows)
+    got = _run_tuned(gpu, x, p, s, GEMM, rows, splits, 0, max_blocks=blocks)
+    assert_parity(got, expected(x, p, s), f"gemm {rows}/{blocks}/{splits} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(17, 2048, 2048), (64, 2048, 5632), (130, 5632, 2048), (512, 2048, 256),
+                                   (33, 8192, 1000)])
+def test_default_dispatch_gemm(gpu, m, k, n):
+    x, p, s = make_case(m, k, n, seed=m + k + 3 * n)
+    assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == "gemm"
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"gemm default M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(48, 2048, 512), (200, 1024, 96)])
+def test_gemm_uses_dequantized_weights(gpu, m, k, n):
+    """The B operand is fp16_rn(code * scale), bit-identical to what
+    w4a16_dequantize_f16 writes: against a float64 product of the activations
+    with those dequantized weights the GEMM is within one fp16 rounding of the
+    output (fp32 accumulation only reorders the sum)."""
+    x, p, s = make_case(m, k, n, seed=m + n)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    wdq = torch.empty((n, k), dtype=torch.float16, device=gpu)
+    _lib.dequantize_f16(pd, sd, wdq, 128)
+    out = _run_tuned(gpu, x, p, s, GEMM, 4, 2, 0, max_blocks=2)
+    ref = (xd.double() @ wdq.double().t()).cpu()
+    got = out.double().cpu()
+    ulp = torch.finfo(torch.float16).eps / 2
+    assert torch.all((got - ref).abs() <= ulp * ref.abs() + 1e-4), float((got - ref).abs().max())
+
+
+def test_gemm_rejects(gpu):
+    x, p, s = make_case(32, 2048, 16, seed=3)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    out = torch.zeros((32, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="splits"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, GEMM, 4, 8, 0, 4)   # 16 tiles with 8 wavefronts
+    with pytest.raises(_lib.W4A16Error, match="rows"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, GEMM, 3, 4, 0, 1)
+    with pytest.raises(_lib.W4A16Error, match="group_size 128"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 64, GEMM, 2, 4, 0, 1)
+    torch.cuda.synchronize()
+    assert not out.any()
 
 
 STREAM_SHAPES = [(2, 4, 2), (2, 8, 4), (4, 4, 3), (4, 8, 2), (4, 4, 4), (8, 4, 2), (8, 8, 2), (2, 4, 3)]
