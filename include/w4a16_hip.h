@@ -45,6 +45,7 @@ extern "C" {
 #define W4A16_KERNEL_MFMA_PAIR 8     /* fp16 MFMA on 8 rows x 2 groups, loads up front (2 <= M <= 8, staged M*K in LDS) */
 #define W4A16_KERNEL_STREAM 9        /* VALU GEMV, resident workgroups streaming rows along K (M = 1, K <= 32768) */
 #define W4A16_KERNEL_GEMM 10         /* fp16 MFMA GEMM on weights decoded in registers (M > 16, prompts) */
+#define W4A16_KERNEL_PAIR_STREAM 11  /* paired MFMA, resident workgroups streaming 8-row blocks (2 <= M <= 8) */
 
 /*
  * Fused W4A16 linear layer.
@@ -59,8 +60,8 @@ extern "C" {
  * the W4A16 GEMM (operands below 4 GiB); anything else takes the generic
  * kernel (the reference routes every M > 8 to its naive kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
- * valu_offset|mfma|mfma_oneshot|mfma_pair|stream selects the kernel family
- * for M <= 8;
+ * valu_offset|mfma|mfma_oneshot|mfma_pair|stream|pair_stream selects the
+ * kernel family for M <= 8;
  * W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront of the VALU
  * kernels (any other value is W4A16_ERR_CONFIG).
  */
@@ -145,6 +146,11 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
  *     (at most ceil(K / 2048)),
  *     max_blocks = grid (0 = the workgroups resident on the device at once).
+ *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
+ *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
+ *     row blocks with the workgroups resident at once; else 1..16), unroll =
+ *     group pairs in flight per wavefront (2|3|4), max_blocks = grid cap
+ *     (0 = none), splits ignored.
  *   W4A16_KERNEL_GEMM (any M; every operand below 4 GiB): rows = 16-row
  *     activation tiles per wavefront (1|2|4), max_blocks = 16-row weight
  *     tiles per wavefront (1|2|4), splits = wavefronts splitting K (2|4|8;

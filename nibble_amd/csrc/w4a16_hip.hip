@@ -25,6 +25,11 @@ bool mfma_pair_instantiated(int64_t M, int sk, int sn, int chunk, int gpw);
 int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int gpw);
 int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream);
+int64_t pair_stream_lds(int64_t M, int64_t K);
+bool pair_stream_instantiated(int depth);
+int pair_stream_waves(int64_t M, int64_t N, int64_t K);
+int launch_pair_stream(int depth, int waves, int max_blocks, int M, const void* x, const uint8_t* w, const void* s,
+                       void* o, int N, int K, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -102,9 +107,10 @@ int read_env(int* family, int* rows_per_wave) {
         else if (std::strcmp(d, "mfma_oneshot") == 0) *family = W4A16_KERNEL_MFMA_ONESHOT;
         else if (std::strcmp(d, "mfma_pair") == 0) *family = W4A16_KERNEL_MFMA_PAIR;
         else if (std::strcmp(d, "stream") == 0) *family = W4A16_KERNEL_STREAM;
+        else if (std::strcmp(d, "pair_stream") == 0) *family = W4A16_KERNEL_PAIR_STREAM;
         else
             return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, mfma_oneshot, "
-                                          "mfma_pair, or stream");
+                                          "mfma_pair, stream, or pair_stream");
     }
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
@@ -361,6 +367,38 @@ bool mfma_pair_fits(int64_t M, int64_t N, int64_t K) {
            w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
 }
 
+// Streaming paired kernel (w4a16_pair.h, M = 2..8, whole rows staged once per
+// workgroup). Plan fields: rows = wavefronts per workgroup (0 = automatic),
+// unroll = pairs in flight per wavefront, max_blocks = grid cap (0 = none).
+// Launch shape from the M = 4 and 8 sweeps: 4 pairs in flight; 16
+// wavefronts from 3072 row blocks of 8 (8192 x 28672: 29.8 us at M = 8,
+// 224 workgroups), else 8 (4096 x 14336: 10.3 us).
+Plan plan_pair_stream(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_PAIR_STREAM;
+    p.rows = (N + 7) / 8 >= 3072 ? 16 : 8;
+    p.splits = 1;
+    p.unroll = 4;
+    p.max_blocks = 0;
+    (void)M;
+    (void)K;
+    return p;
+}
+
+// Wide layers (M >= 3) take the streaming paired kernel where its staging
+// once per workgroup pays: measured against the paired kernel at M = 4 and
+// 8, 8192 x 28672 29.8 against 39.4 us (M = 8), 28.5 against 35.7 (M = 4),
+// 4096 x 14336 10.3 against 10.7; it loses on N <= 8192 (8192 x 8192 M = 8:
+// 16.5 against 12.2), where the paired kernel already stages about once per
+// CU.
+constexpr int64_t kPairStreamMinN = 14336;
+constexpr int64_t kPairStreamMinK = 4096;
+
+bool pair_stream_fits(int64_t M, int64_t K) {
+    return M >= 2 && M <= 8 && K >= 128 && K % 128 == 0 && K <= 32768 &&
+           w4a16_internal::pair_stream_lds(M, K) <= kMaxLdsBytes;
+}
+
 // M = 9..16 on the paired kernel: two launches, rows [0, m1) and [m1, M) with
 // m1 = ceil(M/2) (each half 4..8 rows), each with its own launch shape unless
 // the caller fixed one; the weights are streamed twice.
@@ -425,8 +463,10 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // Measured routing (M = 1..8 sweeps over the benchmark shapes):
     //   M = 1: streaming VALU for long rows of wide layers (K >= 14336,
     //   N >= 4096), else one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
-    //   M >= 3: the paired-group MFMA kernel up to K = 32768 (activations
-    //   staged whole or in chunks); beyond that as before:
+    //   M >= 3: the streaming paired kernel on wide layers (N >= 14336,
+    //   K >= 4096) whose M*K activations fit in LDS, else the paired-group
+    //   MFMA kernel up to K = 32768 (activations staged whole or in chunks);
+    //   beyond that as before:
     //   one-shot MFMA up to K = 4096, one-shot VALU for M <= 4 on
     //   small layers (K, N <= 5632; each workgroup re-stages M*K activations,
     //   which on large layers outweighs the weights it streams), one-shot
@@ -439,6 +479,8 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
             family = W4A16_KERNEL_STREAM;
         else if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
             family = W4A16_KERNEL_ONESHOT;
+        else if (rows == 0 && M >= 3 && N >= kPairStreamMinN && K >= kPairStreamMinK && pair_stream_fits(M, K))
+            family = W4A16_KERNEL_PAIR_STREAM;
         else if (rows == 0 && M >= 3 && mfma_pair_fits(M, N, K))
             family = W4A16_KERNEL_MFMA_PAIR;
         else if (M >= 3 && K <= 4096 && mfma_oneshot_fits(M, K))
@@ -457,6 +499,13 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
             return W4A16_OK;
         }
         family = oneshot_fits(M, K) ? W4A16_KERNEL_ONESHOT : W4A16_KERNEL_VALU;   // M > 1 or rows too short
+    }
+    if (family == W4A16_KERNEL_PAIR_STREAM) {
+        if (pair_stream_fits(M, K)) {
+            *out = plan_pair_stream(M, N, K);
+            return W4A16_OK;
+        }
+        family = W4A16_KERNEL_MFMA_PAIR;   // M = 1 or activations too long for LDS
     }
     if (family == W4A16_KERNEL_MFMA_PAIR) {
         if (mfma_pair_fits(M, N, K)) {
@@ -756,6 +805,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_STREAM:
             return w4a16_internal::launch_stream(p.rows, p.splits, p.unroll, p.max_blocks, x, packed, s, o, (int)N,
                                                  (int)K, st);
+        case W4A16_KERNEL_PAIR_STREAM:
+            return w4a16_internal::launch_pair_stream(p.unroll, p.rows, p.max_blocks, (int)M, x, packed, s, o, (int)N,
+                                                      (int)K, st);
         case W4A16_KERNEL_GEMM:
             return w4a16_internal::launch_gemm(p.rows, p.max_blocks, p.splits, (int)M, x, packed, s, o, (int)N, (int)K,
                                                st);
@@ -868,6 +920,11 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
             return fail(W4A16_ERR_CONFIG,
                         "the streaming kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
                         "weights");
+    } else if (kernel == W4A16_KERNEL_PAIR_STREAM) {
+        if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "the streaming paired kernel needs group_size 128, 2 <= M <= 8 and 16-byte aligned activations "
+                        "and weights");
     } else if (kernel == W4A16_KERNEL_MFMA_PAIR) {
         if (group_size != 128 || M < 2 || M > 16 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
@@ -885,7 +942,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_STREAM, _GEMM, _DIAG or _GENERIC");
+                    "_PAIR_STREAM, _STREAM, _GEMM, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
 }

@@ -279,3 +279,203 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
 }
 
 }  // namespace w4a16
+
+namespace w4a16 {
+
+// ---------------------------------------------------------------------------
+// Streaming paired-group MFMA kernel (runtime M = 2..8, whole rows staged).
+//
+// The paired kernel above stages all M K activations in every workgroup, so
+// a layer of N rows in workgroups of R rows stages them N / R times; with
+// wide layers (N >> 256 R) that staging costs as much as the weights. Here
+// the grid is at most the workgroups resident at once: each workgroup stages
+// the activations once (the layout and per-(group, row) biases of the kernel
+// above) and its W wavefronts then stream 8-row blocks (tasks, dealt
+// round-robin over the grid's wavefronts) pair by pair, each wavefront over
+// whole rows, with D pairs of loads in flight in a ring of registers (one
+// 1 KiB load of 8 rows x 128 bytes and one scale per lane per pair). A
+// wavefront folds the two halves of its tile (lane l + 40 onto lane l) with
+// a lane shuffle and stores its block, so there is no barrier after the
+// staging. The loop's tail is peeled, so no load sits behind a branch; a
+// wavefront with no task requests D pairs of the grid's last block and
+// stores nothing.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int64_t pair_stream_lds_bytes(int64_t M, int64_t pairs) {
+    return pairs * 16 * (2 * pair_row_slots((int)M)) * 16 + pairs * 2 * 64;
+}
+
+template <int MS, int D>
+__global__ void __launch_bounds__(1024)
+gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+                 f16* __restrict__ out, int M, int N, int K) {
+    constexpr int LS = 2 * MS;   // units per line
+    constexpr int B = 8;         // staging units per thread requested at a time
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int G = K >> 7;
+    const int P = (G + 1) >> 1;                                              // pairs per row
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);                              // [P * 16 lines][LS]
+    float* base = reinterpret_cast<float*>(smem + (size_t)P * 16 * LS * 16); // [2 P][16]
+    const int T = blockDim.x;
+    const int W = T >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15, q = lane >> 4;
+    const int brow = col & 7, bhalf = col >> 3;
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+    const int upr = K >> 3;            // 16-byte units per activation row
+    const int CU = 32 * P;             // staged units per activation row (2 P groups x 16)
+    const int NB = (N + 7) >> 3;       // 8-row blocks
+    const int task0 = blockIdx.x * W + wave;
+    const int stride = gridDim.x * W;
+    const int my_tasks = task0 < NB ? (NB - 1 - task0) / stride + 1 : 0;
+    const int units = my_tasks * P;
+    const uint16_t* sbase = reinterpret_cast<const uint16_t*>(scales);
+
+    // staging unit i: activation row i / CU, unit i % CU; units of groups
+    // past K and rows past M read x[0]; every 16 consecutive units are one
+    // (row, group) and sit in one DPP row of 16 lanes
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 b0 = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 b1 = {(f16)1152.0f, (f16)1152.0f};
+    auto stage_load = [&](u32x4 (&a)[B], int first) {
+#pragma unroll
+        for (int p = 0; p < B; ++p) {
+            const int i = first + (int)threadIdx.x + p * T;
+            const int m = i / CU, ul = i % CU;
+            const int g = ul >> 4;
+            const bool valid = m < M && g < G && i < MS * CU;
+            a[p] = *reinterpret_cast<const u32x4*>(x + (valid ? ((size_t)m * upr + (size_t)g * 16 + (ul & 15)) * 8 : 0));
+        }
+    };
+    auto stage_put = [&](const u32x4 (&a)[B], int first) {
+#pragma unroll
+        for (int p = 0; p < B; ++p) {
+            const int i = first + (int)threadIdx.x + p * T;
+            const int m = i / CU, ul = i % CU;
+            const int gl = ul >> 4, qq = (ul >> 2) & 3, t = ul & 3;
+            u32x4 pv = permute8(a[p]);
+            pv.y = as_u32(as_f16x2(pv.y) * sixteenth);
+            pv.w = as_u32(as_f16x2(pv.w) * sixteenth);
+            if (gl >= G) pv = (u32x4){0u, 0u, 0u, 0u};
+            float cs = 0.0f;
+            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.x), b0, cs, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.y), b1, cs, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.z), b0, cs, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(pv.w), b1, cs, false);
+            cs += dpp<0xB1>(cs);
+            cs += dpp<0x4E>(cs);
+            cs += dpp<0x141>(cs);
+            cs += dpp<0x140>(cs);
+            if (m < M && i < MS * CU) {
+                xs[(((gl >> 1) * 4 + t) * 4 + qq) * LS + ((m + MS * (gl & 1) + 4 * qq + t) & (LS - 1))] = pv;
+                if ((ul & 15) == 0) base[gl * 16 + m] = -cs;
+            }
+        }
+    };
+
+    // ring of D pairs in flight: unit (task, pair)
+    u32x4 wv[D];
+    uint32_t sv[D];
+    auto load = [&](int d, int task, int pr) {
+        const int n = min(task * 8 + brow, N - 1);
+        const int gi = min(2 * pr + bhalf, G - 1);
+        sv[d] = sbase[(size_t)n * G + gi];
+        wv[d] = load_stream(reinterpret_cast<const u32x4*>(w + (size_t)n * row_bytes + (uint32_t)gi * 64u + q * 16));
+    };
+
+    // 1. the first staging batch, then the ring's first D pairs, then the rest
+    // of the staging (a wavefront's loads return in issue order)
+    const int total = MS * CU;
+    int lt = min(task0, NB - 1), lp = 0;   // next unit to request
+    {
+        u32x4 a[B];
+        stage_load(a, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load(d, lt, lp);
+            if (++lp == P) { lp = 0; lt += stride; }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        stage_put(a, 0);
+        for (int first = B * T; first < total; first += B * T) {
+            stage_load(a, first);
+            stage_put(a, first);
+        }
+    }
+    __syncthreads();
+    if (units == 0) return;
+
+    // 2. stream: per pair 4 A fragments and the bias from LDS, 4 MFMAs
+    const int arow = brow % M;
+    int toff[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) toff[t] = q * LS + 4 * t * LS + ((arow + MS * bhalf + 4 * q + t) & (LS - 1));
+    const int boff = (q >> 1) * 16 + 4 * (q & 1);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    int ct = task0, cp = 0;   // unit being computed
+
+    auto compute = [&](int d) {
+        u32x4 av[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) av[t] = xs[cp * 16 * LS + toff[t]];
+        f32x4 dv = *reinterpret_cast<const f32x4*>(base + cp * 32 + boff);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const Codes8 cw = unpack8_offset(wv[d][t]);
+            const f16x8 bt = __builtin_bit_cast(
+                f16x8, (u32x4){as_u32(cw.p[0]), as_u32(cw.p[1]), as_u32(cw.p[2]), as_u32(cw.p[3])});
+            dv = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av[t]), bt, dv, 0, 0, 0);
+        }
+        const float sc = 2 * cp + bhalf < G ? (float)__builtin_bit_cast(f16, (uint16_t)sv[d]) : 0.0f;
+        acc = dv * sc + acc;
+        if (cp == P - 1) {
+            // fold the two halves (lane l + 40 onto lane l, q < 2, col < 8) and store
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[e] + __shfl(acc[e], (lane + 40) & 63);
+            const int nn = ct * 8 + col;
+            if (q < 2 && col < 8 && nn < N) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 4 * q + e;
+                    if (m < M) out[(size_t)m * N + nn] = (f16)v[e];
+                }
+            }
+            acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            cp = 0;
+            ct += stride;
+        } else {
+            ++cp;
+        }
+    };
+
+    int u = 0;
+    if (units >= D) {
+        for (; u + 2 * D <= units; u += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                compute(d);
+                load(d, lt, lp);
+                if (++lp == P) { lp = 0; lt += stride; }
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            compute(d);
+            if (u + D + d < units) {
+                load(d, lt, lp);
+                if (++lp == P) { lp = 0; lt += stride; }
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (u + D + d < units) compute(d);
+    } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (d < units) compute(d);
+    }
+}
+
+}  // namespace w4a16

@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "w4a16_pair.h"
@@ -167,6 +168,66 @@ int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, c
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream,
                        static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
                        static_cast<w4a16::f16*>(o), M, N, K);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));
+        return W4A16_ERR_LAUNCH;
+    }
+    return W4A16_OK;
+}
+
+// Streaming paired kernel (gemv_pair_stream): whole rows staged once per
+// workgroup. depth = pairs in flight per wavefront (2, 3 or 4); waves =
+// wavefronts per workgroup (0: the fewest that cover the 8-row blocks with
+// the workgroups that fit on the device at once by LDS, at most 16);
+// max_blocks = grid cap (0: one workgroup per `waves` blocks).
+int64_t pair_stream_lds(int64_t M, int64_t K) { return w4a16::pair_stream_lds_bytes(M, (K / 128 + 1) / 2); }
+
+namespace {
+using StreamKern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int);
+template <int MS>
+StreamKern pick_stream(int depth) {
+    using namespace w4a16;
+    switch (depth) {   // deeper rings spill within the 128 VGPRs of a 1024-thread workgroup
+        case 2: return gemv_pair_stream<MS, 2>;
+        case 3: return gemv_pair_stream<MS, 3>;
+        case 4: return gemv_pair_stream<MS, 4>;
+        default: return nullptr;
+    }
+}
+}  // namespace
+
+bool pair_stream_instantiated(int depth) { return pick_stream<8>(depth) != nullptr; }
+
+int pair_stream_waves(int64_t M, int64_t N, int64_t K) {
+    int cus = 0, device = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
+        cus = 256;
+    const int64_t per_cu = std::max<int64_t>(1, kMaxLdsBytes / std::max<int64_t>(1, pair_stream_lds(M, K)));
+    const int64_t blocks = (N + 7) / 8;
+    const int64_t resident = per_cu * cus;
+    return (int)std::min<int64_t>(16, std::max<int64_t>(1, (blocks + resident - 1) / resident));
+}
+
+int launch_pair_stream(int depth, int waves, int max_blocks, int M, const void* x, const uint8_t* w, const void* s,
+                       void* o, int N, int K, hipStream_t stream) {
+    if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "streaming paired kernel needs 2 <= M <= 8");
+    if (K < 128 || K % 128 != 0 || K > 32768)
+        return fail(W4A16_ERR_CONFIG, "streaming paired kernel: K must be a multiple of 128 up to 32768");
+    const StreamKern kern = M <= 4 ? pick_stream<4>(depth) : pick_stream<8>(depth);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: unroll (pairs in flight) 2, 3 or 4");
+    if (waves == 0) waves = pair_stream_waves(M, N, K);
+    if (waves < 1 || waves > 16) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: rows (wavefronts) 1..16");
+    const int64_t lds = pair_stream_lds(M, K);
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: activations do not fit in LDS");
+    const int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int blocks = (N + 7) / 8;
+    int grid = (blocks + waves - 1) / waves;
+    if (max_blocks > 0 && grid > max_blocks) grid = max_blocks;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * waves), (size_t)lds, stream, static_cast<const w4a16::f16*>(x), w,
+                       static_cast<const w4a16::f16*>(s), static_cast<w4a16::f16*>(o), M, N, K);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));

@@ -174,6 +174,27 @@ def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
     assert (plan["kernel"], plan["rows"], plan["max_blocks"], plan["splits"]) == ("gemm", rows, blocks, splits)
 
 
+@pytest.mark.parametrize("m,n,k,kernel,waves", [
+    (8, 28672, 8192, "pair_stream", 16), (4, 28672, 8192, "pair_stream", 16), (8, 14336, 4096, "pair_stream", 8),
+    (3, 14336, 4096, "pair_stream", 8), (4, 14336, 14336, "pair_stream", 8),
+    (8, 14336, 14336, "mfma_pair", 0),    # 8 x 14336 activations do not fit in LDS
+    (8, 8192, 8192, "mfma_pair", 0), (8, 14336, 2048, "mfma_pair", 0), (2, 28672, 8192, "valu", 0),
+])
+def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
+    """M >= 3 on wide layers (N >= 14336, K >= 4096) whose activations fit
+    in LDS: the streaming paired kernel, 4 pairs in flight, 16 wavefronts
+    from 3072 row blocks of 8, else 8."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+    assert plan["kernel"] == kernel
+    if kernel == "pair_stream":
+        assert (plan["rows"], plan["unroll"], plan["max_blocks"]) == (waves, 4, 0)
+    monkeypatch.setenv("W4A16_DECODE", "pair_stream")   # any layer whose activations fit
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "pair_stream"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 16384, 128)["kernel"] == "mfma_pair"   # too long for LDS
+
+
 def test_stream_env_selector(monkeypatch):
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     monkeypatch.setenv("W4A16_DECODE", "stream")
@@ -188,7 +209,7 @@ def test_plan_misaligned_weights_take_generic():
 
 
 def test_mfma_pair_plan_shapes(monkeypatch):
-    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.setenv("W4A16_DECODE", "mfma_pair")   # wide layers default to the streaming paired kernel
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     # (M, N, K) -> (splits, row-block wavefronts per workgroup, unroll, staged pairs per chunk)
     for m, n, k, splits, blocks, unroll, chunk in [

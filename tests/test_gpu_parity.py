@@ -21,6 +21,7 @@ MFMA_OS = _lib.KERNEL_MFMA_ONESHOT
 MFMA_PAIR = _lib.KERNEL_MFMA_PAIR
 STREAM = _lib.KERNEL_STREAM
 GEMM = _lib.KERNEL_GEMM
+PAIR_STREAM = _lib.KERNEL_PAIR_STREAM
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -238,6 +239,57 @@ def test_mfma_pair_rejects(gpu):
     x, p, s = make_case(8, 8320, 8, seed=2)
     with pytest.raises(_lib.W4A16Error, match="do not fit in LDS"):
         _run_tuned(gpu, x, p, s, MFMA_PAIR, 40, 8, 5, 1)  # whole rows of 40 pairs
+
+
+@pytest.mark.parametrize("depth", [2, 3, 4])
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+@pytest.mark.parametrize("k,n", [(128, 7), (384, 100), (2048, 2048), (5632, 33), (8192, 40), (9216, 9)])
+def test_pair_stream_variants(gpu, depth, m, k, n):
+    """Streaming paired kernel: rows of 1 pair (fewer pairs than the ring),
+    an odd group count (the last pair's second group zero-padded), ragged N,
+    M of 2..8 (4 and 8 row slots) up to the longest rows that fit in LDS."""
+    x, p, s = make_case(m, k, n, seed=m * 7 + k + n + depth)
+    got = _run_tuned(gpu, x, p, s, PAIR_STREAM, 0, 1, depth)
+    assert_parity(got, expected(x, p, s), f"pair_stream d={depth} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("waves,cap", [(1, 1), (3, 2), (16, 1), (5, 7)])
+@pytest.mark.parametrize("m,k,n", [(4, 2048, 300), (8, 1152, 97)])
+def test_pair_stream_many_tasks(gpu, waves, cap, m, k, n):
+    """Explicit wavefront counts and small grid caps: each wavefront streams
+    many 8-row blocks, the ring crossing from one block's pairs to the next."""
+    x, p, s = make_case(m, k, n, seed=waves * 11 + cap + m)
+    got = _run_tuned(gpu, x, p, s, PAIR_STREAM, waves, 1, 3, max_blocks=cap)
+    assert_parity(got, expected(x, p, s), f"pair_stream waves={waves} cap={cap} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 4096, 14343), (8, 8192, 28672), (5, 4224, 16384)])
+def test_default_dispatch_pair_stream(gpu, m, k, n):
+    """Wide layers route to the streaming paired kernel (ragged N, an odd
+    group count at K = 4224)."""
+    x, p, s = make_case(m, k, n, seed=m + k + n)
+    assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == "pair_stream"
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"pair_stream default M={m} K={k} N={n}")
+
+
+def test_pair_stream_rejects(gpu):
+    x, p, s = make_case(8, 10240, 16, seed=4)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    out = torch.zeros((8, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="LDS"):   # 8 x 10240 activations do not fit
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, PAIR_STREAM, 0, 1, 2, 0)
+    x, p, s = make_case(1, 2048, 16, seed=4)
+    out1 = torch.zeros((1, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="2 <= M <= 8"):
+        _lib.linear_f16_tuned(x.to(gpu), p.to(gpu), s.to(gpu), out1, 128, PAIR_STREAM, 0, 1, 2, 0)
+    x, p, s = make_case(4, 2048, 16, seed=4)
+    out4 = torch.zeros((4, 16), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="unroll"):
+        _lib.linear_f16_tuned(x.to(gpu), p.to(gpu), s.to(gpu), out4, 128, PAIR_STREAM, 0, 1, 5, 0)
+    with pytest.raises(_lib.W4A16Error, match="wavefronts"):
+        _lib.linear_f16_tuned(x.to(gpu), p.to(gpu), s.to(gpu), out4, 128, PAIR_STREAM, 17, 1, 2, 0)
+    torch.cuda.synchronize()
+    assert not out.any() and not out1.any() and not out4.any()
 
 
 GEMM_SHAPES = [(1, 1, 2), (2, 1, 4), (4, 1, 8), (1, 2, 4), (2, 2, 8), (4, 2, 2), (1, 4, 8), (2, 4, 4), (4, 4, 2),
