@@ -149,7 +149,7 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
  *     row blocks with the workgroups resident at once; else 1..16), unroll =
- *     group pairs in flight per wavefront (2|3|4), max_blocks = grid cap
+ *     group pairs in flight per wavefront (2|3|4|6), max_blocks = grid cap
  *     (0 = none), splits ignored.
  *   W4A16_KERNEL_GEMM (any M; every operand below 4 GiB): rows = 16-row
  *     activation tiles per wavefront (1|2|4), max_blocks = 16-row weight

@@ -329,7 +329,6 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
     const int stride = gridDim.x * W;
     const int my_tasks = task0 < NB ? (NB - 1 - task0) / stride + 1 : 0;
     const int units = my_tasks * P;
-    const uint16_t* sbase = reinterpret_cast<const uint16_t*>(scales);
 
     // staging unit i: activation row i / CU, unit i % CU; units of groups
     // past K and rows past M read x[0]; every 16 consecutive units are one
@@ -373,14 +372,16 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
         }
     };
 
-    // ring of D pairs in flight: unit (task, pair)
+    // ring of D pairs in flight: unit (task, pair); 32-bit byte offsets (the
+    // host checks that the weights are below 4 GiB)
     u32x4 wv[D];
     uint32_t sv[D];
+    const uint8_t* sbytes = reinterpret_cast<const uint8_t*>(scales);
     auto load = [&](int d, int task, int pr) {
-        const int n = min(task * 8 + brow, N - 1);
-        const int gi = min(2 * pr + bhalf, G - 1);
-        sv[d] = sbase[(size_t)n * G + gi];
-        wv[d] = load_stream(reinterpret_cast<const u32x4*>(w + (size_t)n * row_bytes + (uint32_t)gi * 64u + q * 16));
+        const uint32_t n = (uint32_t)min(task * 8 + brow, N - 1);
+        const uint32_t gi = (uint32_t)min(2 * pr + bhalf, G - 1);
+        sv[d] = *reinterpret_cast<const uint16_t*>(sbytes + (n * (uint32_t)G + gi) * 2u);
+        wv[d] = load_stream(reinterpret_cast<const u32x4*>(w + (n * row_bytes + gi * 64u + (uint32_t)q * 16u)));
     };
 
     // 1. the first staging batch, then the ring's first D pairs, then the rest

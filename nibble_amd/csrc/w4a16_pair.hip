@@ -177,7 +177,7 @@ int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, c
 }
 
 // Streaming paired kernel (gemv_pair_stream): whole rows staged once per
-// workgroup. depth = pairs in flight per wavefront (2, 3 or 4); waves =
+// workgroup. depth = pairs in flight per wavefront (2, 3, 4 or 6); waves =
 // wavefronts per workgroup (0: the fewest that cover the 8-row blocks with
 // the workgroups that fit on the device at once by LDS, at most 16);
 // max_blocks = grid cap (0: one workgroup per `waves` blocks).
@@ -188,10 +188,11 @@ using StreamKern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*
 template <int MS>
 StreamKern pick_stream(int depth) {
     using namespace w4a16;
-    switch (depth) {   // deeper rings spill within the 128 VGPRs of a 1024-thread workgroup
+    switch (depth) {
         case 2: return gemv_pair_stream<MS, 2>;
         case 3: return gemv_pair_stream<MS, 3>;
         case 4: return gemv_pair_stream<MS, 4>;
+        case 6: return gemv_pair_stream<MS, 6>;   // deeper rings spill within 128 VGPRs (1024 threads)
         default: return nullptr;
     }
 }
@@ -215,8 +216,10 @@ int launch_pair_stream(int depth, int waves, int max_blocks, int M, const void* 
     if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "streaming paired kernel needs 2 <= M <= 8");
     if (K < 128 || K % 128 != 0 || K > 32768)
         return fail(W4A16_ERR_CONFIG, "streaming paired kernel: K must be a multiple of 128 up to 32768");
+    if ((int64_t)N * (K / 2) >= ((int64_t)1 << 32))
+        return fail(W4A16_ERR_TOO_LARGE, "streaming paired kernel: weights must be below 4 GiB");
     const StreamKern kern = M <= 4 ? pick_stream<4>(depth) : pick_stream<8>(depth);
-    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: unroll (pairs in flight) 2, 3 or 4");
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: unroll (pairs in flight) 2, 3, 4 or 6");
     if (waves == 0) waves = pair_stream_waves(M, N, K);
     if (waves < 1 || waves > 16) return fail(W4A16_ERR_CONFIG, "streaming paired kernel: rows (wavefronts) 1..16");
     const int64_t lds = pair_stream_lds(M, K);

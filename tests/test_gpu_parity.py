@@ -241,7 +241,7 @@ def test_mfma_pair_rejects(gpu):
         _run_tuned(gpu, x, p, s, MFMA_PAIR, 40, 8, 5, 1)  # whole rows of 40 pairs
 
 
-@pytest.mark.parametrize("depth", [2, 3, 4])
+@pytest.mark.parametrize("depth", [2, 3, 4, 6])
 @pytest.mark.parametrize("m", [2, 3, 5, 8])
 @pytest.mark.parametrize("k,n", [(128, 7), (384, 100), (2048, 2048), (5632, 33), (8192, 40), (9216, 9)])
 def test_pair_stream_variants(gpu, depth, m, k, n):
