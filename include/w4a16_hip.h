@@ -142,9 +142,9 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     3..8|10|12|14|16);
  *     staged activations, biases and reduction within 160 KiB of LDS.
  *   W4A16_KERNEL_STREAM (M = 1, K <= 32768): rows = output rows per
- *     wavefront task (2|4 with unroll 2|3|4, 8 with unroll 2), splits =
+ *     wavefront task (1|2|4 with unroll 2|3|4, 8 with unroll 2), splits =
  *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
- *     (at most ceil(K / 2048)),
+ *     (the ring runs on into the next rows when a row has fewer steps),
  *     max_blocks = grid (0 = the workgroups resident on the device at once).
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8

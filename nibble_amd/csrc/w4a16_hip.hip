@@ -289,8 +289,6 @@ Plan plan_stream(int64_t N, int64_t K) {
     p.rows = longest ? 4 : 2;
     p.splits = longest ? 4 : 8;
     p.unroll = longest ? 2 : 3;
-    const int64_t steps = (K / 32 + 63) / 64;   // 1 KiB loads per row
-    if (p.unroll > steps) p.unroll = (int)steps;
     p.max_blocks = 0;
     (void)N;
     return p;
@@ -298,7 +296,7 @@ Plan plan_stream(int64_t N, int64_t K) {
 
 bool stream_fits(int64_t K) {
     const Plan p = plan_stream(0, K);
-    return K % 128 == 0 && p.unroll >= 2 &&
+    return K % 128 == 0 && K > 0 &&
            w4a16_internal::stream_instantiated(p.rows, p.splits, p.unroll, K) &&
            w4a16_internal::stream_lds_bytes(K) <= kMaxLdsBytes;
 }

@@ -23,7 +23,10 @@
 // requested (the loop's tail is peeled), and a wavefront with no task
 // requests its first D steps on the grid's last task, computes nothing and
 // stores nothing. Branches around loads would make the compiler wait for
-// every outstanding load at the join.
+// every outstanding load at the join. Rows shorter than D steps are fine:
+// the ring simply holds steps of the next task (the first D requests may run
+// past a wavefront's last task; their rows are clamped to N - 1 and their
+// data is not used).
 #pragma once
 
 #include "w4a16_device.h"
@@ -153,6 +156,12 @@ gemv_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
         }
     };
 
+    if (units < D) {   // fewer steps than the ring holds (short rows, one task)
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (d < units) compute(ring[d]);
+        return;
+    }
     // 4. full rounds: every slot is refilled with a step that exists
     int u = 0;
     for (; u + 2 * D <= units; u += D) {
@@ -163,7 +172,7 @@ gemv_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
             if (++ls == steps) { ls = 0; lt += stride; }
         }
     }
-    // 5. the last D .. 2 D - 1 steps (units >= steps >= D)
+    // 5. the last D .. 2 D - 1 steps
 #pragma unroll
     for (int d = 0; d < D; ++d) {
         compute(ring[d]);

@@ -28,7 +28,7 @@ int fail(int code, const std::string& message) {
 
 using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int);
 
-// Instantiated shapes: R in {2, 4} rows per task with D in {2, 3, 4} steps
+// Instantiated shapes: R in {1, 2, 4} rows per task with D in {2, 3, 4} steps
 // in flight, or R = 8 with D = 2 (deeper rings of 8 rows spill), W in {4, 8}
 // wavefronts per workgroup; the activation units per thread cover K <= 16384
 // (half) or K <= 32768 (full).
@@ -38,6 +38,7 @@ Kern pick_w(int rows, int depth, bool full) {
     constexpr int kHalf = 32 / W, kFull = 64 / W;
 #define W4A16_S(R, D)                                                                                         \
     if (rows == R && depth == D) return full ? gemv_stream<R, D, W, kFull> : gemv_stream<R, D, W, kHalf>;
+    W4A16_S(1, 2) W4A16_S(1, 3) W4A16_S(1, 4)
     W4A16_S(2, 2) W4A16_S(2, 3) W4A16_S(2, 4)
     W4A16_S(4, 2) W4A16_S(4, 3) W4A16_S(4, 4)
     W4A16_S(8, 2)
@@ -102,11 +103,8 @@ int launch_stream(int rows, int waves, int depth, int max_blocks, const void* x,
         return fail(W4A16_ERR_CONFIG, "streaming kernel: K must be a multiple of 128 up to 32768");
     const Kern kern = pick(rows, waves, depth, K);
     if (kern == nullptr)
-        return fail(W4A16_ERR_CONFIG, "streaming kernel: rows 2 or 4 with unroll (steps in flight) 2, 3 or 4, or "
+        return fail(W4A16_ERR_CONFIG, "streaming kernel: rows 1, 2 or 4 with unroll (steps in flight) 2, 3 or 4, or "
                                       "rows 8 with unroll 2; splits (wavefronts) 4 or 8");
-    const int steps = (K / 32 + 63) / 64;
-    if (steps < depth)
-        return fail(W4A16_ERR_CONFIG, "streaming kernel: unroll (steps in flight) exceeds the row's K / 2048 steps");
     const int lds = (int)stream_lds_bytes(K);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "streaming kernel: activations do not fit in LDS");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);

@@ -199,7 +199,7 @@ def test_stream_env_selector(monkeypatch):
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     monkeypatch.setenv("W4A16_DECODE", "stream")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 4096, 128)["kernel"] == "stream"     # any N
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "oneshot"    # one step per row
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "stream"     # rows shorter than the ring
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 64, 4096, 128)["kernel"] == "oneshot"    # M > 1
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 34816, 128)["kernel"] == "valu"      # rows too long
 

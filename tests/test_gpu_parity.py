@@ -345,14 +345,18 @@ def test_gemm_rejects(gpu):
     assert not out.any()
 
 
-STREAM_SHAPES = [(2, 4, 2), (2, 8, 4), (4, 4, 3), (4, 8, 2), (4, 4, 4), (8, 4, 2), (8, 8, 2), (2, 4, 3)]
+STREAM_SHAPES = [(2, 4, 2), (2, 8, 4), (4, 4, 3), (4, 8, 2), (4, 4, 4), (8, 4, 2), (8, 8, 2), (2, 4, 3),
+                 (1, 4, 2), (1, 8, 4), (1, 8, 3)]
 
 
 @pytest.mark.parametrize("rows,waves,depth", STREAM_SHAPES)
-@pytest.mark.parametrize("k,n", [(8192, 7), (16384, 40), (16512, 9), (18432, 33), (28672, 21), (32768, 5)])
+@pytest.mark.parametrize("k,n", [(128, 3), (2048, 7), (2176, 100), (8192, 7), (16384, 40), (16512, 9), (18432, 33),
+                                 (28672, 21), (32768, 5)])
 def test_stream_variants(gpu, rows, waves, depth, k, n):
-    """Streaming kernel (M = 1): every instantiated shape on short and ragged
-    rows (16512 = 8 full steps + 4 chunks), both activation-unit counts
+    """Streaming kernel (M = 1): every instantiated shape on ragged rows
+    (2176 = 1 step + 4 chunks, 16512 = 8 steps + 4 chunks), rows of fewer
+    steps than the ring (128, 2048: the ring runs into the next rows, and
+    wavefronts with fewer steps than the ring), both activation-unit counts
     (K <= 16384 and above) and N not a multiple of the rows per task."""
     x, p, s = make_case(1, k, n, seed=k + n + rows)
     got = _run_tuned(gpu, x, p, s, STREAM, rows, waves, depth)
@@ -360,7 +364,7 @@ def test_stream_variants(gpu, rows, waves, depth, k, n):
 
 
 @pytest.mark.parametrize("rows,waves,depth,cap", [(4, 4, 3, 1), (2, 8, 4, 3), (8, 4, 2, 2), (4, 8, 2, 5)])
-@pytest.mark.parametrize("k,n", [(8192, 203), (16512, 77)])
+@pytest.mark.parametrize("k,n", [(2048, 203), (8192, 203), (16512, 77)])
 def test_stream_many_tasks_per_wavefront(gpu, rows, waves, depth, cap, k, n):
     """A small grid cap gives each wavefront many tasks, so the ring of
     in-flight steps crosses from one task's rows to the next (and the
@@ -383,8 +387,8 @@ def test_stream_rejects(gpu):
     with pytest.raises(_lib.W4A16Error, match="M == 1"):
         _lib.linear_f16_tuned(xd, pd, sd, out, 128, STREAM, 4, 4, 2, 0)
     out1 = torch.zeros((1, 16), dtype=torch.float16, device=gpu)
-    with pytest.raises(_lib.W4A16Error, match="exceeds"):   # 4096 = 2 steps of 1 KiB per row
-        _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 4, 4, 3, 0)
+    with pytest.raises(_lib.W4A16Error, match="rows 1, 2 or 4"):
+        _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 3, 4, 3, 0)
     with pytest.raises(_lib.W4A16Error, match="rows 8 with unroll 2"):
         _lib.linear_f16_tuned(xd[:1], pd, sd, out1, 128, STREAM, 8, 4, 3, 0)
     with pytest.raises(_lib.W4A16Error, match="splits"):
