@@ -175,8 +175,8 @@ int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t 
  * 32] fp32) on q and k rounded to fp16; k and v appended to the caches; query t
  * attends to slots 0 .. start + t (slots below start read from the caches):
  * output[t] = softmax(q k^T / 8) v, [tokens, num_heads * 64] fp16.
- * Needs head_dim 64, tokens <= 64, start + tokens <= min(max_seq_len, 256),
- * 16-byte aligned caches.
+ * Needs head_dim 64, start + tokens <= min(max_seq_len, 256), 16-byte
+ * aligned caches. One workgroup per query head and block of 4 tokens.
  */
 int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
                                 const float* sin_table, int64_t start, int64_t tokens, void* output,

@@ -619,34 +619,40 @@ silu_mul_kernel(const f16* __restrict__ gate_up, f16* __restrict__ out, int rows
     out[i] = (f16)((float)sg * u);
 }
 
-// Prefill attention of T new tokens at cache slots start .. start + T - 1,
-// one workgroup of 4 wavefronts per query head. qkv rows (stride
-// (num_heads + 2 num_kv) * 64) hold [q | k | v] as the decode step's; q and
-// k get the rotary embedding of their slot in fp32, rounded to fp16; the
-// workgroup of the group's first query head appends k and v to the caches.
-// Attention: query t sees slots 0 .. start + t (slots below start from the
-// caches), softmax(q k^T / 8) v in fp32 with an online softmax over 64-slot
-// chunks, one query per wavefront at a time; output [T, num_heads * 64] fp16.
-// LDS: q [T][64] fp32, k and v [start + T][kRow] fp16 (rows padded to 72
+// Prefill attention of T new tokens at cache slots start .. start + T - 1.
+// Workgroup (hq, b) of 4 wavefronts takes query head hq and the 4 queries
+// t = 4 b .. 4 b + 3, one per wavefront, so a prompt runs on num_heads *
+// ceil(T / 4) workgroups. qkv rows (stride (num_heads + 2 num_kv) * 64) hold
+// [q | k | v] as the decode step's; q and k get the rotary embedding of their
+// slot in fp32, rounded to fp16; workgroup (hq, 0) of the group's first query
+// head appends all T new k and v rows to the caches. Attention: query t sees
+// slots 0 .. start + t (slots below start from the caches), softmax(q k^T / 8)
+// v in fp32 with an online softmax over 64-slot chunks; output [T,
+// num_heads * 64] fp16. A workgroup stages only the slots its last query
+// sees. LDS: q [4][64] fp32, k and v [slots][kRow] fp16 (rows padded to 72
 // halves, so a wavefront reading 64 rows spreads over the banks).
 constexpr int kPrefillRow = 72;
-constexpr int kPrefillMaxSlots = 256;   // start + tokens: 90 KiB of LDS at 64 tokens
+constexpr int kPrefillMaxSlots = 256;   // start + tokens: 73 KiB of LDS at 256 slots
+constexpr int kPrefillQueries = 4;      // queries per workgroup, one per wavefront
 
 __global__ void __launch_bounds__(256)
 prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
                          const float* __restrict__ cos_table, const float* __restrict__ sin_table, int start,
                          int T, f16* __restrict__ out, int num_heads, int num_kv, int S) {
     constexpr int D = 64;
+    constexpr int QB = kPrefillQueries;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int NK = start + T;
-    float* qs = reinterpret_cast<float*>(smem);                            // [T][64]
-    f16* ks = reinterpret_cast<f16*>(smem + (size_t)T * D * 4);          // [NK][kPrefillRow]
+    const int t0 = blockIdx.y * QB;
+    const int tq = min(QB, T - t0);          // queries of this workgroup
+    const int NK = start + t0 + tq;          // slots its last query sees
+    float* qs = reinterpret_cast<float*>(smem);                            // [QB][64]
+    f16* ks = reinterpret_cast<f16*>(smem + (size_t)QB * D * 4);         // [NK][kPrefillRow]
     f16* vs = ks + (size_t)NK * kPrefillRow;                               // [NK][kPrefillRow]
     __shared__ __align__(16) float probs[4][64];
     const int hq = blockIdx.x;
     const int group = num_heads / num_kv;
     const int hk = hq / group;
-    const bool writer = hq % group == 0;
+    const bool writer = hq % group == 0 && blockIdx.y == 0;
     const int row_stride = (num_heads + 2 * num_kv) * D;
 
     // earlier slots from the caches (16 bytes per thread and step)
@@ -656,24 +662,29 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
         reinterpret_cast<u32x4*>(ks + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(k_cache + g)[c];
         reinterpret_cast<u32x4*>(vs + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(v_cache + g)[c];
     }
-    // the new tokens: rotary q and k, v as is
-    for (int i = threadIdx.x; i < T * D; i += 256) {
+    // the new tokens this workgroup sees (the writer: all T): rotary k, v as
+    // is; rotary q of its own queries
+    const int tk = writer ? T : t0 + tq;
+    for (int i = threadIdx.x; i < tk * D; i += 256) {
         const int t = i / D, d = i - t * D;
         const int slot = start + t;
         const f16* row = qkv + (size_t)t * row_stride;
         const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
         const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
-        const f16* q = row + (size_t)hq * D;
         const f16* k = row + (size_t)num_heads * D + (size_t)hk * D;
         const f16* v = row + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
-        const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
         const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
-        const f16 qr = (f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
         const f16 kr = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
         const f16 vv = v[d];
-        qs[t * D + d] = (float)qr;
-        ks[slot * kPrefillRow + d] = kr;
-        vs[slot * kPrefillRow + d] = vv;
+        if (slot < NK) {
+            ks[slot * kPrefillRow + d] = kr;
+            vs[slot * kPrefillRow + d] = vv;
+        }
+        if (t >= t0 && t < t0 + tq) {
+            const f16* q = row + (size_t)hq * D;
+            const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
+            qs[(t - t0) * D + d] = (float)(f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
+        }
         if (writer) {
             k_cache[((size_t)hk * S + slot) * D + d] = kr;
             v_cache[((size_t)hk * S + slot) * D + d] = vv;
@@ -683,9 +694,10 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float* my_probs = probs[wave];
-    for (int t = wave; t < T; t += 4) {
+    if (wave < tq) {
+        const int t = t0 + wave;
         const int last = start + t;   // highest visible slot
-        const float* qrow = qs + t * D;
+        const float* qrow = qs + wave * D;
         float run_max = -__builtin_inff(), run_sum = 0.0f, acc = 0.0f;
         for (int c0 = 0; c0 <= last; c0 += 64) {
             const int slot = c0 + lane;
@@ -892,20 +904,19 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "prefill attention: head_dim must be 64");
     if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
         return fail(W4A16_ERR_SHAPE, "prefill attention: num_heads must be a positive multiple of num_kv_heads");
-    if (tokens < 0 || tokens > 64 || start < 0 || start + tokens > w4a16::kPrefillMaxSlots ||
-        start + tokens > max_seq_len)
-        return fail(W4A16_ERR_SHAPE,
-                    "prefill attention: needs 0 <= tokens <= 64 and start + tokens <= min(max_seq_len, 256)");
+    if (tokens < 0 || start < 0 || start + tokens > w4a16::kPrefillMaxSlots || start + tokens > max_seq_len)
+        return fail(W4A16_ERR_SHAPE, "prefill attention: needs 0 <= tokens and start + tokens <= min(max_seq_len, 256)");
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(qkv, 2) || !aligned(output, 2))
         return fail(W4A16_ERR_ALIGNMENT, "prefill attention: caches must be 16-byte aligned, qkv and output 2-byte");
-    const int nk = (int)(start + tokens);
-    const size_t lds = (size_t)tokens * 64 * 4 + (size_t)2 * nk * w4a16::kPrefillRow * 2;
+    const int nk = (int)(start + tokens);   // slots the last query block sees
+    const size_t lds = (size_t)w4a16::kPrefillQueries * 64 * 4 + (size_t)2 * nk * w4a16::kPrefillRow * 2;
     const void* kern = reinterpret_cast<const void*>(w4a16::prefill_attention_kernel);
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
     }
-    hipLaunchKernelGGL(w4a16::prefill_attention_kernel, dim3((unsigned)num_heads), dim3(256), lds,
+    const unsigned blocks = (unsigned)((tokens + w4a16::kPrefillQueries - 1) / w4a16::kPrefillQueries);
+    hipLaunchKernelGGL(w4a16::prefill_attention_kernel, dim3((unsigned)num_heads, blocks), dim3(256), lds,
                        static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
                        static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
                        (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads,

@@ -26,7 +26,7 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill of a prompt of up to 64 tokens runs the W4A16 op itself for every
+Prefill of a prompt of up to 256 tokens runs the W4A16 op itself for every
 projection (q|k|v and gate|up as one op each; up to 16 tokens the op takes
 its one-shot MFMA kernel where the activations fit that kernel's LDS and the
 paired MFMA kernel over two halves of the rows elsewhere, as for the
@@ -52,8 +52,8 @@ from nibble_amd.linear import QuantizedLinear
 from nibble_amd.quantization import quantize_and_pack_weights
 
 # Longest prompt the fused prefill takes (w4a16_prefill_attention_f16 holds
-# at most 64 new tokens).
-FUSED_PREFILL_MAX_TOKENS = 64
+# at most 256 cache slots in LDS).
+FUSED_PREFILL_MAX_TOKENS = 256
 # Most rows a prefill projection sends to the W4A16 op in the torch-op
 # prefill; more rows take dequantize + hipBLASLt. Measured on the 1.1B and 8B
 # layer shapes: the op's GEMM is 1.2-3x faster than dequantize + hipBLASLt
@@ -251,7 +251,7 @@ class LlamaDecoder(torch.nn.Module):
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
-        self.fuse_prefill = True   # prompts of <= 64 tokens: fused prefill (see fused_prefill)
+        self.fuse_prefill = True   # prompts of <= 256 tokens: fused prefill (see fused_prefill)
         self.prefill_tokens: torch.Tensor | None = None
         self.prefill_positions: torch.Tensor | None = None
         # fused-step weights (views keep the per-module state-dict entries) and work buffers

@@ -88,7 +88,8 @@ def _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv):
 
 
 @pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
-@pytest.mark.parametrize("tokens,start", [(1, 0), (5, 0), (16, 0), (64, 0), (16, 7), (64, 192)])
+@pytest.mark.parametrize("tokens,start", [(1, 0), (5, 0), (16, 0), (64, 0), (16, 7), (64, 192), (7, 3), (130, 0),
+                                          (256, 0), (100, 101)])
 def test_prefill_attention(gpu, heads, kv, tokens, start):
     S = 256
     gen = torch.Generator().manual_seed(tokens * 13 + start + heads)
@@ -116,16 +117,18 @@ def test_prefill_attention(gpu, heads, kv, tokens, start):
 
 
 def test_prefill_attention_rejects(gpu):
-    heads, kv, S = 8, 2, 64
+    heads, kv, S = 8, 2, 300
     kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
     vd = torch.zeros_like(kd)
     cos, sin = _tables(S)
     cos, sin = cos.to(gpu), sin.to(gpu)
-    for tokens, start in [(65, 0), (10, 60)]:
+    short_k = torch.zeros((kv, 64, 64), dtype=torch.float16, device=gpu)
+    for tokens, start, kc, vc in [(257, 0, kd, vd), (10, 250, kd, vd), (10, 60, short_k, short_k)]:
+        # past the 256 slots the launch holds in LDS, or past the caches' 64 slots
         qkv = torch.zeros((tokens, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
         out = torch.zeros((tokens, heads * 64), dtype=torch.float16, device=gpu)
         with pytest.raises(_lib.W4A16Error, match="tokens"):
-            _lib.prefill_attention_f16(qkv, kd, vd, cos, sin, start, out, heads, kv)
+            _lib.prefill_attention_f16(qkv, kc, vc, cos, sin, start, out, heads, kv)
     qkv = torch.zeros((4, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
     out = torch.zeros((4, heads * 64), dtype=torch.float16, device=gpu)
     with pytest.raises(_lib.W4A16Error, match="head_dim"):
@@ -142,7 +145,7 @@ def _small_cfg():
                        num_kv_heads=2, head_dim=64, max_seq_len=32)
 
 
-@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64])
+@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64, 130])
 def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     """The fused prefill (up to 16 tokens the one-shot / paired MFMA kernels,
     beyond that the GEMM) against the torch-op prefill of the same model and
@@ -152,7 +155,7 @@ def test_fused_prefill_matches_torch_prefill(gpu, tokens):
 
     from nibble_amd.llama import LlamaDecoder
 
-    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=64), device=gpu, seed=11)
+    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=160), device=gpu, seed=11)
     prompt = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(tokens)).to(gpu)
     assert model.fused_prefill(tokens)
     with torch.inference_mode():
