@@ -208,11 +208,11 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),
-        "prefill": "16-token prompt, one HIP graph: per layer RMSNorm, W4A16 op for q|k|v (one-shot MFMA kernel, "
-                   "M=16), rotary+KV append+causal attention, W4A16 op for o + residual add, RMSNorm, W4A16 op "
-                   "for gate|up, SiLU*up, W4A16 op for down (paired MFMA kernel over two 8-row halves, K=5632) + "
-                   "residual add; then RMSNorm+lm_head GEMV and argmax; prefill_eager_ms: the same prompt as "
-                   "eager torch ops around QuantizedLinear",
+        "prefill": "16-token prompt, one HIP graph: RMSNorm of the embeddings, then per layer W4A16 op for "
+                   "q|k|v (one-shot MFMA kernel, M=16), rotary+KV append+causal attention, W4A16 op for o, "
+                   "residual add+RMSNorm, W4A16 op for gate|up, SiLU*up, W4A16 op for down (paired MFMA kernel "
+                   "over two 8-row halves, K=5632), residual add+next RMSNorm; then lm_head GEMV and argmax; "
+                   "prefill_eager_ms: the same prompt as eager torch ops around QuantizedLinear",
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),
         "model": "random-init Llama 22L h2048 i5632 32q/4kv hd64 vocab32000, INT4 g128 on all 155 linears",

@@ -169,6 +169,17 @@ int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output
 int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t inter, void* stream);
 
 /*
+ * Residual add + RMSNorm over `rows` rows of `hidden` fp16 values (hidden <=
+ * 8192): x_out = fp16(x + delta) (an fp16 tensor add's rounding), output =
+ * RMSNorm(x_out) * weight as w4a16_rmsnorm_f16 computes it. x_out may be x.
+ * Replaces the prefill's "x + linear(a)" followed by the next RMSNorm
+ * (HF LlamaDecoderLayer's residual adds and post_attention_layernorm /
+ * the next layer's input_layernorm, scripts/generate.py:260-305).
+ */
+int w4a16_add_rmsnorm_f16(const void* x, const void* delta, const void* weight, float eps, void* x_out,
+                          void* output, int64_t rows, int64_t hidden, void* stream);
+
+/*
  * Attention of `tokens` new tokens at cache slots start .. start + tokens - 1:
  * qkv rows [q (num_heads x 64) | k (num_kv_heads x 64) | v] fp16 as for
  * w4a16_decode_attention_f16; rotary embedding (cos / sin tables [max_seq_len,

@@ -80,6 +80,7 @@ DECODE_SIGNATURES = {
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
     "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
+    "w4a16_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _vp]),
     "w4a16_prefill_attention_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                                    _i64, _vp]),
 }
@@ -277,6 +278,14 @@ def rmsnorm_f16(x, weight, eps: float, output, stream=None) -> None:
     rows, hidden = x.shape
     _raise_on(lib().w4a16_rmsnorm_f16(x.data_ptr(), weight.data_ptr(), float(eps), output.data_ptr(), rows, hidden,
                                       _stream_ptr(stream)))
+
+
+def add_rmsnorm_f16(x, delta, weight, eps: float, x_out, output, stream=None) -> None:
+    """``w4a16_add_rmsnorm_f16``: x_out <- x + delta, output <- RMSNorm(x_out) * weight
+    over the rows of x [rows, hidden] (x_out may be x)."""
+    rows, hidden = x.shape
+    _raise_on(lib().w4a16_add_rmsnorm_f16(x.data_ptr(), delta.data_ptr(), weight.data_ptr(), float(eps),
+                                          x_out.data_ptr(), output.data_ptr(), rows, hidden, _stream_ptr(stream)))
 
 
 def silu_mul_f16(gate_up, output, stream=None) -> None:

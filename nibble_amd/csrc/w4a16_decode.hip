@@ -606,6 +606,115 @@ rmsnorm_rows_kernel(const f16* __restrict__ x, const f16* __restrict__ w, float 
     for (int i = threadIdx.x; i < hidden; i += 256) orow[i] = (f16)(((float)xr[i] * inv) * (float)w[i]);
 }
 
+// Residual add + RMSNorm of rows of at most kAddNormMax elements, one
+// workgroup per row: s = fp16(fp32(x[r]) + fp32(delta[r])) (the rounding of
+// an fp16 tensor add) is written to x_out[r], and out[r] = fp16((fp32(s) *
+// inv) * fp32(w)) with inv = 1 / sqrt(mean(s^2) + eps). Every load of a
+// thread is issued before its first store (x_out may be x, so a store
+// would otherwise order the loads after it), and the row stays in registers
+// between the two passes.
+constexpr int kAddNormPer = 32;                  // elements per thread
+constexpr int kAddNormMax = 256 * kAddNormPer;   // 8192
+
+__global__ void __launch_bounds__(256)
+add_rmsnorm_rows_kernel(const f16* x, const f16* __restrict__ delta, const f16* __restrict__ w, float eps,
+                        f16* x_out, f16* __restrict__ out, int hidden) {
+    __shared__ float partial[4];
+    const size_t row = (size_t)blockIdx.x * hidden;
+    f16 xa[kAddNormPer], da[kAddNormPer];
+#pragma unroll
+    for (int j = 0; j < kAddNormPer; ++j) {
+        const int i = min((int)threadIdx.x + 256 * j, hidden - 1);
+        xa[j] = x[row + i];
+        da[j] = delta[row + i];
+    }
+    float v[kAddNormPer];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kAddNormPer; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        const f16 sum = (f16)((float)xa[j] + (float)da[j]);
+        const float sv = i < hidden ? (float)sum : 0.0f;
+        if (i < hidden) x_out[row + i] = sum;
+        v[j] = sv;
+        ss = __builtin_fmaf(sv, sv, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)hidden + eps);
+#pragma unroll
+    for (int j = 0; j < kAddNormPer; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < hidden) out[row + i] = (f16)((v[j] * inv) * (float)w[i]);
+    }
+}
+
+// The same two launches on 16-byte units (rows a multiple of 8 elements, at
+// most kAddNormMax, every buffer 16-byte aligned): thread t holds units t,
+// t + 256, ... of its row, all requested before any store. ADD = false is
+// the plain RMSNorm (x_out, delta unused).
+constexpr int kNormUnits = kAddNormMax / 8 / 256;   // 16-byte units per thread (4)
+
+template <bool ADD>
+__global__ void __launch_bounds__(256)
+norm_rows_vec_kernel(const f16* x, const f16* __restrict__ delta, const f16* __restrict__ w, float eps,
+                     f16* x_out, f16* __restrict__ out, int hidden) {
+    __shared__ float partial[4];
+    const size_t row = (size_t)blockIdx.x * hidden;
+    const int units = hidden >> 3;
+    u32x4 xv[kNormUnits], dv[kNormUnits], wv[kNormUnits];
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = min((int)threadIdx.x + 256 * u, units - 1);
+        xv[u] = *reinterpret_cast<const u32x4*>(x + row + (size_t)i * 8);
+        if (ADD) dv[u] = *reinterpret_cast<const u32x4*>(delta + row + (size_t)i * 8);
+        wv[u] = *reinterpret_cast<const u32x4*>(w + (size_t)i * 8);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (ADD) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 a = as_f16x2(xv[u][e]), b = as_f16x2(dv[u][e]);
+                const f16x2 sum = {(f16)((float)a.x + (float)b.x), (f16)((float)a.y + (float)b.y)};
+                xv[u][e] = as_u32(sum);
+            }
+            if (i < units) *reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8) = xv[u];
+        }
+        if (i < units) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 a = as_f16x2(xv[u][e]);
+                ss = __builtin_fmaf((float)a.x, (float)a.x, ss);
+                ss = __builtin_fmaf((float)a.y, (float)a.y, ss);
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)hidden + eps);
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < units) {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 a = as_f16x2(xv[u][e]), g = as_f16x2(wv[u][e]);
+                const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
+                o[e] = as_u32(y);
+            }
+            *reinterpret_cast<u32x4*>(out + row + (size_t)i * 8) = o;
+        }
+    }
+}
+
 // out[r, i] = fp16(fp16(silu(g)) * u), g = gate_up[r, i], u = gate_up[r, inter + i]:
 // the roundings of torch's silu(g) * u on fp16 tensors.
 __global__ void __launch_bounds__(256)
@@ -874,9 +983,43 @@ int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output
     if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "rmsnorm: eps must be non-negative");
     if (!aligned(x, 2) || !aligned(weight, 2) || !aligned(output, 2))
         return fail(W4A16_ERR_ALIGNMENT, "rmsnorm: fp16 buffers must be 2-byte aligned");
+    using w4a16::f16;
+    if (hidden % 8 == 0 && hidden <= w4a16::kAddNormMax && aligned(x, 16) && aligned(weight, 16) &&
+        aligned(output, 16)) {
+        hipLaunchKernelGGL(w4a16::norm_rows_vec_kernel<false>, dim3((unsigned)rows), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const f16*>(x), nullptr,
+                           static_cast<const f16*>(weight), eps, nullptr, static_cast<f16*>(output), (int)hidden);
+        return check_launch();
+    }
     hipLaunchKernelGGL(w4a16::rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(x),
-                       static_cast<const w4a16::f16*>(weight), eps, static_cast<w4a16::f16*>(output), (int)hidden);
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(x), static_cast<const f16*>(weight),
+                       eps, static_cast<f16*>(output), (int)hidden);
+    return check_launch();
+}
+
+int w4a16_add_rmsnorm_f16(const void* x, const void* delta, const void* weight, float eps, void* x_out,
+                          void* output, int64_t rows, int64_t hidden, void* stream) {
+    if (rows == 0) return W4A16_OK;
+    if (!x || !delta || !weight || !x_out || !output)
+        return fail(W4A16_ERR_NULL, "add_rmsnorm: every pointer must be non-NULL");
+    if (rows < 0 || rows > INT32_MAX || hidden <= 0 || hidden > w4a16::kAddNormMax)
+        return fail(W4A16_ERR_SHAPE, "add_rmsnorm: rows must be non-negative and 0 < hidden <= 8192");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "add_rmsnorm: eps must be non-negative");
+    if (!aligned(x, 2) || !aligned(delta, 2) || !aligned(weight, 2) || !aligned(x_out, 2) || !aligned(output, 2))
+        return fail(W4A16_ERR_ALIGNMENT, "add_rmsnorm: fp16 buffers must be 2-byte aligned");
+    using w4a16::f16;
+    if (hidden % 8 == 0 && aligned(x, 16) && aligned(delta, 16) && aligned(weight, 16) && aligned(x_out, 16) &&
+        aligned(output, 16)) {
+        hipLaunchKernelGGL(w4a16::norm_rows_vec_kernel<true>, dim3((unsigned)rows), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const f16*>(x), static_cast<const f16*>(delta),
+                           static_cast<const f16*>(weight), eps, static_cast<f16*>(x_out), static_cast<f16*>(output),
+                           (int)hidden);
+        return check_launch();
+    }
+    hipLaunchKernelGGL(w4a16::add_rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(x), static_cast<const f16*>(delta),
+                       static_cast<const f16*>(weight), eps, static_cast<f16*>(x_out), static_cast<f16*>(output),
+                       (int)hidden);
     return check_launch();
 }
 

@@ -304,10 +304,13 @@ class LlamaDecoder(torch.nn.Module):
 
     def _prefill_fused(self, prompt: torch.Tensor) -> None:
         """The prompt (cache slots 0 .. T-1) with the decode step's roundings:
-        per layer RMSNorm, q|k|v op, rotary + KV append + causal attention, o
-        op + residual, RMSNorm, gate|up op, SiLU * up, down op + residual; then
-        RMSNorm + lm_head GEMV and the greedy argmax, which also gathers the
-        first decode step's input row."""
+        RMSNorm of the embeddings, then per layer the q|k|v op, rotary + KV
+        append + causal attention, the o op, residual add + RMSNorm, the
+        gate|up op, SiLU * up, the down op and residual add + the next RMSNorm
+        (the next layer's input norm, or the final norm after the last layer);
+        then the lm_head GEMV on the last normed row and the greedy argmax,
+        which also gathers the first decode step's input row. 8 launches per
+        layer."""
         cfg = self.cfg
         t = prompt.numel()
         g = cfg.group_size
@@ -315,20 +318,22 @@ class LlamaDecoder(torch.nn.Module):
         h = torch.empty_like(x)
         attn = torch.empty((t, cfg.num_heads * cfg.head_dim), dtype=torch.float16, device=x.device)
         mlp = torch.empty((t, cfg.intermediate_size), dtype=torch.float16, device=x.device)
+        first = self.layers[0].input_norm
+        _lib.rmsnorm_f16(x, first.weight, first.eps, h)
         for i, b in enumerate(self.layers):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
-            _lib.rmsnorm_f16(x, b.input_norm.weight, b.input_norm.eps, h)
             qkv = torch.ops.w4a16.linear(h, qkv_w, qkv_s, g)
             _lib.prefill_attention_f16(qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, attn,
                                        cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
-            x = x + torch.ops.w4a16.linear(attn, b.o_proj.packed_weights, b.o_proj.scales, g)
-            _lib.rmsnorm_f16(x, b.post_norm.weight, b.post_norm.eps, h)
+            o = torch.ops.w4a16.linear(attn, b.o_proj.packed_weights, b.o_proj.scales, g)
+            _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
             gu = torch.ops.w4a16.linear(h, gu_w, gu_s, g)
             _lib.silu_mul_f16(gu, mlp)
-            x = x + torch.ops.w4a16.linear(mlp, b.down_proj.packed_weights, b.down_proj.scales, g)
-        _lib.gemv_fused_f16(x[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits,
-                            norm_weight=self.norm.weight, eps=self.norm.eps)
+            d = torch.ops.w4a16.linear(mlp, b.down_proj.packed_weights, b.down_proj.scales, g)
+            nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.norm
+            _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
+        _lib.gemv_fused_f16(h[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits)
         _lib.argmax_embed_f16(self.logits, self.token, None, self.embed, self.x_buf)
         self.position.fill_(t)
 

@@ -45,6 +45,47 @@ def test_rmsnorm_rows(gpu, rows, hidden):
     assert torch.all((got - ref).abs() <= ULP * ref.abs() + 2 ** -24), float((got - ref).abs().max())
 
 
+@pytest.mark.parametrize("rows,hidden,alias", [(1, 2048, True), (64, 2048, True), (7, 5632, False), (3, 100, False),
+                                              (2, 8192, True)])
+def test_add_rmsnorm_rows(gpu, rows, hidden, alias):
+    """x_out = x + delta with the rounding of an fp16 tensor add (bit-exact
+    against torch), output = RMSNorm(x_out) * w within one fp16 rounding of
+    float64; x_out may be x itself."""
+    gen = torch.Generator().manual_seed(rows * 3 + hidden)
+    x = (3.0 * torch.randn((rows, hidden), generator=gen)).to(torch.float16)
+    d = (2.0 * torch.randn((rows, hidden), generator=gen)).to(torch.float16)
+    w = (1.0 + 0.5 * torch.randn((hidden,), generator=gen)).to(torch.float16)
+    eps = 1e-5
+    s_ref = (x.float() + d.float()).to(torch.float16)
+    sd = s_ref.double()
+    ref = (sd * torch.rsqrt(sd.pow(2).mean(dim=-1, keepdim=True) + eps)) * w.double()
+    xd, dd = x.to(gpu), d.to(gpu)
+    x_out = xd if alias else torch.full_like(xd, float("nan"))
+    out = torch.full((rows, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] add_rmsnorm rows={rows} hidden={hidden} alias={alias}", flush=True)
+    _lib.add_rmsnorm_f16(xd, dd, w.to(gpu), eps, x_out, out)
+    torch.cuda.synchronize()
+    assert torch.equal(x_out.cpu(), s_ref)
+    got = out.double().cpu()
+    assert torch.all((got - ref).abs() <= ULP * ref.abs() + 2 ** -24), float((got - ref).abs().max())
+    # w4a16_rmsnorm_f16 on the sum agrees to one fp16 rounding (measured: 7
+    # of 131072 outputs one ulp apart at 64 x 2048; the two launches' fp32
+    # normalisers can differ in the last bit)
+    plain = torch.empty_like(out)
+    _lib.rmsnorm_f16(s_ref.to(gpu), w.to(gpu), eps, plain)
+    torch.cuda.synchronize()
+    pf = plain.double().cpu()
+    assert torch.all((pf - got).abs() <= ULP * pf.abs()), float((pf - got).abs().max())
+
+
+def test_add_rmsnorm_rejects(gpu):
+    x = torch.zeros((2, 8200), dtype=torch.float16, device=gpu)
+    w = torch.ones((8200,), dtype=torch.float16, device=gpu)
+    out = torch.zeros_like(x)
+    with pytest.raises(_lib.W4A16Error, match="8192"):
+        _lib.add_rmsnorm_f16(x, x, w, 1e-5, x, out)
+
+
 @pytest.mark.parametrize("rows,inter", [(1, 5632), (16, 5632), (5, 77)])
 def test_silu_mul(gpu, rows, inter):
     gen = torch.Generator().manual_seed(rows + inter)
