@@ -46,6 +46,7 @@ extern "C" {
 #define W4A16_KERNEL_STREAM 9        /* VALU GEMV, resident workgroups streaming rows along K (M = 1, K <= 32768) */
 #define W4A16_KERNEL_GEMM 10         /* fp16 MFMA GEMM on weights decoded in registers (M > 16, prompts) */
 #define W4A16_KERNEL_PAIR_STREAM 11  /* paired MFMA, resident workgroups streaming 8-row blocks (2 <= M <= 8) */
+#define W4A16_KERNEL_GEMM_LDS 12     /* GEMM with the activation block staged in LDS per round of groups (large M) */
 
 /*
  * Fused W4A16 linear layer.
@@ -155,6 +156,11 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     activation tiles per wavefront (1|2|4), max_blocks = 16-row weight
  *     tiles per wavefront (1|2|4), splits = wavefronts splitting K (2|4|8;
  *     not 8 with rows = max_blocks = 4), unroll ignored.
+ *   W4A16_KERNEL_GEMM_LDS (any M; every operand below 4 GiB): rows = 16-row
+ *     activation tiles per wavefront (2|4), max_blocks = 16-row weight tiles
+ *     per wavefront (2|4), unroll = wavefronts sharing each staged round on
+ *     different weight tiles (2|4), splits = wavefronts splitting K (1|2|4;
+ *     4 needs unroll 2 and rows * max_blocks < 16, or rows * max_blocks < 8).
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

@@ -37,11 +37,13 @@ KERNEL_MFMA_PAIR = 8
 KERNEL_STREAM = 9
 KERNEL_GEMM = 10
 KERNEL_PAIR_STREAM = 11
+KERNEL_GEMM_LDS = 12
 KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic",
                 KERNEL_DIAG: "diag", KERNEL_VALU_OFFSET: "valu_offset",
                 KERNEL_ONESHOT: "oneshot", KERNEL_MFMA_ONESHOT: "mfma_oneshot",
                 KERNEL_MFMA_PAIR: "mfma_pair", KERNEL_STREAM: "stream",
-                KERNEL_GEMM: "gemm", KERNEL_PAIR_STREAM: "pair_stream"}
+                KERNEL_GEMM: "gemm", KERNEL_PAIR_STREAM: "pair_stream",
+                KERNEL_GEMM_LDS: "gemm_lds"}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

@@ -196,3 +196,210 @@ gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* 
 }
 
 }  // namespace w4a16
+
+namespace w4a16 {
+
+// ---------------------------------------------------------------------------
+// W4A16 GEMM with the activation block staged in LDS (large M).
+//
+// gemm_w4a16 above reads each wavefront's A fragments from memory, so every
+// workgroup of 16 RB weight rows re-reads its 16 MT activation rows over all
+// of K (at M = 256 on 4096 x 14336: 470 MB of L2 reads, about half of the
+// kernel's time). Here a workgroup of SN x SK wavefronts covers 16 RB SN
+// weight rows: wavefront (sn, sk) owns weight tiles sn * RB .. and the groups
+// g = sk, sk + SK, ...; round r stages groups r SK .. r SK + SK - 1 of the
+// workgroup's activation rows in LDS once (double-buffered, one barrier per
+// round, round r + 1 requested while round r is computed), and the SN
+// wavefronts of each sk read their A fragments from it. Weights come from a
+// ring of DB rounds in flight per wavefront (HBM latency is longer than one
+// round's MFMAs). The rounds run to a multiple of DB; groups past K are
+// staged as zeros and their weight loads clamped, so no load sits behind a
+// branch. Decode, tile layout, k order and the SK reduction are those of
+// gemm_w4a16; the grid mapping is the same with 16 RB SN weight rows per
+// block.
+//
+// LDS: two buffers of [SK][16 MT][kGemmRow] halves (rows of one group padded
+// from 128 to 136 halves: the 16 rows of a fragment read fall on distinct
+// banks); after the last round the same memory holds the SK reduction's
+// [SK - 1][SN][MT][RB][64] f32x4.
+// ---------------------------------------------------------------------------
+constexpr int kGemmRow = 136;
+constexpr int kGemmRing = 4;   // rounds of weights in flight per wavefront
+
+__host__ __device__ constexpr int64_t gemm2_lds_bytes(int mt, int rb, int sn, int sk) {
+    return (int64_t)2 * sk * 16 * mt * kGemmRow * 2 > (int64_t)(sk - 1) * sn * mt * rb * 64 * 16
+               ? (int64_t)2 * sk * 16 * mt * kGemmRow * 2
+               : (int64_t)(sk - 1) * sn * mt * rb * 64 * 16;
+}
+
+template <int MT, int RB, int SN, int SK>
+__global__ void __launch_bounds__(64 * SN * SK)
+gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+            f16* __restrict__ out, int M, int N, int K, int nblocks) {
+    constexpr int T = 64 * SN * SK;
+    constexpr int DB = kGemmRing;
+    constexpr int UNITS = SK * 16 * MT * 16;   // 16-byte units staged per round
+    static_assert(UNITS % T == 0, "whole staging units per thread");
+    constexpr int UPT = UNITS / T;
+    constexpr int BUF = SK * 16 * MT * kGemmRow;   // halves per staging buffer
+    const int b = blockIdx.x;
+    const int mblocks = (int)gridDim.x / ((nblocks + 7) & ~7);
+    const int s = b >> 3;
+    const int nbk = 8 * (s / mblocks) + (b & 7);
+    const int mbk = s % mblocks;
+    if (nbk >= nblocks) return;   // padding workgroup: whole workgroup, before any barrier
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16* as = reinterpret_cast<f16*>(smem);                                   // [2][SK][16 MT][kGemmRow]
+    f32x4* red = reinterpret_cast<f32x4*>(smem);   // [SK - 1][SN][MT][RB][64], after the last round
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, q = lane >> 4;
+    const int sk = wave % SK, sn = wave / SK;
+    const int G = K >> 7;
+    const int R = (G + SK - 1) / SK;
+    const int RP = (R + DB - 1) / DB * DB;   // rounds run, a multiple of the ring
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+    const int n0 = nbk * 16 * RB * SN + sn * 16 * RB;
+    const int m0 = mbk * 16 * MT;
+
+    // staging: unit u = (group gl, row, 16-byte part p) of the round
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(x);
+    auto stage_load = [&](u32x4 (&a)[UPT], int r) {
+#pragma unroll
+        for (int p = 0; p < UPT; ++p) {
+            const int u = threadIdx.x + p * T;
+            const int gl = u / (16 * MT * 16), rem = u % (16 * MT * 16);
+            const int row = rem >> 4, part = rem & 15;
+            const int g = min(r * SK + gl, G - 1);
+            const uint32_t m = (uint32_t)min(m0 + row, M - 1);
+            a[p] = *reinterpret_cast<const u32x4*>(xbase + (m * (uint32_t)K + (uint32_t)g * 128u + part * 8u) * 2u);
+        }
+    };
+    auto stage_put = [&](const u32x4 (&a)[UPT], int r, int buf) {
+#pragma unroll
+        for (int p = 0; p < UPT; ++p) {
+            const int u = threadIdx.x + p * T;
+            const int gl = u / (16 * MT * 16), rem = u % (16 * MT * 16);
+            const int row = rem >> 4, part = rem & 15;
+            const bool live = r * SK + gl < G;
+            *reinterpret_cast<u32x4*>(as + (size_t)buf * BUF + ((size_t)gl * 16 * MT + row) * kGemmRow + part * 8) =
+                live ? a[p] : (u32x4){0u, 0u, 0u, 0u};
+        }
+    };
+
+    // weights: ring slot d holds round r's group g = r SK + sk (clamped)
+    const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scales);
+    uint32_t wrow[RB], srow[RB];
+#pragma unroll
+    for (int t = 0; t < RB; ++t) {
+        const uint32_t n = (uint32_t)min(n0 + 16 * t + c, N - 1);
+        wrow[t] = n * row_bytes + 16u * q;
+        srow[t] = n * (uint32_t)G * 2u;
+    }
+    u32x4 wv[DB][RB];
+    uint32_t sv[DB][RB];
+    auto load_w = [&](int d, int r) {
+        const uint32_t g = (uint32_t)min(r * SK + sk, G - 1);
+#pragma unroll
+        for (int t = 0; t < RB; ++t) sv[d][t] = *reinterpret_cast<const uint16_t*>(sbase + srow[t] + g * 2u);
+#pragma unroll
+        for (int t = 0; t < RB; ++t) wv[d][t] = *reinterpret_cast<const u32x4*>(w + wrow[t] + g * 64u);
+    };
+
+    f32x4 acc[MT][RB];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[t][r] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+    const f16x2 off = {(f16)-1032.0f, (f16)-72.0f};
+    auto compute = [&](int d, int buf) {
+        const f16* ab = as + (size_t)buf * BUF + (size_t)sk * 16 * MT * kGemmRow;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            u32x4 af[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                af[t] = *reinterpret_cast<const u32x4*>(ab + (16 * t + c) * kGemmRow + 32 * q + 8 * st);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const f16 sc = __builtin_bit_cast(f16, (uint16_t)sv[d][r]);
+                const f16x2 sc2 = {sc, sc};
+                const uint32_t word = wv[d][r][st];
+                f16x2 pr[4];
+#pragma unroll
+                for (int by = 0; by < 4; ++by) {
+                    const uint32_t sel = (0x0Cu << 24) | ((uint32_t)by << 16) | (0x0Cu << 8) | (uint32_t)by;
+                    const uint32_t v = __builtin_amdgcn_bitop3_b32(perm(word, word, sel), 0x00F0000Fu, 0x64806408u,
+                                                                   0x6A);
+                    pr[by] = __builtin_elementwise_fma(as_f16x2(v), mul, off) * sc2;
+                }
+                const f16x8 bt = __builtin_bit_cast(
+                    f16x8, (u32x4){as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])});
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[t]), bt,
+                                                                       acc[t][r], 0, 0, 0);
+            }
+        }
+    };
+
+    // prologue: round 0 staged, the ring's first DB rounds requested
+    {
+        u32x4 a[UPT];
+        stage_load(a, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) load_w(d, d);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_put(a, 0, 0);
+    }
+    __syncthreads();
+    for (int r0 = 0; r0 < RP; r0 += DB) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const int r = r0 + d;
+            u32x4 a[UPT];
+            stage_load(a, r + 1);   // past the last round: clamped, staged as zeros, never read
+            compute(d, r & 1);
+            load_w(d, r + DB);
+            stage_put(a, r + 1, (r + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // SK partial tiles: wavefronts sk > 0 write, sk = 0 sums in order
+    if (SK > 1) {
+        if (sk > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < RB; ++r)
+                    red[((((sk - 1) * SN + sn) * MT + t) * RB + r) * 64 + lane] = acc[t][r];
+        }
+        __syncthreads();
+        if (sk > 0) return;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int k2 = 1; k2 < SK; ++k2) acc[t][r] += red[((((k2 - 1) * SN + sn) * MT + t) * RB + r) * 64 + lane];
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int n = n0 + 16 * r + c;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + 16 * t + 4 * q + e;
+                if (m < M && n < N) out[(size_t)m * N + n] = (f16)acc[t][r][e];
+            }
+        }
+    }
+}
+
+}  // namespace w4a16

@@ -91,4 +91,67 @@ int launch_gemm(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, 
     return W4A16_OK;
 }
 
+// LDS-staged GEMM (gemm2_w4a16): mt activation tiles and rb weight tiles per
+// wavefront, sn wavefronts on weight tiles sharing each staged round, sk
+// wavefronts splitting K. Instantiated: mt 2 or 4, rb 2 or 4, sn 2 or 4,
+// sk 1, 2 or 4, except sk = 4 with sn = 4 and mt * rb >= 8 or with mt = rb =
+// 4 (they spill).
+namespace {
+template <int MT, int RB, int SN>
+Kern pick2_sk(int sk) {
+    using namespace w4a16;
+    if (sk == 1) return gemm2_w4a16<MT, RB, SN, 1>;
+    if (sk == 2) return gemm2_w4a16<MT, RB, SN, 2>;
+    // 16 wavefronts with 8+ tiles each, or 8 with 16 tiles, spill
+    if constexpr (!((SN == 4 && MT * RB >= 8) || (MT * RB == 16))) {
+        if (sk == 4) return gemm2_w4a16<MT, RB, SN, 4>;
+    }
+    return nullptr;
+}
+template <int MT, int RB>
+Kern pick2_sn(int sn, int sk) {
+    if (sn == 2) return pick2_sk<MT, RB, 2>(sk);
+    if (sn == 4) return pick2_sk<MT, RB, 4>(sk);
+    return nullptr;
+}
+template <int MT>
+Kern pick2_rb(int rb, int sn, int sk) {
+    if (rb == 2) return pick2_sn<MT, 2>(sn, sk);
+    if (rb == 4) return pick2_sn<MT, 4>(sn, sk);
+    return nullptr;
+}
+Kern pick2(int mt, int rb, int sn, int sk) {
+    if (mt == 2) return pick2_rb<2>(rb, sn, sk);
+    if (mt == 4) return pick2_rb<4>(rb, sn, sk);
+    return nullptr;
+}
+}  // namespace
+
+bool gemm2_instantiated(int mt, int rb, int sn, int sk) { return pick2(mt, rb, sn, sk) != nullptr; }
+
+int launch_gemm2(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N,
+                 int K, hipStream_t stream) {
+    if (M < 1 || N < 1 || !gemm_fits(M, N, K))
+        return fail(W4A16_ERR_CONFIG, "LDS GEMM kernel: K must be a positive multiple of 128 and every operand below 4 GiB");
+    const Kern kern = pick2(mt, rb, sn, sk);
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, "LDS GEMM kernel: rows (activation tiles) 2 or 4, max_blocks (weight tiles) 2 or "
+                                      "4, unroll (wavefronts sharing the staging) 2 or 4, splits 1, 2 or 4 (splits 4 "
+                                      "needs unroll 2 and rows * max_blocks < 16, or rows * max_blocks < 8)");
+    const int64_t lds = w4a16::gemm2_lds_bytes(mt, rb, sn, sk);
+    if (lds > 160 * 1024) return fail(W4A16_ERR_CONFIG, "LDS GEMM kernel: staging exceeds LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int nblocks = (N + 16 * rb * sn - 1) / (16 * rb * sn);
+    const int mblocks = (M + 16 * mt - 1) / (16 * mt);
+    const int64_t grid = (int64_t)((nblocks + 7) & ~7) * mblocks;
+    if (grid > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "LDS GEMM kernel: too many workgroups");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * sn * sk), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, N, K, nblocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
 }  // namespace w4a16_internal

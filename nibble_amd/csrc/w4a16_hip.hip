@@ -40,6 +40,9 @@ bool gemm_instantiated(int mt, int rb, int sk);
 bool gemm_fits(int64_t M, int64_t N, int64_t K);
 int launch_gemm(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N, int K,
                 hipStream_t stream);
+bool gemm2_instantiated(int mt, int rb, int sn, int sk);
+int launch_gemm2(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N,
+                 int K, hipStream_t stream);
 }  // namespace w4a16_internal
 
 namespace {
@@ -336,6 +339,32 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
+// LDS-staged GEMM (w4a16_gemm.h, gemm2_w4a16) for M >= 128 where its shared
+// staging pays: measured at M = 256 against gemm_w4a16, 4096 x 14336 51.0
+// against 90.2 us, 2048 x 11264 28.7 against 38.2, 2048 x 5632 19.8 against
+// 25.6, 14336 x 4096 68.5 against 78.5; at M = 64 it loses on long rows (5632
+// x 2048: 20.4 against 10.3, its per-round barriers) and on narrow layers.
+// Plan fields: rows = MT, max_blocks = RB, unroll = SN wavefronts sharing the
+// staging, splits = SK. Shape: 4 activation tiles, 2 weight tiles; 4
+// wavefronts on weight tiles with no K split from N = 11264, else 2 with K
+// split 4 ways from K = 5632 (2 below).
+Plan plan_gemm_lds(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_GEMM_LDS;
+    p.rows = 4;
+    p.max_blocks = 2;
+    p.unroll = N >= 11264 ? 4 : 2;
+    p.splits = N >= 11264 ? 1 : (K >= 5632 ? 4 : 2);
+    (void)M;
+    return p;
+}
+
+bool gemm_lds_route(int64_t M, int64_t N, int64_t K) {
+    const Plan p = plan_gemm_lds(M, N, K);
+    return M >= 128 && (K <= 4096 || N >= 4096) && w4a16_internal::gemm_fits(M, N, K) &&
+           w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits);
+}
+
 // Largest M the dispatcher sends to the GEMM kernel.
 constexpr int64_t kGemmMaxM = 1 << 20;
 
@@ -438,9 +467,9 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
-    // M > 16 (a prompt): the W4A16 GEMM
+    // M > 16 (a prompt): the W4A16 GEMM, its LDS-staged form for M >= 128
     if (aligned && M > 16 && gemm_fits(M, N, K)) {
-        *out = plan_gemm(M, N, K);
+        *out = gemm_lds_route(M, N, K) ? plan_gemm_lds(M, N, K) : plan_gemm(M, N, K);
         return W4A16_OK;
     }
     const bool tuned = aligned && M <= 8;
@@ -809,6 +838,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_GEMM:
             return w4a16_internal::launch_gemm(p.rows, p.max_blocks, p.splits, (int)M, x, packed, s, o, (int)N, (int)K,
                                                st);
+        case W4A16_KERNEL_GEMM_LDS:
+            return w4a16_internal::launch_gemm2(p.rows, p.max_blocks, p.unroll, p.splits, (int)M, x, packed, s, o, (int)N,
+                                                (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -909,7 +941,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_GEMM) {
+    if (kernel == W4A16_KERNEL_GEMM || kernel == W4A16_KERNEL_GEMM_LDS) {
         if (group_size != 128 || M > INT32_MAX || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "the GEMM kernel needs group_size 128 and 16-byte aligned activations and weights");
@@ -940,7 +972,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_PAIR_STREAM, _STREAM, _GEMM, _DIAG or _GENERIC");
+                    "_PAIR_STREAM, _STREAM, _GEMM, _GEMM_LDS, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
 }

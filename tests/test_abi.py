@@ -167,7 +167,7 @@ def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
     # best shapes of the M = 32..256 sweep on the 1.1B / 8B layers
     (32, 2560, 2048, 1, 2, 4), (32, 2048, 2048, 1, 1, 4), (32, 11264, 2048, 2, 4, 2), (32, 14336, 4096, 2, 4, 2),
     (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (64, 11264, 2048, 4, 4, 2), (64, 4096, 14336, 2, 2, 4),
-    (128, 2560, 2048, 2, 4, 2), (128, 14336, 4096, 4, 4, 2), (256, 2048, 2048, 2, 4, 2), (256, 4096, 14336, 4, 4, 2),
+    (100, 2560, 2048, 2, 4, 2), (256, 2048, 5632, 2, 4, 2),   # M >= 128 mostly takes the LDS-staged GEMM
     (17, 64, 256, 1, 1, 2),     # few workgroups whatever the shape: the most; short rows: 2 wavefronts
 ])
 def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
@@ -198,6 +198,23 @@ def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
     monkeypatch.setenv("W4A16_DECODE", "pair_stream")   # any layer whose activations fit
     assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "pair_stream"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 16384, 128)["kernel"] == "mfma_pair"   # too long for LDS
+
+
+@pytest.mark.parametrize("m,n,k,kernel,shape", [
+    (256, 14336, 4096, "gemm_lds", (4, 2, 4, 1)), (256, 11264, 2048, "gemm_lds", (4, 2, 4, 1)),
+    (256, 5632, 2048, "gemm_lds", (4, 2, 2, 2)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
+    (256, 2048, 5632, "gemm", None),   # long rows of a narrow layer: the per-round barriers lose
+    (64, 11264, 2048, "gemm", None), (127, 14336, 4096, "gemm", None),
+])
+def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
+    """M >= 128 with K <= 4096 or N >= 4096: the LDS-staged GEMM, 4 activation
+    and 2 weight tiles per wavefront; (rows, max_blocks, unroll = wavefronts
+    sharing the staging, splits)."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+    assert plan["kernel"] == kernel
+    if shape:
+        assert (plan["rows"], plan["max_blocks"], plan["unroll"], plan["splits"]) == shape
 
 
 def test_stream_env_selector(monkeypatch):

@@ -22,6 +22,7 @@ MFMA_PAIR = _lib.KERNEL_MFMA_PAIR
 STREAM = _lib.KERNEL_STREAM
 GEMM = _lib.KERNEL_GEMM
 PAIR_STREAM = _lib.KERNEL_PAIR_STREAM
+GEMM_LDS = _lib.KERNEL_GEMM_LDS
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -306,11 +307,27 @@ def test_gemm_variants(gpu, rows, blocks, splits, m, k, n):
     assert_parity(got, expected(x, p, s), f"gemm {rows}/{blocks}/{splits} M={m} K={k} N={n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(17, 2048, 2048), (64, 2048, 5632), (130, 5632, 2048), (512, 2048, 256),
-                                   (33, 8192, 1000)])
-def test_default_dispatch_gemm(gpu, m, k, n):
+GEMM_LDS_SHAPES = [(2, 2, 2, 1), (2, 2, 2, 4), (2, 4, 2, 2), (2, 4, 4, 1), (4, 2, 2, 2), (4, 2, 4, 2), (4, 4, 2, 1),
+                   (4, 4, 4, 2), (2, 2, 4, 4), (4, 2, 2, 4)]
+
+
+@pytest.mark.parametrize("rows,blocks,sn,splits", GEMM_LDS_SHAPES)
+@pytest.mark.parametrize("m,k,n", [(17, 2048, 200), (64, 384, 33), (100, 5632, 48), (3, 1152, 100), (70, 128, 300)])
+def test_gemm_lds_variants(gpu, rows, blocks, sn, splits, m, k, n):
+    """The LDS-staged GEMM's tilings on ragged M and N, K of 1..44 groups
+    (rounds past the last group staged as zeros, rounds run to a multiple of
+    the weight ring)."""
+    x, p, s = make_case(m, k, n, seed=m * 3 + k + n + rows + sn)
+    got = _run_tuned(gpu, x, p, s, GEMM_LDS, rows, splits, sn, max_blocks=blocks)
+    assert_parity(got, expected(x, p, s), f"gemm_lds {rows}/{blocks}/{sn}/{splits} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm"), (130, 5632, 2048, "gemm"),
+                                          (512, 2048, 256, "gemm_lds"), (33, 8192, 1000, "gemm"),
+                                          (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm_lds")])
+def test_default_dispatch_gemm(gpu, m, k, n, kernel):
     x, p, s = make_case(m, k, n, seed=m + k + 3 * n)
-    assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == "gemm"
+    assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == kernel
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"gemm default M={m} K={k} N={n}")
 
 
