@@ -24,6 +24,7 @@ CPU oracle's time for the same layers on the host cores (`cpu_baseline`; a
 reported baseline, not a target).
 
 usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables]
+       python bench.py --layer-pass M K N COPIES CALLS | --prefill-pass TOKENS   (profiler passes)
 """
 
 from __future__ import annotations
@@ -221,47 +222,52 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
-def prefill_long(device, prompt_len: int = 64, runs: int = 5) -> dict:
-    """A 64-token prompt on the random-init 1.1B Llama, each path recorded in
-    a HIP graph: the fused prefill (every projection on the W4A16 op, which
-    runs its GEMM at M = 64) against the reference's prefill path (every
-    projection as dequantize + hipBLASLt inside QuantizedLinear, torch ops
-    around them)."""
+def prefill_long(device, lengths=(64, 256), runs: int = 5) -> dict:
+    """Prompts of 64 and 256 tokens on the random-init 1.1B Llama, each path
+    recorded in a HIP graph: the fused prefill (every projection on the W4A16
+    op: its GEMM at M = 64, the LDS-staged GEMM at M = 256) against the
+    reference's prefill path (every projection as dequantize + hipBLASLt
+    inside QuantizedLinear, torch ops around them)."""
     import torch
 
     from nibble_amd.llama import LlamaConfig, LlamaDecoder
 
-    model = LlamaDecoder(LlamaConfig(max_seq_len=prompt_len), device=device, seed=0)
+    model = LlamaDecoder(LlamaConfig(max_seq_len=max(lengths)), device=device, seed=0)
     gen = torch.Generator().manual_seed(1)
-    prompt = torch.randint(0, model.cfg.vocab_size, (prompt_len,), generator=gen).to(device)
+    result = {}
+    for prompt_len in lengths:
+        prompt = torch.randint(0, model.cfg.vocab_size, (prompt_len,), generator=gen).to(device)
 
-    def timed() -> float:
-        model.capture_prefill(prompt_len)
-        ts = []
-        for _ in range(runs + 1):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            model.prefill(prompt)
-            torch.cuda.synchronize()
-            ts.append(time.perf_counter() - t0)
-        ts = sorted(ts[1:])
-        return ts[len(ts) // 2]
+        def timed() -> float:
+            model.capture_prefill(prompt_len)
+            ts = []
+            for _ in range(runs + 1):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                model.prefill(prompt)
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t0)
+            ts = sorted(ts[1:])
+            return ts[len(ts) // 2]
 
-    model.fused = True
-    fused = timed()
-    model.fused = False
-    for b in model.layers:
-        b.native_prefill = False
-    dequant = timed()
+        model.fused = True
+        for b in model.layers:
+            b.native_prefill = True
+        fused = timed()
+        model.fused = False
+        for b in model.layers:
+            b.native_prefill = False
+        dequant = timed()
+        result[f"prefill{prompt_len}_ms"] = round(fused * 1e3, 3)
+        result[f"prefill{prompt_len}_dequant_ms"] = round(dequant * 1e3, 3)
+    model.prefill_graph = None
     del model
     torch.cuda.empty_cache()
-    return {
-        "prefill64_ms": round(fused * 1e3, 3),
-        "prefill64_dequant_ms": round(dequant * 1e3, 3),
-        "prefill64": f"{prompt_len}-token prompt, one HIP graph each: the fused prefill (W4A16 GEMM for q|k|v, o, "
-                     "gate|up, down at M=64) against dequantize + hipBLASLt for every projection with torch ops "
-                     "around them (the reference's prefill path)",
-    }
+    result["prefill_long"] = ("prompts of " + " and ".join(str(n) for n in lengths) + " tokens, one HIP graph "
+                              "each: the fused prefill (W4A16 GEMM for q|k|v, o, gate|up, down) against dequantize "
+                              "+ hipBLASLt for every projection with torch ops around them (the reference's "
+                              "prefill path)")
+    return result
 
 
 def _copies(nbytes: int, floor_bytes: int = 512 << 20) -> int:
@@ -330,6 +336,9 @@ def main() -> int:
     ap.add_argument("--layer-pass", type=int, nargs=5, metavar=("M", "K", "N", "COPIES", "CALLS"),
                     help="eager launches only, for rocprofv3 --pmc: CALLS default-dispatch calls of one "
                          "[M, K] x [N, K] layer on COPIES rotated weight copies; no JSON")
+    ap.add_argument("--prefill-pass", type=int, metavar="TOKENS",
+                    help="for rocprofv3 --kernel-trace: capture the fused prefill of a TOKENS-token prompt on the "
+                         "random-init 1.1B Llama and replay it 10 times; no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -348,6 +357,20 @@ def main() -> int:
         raise RuntimeError(f"W4A16 HIP extension not loaded: {nibble_amd.cuda.extension_load_error()}")
     device = torch.device("cuda:0")
     torch.manual_seed(0)
+
+    if args.prefill_pass:
+        from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+        t = args.prefill_pass
+        model = LlamaDecoder(LlamaConfig(max_seq_len=max(48, t)), device=device, seed=0)
+        prompt = torch.randint(0, model.cfg.vocab_size, (t,), generator=torch.Generator().manual_seed(0)).to(device)
+        model.capture_prefill(t)
+        torch.cuda.synchronize()
+        for _ in range(10):
+            model.prefill(prompt)
+        torch.cuda.synchronize()
+        print("prefill pass done", flush=True)
+        return 0
 
     if args.layer_pass:
         m, k, n, lcopies, calls = args.layer_pass

@@ -86,7 +86,7 @@ def test_add_rmsnorm_rejects(gpu):
         _lib.add_rmsnorm_f16(x, x, w, 1e-5, x, out)
 
 
-@pytest.mark.parametrize("rows,inter", [(1, 5632), (16, 5632), (5, 77)])
+@pytest.mark.parametrize("rows,inter", [(1, 5632), (16, 5632), (5, 77), (64, 5632), (3, 40)])
 def test_silu_mul(gpu, rows, inter):
     gen = torch.Generator().manual_seed(rows + inter)
     gu = (4.0 * torch.randn((rows, 2 * inter), generator=gen)).to(torch.float16)
