@@ -169,6 +169,21 @@ int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output
 int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t inter, void* stream);
 
 /*
+ * SiLU-gated projection: output[m, i] = fp16(fp16(silu(g)) * u) with g =
+ * (activations @ W[i]^T) and u = (activations @ W[inter + i]^T) each rounded
+ * to fp16, for packed_weights [2 inter, K / 2] and scales [2 inter, K / 128]
+ * holding the gate rows then the up rows. The same values as
+ * w4a16_linear_f16 over the 2 inter rows followed by w4a16_silu_mul_f16, in
+ * one launch: the W4A16 GEMM with the multiply in its epilogue (M >= 2, or
+ * K > 16384), or the decode step's paired fused GEMV (M = 1). Replaces the
+ * gate_proj / up_proj QuantizedLinear calls and act_fn(gate) * up of HF's
+ * LlamaMLP (w4a16/linear.py:154-200 for each projection). Needs group_size
+ * 128, 16-byte aligned activations and weights, operands below 4 GiB.
+ */
+int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,
+                          int64_t M, int64_t inter, int64_t K, int64_t group_size, void* stream);
+
+/*
  * Residual add + RMSNorm over `rows` rows of `hidden` fp16 values (hidden <=
  * 8192): x_out = fp16(x + delta) (an fp16 tensor add's rounding), output =
  * RMSNorm(x_out) * weight as w4a16_rmsnorm_f16 computes it. x_out may be x.

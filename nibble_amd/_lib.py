@@ -83,6 +83,7 @@ DECODE_SIGNATURES = {
     "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
     "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
     "w4a16_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _vp]),
+    "w4a16_linear_silu_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "w4a16_prefill_attention_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                                    _i64, _vp]),
 }
@@ -288,6 +289,15 @@ def add_rmsnorm_f16(x, delta, weight, eps: float, x_out, output, stream=None) ->
     rows, hidden = x.shape
     _raise_on(lib().w4a16_add_rmsnorm_f16(x.data_ptr(), delta.data_ptr(), weight.data_ptr(), float(eps),
                                           x_out.data_ptr(), output.data_ptr(), rows, hidden, _stream_ptr(stream)))
+
+
+def linear_silu_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None) -> None:
+    """``w4a16_linear_silu_f16``: output [M, inter] <- silu(x W_gate^T) * (x W_up^T) for
+    packed_weights [2 inter, K / 2] ([gate; up] rows)."""
+    m, k = activations.shape
+    inter = packed_weights.shape[0] // 2
+    _raise_on(lib().w4a16_linear_silu_f16(activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(),
+                                          output.data_ptr(), m, inter, k, group_size, _stream_ptr(stream)))
 
 
 def silu_mul_f16(gate_up, output, stream=None) -> None:

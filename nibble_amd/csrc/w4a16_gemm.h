@@ -55,10 +55,23 @@ struct GemmGroup {
     uint32_t s[RB];   // fp16 bits of the group scale
 };
 
-template <int MT, int RB, int SK>
+// SiLU-multiply epilogue of a [gate; up] weight pair (PAIRED): N is the
+// output width `inter`, the packed weights hold 2 inter rows (gate rows, then
+// up rows), and a wavefront's RB weight tiles are RB / 2 gate tiles and the
+// up tiles of the same columns; out[m][n] = fp16(fp16(silu(fp16(g))) *
+// fp16(u)), the roundings of silu(gate) * up on the op's fp16 outputs.
+__device__ __forceinline__ f16 gemm_silu_mul(float g, float u) {
+    const float gh = (float)(f16)g;
+    const f16 sg = (f16)(gh / (1.0f + __expf(-gh)));
+    return (f16)((float)sg * (float)(f16)u);
+}
+
+template <int MT, int RB, int SK, bool PAIRED = false>
 __global__ void __launch_bounds__(64 * SK)
 gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
            f16* __restrict__ out, int M, int N, int K, int nblocks) {
+    static_assert(!PAIRED || RB % 2 == 0, "paired tiles come in gate / up pairs");
+    constexpr int RO = PAIRED ? RB / 2 : RB;   // output tiles per wavefront
     const int b = blockIdx.x;
     const int mblocks = (int)gridDim.x / ((nblocks + 7) & ~7);
     const int s = b >> 3;
@@ -73,7 +86,7 @@ gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* 
     const int c = lane & 15, q = lane >> 4;
     const int G = K >> 7;
     const uint32_t row_bytes = (uint32_t)(K >> 1);
-    const int n0 = nbk * 16 * RB;
+    const int n0 = nbk * 16 * RO;
     const int m0 = mbk * 16 * MT;
     const int ng = wave < G ? (G - 1 - wave) / SK + 1 : 0;   // groups of this wavefront
 
@@ -84,7 +97,9 @@ gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* 
     uint32_t wrow[RB], srow[RB], xrow[MT];
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
-        const uint32_t n = (uint32_t)min(n0 + 16 * r + c, N - 1);
+        // PAIRED: tiles RO .. RB - 1 are the up rows (N .. 2 N - 1) of tiles 0 .. RO - 1
+        const uint32_t n = PAIRED && r >= RO ? (uint32_t)(N + min(n0 + 16 * (r - RO) + c, N - 1))
+                                             : (uint32_t)min(n0 + 16 * r + c, N - 1);
         wrow[r] = n * row_bytes + 16u * q;
         srow[r] = n * (uint32_t)G * 2u;
     }
@@ -184,12 +199,14 @@ gemm_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* 
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
+        for (int r = 0; r < RO; ++r) {
             const int n = n0 + 16 * r + c;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = m0 + 16 * t + 4 * q + e;
-                if (m < M && n < N) out[(size_t)m * N + n] = (f16)acc[t][r][e];
+                if (m < M && n < N)
+                    out[(size_t)m * N + n] = PAIRED ? gemm_silu_mul(acc[t][r][e], acc[t][r + RO][e])
+                                                    : (f16)acc[t][r][e];
             }
         }
     }
@@ -232,10 +249,12 @@ __host__ __device__ constexpr int64_t gemm2_lds_bytes(int mt, int rb, int sn, in
                : (int64_t)(sk - 1) * sn * mt * rb * 64 * 16;
 }
 
-template <int MT, int RB, int SN, int SK>
+template <int MT, int RB, int SN, int SK, bool PAIRED = false>
 __global__ void __launch_bounds__(64 * SN * SK)
 gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
             f16* __restrict__ out, int M, int N, int K, int nblocks) {
+    static_assert(!PAIRED || RB % 2 == 0, "paired tiles come in gate / up pairs");
+    constexpr int RO = PAIRED ? RB / 2 : RB;   // output tiles per wavefront (PAIRED: as gemm_w4a16)
     constexpr int T = 64 * SN * SK;
     constexpr int DB = kGemmRing;
     constexpr int UNITS = SK * 16 * MT * 16;   // 16-byte units staged per round
@@ -260,7 +279,7 @@ gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
     const int R = (G + SK - 1) / SK;
     const int RP = (R + DB - 1) / DB * DB;   // rounds run, a multiple of the ring
     const uint32_t row_bytes = (uint32_t)(K >> 1);
-    const int n0 = nbk * 16 * RB * SN + sn * 16 * RB;
+    const int n0 = nbk * 16 * RO * SN + sn * 16 * RO;
     const int m0 = mbk * 16 * MT;
 
     // staging: unit u = (group gl, row, 16-byte part p) of the round
@@ -293,7 +312,8 @@ gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
     uint32_t wrow[RB], srow[RB];
 #pragma unroll
     for (int t = 0; t < RB; ++t) {
-        const uint32_t n = (uint32_t)min(n0 + 16 * t + c, N - 1);
+        const uint32_t n = PAIRED && t >= RO ? (uint32_t)(N + min(n0 + 16 * (t - RO) + c, N - 1))
+                                             : (uint32_t)min(n0 + 16 * t + c, N - 1);
         wrow[t] = n * row_bytes + 16u * q;
         srow[t] = n * (uint32_t)G * 2u;
     }
@@ -391,12 +411,14 @@ gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
 #pragma unroll
-        for (int r = 0; r < RB; ++r) {
+        for (int r = 0; r < RO; ++r) {
             const int n = n0 + 16 * r + c;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = m0 + 16 * t + 4 * q + e;
-                if (m < M && n < N) out[(size_t)m * N + n] = (f16)acc[t][r][e];
+                if (m < M && n < N)
+                    out[(size_t)m * N + n] = PAIRED ? gemm_silu_mul(acc[t][r][e], acc[t][r + RO][e])
+                                                    : (f16)acc[t][r][e];
             }
         }
     }

@@ -154,4 +154,93 @@ int launch_gemm2(int mt, int rb, int sn, int sk, int M, const void* x, const uin
     return W4A16_OK;
 }
 
+// gemm_w4a16 with the SiLU-multiply epilogue of a [gate; up] pair: N = inter
+// output columns, the weights 2 inter rows; rb weight tiles per wavefront
+// (2 or 4: rb / 2 gate tiles and their up tiles).
+namespace {
+template <int MT, int RB>
+Kern pick_silu_sk(int sk) {
+    using namespace w4a16;
+    if (sk == 2) return gemm_w4a16<MT, RB, 2, true>;
+    if (sk == 4) return gemm_w4a16<MT, RB, 4, true>;
+    if constexpr (MT * RB < 16) {
+        if (sk == 8) return gemm_w4a16<MT, RB, 8, true>;
+    }
+    return nullptr;
+}
+Kern pick_silu(int mt, int rb, int sk) {
+    if (rb == 2) {
+        if (mt == 1) return pick_silu_sk<1, 2>(sk);
+        if (mt == 2) return pick_silu_sk<2, 2>(sk);
+        if (mt == 4) return pick_silu_sk<4, 2>(sk);
+    }
+    if (rb == 4) {
+        if (mt == 1) return pick_silu_sk<1, 4>(sk);
+        if (mt == 2) return pick_silu_sk<2, 4>(sk);
+        if (mt == 4) return pick_silu_sk<4, 4>(sk);
+    }
+    return nullptr;
+}
+}  // namespace
+
+bool gemm_silu_instantiated(int mt, int rb, int sk) { return pick_silu(mt, rb, sk) != nullptr; }
+
+// gemm2_w4a16 with the SiLU-multiply epilogue: the LDS-staged GEMM's shapes
+// for prompts of 128+ rows (4 activation tiles, one gate and one up tile per
+// wavefront).
+namespace {
+Kern pick2_silu(int mt, int rb, int sn, int sk) {
+    using namespace w4a16;
+    if (mt != 4 || rb != 2) return nullptr;
+    if (sn == 4 && sk == 1) return gemm2_w4a16<4, 2, 4, 1, true>;
+    if (sn == 2 && sk == 2) return gemm2_w4a16<4, 2, 2, 2, true>;
+    if (sn == 2 && sk == 4) return gemm2_w4a16<4, 2, 2, 4, true>;
+    return nullptr;
+}
+}  // namespace
+
+bool gemm2_silu_instantiated(int mt, int rb, int sn, int sk) { return pick2_silu(mt, rb, sn, sk) != nullptr; }
+
+int launch_gemm2_silu(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o,
+                      int inter, int K, hipStream_t stream) {
+    if (M < 1 || inter < 1 || !gemm_fits(M, 2 * (int64_t)inter, K))
+        return fail(W4A16_ERR_CONFIG, "LDS GEMM kernel: K must be a positive multiple of 128 and every operand below 4 GiB");
+    const Kern kern = pick2_silu(mt, rb, sn, sk);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "paired LDS GEMM kernel: no instantiation for this shape");
+    const int64_t lds = w4a16::gemm2_lds_bytes(mt, rb, sn, sk);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int nblocks = (inter + 8 * rb * sn - 1) / (8 * rb * sn);
+    const int mblocks = (M + 16 * mt - 1) / (16 * mt);
+    const int64_t grid = (int64_t)((nblocks + 7) & ~7) * mblocks;
+    if (grid > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "LDS GEMM kernel: too many workgroups");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * sn * sk), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, inter, K, nblocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
+int launch_gemm_silu(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int inter,
+                     int K, hipStream_t stream) {
+    if (M < 1 || inter < 1 || !gemm_fits(M, 2 * (int64_t)inter, K))
+        return fail(W4A16_ERR_CONFIG, "GEMM kernel: K must be a positive multiple of 128 and every operand below 4 GiB");
+    const Kern kern = pick_silu(mt, rb, sk);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "paired GEMM kernel: no instantiation for this shape");
+    const int lds = (int)w4a16::gemm_lds_bytes(mt, rb, sk);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    if (rc != W4A16_OK) return rc;
+    const int nblocks = (inter + 8 * rb - 1) / (8 * rb);
+    const int mblocks = (M + 16 * mt - 1) / (16 * mt);
+    const int64_t grid = (int64_t)((nblocks + 7) & ~7) * mblocks;
+    if (grid > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "GEMM kernel: too many workgroups");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * sk), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, inter, K, nblocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
 }  // namespace w4a16_internal

@@ -41,6 +41,12 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K);
 int launch_gemm(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N, int K,
                 hipStream_t stream);
 bool gemm2_instantiated(int mt, int rb, int sn, int sk);
+bool gemm_silu_instantiated(int mt, int rb, int sk);
+int launch_gemm_silu(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int inter,
+                     int K, hipStream_t stream);
+bool gemm2_silu_instantiated(int mt, int rb, int sn, int sk);
+int launch_gemm2_silu(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o,
+                      int inter, int K, hipStream_t stream);
 int launch_gemm2(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N,
                  int K, hipStream_t stream);
 }  // namespace w4a16_internal
@@ -1013,6 +1019,42 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
                   : launch_fused_t<false, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
     return nw ? launch_fused_t<true, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
               : launch_fused_t<false, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
+}
+
+int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,
+                          int64_t M, int64_t inter, int64_t K, int64_t group_size, void* stream) {
+    int rc = check_scalar_args(M, 2 * inter, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    if (group_size != 128) return fail(W4A16_ERR_GROUP_SIZE, "linear + SiLU needs group_size 128");
+    if (M * inter == 0) return W4A16_OK;
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    if (!aligned16(activations) || !aligned16(packed_weights))
+        return fail(W4A16_ERR_ALIGNMENT, "linear + SiLU needs 16-byte aligned activations and weights");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    using w4a16::f16;
+    if (M == 1 && K <= 16384) {   // one row: the paired fused GEMV of the decode step
+        int R, W;
+        fused_shape(true, false, 2 * inter, R, W);
+        w4a16::GemvFusion fz{};
+        return launch_fused_t<false, true>(oneshot_loads(K), R, W, static_cast<const f16*>(activations), fz,
+                                           packed_weights, static_cast<const f16*>(scales), static_cast<f16*>(output),
+                                           (int)(2 * inter), (int)K, st);
+    }
+    if (!w4a16_internal::gemm_fits(M, 2 * inter, K))
+        return fail(W4A16_ERR_TOO_LARGE, "linear + SiLU: every operand must be below 4 GiB");
+    // the GEMM the op would run over the 2 inter rows, with an even number of weight tiles per wavefront
+    if (gemm_lds_route(M, 2 * inter, K)) {
+        const Plan q = plan_gemm_lds(M, 2 * inter, K);
+        if (w4a16_internal::gemm2_silu_instantiated(q.rows, q.max_blocks, q.unroll, q.splits))
+            return w4a16_internal::launch_gemm2_silu(q.rows, q.max_blocks, q.unroll, q.splits, (int)M, activations,
+                                                     packed_weights, scales, output, (int)inter, (int)K, st);
+    }
+    Plan p = plan_gemm(M, 2 * inter, K);
+    if (p.max_blocks == 1) p.max_blocks = 2;
+    if (!w4a16_internal::gemm_silu_instantiated(p.rows, p.max_blocks, p.splits)) p.splits = 2;
+    return w4a16_internal::launch_gemm_silu(p.rows, p.max_blocks, p.splits, (int)M, activations, packed_weights, scales,
+                                            output, (int)inter, (int)K, st);
 }
 
 int64_t w4a16_gemv_argmax_workspace_bytes(int64_t N) { return N <= 0 ? 0 : argmax_workspace_bytes(N); }

@@ -306,11 +306,11 @@ class LlamaDecoder(torch.nn.Module):
         """The prompt (cache slots 0 .. T-1) with the decode step's roundings:
         RMSNorm of the embeddings, then per layer the q|k|v op, rotary + KV
         append + causal attention, the o op, residual add + RMSNorm, the
-        gate|up op, SiLU * up, the down op and residual add + the next RMSNorm
-        (the next layer's input norm, or the final norm after the last layer);
-        then the lm_head GEMV on the last normed row and the greedy argmax,
-        which also gathers the first decode step's input row. 8 launches per
-        layer."""
+        gate|up projection with its SiLU * up epilogue, the down op and
+        residual add + the next RMSNorm (the next layer's input norm, or the
+        final norm after the last layer); then the lm_head GEMV on the last
+        normed row and the greedy argmax, which also gathers the first decode
+        step's input row. 7 launches per layer."""
         cfg = self.cfg
         t = prompt.numel()
         g = cfg.group_size
@@ -328,8 +328,7 @@ class LlamaDecoder(torch.nn.Module):
                                        cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
             o = torch.ops.w4a16.linear(attn, b.o_proj.packed_weights, b.o_proj.scales, g)
             _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
-            gu = torch.ops.w4a16.linear(h, gu_w, gu_s, g)
-            _lib.silu_mul_f16(gu, mlp)
+            _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
             d = torch.ops.w4a16.linear(mlp, b.down_proj.packed_weights, b.down_proj.scales, g)
             nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.norm
             _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)

@@ -105,6 +105,47 @@ def test_silu_mul(gpu, rows, inter):
     assert torch.all((got - torch_ref).abs() <= 2 * ULP * torch_ref.abs() + 2 ** -20)
 
 
+@pytest.mark.parametrize("m,k,inter", [(1, 2048, 5632), (2, 2048, 5632), (16, 2048, 5632), (64, 2048, 5632),
+                                       (37, 1152, 100), (1, 20480, 64), (130, 4096, 257), (256, 2048, 5632),
+                                       (128, 5632, 2100)])
+def test_linear_silu(gpu, m, k, inter):
+    """w4a16_linear_silu_f16 against the op over the 2 inter rows followed by
+    SiLU * up: bit-identical to the same GEMM shape (or, at M = 1 with K <=
+    16384, to the paired fused GEMV), and within the parity bar of the oracle's
+    fp32 products pushed through the same fp16 roundings."""
+    from tests._cases import expected, make_case
+
+    x, p, s = make_case(m, k, 2 * inter, seed=m + k + inter)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    out = torch.full((m, inter), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] linear_silu M={m} K={k} inter={inter}", flush=True)
+    _lib.linear_silu_f16(xd, pd, sd, out)
+    gu = torch.empty((m, 2 * inter), dtype=torch.float16, device=gpu)
+    if m == 1 and k <= 16384:
+        _lib.gemv_fused_f16(xd[0], pd, sd, out_ref := torch.empty((inter,), dtype=torch.float16, device=gpu),
+                            paired=True)
+        ref = out_ref.view(1, inter)
+    else:
+        # the same GEMM over the 2 inter rows (the op's shape), then SiLU * up
+        plan = _lib.plan_linear(1 << 20, 1 << 20, m, 2 * inter, k, 128)
+        if plan["kernel"] == "gemm_lds":
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM_LDS, 4, plan["splits"], plan["unroll"], 2)
+        elif plan["kernel"] == "gemm":
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM, plan["rows"], plan["splits"], 0, 2)
+        else:   # M = 1, K > 16384: the op runs a GEMV; compare with the GEMM at 1 activation tile
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM, 1, 4, 0, 2)
+        ref = torch.empty_like(out)
+        _lib.silu_mul_f16(gu, ref)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, ref)
+    g = torch.from_numpy(expected(x, p, s)).to(torch.float16).double()   # the op's fp16 outputs (oracle)
+    sg = (g[:, :inter] / (1 + torch.exp(-g[:, :inter]))).to(torch.float16).double()
+    want = sg * g[:, inter:]
+    got = out.double().cpu()
+    assert torch.all((got - want).abs() <= 1e-2 * (1 + want.abs())), float((got - want).abs().max())
+
+
 def _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv):
     """float64 restatement: rotary q / k rounded to fp16, causal softmax attention."""
     t = qkv.shape[0]
