@@ -55,10 +55,9 @@ extern "C" {
  * activations: fp16 [M, K] row-major; packed_weights: uint8 [N, K/2];
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
- * takes the tuned kernels, M = 9..16 the one-shot MFMA kernel when its
- * activations fit in LDS (M*K*2 bytes, K <= 4096 at M = 16), else the
- * paired MFMA kernel over two halves of the rows (K <= 32768), and M > 16
- * the W4A16 GEMM (operands below 4 GiB); anything else takes the generic
+ * takes the tuned kernels and M > 8 the W4A16 GEMM (operands below 4 GiB;
+ * its LDS-staged form from M = 128; W4A16_DECODE = mfma_oneshot or mfma_pair
+ * selects those kernels for M = 9..16); anything else takes the generic
  * kernel (the reference routes every M > 8 to its naive kernel).
  * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
  * valu_offset|mfma|mfma_oneshot|mfma_pair|stream|pair_stream selects the

@@ -376,7 +376,7 @@ constexpr int64_t kGemmMaxM = 1 << 20;
 
 bool gemm_fits(int64_t M, int64_t N, int64_t K) {
     const Plan p = plan_gemm(M, N, K);
-    return M > 16 && M <= kGemmMaxM && w4a16_internal::gemm_fits(M, N, K) &&
+    return M > 8 && M <= kGemmMaxM && w4a16_internal::gemm_fits(M, N, K) &&
            w4a16_internal::gemm_instantiated(p.rows, p.max_blocks, p.splits);
 }
 
@@ -460,21 +460,22 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         return W4A16_OK;
     }
     const bool aligned = G == 128 && aligned16(act) && aligned16(packed);
-    // M = 9..16 (a short prompt) is one MFMA tile: the one-shot MFMA kernel
-    // when the activations fit in LDS, else the paired kernel over two halves
-    // of the rows (K up to 32768), else the generic kernel.
-    if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_ONESHOT) &&
-        mfma_oneshot_fits(M, K)) {
+    // M = 9..16 (a short prompt) is one MFMA tile of activation rows: the
+    // GEMM by default (measured against the one-shot MFMA kernel and the
+    // paired kernel over two halves, M = 9..16 on the 1.1B / 8B layers: M =
+    // 16 4096 x 14336 14.0 against 20.2 us, 5632 x 2048 8.6 against 10.8,
+    // 2048 x 2560 4.9 against 6.3; tied at 2048 x 11264); W4A16_DECODE =
+    // mfma_oneshot or mfma_pair selects those kernels where they fit.
+    if (aligned && M > 8 && M <= 16 && family == W4A16_KERNEL_MFMA_ONESHOT && mfma_oneshot_fits(M, K)) {
         *out = plan_mfma_oneshot(M, N, K);
         return W4A16_OK;
     }
-    if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_MFMA_PAIR) &&
-        mfma_pair_fits(M, N, K)) {
+    if (aligned && M > 8 && M <= 16 && family == W4A16_KERNEL_MFMA_PAIR && mfma_pair_fits(M, N, K)) {
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
-    // M > 16 (a prompt): the W4A16 GEMM, its LDS-staged form for M >= 128
-    if (aligned && M > 16 && gemm_fits(M, N, K)) {
+    // M > 8 (a prompt): the W4A16 GEMM, its LDS-staged form for M >= 128
+    if (aligned && M > 8 && gemm_fits(M, N, K)) {
         *out = gemm_lds_route(M, N, K) ? plan_gemm_lds(M, N, K) : plan_gemm(M, N, K);
         return W4A16_OK;
     }

@@ -27,13 +27,12 @@ the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
 Prefill of a prompt of up to 256 tokens runs the W4A16 op itself for every
-projection (q|k|v and gate|up as one op each; up to 16 tokens the op takes
-its one-shot MFMA kernel where the activations fit that kernel's LDS and the
-paired MFMA kernel over two halves of the rows elsewhere, as for the
-5632-wide down projection; beyond 16 its W4A16 GEMM) with one launch each
-for the RMSNorms, the rotary + KV append + causal attention and the
-SiLU-multiply; longer prompts run torch ops around the same op (the GEMM up
-to 256 rows, dequantize + hipBLASLt beyond). ``capture_prefill(T)`` records
+projection (q|k|v as one op; the op's W4A16 GEMM from 9 rows, its LDS-staged
+form from 128; up to 8 rows its small-batch kernels), gate|up as one GEMM
+with the SiLU-multiply in its epilogue, and one launch each for the residual
+add + RMSNorm and the rotary + KV append + causal attention; longer prompts
+run torch ops around the same op (the GEMM up to 256 rows, dequantize +
+hipBLASLt beyond). ``capture_prefill(T)`` records
 a T-token prefill in a HIP graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.

@@ -124,11 +124,11 @@ ALIGNED = 1 << 20
         (5, 2048, 128, ALIGNED, "mfma_pair"),
         (8, 4096, 128, ALIGNED, "mfma_pair"),
         (8, 5632, 128, ALIGNED, "mfma_pair"),
-        (9, 2048, 128, ALIGNED, "mfma_oneshot"),   # a short prompt: one MFMA tile of rows
-        (16, 4096, 128, ALIGNED, "mfma_oneshot"),
-        (16, 5632, 128, ALIGNED, "mfma_pair"),     # beyond the one-shot kernel's LDS: two paired launches
-        (9, 28672, 128, ALIGNED, "mfma_pair"),
-        (16, 34816, 128, ALIGNED, "generic"),      # beyond the paired kernel's rows
+        (9, 2048, 128, ALIGNED, "gemm"),           # a short prompt: the GEMM at one activation tile
+        (16, 4096, 128, ALIGNED, "gemm"),
+        (16, 5632, 128, ALIGNED, "gemm"),
+        (9, 28672, 128, ALIGNED, "gemm"),
+        (16, 34816, 128, ALIGNED, "gemm"),
         (17, 2048, 128, ALIGNED, "gemm"),          # prompts above one tile: the W4A16 GEMM
         (64, 5632, 128, ALIGNED, "gemm"),
         (300, 34816, 128, ALIGNED, "gemm"),

@@ -196,9 +196,11 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
 @pytest.mark.parametrize("m,k,n", [(3, 2048, 5632), (5, 4096, 4096), (7, 5632, 2048), (8, 8192, 1000),
                                    (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
                                    (5, 8320, 77),
-                                   # M = 9..16 past the one-shot MFMA kernel's LDS: two launches
+                                   # M = 9..16 with the selector: two launches over the row halves
                                    (16, 5632, 2048), (9, 28672, 100), (13, 8192, 77)])
-def test_default_dispatch_mfma_pair(gpu, m, k, n):
+def test_default_dispatch_mfma_pair(gpu, m, k, n, monkeypatch):
+    if m > 8:
+        monkeypatch.setenv("W4A16_DECODE", "mfma_pair")   # M = 9..16 defaults to the GEMM
     x, p, s = make_case(m, k, n, seed=m + k + n)
     assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "mfma_pair"
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"pair default M={m} K={k} N={n}")
@@ -414,11 +416,18 @@ def test_stream_rejects(gpu):
     assert not out.any() and not out1.any()
 
 
-@pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7)])
-def test_default_dispatch_short_prompt(gpu, m, k, n):
+@pytest.mark.parametrize("kernel", ["gemm", "mfma_oneshot"])
+@pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7), (16, 5632, 2048)])
+def test_default_dispatch_short_prompt(gpu, m, k, n, kernel, monkeypatch):
+    """M = 9..16: the GEMM by default, the one-shot MFMA kernel with its
+    selector (where its activations fit in LDS)."""
+    if kernel == "mfma_oneshot":
+        if m * k * 2 > 100 * 1024:
+            pytest.skip("activations past the one-shot MFMA kernel's LDS")
+        monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
     x, p, s = make_case(m, k, n, seed=m + k)
-    assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "mfma_oneshot"
-    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"prompt M={m} K={k} N={n}")
+    assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == kernel
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"prompt M={m} K={k} N={n} {kernel}")
 
 
 def test_mfma_oneshot_rejects(gpu):
