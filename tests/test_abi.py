@@ -62,6 +62,12 @@ def test_decode_entry_points_validate_before_launch():
     assert lib.w4a16_add_rmsnorm_f16(a, 0, a, 1e-5, a, a, 4, 2048, 0) == _lib.W4A16_ERR_NULL
     assert lib.w4a16_add_rmsnorm_f16(a, a, a, -1.0, a, a, 4, 2048, 0) == _lib.W4A16_ERR_CONFIG
     assert lib.w4a16_add_rmsnorm_f16(a, a, a, 1e-5, a, a, 0, 2048, 0) == _lib.W4A16_OK   # no rows: nothing
+    # linear + SiLU: group size, shapes, NULL pointers, alignment, empty
+    assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 256, 64, 0) == _lib.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 200, 128, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_linear_silu_f16(a, 0, a, a, 4, 64, 256, 128, 0) == _lib.W4A16_ERR_NULL
+    assert lib.w4a16_linear_silu_f16(a + 2, a, a, a, 4, 64, 256, 128, 0) == _lib.W4A16_ERR_ALIGNMENT
+    assert lib.w4a16_linear_silu_f16(a, a, a, a, 0, 64, 256, 128, 0) == _lib.W4A16_OK   # M = 0: nothing
 
 
 def test_version():
