@@ -756,8 +756,9 @@ silu_mul_vec_kernel(const f16* __restrict__ gate_up, f16* __restrict__ out, int 
 // t = 4 b .. 4 b + 3, one per wavefront, so a prompt runs on num_heads *
 // ceil(T / 4) workgroups. qkv rows (stride (num_heads + 2 num_kv) * 64) hold
 // [q | k | v] as the decode step's; q and k get the rotary embedding of their
-// slot in fp32, rounded to fp16; workgroup (hq, 0) of the group's first query
-// head appends all T new k and v rows to the caches. Attention: query t sees
+// slot in fp32, rounded to fp16; the workgroups (hq, b) of the group's first
+// query head append the k and v rows of their own 4 tokens to the caches (so
+// the append is spread over the grid). Attention: query t sees
 // slots 0 .. start + t (slots below start from the caches), softmax(q k^T / 8)
 // v in fp32 with an online softmax over 64-slot chunks; output [T,
 // num_heads * 64] fp16. A workgroup stages only the slots its last query
@@ -784,7 +785,7 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
     const int hq = blockIdx.x;
     const int group = num_heads / num_kv;
     const int hk = hq / group;
-    const bool writer = hq % group == 0 && blockIdx.y == 0;
+    const bool writer = hq % group == 0;   // appends the rows of tokens t0 .. t0 + tq - 1
     const int row_stride = (num_heads + 2 * num_kv) * D;
 
     // earlier slots from the caches (16 bytes per thread and step)
@@ -794,9 +795,9 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
         reinterpret_cast<u32x4*>(ks + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(k_cache + g)[c];
         reinterpret_cast<u32x4*>(vs + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(v_cache + g)[c];
     }
-    // the new tokens this workgroup sees (the writer: all T): rotary k, v as
-    // is; rotary q of its own queries
-    const int tk = writer ? T : t0 + tq;
+    // the new tokens this workgroup sees: rotary k, v as is; rotary q of its
+    // own queries
+    const int tk = t0 + tq;
     for (int i = threadIdx.x; i < tk * D; i += 256) {
         const int t = i / D, d = i - t * D;
         const int slot = start + t;
@@ -808,18 +809,16 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
         const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
         const f16 kr = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
         const f16 vv = v[d];
-        if (slot < NK) {
-            ks[slot * kPrefillRow + d] = kr;
-            vs[slot * kPrefillRow + d] = vv;
-        }
-        if (t >= t0 && t < t0 + tq) {
+        ks[slot * kPrefillRow + d] = kr;
+        vs[slot * kPrefillRow + d] = vv;
+        if (t >= t0) {
             const f16* q = row + (size_t)hq * D;
             const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
             qs[(t - t0) * D + d] = (float)(f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
-        }
-        if (writer) {
-            k_cache[((size_t)hk * S + slot) * D + d] = kr;
-            v_cache[((size_t)hk * S + slot) * D + d] = vv;
+            if (writer) {
+                k_cache[((size_t)hk * S + slot) * D + d] = kr;
+                v_cache[((size_t)hk * S + slot) * D + d] = vv;
+            }
         }
     }
     __syncthreads();
