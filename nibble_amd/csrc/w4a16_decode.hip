@@ -751,27 +751,56 @@ silu_mul_vec_kernel(const f16* __restrict__ gate_up, f16* __restrict__ out, int 
     *reinterpret_cast<u32x4*>(out + r * inter + c) = o;
 }
 
-// Prefill attention of T new tokens at cache slots start .. start + T - 1.
-// Workgroup (hq, b) of 4 wavefronts takes query head hq and the 4 queries
-// t = 4 b .. 4 b + 3, one per wavefront, so a prompt runs on num_heads *
-// ceil(T / 4) workgroups. qkv rows (stride (num_heads + 2 num_kv) * 64) hold
-// [q | k | v] as the decode step's; q and k get the rotary embedding of their
-// slot in fp32, rounded to fp16; the workgroups (hq, b) of the group's first
-// query head append the k and v rows of their own 4 tokens to the caches (so
-// the append is spread over the grid). Attention: query t sees
-// slots 0 .. start + t (slots below start from the caches), softmax(q k^T / 8)
-// v in fp32 with an online softmax over 64-slot chunks; output [T,
-// num_heads * 64] fp16. A workgroup stages only the slots its last query
-// sees. LDS: q [4][64] fp32, k and v [slots][kRow] fp16 (rows padded to 72
-// halves, so a wavefront reading 64 rows spreads over the banks).
+// Prefill attention of T new tokens at cache slots start .. start + T - 1, in
+// two launches (one for short prompts, below). prefill_rope_append_kernel:
+// the rotary embedding of the new k rows (fp32, rounded to fp16) and the v
+// rows, written to the caches, one thread per (token, kv head, dim). prefill_attention_kernel: workgroup (hq,
+// b) of 4 wavefronts takes query head hq and the 4 queries t = 4 b .. 4 b +
+// 3, one per wavefront (num_heads * ceil(T / 4) workgroups); it stages the k
+// and v rows of the slots its last query sees from the caches (16-byte
+// loads) and the rotary q of its queries, and computes softmax(q k^T / 8) v
+// in fp32 with an online softmax over 64-slot chunks; query t sees slots 0 ..
+// start + t. qkv rows (stride (num_heads + 2 num_kv) * 64) hold [q | k | v]
+// as the decode step's; output [T, num_heads * 64] fp16. LDS: q [4][64]
+// fp32, k and v [slots][kRow] fp16 (rows padded to 72 halves, so a wavefront
+// reading 64 rows spreads over the banks). The rotary k is computed once per
+// (token, kv head), not once per workgroup that sees it. Up to
+// kPrefillOneLaunch tokens the attention launch does the append itself
+// (FUSED): each workgroup computes the rotary k of the new slots it sees, and
+// the workgroups of the group's first query head write their own 4 tokens'
+// rows to the caches; at those lengths the recomputation costs less than a
+// second launch.
 constexpr int kPrefillRow = 72;
+constexpr int kPrefillOneLaunch = 16;
 constexpr int kPrefillMaxSlots = 256;   // start + tokens: 73 KiB of LDS at 256 slots
 constexpr int kPrefillQueries = 4;      // queries per workgroup, one per wavefront
 
 __global__ void __launch_bounds__(256)
+prefill_rope_append_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
+                           const float* __restrict__ cos_table, const float* __restrict__ sin_table, int start,
+                           int T, int num_heads, int num_kv, int S) {
+    constexpr int D = 64;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)T * num_kv * D) return;
+    const int d = (int)(i % D);
+    const int hk = (int)((i / D) % num_kv);
+    const int t = (int)(i / ((int64_t)D * num_kv));
+    const int slot = start + t;
+    const f16* row = qkv + (size_t)t * (num_heads + 2 * num_kv) * D;
+    const f16* k = row + (size_t)num_heads * D + (size_t)hk * D;
+    const f16* v = row + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
+    const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
+    const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
+    const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
+    k_cache[((size_t)hk * S + slot) * D + d] = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
+    v_cache[((size_t)hk * S + slot) * D + d] = v[d];
+}
+
+template <bool FUSED>
+__global__ void __launch_bounds__(256)
 prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
-                         const float* __restrict__ cos_table, const float* __restrict__ sin_table, int start,
-                         int T, f16* __restrict__ out, int num_heads, int num_kv, int S) {
+                         const float* __restrict__ cos_table, const float* __restrict__ sin_table, int start, int T,
+                         f16* __restrict__ out, int num_heads, int num_kv, int S) {
     constexpr int D = 64;
     constexpr int QB = kPrefillQueries;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -785,41 +814,49 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
     const int hq = blockIdx.x;
     const int group = num_heads / num_kv;
     const int hk = hq / group;
-    const bool writer = hq % group == 0;   // appends the rows of tokens t0 .. t0 + tq - 1
     const int row_stride = (num_heads + 2 * num_kv) * D;
 
-    // earlier slots from the caches (16 bytes per thread and step)
-    for (int i = threadIdx.x; i < start * 8; i += 256) {
+    // the visible slots' k and v rows from the caches (16 bytes per thread
+    // and step): all of them, or (FUSED) those below start
+    const int cached = FUSED ? start : NK;
+    for (int i = threadIdx.x; i < cached * 8; i += 256) {
         const int srow = i >> 3, c = i & 7;
         const size_t g = ((size_t)hk * S + srow) * D;
         reinterpret_cast<u32x4*>(ks + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(k_cache + g)[c];
         reinterpret_cast<u32x4*>(vs + srow * kPrefillRow)[c] = reinterpret_cast<const u32x4*>(v_cache + g)[c];
     }
-    // the new tokens this workgroup sees: rotary k, v as is; rotary q of its
-    // own queries
-    const int tk = t0 + tq;
-    for (int i = threadIdx.x; i < tk * D; i += 256) {
-        const int t = i / D, d = i - t * D;
-        const int slot = start + t;
-        const f16* row = qkv + (size_t)t * row_stride;
-        const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
-        const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
-        const f16* k = row + (size_t)num_heads * D + (size_t)hk * D;
-        const f16* v = row + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
-        const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
-        const f16 kr = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
-        const f16 vv = v[d];
-        ks[slot * kPrefillRow + d] = kr;
-        vs[slot * kPrefillRow + d] = vv;
-        if (t >= t0) {
-            const f16* q = row + (size_t)hq * D;
-            const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
-            qs[(t - t0) * D + d] = (float)(f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
-            if (writer) {
+    if (FUSED) {
+        // the new slots it sees: rotary k and v; the group's first query head
+        // appends the rows of its own tokens t0 .. t0 + tq - 1
+        const bool writer = hq % group == 0;
+        for (int i = threadIdx.x; i < (t0 + tq) * D; i += 256) {
+            const int t = i / D, d = i - t * D;
+            const int slot = start + t;
+            const f16* row = qkv + (size_t)t * row_stride;
+            const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
+            const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
+            const f16* k = row + (size_t)num_heads * D + (size_t)hk * D;
+            const f16* v = row + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
+            const float k1 = (float)k[d & 31], k2 = (float)k[(d & 31) + 32];
+            const f16 kr = (f16)(d < 32 ? k1 * c - k2 * sn : k2 * c + k1 * sn);
+            const f16 vv = v[d];
+            ks[slot * kPrefillRow + d] = kr;
+            vs[slot * kPrefillRow + d] = vv;
+            if (writer && t >= t0) {
                 k_cache[((size_t)hk * S + slot) * D + d] = kr;
                 v_cache[((size_t)hk * S + slot) * D + d] = vv;
             }
         }
+    }
+    // rotary q of this workgroup's queries
+    for (int i = threadIdx.x; i < tq * D; i += 256) {
+        const int tl = i / D, d = i - tl * D;
+        const int slot = start + t0 + tl;
+        const f16* q = qkv + (size_t)(t0 + tl) * row_stride + (size_t)hq * D;
+        const float c = cos_table[(size_t)slot * (D / 2) + (d & 31)];
+        const float sn = sin_table[(size_t)slot * (D / 2) + (d & 31)];
+        const float q1 = (float)q[d & 31], q2 = (float)q[(d & 31) + 32];
+        qs[tl * D + d] = (float)(f16)(d < 32 ? q1 * c - q2 * sn : q2 * c + q1 * sn);
     }
     __syncthreads();
 
@@ -1082,17 +1119,27 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
         return fail(W4A16_ERR_ALIGNMENT, "prefill attention: caches must be 16-byte aligned, qkv and output 2-byte");
     const int nk = (int)(start + tokens);   // slots the last query block sees
     const size_t lds = (size_t)w4a16::kPrefillQueries * 64 * 4 + (size_t)2 * nk * w4a16::kPrefillRow * 2;
-    const void* kern = reinterpret_cast<const void*>(w4a16::prefill_attention_kernel);
+    const bool fused = tokens <= w4a16::kPrefillOneLaunch;
+    const auto attend = fused ? w4a16::prefill_attention_kernel<true> : w4a16::prefill_attention_kernel<false>;
+    const void* kern = reinterpret_cast<const void*>(attend);
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
     }
     const unsigned blocks = (unsigned)((tokens + w4a16::kPrefillQueries - 1) / w4a16::kPrefillQueries);
-    hipLaunchKernelGGL(w4a16::prefill_attention_kernel, dim3((unsigned)num_heads, blocks), dim3(256), lds,
-                       static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
-                       static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
-                       (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads,
-                       (int)max_seq_len);
+    if (!fused) {
+        const int64_t appends = tokens * num_kv_heads * 64;
+        hipLaunchKernelGGL(w4a16::prefill_rope_append_kernel, dim3((unsigned)((appends + 255) / 256)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
+                           (int)start, (int)tokens, (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
+        const int rc = check_launch();
+        if (rc != W4A16_OK) return rc;
+    }
+    hipLaunchKernelGGL(attend, dim3((unsigned)num_heads, blocks), dim3(256), lds, static_cast<hipStream_t>(stream),
+                       static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),
+                       static_cast<w4a16::f16*>(v_cache), cos_table, sin_table, (int)start, (int)tokens,
+                       static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
     return check_launch();
 }
 
