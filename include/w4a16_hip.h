@@ -47,6 +47,7 @@ extern "C" {
 #define W4A16_KERNEL_GEMM 10         /* fp16 MFMA GEMM on weights decoded in registers (M > 16, prompts) */
 #define W4A16_KERNEL_PAIR_STREAM 11  /* paired MFMA, resident workgroups streaming 8-row blocks (2 <= M <= 8) */
 #define W4A16_KERNEL_GEMM_LDS 12     /* GEMM with the activation block staged in LDS per round of groups (large M) */
+#define W4A16_KERNEL_PAIR_SPLIT 13   /* PAIR_STREAM over K slices, fp32 partials in a workspace + reduce (2 <= M <= 8) */
 
 /*
  * Fused W4A16 linear layer.
@@ -68,6 +69,29 @@ extern "C" {
 int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights,
                      const void* scales, void* output, int64_t M, int64_t N,
                      int64_t K, int64_t group_size, void* stream);
+
+/*
+ * Bytes of workspace w4a16_linear_ws_f16 uses for these sizes with group
+ * size 128 and 16-byte aligned activations and weights under the default
+ * routing (0: none). No reference counterpart (the reference's kernels keep
+ * no partial sums).
+ */
+int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size);
+
+/*
+ * w4a16_linear_f16 with a caller workspace (device memory, 16-byte aligned,
+ * contents ignored; workspace_bytes >= w4a16_linear_workspace_bytes): with
+ * it, M = 3..8 layers with K > 16384 and N >= 4096 take
+ * W4A16_KERNEL_PAIR_SPLIT, the streaming paired kernel over K slices whose
+ * fp32 partial sums are added in slice order by a second launch. workspace == NULL routes exactly as w4a16_linear_f16;
+ * a smaller non-NULL workspace is W4A16_ERR_CONFIG. The torch op
+ * w4a16::linear (reference csrc/int4_linear.cpp:16-28) calls this entry
+ * point with a workspace from the caching allocator.
+ */
+int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights,
+                        const void* scales, void* output, int64_t M, int64_t N,
+                        int64_t K, int64_t group_size, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /*
  * Dequantize packed INT4 weights to fp16 [N, K]: out = fp16_rn(code * scale),
@@ -151,6 +175,11 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     row blocks with the workgroups resident at once; else 1..16), unroll =
  *     group pairs in flight per wavefront (2|3|4|6), max_blocks = grid cap
  *     (0 = none), splits ignored.
+ *   W4A16_KERNEL_PAIR_SPLIT (2 <= M <= 8, K <= 65536, needs a workspace of
+ *     splits * M * N * 4 bytes): splits = K slices (2..16, every slice
+ *     non-empty, M K / splits activations in LDS), rows = wavefronts per
+ *     workgroup (0 = automatic; else 1..16), unroll = group pairs in flight
+ *     (2|3|4|6), max_blocks = workgroups per slice cap (0 = none).
  *   W4A16_KERNEL_GEMM (any M; every operand below 4 GiB): rows = 16-row
  *     activation tiles per wavefront (1|2|4), max_blocks = 16-row weight
  *     tiles per wavefront (1|2|4), splits = wavefronts splitting K (2|4|8;
@@ -163,13 +192,16 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte
- * aligned activations and weights. No reference counterpart (the reference's
- * W4A16_DECODE / W4A16_ROWS_PER_WARP selectors play this role).
+ * aligned activations and weights. workspace / workspace_bytes: as for
+ * w4a16_linear_ws_f16 (only W4A16_KERNEL_PAIR_SPLIT uses them; NULL / 0
+ * otherwise). No reference counterpart (the reference's W4A16_DECODE /
+ * W4A16_ROWS_PER_WARP selectors play this role).
  */
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,
                            const void* scales, void* output, int64_t M, int64_t N,
                            int64_t K, int64_t group_size, void* stream,
-                           int kernel, int rows, int splits, int unroll, int max_blocks);
+                           int kernel, int rows, int splits, int unroll, int max_blocks,
+                           void* workspace, int64_t workspace_bytes);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* w4a16_last_error(void);

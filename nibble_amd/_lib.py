@@ -38,12 +38,13 @@ KERNEL_STREAM = 9
 KERNEL_GEMM = 10
 KERNEL_PAIR_STREAM = 11
 KERNEL_GEMM_LDS = 12
+KERNEL_PAIR_SPLIT = 13
 KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic",
                 KERNEL_DIAG: "diag", KERNEL_VALU_OFFSET: "valu_offset",
                 KERNEL_ONESHOT: "oneshot", KERNEL_MFMA_ONESHOT: "mfma_oneshot",
                 KERNEL_MFMA_PAIR: "mfma_pair", KERNEL_STREAM: "stream",
                 KERNEL_GEMM: "gemm", KERNEL_PAIR_STREAM: "pair_stream",
-                KERNEL_GEMM_LDS: "gemm_lds"}
+                KERNEL_GEMM_LDS: "gemm_lds", KERNEL_PAIR_SPLIT: "pair_split"}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -56,9 +57,11 @@ SIGNATURES = {
     "w4a16_check_linear_shapes": (ctypes.c_int, [_i64] * 7),
     "w4a16_check_dequantize_shapes": (ctypes.c_int, [_i64] * 5 + [ctypes.c_uint64]),
     "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip, _ip]),
+    "w4a16_linear_workspace_bytes": (_i64, [_i64] * 4),
+    "w4a16_linear_ws_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w4a16_linear_f16_tuned": (
         ctypes.c_int,
-        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp] + [ctypes.c_int] * 5,
+        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp] + [ctypes.c_int] * 5 + [_vp, _i64],
     ),
     "w4a16_last_error": (ctypes.c_char_p, []),
     "w4a16_version": (ctypes.c_char_p, []),
@@ -129,26 +132,57 @@ def _stream_ptr(stream) -> int:
     return int(stream.cuda_stream)
 
 
-def linear_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None) -> None:
-    """Run ``w4a16_linear_f16`` on torch device tensors (no checks beyond the C ABI's)."""
+def linear_workspace_bytes(m: int, n: int, k: int, group_size: int = 128) -> int:
+    """Workspace bytes ``w4a16_linear_ws_f16`` uses for these sizes (host-only)."""
+    return int(lib().w4a16_linear_workspace_bytes(m, n, k, group_size))
+
+
+def _workspace(nbytes: int, device):
+    return torch.empty(((nbytes + 3) // 4,), dtype=torch.float32, device=device)
+
+
+def linear_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None,
+               workspace="auto") -> None:
+    """Run the W4A16 linear layer on torch device tensors (no checks beyond the
+    C ABI's): ``w4a16_linear_ws_f16`` with a workspace from the caching
+    allocator when the plan uses one (``workspace="auto"``, as the torch op
+    does), a given fp32 tensor, or ``None`` for ``w4a16_linear_f16``."""
     m, k = activations.shape
     n = packed_weights.shape[0]
+    if isinstance(workspace, str):
+        nbytes = linear_workspace_bytes(m, n, k, group_size)
+        workspace = _workspace(nbytes, output.device) if nbytes > 0 else None
+    if workspace is None:
+        _raise_on(
+            lib().w4a16_linear_f16(
+                activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
+                m, n, k, group_size, _stream_ptr(stream),
+            )
+        )
+        return
     _raise_on(
-        lib().w4a16_linear_f16(
+        lib().w4a16_linear_ws_f16(
             activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
-            m, n, k, group_size, _stream_ptr(stream),
+            m, n, k, group_size, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            _stream_ptr(stream),
         )
     )
 
 
 def linear_f16_tuned(activations, packed_weights, scales, output, group_size, kernel, rows, splits, unroll,
-                     max_blocks=0, stream=None) -> None:
+                     max_blocks=0, stream=None, workspace=None) -> None:
+    """``w4a16_linear_f16_tuned``; the split-K family gets a workspace of
+    splits * M * N fp32 from the caching allocator unless one is given."""
     m, k = activations.shape
     n = packed_weights.shape[0]
+    if workspace is None and kernel == KERNEL_PAIR_SPLIT:
+        workspace = _workspace(max(1, splits) * m * n * 4, output.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _raise_on(
         lib().w4a16_linear_f16_tuned(
             activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
-            m, n, k, group_size, _stream_ptr(stream), kernel, rows, splits, unroll, max_blocks,
+            m, n, k, group_size, _stream_ptr(stream), kernel, rows, splits, unroll, max_blocks, ws_ptr, ws_bytes,
         )
     )
 

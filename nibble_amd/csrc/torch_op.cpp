@@ -52,8 +52,14 @@ at::Tensor linear(const at::Tensor& activations, const at::Tensor& packed_weight
     at::Tensor output = at::empty({M, N}, activations.options());
     if (M * N == 0) return output;
 
-    rc = w4a16_linear_f16(activations.data_ptr(), packed_weights.data_ptr<uint8_t>(), scales.data_ptr(),
-                          output.data_ptr(), M, N, K, group_size, current_stream(activations.device()));
+    // partial sums of the split-K kernel, from the caching allocator (so the
+    // op stays graph-capture safe)
+    const int64_t ws_bytes = w4a16_linear_workspace_bytes(M, N, K, group_size);
+    at::Tensor workspace;
+    if (ws_bytes > 0) workspace = at::empty({(ws_bytes + 3) / 4}, activations.options().dtype(at::kFloat));
+    rc = w4a16_linear_ws_f16(activations.data_ptr(), packed_weights.data_ptr<uint8_t>(), scales.data_ptr(),
+                             output.data_ptr(), M, N, K, group_size, ws_bytes > 0 ? workspace.data_ptr() : nullptr,
+                             ws_bytes, current_stream(activations.device()));
     TORCH_CHECK(rc == W4A16_OK, w4a16_last_error());
     return output;
 }

@@ -30,6 +30,11 @@ bool pair_stream_instantiated(int depth);
 int pair_stream_waves(int64_t M, int64_t N, int64_t K);
 int launch_pair_stream(int depth, int waves, int max_blocks, int M, const void* x, const uint8_t* w, const void* s,
                        void* o, int N, int K, hipStream_t stream);
+int64_t pair_split_lds(int64_t M, int64_t K, int slices);
+int64_t pair_split_workspace_bytes(int64_t M, int64_t N, int slices);
+bool pair_split_valid(int64_t K, int slices);
+int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, const void* x, const uint8_t* w,
+                      const void* s, void* o, int N, int K, void* part, int64_t part_bytes, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -432,6 +437,44 @@ bool pair_stream_fits(int64_t M, int64_t K) {
            w4a16_internal::pair_stream_lds(M, K) <= kMaxLdsBytes;
 }
 
+// Split-K streaming paired kernel (w4a16_pair.h, M = 2..8 with a caller
+// workspace): rows too long for the whole-row kernels' LDS. Plan fields:
+// splits = K slices, rows = wavefronts per workgroup (0 = automatic), unroll
+// = pairs in flight, max_blocks = workgroups per slice cap (0 = none).
+// Measured (sweep of slices 2..16, depth 3/4/6, 0/8/16 wavefronts, graph
+// timing over 5 rotated copies): K = 28672 x N = 8192 takes 30.1 us at M =
+// 8 (4 slices, depth 4, automatic wavefronts) against 38.9 on the paired
+// kernel, 28.4 against 30.8 at M = 4; at K <= 14336 the reduce launch costs
+// more than the split saves (14336 x 4096 M = 8: 12.5 against 11.0; 8192 x
+// 8192: 13.2 against 11.3; 8192 x 28672: 33.0 against 29.8 streaming whole
+// rows). Slices: the fewest from 4 up whose staging fits in LDS.
+constexpr int64_t kPairSplitMinN = 4096;
+constexpr int64_t kPairSplitMinK = 16384;   // K above this
+
+Plan plan_pair_split(int64_t M, int64_t N, int64_t K) {
+    Plan p;
+    p.kernel = W4A16_KERNEL_PAIR_SPLIT;
+    p.rows = 0;
+    p.unroll = 4;
+    p.max_blocks = 0;
+    p.splits = 4;
+    while (p.splits < 16 && w4a16_internal::pair_split_lds(M, K, p.splits) > kMaxLdsBytes) ++p.splits;
+    while (p.splits > 2 && !w4a16_internal::pair_split_valid(K, p.splits)) --p.splits;
+    (void)N;
+    return p;
+}
+
+bool pair_split_fits(int64_t M, int64_t N, int64_t K) {
+    if (M < 2 || M > 8 || K < 256 || K % 128 != 0 || K > 65536 || N * (K / 2) >= ((int64_t)1 << 32)) return false;
+    const Plan p = plan_pair_split(M, N, K);
+    return w4a16_internal::pair_split_valid(K, p.splits) &&
+           w4a16_internal::pair_split_lds(M, K, p.splits) <= kMaxLdsBytes;
+}
+
+bool pair_split_route(int64_t M, int64_t N, int64_t K) {
+    return M >= 3 && N >= kPairSplitMinN && K > kPairSplitMinK && pair_split_fits(M, N, K);
+}
+
 // M = 9..16 on the paired kernel: two launches, rows [0, m1) and [m1, M) with
 // m1 = ceil(M/2) (each half 4..8 rows), each with its own launch shape unless
 // the caller fixed one; the weights are streamed twice.
@@ -451,7 +494,8 @@ int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16
     return W4A16_OK;
 }
 
-int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out) {
+int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out,
+              bool workspace = false) {
     int family = 0, rows = 0;
     const int rc = read_env(&family, &rows);
     if (rc != W4A16_OK) return rc;
@@ -507,6 +551,10 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     //   MFMA up to K = 8192 when N >= 4096 gives it enough row blocks;
     //   otherwise the looped VALU kernel for M = 1, M = 2 (K <= 16384) or
     //   M <= 4 (K <= 4096), else the looped MFMA kernel.
+    if (family == 0 && rows == 0 && workspace && pair_split_route(M, N, K)) {
+        *out = plan_pair_split(M, N, K);
+        return W4A16_OK;
+    }
     if (family == 0) {
         const bool small = K <= 5632 && N <= 5632;
         if (rows == 0 && M == 1 && K >= kStreamMinK && N >= kStreamMinN && stream_fits(K))
@@ -820,7 +868,8 @@ int check_scalar_args(int64_t M, int64_t N, int64_t K, int64_t G) {
 }
 
 int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* scales, void* out,
-             int64_t M, int64_t N, int64_t K, int64_t G, void* stream, bool own_plans = true) {
+             int64_t M, int64_t N, int64_t K, int64_t G, void* stream, bool own_plans = true,
+             void* workspace = nullptr, int64_t workspace_bytes = 0) {
     using w4a16::f16;
     const f16* x = static_cast<const f16*>(act);
     const f16* s = static_cast<const f16*>(scales);
@@ -842,6 +891,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_PAIR_STREAM:
             return w4a16_internal::launch_pair_stream(p.unroll, p.rows, p.max_blocks, (int)M, x, packed, s, o, (int)N,
                                                       (int)K, st);
+        case W4A16_KERNEL_PAIR_SPLIT:
+            return w4a16_internal::launch_pair_split(p.unroll, p.rows, p.splits, p.max_blocks, (int)M, x, packed, s, o,
+                                                     (int)N, (int)K, workspace, workspace_bytes, st);
         case W4A16_KERNEL_GEMM:
             return w4a16_internal::launch_gemm(p.rows, p.max_blocks, p.splits, (int)M, x, packed, s, o, (int)N, (int)K,
                                                st);
@@ -921,22 +973,38 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, in
     return W4A16_OK;
 }
 
-int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
-                     void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream) {
+int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,
+                        int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
+                        int64_t workspace_bytes, void* stream) {
     int rc = check_scalar_args(M, N, K, group_size);
     if (rc != W4A16_OK) return rc;
     Plan p;
-    rc = make_plan(activations, packed_weights, M, N, K, group_size, &p);
+    rc = make_plan(activations, packed_weights, M, N, K, group_size, &p, workspace != nullptr);
     if (rc != W4A16_OK) return rc;
     if (p.kernel == W4A16_KERNEL_NONE) return W4A16_OK;
     rc = check_pointers(activations, packed_weights, scales, output);
     if (rc != W4A16_OK) return rc;
-    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream);
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, true, workspace,
+                    workspace_bytes);
+}
+
+int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
+                     void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream) {
+    return w4a16_linear_ws_f16(activations, packed_weights, scales, output, M, N, K, group_size, nullptr, 0, stream);
+}
+
+int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+    if (check_scalar_args(M, N, K, group_size) != W4A16_OK || M * N == 0) return 0;
+    Plan p;
+    alignas(16) static const uint8_t probe[16] = {};   // stands for 16-byte aligned operands
+    if (make_plan(probe, probe, M, N, K, group_size, &p, true) != W4A16_OK) return 0;
+    return p.kernel == W4A16_KERNEL_PAIR_SPLIT ? w4a16_internal::pair_split_workspace_bytes(M, N, p.splits) : 0;
 }
 
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights, const void* scales,
                            void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream,
-                           int kernel, int rows, int splits, int unroll, int max_blocks) {
+                           int kernel, int rows, int splits, int unroll, int max_blocks, void* workspace,
+                           int64_t workspace_bytes) {
     int rc = check_scalar_args(M, N, K, group_size);
     if (rc != W4A16_OK) return rc;
     if (M * N == 0) return W4A16_OK;
@@ -962,6 +1030,11 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
             return fail(W4A16_ERR_CONFIG,
                         "the streaming paired kernel needs group_size 128, 2 <= M <= 8 and 16-byte aligned activations "
                         "and weights");
+    } else if (kernel == W4A16_KERNEL_PAIR_SPLIT) {
+        if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+            return fail(W4A16_ERR_CONFIG,
+                        "the split-K paired kernel needs group_size 128, 2 <= M <= 8 and 16-byte aligned activations "
+                        "and weights");
     } else if (kernel == W4A16_KERNEL_MFMA_PAIR) {
         if (group_size != 128 || M < 2 || M > 16 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
@@ -979,9 +1052,10 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_PAIR_STREAM, _STREAM, _GEMM, _GEMM_LDS, _DIAG or _GENERIC");
+                    "_PAIR_STREAM, _PAIR_SPLIT, _STREAM, _GEMM, _GEMM_LDS, _DIAG or _GENERIC");
     }
-    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false);
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false, workspace,
+                    workspace_bytes);
 }
 
 int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float eps,

@@ -299,20 +299,38 @@ namespace w4a16 {
 // staging. The loop's tail is peeled, so no load sits behind a branch; a
 // wavefront with no task requests D pairs of the grid's last block and
 // stores nothing.
+//
+// SPLIT (split K, for rows whose M K activations do not fit in LDS): the
+// pairs of a row are cut into S slices of ceil(P / S) pairs; workgroup b
+// takes slice b mod S (it stages only that slice's activations) and the
+// tasks of that slice with its gridDim / S peers, and stores fp32 partial
+// sums to part[slice][m][n]; pair_split_reduce adds the S slices in slice
+// order and rounds to fp16.
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int64_t pair_stream_lds_bytes(int64_t M, int64_t pairs) {
     return pairs * 16 * (2 * pair_row_slots((int)M)) * 16 + pairs * 2 * 64;
 }
 
-template <int MS, int D>
+template <int MS, int D, bool SPLIT = false>
 __global__ void __launch_bounds__(1024)
 gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
-                 f16* __restrict__ out, int M, int N, int K) {
+                 f16* __restrict__ out, int M, int N, int K, float* __restrict__ part, int S) {
     constexpr int LS = 2 * MS;   // units per line
     constexpr int B = 8;         // staging units per thread requested at a time
     extern __shared__ __align__(16) uint8_t smem[];
-    const int G = K >> 7;
-    const int P = (G + 1) >> 1;                                              // pairs per row
+    const int Gall = K >> 7;                                                 // groups per row
+    const int Pall = (Gall + 1) >> 1;                                        // pairs per row
+    int sl = 0, peer = blockIdx.x, peers = gridDim.x, pair0 = 0, P = Pall;
+    if (SPLIT) {   // slice sl: pairs pair0 .. pair0 + P - 1 (the host keeps every slice non-empty)
+        const int PS = (Pall + S - 1) / S;
+        sl = blockIdx.x % S;
+        peer = blockIdx.x / S;
+        peers = gridDim.x / S;
+        pair0 = sl * PS;
+        P = min(PS, Pall - pair0);
+    }
+    const int g0 = 2 * pair0;              // first group of the slice
+    const int G = min(2 * P, Gall - g0);   // groups of the slice
     u32x4* xs = reinterpret_cast<u32x4*>(smem);                              // [P * 16 lines][LS]
     float* base = reinterpret_cast<float*>(smem + (size_t)P * 16 * LS * 16); // [2 P][16]
     const int T = blockDim.x;
@@ -325,8 +343,8 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
     const int upr = K >> 3;            // 16-byte units per activation row
     const int CU = 32 * P;             // staged units per activation row (2 P groups x 16)
     const int NB = (N + 7) >> 3;       // 8-row blocks
-    const int task0 = blockIdx.x * W + wave;
-    const int stride = gridDim.x * W;
+    const int task0 = peer * W + wave;
+    const int stride = peers * W;
     const int my_tasks = task0 < NB ? (NB - 1 - task0) / stride + 1 : 0;
     const int units = my_tasks * P;
 
@@ -343,7 +361,8 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
             const int m = i / CU, ul = i % CU;
             const int g = ul >> 4;
             const bool valid = m < M && g < G && i < MS * CU;
-            a[p] = *reinterpret_cast<const u32x4*>(x + (valid ? ((size_t)m * upr + (size_t)g * 16 + (ul & 15)) * 8 : 0));
+            a[p] = *reinterpret_cast<const u32x4*>(
+                x + (valid ? ((size_t)m * upr + (size_t)(g0 + g) * 16 + (ul & 15)) * 8 : 0));
         }
     };
     auto stage_put = [&](const u32x4 (&a)[B], int first) {
@@ -379,8 +398,8 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
     const uint8_t* sbytes = reinterpret_cast<const uint8_t*>(scales);
     auto load = [&](int d, int task, int pr) {
         const uint32_t n = (uint32_t)min(task * 8 + brow, N - 1);
-        const uint32_t gi = (uint32_t)min(2 * pr + bhalf, G - 1);
-        sv[d] = *reinterpret_cast<const uint16_t*>(sbytes + (n * (uint32_t)G + gi) * 2u);
+        const uint32_t gi = (uint32_t)min(g0 + 2 * pr + bhalf, Gall - 1);
+        sv[d] = *reinterpret_cast<const uint16_t*>(sbytes + (n * (uint32_t)Gall + gi) * 2u);
         wv[d] = load_stream(reinterpret_cast<const u32x4*>(w + (n * row_bytes + gi * 64u + (uint32_t)q * 16u)));
     };
 
@@ -440,7 +459,12 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int m = 4 * q + e;
-                    if (m < M) out[(size_t)m * N + nn] = (f16)v[e];
+                    if (m < M) {
+                        if (SPLIT)
+                            part[((size_t)sl * M + m) * N + nn] = v[e];
+                        else
+                            out[(size_t)m * N + nn] = (f16)v[e];
+                    }
                 }
             }
             acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -476,6 +500,26 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
 #pragma unroll
         for (int d = 0; d < D; ++d)
             if (d < units) compute(d);
+    }
+}
+
+// out[i] = fp16(part[0][i] + part[1][i] + ... + part[S - 1][i]) over the
+// MN = M N outputs, 4 per thread (16-byte loads when MN % 4 == 0).
+__global__ void __launch_bounds__(256)
+pair_split_reduce(const float* __restrict__ part, f16* __restrict__ out, int S, int MN) {
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= MN) return;
+    if ((MN & 3) == 0) {
+        f32x4 acc = *reinterpret_cast<const f32x4*>(part + i);
+        for (int s = 1; s < S; ++s) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * MN + i);
+        const f16x2 lo = {(f16)acc[0], (f16)acc[1]}, hi = {(f16)acc[2], (f16)acc[3]};
+        *reinterpret_cast<uint2*>(out + i) = make_uint2(as_u32(lo), as_u32(hi));
+        return;
+    }
+    for (int e = i; e < min(i + 4, MN); ++e) {
+        float acc = part[e];
+        for (int s = 1; s < S; ++s) acc += part[(size_t)s * MN + e];
+        out[e] = (f16)acc;
     }
 }
 

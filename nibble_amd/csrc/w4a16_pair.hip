@@ -26,7 +26,7 @@ constexpr int kChunkPairs = 8;   // group pairs per staged chunk (K = 2048 per c
 // behind all of the weights.
 constexpr int kLookahead = 2;
 
-int fail(int code, const char* message) {
+int fail(int code, const std::string& message) {
     w4a16_internal::set_last_error(message);
     return code;
 }
@@ -184,27 +184,33 @@ int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, c
 int64_t pair_stream_lds(int64_t M, int64_t K) { return w4a16::pair_stream_lds_bytes(M, (K / 128 + 1) / 2); }
 
 namespace {
-using StreamKern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int);
-template <int MS>
+using StreamKern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int,
+                           float*, int);
+template <int MS, bool SPLIT = false>
 StreamKern pick_stream(int depth) {
     using namespace w4a16;
     switch (depth) {
-        case 2: return gemv_pair_stream<MS, 2>;
-        case 3: return gemv_pair_stream<MS, 3>;
-        case 4: return gemv_pair_stream<MS, 4>;
-        case 6: return gemv_pair_stream<MS, 6>;   // deeper rings spill within 128 VGPRs (1024 threads)
+        case 2: return gemv_pair_stream<MS, 2, SPLIT>;
+        case 3: return gemv_pair_stream<MS, 3, SPLIT>;
+        case 4: return gemv_pair_stream<MS, 4, SPLIT>;
+        case 6: return gemv_pair_stream<MS, 6, SPLIT>;   // deeper rings spill within 128 VGPRs (1024 threads)
         default: return nullptr;
     }
+}
+
+int cu_count() {
+    int cus = 0, device = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
+        cus = 256;
+    return cus;
 }
 }  // namespace
 
 bool pair_stream_instantiated(int depth) { return pick_stream<8>(depth) != nullptr; }
 
 int pair_stream_waves(int64_t M, int64_t N, int64_t K) {
-    int cus = 0, device = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus < 1)
-        cus = 256;
+    const int cus = cu_count();
     const int64_t per_cu = std::max<int64_t>(1, kMaxLdsBytes / std::max<int64_t>(1, pair_stream_lds(M, K)));
     const int64_t blocks = (N + 7) / 8;
     const int64_t resident = per_cu * cus;
@@ -230,8 +236,73 @@ int launch_pair_stream(int depth, int waves, int max_blocks, int M, const void* 
     int grid = (blocks + waves - 1) / waves;
     if (max_blocks > 0 && grid > max_blocks) grid = max_blocks;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * waves), (size_t)lds, stream, static_cast<const w4a16::f16*>(x), w,
-                       static_cast<const w4a16::f16*>(s), static_cast<w4a16::f16*>(o), M, N, K);
+                       static_cast<const w4a16::f16*>(s), static_cast<w4a16::f16*>(o), M, N, K, nullptr, 1);
     const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));
+        return W4A16_ERR_LAUNCH;
+    }
+    return W4A16_OK;
+}
+
+// Split-K streaming paired kernel: `slices` K slices of ceil(P / slices)
+// pairs (P = K / 256 rounded up), each staged by its own workgroups; fp32
+// partial sums in `part` ([slices][M][N], pair_split_workspace_bytes), then
+// pair_split_reduce into `o`. waves = 0: the fewest wavefronts per workgroup
+// (at most 16) with which slices x ceil(N / 8 / waves) workgroups fit on
+// the device at once by LDS; max_blocks > 0 caps the workgroups per slice.
+int64_t pair_split_lds(int64_t M, int64_t K, int slices) {
+    const int64_t pairs = (K / 128 + 1) / 2;
+    return w4a16::pair_stream_lds_bytes(M, (pairs + slices - 1) / slices);
+}
+
+int64_t pair_split_workspace_bytes(int64_t M, int64_t N, int slices) { return (int64_t)slices * M * N * 4; }
+
+bool pair_split_valid(int64_t K, int slices) {
+    const int64_t pairs = (K / 128 + 1) / 2;
+    return slices >= 2 && slices <= 16 && (int64_t)(slices - 1) * ((pairs + slices - 1) / slices) < pairs;
+}
+
+int pair_split_waves(int64_t M, int64_t N, int64_t K, int slices) {
+    const int64_t per_cu = std::max<int64_t>(1, kMaxLdsBytes / std::max<int64_t>(1, pair_split_lds(M, K, slices)));
+    const int64_t resident = per_cu * cu_count();
+    const int64_t blocks = (N + 7) / 8 * slices;
+    return (int)std::min<int64_t>(16, std::max<int64_t>(1, (blocks + resident - 1) / resident));
+}
+
+int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, const void* x, const uint8_t* w,
+                      const void* s, void* o, int N, int K, void* part, int64_t part_bytes, hipStream_t stream) {
+    if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "split-K paired kernel needs 2 <= M <= 8");
+    if (K < 128 || K % 128 != 0 || K > 65536)
+        return fail(W4A16_ERR_CONFIG, "split-K paired kernel: K must be a multiple of 128 up to 65536");
+    if ((int64_t)N * (K / 2) >= ((int64_t)1 << 32))
+        return fail(W4A16_ERR_TOO_LARGE, "split-K paired kernel: weights must be below 4 GiB");
+    if (!pair_split_valid(K, slices))
+        return fail(W4A16_ERR_CONFIG, "split-K paired kernel: splits (K slices) 2..16, each slice non-empty");
+    const StreamKern kern = M <= 4 ? pick_stream<4, true>(depth) : pick_stream<8, true>(depth);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "split-K paired kernel: unroll (pairs in flight) 2, 3, 4 or 6");
+    if (waves == 0) waves = pair_split_waves(M, N, K, slices);
+    if (waves < 1 || waves > 16) return fail(W4A16_ERR_CONFIG, "split-K paired kernel: rows (wavefronts) 1..16");
+    const int64_t need = pair_split_workspace_bytes(M, N, slices);
+    if (part == nullptr || part_bytes < need || (reinterpret_cast<uintptr_t>(part) & 15u))
+        return fail(W4A16_ERR_CONFIG, "split-K paired kernel: needs a 16-byte aligned workspace of " +
+                                          std::to_string(need) + " bytes (w4a16_linear_workspace_bytes)");
+    const int64_t lds = pair_split_lds(M, K, slices);
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "split-K paired kernel: a slice does not fit in LDS");
+    const int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    int per_slice = ((N + 7) / 8 + waves - 1) / waves;
+    if (max_blocks > 0 && per_slice > max_blocks) per_slice = max_blocks;
+    hipLaunchKernelGGL(kern, dim3(per_slice * slices), dim3(64 * waves), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, N, K, static_cast<float*>(part), slices);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) {
+        const int64_t mn = (int64_t)M * N;
+        hipLaunchKernelGGL(w4a16::pair_split_reduce, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, stream,
+                           static_cast<const float*>(part), static_cast<w4a16::f16*>(o), slices, (int)mn);
+        e = hipGetLastError();
+    }
     if (e != hipSuccess) {
         set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));
         return W4A16_ERR_LAUNCH;

@@ -326,9 +326,46 @@ def test_scalar_argument_errors():
     assert lib.w4a16_linear_f16(None, None, None, None, 0, 8, 256, 128, None) == _lib.W4A16_OK
     assert lib.w4a16_dequantize_f16(None, None, None, 8, 256, 48, None) == _lib.W4A16_ERR_GROUP_SIZE
     assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 8, 256, 128, None,
-                                      _lib.KERNEL_VALU, 3, 1, 1, 0) == _lib.W4A16_ERR_CONFIG
+                                      _lib.KERNEL_VALU, 3, 1, 1, 0, None, 0) == _lib.W4A16_ERR_CONFIG
     assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 1, 8, 256, 64, None,
-                                      _lib.KERNEL_MFMA, 1, 1, 1, 0) == _lib.W4A16_ERR_CONFIG
+                                      _lib.KERNEL_MFMA, 1, 1, 1, 0, None, 0) == _lib.W4A16_ERR_CONFIG
+    # the split-K family without (or with too small) a workspace
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 4096, 28672, 128, None,
+                                      _lib.KERNEL_PAIR_SPLIT, 0, 8, 4, 0, None, 0) == _lib.W4A16_ERR_CONFIG
+    assert "workspace" in _lib.last_error()
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 4096, 28672, 128, None,
+                                      _lib.KERNEL_PAIR_SPLIT, 0, 8, 4, 0, ALIGNED, 1024) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_linear_ws_f16(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 8192, 28672, 128, ALIGNED, 1024,
+                                   None) == _lib.W4A16_ERR_CONFIG
+    assert "workspace" in _lib.last_error()
+    # slices that leave one empty, or a slice too long for LDS
+    for splits in (1, 17):
+        assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 4096, 28672, 128, None,
+                                          _lib.KERNEL_PAIR_SPLIT, 0, splits, 4, 0, ALIGNED,
+                                          1 << 30) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 4096, 1024, 128, None,
+                                      _lib.KERNEL_PAIR_SPLIT, 0, 5, 4, 0, ALIGNED, 1 << 30) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_linear_f16_tuned(ALIGNED, ALIGNED, ALIGNED, ALIGNED, 8, 4096, 28672, 128, None,
+                                      _lib.KERNEL_PAIR_SPLIT, 0, 2, 4, 0, ALIGNED, 1 << 30) == _lib.W4A16_ERR_CONFIG
+    assert "LDS" in _lib.last_error()
+
+
+@pytest.mark.parametrize("m,n,k,splits", [
+    (8, 8192, 28672, None), (8, 4096, 14336, 0), (4, 8192, 28672, None), (3, 4096, 28672, None),
+    (3, 4096, 14336, 0), (5, 4096, 20480, None), (8, 4095, 28672, 0), (8, 8192, 16384, 0),
+    (8, 2048, 5632, 0), (8, 28672, 8192, 0), (1, 8192, 28672, 0), (2, 8192, 28672, 0), (16, 8192, 28672, 0),
+    (8, 4096, 4096, 0), (4, 4096, 8192, 0)])
+def test_linear_workspace_bytes(m, n, k, splits):
+    """M = 3..8 layers with K > 16384 and N >= 4096 use splits * M * N fp32
+    of workspace (the split-K kernel); everything else none."""
+    got = _lib.linear_workspace_bytes(m, n, k)
+    if splits == 0:
+        assert got == 0
+    else:
+        assert got > 0 and got % (m * n * 4) == 0
+        s = got // (m * n * 4)
+        assert 2 <= s <= 16
+    assert _lib.linear_workspace_bytes(m, n, k, 64) == 0   # other group sizes: the generic kernel
 
 
 def test_torch_op_schemas_match_reference():

@@ -23,6 +23,7 @@ STREAM = _lib.KERNEL_STREAM
 GEMM = _lib.KERNEL_GEMM
 PAIR_STREAM = _lib.KERNEL_PAIR_STREAM
 GEMM_LDS = _lib.KERNEL_GEMM_LDS
+PAIR_SPLIT = _lib.KERNEL_PAIR_SPLIT
 
 
 def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=0, group_size=128):
@@ -35,11 +36,12 @@ def _run_tuned(dev, x, packed, scales, kernel, rows, splits, unroll, max_blocks=
     return out
 
 
-def _run_default(dev, x, packed, scales, group_size=128):
+def _run_default(dev, x, packed, scales, group_size=128, workspace="auto"):
     xd, pd, sd = x.to(dev), packed.to(dev), scales.to(dev)
     out = torch.full((x.shape[0], packed.shape[0]), float("nan"), dtype=torch.float16, device=dev)
-    print(f"[case] default M={x.shape[0]} K={x.shape[1]} N={packed.shape[0]} G={group_size}", flush=True)
-    _lib.linear_f16(xd, pd, sd, out, group_size)
+    print(f"[case] default M={x.shape[0]} K={x.shape[1]} N={packed.shape[0]} G={group_size} ws={workspace is not None}",
+          flush=True)
+    _lib.linear_f16(xd, pd, sd, out, group_size, workspace=workspace)
     torch.cuda.synchronize()
     return out
 
@@ -272,7 +274,59 @@ def test_default_dispatch_pair_stream(gpu, m, k, n):
     group count at K = 4224)."""
     x, p, s = make_case(m, k, n, seed=m + k + n)
     assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == "pair_stream"
-    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"pair_stream default M={m} K={k} N={n}")
+    assert_parity(_run_default(gpu, x, p, s, workspace=None), expected(x, p, s),
+                  f"pair_stream default M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("depth", [2, 4, 6])
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+@pytest.mark.parametrize("k,n,splits", [(512, 7, 2), (1152, 100, 2), (1152, 33, 3), (2048, 2048, 4), (5504, 40, 11),
+                                        (9216, 9, 5), (14336, 64, 7), (28672, 24, 16)])
+def test_pair_split_variants(gpu, depth, m, k, n, splits):
+    """Split-K streaming paired kernel: slices of one pair, a last slice
+    shorter than the others and with an odd group count (K = 1152: 9 groups,
+    slices of 3 + 2 pairs, or 2 + 2 + 1 with a last slice of one group; 5504
+    over 11 slices: 2 pairs each, the last 3 groups), ragged N, M of 2..8, up
+    to K = 28672 in 16 slices."""
+    x, p, s = make_case(m, k, n, seed=m * 5 + k + n + depth + splits)
+    got = _run_tuned(gpu, x, p, s, PAIR_SPLIT, 0, splits, depth)
+    assert_parity(got, expected(x, p, s), f"pair_split d={depth} S={splits} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("waves,cap", [(1, 1), (3, 2), (16, 1), (5, 7)])
+@pytest.mark.parametrize("m,k,n,splits", [(4, 2048, 300, 2), (8, 1152, 97, 3), (8, 14336, 130, 4)])
+def test_pair_split_many_tasks(gpu, waves, cap, m, k, n, splits):
+    """Explicit wavefront counts and small caps on the workgroups per slice:
+    each wavefront streams many 8-row blocks of its slice."""
+    x, p, s = make_case(m, k, n, seed=waves * 13 + cap + m + splits)
+    got = _run_tuned(gpu, x, p, s, PAIR_SPLIT, waves, splits, 3, max_blocks=cap)
+    assert_parity(got, expected(x, p, s), f"pair_split waves={waves} cap={cap} S={splits} M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(8, 28672, 8192), (3, 28672, 8200), (5, 20480, 4096), (4, 16512, 4104)])
+def test_default_dispatch_pair_split(gpu, m, k, n):
+    """With a workspace, M = 3..8 layers with K > 16384 take the split-K
+    kernel (the torch op's route; ragged N; K = 16512 has 129 groups, so the
+    last of its 4 slices holds 27); without one, the same call takes the
+    workspace-free route, also within the bar."""
+    x, p, s = make_case(m, k, n, seed=m + k + n + 1)
+    assert _lib.linear_workspace_bytes(m, n, k) > 0
+    ref = expected(x, p, s)
+    assert_parity(_run_default(gpu, x, p, s), ref, f"pair_split default M={m} K={k} N={n}")
+    assert_parity(_run_default(gpu, x, p, s, workspace=None), ref, f"no workspace M={m} K={k} N={n}")
+
+
+def test_pair_split_workspace_reused(gpu):
+    """Two calls in a row on one workspace (the second smaller), each against
+    the oracle: partial sums of the first call do not leak into the second."""
+    ws = torch.full((8 * 4096 * 16,), float("nan"), dtype=torch.float32, device=gpu)
+    for m, k, n, splits in [(8, 14336, 4096, 14), (3, 2048, 1000, 2)]:
+        x, p, s = make_case(m, k, n, seed=k + m)
+        out = torch.full((m, n), float("nan"), dtype=torch.float16, device=gpu)
+        print(f"[case] pair_split workspace reuse M={m} K={k} N={n} S={splits}", flush=True)
+        _lib.linear_f16_tuned(x.to(gpu), p.to(gpu), s.to(gpu), out, 128, PAIR_SPLIT, 0, splits, 4, 0, workspace=ws)
+        torch.cuda.synchronize()
+        assert_parity(out, expected(x, p, s), f"pair_split reuse M={m} K={k} N={n}")
 
 
 def test_pair_stream_rejects(gpu):
