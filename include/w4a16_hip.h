@@ -81,7 +81,7 @@ int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gr
 /*
  * w4a16_linear_f16 with a caller workspace (device memory, 16-byte aligned,
  * contents ignored; workspace_bytes >= w4a16_linear_workspace_bytes): with
- * it, M = 3..8 layers with K > 16384 and N >= 4096 take
+ * it, M = 3..8 layers with K > 16384 and N >= 8192 take
  * W4A16_KERNEL_PAIR_SPLIT, the streaming paired kernel over K slices whose
  * fp32 partial sums are added in slice order by a second launch. workspace == NULL routes exactly as w4a16_linear_f16;
  * a smaller non-NULL workspace is W4A16_ERR_CONFIG. The torch op

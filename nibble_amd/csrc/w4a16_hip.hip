@@ -443,12 +443,14 @@ bool pair_stream_fits(int64_t M, int64_t K) {
 // = pairs in flight, max_blocks = workgroups per slice cap (0 = none).
 // Measured (sweep of slices 2..16, depth 3/4/6, 0/8/16 wavefronts, graph
 // timing over 5 rotated copies): K = 28672 x N = 8192 takes 30.1 us at M =
-// 8 (4 slices, depth 4, automatic wavefronts) against 38.9 on the paired
-// kernel, 28.4 against 30.8 at M = 4; at K <= 14336 the reduce launch costs
-// more than the split saves (14336 x 4096 M = 8: 12.5 against 11.0; 8192 x
-// 8192: 13.2 against 11.3; 8192 x 28672: 33.0 against 29.8 streaming whole
-// rows). Slices: the fewest from 4 up whose staging fits in LDS.
-constexpr int64_t kPairSplitMinN = 4096;
+// 8 (4 slices, depth 4, automatic wavefronts; 29.6 with the reduce's
+// loads all issued at once) against 37.0-38.9 on the paired kernel, 27.4
+// against 29.6 at M = 4; at K <= 14336 or N <= 4096 the reduce launch costs
+// more than the split saves (14336 x 4096 M = 8: 11.7 against 11.1; 20480 x
+// 4096: 15.4 against 15.2; 8192 x 8192: 12.8 against 11.2; 8192 x 28672:
+// 33.0 against 29.8 streaming whole rows). Slices: the fewest from 4 up
+// whose staging fits in LDS.
+constexpr int64_t kPairSplitMinN = 8192;
 constexpr int64_t kPairSplitMinK = 16384;   // K above this
 
 Plan plan_pair_split(int64_t M, int64_t N, int64_t K) {

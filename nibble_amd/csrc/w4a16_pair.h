@@ -504,20 +504,28 @@ gemv_pair_stream(const f16* __restrict__ x, const uint8_t* __restrict__ w, const
 }
 
 // out[i] = fp16(part[0][i] + part[1][i] + ... + part[S - 1][i]) over the
-// MN = M N outputs, 4 per thread (16-byte loads when MN % 4 == 0).
+// MN = M N outputs, 4 per thread (16-byte loads when MN % 4 == 0). S is a
+// template argument so that a thread's S loads are all requested before the
+// first add (a runtime loop would wait for each in turn).
+template <int S>
 __global__ void __launch_bounds__(256)
-pair_split_reduce(const float* __restrict__ part, f16* __restrict__ out, int S, int MN) {
+pair_split_reduce(const float* __restrict__ part, f16* __restrict__ out, int MN) {
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= MN) return;
     if ((MN & 3) == 0) {
-        f32x4 acc = *reinterpret_cast<const f32x4*>(part + i);
-        for (int s = 1; s < S; ++s) acc += *reinterpret_cast<const f32x4*>(part + (size_t)s * MN + i);
+        f32x4 v[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) v[s] = *reinterpret_cast<const f32x4*>(part + (size_t)s * MN + i);
+        f32x4 acc = v[0];
+#pragma unroll
+        for (int s = 1; s < S; ++s) acc += v[s];
         const f16x2 lo = {(f16)acc[0], (f16)acc[1]}, hi = {(f16)acc[2], (f16)acc[3]};
         *reinterpret_cast<uint2*>(out + i) = make_uint2(as_u32(lo), as_u32(hi));
         return;
     }
     for (int e = i; e < min(i + 4, MN); ++e) {
         float acc = part[e];
+#pragma unroll
         for (int s = 1; s < S; ++s) acc += part[(size_t)s * MN + e];
         out[e] = (f16)acc;
     }

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <string>
+#include <utility>
 
 #include "w4a16_pair.h"
 
@@ -198,6 +199,15 @@ StreamKern pick_stream(int depth) {
     }
 }
 
+using ReduceKern = void (*)(const float*, w4a16::f16*, int);
+template <int... S>
+ReduceKern reduce_table(int slices, std::integer_sequence<int, S...>) {
+    static constexpr ReduceKern table[] = {w4a16::pair_split_reduce<S + 2>...};
+    return table[slices - 2];
+}
+// pair_split_reduce<slices> for slices 2..16 (the launcher checks the range)
+ReduceKern pick_reduce(int slices) { return reduce_table(slices, std::make_integer_sequence<int, 15>{}); }
+
 int cu_count() {
     int cus = 0, device = 0;
     if (hipGetDevice(&device) != hipSuccess ||
@@ -299,8 +309,8 @@ int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, c
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) {
         const int64_t mn = (int64_t)M * N;
-        hipLaunchKernelGGL(w4a16::pair_split_reduce, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, stream,
-                           static_cast<const float*>(part), static_cast<w4a16::f16*>(o), slices, (int)mn);
+        hipLaunchKernelGGL(pick_reduce(slices), dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, stream,
+                           static_cast<const float*>(part), static_cast<w4a16::f16*>(o), (int)mn);
         e = hipGetLastError();
     }
     if (e != hipSuccess) {

@@ -351,12 +351,12 @@ def test_scalar_argument_errors():
 
 
 @pytest.mark.parametrize("m,n,k,splits", [
-    (8, 8192, 28672, None), (8, 4096, 14336, 0), (4, 8192, 28672, None), (3, 4096, 28672, None),
-    (3, 4096, 14336, 0), (5, 4096, 20480, None), (8, 4095, 28672, 0), (8, 8192, 16384, 0),
+    (8, 8192, 28672, None), (8, 4096, 14336, 0), (4, 8192, 28672, None), (3, 8192, 28672, None),
+    (3, 4096, 14336, 0), (5, 8192, 20480, None), (5, 4096, 20480, 0), (8, 8191, 28672, 0), (8, 8192, 16384, 0),
     (8, 2048, 5632, 0), (8, 28672, 8192, 0), (1, 8192, 28672, 0), (2, 8192, 28672, 0), (16, 8192, 28672, 0),
     (8, 4096, 4096, 0), (4, 4096, 8192, 0)])
 def test_linear_workspace_bytes(m, n, k, splits):
-    """M = 3..8 layers with K > 16384 and N >= 4096 use splits * M * N fp32
+    """M = 3..8 layers with K > 16384 and N >= 8192 use splits * M * N fp32
     of workspace (the split-K kernel); everything else none."""
     got = _lib.linear_workspace_bytes(m, n, k)
     if splits == 0:

@@ -303,9 +303,9 @@ def test_pair_split_many_tasks(gpu, waves, cap, m, k, n, splits):
     assert_parity(got, expected(x, p, s), f"pair_split waves={waves} cap={cap} S={splits} M={m} K={k} N={n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(8, 28672, 8192), (3, 28672, 8200), (5, 20480, 4096), (4, 16512, 4104)])
+@pytest.mark.parametrize("m,k,n", [(8, 28672, 8192), (3, 28672, 8200), (5, 20480, 8192), (4, 16512, 8200)])
 def test_default_dispatch_pair_split(gpu, m, k, n):
-    """With a workspace, M = 3..8 layers with K > 16384 take the split-K
+    """With a workspace, M = 3..8 layers with K > 16384 and N >= 8192 take the split-K
     kernel (the torch op's route; ragged N; K = 16512 has 129 groups, so the
     last of its 4 slices holds 27); without one, the same call takes the
     workspace-free route, also within the bar."""
