@@ -402,3 +402,23 @@ def test_fake_kernels_give_shapes():
         w = torch.ops.w4a16.dequantize(p, s, 128)
     assert tuple(y.shape) == (3, 8) and y.dtype == torch.float16
     assert tuple(w.shape) == (8, 256) and w.dtype == torch.float16
+
+
+def test_split_plans_are_launchable():
+    """Every split-K plan the router can make (M = 3..8, K = 16512..65536 and
+    beyond) is one the launcher accepts: 2..16 slices, none empty, a slice's
+    staging within 160 KiB of LDS (8 row slots for M > 4, else 4); past
+    K = 65536 no workspace is asked for."""
+    for m in range(3, 9):
+        slots = 8 if m > 4 else 4
+        for k in list(range(16512, 65537, 1152)) + [65536, 65664, 131072]:
+            ws = _lib.linear_workspace_bytes(m, 8192, k)
+            if k > 65536:
+                assert ws == 0, (m, k)
+                continue
+            assert ws > 0 and ws % (m * 8192 * 4) == 0, (m, k)
+            s = ws // (m * 8192 * 4)
+            pairs = (k // 128 + 1) // 2
+            per_slice = -(-pairs // s)
+            assert 2 <= s <= 16 and (s - 1) * per_slice < pairs, (m, k, s)
+            assert per_slice * 16 * (2 * slots) * 16 + per_slice * 128 <= 160 * 1024, (m, k, s)
