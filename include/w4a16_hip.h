@@ -60,11 +60,19 @@ extern "C" {
  * its LDS-staged form from M = 128; W4A16_DECODE = mfma_oneshot or mfma_pair
  * selects those kernels for M = 9..16); anything else takes the generic
  * kernel (the reference routes every M > 8 to its naive kernel).
- * Environment, read at every call: W4A16_DECODE = auto|oneshot|valu|
- * valu_offset|mfma|mfma_oneshot|mfma_pair|stream|pair_stream selects the
- * kernel family for M <= 8;
- * W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront of the VALU
- * kernels (any other value is W4A16_ERR_CONFIG).
+ * Environment, read at every call, with the reference's semantics
+ * (csrc/int4_linear_kernel.cu:459-491, :713-749):
+ *   W4A16_DECODE = v1|v2|v3 selects an M = 1 variant on the tuned path
+ *   (v1: looped VALU kernel, v2: diagonal MFMA kernel, v3: offset-decode
+ *   VALU kernel, each one row per wavefront); v4, auto, unset and any
+ *   value not listed here are the default routing. This build's family
+ *   names oneshot|valu|valu_offset|mfma|mfma_oneshot|mfma_pair|stream|
+ *   pair_stream select a kernel family for M <= 8 (and mfma_oneshot /
+ *   mfma_pair for M = 9..16).
+ *   W4A16_ROWS_PER_WARP = 1|2|4 sets output rows per wavefront at M = 1
+ *   (the default routing then runs the looped VALU kernel with that many
+ *   rows); it is read only at M = 1 on the tuned path and not under
+ *   v1..v3, and there any other value is W4A16_ERR_CONFIG.
  */
 int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights,
                      const void* scales, void* output, int64_t M, int64_t N,

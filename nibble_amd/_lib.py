@@ -137,8 +137,15 @@ def linear_workspace_bytes(m: int, n: int, k: int, group_size: int = 128) -> int
     return int(lib().w4a16_linear_workspace_bytes(m, n, k, group_size))
 
 
-def _workspace(nbytes: int, device):
-    return torch.empty(((nbytes + 3) // 4,), dtype=torch.float32, device=device)
+def _workspace(nbytes: int, device, stream=None):
+    """An fp32 workspace from the caching allocator. When the launches run on
+    a stream other than the current one, the block is recorded on that
+    stream, so the allocator does not hand it out again while those launches
+    may still read or write it."""
+    ws = torch.empty(((nbytes + 3) // 4,), dtype=torch.float32, device=device)
+    if stream is not None and stream != torch.cuda.current_stream(device):
+        ws.record_stream(stream)
+    return ws
 
 
 def linear_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None,
@@ -151,7 +158,7 @@ def linear_f16(activations, packed_weights, scales, output, group_size: int = 12
     n = packed_weights.shape[0]
     if isinstance(workspace, str):
         nbytes = linear_workspace_bytes(m, n, k, group_size)
-        workspace = _workspace(nbytes, output.device) if nbytes > 0 else None
+        workspace = _workspace(nbytes, output.device, stream) if nbytes > 0 else None
     if workspace is None:
         _raise_on(
             lib().w4a16_linear_f16(
@@ -176,7 +183,7 @@ def linear_f16_tuned(activations, packed_weights, scales, output, group_size, ke
     m, k = activations.shape
     n = packed_weights.shape[0]
     if workspace is None and kernel == KERNEL_PAIR_SPLIT:
-        workspace = _workspace(max(1, splits) * m * n * 4, output.device)
+        workspace = _workspace(max(1, splits) * m * n * 4, output.device, stream)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _raise_on(

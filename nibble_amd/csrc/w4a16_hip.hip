@@ -106,33 +106,56 @@ int valu_lds_bytes(int64_t M, int64_t K, const Plan& p) {
     return (int)(M * K * 2 + sums);
 }
 int mfma_lds_bytes(const Plan& p) { return p.splits > 1 ? p.splits * p.rows * 64 * 16 : 0; }
+// LDS of the diagonal MFMA kernel: the activation row in 1 KiB spans' units.
+int64_t diag_lds_bytes(int64_t K) { return (K / 32 + 63) / 64 * 64 * 64; }
 
-// Environment selectors, read at every call (as reference
-// csrc/int4_linear_kernel.cu:464-491 does) so tests can switch them.
-int read_env(int* family, int* rows_per_wave) {
-    *family = 0;  // auto
+// W4A16_DECODE values of the reference (csrc/int4_linear_kernel.cu:459-476),
+// which compares the three M = 1 variants it keeps against its default. Each
+// maps to the kernel of this build nearest to it; they apply at M = 1 on the
+// tuned path only, where the reference reads them.
+constexpr int kDecodeV1 = -1;   // v1, LDS-staged activations, one row per warp: looped VALU kernel, 1 row
+constexpr int kDecodeV2 = -2;   // v2, 16-byte weight loads, one row per warp: diagonal MFMA kernel, 1 row
+constexpr int kDecodeV3 = -3;   // v3, v2 with the cheaper unpack: offset-decode VALU kernel, 1 row
+
+// W4A16_DECODE, read at every call (as the reference does) so tests can switch
+// it. v1, v2 and v3 select the variants above; this build's family names
+// select a kernel family; v4, auto and any other value (the reference treats
+// every value it does not know as v4) are the default routing.
+int read_decode_env() {
     const char* d = std::getenv("W4A16_DECODE");
-    if (d != nullptr && d[0] != '\0') {
-        if (std::strcmp(d, "auto") == 0) *family = 0;
-        else if (std::strcmp(d, "valu") == 0) *family = W4A16_KERNEL_VALU;
-        else if (std::strcmp(d, "valu_offset") == 0) *family = W4A16_KERNEL_VALU_OFFSET;
-        else if (std::strcmp(d, "mfma") == 0) *family = W4A16_KERNEL_MFMA;
-        else if (std::strcmp(d, "oneshot") == 0) *family = W4A16_KERNEL_ONESHOT;
-        else if (std::strcmp(d, "mfma_oneshot") == 0) *family = W4A16_KERNEL_MFMA_ONESHOT;
-        else if (std::strcmp(d, "mfma_pair") == 0) *family = W4A16_KERNEL_MFMA_PAIR;
-        else if (std::strcmp(d, "stream") == 0) *family = W4A16_KERNEL_STREAM;
-        else if (std::strcmp(d, "pair_stream") == 0) *family = W4A16_KERNEL_PAIR_STREAM;
-        else
-            return fail(W4A16_ERR_CONFIG, "W4A16_DECODE must be auto, valu, valu_offset, oneshot, mfma, mfma_oneshot, "
-                                          "mfma_pair, stream, or pair_stream");
-    }
+    if (d == nullptr) return 0;
+    static const struct {
+        const char* name;
+        int family;
+    } kNames[] = {
+        {"v1", kDecodeV1},
+        {"v2", kDecodeV2},
+        {"v3", kDecodeV3},
+        {"valu", W4A16_KERNEL_VALU},
+        {"valu_offset", W4A16_KERNEL_VALU_OFFSET},
+        {"mfma", W4A16_KERNEL_MFMA},
+        {"oneshot", W4A16_KERNEL_ONESHOT},
+        {"mfma_oneshot", W4A16_KERNEL_MFMA_ONESHOT},
+        {"mfma_pair", W4A16_KERNEL_MFMA_PAIR},
+        {"stream", W4A16_KERNEL_STREAM},
+        {"pair_stream", W4A16_KERNEL_PAIR_STREAM},
+    };
+    for (const auto& e : kNames)
+        if (std::strcmp(d, e.name) == 0) return e.family;
+    return 0;
+}
+
+// W4A16_ROWS_PER_WARP (reference csrc/int4_linear_kernel.cu:481-491: unset
+// means the default, anything but 1, 2 or 4 is an error). The caller reads
+// it only where the reference does: M = 1 on the tuned path, unless
+// W4A16_DECODE chose v1, v2 or v3 (reference :713-749).
+int read_rows_env(int* rows_per_wave) {
     *rows_per_wave = 0;
     const char* r = std::getenv("W4A16_ROWS_PER_WARP");
-    if (r != nullptr) {
-        const int v = std::atoi(r);
-        if (!(v == 1 || v == 2 || v == 4)) return fail(W4A16_ERR_CONFIG, "W4A16_ROWS_PER_WARP must be 1, 2, or 4");
-        *rows_per_wave = v;
-    }
+    if (r == nullptr) return W4A16_OK;
+    const int v = std::atoi(r);
+    if (!(v == 1 || v == 2 || v == 4)) return fail(W4A16_ERR_CONFIG, "W4A16_ROWS_PER_WARP must be 1, 2, or 4");
+    *rows_per_wave = v;
     return W4A16_OK;
 }
 
@@ -498,14 +521,43 @@ int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16
 
 int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t K, int64_t G, Plan* out,
               bool workspace = false) {
-    int family = 0, rows = 0;
-    const int rc = read_env(&family, &rows);
-    if (rc != W4A16_OK) return rc;
+    int family = read_decode_env(), rows = 0;
     if (M * N == 0) {
         *out = Plan();
         return W4A16_OK;
     }
     const bool aligned = G == 128 && aligned16(act) && aligned16(packed);
+    // The reference reads its selectors on the M = 1 tuned path only: v1..v3
+    // elsewhere are the default, and W4A16_ROWS_PER_WARP is read (and
+    // rejected when malformed) at M = 1 unless v1..v3 was chosen.
+    const bool tuned_m1 = aligned && M == 1;
+    if (family < 0 && !tuned_m1) family = 0;
+    if (tuned_m1 && family >= 0) {
+        const int rc = read_rows_env(&rows);
+        if (rc != W4A16_OK) return rc;
+    }
+    if (family < 0) {
+        Plan p;
+        if (family == kDecodeV2) {
+            p.kernel = W4A16_KERNEL_DIAG;
+            p.rows = 1;
+            p.splits = 4;
+            p.unroll = 2;
+            p.max_blocks = 1024;
+            if (diag_lds_bytes(K) <= kMaxLdsBytes) {
+                *out = p;
+                return W4A16_OK;
+            }
+        } else {
+            p = plan_valu(1, N, K, 1);
+            p.kernel = family == kDecodeV1 ? W4A16_KERNEL_VALU : W4A16_KERNEL_VALU_OFFSET;
+            if (valu_lds_bytes(1, K, p) <= kMaxLdsBytes) {
+                *out = p;
+                return W4A16_OK;
+            }
+        }
+        family = 0;   // activations past LDS: the default routing
+    }
     // M = 9..16 (a short prompt) is one MFMA tile of activation rows: the
     // GEMM by default (measured against the one-shot MFMA kernel and the
     // paired kernel over two halves, M = 9..16 on the 1.1B / 8B layers: M =
@@ -821,15 +873,14 @@ int launch_diag(const Plan& p, int M, const w4a16::f16* x, const uint8_t* w, con
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: rows 1, 2, 4 and unroll 1, 2, 4 (4 needs rows <= 2)");
     if (p.splits < 1 || p.splits > 4) return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: 1..4 wavefronts per workgroup");
-    const int spans = (K / 32 + 63) / 64;
-    const int lds = spans * 64 * 64;
+    const int64_t lds = diag_lds_bytes(K);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "diagonal MFMA kernel: activations do not fit in LDS");
-    int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
     if (rc != W4A16_OK) return rc;
     const int tasks = (N + p.rows - 1) / p.rows;
     int blocks = (tasks + p.splits - 1) / p.splits;
     if (p.max_blocks > 0 && blocks > p.max_blocks) blocks = p.max_blocks;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), lds, stream, x, w, s, o, N, K, tasks);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * p.splits), (int)lds, stream, x, w, s, o, N, K, tasks);
     return check_launch();
 }
 

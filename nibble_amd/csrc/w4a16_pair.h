@@ -512,7 +512,9 @@ __global__ void __launch_bounds__(256)
 pair_split_reduce(const float* __restrict__ part, f16* __restrict__ out, int MN) {
     const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= MN) return;
-    if ((MN & 3) == 0) {
+    // 8-byte stores need whole quads and an 8-byte aligned output (the C ABI
+    // asks only for 2-byte alignment)
+    if ((MN & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 7u) == 0) {
         f32x4 v[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) v[s] = *reinterpret_cast<const f32x4*>(part + (size_t)s * MN + i);

@@ -258,8 +258,8 @@ def test_mfma_pair_plan_shapes(monkeypatch):
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "mfma"   # M = 1
     assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 32896, 128)["kernel"] == "mfma"   # too long
     monkeypatch.delenv("W4A16_DECODE")
-    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # an explicit VALU row count keeps auto off it
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] != "mfma_pair"
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")   # read at M = 1 only, as in the reference
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "mfma_pair"
 
 
 def test_mfma_oneshot_plan_shapes(monkeypatch):
@@ -306,8 +306,64 @@ def test_env_selectors(monkeypatch):
     with pytest.raises(_lib.W4A16Error, match="W4A16_ROWS_PER_WARP must be 1, 2, or 4"):
         _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
     monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")
-    monkeypatch.setenv("W4A16_DECODE", "v9")
-    with pytest.raises(_lib.W4A16Error, match="W4A16_DECODE"):
+    monkeypatch.setenv("W4A16_DECODE", "v9")   # unknown values are the default, as in the reference
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "oneshot"
+
+
+@pytest.mark.parametrize("value,kernel", [("v1", "valu"), ("v2", "diag"), ("v3", "valu_offset")])
+def test_reference_decode_versions(monkeypatch, value, kernel):
+    """Reference csrc/int4_linear_kernel.cu:464-476: v1..v3 pick M = 1
+    variants (one row per wavefront here) on the tuned path and nothing
+    else; W4A16_ROWS_PER_WARP is not read under them (:713-749)."""
+    monkeypatch.setenv("W4A16_DECODE", value)
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "3")   # ignored under v1..v3
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 2048, 2048, 128)
+    assert (plan["kernel"], plan["rows"]) == (kernel, 1)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP")
+    for m, k, n in [(1, 256, 7), (1, 5632, 2048), (1, 28672, 64)]:
+        assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] == kernel
+    # M > 1, misaligned operands, other group sizes: the default routing
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "mfma_pair"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 16, 64, 2048, 128)["kernel"] == "gemm"
+    assert _lib.plan_linear(ALIGNED + 2, ALIGNED, 1, 64, 2048, 128)["kernel"] == "generic"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 64)["kernel"] == "generic"
+    # activations past LDS: the default routing
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 131072, 128)["kernel"] == "mfma"
+
+
+def test_reference_v4_and_default_match(monkeypatch):
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    shapes = [(1, 2048, 2048), (1, 4096, 14336), (1, 14336, 4096), (4, 2048, 5632), (8, 28672, 8192),
+              (64, 2048, 2048)]
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    default = [_lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128) for m, k, n in shapes]
+    for value in ("v4", "auto", "", "V4", "nonsense"):
+        monkeypatch.setenv("W4A16_DECODE", value)
+        assert [_lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128) for m, k, n in shapes] == default, value
+
+
+def test_rows_per_warp_read_only_where_the_reference_reads_it(monkeypatch):
+    """Reference :713-749 reads W4A16_ROWS_PER_WARP only for M = 1 on the
+    warp kernels with the default selector: a bad value raises there and is
+    ignored everywhere else."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "3")
+    with pytest.raises(_lib.W4A16Error, match="W4A16_ROWS_PER_WARP must be 1, 2, or 4"):
+        _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    monkeypatch.setenv("W4A16_DECODE", "v4")
+    with pytest.raises(_lib.W4A16Error, match="W4A16_ROWS_PER_WARP must be 1, 2, or 4"):
+        _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    for m in (2, 4, 8, 9, 64):   # small batch and prompts
+        _lib.plan_linear(ALIGNED, ALIGNED, m, 64, 2048, 128)
+    _lib.plan_linear(ALIGNED + 2, ALIGNED, 1, 64, 2048, 128)   # misaligned: the generic kernel
+    _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 64)        # group size other than 128
+    _lib.plan_linear(ALIGNED, ALIGNED, 0, 64, 2048, 128)       # empty
+    monkeypatch.setenv("W4A16_DECODE", "v1")
+    _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "")   # atoi("") = 0, rejected as in the reference
+    monkeypatch.setenv("W4A16_DECODE", "v4")
+    with pytest.raises(_lib.W4A16Error):
         _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
 
 

@@ -62,6 +62,15 @@ def test_default_dispatch_small_batch(gpu, m):
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M={m}")
 
 
+@pytest.mark.parametrize("m", [2, 4, 8])
+@pytest.mark.parametrize("k,n", [(2048, 2048), (2048, 5632), (5632, 2048)])
+def test_default_dispatch_configs2(gpu, m, k, n):
+    """every M in {2, 4, 8} on its three layer shapes, at full size,
+    through the default route the benchmark times."""
+    x, p, s = make_case(m, k, n, seed=100 * m + k + n)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"configs2 M={m} K={k} N={n}")
+
+
 @pytest.mark.parametrize("m", [2, 8])
 def test_small_batch_n7(gpu, m):
     x, p, s = make_case(m, 256, 7, seed=7)
@@ -314,6 +323,25 @@ def test_default_dispatch_pair_split(gpu, m, k, n):
     ref = expected(x, p, s)
     assert_parity(_run_default(gpu, x, p, s), ref, f"pair_split default M={m} K={k} N={n}")
     assert_parity(_run_default(gpu, x, p, s, workspace=None), ref, f"no workspace M={m} K={k} N={n}")
+
+
+@pytest.mark.parametrize("offset", [1, 2, 3])
+def test_pair_split_unaligned_output(gpu, offset):
+    """The reduce stores 4 outputs at a time only into an 8-byte aligned
+    output; an output 2, 4 or 6 bytes past that (the C ABI asks for 2) takes
+    the element-wise stores. M * N is a multiple of 4 here, and the elements
+    around the output stay untouched."""
+    m, k, n = 4, 20480, 8192
+    x, p, s = make_case(m, k, n, seed=offset + 77)
+    assert _lib.linear_workspace_bytes(m, n, k) > 0
+    buf = torch.full((m * n + 8,), -7.0, dtype=torch.float16, device=gpu)
+    out = buf[offset:offset + m * n].view(m, n)
+    print(f"[case] pair_split output offset {2 * offset} B M={m} K={k} N={n}", flush=True)
+    _lib.linear_f16(x.to(gpu), p.to(gpu), s.to(gpu), out)
+    torch.cuda.synchronize()
+    assert_parity(out, expected(x, p, s), f"pair_split offset {offset}")
+    rest = torch.cat([buf[:offset], buf[offset + m * n:]]).cpu()
+    assert torch.all(rest == -7.0)
 
 
 def test_pair_split_workspace_reused(gpu):
