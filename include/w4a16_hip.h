@@ -101,6 +101,29 @@ int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights,
                         int64_t K, int64_t group_size, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* Bytes of device scratch w4a16_linear_noalloc_f16 holds per GPU (8 MiB). */
+#define W4A16_NOALLOC_SCRATCH_BYTES (8LL << 20)
+
+/*
+ * w4a16_linear_ws_f16's routing (split-K kernel included) with no allocation
+ * of any kind: the split-K partial sums go to a device array of
+ * W4A16_NOALLOC_SCRATCH_BYTES that the library carries (one per GPU, held
+ * until the process ends), so the call makes no hipMalloc, hipFree or
+ * allocating library call. No counterpart in the reference (its kernels
+ * keep no partial sums): it is for callers that cannot allocate, such as
+ * code under HIP graph capture, tight serving loops or harnesses that
+ * forbid allocation. Results are bit-identical to w4a16_linear_ws_f16 with
+ * a caller workspace. A layer whose split-K partials need more than the
+ * scratch (slices * M * N * 4 bytes) is W4A16_ERR_TOO_LARGE. Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU (two
+ * streams, two threads) race and must be serialised by the caller. The
+ * first call on a device that needs the scratch looks up its address
+ * (hipGetSymbolAddress); make that call outside graph capture.
+ */
+int w4a16_linear_noalloc_f16(const void* activations, const uint8_t* packed_weights,
+                             const void* scales, void* output, int64_t M, int64_t N,
+                             int64_t K, int64_t group_size, void* stream);
+
 /*
  * Dequantize packed INT4 weights to fp16 [N, K]: out = fp16_rn(code * scale),
  * bit-identical to reference w4a16/reference.py:6-46 followed by .to(float16).

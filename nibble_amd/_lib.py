@@ -59,6 +59,7 @@ SIGNATURES = {
     "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip, _ip]),
     "w4a16_linear_workspace_bytes": (_i64, [_i64] * 4),
     "w4a16_linear_ws_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "w4a16_linear_noalloc_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "w4a16_linear_f16_tuned": (
         ctypes.c_int,
         [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp] + [ctypes.c_int] * 5 + [_vp, _i64],
@@ -172,6 +173,22 @@ def linear_f16(activations, packed_weights, scales, output, group_size: int = 12
             activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
             m, n, k, group_size, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
             _stream_ptr(stream),
+        )
+    )
+
+
+NOALLOC_SCRATCH_BYTES = 8 << 20   # W4A16_NOALLOC_SCRATCH_BYTES
+
+
+def linear_noalloc_f16(activations, packed_weights, scales, output, group_size: int = 128, stream=None) -> None:
+    """``w4a16_linear_noalloc_f16``: the default routing with the split-K
+    partial sums in the library's own device scratch (no allocation)."""
+    m, k = activations.shape
+    n = packed_weights.shape[0]
+    _raise_on(
+        lib().w4a16_linear_noalloc_f16(
+            activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), output.data_ptr(),
+            m, n, k, group_size, _stream_ptr(stream),
         )
     )
 

@@ -967,6 +967,39 @@ int check_pointers(const void* act, const void* packed, const void* scales, cons
     return W4A16_OK;
 }
 
+// Scratch of w4a16_linear_noalloc_f16: the split-K kernel's fp32 partial sums
+// ([slices][M][N]) in a device array the code object carries, so that entry
+// point never allocates. Each device holds its own copy at its own address;
+// in host code the array's name stands for the host-side shadow, never for
+// device memory, so launches take the address hipGetSymbolAddress returns
+// for the current device, looked up once per device on the first call that
+// needs it. The split-K kernel writes every partial sum before its reduce
+// reads them, so nothing has to be cleared between calls.
+constexpr int64_t kNoAllocScratchBytes = W4A16_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (device < 0 || device >= kMaxDevices)
+        return fail(W4A16_ERR_CONFIG, "w4a16_linear_noalloc_f16: device ordinal past the library's table of 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return fail(W4A16_ERR_LAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return W4A16_OK;
+}
+
 }  // namespace
 
 namespace w4a16_internal {
@@ -1044,6 +1077,32 @@ int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights, 
 int w4a16_linear_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
                      void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream) {
     return w4a16_linear_ws_f16(activations, packed_weights, scales, output, M, N, K, group_size, nullptr, 0, stream);
+}
+
+int w4a16_linear_noalloc_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
+                             void* output, int64_t M, int64_t N, int64_t K, int64_t group_size, void* stream) {
+    int rc = check_scalar_args(M, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    Plan p;
+    rc = make_plan(activations, packed_weights, M, N, K, group_size, &p, true);
+    if (rc != W4A16_OK) return rc;
+    if (p.kernel == W4A16_KERNEL_NONE) return W4A16_OK;
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    const int64_t need =
+        p.kernel == W4A16_KERNEL_PAIR_SPLIT ? w4a16_internal::pair_split_workspace_bytes(M, N, p.splits) : 0;
+    if (need > kNoAllocScratchBytes)
+        return fail(W4A16_ERR_TOO_LARGE, "w4a16_linear_noalloc_f16: this layer needs " + std::to_string(need) +
+                                             " bytes of split-K scratch, more than the library's " +
+                                             std::to_string(kNoAllocScratchBytes) +
+                                             "; use w4a16_linear_ws_f16 with a caller workspace");
+    void* ws = nullptr;
+    if (need > 0) {
+        rc = scratch_address(&ws);
+        if (rc != W4A16_OK) return rc;
+    }
+    return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, true, ws,
+                    need > 0 ? kNoAllocScratchBytes : 0);
 }
 
 int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {

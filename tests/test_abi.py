@@ -373,6 +373,23 @@ def test_valu_falls_back_to_mfma_when_activations_exceed_lds(monkeypatch):
     assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 14336, 128)["kernel"] == "mfma"
 
 
+def test_noalloc_rejects_before_launch():
+    """w4a16_linear_noalloc_f16 checks its arguments and the scratch size on
+    the host: a layer whose split-K partials exceed the 8 MiB scratch is
+    W4A16_ERR_TOO_LARGE (nothing launched, so stand-in addresses are safe)."""
+    lib = _lib.lib()
+    assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 1, 8, 256, 0, None) == _lib.W4A16_ERR_GROUP_SIZE
+    assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 1, 8, 256, 128, None) == _lib.W4A16_ERR_NULL
+    assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 0, 8, 256, 128, None) == _lib.W4A16_OK
+    m, k, n = 8, 20480, 65544
+    need = _lib.linear_workspace_bytes(m, n, k)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    a = ALIGNED
+    assert lib.w4a16_linear_noalloc_f16(a, a, a, a, m, n, k, 128, None) == _lib.W4A16_ERR_TOO_LARGE
+    assert str(need) in _lib.last_error() and "w4a16_linear_ws_f16" in _lib.last_error()
+    assert _lib.linear_workspace_bytes(m, 65536, k) == _lib.NOALLOC_SCRATCH_BYTES   # the largest that fits
+
+
 def test_scalar_argument_errors():
     lib = _lib.lib()
     assert lib.w4a16_linear_f16(None, None, None, None, 1, 8, 256, 0, None) == _lib.W4A16_ERR_GROUP_SIZE
