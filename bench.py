@@ -14,14 +14,21 @@ stream between two synchronisations. `value` = algorithmic bytes moved by
 the K steps / elapsed time (GB/s), with algorithmic bytes per call
 N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 (reference scripts/profile_kernel.py:310-323).
 
+Rotation: step g reads copy g mod 64 of one continuous sequence -- an untimed
+64-step pre-roll, the warm-up steps, the timed steps -- so every timed call
+reads a copy last read 64 steps (762 MB of other weights) earlier.
+
 Also reported: per-layer us / GB/s / % of the 8 TB/s HBM peak for each shape
-(graph replay, 100 calls), the configs[2] small-batch table (M = 1, 2, 4, 8
+(graph replay of whole rotations over the copies, at least 100 calls) with
+the single-call eager latency (`eager_us`, launch included), GPU clocks and
+power sampled under load, the configs[2] small-batch table (M = 1, 2, 4, 8
 on 2048x2048, 2048x5632, 5632x2048, next to fp16 hipBLASLt on the dequantized
 weights) and the configs[3] large-layer table (M = 1, 8), a measured device
 copy bandwidth, end-to-end greedy decode tokens/s of the random-init 1.1B
 Llama-architecture model (configs[4], decode step in a HIP graph), and the
 CPU oracle's time for the same layers on the host cores (`cpu_baseline`; a
-reported baseline, not a target).
+reported baseline, not a target), with configs[0] (M = 1, 2048 x 2048) timed
+on the product's torch CPU path beside the oracle, and the CPU model.
 
 usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables]
        python bench.py --layer-pass M K N COPIES CALLS | --prefill-pass TOKENS   (profiler passes)
@@ -45,6 +52,7 @@ HBM_PEAK_GBPS = 8000.0
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
 # reads half the bytes on this part, WRITE_SIZE is exact).
 MEASURED_TRAFFIC_BYTES = 6070301
+TRAFFIC_SOURCE = "profiles/gemv_oneshot_m1_mlp_traffic.md"
 
 
 def _kernel_name(plan: dict) -> str:
@@ -105,12 +113,96 @@ def time_graph(graph, reps: int = 1) -> float:
 
 
 def per_layer(op, copies: int, calls: int = 100, samples: int = 20) -> float:
-    """Median microseconds per call over `samples` replays of a `calls`-call graph."""
+    """Median microseconds per call over `samples` replays of a graph of at
+    least `calls` calls over the rotated copies. The graph holds whole
+    rotations (a multiple of `copies` calls), so across replays as within one
+    every copy is read again only after all the other copies were."""
+    calls = copies * -(-calls // copies)
     graph = capture(lambda i: op(i % copies), calls)
     for _ in range(3):
         graph.replay()
     times = sorted(time_graph(graph) / calls * 1e6 for _ in range(samples))
     return times[len(times) // 2]
+
+
+def eager_us(op, copies: int, samples: int = 20) -> float:
+    """Single-call latency with launch overhead (reference
+    scripts/profile_kernel.py:531-534): events around one eager call, median
+    over `samples` calls on successive rotated copies."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    times = []
+    for i in range(samples):
+        torch.cuda.synchronize()
+        start.record()
+        op(i % copies)
+        end.record()
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e3)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def gpu_state_under_load(graph, seconds: float = 1.0) -> dict | None:
+    """GFX / memory clocks and socket power sampled with amdsmi while `graph`
+    replays back to back (the counterpart of reference
+    scripts/profile_kernel.py:256-307); None when amdsmi is unavailable."""
+    import threading
+
+    import torch
+
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+    except Exception:
+        return None
+    samples, stop = [], threading.Event()
+
+    def sampler(handle):
+        while not stop.is_set():
+            try:
+                gfx = amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)
+                mem = amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.MEM)
+                power = amdsmi.amdsmi_get_power_info(handle)
+                watts = power.get("socket_power")
+                if not isinstance(watts, (int, float)):
+                    watts = power.get("current_socket_power")
+                samples.append((gfx.get("clk"), mem.get("clk"), watts))
+            except Exception:
+                pass
+            stop.wait(0.05)
+
+    try:
+        handles = amdsmi.amdsmi_get_processor_handles()
+        if not handles:
+            return None
+        thread = threading.Thread(target=sampler, args=(handles[0],), daemon=True)
+        thread.start()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            graph.replay()
+            torch.cuda.synchronize()
+        stop.set()
+        thread.join()
+    finally:
+        stop.set()
+        try:
+            amdsmi.amdsmi_shut_down()
+        except Exception:
+            pass
+
+    def stats(values):
+        vals = [v for v in values if isinstance(v, (int, float)) and v not in (0xFFFF, 0xFFFFFFFF)]
+        if not vals:
+            return None
+        vals.sort()
+        return {"min": vals[0], "median": vals[len(vals) // 2], "max": vals[-1]}
+
+    return {"samples": len(samples), "gfx_clock_mhz": stats([s[0] for s in samples]),
+            "mem_clock_mhz": stats([s[1] for s in samples]), "socket_power_w": stats([s[2] for s in samples])}
 
 
 def copy_bandwidth(device) -> float:
@@ -126,13 +218,43 @@ def copy_bandwidth(device) -> float:
     return 2 * (1 << 30) * 5 / t / 1e9
 
 
-def cpu_baseline(shapes, budget_s: float = 12.0) -> dict:
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_call_us(fn, budget_s: float) -> tuple[float, int]:
+    """Median wall time of fn() in microseconds over calls filling budget_s
+    (after one warm-up call), and the number of timed calls."""
+    fn()
+    times = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or len(times) < 5:
+        t1 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t1)
+    times.sort()
+    return times[len(times) // 2] * 1e6, len(times)
+
+
+def cpu_baseline(shapes, budget_s: float = 12.0, configs0_budget_s: float = 3.0) -> dict:
     """The CPU oracle (C restatement of reference w4a16/reference.py:49-80:
     full fp32 dequantize + fp32 matmul + fp16 cast) on the host cores, on a
-    bounded sample of the same layers (M = 1, one weight copy per shape)."""
+    bounded sample of the same layers (M = 1, one weight copy per shape); and
+    configs[0] (M = 1, 2048 x 2048), the reference's own CPU path, timed both
+    as the product's torch restatement (nibble_amd.reference.linear_reference,
+    which QuantizedLinear runs for CPU tensors) and as the C oracle."""
     import numpy as np
+    import torch
 
     import oracle
+    from nibble_amd.reference import linear_reference
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     rng = np.random.default_rng(0)
@@ -152,6 +274,26 @@ def cpu_baseline(shapes, budget_s: float = 12.0) -> dict:
             calls += 1
             total_bytes += nbytes
     elapsed = time.perf_counter() - t0
+
+    # seed 0, weights randn(N, K) * 0.02 fp32 -> RTN group 128,
+    # activations randn(1, K) -> fp16, as BASELINE.json states it
+    k0 = n0 = 2048
+    gen = torch.Generator().manual_seed(0)
+    w0 = torch.randn((n0, k0), generator=gen) * 0.02
+    from nibble_amd.quantization import quantize_and_pack_weights
+
+    p0, s0 = quantize_and_pack_weights(w0, 128)
+    x0 = torch.randn((1, k0), generator=gen).to(torch.float16)
+    torch_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        torch_us, torch_calls = _median_call_us(lambda: linear_reference(x0, p0, s0, 128), configs0_budget_s)
+    finally:
+        torch.set_num_threads(torch_threads)
+    xn, pn, sn = x0.numpy(), p0.numpy(), s0.numpy()
+    port_us, port_calls = _median_call_us(lambda: oracle.linear(xn, pn, sn, 128, threads=threads),
+                                          configs0_budget_s)
+    b0 = payload_bytes(1, n0, k0)
     return {
         "value": round(total_bytes / elapsed / 1e9, 3),
         "unit": "GB/s",
@@ -160,6 +302,18 @@ def cpu_baseline(shapes, budget_s: float = 12.0) -> dict:
         "sample": f"{calls} single-token calls alternating up (2048x5632) and down (5632x2048) "
                   f"in {elapsed:.1f} s, 1 weight copy per shape",
         "us_per_call": round(elapsed / calls * 1e6, 1),
+        "cpu_model": _cpu_model(),
+        "logical_cpus": os.cpu_count(),
+        "configs0": {
+            "workload": "configs[0]: M=1 K=2048 N=2048 group 128, the reference's CPU path",
+            "torch_reference_us": round(torch_us, 1),
+            "torch_reference_GBps": round(b0 / torch_us / 1e3, 3),
+            "torch_reference": f"nibble_amd.reference.linear_reference (torch CPU, {threads} threads), "
+                               f"median of {torch_calls} calls",
+            "port_us": round(port_us, 1),
+            "port_GBps": round(b0 / port_us / 1e3, 3),
+            "port": f"oracle.linear (C, OpenMP, {threads} threads), median of {port_calls} calls",
+        },
     }
 
 
@@ -305,7 +459,9 @@ def layer_tables(device) -> dict:
                 kernel = "pair_split" if _lib.linear_workspace_bytes(m, n, k) > 0 else plan["kernel"]
                 gbs = payload_bytes(m, n, k) / us / 1e3
                 row = {"K": k, "N": n, "M": m, "us": round(us, 3), "GBps": round(gbs, 1),
-                       "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": kernel}
+                       "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": kernel,
+                       "eager_us": round(eager_us(lambda i: torch.ops.w4a16.linear(x, packed[i], scales[i], 128),
+                                                  copies), 3)}
                 if m == 1:
                     base_us = us
                 else:
@@ -414,12 +570,20 @@ def main() -> int:
         return 0
 
     # ---- headline: K timed steps (one call of each MLP shape per step) ----
-    def step(i: int) -> None:
-        call_raw(0, i)
-        call_raw(1, i)
+    # Step g of one continuous sequence calls both shapes on copy g mod 64.
+    # An untimed pre-roll of 64 steps (every copy once) comes first, then
+    # the W warm-up steps, then the K timed steps; so every timed call reads
+    # a copy that was last read 64 steps earlier, with the other 63 copies of
+    # both shapes (750 MB, three times the Infinity Cache) read in between.
+    def step(g: int) -> None:
+        call_raw(0, g % copies)
+        call_raw(1, g % copies)
 
-    warm = capture(step, max(args.warmup, 1))
-    timed = capture(step, args.steps)
+    warmup = max(args.warmup, 1)
+    preroll = capture(step, copies)
+    warm = capture(lambda i: step(copies + i), warmup)
+    timed = capture(lambda i: step(copies + warmup + i), args.steps)
+    preroll.replay()
     warm.replay()
     torch.cuda.synchronize()
     elapsed = time_graph(timed)
@@ -434,8 +598,11 @@ def main() -> int:
         plan = _lib.plan_linear(xs[j].data_ptr(), layers[j][0][0].data_ptr(), 1, n, k)
         layer_rows[f"K{k}xN{n}"] = {"us": round(us, 3), "GBps": round(gbs, 1),
                                     "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": plan}
-    # torch-op path (drop-in API) for the same shapes, for comparison with the raw C ABI
+    # torch-op path (drop-in API) for the same shapes, graph-timed, and its
+    # single-call eager latency (launch and Python dispatch included)
     op_us = {f"K{k}xN{n}": round(per_layer(lambda i, j=j: call(j, i), copies), 3) for j, (k, n) in enumerate(shapes)}
+    op_eager_us = {f"K{k}xN{n}": round(eager_us(lambda i, j=j: call(j, i), copies), 3)
+                   for j, (k, n) in enumerate(shapes)}
 
     achieved = step_bytes / (elapsed / args.steps) / 1e9  # = value; per-launch average over the two shapes
     roofline = {
@@ -445,6 +612,7 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBPS, 4),
         "traffic": MEASURED_TRAFFIC_BYTES,
+        "traffic_source": TRAFFIC_SOURCE,
         "kernel": " + ".join(_kernel_name(r["kernel"]) for r in layer_rows.values()),
         "bytes_per_launch": step_bytes // 2,
         "us_per_launch": round(elapsed / args.steps / 2 * 1e6, 3),
@@ -465,13 +633,19 @@ def main() -> int:
         "data": "synthetic (weights ~N(0,0.02) fp32 RTN-quantized to INT4 g128, activations ~N(0,1) fp16)",
         "config": {
             "workload": "configs[1]: M=1 MLP layers K2048xN5632 + K5632xN2048, group 128, 64 rotated copies each",
-            "step": "one call of each shape on its next weight copy, HIP-graph replay",
+            "step": "one call of each shape, HIP-graph replay; step g reads copy g mod 64",
+            "rotation": "an untimed 64-step pre-roll, then the warm-up steps, then the timed steps, all one "
+                        "sequence: every timed call reads a copy last read 64 steps (762 MB of weights) earlier; "
+                        f"the timed steps read copies {(copies + warmup) % copies}.. of 64",
+            "timed_copies": min(args.steps, copies),
             "parallelism": "single GPU",
         },
         "layers_us": layer_rows,
         "torch_op_us": op_us,
+        "torch_op_eager_us": op_eager_us,
         "roofline": roofline,
     }
+    line["gpu_state"] = gpu_state_under_load(timed)
     line["copy_GBps"] = round(copy_bandwidth(device), 1)
     if not args.no_tables:
         line["layers"] = layer_tables(device)
