@@ -384,6 +384,7 @@ def prefill_long(device, lengths=(64, 256), runs: int = 5) -> dict:
     inside QuantizedLinear, torch ops around them)."""
     import torch
 
+    from nibble_amd.linear import FUSED_MAX_ROWS, NATIVE_GEMM_MAX_ROWS
     from nibble_amd.llama import LlamaConfig, LlamaDecoder
 
     model = LlamaDecoder(LlamaConfig(max_seq_len=max(lengths)), device=device, seed=0)
@@ -411,7 +412,11 @@ def prefill_long(device, lengths=(64, 256), runs: int = 5) -> dict:
         model.fused = False
         for b in model.layers:
             b.native_prefill = False
+        for mod in model.linear_layers():   # the reference's routing: dequantize + GEMM for every M > 8
+            mod.native_max_rows = FUSED_MAX_ROWS
         dequant = timed()
+        for mod in model.linear_layers():
+            mod.native_max_rows = NATIVE_GEMM_MAX_ROWS
         result[f"prefill{prompt_len}_ms"] = round(fused * 1e3, 3)
         result[f"prefill{prompt_len}_dequant_ms"] = round(dequant * 1e3, 3)
     model.prefill_graph = None

@@ -8,9 +8,16 @@ Mirrors reference ``w4a16/linear.py`` (constructor checks, buffers
 * CPU tensors: the pure-PyTorch ``linear_reference``;
 * GPU tensors, ``fused`` and M <= ``FUSED_MAX_ROWS``: ``w4a16::linear``
   (the gfx950 GEMV / small-batch kernels);
-* GPU tensors otherwise (prefill, ``fused=False``): ``w4a16::dequantize``
-  then ``F.linear`` (hipBLASLt) when group_size is a multiple of 32, else
-  ``w4a16::linear``'s generic kernel (any M, any even group size).
+* GPU tensors, ``fused``, group_size 128 and M <= ``NATIVE_GEMM_MAX_ROWS``
+  (prompts): ``w4a16::linear`` as well, which runs the W4A16 MFMA GEMM on
+  weights decoded in registers, bit-identical to the dequantized fp16 weights,
+  with fp32 accumulation; the reference sends these rows to dequantize +
+  cuBLAS, and the result agrees with that path within its own prefill
+  tolerance (reference tests/test_linear.py:207-225, rtol = atol = 1e-3);
+* GPU tensors otherwise (longer prompts, ``fused=False``):
+  ``w4a16::dequantize`` then ``F.linear`` (hipBLASLt) when group_size is a
+  multiple of 32, else ``w4a16::linear``'s generic kernel (any M, any even
+  group size).
 
 GPU tensors never take a torch or CPU fallback: without the extension they
 raise ``RuntimeError``.
@@ -27,6 +34,12 @@ from nibble_amd.reference import dequantize_weights, linear_reference
 
 # Largest M routed to the fused kernels; larger M dequantizes and uses a GEMM.
 FUSED_MAX_ROWS = 8
+# Largest M routed to the W4A16 GEMM when fused (group size 128): measured
+# against dequantize + hipBLASLt on the 1.1B / 8B layers up to M = 256
+# (e.g. M = 256, K 4096 x N 14336: 51 us against 81 us; M = 64, 5632 x 2048:
+# 10 us against 32 us); longer prompts keep dequantize + hipBLASLt, whose
+# MFMA efficiency the GEMM does not reach.
+NATIVE_GEMM_MAX_ROWS = 256
 
 
 class QuantizedLinear(torch.nn.Module):
@@ -68,6 +81,10 @@ class QuantizedLinear(torch.nn.Module):
         self.register_buffer("scales", scales.detach())
         self.register_buffer("bias", None if bias is None else bias.detach())
         self.fused = fused
+        # prompt rows up to this count take the W4A16 GEMM when fused (set it
+        # to FUSED_MAX_ROWS for the reference's routing: dequantize + GEMM for
+        # every M > 8)
+        self.native_max_rows = NATIVE_GEMM_MAX_ROWS
 
     @classmethod
     def from_float(cls, layer: torch.nn.Linear, group_size: int = 128, fused: bool = True) -> "QuantizedLinear":
@@ -139,6 +156,8 @@ class QuantizedLinear(torch.nn.Module):
             if not self.scales.is_contiguous():
                 raise ValueError("scales must be contiguous")
             if self.fused and rows <= FUSED_MAX_ROWS:
+                out = linear_cuda(flat, self.packed_weights, self.scales, self.group_size)
+            elif self.fused and self.group_size == 128 and rows <= self.native_max_rows:
                 out = linear_cuda(flat, self.packed_weights, self.scales, self.group_size)
             elif self.group_size % 32 == 0:
                 out = self._dequant_linear(flat)

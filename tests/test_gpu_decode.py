@@ -501,6 +501,42 @@ def test_fused_decode_graph_matches_eager(gpu):
         assert torch.equal(model.generate(prompt, 10, use_graph=True), eager)
 
 
+def test_full_size_fused_step_and_graphed_tokens(gpu):
+    """configs[4] at full size (22 layers, hidden 2048, 155 INT4 linears, the
+    benchmark's seeds): one fused decode step against the torch-op step from
+    the same state (logits |err| <= 2e-2 (1 + |ref|)), and 32 greedy tokens
+    from HIP-graph replays equal to eager fused decode."""
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(max_seq_len=48)
+    model = LlamaDecoder(cfg, device=gpu, seed=0)
+    assert model.fused and model.attn_o and len(model.linear_layers()) == 155
+    prompt = torch.randint(0, cfg.vocab_size, (16,), generator=torch.Generator().manual_seed(0)).to(gpu)
+    print("[case] full-size 1.1B: prefill + one step each path", flush=True)
+    model.prefill(prompt)
+    state = (model.k_cache.clone(), model.v_cache.clone(), model.token.clone(), model.position.clone(),
+             model.x_buf.clone())
+    with torch.inference_mode():
+        model.fused = False
+        model.step()
+        ref_logits = model.logits.clone()
+        for t, s in zip((model.k_cache, model.v_cache, model.token, model.position, model.x_buf), state):
+            t.copy_(s)
+        model.fused = True
+        model.host_position = int(state[3])
+        model.step()
+    torch.cuda.synchronize()
+    got, ref = model.logits.float().cpu(), ref_logits.float().cpu()
+    assert torch.isfinite(got).all()
+    assert torch.all((got - ref).abs() <= 2e-2 * (1 + ref.abs())), float((got - ref).abs().max())
+    print("[case] full-size 1.1B: 32 tokens eager vs graph", flush=True)
+    eager = model.generate(prompt, 32, use_graph=False)
+    model.prefill(prompt)
+    model.capture()
+    graphed = model.generate(prompt, 32, use_graph=True)
+    assert graphed.shape == (32,) and torch.equal(graphed, eager)
+
+
 def test_checkpoint_into_fused_decoder(gpu, tmp_path):
     """A whole-model checkpoint (reference format) from an offline Hugging Face
     Llama with head_dim 64 runs on the fused step: graph replays equal eager

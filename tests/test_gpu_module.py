@@ -110,13 +110,37 @@ def test_module_noncontiguous_and_3d(gpu):
     assert_parity(out3.reshape(6, 16), expected(x, p, s), "3-D")
 
 
-@pytest.mark.parametrize("fused,m", [(True, 16), (False, 1), (False, 4)])
-def test_module_dequant_gemm_path(gpu, fused, m):
-    # M > FUSED_MAX_ROWS or fused=False: HIP dequantize + F.linear (hipBLASLt)
-    x, p, s = make_case(m, 128, 8, seed=3)
+@pytest.mark.parametrize("fused,m,k,n", [(True, 16, 128, 8), (True, 300, 128, 8), (False, 1, 128, 8),
+                                         (False, 4, 128, 8), (True, 64, 2048, 5632), (True, 256, 4096, 512),
+                                         (True, 9, 5632, 300)])
+def test_module_prefill_paths_match_dequant_linear(gpu, fused, m, k, n):
+    """Prompts: fused layers run the W4A16 GEMM up to NATIVE_GEMM_MAX_ROWS
+    rows, longer prompts and fused=False layers dequantize + F.linear
+    (hipBLASLt); every path agrees with F.linear on the dequantized fp16
+    weights at the reference's prefill tolerance (reference
+    tests/test_linear.py:207-243, rtol = atol = 1e-3)."""
+    from nibble_amd.linear import NATIVE_GEMM_MAX_ROWS
+
+    x, p, s = make_case(m, k, n, seed=3 + m)
     layer = QuantizedLinear(*_on(gpu, p, s), group_size=128, fused=fused)
     w16 = torch.from_numpy(oracle.dequantize_f16(p.numpy(), s.numpy(), 128)).to(gpu)
-    torch.testing.assert_close(layer(x.to(gpu)), F.linear(x.to(gpu), w16), rtol=1e-3, atol=1e-3)
+    out = layer(x.to(gpu))
+    torch.testing.assert_close(out, F.linear(x.to(gpu), w16), rtol=1e-3, atol=1e-3)
+    if fused and 8 < m <= NATIVE_GEMM_MAX_ROWS:
+        # the module's prompt rows are the op's, bit for bit
+        assert torch.equal(out, linear_cuda(x.to(gpu), *_on(gpu, p, s), 128))
+
+
+def test_module_prefill_matches_dequant_linear_reference_case(gpu):
+    """Reference tests/test_linear.py:207-225 with its inputs: fp16 randn
+    weights quantized on the device, M = 16 > FUSED_MAX_ROWS."""
+    torch.manual_seed(0)
+    activations = torch.randn((16, 128), dtype=torch.float16, device=gpu)
+    weights = torch.randn((8, 128), dtype=torch.float16, device=gpu)
+    packed, scales = quantize_and_pack_weights(weights, group_size=128)
+    layer = QuantizedLinear(packed, scales, group_size=128, fused=True)
+    w16 = dequantize_cuda(packed, scales, 128)
+    torch.testing.assert_close(layer(activations), F.linear(activations, w16), rtol=1e-3, atol=1e-3)
 
 
 def test_module_prefill_odd_group_uses_generic_kernel(gpu):
