@@ -175,10 +175,20 @@ def gpu_state_under_load(graph, seconds: float = 1.0) -> dict | None:
                 pass
             stop.wait(0.05)
 
+    firmware = {}
     try:
         handles = amdsmi.amdsmi_get_processor_handles()
         if not handles:
             return None
+        try:
+            # The compute microcode (MEC) decides whether kernel arguments are
+            # preloaded into SGPRs or loaded by the code object's prologue.
+            for entry in amdsmi.amdsmi_get_fw_info(handles[0]).get("fw_list", []):
+                name = str(entry.get("fw_name", entry.get("fw_id", "")))
+                if "MEC" in name or "RLC" in name:
+                    firmware[name.split(".")[-1]] = str(entry.get("fw_version"))
+        except Exception:
+            pass
         thread = threading.Thread(target=sampler, args=(handles[0],), daemon=True)
         thread.start()
         t0 = time.perf_counter()
@@ -202,7 +212,8 @@ def gpu_state_under_load(graph, seconds: float = 1.0) -> dict | None:
         return {"min": vals[0], "median": vals[len(vals) // 2], "max": vals[-1]}
 
     return {"samples": len(samples), "gfx_clock_mhz": stats([s[0] for s in samples]),
-            "mem_clock_mhz": stats([s[1] for s in samples]), "socket_power_w": stats([s[2] for s in samples])}
+            "mem_clock_mhz": stats([s[1] for s in samples]), "socket_power_w": stats([s[2] for s in samples]),
+            "firmware": firmware or None}
 
 
 def copy_bandwidth(device) -> float:
