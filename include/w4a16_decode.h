@@ -121,6 +121,45 @@ int w4a16_attention_o_f16(const void* qkv, void* k_cache, void* v_cache, const f
                           int64_t group_size, void* stream);
 
 /*
+ * The q|k|v projection of a decode step with the rotary embedding and the
+ * KV-cache append in its epilogue: qkv = W . x' as w4a16_gemv_fused_f16
+ * (norm_weight optional), N = (num_heads + 2 num_kv_heads) * 64 rows in the
+ * layout of w4a16_decode_attention_f16, each rounded to fp16; then every q
+ * and k head's dims (d, d + 32), d < 32, are rotated by the fp32 angle
+ * position * inv_freq[d] (fp32 products of the fp16 values, rounded to
+ * fp16), the rotated q and k and the v rows are stored in qkv, and when
+ * 0 <= position < max_seq_len the k and v rows go to cache slot `position`
+ * of k_cache / v_cache [num_kv_heads, max_seq_len, 64] (other slots are not
+ * touched). Needs head_dim 64, group_size 128, K a multiple of 128 up to
+ * 16384, 16-byte aligned activations, norm_weight and packed_weights.
+ * Replaces (reference): Llama input RMSNorm + q_proj / k_proj / v_proj
+ * QuantizedLinear calls (w4a16/linear.py:154-200) + rotary embedding +
+ * static-cache update of HF LlamaAttention in scripts/generate.py:260-305.
+ */
+int w4a16_gemv_qkv_rope_f16(const void* activations, const void* norm_weight, float eps,
+                            const uint8_t* packed_weights, const void* scales, void* qkv,
+                            void* k_cache, void* v_cache, const float* inv_freq,
+                            const int64_t* position, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t max_seq_len, int64_t K,
+                            int64_t group_size, void* stream);
+
+/*
+ * w4a16_attention_o_f16 after w4a16_gemv_qkv_rope_f16: q in qkv is already
+ * rotated and slot `position` of the caches already holds the new k and v,
+ * so the kernel only reads them (k and v in qkv are not used): residual[n] =
+ * fp16(residual[n] + fp16(o_packed[n] . attn)), attn = softmax(q k^T / 8) v
+ * over cache slots 0..position. Same requirements and out-of-range
+ * behaviour as w4a16_attention_o_f16 (NaN rows, caches untouched).
+ * Replaces (reference): as w4a16_attention_o_f16, without the rotary
+ * embedding and cache update.
+ */
+int w4a16_attention_o_cached_f16(const void* qkv, const void* k_cache, const void* v_cache,
+                                 const int64_t* position, const uint8_t* o_packed,
+                                 const void* o_scales, void* residual, int64_t num_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len,
+                                 int64_t hidden, int64_t group_size, void* stream);
+
+/*
  * Greedy token: *token = first index of the maximum of logits[0..n) (fp16);
  * if position != NULL, *position += 1.
  * Replaces (reference): the greedy pick of HF generate(do_sample=False),

@@ -76,6 +76,11 @@ DECODE_SIGNATURES = {
     ),
     "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
     "w4a16_attention_o_f16": (ctypes.c_int, [_vp] * 8 + [_i64] * 6 + [_vp]),
+    "w4a16_gemv_qkv_rope_f16": (
+        ctypes.c_int,
+        [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp] + [_i64] * 6 + [_vp],
+    ),
+    "w4a16_attention_o_cached_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 6 + [_vp]),
     "w4a16_gemv_argmax_workspace_bytes": (_i64, [_i64]),
     "w4a16_gemv_argmax_f16": (
         ctypes.c_int,
@@ -287,6 +292,36 @@ def attention_o_f16(qkv, k_cache, v_cache, inv_freq, position, o_packed, o_scale
             qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), inv_freq.data_ptr(), position.data_ptr(),
             o_packed.data_ptr(), o_scales.data_ptr(), residual.data_ptr(), num_heads, num_kv_heads, head_dim,
             k_cache.shape[-2], residual.numel(), group_size, _stream_ptr(stream),
+        )
+    )
+
+
+def gemv_qkv_rope_f16(activations, packed_weights, scales, qkv, k_cache, v_cache, inv_freq, position,
+                      num_heads: int, num_kv_heads: int, norm_weight=None, eps: float = 1e-5, head_dim: int = 64,
+                      group_size: int = 128, stream=None) -> None:
+    """``w4a16_gemv_qkv_rope_f16``: RMSNorm (optional) + the q|k|v GEMV of one
+    row, q / k rotated at the device position, k / v appended to the caches
+    [kv_heads, S, head_dim]; qkv receives the rotated q, k and the v rows."""
+    _raise_on(
+        lib().w4a16_gemv_qkv_rope_f16(
+            activations.data_ptr(), _ptr(norm_weight), float(eps), packed_weights.data_ptr(), scales.data_ptr(),
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), inv_freq.data_ptr(), position.data_ptr(),
+            num_heads, num_kv_heads, head_dim, k_cache.shape[-2], activations.shape[-1], group_size,
+            _stream_ptr(stream),
+        )
+    )
+
+
+def attention_o_cached_f16(qkv, k_cache, v_cache, position, o_packed, o_scales, residual, num_heads: int,
+                           num_kv_heads: int, head_dim: int = 64, group_size: int = 128, stream=None) -> None:
+    """``w4a16_attention_o_cached_f16``: attention + o projection + residual
+    after ``gemv_qkv_rope_f16`` (rotated q in qkv, slot `position` already in
+    the caches; position < 64)."""
+    _raise_on(
+        lib().w4a16_attention_o_cached_f16(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), position.data_ptr(), o_packed.data_ptr(),
+            o_scales.data_ptr(), residual.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2],
+            residual.numel(), group_size, _stream_ptr(stream),
         )
     )
 

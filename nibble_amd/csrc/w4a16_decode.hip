@@ -307,8 +307,11 @@ embedding_kernel(const f16* __restrict__ table, int64_t vocab, int hidden, const
 // Grid: ceil(N / (R * KV)) workgroups of KV wavefronts, N = hidden size.
 // Every workgroup recomputes the whole attention output (all H = KV * group
 // query heads over slots 0..p) from the caches, keeps it in LDS as the o
-// GEMV's activation row and then runs the one-shot GEMV for its R * KV
-// output rows; the o weights are requested at launch, so they stream in
+// GEMV's activation row (unit-major: 16-byte unit q of 32-weight chunk c at
+// slot q C + c, natural order) and then runs the GEMV for its R * KV output
+// rows with the exact decode (unpack8 against permute8 of the unit), so no
+// staging pass or second barrier follows the attention; the o weights and
+// the rows' residual values are requested at launch, so they stream in
 // while the attention runs. Wavefront g handles KV head g and its `group`
 // query heads (group <= 16) on the matrix cores:
 //   S^T = K Q^T (v_mfma_f32_16x16x32_f16; A = cache rows, lane (q4, j) holds
@@ -338,6 +341,28 @@ constexpr int kVStride = 72;   // V tile row stride in halves (144 bytes: confli
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
+// Max / sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four 16-lane
+// rows), in every lane: v_permlane16_swap / v_permlane32_swap hand each lane
+// its partner's value without LDS. Sums pair the rows as (r0 + r1) + (r2 + r3)
+// in every lane, so all lanes hold the same bits.
+__device__ __forceinline__ float row_pair_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    v = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+
+__device__ __forceinline__ float row_pair_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    v = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
+                                                    false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
+}
+
 // ds_read_b64_tr_b16 at an LDS address (see attn_o_kernel for the lane mapping)
 __device__ __forceinline__ uint2 lds_read_tr16(const f16* p) {
     const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -345,7 +370,7 @@ __device__ __forceinline__ uint2 lds_read_tr16(const f16* p) {
     return __builtin_bit_cast(uint2, v);
 }
 
-template <int KV, int R, int L>
+template <int KV, int R, int L, bool CACHED>
 __global__ void __launch_bounds__(64 * KV)
 attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
               const float* __restrict__ inv_freq, const int64_t* __restrict__ position,
@@ -353,17 +378,15 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
               int N) {
     constexpr int D = 64;
     const int64_t p64 = position[0];
-    const float freq = inv_freq[threadIdx.x & 31];
+    const float freq = CACHED ? 0.0f : inv_freq[threadIdx.x & 31];
     __builtin_amdgcn_sched_barrier(0);
     extern __shared__ __align__(16) uint8_t smem[];
     const int H = KV * group;
     const int K = H * D;                 // o projection input width
     const int C = K >> 5, G = K >> 7;
     f16* vt_all = reinterpret_cast<f16*>(smem);                        // [KV][64 slots][kVStride]
-    f16* att = vt_all + KV * kAttnOSlots * kVStride;                    // [H * 64]
-    u32x4* xs = reinterpret_cast<u32x4*>(att + K);                      // staged GEMV activations
-    float* cbias = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(xs) + (size_t)K * 2);
-    float* trig_all = cbias + C;                                        // [KV][64]: cos | sin
+    u32x4* xs = reinterpret_cast<u32x4*>(vt_all + KV * kAttnOSlots * kVStride);   // [4][C] attention units
+    float* trig_all = reinterpret_cast<float*>(xs + 4 * C);             // [KV][64]: cos | sin
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -391,9 +414,9 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         qb[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)hq * D + 32 * s + 8 * q4);
-        kn[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)(H + g) * D + 32 * s + 8 * q4);
+        if (!CACHED) kn[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)(H + g) * D + 32 * s + 8 * q4);
     }
-    const f16 vn = qkv[(size_t)(H + KV + g) * D + lane];
+    const f16 vn = CACHED ? (f16)0.0f : qkv[(size_t)(H + KV + g) * D + lane];
     // o weights and scales of this wavefront's R rows (one-shot layout)
     const int row0 = (blockIdx.x * KV + wave) * R;
     const uint32_t row_bytes = (uint32_t)(K >> 1);
@@ -416,51 +439,62 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
             wv[r][l] = load_stream(reinterpret_cast<const u32x4*>(wrow + c * 16u));
         }
     }
+    // the rows' residual values (each is read and rewritten by this lane 0 only)
+    f16 res[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) res[r] = resid[min(row0 + r, N - 1)];
     __builtin_amdgcn_sched_barrier(0);
 
     const bool valid = p64 >= 0 && p64 < S && p64 < kAttnOSlots;
     const int p = valid ? (int)p64 : 0;
 
-    // 2. cos / sin of p * inv_freq, one frequency per lane (two copies)
-    float* trig = trig_all + wave * 64;
-    {
-        float sn, cs;
-        sincosf((float)p * freq, &sn, &cs);
-        trig[lane] = lane < 32 ? cs : sn;
-    }
-    wave_lds_sync();
-    // rotate q (B operand) and the new k: dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i (s = 1)
-    u32x4 qr[2], kr[2];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const float c0 = trig[8 * q4 + 2 * h], c1 = trig[8 * q4 + 2 * h + 1];
-        const float s0 = trig[32 + 8 * q4 + 2 * h], s1 = trig[32 + 8 * q4 + 2 * h + 1];
-        const f16x2 qa = as_f16x2(qb[0][h]), qz = as_f16x2(qb[1][h]);
-        const f16x2 ka2 = as_f16x2(kn[0][h]), kz = as_f16x2(kn[1][h]);
-        const f16x2 qlo = {(f16)((float)qa.x * c0 - (float)qz.x * s0), (f16)((float)qa.y * c1 - (float)qz.y * s1)};
-        const f16x2 qhi = {(f16)((float)qz.x * c0 + (float)qa.x * s0), (f16)((float)qz.y * c1 + (float)qa.y * s1)};
-        const f16x2 klo = {(f16)((float)ka2.x * c0 - (float)kz.x * s0), (f16)((float)ka2.y * c1 - (float)kz.y * s1)};
-        const f16x2 khi = {(f16)((float)kz.x * c0 + (float)ka2.x * s0), (f16)((float)kz.y * c1 + (float)ka2.y * s1)};
-        qr[0][h] = as_u32(qlo);
-        qr[1][h] = as_u32(qhi);
-        kr[0][h] = as_u32(klo);
-        kr[1][h] = as_u32(khi);
-    }
-    // slot p's key row is the new k (never the cache line being written)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const bool is_p = 16 * mt + j == p;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) ka[mt][s] = is_p ? kr[s] : ka[mt][s];
-    }
-    // the append: workgroup 0 writes slot p of this KV head
-    if (blockIdx.x == 0 && valid) {
-        if (j == 0) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-                *reinterpret_cast<u32x4*>(k_cache + ((size_t)g * S + p) * D + 32 * s + 8 * q4) = kr[s];
+    u32x4 qr[2];
+    if constexpr (CACHED) {
+        // q arrives rotated and slot p is already in the caches
+        qr[0] = qb[0];
+        qr[1] = qb[1];
+    } else {
+        // 2. cos / sin of p * inv_freq, one frequency per lane (two copies)
+        float* trig = trig_all + wave * 64;
+        {
+            float sn, cs;
+            sincosf((float)p * freq, &sn, &cs);
+            trig[lane] = lane < 32 ? cs : sn;
         }
-        v_cache[((size_t)g * S + p) * D + lane] = vn;
+        wave_lds_sync();
+        // rotate q (B operand) and the new k: dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i (s = 1)
+        u32x4 kr[2];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const float c0 = trig[8 * q4 + 2 * h], c1 = trig[8 * q4 + 2 * h + 1];
+            const float s0 = trig[32 + 8 * q4 + 2 * h], s1 = trig[32 + 8 * q4 + 2 * h + 1];
+            const f16x2 qa = as_f16x2(qb[0][h]), qz = as_f16x2(qb[1][h]);
+            const f16x2 ka2 = as_f16x2(kn[0][h]), kz = as_f16x2(kn[1][h]);
+            const f16x2 qlo = {(f16)((float)qa.x * c0 - (float)qz.x * s0), (f16)((float)qa.y * c1 - (float)qz.y * s1)};
+            const f16x2 qhi = {(f16)((float)qz.x * c0 + (float)qa.x * s0), (f16)((float)qz.y * c1 + (float)qa.y * s1)};
+            const f16x2 klo = {(f16)((float)ka2.x * c0 - (float)kz.x * s0), (f16)((float)ka2.y * c1 - (float)kz.y * s1)};
+            const f16x2 khi = {(f16)((float)kz.x * c0 + (float)ka2.x * s0), (f16)((float)kz.y * c1 + (float)ka2.y * s1)};
+            qr[0][h] = as_u32(qlo);
+            qr[1][h] = as_u32(qhi);
+            kr[0][h] = as_u32(klo);
+            kr[1][h] = as_u32(khi);
+        }
+        // slot p's key row is the new k (never the cache line being written)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const bool is_p = 16 * mt + j == p;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) ka[mt][s] = is_p ? kr[s] : ka[mt][s];
+        }
+        // the append: workgroup 0 writes slot p of this KV head
+        if (blockIdx.x == 0 && valid) {
+            if (j == 0) {
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+                    *reinterpret_cast<u32x4*>(k_cache + ((size_t)g * S + p) * D + 32 * s + 8 * q4) = kr[s];
+            }
+            v_cache[((size_t)g * S + p) * D + lane] = vn;
+        }
     }
 
     // 3. V tile into LDS, row-major: lane l stores slot l (zero past p), then
@@ -471,8 +505,10 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
         u32x4* row = reinterpret_cast<u32x4*>(vt + lane * kVStride);
 #pragma unroll
         for (int e = 0; e < 8; ++e) row[e] = live ? vr[e] : (u32x4){0u, 0u, 0u, 0u};
-        wave_lds_sync();
-        vt[p * kVStride + lane] = vn;
+        if (!CACHED) {
+            wave_lds_sync();
+            vt[p * kVStride + lane] = vn;
+        }
     }
 
     // 4. S^T = K Q^T, softmax over the head's 64 slots
@@ -494,8 +530,7 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
             st[mt][e] = slot <= p ? st[mt][e] * 0.125f : -__builtin_inff();
             mx = fmaxf(mx, st[mt][e]);
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = row_pair_max(mx);
     float sum = 0.0f;
     u32x4 pb[2];   // P^T as the B operand of the two k-steps
 #pragma unroll
@@ -511,8 +546,7 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
         pb[mt >> 1][2 * (mt & 1)] = as_u32(a);
         pb[mt >> 1][2 * (mt & 1) + 1] = as_u32(b);
     }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum = row_pair_sum(sum);
     wave_lds_sync();
 
     // 5. O^T = V^T P^T; lane (q4, j) receives head j, dims 16 md + 4 q4 + e
@@ -533,49 +567,42 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
         if (j < group) {
             const f16x2 a = {(f16)(o[0] * inv_sum), (f16)(o[1] * inv_sum)};
             const f16x2 b = {(f16)(o[2] * inv_sum), (f16)(o[3] * inv_sum)};
-            *reinterpret_cast<uint2*>(att + (size_t)(g * group + j) * D + 16 * md + 4 * q4) = make_uint2(as_u32(a), as_u32(b));
+            // dims k .. k+3 of the row: chunk k / 32, unit (k / 8) % 4, halves k % 8 ..
+            const int k = (g * group + j) * D + 16 * md + 4 * q4;
+            uint8_t* dst = reinterpret_cast<uint8_t*>(xs + ((k >> 3) & 3) * C + (k >> 5)) + (k & 7) * 2;
+            *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(a), as_u32(b));
         }
     }
     __syncthreads();
 
-    // 6. the attention row as the o GEMV's staged activations (offset decode)
-    constexpr int T = 64 * KV;
-    const int units = K >> 3;
-    for (int i0 = 0; i0 < units; i0 += T) {
-        const int i = i0 + threadIdx.x;
-        float bias;
-        const u32x4 v = stage_offset(reinterpret_cast<const u32x4*>(att)[min(i, units - 1)], bias);
-        if (i < units) {
-            xs[(i & 3) * C + (i >> 2)] = v;
-            if ((i & 3) == 0) cbias[i >> 2] = bias;
-        }
-    }
-    __syncthreads();
-
-    // 7. o rows: dot products (as gemv_oneshot, M = 1) and the residual add
+    // 6. o rows: exact decode against the permuted attention units, then the
+    // residual add
+    u32x4 xp[L][4];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) xp[l][qq] = permute8(xs[qq * C + min(l * 64 + lane, C - 1)]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         float acc = 0.0f;
 #pragma unroll
         for (int l = 0; l < L; ++l) {
             const int c = l * 64 + lane;
-            const int cc = min(c, C - 1);
-            float d = cbias[cc];
+            float d = 0.0f;
 #pragma unroll
             for (int qq = 0; qq < 4; ++qq) {
-                const Codes8 cw = unpack8_offset(wv[r][l][qq]);
-                const u32x4 xv = xs[qq * C + cc];
-                d = __builtin_amdgcn_fdot2(as_f16x2(xv.x), cw.p[0], d, false);
-                d = __builtin_amdgcn_fdot2(as_f16x2(xv.y), cw.p[1], d, false);
-                d = __builtin_amdgcn_fdot2(as_f16x2(xv.z), cw.p[2], d, false);
-                d = __builtin_amdgcn_fdot2(as_f16x2(xv.w), cw.p[3], d, false);
+                const Codes8 cw = unpack8(wv[r][l][qq]);
+                d = __builtin_amdgcn_fdot2(as_f16x2(xp[l][qq].x), cw.p[0], d, false);
+                d = __builtin_amdgcn_fdot2(as_f16x2(xp[l][qq].y), cw.p[1], d, false);
+                d = __builtin_amdgcn_fdot2(as_f16x2(xp[l][qq].z), cw.p[2], d, false);
+                d = __builtin_amdgcn_fdot2(as_f16x2(xp[l][qq].w), cw.p[3], d, false);
             }
             const float sc = (float)__builtin_bit_cast(f16, (uint16_t)sv[r][l]);
             acc = __builtin_fmaf(c < C ? d : 0.0f, sc, acc);
         }
         const float v = wave_sum(acc);
         const int n = row0 + r;
-        if (lane == 0 && n < N) resid[n] = (f16)((float)resid[n] + (float)(f16)v);
+        if (lane == 0 && n < N) resid[n] = (f16)((float)res[r] + (float)(f16)v);
     }
 }
 
@@ -928,6 +955,59 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 }  // namespace
 
+namespace {
+
+// Shape checks and launch shared by the two attention + o entry points.
+template <bool CACHED>
+int launch_attention_o(const void* qkv, void* k_cache, void* v_cache, const float* inv_freq, const int64_t* position,
+                       const uint8_t* o_packed, const void* o_scales, void* residual, int64_t num_heads,
+                       int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len, int64_t hidden,
+                       int64_t group_size, void* stream) {
+    using namespace w4a16;
+    if (!qkv || !k_cache || !v_cache || (!CACHED && !inv_freq) || !position || !o_packed || !o_scales || !residual)
+        return fail(W4A16_ERR_NULL, "attention_o: every pointer must be non-NULL");
+    if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "attention_o: head_dim must be 64");
+    if (group_size != 128) return fail(W4A16_ERR_CONFIG, "attention_o: group_size must be 128");
+    if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
+        return fail(W4A16_ERR_CONFIG, "attention_o: num_kv_heads must be 1, 2, 4 or 8");
+    if (num_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 16 || num_heads * 64 > 4096)
+        return fail(W4A16_ERR_SHAPE,
+                    "attention_o: num_heads must be a multiple of num_kv_heads, at most 16 per KV head and 64 in all");
+    if (max_seq_len <= 0 || max_seq_len > 16384)
+        return fail(W4A16_ERR_SHAPE, "attention_o: max_seq_len must be in 1..16384");
+    if (hidden <= 0 || hidden > INT32_MAX / 2) return fail(W4A16_ERR_SHAPE, "attention_o: hidden must be positive");
+    if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o_packed, 16) ||
+        !aligned(o_scales, 2) || !aligned(residual, 2) || (!CACHED && !aligned(inv_freq, 4)))
+        return fail(W4A16_ERR_ALIGNMENT, "attention_o: qkv, caches and o_packed must be 16-byte aligned");
+    const int KV = (int)num_kv_heads, group = (int)(num_heads / num_kv_heads);
+    const int K = (int)num_heads * 64;
+    const int L = (K / 32 + 63) / 64;   // 1 KiB loads per o row: 1 or 2
+    constexpr int R = 2;                // o rows per wavefront
+    void (*kern)(const f16*, f16*, f16*, const float*, const int64_t*, const uint8_t*, const f16*, f16*, int, int,
+                 int) = nullptr;
+    switch (KV) {
+        case 1: kern = L == 1 ? attn_o_kernel<1, R, 1, CACHED> : attn_o_kernel<1, R, 2, CACHED>; break;
+        case 2: kern = L == 1 ? attn_o_kernel<2, R, 1, CACHED> : attn_o_kernel<2, R, 2, CACHED>; break;
+        case 4: kern = L == 1 ? attn_o_kernel<4, R, 1, CACHED> : attn_o_kernel<4, R, 2, CACHED>; break;
+        default: kern = L == 1 ? attn_o_kernel<8, R, 1, CACHED> : attn_o_kernel<8, R, 2, CACHED>; break;
+    }
+    const int lds = KV * kAttnOSlots * kVStride * 2 + K * 2 + KV * 64 * 4;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "attention_o: LDS request refused");
+    }
+    const int rows_per_block = R * KV;
+    const int blocks = (int)((hidden + rows_per_block - 1) / rows_per_block);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * KV), lds, static_cast<hipStream_t>(stream),
+                       static_cast<const f16*>(qkv), static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), inv_freq,
+                       position, o_packed, static_cast<const f16*>(o_scales), static_cast<f16*>(residual), group,
+                       (int)max_seq_len, (int)hidden);
+    return check_launch();
+}
+
+}  // namespace
+
 extern "C" {
 
 int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
@@ -960,47 +1040,17 @@ int w4a16_attention_o_f16(const void* qkv, void* k_cache, void* v_cache, const f
                           const int64_t* position, const uint8_t* o_packed, const void* o_scales, void* residual,
                           int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len,
                           int64_t hidden, int64_t group_size, void* stream) {
-    using namespace w4a16;
-    if (!qkv || !k_cache || !v_cache || !inv_freq || !position || !o_packed || !o_scales || !residual)
-        return fail(W4A16_ERR_NULL, "attention_o: every pointer must be non-NULL");
-    if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "attention_o: head_dim must be 64");
-    if (group_size != 128) return fail(W4A16_ERR_CONFIG, "attention_o: group_size must be 128");
-    if (num_kv_heads != 1 && num_kv_heads != 2 && num_kv_heads != 4 && num_kv_heads != 8)
-        return fail(W4A16_ERR_CONFIG, "attention_o: num_kv_heads must be 1, 2, 4 or 8");
-    if (num_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > 16 || num_heads * 64 > 4096)
-        return fail(W4A16_ERR_SHAPE,
-                    "attention_o: num_heads must be a multiple of num_kv_heads, at most 16 per KV head and 64 in all");
-    if (max_seq_len <= 0 || max_seq_len > 16384)
-        return fail(W4A16_ERR_SHAPE, "attention_o: max_seq_len must be in 1..16384");
-    if (hidden <= 0 || hidden > INT32_MAX / 2) return fail(W4A16_ERR_SHAPE, "attention_o: hidden must be positive");
-    if (!aligned(qkv, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o_packed, 16) ||
-        !aligned(o_scales, 2) || !aligned(residual, 2) || !aligned(inv_freq, 4))
-        return fail(W4A16_ERR_ALIGNMENT, "attention_o: qkv, caches and o_packed must be 16-byte aligned");
-    const int KV = (int)num_kv_heads, group = (int)(num_heads / num_kv_heads);
-    const int K = (int)num_heads * 64;
-    const int L = (K / 32 + 63) / 64;   // 1 KiB loads per o row: 1 or 2
-    constexpr int R = 2;                // o rows per wavefront
-    void (*kern)(const f16*, f16*, f16*, const float*, const int64_t*, const uint8_t*, const f16*, f16*, int, int,
-                 int) = nullptr;
-    switch (KV) {
-        case 1: kern = L == 1 ? attn_o_kernel<1, R, 1> : attn_o_kernel<1, R, 2>; break;
-        case 2: kern = L == 1 ? attn_o_kernel<2, R, 1> : attn_o_kernel<2, R, 2>; break;
-        case 4: kern = L == 1 ? attn_o_kernel<4, R, 1> : attn_o_kernel<4, R, 2>; break;
-        default: kern = L == 1 ? attn_o_kernel<8, R, 1> : attn_o_kernel<8, R, 2>; break;
-    }
-    const int lds = KV * kAttnOSlots * kVStride * 2 + K * 4 + (K / 32) * 4 + KV * 64 * 4;
-    if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "attention_o: LDS request refused");
-    }
-    const int rows_per_block = R * KV;
-    const int blocks = (int)((hidden + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * KV), lds, static_cast<hipStream_t>(stream),
-                       static_cast<const f16*>(qkv), static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), inv_freq,
-                       position, o_packed, static_cast<const f16*>(o_scales), static_cast<f16*>(residual), group,
-                       (int)max_seq_len, (int)hidden);
-    return check_launch();
+    return launch_attention_o<false>(qkv, k_cache, v_cache, inv_freq, position, o_packed, o_scales, residual,
+                                     num_heads, num_kv_heads, head_dim, max_seq_len, hidden, group_size, stream);
+}
+
+int w4a16_attention_o_cached_f16(const void* qkv, const void* k_cache, const void* v_cache, const int64_t* position,
+                                 const uint8_t* o_packed, const void* o_scales, void* residual, int64_t num_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len, int64_t hidden,
+                                 int64_t group_size, void* stream) {
+    return launch_attention_o<true>(qkv, const_cast<void*>(k_cache), const_cast<void*>(v_cache), nullptr, position,
+                                    o_packed, o_scales, residual, num_heads, num_kv_heads, head_dim, max_seq_len,
+                                    hidden, group_size, stream);
 }
 
 int w4a16_argmax_f16(const void* logits, int64_t n, int64_t* token, int64_t* position, void* stream) {

@@ -769,17 +769,17 @@ int launch_oneshot(Plan p, int M, const w4a16::f16* x, const uint8_t* w, const w
 // sweeps: paired rows R = 2 with 8 wavefronts per workgroup; very wide
 // layers (N >= 16384, the lm_head) 4 rows per wavefront; the other RMSNorm
 // layers (q|k|v) 2 rows and 8 wavefronts; residual layers 1 row and 8.
-template <bool NORM, bool PAIRED, bool ARGMAX = false>
+template <bool NORM, bool PAIRED, bool ARGMAX = false, bool ROPE = false, bool RESID = false>
 int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::GemvFusion& fz, const uint8_t* w,
                    const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
     void (*kern)(const f16*, const uint8_t*, const f16*, f16*, int, int, GemvFusion) = nullptr;
 #define W4A16_PICK_L(RR, LL, WW) \
-    if (R == RR && L == LL && W == WW) kern = gemv_oneshot<1, RR, LL, WW, NORM, PAIRED, ARGMAX>;
+    if (R == RR && L == LL && W == WW) kern = gemv_oneshot<1, RR, LL, WW, NORM, PAIRED, ARGMAX, ROPE, RESID>;
 #define W4A16_PICK(RR, WW)                                                                               \
     W4A16_PICK_L(RR, 1, WW) W4A16_PICK_L(RR, 2, WW) W4A16_PICK_L(RR, 3, WW) W4A16_PICK_L(RR, 4, WW)   \
     W4A16_PICK_L(RR, 5, WW) W4A16_PICK_L(RR, 6, WW) W4A16_PICK_L(RR, 7, WW) W4A16_PICK_L(RR, 8, WW)
-    if constexpr (PAIRED) {
+    if constexpr (PAIRED || ROPE) {
         W4A16_PICK(2, 8)
     } else {
         W4A16_PICK(1, 8) W4A16_PICK(2, 8) W4A16_PICK(4, 4)
@@ -790,7 +790,7 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::GemvFu
     const int lds = (int)oneshot_lds_bytes(1, K, true);
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);
     if (rc != W4A16_OK) return rc;
-    const int tasks = PAIRED ? N / 2 : (N + R - 1) / R;
+    const int tasks = (PAIRED || ROPE) ? N / 2 : (N + R - 1) / R;
     const int blocks = (tasks + W - 1) / W;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * W), lds, stream, x, w, s, o, N, K, fz);
     return check_launch();
@@ -1204,8 +1204,53 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
     if (paired)
         return nw ? launch_fused_t<true, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
                   : launch_fused_t<false, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
+    if (residual)
+        return nw ? launch_fused_t<true, false, false, false, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
+                  : launch_fused_t<false, false, false, false, true>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
     return nw ? launch_fused_t<true, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st)
               : launch_fused_t<false, false>(L, R, W, x, fz, packed_weights, sc, o, n, k, st);
+}
+
+int w4a16_gemv_qkv_rope_f16(const void* activations, const void* norm_weight, float eps,
+                            const uint8_t* packed_weights, const void* scales, void* qkv, void* k_cache,
+                            void* v_cache, const float* inv_freq, const int64_t* position, int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t max_seq_len, int64_t K,
+                            int64_t group_size, void* stream) {
+    if (!activations || !packed_weights || !scales || !qkv || !k_cache || !v_cache || !inv_freq || !position)
+        return fail(W4A16_ERR_NULL, "qkv rope: every pointer except norm_weight must be non-NULL");
+    if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "qkv rope: head_dim must be 64");
+    if (group_size != 128) return fail(W4A16_ERR_GROUP_SIZE, "qkv rope needs group_size 128");
+    if (K <= 0 || K > 16384 || K % 128 != 0)
+        return fail(W4A16_ERR_SHAPE, "qkv rope needs K a multiple of 128 in 128..16384");
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads + 2 * num_kv_heads > 4096)
+        return fail(W4A16_ERR_SHAPE, "qkv rope: num_heads and num_kv_heads must be positive, at most 4096 rows of heads");
+    if (max_seq_len <= 0 || max_seq_len > (int64_t)INT32_MAX / 64)
+        return fail(W4A16_ERR_SHAPE, "qkv rope: max_seq_len must be in 1..2^25");
+    if (!aligned16(activations) || !aligned16(packed_weights) || (norm_weight && !aligned16(norm_weight)))
+        return fail(W4A16_ERR_ALIGNMENT, "qkv rope needs 16-byte aligned activations, norm_weight and weights");
+    if ((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(k_cache) |
+         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(scales)) & 1u)
+        return fail(W4A16_ERR_ALIGNMENT, "qkv rope: qkv, caches and scales must be 2-byte aligned");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "eps must be non-negative");
+    using w4a16::f16;
+    const int N = (int)((num_heads + 2 * num_kv_heads) * 64);
+    w4a16::GemvFusion fz{};
+    fz.norm_weight = static_cast<const f16*>(norm_weight);
+    fz.eps = eps;
+    fz.position = const_cast<int64_t*>(position);
+    fz.inv_freq = inv_freq;
+    fz.k_cache = static_cast<f16*>(k_cache);
+    fz.v_cache = static_cast<f16*>(v_cache);
+    fz.rope_heads = (int)num_heads;
+    fz.rope_pairs = (int)(num_heads + num_kv_heads) * 32;
+    fz.max_seq = (int)max_seq_len;
+    const f16* x = static_cast<const f16*>(activations);
+    const f16* sc = static_cast<const f16*>(scales);
+    f16* o = static_cast<f16*>(qkv);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int L = oneshot_loads(K);
+    return norm_weight ? launch_fused_t<true, false, false, true>(L, 2, 8, x, fz, packed_weights, sc, o, N, (int)K, st)
+                       : launch_fused_t<false, false, false, true>(L, 2, 8, x, fz, packed_weights, sc, o, N, (int)K, st);
 }
 
 int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,

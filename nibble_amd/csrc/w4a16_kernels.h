@@ -286,14 +286,21 @@ gemv_valu(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 //   NORM (norm_weight): the activation row is RMS-normalised while it is staged,
 //     y = fp16((fp32(x) * rsqrt(mean(x^2) + eps)) * fp32(norm_weight)),
 //     the fp32 operation order of an RMSNorm that returns fp16;
-//   residual: out[n] = fp16(fp32(residual[n]) + fp32(fp16(dot))), the fp16
+//   RESID (residual): out[n] = fp16(fp32(residual[n]) + fp32(fp16(dot))), the fp16
 //     "x + linear(a)" of a residual stream (residual may alias out: each
 //     row is read and written by the same lane);
 //   PAIRED (R = 2): wavefront i owns rows i and i + N/2 of a [gate; up]
 //     weight pair and stores out[i] = fp16(silu(g) * u) with g, u, silu(g)
 //     each rounded to fp16 first, as fp16 tensors would be;
 //   ARGMAX: the rows' fp16 logits (stored when out != nullptr) feed a greedy
-//     argmax over all N rows in the kernel's tail (argmax_tail).
+//     argmax over all N rows in the kernel's tail (argmax_tail);
+//   ROPE (R = 2, the q|k|v projection of a decode step, head_dim 64): the
+//     first rope_pairs = (H + KV) * 32 wavefronts own rows 64 h + d and
+//     64 h + d + 32 of q or k head h (d < 32), the rest own v rows 2 i and
+//     2 i + 1; the epilogue rounds both rows to fp16, rotates q / k pairs by
+//     the angle fp32(position) * inv_freq[d] (fp32 sincosf, as the separate
+//     rotary step), stores the rotated rows and, when 0 <= position <
+//     max_seq, writes k and v into cache slot `position`.
 // ---------------------------------------------------------------------------
 
 struct GemvFusion {
@@ -309,6 +316,13 @@ struct GemvFusion {
     int64_t vocab;
     int hidden;
     f16* emb_out;
+    // rotary + KV append epilogue (ROPE; position above)
+    const float* inv_freq;    // [32]
+    f16* k_cache;             // [KV][max_seq][64]
+    f16* v_cache;
+    int rope_heads;           // H (query heads)
+    int rope_pairs;           // (H + KV) * 32
+    int max_seq;
 };
 
 // Order-preserving key of an fp16 logit at index n: larger logit first,
@@ -393,11 +407,14 @@ __device__ __forceinline__ void argmax_tail(const float (&rowsum)[R], int row0, 
         fz.emb_out[i] = (t >= 0 && t < fz.vocab) ? fz.table[t * fz.hidden + i] : (f16)0.0f;
 }
 
-template <int M, int R, int L, int W, bool NORM, bool PAIRED, bool ARGMAX = false>
+template <int M, int R, int L, int W, bool NORM, bool PAIRED, bool ARGMAX = false, bool ROPE = false,
+          bool RESID = false>
 __global__ void __launch_bounds__(64 * W)
 gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
              const f16* __restrict__ scales, f16* out, int N, int K, GemvFusion fz) {
     static_assert(!PAIRED || (M == 1 && R == 2), "paired rows are an M = 1, R = 2 layout");
+    static_assert(!ROPE || (M == 1 && R == 2 && !PAIRED && !ARGMAX), "rotary rows are an M = 1, R = 2 layout");
+    static_assert(!RESID || (M == 1 && !PAIRED && !ARGMAX && !ROPE), "the residual add is a plain-row M = 1 epilogue");
     static_assert(!ARGMAX || (M == 1 && !PAIRED), "the argmax epilogue is an M = 1 plain-row layout");
     static_assert(!NORM || M == 1, "the RMSNorm prologue normalises one activation row");
     extern __shared__ __align__(16) uint8_t smem[];
@@ -411,9 +428,10 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     const int task = blockIdx.x * W + wave;
     // row r of this wavefront, and the number of valid tasks
     const int half = N >> 1;
-    const int row0 = PAIRED ? task : task * R;
-    const int row_step = PAIRED ? half : 1;
-    const bool valid = PAIRED ? task < half : row0 < N;
+    const bool rot = ROPE && task < fz.rope_pairs;   // a q / k rotary pair (else v rows)
+    const int row0 = PAIRED ? task : ROPE ? (rot ? (task >> 5) * 64 + (task & 31) : 2 * task) : task * R;
+    const int row_step = PAIRED ? half : (ROPE && rot) ? 32 : 1;
+    const bool valid = (PAIRED || ROPE) ? task < half : row0 < N;
 
     // 1. activations: units i = m * 4C + u, u = 4c + q. Up to kFirst units
     // per thread are requested ahead of the weights; any rest (large M * K)
@@ -427,6 +445,13 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     const int units = M * 4 * C;
     const int units_per_row = 4 * C;
     static_assert(!NORM || kPer == kFirst, "the RMSNorm prologue holds the whole row in registers");
+    // the rotary epilogue's position and frequency, requested first
+    int64_t rope_pos = 0;
+    float rope_freq = 0.0f;
+    if constexpr (ROPE) {
+        rope_pos = fz.position[0];
+        rope_freq = fz.inv_freq[task & 31];
+    }
     u32x4 a[kFirst];
     u32x4 nw[NORM ? kFirst : 1];
 #pragma unroll
@@ -465,6 +490,14 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
             const uint32_t c = (uint32_t)min(j * 64 + lane, C - 1);
             wv[r][j] = load_stream(reinterpret_cast<const u32x4*>(wrow + c * 16u));
         }
+    }
+    // the rows' residual values (RESID), requested with the weights so the
+    // epilogue does not wait a round trip for them (residual[n] is read and
+    // rewritten by this lane only)
+    f16 resv[R];
+    if constexpr (RESID) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) resv[r] = fz.residual[min(row0 + r, N - 1)];
     }
     // keep every request above ahead of the first wait below
     __builtin_amdgcn_sched_barrier(0);
@@ -531,6 +564,11 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
     }
     __syncthreads();
     if (!valid && !ARGMAX) return;   // the argmax tail needs every wavefront at its barriers
+    // the rotation's cos / sin, while the weights are still arriving
+    float rope_cos = 1.0f, rope_sin = 0.0f;
+    if constexpr (ROPE) {
+        if (rot) sincosf((float)rope_pos * rope_freq, &rope_sin, &rope_cos);
+    }
 
     // 4. dot products, row by row in arrival order. Straight-line code (no
     // branch per chunk, so each chunk waits only for its own load): lanes
@@ -567,11 +605,37 @@ gemv_oneshot(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             rowsum[r][m] = wave_sum(acc[m]);
-            if (!PAIRED && lane == 0 && row0 + r < N && (!ARGMAX || out != nullptr)) {
+            if (!PAIRED && !ROPE && lane == 0 && row0 + r < N && (!ARGMAX || out != nullptr)) {
                 const int n = row0 + r;
                 f16 v = (f16)rowsum[r][m];
-                if (fz.residual != nullptr) v = (f16)((float)fz.residual[n] + (float)v);
+                if constexpr (RESID) v = (f16)((float)resv[r] + (float)v);
                 out[(size_t)m * N + n] = v;
+            }
+        }
+    }
+    if constexpr (ROPE) {
+        if (lane == 0) {
+            const f16 a0 = (f16)rowsum[0][0], a1 = (f16)rowsum[1][0];
+            f16 y0 = a0, y1 = a1;
+            if (rot) {
+                y0 = (f16)((float)a0 * rope_cos - (float)a1 * rope_sin);
+                y1 = (f16)((float)a1 * rope_cos + (float)a0 * rope_sin);
+            }
+            const int n1 = row0 + row_step;
+            out[row0] = y0;
+            out[n1] = y1;
+            if (rope_pos >= 0 && rope_pos < fz.max_seq) {
+                const size_t p = (size_t)rope_pos;
+                if (!rot) {   // v rows 2i, 2i+1 of the v block
+                    const int vi = row0 - 2 * fz.rope_pairs;
+                    f16* vc = fz.v_cache + ((size_t)(vi >> 6) * fz.max_seq + p) * 64 + (vi & 63);
+                    vc[0] = y0;
+                    vc[1] = y1;
+                } else if ((row0 >> 6) >= fz.rope_heads) {   // a k head
+                    f16* kc = fz.k_cache + ((size_t)((row0 >> 6) - fz.rope_heads) * fz.max_seq + p) * 64 + (row0 & 63);
+                    kc[0] = y0;
+                    kc[32] = y1;
+                }
             }
         }
     }

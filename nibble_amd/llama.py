@@ -17,10 +17,14 @@ residual, (4) RMSNorm + gate|up GEMV with the SiLU-multiply epilogue, (5)
 down GEMV + residual; then RMSNorm + lm_head GEMV and the greedy argmax,
 which also advances the position and gathers the next token's embedding: 5
 launches per layer plus 2. While the position
-is below 64 (and the head layout allows it), (2) and (3) are one launch
-(``w4a16_attention_o_f16``: every o-projection workgroup recomputes the
-one-chunk attention on the matrix cores), so a step is 4 launches per layer;
-the host tracks the position to pick that step. The q/k/v and
+is below 64 (and the head layout allows it), the rotary embedding and the
+KV-cache append move into the q|k|v GEMV's epilogue
+(``w4a16_gemv_qkv_rope_f16``) and attention + o GEMV + residual are one
+launch (``w4a16_attention_o_cached_f16``: every o-projection workgroup
+recomputes the one-chunk attention on the matrix cores), so a step is 4
+launches per layer; the host tracks the position to pick that step
+(``qkv_rope=False`` keeps rotary and append in the attention launch,
+``w4a16_attention_o_f16``). The q/k/v and
 gate/up weights live in one buffer each, and every ``QuantizedLinear`` keeps
 a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
@@ -248,6 +252,8 @@ class LlamaDecoder(torch.nn.Module):
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
+        # position < 64: rotary + KV append in the q|k|v GEMV's epilogue (else in the attention + o launch)
+        self.qkv_rope = True
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
         self.fuse_prefill = True   # prompts of <= 256 tokens: fused prefill (see fused_prefill)
@@ -394,13 +400,22 @@ class LlamaDecoder(torch.nn.Module):
         for i, b in enumerate(self.layers):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
-            _lib.gemv_fused_f16(x, qkv_w, qkv_s, self.qkv_buf, norm_weight=b.input_norm.weight,
-                                eps=b.input_norm.eps)
-            if short:
+            if short and self.qkv_rope:
+                _lib.gemv_qkv_rope_f16(x, qkv_w, qkv_s, self.qkv_buf, self.k_cache[i], self.v_cache[i],
+                                       self.inv_freq, self.position, cfg.num_heads, cfg.num_kv_heads,
+                                       norm_weight=b.input_norm.weight, eps=b.input_norm.eps)
+                _lib.attention_o_cached_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.position,
+                                            b.o_proj.packed_weights, b.o_proj.scales, x, cfg.num_heads,
+                                            cfg.num_kv_heads, cfg.head_dim, cfg.group_size)
+            elif short:
+                _lib.gemv_fused_f16(x, qkv_w, qkv_s, self.qkv_buf, norm_weight=b.input_norm.weight,
+                                    eps=b.input_norm.eps)
                 _lib.attention_o_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.inv_freq, self.position,
                                      b.o_proj.packed_weights, b.o_proj.scales, x, cfg.num_heads, cfg.num_kv_heads,
                                      cfg.head_dim, cfg.group_size)
             else:
+                _lib.gemv_fused_f16(x, qkv_w, qkv_s, self.qkv_buf, norm_weight=b.input_norm.weight,
+                                    eps=b.input_norm.eps)
                 _lib.decode_attention_f16(self.qkv_buf, self.k_cache[i], self.v_cache[i], self.cos, self.sin,
                                           self.position, self.attn_buf, cfg.num_heads, cfg.num_kv_heads,
                                           cfg.head_dim)

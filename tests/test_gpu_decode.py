@@ -289,6 +289,176 @@ def test_attention_o_rejects(gpu):
         _lib.attention_o_f16(t, cache, cache, inv, pos, w, t, t[:64], 34, 2)
 
 
+# -------------------------------- q|k|v GEMV with rotary + KV append, cached attention + o ----
+def _qkv_rope_ref(x, nw, p_, s_, pos, heads, kv):
+    """fp16 q|k|v rows (CPU oracle on the RMS-normalised row), then q / k rotated
+    at the fp32 angle pos * inv_freq in float64 and rounded to fp16."""
+    xin = _rms_norm_f16(x, nw, 1e-5) if nw is not None else x
+    rows = torch.from_numpy(_f16(_linear_ref(xin, p_, s_))).to(torch.float16)
+    ang = (torch.tensor(float(pos)) * _inv_freq()).double()
+    c, s = ang.cos(), ang.sin()
+    nq = (heads + kv) * 64
+    rot = _rope64(rows[:nq].view(heads + kv, 64), c, s).to(torch.float16).reshape(-1)
+    return torch.cat((rot, rows[nq:]))
+
+
+@pytest.mark.parametrize("heads,kv,k", [(32, 4, 2048), (8, 2, 256), (4, 1, 5632), (16, 8, 1024)])
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("pos", [0, 17, 63])
+def test_gemv_qkv_rope(gpu, heads, kv, k, norm, pos):
+    """qkv rows within 1e-2 (1 + |ref|) of the oracle + float64 rotation; cache
+    slot pos holds the rotated k / the v rows (same bar), every other slot is
+    untouched (NaN patterns included)."""
+    n = (heads + 2 * kv) * 64
+    S = 64
+    x, p_, s_ = make_case(1, k, n, seed=pos * 7 + heads + k)
+    gen = torch.Generator().manual_seed(pos + k)
+    nw = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16) if norm else None
+    ref = _qkv_rope_ref(x, nw, p_, s_, pos, heads, kv)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    k_cache[:, pos + 1:] = float("nan")
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = torch.full((n,), float("nan"), dtype=torch.float16, device=gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] qkv rope heads={heads} kv={kv} K={k} norm={norm} pos={pos}", flush=True)
+    _lib.gemv_qkv_rope_f16(x.to(gpu), p_.to(gpu), s_.to(gpu), out, kd, vd, _inv_freq().to(gpu), position, heads, kv,
+                           norm_weight=nw.to(gpu) if norm else None, eps=1e-5)
+    torch.cuda.synchronize()
+    assert_parity(out.view(1, n), ref.float().numpy().reshape(1, n), f"qkv rope heads={heads} K={k}")
+    kg, vg = kd.cpu(), vd.cpu()
+    others = [t for t in range(S) if t != pos]
+    assert torch.equal(kg[:, others].isnan(), k_cache[:, others].isnan())
+    fin = [t for t in others if t < pos]
+    assert torch.equal(kg[:, fin], k_cache[:, fin]) and torch.equal(vg[:, others], v_cache[:, others])
+    qk = out.cpu()
+    # the cache slot holds exactly what qkv holds
+    assert torch.equal(kg[:, pos], qk[heads * 64: (heads + kv) * 64].view(kv, 64))
+    assert torch.equal(vg[:, pos], qk[(heads + kv) * 64:].view(kv, 64))
+
+
+def test_gemv_qkv_rope_position_out_of_range(gpu):
+    heads, kv, k, S = 8, 2, 256, 16
+    n = (heads + 2 * kv) * 64
+    x, p_, s_ = make_case(1, k, n, seed=5)
+    for bad in (S, -1, 1 << 40):
+        kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+        vd = torch.zeros_like(kd)
+        out = torch.zeros((n,), dtype=torch.float16, device=gpu)
+        position = torch.tensor([bad], dtype=torch.int64, device=gpu)
+        print(f"[case] qkv rope out of range pos={bad}", flush=True)
+        _lib.gemv_qkv_rope_f16(x.to(gpu), p_.to(gpu), s_.to(gpu), out, kd, vd, _inv_freq().to(gpu), position,
+                               heads, kv)
+        torch.cuda.synchronize()
+        assert not kd.any() and not vd.any()
+        # the v rows are stored unrotated whatever the position
+        ref = _f16(_linear_ref(x, p_, s_))[(heads + kv) * 64:]
+        assert_parity(out[(heads + kv) * 64:].view(1, -1), ref.reshape(1, -1), "qkv rope v rows")
+
+
+def test_gemv_qkv_rope_rejects(gpu):
+    t = torch.zeros((4096,), dtype=torch.float16, device=gpu)
+    cache = torch.zeros((2, 16, 64), dtype=torch.float16, device=gpu)
+    pos = torch.zeros((1,), dtype=torch.int64, device=gpu)
+    inv = _inv_freq().to(gpu)
+    w = torch.zeros((768, 128), dtype=torch.uint8, device=gpu)
+    sc = torch.zeros((768, 2), dtype=torch.float16, device=gpu)
+    x = torch.zeros((256,), dtype=torch.float16, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="head_dim"):
+        _lib.gemv_qkv_rope_f16(x, w, sc, t, cache, cache, inv, pos, 8, 2, head_dim=128)
+    with pytest.raises(_lib.W4A16Error, match="group_size"):
+        _lib.gemv_qkv_rope_f16(x, w, sc, t, cache, cache, inv, pos, 8, 2, group_size=64)
+    with pytest.raises(_lib.W4A16Error, match="K a multiple of 128"):
+        _lib.gemv_qkv_rope_f16(x[:200], w, sc, t, cache, cache, inv, pos, 8, 2)
+    with pytest.raises(_lib.W4A16Error, match="aligned"):
+        _lib.gemv_qkv_rope_f16(x[1:129], w, sc, t, cache, cache, inv, pos, 8, 2)
+
+
+@pytest.mark.parametrize("heads,kv,hidden", [(32, 4, 2048), (8, 2, 300), (64, 8, 1000), (16, 1, 512)])
+@pytest.mark.parametrize("pos", [0, 5, 47, 63])
+def test_attention_o_cached(gpu, heads, kv, hidden, pos):
+    """Rotated q in qkv and slot pos already in the caches (slots past pos
+    NaN, which must not leak in): out = fp16(resid + fp16(o . attn)) within
+    1e-2 (1 + |ref|) of the float64 attention through the CPU oracle; the
+    caches are only read."""
+    S = 64
+    gen = torch.Generator().manual_seed(pos * 3 + hidden + heads)
+    qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    attn, k_new, v_new = _attention_ref(qkv, k_cache, v_cache, pos, heads, kv)
+    ang = (torch.tensor(float(pos)) * _inv_freq()).double()
+    q_rot = _rope64(qkv[: heads * 64].view(heads, 64), ang.cos(), ang.sin()).to(torch.float16).reshape(-1)
+    qkv_rot = torch.cat((q_rot, torch.full(((2 * kv) * 64,), float("nan"), dtype=torch.float16)))
+    k_cache[:, pos], v_cache[:, pos] = k_new, v_new
+    k_cache[:, pos + 1:] = float("nan")
+    v_cache[:, pos + 1:] = float("nan")
+    _, op, os_ = make_case(1, heads * 64, hidden, seed=hidden + 1)
+    resid = torch.randn((hidden,), generator=gen).to(torch.float16)
+    ref = _f16(resid.float().numpy() + _f16(_linear_ref(attn.to(torch.float16), op, os_)))
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = resid.to(gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] attention_o cached heads={heads} kv={kv} hidden={hidden} pos={pos}", flush=True)
+    _lib.attention_o_cached_f16(qkv_rot.to(gpu), kd, vd, position, op.to(gpu), os_.to(gpu), out, heads, kv)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert_parity(out.view(1, hidden), ref.reshape(1, hidden), f"attention_o cached heads={heads} hidden={hidden}")
+    assert torch.equal(kd.cpu().isnan(), k_cache.isnan()) and torch.equal(vd.cpu().isnan(), v_cache.isnan())
+    fin = list(range(pos + 1))
+    assert torch.equal(kd.cpu()[:, fin], k_cache[:, fin]) and torch.equal(vd.cpu()[:, fin], v_cache[:, fin])
+
+
+def test_attention_o_cached_position_out_of_range(gpu):
+    heads, kv = 8, 2
+    qkv = torch.randn(((heads + 2 * kv) * 64,)).to(torch.float16).to(gpu)
+    op, os_ = _identity_o(heads * 64)
+    op, os_ = op.to(gpu), os_.to(gpu)
+    for S, bad in ((48, 48), (48, -1), (128, 64), (128, 100)):
+        kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+        vd = torch.zeros_like(kd)
+        resid = torch.zeros((heads * 64,), dtype=torch.float16, device=gpu)
+        position = torch.tensor([bad], dtype=torch.int64, device=gpu)
+        print(f"[case] attention_o cached out of range S={S} pos={bad}", flush=True)
+        _lib.attention_o_cached_f16(qkv, kd, vd, position, op, os_, resid, heads, kv)
+        torch.cuda.synchronize()
+        assert torch.isnan(resid).all()
+        assert not kd.any() and not vd.any()
+
+
+@pytest.mark.parametrize("heads,kv,hidden", [(32, 4, 2048), (8, 2, 512)])
+@pytest.mark.parametrize("pos", [3, 63])
+def test_qkv_rope_pair_matches_attention_o(gpu, heads, kv, hidden, pos):
+    """gemv_qkv_rope + attention_o_cached against gemv_fused + attention_o (rotary
+    and append in the attention launch) on the same state: the residual rows
+    within 1e-2 (1 + |ref|), cache slot pos within one fp16 rounding."""
+    S, k = 64, hidden
+    n = (heads + 2 * kv) * 64
+    x, p_, s_ = make_case(1, k, n, seed=pos + heads)
+    _, op, os_ = make_case(1, heads * 64, hidden, seed=hidden + 7)
+    gen = torch.Generator().manual_seed(pos)
+    nw = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16).to(gpu)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    resid = torch.randn((hidden,), generator=gen).to(torch.float16)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    inv = _inv_freq().to(gpu)
+    xg, pg, sg, opg, osg = x.to(gpu), p_.to(gpu), s_.to(gpu), op.to(gpu), os_.to(gpu)
+    print(f"[case] qkv rope pair heads={heads} kv={kv} hidden={hidden} pos={pos}", flush=True)
+    k1, v1, r1 = k_cache.to(gpu), v_cache.to(gpu), resid.to(gpu)
+    qkv1 = torch.empty((n,), dtype=torch.float16, device=gpu)
+    _lib.gemv_fused_f16(xg, pg, sg, qkv1, norm_weight=nw, eps=1e-5)
+    _lib.attention_o_f16(qkv1, k1, v1, inv, position, opg, osg, r1, heads, kv)
+    k2, v2, r2 = k_cache.to(gpu), v_cache.to(gpu), resid.to(gpu)
+    qkv2 = torch.empty((n,), dtype=torch.float16, device=gpu)
+    _lib.gemv_qkv_rope_f16(xg, pg, sg, qkv2, k2, v2, inv, position, heads, kv, norm_weight=nw, eps=1e-5)
+    _lib.attention_o_cached_f16(qkv2, k2, v2, position, opg, osg, r2, heads, kv)
+    torch.cuda.synchronize()
+    assert_parity(r2.view(1, hidden), r1.float().cpu().numpy().reshape(1, hidden), "qkv rope pair")
+    assert torch.equal(v2.cpu(), v1.cpu())
+    assert torch.allclose(k2.cpu().float(), k1.cpu().float(), rtol=2 ** -10, atol=2 ** -14)
+
+
 # ------------------------------------------------------- lm_head + argmax ----
 @pytest.mark.parametrize("k,n", [(256, 1), (256, 7), (2048, 1000), (2048, 32000), (1024, 50257)])
 @pytest.mark.parametrize("norm", [False, True])
