@@ -48,6 +48,7 @@ extern "C" {
 #define W4A16_KERNEL_PAIR_STREAM 11  /* paired MFMA, resident workgroups streaming 8-row blocks (2 <= M <= 8) */
 #define W4A16_KERNEL_GEMM_LDS 12     /* GEMM with the activation block staged in LDS per round of groups (large M) */
 #define W4A16_KERNEL_PAIR_SPLIT 13   /* PAIR_STREAM over K slices, fp32 partials in a workspace + reduce (2 <= M <= 8) */
+#define W4A16_KERNEL_GEMM32 14       /* GEMM_LDS on 32x32x16 MFMA tiles (large M, rows of up to 4096 weights) */
 
 /*
  * Fused W4A16 linear layer.
@@ -220,6 +221,10 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     per wavefront (2|4), unroll = wavefronts sharing each staged round on
  *     different weight tiles (2|4), splits = wavefronts splitting K (1|2|4;
  *     4 needs unroll 2 and rows * max_blocks < 16, or rows * max_blocks < 8).
+ *   W4A16_KERNEL_GEMM32 (any M; every operand below 4 GiB): as
+ *     W4A16_KERNEL_GEMM_LDS with 32-row tiles; (rows, max_blocks, unroll,
+ *     splits) one of (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1),
+ *     (4, 1, 2, 2).
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

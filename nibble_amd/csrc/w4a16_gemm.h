@@ -424,4 +424,216 @@ gemm2_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
     }
 }
 
+// ---------------------------------------------------------------------------
+// W4A16 GEMM on 32x32 tiles (large M).
+//
+// gemm2_w4a16 on v_mfma_f32_32x32x16_f16: every decoded B fragment (8
+// weights per lane) and every A fragment read from LDS now feed an MFMA of
+// 32 x 32 x 16 instead of 16 x 16 x 32, so the decode VALU work and the LDS
+// reads per FLOP are halved. Lane layout (checked on the device): A lane l
+// holds row l % 32, k = 8 (l / 32) .. + 7 of its 32 x 16 step; B lane l holds
+// column l % 32 of the same k; D register e of lane l is row
+// 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
+//
+// Within a 128-weight group, step s (0..7) of lane half h = l / 32 takes
+// k = 64 h + 8 s .. + 7, so a lane's weights of one group are bytes 32 h ..
+// 32 h + 31 of its row's 64-byte group (two 16-byte loads, word s % 4 of
+// the first or second) and its A fragment of step s is the 16 contiguous
+// bytes at halves 64 h + 8 s of its activation row's staged group. Decode,
+// staging (rows of 136 halves), the ring of weight rounds, the XCD-aware grid
+// and the fixed-order SK reduction are those of gemm2_w4a16, with tiles of
+// 32 rows.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int64_t gemm3_lds_bytes(int mt, int rb, int sn, int sk) {
+    return (int64_t)2 * sk * 32 * mt * kGemmRow * 2 > (int64_t)(sk - 1) * sn * mt * rb * 64 * 64
+               ? (int64_t)2 * sk * 32 * mt * kGemmRow * 2
+               : (int64_t)(sk - 1) * sn * mt * rb * 64 * 64;
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int MT, int RB, int SN, int SK, bool PAIRED = false>
+__global__ void __launch_bounds__(64 * SN * SK)
+gemm3_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+            f16* __restrict__ out, int M, int N, int K, int nblocks) {
+    static_assert(!PAIRED || RB % 2 == 0, "paired tiles come in gate / up pairs");
+    constexpr int RO = PAIRED ? RB / 2 : RB;   // output tiles per wavefront
+    constexpr int T = 64 * SN * SK;
+    constexpr int DB = kGemmRing;
+    constexpr int UNITS = SK * 32 * MT * 16;   // 16-byte units staged per round
+    static_assert(UNITS % T == 0, "whole staging units per thread");
+    constexpr int UPT = UNITS / T;
+    constexpr int BUF = SK * 32 * MT * kGemmRow;   // halves per staging buffer
+    const int b = blockIdx.x;
+    const int mblocks = (int)gridDim.x / ((nblocks + 7) & ~7);
+    const int sidx = b >> 3;
+    const int nbk = 8 * (sidx / mblocks) + (b & 7);
+    const int mbk = sidx % mblocks;
+    if (nbk >= nblocks) return;   // padding workgroup: whole workgroup, before any barrier
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    f16* as = reinterpret_cast<f16*>(smem);                                   // [2][SK][32 MT][kGemmRow]
+    f32x16* red = reinterpret_cast<f32x16*>(smem);   // [SK - 1][SN][MT][RB][64], after the last round
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 31, h = lane >> 5;
+    const int sk = wave % SK, sn = wave / SK;
+    const int G = K >> 7;
+    const int R = (G + SK - 1) / SK;
+    const int RP = (R + DB - 1) / DB * DB;   // rounds run, a multiple of the ring
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+    const int n0 = nbk * 32 * RO * SN + sn * 32 * RO;
+    const int m0 = mbk * 32 * MT;
+
+    // staging: unit u = (group gl, row, 16-byte part p) of the round
+    const uint8_t* xbase = reinterpret_cast<const uint8_t*>(x);
+    auto stage_load = [&](u32x4 (&a)[UPT], int r) {
+#pragma unroll
+        for (int p = 0; p < UPT; ++p) {
+            const int u = threadIdx.x + p * T;
+            const int gl = u / (32 * MT * 16), rem = u % (32 * MT * 16);
+            const int row = rem >> 4, part = rem & 15;
+            const int g = min(r * SK + gl, G - 1);
+            const uint32_t m = (uint32_t)min(m0 + row, M - 1);
+            a[p] = *reinterpret_cast<const u32x4*>(xbase + (m * (uint32_t)K + (uint32_t)g * 128u + part * 8u) * 2u);
+        }
+    };
+    auto stage_put = [&](const u32x4 (&a)[UPT], int r, int buf) {
+#pragma unroll
+        for (int p = 0; p < UPT; ++p) {
+            const int u = threadIdx.x + p * T;
+            const int gl = u / (32 * MT * 16), rem = u % (32 * MT * 16);
+            const int row = rem >> 4, part = rem & 15;
+            const bool live = r * SK + gl < G;
+            *reinterpret_cast<u32x4*>(as + (size_t)buf * BUF + ((size_t)gl * 32 * MT + row) * kGemmRow + part * 8) =
+                live ? a[p] : (u32x4){0u, 0u, 0u, 0u};
+        }
+    };
+
+    // weights: ring slot d holds round r's group g = r SK + sk (clamped), 32
+    // bytes per lane and weight tile (two 16-byte loads)
+    const uint8_t* sbase = reinterpret_cast<const uint8_t*>(scales);
+    uint32_t wrow[RB], srow[RB];
+#pragma unroll
+    for (int t = 0; t < RB; ++t) {
+        const uint32_t n = PAIRED && t >= RO ? (uint32_t)(N + min(n0 + 32 * (t - RO) + c, N - 1))
+                                             : (uint32_t)min(n0 + 32 * t + c, N - 1);
+        wrow[t] = n * row_bytes + 32u * h;
+        srow[t] = n * (uint32_t)G * 2u;
+    }
+    u32x4 wv[DB][RB][2];
+    uint32_t sv[DB][RB];
+    auto load_w = [&](int d, int r) {
+        const uint32_t g = (uint32_t)min(r * SK + sk, G - 1);
+#pragma unroll
+        for (int t = 0; t < RB; ++t) sv[d][t] = *reinterpret_cast<const uint16_t*>(sbase + srow[t] + g * 2u);
+#pragma unroll
+        for (int t = 0; t < RB; ++t) {
+            wv[d][t][0] = *reinterpret_cast<const u32x4*>(w + wrow[t] + g * 64u);
+            wv[d][t][1] = *reinterpret_cast<const u32x4*>(w + wrow[t] + g * 64u + 16u);
+        }
+    };
+
+    f32x16 acc[MT][RB];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[t][r][e] = 0.0f;
+
+    const f16x2 mul = {(f16)1.0f, (f16)0.0625f};
+    const f16x2 off = {(f16)-1032.0f, (f16)-72.0f};
+    auto compute = [&](int d, int buf) {
+        const f16* ab = as + (size_t)buf * BUF + (size_t)sk * 32 * MT * kGemmRow;
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            u32x4 af[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                af[t] = *reinterpret_cast<const u32x4*>(ab + (32 * t + c) * kGemmRow + 64 * h + 8 * st);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const f16 sc = __builtin_bit_cast(f16, (uint16_t)sv[d][r]);
+                const f16x2 sc2 = {sc, sc};
+                const uint32_t word = wv[d][r][st >> 2][st & 3];
+                f16x2 pr[4];
+#pragma unroll
+                for (int by = 0; by < 4; ++by) {
+                    const uint32_t sel = (0x0Cu << 24) | ((uint32_t)by << 16) | (0x0Cu << 8) | (uint32_t)by;
+                    const uint32_t v = __builtin_amdgcn_bitop3_b32(perm(word, word, sel), 0x00F0000Fu, 0x64806408u,
+                                                                   0x6A);
+                    pr[by] = __builtin_elementwise_fma(as_f16x2(v), mul, off) * sc2;
+                }
+                const f16x8 bt = __builtin_bit_cast(
+                    f16x8, (u32x4){as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])});
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    acc[t][r] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, af[t]), bt,
+                                                                       acc[t][r], 0, 0, 0);
+            }
+        }
+    };
+
+    // prologue: round 0 staged, round 1 requested, the ring's first DB rounds
+    // of weights requested. Staging runs two rounds ahead: round r's loop
+    // requests round r + 2 into the register set round r came from and puts
+    // round r + 1 (requested a round earlier) into LDS, so a staging load has
+    // two rounds of MFMAs to arrive.
+    u32x4 a[2][UPT];
+    stage_load(a[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) load_w(d, d);
+    stage_load(a[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    stage_put(a[0], 0, 0);
+    __syncthreads();
+    static_assert(DB % 2 == 0, "the staging register sets alternate within the weight ring");
+    for (int r0 = 0; r0 < RP; r0 += DB) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+            const int r = r0 + d;
+            stage_load(a[d & 1], r + 2);   // past the last round: clamped, staged as zeros, never read
+            compute(d, r & 1);
+            load_w(d, r + DB);
+            stage_put(a[(d + 1) & 1], r + 1, (r + 1) & 1);
+            __syncthreads();
+        }
+    }
+
+    // SK partial tiles: wavefronts sk > 0 write, sk = 0 sums in order
+    if (SK > 1) {
+        if (sk > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int r = 0; r < RB; ++r)
+                    red[((((sk - 1) * SN + sn) * MT + t) * RB + r) * 64 + lane] = acc[t][r];
+        }
+        __syncthreads();
+        if (sk > 0) return;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int k2 = 1; k2 < SK; ++k2) acc[t][r] += red[((((k2 - 1) * SN + sn) * MT + t) * RB + r) * 64 + lane];
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+#pragma unroll
+        for (int r = 0; r < RO; ++r) {
+            const int n = n0 + 32 * r + c;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (m < M && n < N)
+                    out[(size_t)m * N + n] = PAIRED ? gemm_silu_mul(acc[t][r][e], acc[t][r + RO][e])
+                                                    : (f16)acc[t][r][e];
+            }
+        }
+    }
+}
+
 }  // namespace w4a16

@@ -222,6 +222,61 @@ int launch_gemm2_silu(int mt, int rb, int sn, int sk, int M, const void* x, cons
     return W4A16_OK;
 }
 
+// GEMM on 32x32 tiles (gemm3_w4a16): mt activation tiles and rb weight
+// tiles of 32 rows per wavefront, sn wavefronts on weight tiles sharing each
+// staged round, sk wavefronts splitting K. Instantiated (M = 256 sweep of
+// 4096 x 14336, 2048 x 11264 / 5632, 14336 x 4096 and M = 128 4096 x 14336):
+// (mt, rb, sn, sk) = (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1)
+// and (4, 1, 2, 2); the SiLU-multiply form (rb / 2 gate tiles and their up
+// tiles) as (2, 2, 4, 1) and (2, 2, 2, 2).
+namespace {
+Kern pick3(int mt, int rb, int sn, int sk, bool paired) {
+    using namespace w4a16;
+    if (paired) {
+        if (mt == 2 && rb == 2 && sn == 4 && sk == 1) return gemm3_w4a16<2, 2, 4, 1, true>;
+        if (mt == 2 && rb == 2 && sn == 2 && sk == 2) return gemm3_w4a16<2, 2, 2, 2, true>;
+        return nullptr;
+    }
+    if (mt == 4 && rb == 1 && sn == 4 && sk == 1) return gemm3_w4a16<4, 1, 4, 1>;
+    if (mt == 2 && rb == 1 && sn == 4 && sk == 2) return gemm3_w4a16<2, 1, 4, 2>;
+    if (mt == 2 && rb == 2 && sn == 2 && sk == 2) return gemm3_w4a16<2, 2, 2, 2>;
+    if (mt == 2 && rb == 2 && sn == 4 && sk == 1) return gemm3_w4a16<2, 2, 4, 1>;
+    if (mt == 4 && rb == 1 && sn == 2 && sk == 2) return gemm3_w4a16<4, 1, 2, 2>;
+    return nullptr;
+}
+}  // namespace
+
+bool gemm3_instantiated(int mt, int rb, int sn, int sk, bool paired) { return pick3(mt, rb, sn, sk, paired) != nullptr; }
+
+// paired: the SiLU-multiply epilogue over a [gate; up] pair, N = inter output
+// columns and 2 inter weight rows.
+int launch_gemm3(int mt, int rb, int sn, int sk, bool paired, int M, const void* x, const uint8_t* w, const void* s,
+                 void* o, int N, int K, hipStream_t stream) {
+    if (M < 1 || N < 1 || !gemm_fits(M, paired ? 2 * (int64_t)N : N, K))
+        return fail(W4A16_ERR_CONFIG, "32x32 GEMM kernel: K must be a positive multiple of 128 and every operand below 4 GiB");
+    const Kern kern = pick3(mt, rb, sn, sk, paired);
+    if (kern == nullptr)
+        return fail(W4A16_ERR_CONFIG, paired ? "paired 32x32 GEMM kernel: (rows, max_blocks, unroll, splits) must be "
+                                               "(2, 2, 4, 1) or (2, 2, 2, 2)"
+                                             : "32x32 GEMM kernel: (rows, max_blocks, unroll, splits) must be (4, 1, 4, "
+                                               "1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1) or (4, 1, 2, 2)");
+    const int64_t lds = w4a16::gemm3_lds_bytes(mt, rb, sn, sk);
+    if (lds > 160 * 1024) return fail(W4A16_ERR_CONFIG, "32x32 GEMM kernel: staging exceeds LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int cols = (paired ? 16 : 32) * rb * sn;   // output columns per workgroup
+    const int nblocks = (N + cols - 1) / cols;
+    const int mblocks = (M + 32 * mt - 1) / (32 * mt);
+    const int64_t grid = (int64_t)((nblocks + 7) & ~7) * mblocks;
+    if (grid > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "32x32 GEMM kernel: too many workgroups");
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * sn * sk), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, N, K, nblocks);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
 int launch_gemm_silu(int mt, int rb, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int inter,
                      int K, hipStream_t stream) {
     if (M < 1 || inter < 1 || !gemm_fits(M, 2 * (int64_t)inter, K))

@@ -54,6 +54,9 @@ int launch_gemm2_silu(int mt, int rb, int sn, int sk, int M, const void* x, cons
                       int inter, int K, hipStream_t stream);
 int launch_gemm2(int mt, int rb, int sn, int sk, int M, const void* x, const uint8_t* w, const void* s, void* o, int N,
                  int K, hipStream_t stream);
+bool gemm3_instantiated(int mt, int rb, int sn, int sk, bool paired);
+int launch_gemm3(int mt, int rb, int sn, int sk, bool paired, int M, const void* x, const uint8_t* w, const void* s,
+                 void* o, int N, int K, hipStream_t stream);
 }  // namespace w4a16_internal
 
 namespace {
@@ -382,21 +385,49 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
 // staging, splits = SK. Shape: 4 activation tiles, 2 weight tiles; 4
 // wavefronts on weight tiles with no K split from N = 11264, else 2 with K
 // split 4 ways from K = 5632 (2 below).
+//
+// The same staging on 32x32x16 MFMAs (gemm3_w4a16, W4A16_KERNEL_GEMM32) takes
+// rows of up to 4096 weights when its grid fills the chip (M = 256:
+// 4096 x 14336 48.0 against 56.9 us for the staged 16x16 kernel in the same
+// sweep, 2048 x 11264 26.4 against 31.6, 2048 x 5632 17.1 against 22.0; M =
+// 128 4096 x 14336 31.0 against 40.4): 4 activation tiles of 32 rows and 4
+// wavefronts on 32-row weight tiles when that makes >= 160 workgroups, else
+// 2 tiles with 4 wavefronts on weight tiles and K split 2 ways when that
+// makes >= 128; narrower grids (2048 x 2048 at M = 128: 17.2 against 14.3)
+// and longer rows (14336 x 4096, 5632 x 2048) keep the 16x16 kernels.
 Plan plan_gemm_lds(int64_t M, int64_t N, int64_t K) {
     Plan p;
+    const int64_t nb = (N + 127) / 128;
+    if (K <= 4096 && nb * ((M + 127) / 128) >= 160) {
+        p.kernel = W4A16_KERNEL_GEMM32;
+        p.rows = 4;
+        p.max_blocks = 1;
+        p.unroll = 4;
+        p.splits = 1;
+        return p;
+    }
+    if (K <= 4096 && nb * ((M + 63) / 64) >= 128) {
+        p.kernel = W4A16_KERNEL_GEMM32;
+        p.rows = 2;
+        p.max_blocks = 1;
+        p.unroll = 4;
+        p.splits = 2;
+        return p;
+    }
     p.kernel = W4A16_KERNEL_GEMM_LDS;
     p.rows = 4;
     p.max_blocks = 2;
     p.unroll = N >= 11264 ? 4 : 2;
     p.splits = N >= 11264 ? 1 : (K >= 5632 ? 4 : 2);
-    (void)M;
     return p;
 }
 
 bool gemm_lds_route(int64_t M, int64_t N, int64_t K) {
     const Plan p = plan_gemm_lds(M, N, K);
     return M >= 128 && (K <= 4096 || N >= 4096) && w4a16_internal::gemm_fits(M, N, K) &&
-           w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits);
+           (p.kernel == W4A16_KERNEL_GEMM32
+                ? w4a16_internal::gemm3_instantiated(p.rows, p.max_blocks, p.unroll, p.splits, false)
+                : w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits));
 }
 
 // Largest M the dispatcher sends to the GEMM kernel.
@@ -953,6 +984,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_GEMM_LDS:
             return w4a16_internal::launch_gemm2(p.rows, p.max_blocks, p.unroll, p.splits, (int)M, x, packed, s, o, (int)N,
                                                 (int)K, st);
+        case W4A16_KERNEL_GEMM32:
+            return w4a16_internal::launch_gemm3(p.rows, p.max_blocks, p.unroll, p.splits, false, (int)M, x, packed, s, o,
+                                                (int)N, (int)K, st);
         case W4A16_KERNEL_GENERIC: return launch_generic((int)M, x, packed, s, o, (int)N, (int)K, (int)G, st);
         default: return fail(W4A16_ERR_CONFIG, "unknown kernel family");
     }
@@ -1128,7 +1162,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     p.splits = splits;
     p.unroll = unroll;
     p.max_blocks = max_blocks;
-    if (kernel == W4A16_KERNEL_GEMM || kernel == W4A16_KERNEL_GEMM_LDS) {
+    if (kernel == W4A16_KERNEL_GEMM || kernel == W4A16_KERNEL_GEMM_LDS || kernel == W4A16_KERNEL_GEMM32) {
         if (group_size != 128 || M > INT32_MAX || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
                         "the GEMM kernel needs group_size 128 and 16-byte aligned activations and weights");
@@ -1164,7 +1198,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_PAIR_STREAM, _PAIR_SPLIT, _STREAM, _GEMM, _GEMM_LDS, _DIAG or _GENERIC");
+                    "_PAIR_STREAM, _PAIR_SPLIT, _STREAM, _GEMM, _GEMM_LDS, _GEMM32, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false, workspace,
                     workspace_bytes);
@@ -1277,6 +1311,12 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
         return fail(W4A16_ERR_TOO_LARGE, "linear + SiLU: every operand must be below 4 GiB");
     // the GEMM the op would run over the 2 inter rows, with an even number of weight tiles per wavefront
     if (gemm_lds_route(M, 2 * inter, K)) {
+        // the 32x32 kernel's SiLU form: rb = 2 (a gate tile and its up tile),
+        // 4 wavefronts on weight tiles, when its grid fills the chip
+        const int64_t wg = (inter + 127) / 128 * ((M + 63) / 64);
+        if (K <= 4096 && wg >= 128)
+            return w4a16_internal::launch_gemm3(2, 2, 4, 1, true, (int)M, activations, packed_weights, scales, output,
+                                                (int)inter, (int)K, st);
         const Plan q = plan_gemm_lds(M, 2 * inter, K);
         if (w4a16_internal::gemm2_silu_instantiated(q.rows, q.max_blocks, q.unroll, q.splits))
             return w4a16_internal::launch_gemm2_silu(q.rows, q.max_blocks, q.unroll, q.splits, (int)M, activations,

@@ -207,15 +207,20 @@ def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
 
 
 @pytest.mark.parametrize("m,n,k,kernel,shape", [
-    (256, 14336, 4096, "gemm_lds", (4, 2, 4, 1)), (256, 11264, 2048, "gemm_lds", (4, 2, 4, 1)),
-    (256, 5632, 2048, "gemm_lds", (4, 2, 2, 2)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
+    (256, 14336, 4096, "gemm32", (4, 1, 4, 1)), (256, 11264, 2048, "gemm32", (4, 1, 4, 1)),
+    (256, 5632, 2048, "gemm32", (2, 1, 4, 2)), (128, 14336, 4096, "gemm32", (2, 1, 4, 2)),
+    (128, 2048, 2048, "gemm_lds", (4, 2, 2, 2)),   # grid too small for the 32x32 tiles
+    (256, 4096, 14336, "gemm_lds", (4, 2, 2, 4)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
     (256, 2048, 5632, "gemm", None),   # long rows of a narrow layer: the per-round barriers lose
     (64, 11264, 2048, "gemm", None), (127, 14336, 4096, "gemm", None),
 ])
 def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
-    """M >= 128 with K <= 4096 or N >= 4096: the LDS-staged GEMM, 4 activation
-    and 2 weight tiles per wavefront; (rows, max_blocks, unroll = wavefronts
-    sharing the staging, splits)."""
+    """M >= 128 with K <= 4096 or N >= 4096: the LDS-staged GEMM; on 32x32
+    tiles (4 activation tiles and 4 wavefronts on single weight tiles from
+    160 workgroups, else 2 activation tiles with K split 2 ways from 128) for
+    rows of up to 4096 weights, else on 16x16 tiles with 4 activation and 2
+    weight tiles per wavefront; (rows, max_blocks, unroll = wavefronts sharing
+    the staging, splits)."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
     assert plan["kernel"] == kernel

@@ -23,6 +23,7 @@ STREAM = _lib.KERNEL_STREAM
 GEMM = _lib.KERNEL_GEMM
 PAIR_STREAM = _lib.KERNEL_PAIR_STREAM
 GEMM_LDS = _lib.KERNEL_GEMM_LDS
+GEMM32 = _lib.KERNEL_GEMM32
 PAIR_SPLIT = _lib.KERNEL_PAIR_SPLIT
 
 
@@ -406,9 +407,31 @@ def test_gemm_lds_variants(gpu, rows, blocks, sn, splits, m, k, n):
     assert_parity(got, expected(x, p, s), f"gemm_lds {rows}/{blocks}/{sn}/{splits} M={m} K={k} N={n}")
 
 
+GEMM32_SHAPES = [(4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2)]
+
+
+@pytest.mark.parametrize("rows,blocks,sn,splits", GEMM32_SHAPES)
+@pytest.mark.parametrize("m,k,n", [(17, 2048, 200), (64, 384, 33), (100, 5632, 48), (3, 1152, 100), (70, 128, 300),
+                                   (300, 4096, 700)])
+def test_gemm32_variants(gpu, rows, blocks, sn, splits, m, k, n):
+    """The 32x32-tile GEMM's tilings on ragged M and N, K of 1..44 groups
+    (rounds past the last group staged as zeros; staging two rounds ahead
+    runs past the end on clamped, never-read rounds)."""
+    x, p, s = make_case(m, k, n, seed=m * 7 + k + n + rows + sn)
+    got = _run_tuned(gpu, x, p, s, GEMM32, rows, splits, sn, max_blocks=blocks)
+    assert_parity(got, expected(x, p, s), f"gemm32 {rows}/{blocks}/{sn}/{splits} M={m} K={k} N={n}")
+
+
+def test_gemm32_rejects(gpu):
+    x, p, s = make_case(64, 256, 64, seed=1)
+    with pytest.raises(_lib.W4A16Error, match="32x32 GEMM kernel"):
+        _run_tuned(gpu, x, p, s, GEMM32, 4, 1, 4, max_blocks=2)
+
+
 @pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm"), (130, 5632, 2048, "gemm"),
                                           (512, 2048, 256, "gemm_lds"), (33, 8192, 1000, "gemm"),
-                                          (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm_lds")])
+                                          (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm32"),
+                                          (256, 2048, 5632, "gemm32"), (128, 1024, 20480, "gemm32")])
 def test_default_dispatch_gemm(gpu, m, k, n, kernel):
     x, p, s = make_case(m, k, n, seed=m + k + 3 * n)
     assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == kernel
@@ -425,11 +448,11 @@ def test_gemm_uses_dequantized_weights(gpu, m, k, n):
     xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
     wdq = torch.empty((n, k), dtype=torch.float16, device=gpu)
     _lib.dequantize_f16(pd, sd, wdq, 128)
-    out = _run_tuned(gpu, x, p, s, GEMM, 4, 2, 0, max_blocks=2)
     ref = (xd.double() @ wdq.double().t()).cpu()
-    got = out.double().cpu()
     ulp = torch.finfo(torch.float16).eps / 2
-    assert torch.all((got - ref).abs() <= ulp * ref.abs() + 1e-4), float((got - ref).abs().max())
+    for kernel, rows, splits, unroll, blocks in ((GEMM, 4, 2, 0, 2), (GEMM_LDS, 4, 2, 2, 2), (GEMM32, 2, 2, 4, 1)):
+        got = _run_tuned(gpu, x, p, s, kernel, rows, splits, unroll, max_blocks=blocks).double().cpu()
+        assert torch.all((got - ref).abs() <= ulp * ref.abs() + 1e-4), (kernel, float((got - ref).abs().max()))
 
 
 def test_gemm_rejects(gpu):

@@ -128,7 +128,10 @@ def test_linear_silu(gpu, m, k, inter):
     else:
         # the same GEMM over the 2 inter rows (the op's shape), then SiLU * up
         plan = _lib.plan_linear(1 << 20, 1 << 20, m, 2 * inter, k, 128)
-        if plan["kernel"] == "gemm_lds":
+        if plan["kernel"] in ("gemm_lds", "gemm32") and k <= 4096 and -(-inter // 128) * -(-m // 64) >= 128:
+            # the SiLU form of the 32x32 kernel: 2 activation tiles, a gate and an up tile, 4 wavefronts, no K split
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM32, 2, 1, 4, 2)
+        elif plan["kernel"] == "gemm_lds":
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM_LDS, 4, plan["splits"], plan["unroll"], 2)
         elif plan["kernel"] == "gemm":
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM, plan["rows"], plan["splits"], 0, 2)
