@@ -452,7 +452,7 @@ __host__ __device__ constexpr int64_t gemm3_lds_bytes(int mt, int rb, int sn, in
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int MT, int RB, int SN, int SK, bool PAIRED = false>
+template <int MT, int RB, int SN, int SK, bool PAIRED = false, int LA = 2>
 __global__ void __launch_bounds__(64 * SN * SK)
 gemm3_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
             f16* __restrict__ out, int M, int N, int K, int nblocks) {
@@ -580,12 +580,15 @@ gemm3_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
     // requests round r + 2 into the register set round r came from and puts
     // round r + 1 (requested a round earlier) into LDS, so a staging load has
     // two rounds of MFMAs to arrive.
-    u32x4 a[2][UPT];
+    // (LA = 1: round r requests round r + 1 and puts it after its MFMAs, for
+    // shapes whose registers only hold one staging set.)
+    static_assert(LA == 1 || LA == 2, "staging runs one or two rounds ahead");
+    u32x4 a[LA][UPT];
     stage_load(a[0], 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < DB; ++d) load_w(d, d);
-    stage_load(a[1], 1);
+    if constexpr (LA == 2) stage_load(a[LA - 1], 1);
     __builtin_amdgcn_sched_barrier(0);
     stage_put(a[0], 0, 0);
     __syncthreads();
@@ -594,10 +597,12 @@ gemm3_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
 #pragma unroll
         for (int d = 0; d < DB; ++d) {
             const int r = r0 + d;
-            stage_load(a[d & 1], r + 2);   // past the last round: clamped, staged as zeros, never read
+            // past the last round: clamped, staged as zeros, never read
+            if constexpr (LA == 2) stage_load(a[d & 1], r + 2);
+            else stage_load(a[0], r + 1);
             compute(d, r & 1);
             load_w(d, r + DB);
-            stage_put(a[(d + 1) & 1], r + 1, (r + 1) & 1);
+            stage_put(a[LA == 2 ? (d + 1) & 1 : 0], r + 1, (r + 1) & 1);
             __syncthreads();
         }
     }

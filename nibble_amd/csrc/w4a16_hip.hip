@@ -376,58 +376,84 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
-// LDS-staged GEMM (w4a16_gemm.h, gemm2_w4a16) for M >= 128 where its shared
-// staging pays: measured at M = 256 against gemm_w4a16, 4096 x 14336 51.0
-// against 90.2 us, 2048 x 11264 28.7 against 38.2, 2048 x 5632 19.8 against
-// 25.6, 14336 x 4096 68.5 against 78.5; at M = 64 it loses on long rows (5632
-// x 2048: 20.4 against 10.3, its per-round barriers) and on narrow layers.
-// Plan fields: rows = MT, max_blocks = RB, unroll = SN wavefronts sharing the
-// staging, splits = SK. Shape: 4 activation tiles, 2 weight tiles; 4
-// wavefronts on weight tiles with no K split from N = 11264, else 2 with K
-// split 4 ways from K = 5632 (2 below).
-//
-// The same staging on 32x32x16 MFMAs (gemm3_w4a16, W4A16_KERNEL_GEMM32) takes
-// rows of up to 4096 weights when its grid fills the chip (M = 256:
-// 4096 x 14336 48.0 against 56.9 us for the staged 16x16 kernel in the same
-// sweep, 2048 x 11264 26.4 against 31.6, 2048 x 5632 17.1 against 22.0; M =
-// 128 4096 x 14336 31.0 against 40.4): 4 activation tiles of 32 rows and 4
-// wavefronts on 32-row weight tiles when that makes >= 160 workgroups, else
-// 2 tiles with 4 wavefronts on weight tiles and K split 2 ways when that
-// makes >= 128; narrower grids (2048 x 2048 at M = 128: 17.2 against 14.3)
-// and longer rows (14336 x 4096, 5632 x 2048) keep the 16x16 kernels.
+// LDS-staged GEMM (w4a16_gemm.h, gemm2_w4a16) for M >= 128 on rows longer
+// than 4096 weights with N >= 4096 (M = 256, 14336 x 4096: 68.5 against
+// 78.5 us for gemm_w4a16; shorter rows take the 32x32 kernel below or
+// gemm_w4a16). Plan fields: rows = MT, max_blocks = RB, unroll = SN
+// wavefronts sharing the staging, splits = SK. Shape: 4 activation tiles, 2
+// weight tiles; 4 wavefronts on weight tiles with no K split from N =
+// 11264, else 2 with K split 4 ways from K = 5632 (2 below).
 Plan plan_gemm_lds(int64_t M, int64_t N, int64_t K) {
     Plan p;
-    const int64_t nb = (N + 127) / 128;
-    if (K <= 4096 && nb * ((M + 127) / 128) >= 160) {
-        p.kernel = W4A16_KERNEL_GEMM32;
-        p.rows = 4;
-        p.max_blocks = 1;
-        p.unroll = 4;
-        p.splits = 1;
-        return p;
-    }
-    if (K <= 4096 && nb * ((M + 63) / 64) >= 128) {
-        p.kernel = W4A16_KERNEL_GEMM32;
-        p.rows = 2;
-        p.max_blocks = 1;
-        p.unroll = 4;
-        p.splits = 2;
-        return p;
-    }
     p.kernel = W4A16_KERNEL_GEMM_LDS;
     p.rows = 4;
     p.max_blocks = 2;
     p.unroll = N >= 11264 ? 4 : 2;
     p.splits = N >= 11264 ? 1 : (K >= 5632 ? 4 : 2);
+    (void)M;
     return p;
 }
 
 bool gemm_lds_route(int64_t M, int64_t N, int64_t K) {
     const Plan p = plan_gemm_lds(M, N, K);
-    return M >= 128 && (K <= 4096 || N >= 4096) && w4a16_internal::gemm_fits(M, N, K) &&
-           (p.kernel == W4A16_KERNEL_GEMM32
-                ? w4a16_internal::gemm3_instantiated(p.rows, p.max_blocks, p.unroll, p.splits, false)
-                : w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits));
+    return M >= 128 && K > 4096 && N >= 4096 && w4a16_internal::gemm_fits(M, N, K) &&
+           w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits);
+}
+
+// The staged GEMM on 32x32x16 MFMAs (gemm3_w4a16, W4A16_KERNEL_GEMM32) for M
+// >= 64 on rows of up to 4096 weights: the first of (MT, RB, SN, SK) =
+// (4, 1, 4, 1), (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) -- 128 x 128, 64 x
+// 128, 64 x 64, 64 x 32 output tiles -- that makes at least 160 workgroups.
+// On the sweep of M = 64, 128, 256 over N x K = 2560 / 2048 / 11264 / 5632 x
+// 2048 and 14336 / 4096 / 6144 x 4096 this picks the fastest of the 16x16
+// kernels and the four shapes in every case, or one within 4% (M = 256:
+// 4096 x 14336 44.6 against 51.9 us for the staged 16x16 kernel, 2048 x 11264
+// 23.8 against 29.5, 2048 x 5632 15.9 against 20.5; M = 64 4096 x 14336 21.5
+// against 27.4 for gemm_w4a16); where no shape reaches 160 workgroups
+// (2048 x 2048 at M <= 128) gemm_w4a16 wins and keeps the layer.
+bool plan_gemm32(int64_t M, int64_t N, int64_t K, Plan* out) {
+    static const int kShapes[4][4] = {{4, 1, 4, 1}, {2, 1, 4, 2}, {2, 1, 2, 4}, {2, 1, 1, 4}};
+    if (M < 64 || K > 4096 || !w4a16_internal::gemm_fits(M, N, K)) return false;
+    for (const auto& sh : kShapes) {
+        const int64_t cols = 32 * sh[1] * sh[2];
+        const int64_t wgs = ((N + cols - 1) / cols) * ((M + 32 * sh[0] - 1) / (32 * sh[0]));
+        if (wgs >= 160) {
+            Plan p;
+            p.kernel = W4A16_KERNEL_GEMM32;
+            p.rows = sh[0];
+            p.max_blocks = sh[1];
+            p.unroll = sh[2];
+            p.splits = sh[3];
+            *out = p;
+            return true;
+        }
+    }
+    return false;
+}
+
+// The SiLU-multiply form of the 32x32 kernel over a [gate; up] pair (a gate
+// tile and its up tile per wavefront): the first of (MT, RB, SN, SK) =
+// (2, 2, 4, 1), (2, 2, 2, 2), (2, 2, 1, 4) -- 128, 64, 32 output columns of
+// 64 rows -- that makes at least 160 workgroups (the paired analogues of the
+// plain shapes above, 2 weight tiles per wavefront instead of 1).
+bool plan_gemm32_silu(int64_t M, int64_t inter, int64_t K, Plan* out) {
+    static const int kShapes[3][4] = {{2, 2, 4, 1}, {2, 2, 2, 2}, {2, 2, 1, 4}};
+    if (M < 64 || K > 4096 || !w4a16_internal::gemm_fits(M, 2 * inter, K)) return false;
+    for (const auto& sh : kShapes) {
+        const int64_t cols = 16 * sh[1] * sh[2];
+        const int64_t wgs = ((inter + cols - 1) / cols) * ((M + 32 * sh[0] - 1) / (32 * sh[0]));
+        if (wgs >= 160) {
+            Plan p;
+            p.kernel = W4A16_KERNEL_GEMM32;
+            p.rows = sh[0];
+            p.max_blocks = sh[1];
+            p.unroll = sh[2];
+            p.splits = sh[3];
+            *out = p;
+            return true;
+        }
+    }
+    return false;
 }
 
 // Largest M the dispatcher sends to the GEMM kernel.
@@ -603,9 +629,11 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
-    // M > 8 (a prompt): the W4A16 GEMM, its LDS-staged form for M >= 128
+    // M > 8 (a prompt): the W4A16 GEMM; from M = 64 on rows of up to 4096
+    // weights its staged 32x32 form, and the staged 16x16 form on longer rows
+    // of wide layers from M = 128
     if (aligned && M > 8 && gemm_fits(M, N, K)) {
-        *out = gemm_lds_route(M, N, K) ? plan_gemm_lds(M, N, K) : plan_gemm(M, N, K);
+        if (!plan_gemm32(M, N, K, out)) *out = gemm_lds_route(M, N, K) ? plan_gemm_lds(M, N, K) : plan_gemm(M, N, K);
         return W4A16_OK;
     }
     const bool tuned = aligned && M <= 8;
@@ -1310,13 +1338,12 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
     if (!w4a16_internal::gemm_fits(M, 2 * inter, K))
         return fail(W4A16_ERR_TOO_LARGE, "linear + SiLU: every operand must be below 4 GiB");
     // the GEMM the op would run over the 2 inter rows, with an even number of weight tiles per wavefront
+    Plan q3;
+    if (plan_gemm32_silu(M, inter, K, &q3) &&
+        w4a16_internal::gemm3_instantiated(q3.rows, q3.max_blocks, q3.unroll, q3.splits, true))
+        return w4a16_internal::launch_gemm3(q3.rows, q3.max_blocks, q3.unroll, q3.splits, true, (int)M, activations,
+                                            packed_weights, scales, output, (int)inter, (int)K, st);
     if (gemm_lds_route(M, 2 * inter, K)) {
-        // the 32x32 kernel's SiLU form: rb = 2 (a gate tile and its up tile),
-        // 4 wavefronts on weight tiles, when its grid fills the chip
-        const int64_t wg = (inter + 127) / 128 * ((M + 63) / 64);
-        if (K <= 4096 && wg >= 128)
-            return w4a16_internal::launch_gemm3(2, 2, 4, 1, true, (int)M, activations, packed_weights, scales, output,
-                                                (int)inter, (int)K, st);
         const Plan q = plan_gemm_lds(M, 2 * inter, K);
         if (w4a16_internal::gemm2_silu_instantiated(q.rows, q.max_blocks, q.unroll, q.splits))
             return w4a16_internal::launch_gemm2_silu(q.rows, q.max_blocks, q.unroll, q.splits, (int)M, activations,

@@ -172,8 +172,8 @@ def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
 @pytest.mark.parametrize("m,n,k,rows,blocks,splits", [
     # best shapes of the M = 32..256 sweep on the 1.1B / 8B layers
     (32, 2560, 2048, 1, 2, 4), (32, 2048, 2048, 1, 1, 4), (32, 11264, 2048, 2, 4, 2), (32, 14336, 4096, 2, 4, 2),
-    (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (64, 11264, 2048, 4, 4, 2), (64, 4096, 14336, 2, 2, 4),
-    (100, 2560, 2048, 2, 4, 2), (256, 2048, 5632, 2, 4, 2),   # M >= 128 mostly takes the LDS-staged GEMM
+    (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (48, 11264, 2048, 2, 4, 2), (64, 4096, 14336, 2, 2, 4),
+    (100, 2048, 5632, 2, 2, 4), (256, 2048, 5632, 2, 4, 2),   # from M = 64 short rows mostly take the 32x32 GEMM
     (17, 64, 256, 1, 1, 2),     # few workgroups whatever the shape: the most; short rows: 2 wavefronts
 ])
 def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
@@ -209,18 +209,21 @@ def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
 @pytest.mark.parametrize("m,n,k,kernel,shape", [
     (256, 14336, 4096, "gemm32", (4, 1, 4, 1)), (256, 11264, 2048, "gemm32", (4, 1, 4, 1)),
     (256, 5632, 2048, "gemm32", (2, 1, 4, 2)), (128, 14336, 4096, "gemm32", (2, 1, 4, 2)),
-    (128, 2048, 2048, "gemm_lds", (4, 2, 2, 2)),   # grid too small for the 32x32 tiles
+    (127, 14336, 4096, "gemm32", (2, 1, 4, 2)), (64, 11264, 2048, "gemm32", (2, 1, 2, 4)),
+    (256, 2560, 2048, "gemm32", (2, 1, 2, 4)), (64, 5632, 2048, "gemm32", (2, 1, 1, 4)),
+    (256, 2048, 2048, "gemm32", (2, 1, 1, 4)), (1024, 2048, 2048, "gemm32", (2, 1, 4, 2)),
+    (128, 2048, 2048, "gemm", None),   # no 32x32 shape reaches 160 workgroups
+    (64, 4096, 4096, "gemm", None), (32, 11264, 2048, "gemm", None), (63, 14336, 4096, "gemm", None),
     (256, 4096, 14336, "gemm_lds", (4, 2, 2, 4)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
     (256, 2048, 5632, "gemm", None),   # long rows of a narrow layer: the per-round barriers lose
-    (64, 11264, 2048, "gemm", None), (127, 14336, 4096, "gemm", None),
 ])
 def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
-    """M >= 128 with K <= 4096 or N >= 4096: the LDS-staged GEMM; on 32x32
-    tiles (4 activation tiles and 4 wavefronts on single weight tiles from
-    160 workgroups, else 2 activation tiles with K split 2 ways from 128) for
-    rows of up to 4096 weights, else on 16x16 tiles with 4 activation and 2
-    weight tiles per wavefront; (rows, max_blocks, unroll = wavefronts sharing
-    the staging, splits)."""
+    """M >= 64 on rows of up to 4096 weights: the 32x32 staged GEMM, the first
+    of (rows, max_blocks, unroll = wavefronts sharing the staging, splits) =
+    (4, 1, 4, 1), (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) with >= 160
+    workgroups; M >= 128 on longer rows of layers with N >= 4096: the 16x16
+    staged GEMM, 4 activation and 2 weight tiles per wavefront; else
+    gemm_w4a16."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
     assert plan["kernel"] == kernel

@@ -428,10 +428,11 @@ def test_gemm32_rejects(gpu):
         _run_tuned(gpu, x, p, s, GEMM32, 4, 1, 4, max_blocks=2)
 
 
-@pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm"), (130, 5632, 2048, "gemm"),
-                                          (512, 2048, 256, "gemm_lds"), (33, 8192, 1000, "gemm"),
+@pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm32"), (130, 5632, 2048, "gemm"),
+                                          (512, 2048, 256, "gemm"), (33, 8192, 1000, "gemm"),
                                           (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm32"),
-                                          (256, 2048, 5632, "gemm32"), (128, 1024, 20480, "gemm32")])
+                                          (256, 2048, 5632, "gemm32"), (128, 1024, 20480, "gemm32"),
+                                          (100, 2048, 6000, "gemm32"), (64, 2048, 2048, "gemm")])
 def test_default_dispatch_gemm(gpu, m, k, n, kernel):
     x, p, s = make_case(m, k, n, seed=m + k + 3 * n)
     assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == kernel

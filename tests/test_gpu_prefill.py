@@ -128,9 +128,14 @@ def test_linear_silu(gpu, m, k, inter):
     else:
         # the same GEMM over the 2 inter rows (the op's shape), then SiLU * up
         plan = _lib.plan_linear(1 << 20, 1 << 20, m, 2 * inter, k, 128)
-        if plan["kernel"] in ("gemm_lds", "gemm32") and k <= 4096 and -(-inter // 128) * -(-m // 64) >= 128:
-            # the SiLU form of the 32x32 kernel: 2 activation tiles, a gate and an up tile, 4 wavefronts, no K split
-            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM32, 2, 1, 4, 2)
+        # the SiLU form of the 32x32 kernel: the first of 128, 64, 32 output
+        # columns per workgroup (K split 1, 2, 4 ways) with >= 160 workgroups;
+        # the plain 32x32 GEMM with the same K split sums in the same order
+        silu32 = [sk for cols, sk in ((128, 1), (64, 2), (32, 4))
+                  if m >= 64 and k <= 4096 and -(-inter // cols) * -(-m // 64) >= 160]
+        if silu32:
+            rows, unroll = {1: (4, 4), 2: (2, 4), 4: (2, 2)}[silu32[0]]
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM32, rows, silu32[0], unroll, 1)
         elif plan["kernel"] == "gemm_lds":
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM_LDS, 4, plan["splits"], plan["unroll"], 2)
         elif plan["kernel"] == "gemm":
