@@ -52,6 +52,10 @@ HBM_PEAK_GBPS = 8000.0
 # Untimed back-to-back replays before the headline's timed steps: the GPU's
 # clock rises from idle only under sustained load.
 SETTLE_SECONDS = 0.25
+# Decode steps per graph replay in the decode measurement (the generation
+# loop replays a graph of this many steps while the position allows it, one
+# step otherwise); the one-step-per-replay rate is reported beside it.
+TOKENS_PER_REPLAY = 8
 # HBM bytes per launch of the M=1 GEMV on the two configs[1] shapes (mean),
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
@@ -347,10 +351,10 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=gen).to(device)
 
-    def timed(fused: bool):
+    def timed(fused: bool, per_replay: int = 1):
         model.fused = fused
         model.prefill(prompt)
-        model.capture()
+        model.capture(tokens_per_replay=per_replay)
         decode_s, prefill_s = [], []
         for _ in range(runs + 1):
             torch.cuda.synchronize()
@@ -358,8 +362,9 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
             model.prefill(prompt)
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            for _ in range(new_tokens - 1):
-                model.replay()
+            left = new_tokens - 1
+            while left > 0:
+                left -= model.replay_tokens(limit=left).numel()
             torch.cuda.synchronize()
             t2 = time.perf_counter()
             prefill_s.append(t1 - t0)
@@ -370,13 +375,17 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     unfused_s, prefill_eager = timed(False)
     model.fused = True   # the prefill graph records the fused prefill
     model.capture_prefill(prompt_len)
-    med, prefill = timed(True)
+    single, _ = timed(True)
+    med, prefill = timed(True, TOKENS_PER_REPLAY)
     return {
         "decode_tok_s": round((new_tokens - 1) / med, 1),
         "ms_per_token": round(med / (new_tokens - 1) * 1e3, 3),
+        "tokens_per_replay": TOKENS_PER_REPLAY,
+        "decode_tok_s_one_step_per_replay": round((new_tokens - 1) / single, 1),
         "weight_GBps": round(model.packed_bytes() * (new_tokens - 1) / med / 1e9, 1),
-        "step": "fused: RMSNorm+qkv GEMV, rotary+KV append+attention, o GEMV+residual, "
-                "RMSNorm+gate|up GEMV+SiLU*up, down GEMV+residual per layer; RMSNorm+lm_head GEMV, argmax",
+        "step": "fused, positions < 64: RMSNorm+qkv GEMV+rotary+KV append, attention+o GEMV+residual, "
+                "RMSNorm+gate|up GEMV+SiLU*up, down GEMV+residual per layer; RMSNorm+lm_head GEMV, argmax; "
+                f"{TOKENS_PER_REPLAY} steps per graph replay while the position allows, else one",
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),

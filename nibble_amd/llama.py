@@ -252,6 +252,9 @@ class LlamaDecoder(torch.nn.Module):
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
+        # several short steps in one graph (capture(tokens_per_replay=T)); step j's token goes to multi_tokens[j]
+        self.graph_multi: torch.cuda.CUDAGraph | None = None
+        self.multi_tokens: torch.Tensor | None = None
         # position < 64: rotary + KV append in the q|k|v GEMV's epilogue (else in the attention + o launch)
         self.qkv_rope = True
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
@@ -451,12 +454,34 @@ class LlamaDecoder(torch.nn.Module):
         torch.cuda.synchronize()
         return graph
 
+    def _capture_steps(self, count: int) -> torch.cuda.CUDAGraph:
+        """`count` short steps in one HIP graph, each followed by a copy of its
+        token into multi_tokens[j] (a warm-up run on a side stream first)."""
+        def steps():
+            for j in range(count):
+                self._step(True)
+                self.multi_tokens[j].copy_(self.token[0])
+
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            steps()
+        torch.cuda.current_stream().wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            steps()
+        torch.cuda.synchronize()
+        return graph
+
     @torch.inference_mode()
-    def capture(self) -> None:
+    def capture(self, tokens_per_replay: int = 1) -> None:
         """Record the decode step in HIP graphs: the general one and, when the
-        attention + o launch applies, the step for positions below 64. The KV
-        cache, position and the fused step's input row are restored afterwards
-        (capturing runs steps)."""
+        attention + o launch applies, the step for positions below 64; with
+        tokens_per_replay = T > 1 also T of those short steps in one graph,
+        which `replay_tokens` uses while the position stays below 64 (every
+        graph replay costs a fixed 12-16 us of GPU time, so T steps per replay
+        pay it once). The KV cache, position and the fused step's input row are
+        restored afterwards (capturing runs steps)."""
         saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone(),
                  self.x_buf.clone())
 
@@ -469,11 +494,19 @@ class LlamaDecoder(torch.nn.Module):
 
         self.graph = self._capture_step(False)
         restore()
+        self.graph_multi = None
         if self.attn_o:
             # the warm-up step must see a position the short step accepts
-            self.position.fill_(min(self.host_position, min(64, self.cfg.max_seq_len) - 1))
+            short_end = min(64, self.cfg.max_seq_len)
+            self.position.fill_(min(self.host_position, short_end - 1))
             self.graph_short = self._capture_step(True)
             restore()
+            if tokens_per_replay > 1 and tokens_per_replay <= short_end:
+                self.multi_tokens = torch.zeros((tokens_per_replay,), dtype=torch.int64, device=self.position.device)
+                # the capture runs 2 T steps (warm-up and recording) from a position they all accept
+                self.position.fill_(max(0, min(self.host_position, short_end - tokens_per_replay)))
+                self.graph_multi = self._capture_steps(tokens_per_replay)
+                restore()
         torch.cuda.synchronize()
 
     def replay(self) -> None:
@@ -485,14 +518,38 @@ class LlamaDecoder(torch.nn.Module):
             self.graph.replay()
         self.host_position += 1
 
+    def multi_steps(self) -> int:
+        """Steps the multi-step graph would take now (0 when it does not apply:
+        not captured, or the position would pass 63 within it)."""
+        if self.graph_multi is None:
+            return 0
+        t = self.multi_tokens.numel()
+        return t if self.host_position + t <= min(64, self.cfg.max_seq_len) else 0
+
+    def replay_tokens(self, limit: int | None = None) -> torch.Tensor:
+        """Replay decode graphs for the next tokens: the multi-step graph when it
+        applies and at most `limit` tokens are wanted, else one step. Returns the
+        new tokens (int64 [n], on the device)."""
+        t = self.multi_steps()
+        if t and (limit is None or t <= limit):
+            self.graph_multi.replay()
+            self.host_position += t
+            return self.multi_tokens.clone()
+        self.replay()
+        return self.token.clone()
+
     @torch.inference_mode()
     def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True) -> torch.Tensor:
-        """Greedy decode: prefill, then new_tokens - 1 decode steps."""
+        """Greedy decode: prefill, then new_tokens - 1 decode steps (several per
+        graph replay when capture(tokens_per_replay > 1) recorded them)."""
         out = [self.prefill(prompt)]
-        for _ in range(new_tokens - 1):
+        left = new_tokens - 1
+        while left > 0:
             if use_graph:
-                self.replay()
-                out.append(self.token.clone())
+                toks = self.replay_tokens(limit=left)
+                out.append(toks)
+                left -= toks.numel()
             else:
                 out.append(self.step())
+                left -= 1
         return torch.cat(out)

@@ -671,6 +671,31 @@ def test_fused_decode_graph_matches_eager(gpu):
         assert torch.equal(model.generate(prompt, 10, use_graph=True), eager)
 
 
+@pytest.mark.parametrize("tokens_per_replay", [2, 4, 7])
+def test_multi_step_graph_matches_eager(gpu, tokens_per_replay):
+    """Several decode steps per graph replay (capture(tokens_per_replay=T)):
+    the same tokens as eager decode, and as one step per replay; prompts that
+    leave the graph's range (position 64) fall back to single steps."""
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    cfg = LlamaConfig(vocab_size=512, hidden_size=512, intermediate_size=1280, num_layers=2, num_heads=8,
+                      num_kv_heads=2, head_dim=64, max_seq_len=80)
+    model = LlamaDecoder(cfg, device=gpu, seed=5)
+    for plen, new in ((10, 20), (50, 25)):
+        prompt = torch.randint(0, 512, (plen,), generator=torch.Generator().manual_seed(plen)).to(gpu)
+        print(f"[case] multi-step T={tokens_per_replay} prompt={plen} new={new}", flush=True)
+        eager = model.generate(prompt, new, use_graph=False)
+        model.prefill(prompt)
+        model.capture()
+        single = model.generate(prompt, new, use_graph=True)
+        model.prefill(prompt)
+        model.capture(tokens_per_replay=tokens_per_replay)
+        assert model.graph_multi is not None
+        multi = model.generate(prompt, new, use_graph=True)
+        assert torch.equal(single, eager)
+        assert torch.equal(multi, eager)
+
+
 def test_full_size_fused_step_and_graphed_tokens(gpu):
     """configs[4] at full size (22 layers, hidden 2048, 155 INT4 linears, the
     benchmark's seeds): one fused decode step against the torch-op step from
