@@ -546,12 +546,21 @@ gemm3_w4a16(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16*
     const f16x2 off = {(f16)-1032.0f, (f16)-72.0f};
     auto compute = [&](int d, int buf) {
         const f16* ab = as + (size_t)buf * BUF + (size_t)sk * 32 * MT * kGemmRow;
+        // A fragments one step ahead: step st + 1's LDS reads are in flight
+        // while step st decodes and runs its MFMAs
+        u32x4 afn[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) afn[t] = *reinterpret_cast<const u32x4*>(ab + (32 * t + c) * kGemmRow + 64 * h);
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             u32x4 af[MT];
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
-                af[t] = *reinterpret_cast<const u32x4*>(ab + (32 * t + c) * kGemmRow + 64 * h + 8 * st);
+            for (int t = 0; t < MT; ++t) af[t] = afn[t];
+            if (st < 7) {
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+                    afn[t] = *reinterpret_cast<const u32x4*>(ab + (32 * t + c) * kGemmRow + 64 * h + 8 * (st + 1));
+            }
 #pragma unroll
             for (int r = 0; r < RB; ++r) {
                 const f16 sc = __builtin_bit_cast(f16, (uint16_t)sv[d][r]);
