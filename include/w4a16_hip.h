@@ -223,8 +223,8 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     4 needs unroll 2 and rows * max_blocks < 16, or rows * max_blocks < 8).
  *   W4A16_KERNEL_GEMM32 (any M; every operand below 4 GiB): as
  *     W4A16_KERNEL_GEMM_LDS with 32-row tiles; (rows, max_blocks, unroll,
- *     splits) one of (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1),
- *     (4, 1, 2, 2).
+ *     splits) one of (4, 2, 4, 1), (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2),
+ *     (2, 2, 4, 1), (4, 1, 2, 2), (2, 1, 2, 4), (2, 1, 1, 4).
  *   W4A16_KERNEL_GENERIC: other arguments ignored.
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte

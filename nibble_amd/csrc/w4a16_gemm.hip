@@ -225,10 +225,11 @@ int launch_gemm2_silu(int mt, int rb, int sn, int sk, int M, const void* x, cons
 // GEMM on 32x32 tiles (gemm3_w4a16): mt activation tiles and rb weight
 // tiles of 32 rows per wavefront, sn wavefronts on weight tiles sharing each
 // staged round, sk wavefronts splitting K. Instantiated (M = 256 sweep of
-// 4096 x 14336, 2048 x 11264 / 5632, 14336 x 4096 and M = 128 4096 x 14336):
-// (mt, rb, sn, sk) = (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1),
-// (4, 1, 2, 2), (2, 1, 2, 4) and (2, 1, 1, 4) (staging one round ahead: two
-// register sets of 16 units would not fit); the SiLU-multiply form (rb / 2
+// 4096 x 14336, 2048 x 11264 / 5632, 14336 x 4096, M = 128 4096 x 14336 and
+// M = 512..2048 sweep): (mt, rb, sn, sk) = (4, 2, 4, 1), (4, 1, 4, 1),
+// (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2), (2, 1, 2, 4) and
+// (2, 1, 1, 4) (staging one round ahead: two register sets of 16 units would
+// not fit); the SiLU-multiply form (rb / 2
 // gate tiles and their up tiles) as (2, 2, 4, 1), (2, 2, 2, 2) and (2, 2, 1, 4)
 // (one staging set).
 namespace {
@@ -240,6 +241,7 @@ Kern pick3(int mt, int rb, int sn, int sk, bool paired) {
         if (mt == 2 && rb == 2 && sn == 1 && sk == 4) return gemm3_w4a16<2, 2, 1, 4, true, 1>;
         return nullptr;
     }
+    if (mt == 4 && rb == 2 && sn == 4 && sk == 1) return gemm3_w4a16<4, 2, 4, 1>;
     if (mt == 4 && rb == 1 && sn == 4 && sk == 1) return gemm3_w4a16<4, 1, 4, 1>;
     if (mt == 2 && rb == 1 && sn == 4 && sk == 2) return gemm3_w4a16<2, 1, 4, 2>;
     if (mt == 2 && rb == 2 && sn == 2 && sk == 2) return gemm3_w4a16<2, 2, 2, 2>;
@@ -263,9 +265,9 @@ int launch_gemm3(int mt, int rb, int sn, int sk, bool paired, int M, const void*
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG, paired ? "paired 32x32 GEMM kernel: (rows, max_blocks, unroll, splits) must be "
                                                "(2, 2, 4, 1), (2, 2, 2, 2) or (2, 2, 1, 4)"
-                                             : "32x32 GEMM kernel: (rows, max_blocks, unroll, splits) must be (4, 1, 4, "
-                                               "1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2), (2, 1, 2, 4) "
-                                               "or (2, 1, 1, 4)");
+                                             : "32x32 GEMM kernel: (rows, max_blocks, unroll, splits) must be (4, 2, 4, "
+                                               "1), (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2), "
+                                               "(2, 1, 2, 4) or (2, 1, 1, 4)");
     const int64_t lds = w4a16::gemm3_lds_bytes(mt, rb, sn, sk);
     if (lds > 160 * 1024) return fail(W4A16_ERR_CONFIG, "32x32 GEMM kernel: staging exceeds LDS");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);

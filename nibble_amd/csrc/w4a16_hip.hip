@@ -401,20 +401,32 @@ bool gemm_lds_route(int64_t M, int64_t N, int64_t K) {
 }
 
 // The staged GEMM on 32x32x16 MFMAs (gemm3_w4a16, W4A16_KERNEL_GEMM32) for M
-// >= 64 on rows of up to 4096 weights: the first of (MT, RB, SN, SK) =
-// (4, 1, 4, 1), (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) -- 128 x 128, 64 x
-// 128, 64 x 64, 64 x 32 output tiles -- that makes at least 160 workgroups.
+// >= 64 on rows of up to 4096 weights, and for M >= 512 on any rows: the
+// first of (MT, RB, SN, SK) = (4, 2, 4, 1) (M >= 256 only), (4, 1, 4, 1),
+// (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) (rows of up to 4096 weights only)
+// -- 128 x 256, 128 x 128, 64 x 128, 64 x 64, 64 x 32 output tiles -- that
+// makes at least 160 workgroups.
 // On the sweep of M = 64, 128, 256 over N x K = 2560 / 2048 / 11264 / 5632 x
 // 2048 and 14336 / 4096 / 6144 x 4096 this picks the fastest of the 16x16
-// kernels and the four shapes in every case, or one within 4% (M = 256:
+// kernels and the 32x32 shapes in every case, or one within 4% (M = 256:
 // 4096 x 14336 44.6 against 51.9 us for the staged 16x16 kernel, 2048 x 11264
 // 23.8 against 29.5, 2048 x 5632 15.9 against 20.5; M = 64 4096 x 14336 21.5
 // against 27.4 for gemm_w4a16); where no shape reaches 160 workgroups
-// (2048 x 2048 at M <= 128) gemm_w4a16 wins and keeps the layer.
+// (2048 x 2048 at M <= 128) gemm_w4a16 wins and keeps the layer. Two weight
+// tiles per wavefront, (4, 2, 4, 1), halve the LDS reads per MFMA and win
+// once the grid of 128 x 256 tiles fills the chip (M = 512: 4096 x 14336
+// 69.0 against 88.4 us for (4, 1, 4, 1), 2048 x 11264 37.4 against 47.7,
+// 8192 x 28672 263.7 against 334.4 for the staged 16x16 kernel). From M = 512
+// the 32x32 shapes also beat the 16x16 kernels on long rows (14336 x 4096
+// 86.1 against 136.6 us, at M = 1024 147.6 against 276.9; 5632 x 2048 27.2
+// against 31.5); below that the 16x16 kernels keep them (M = 256, 5632 x
+// 2048: 39.6 us on (2, 1, 1, 4) against 20.2 for gemm_w4a16).
 bool plan_gemm32(int64_t M, int64_t N, int64_t K, Plan* out) {
-    static const int kShapes[4][4] = {{4, 1, 4, 1}, {2, 1, 4, 2}, {2, 1, 2, 4}, {2, 1, 1, 4}};
-    if (M < 64 || K > 4096 || !w4a16_internal::gemm_fits(M, N, K)) return false;
+    static const int kShapes[5][4] = {{4, 2, 4, 1}, {4, 1, 4, 1}, {2, 1, 4, 2}, {2, 1, 2, 4}, {2, 1, 1, 4}};
+    if (M < 64 || (K > 4096 && M < 512) || !w4a16_internal::gemm_fits(M, N, K)) return false;
     for (const auto& sh : kShapes) {
+        if (sh[1] == 2 && M < 256) continue;                  // half of each 128-row tile would be padding
+        if (sh[2] == 1 && sh[3] == 4 && K > 4096) continue;   // one weight tile per workgroup on long rows
         const int64_t cols = 32 * sh[1] * sh[2];
         const int64_t wgs = ((N + cols - 1) / cols) * ((M + 32 * sh[0] - 1) / (32 * sh[0]));
         if (wgs >= 160) {

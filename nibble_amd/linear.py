@@ -35,11 +35,14 @@ from nibble_amd.reference import dequantize_weights, linear_reference
 # Largest M routed to the fused kernels; larger M dequantizes and uses a GEMM.
 FUSED_MAX_ROWS = 8
 # Largest M routed to the W4A16 GEMM when fused (group size 128): measured
-# against dequantize + hipBLASLt on the 1.1B / 8B layers up to M = 256
-# (e.g. M = 256, K 4096 x N 14336: 51 us against 81 us; M = 64, 5632 x 2048:
-# 10 us against 32 us); longer prompts keep dequantize + hipBLASLt, whose
-# MFMA efficiency the GEMM does not reach.
-NATIVE_GEMM_MAX_ROWS = 256
+# against dequantize + hipBLASLt on the 1.1B / 8B / 70B layers (e.g. M = 256,
+# K 4096 x N 14336: 45 us against 81 us; M = 64, 5632 x 2048: 10 us against
+# 32 us; M = 512: 69 against 95 us, 14336 x 4096 86 against 117, 8192 x 28672
+# 264 against 331, and every other swept layer faster too); from M = 1024
+# dequantize + hipBLASLt wins on the wide layers (4096 x 14336 138 against
+# 131 us, 2048 x 11264 75 against 69) and on most layers at M = 2048, so
+# longer prompts keep it.
+NATIVE_GEMM_MAX_ROWS = 512
 
 
 class QuantizedLinear(torch.nn.Module):

@@ -212,18 +212,25 @@ def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
     (127, 14336, 4096, "gemm32", (2, 1, 4, 2)), (64, 11264, 2048, "gemm32", (2, 1, 2, 4)),
     (256, 2560, 2048, "gemm32", (2, 1, 2, 4)), (64, 5632, 2048, "gemm32", (2, 1, 1, 4)),
     (256, 2048, 2048, "gemm32", (2, 1, 1, 4)), (1024, 2048, 2048, "gemm32", (2, 1, 4, 2)),
+    (512, 14336, 4096, "gemm32", (4, 2, 4, 1)), (512, 11264, 2048, "gemm32", (4, 2, 4, 1)),
+    (256, 32000, 2048, "gemm32", (4, 2, 4, 1)), (255, 32000, 2048, "gemm32", (4, 1, 4, 1)),
+    (512, 4096, 14336, "gemm32", (2, 1, 4, 2)), (512, 2048, 5632, "gemm32", (2, 1, 2, 4)),
+    (1024, 4096, 14336, "gemm32", (4, 1, 4, 1)), (512, 28672, 8192, "gemm32", (4, 2, 4, 1)),
+    (512, 1000, 5632, "gemm", None),   # long rows: no (2, 1, 1, 4); the others stay under 160 workgroups
+    (511, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
     (128, 2048, 2048, "gemm", None),   # no 32x32 shape reaches 160 workgroups
     (64, 4096, 4096, "gemm", None), (32, 11264, 2048, "gemm", None), (63, 14336, 4096, "gemm", None),
     (256, 4096, 14336, "gemm_lds", (4, 2, 2, 4)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
     (256, 2048, 5632, "gemm", None),   # long rows of a narrow layer: the per-round barriers lose
 ])
 def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
-    """M >= 64 on rows of up to 4096 weights: the 32x32 staged GEMM, the first
-    of (rows, max_blocks, unroll = wavefronts sharing the staging, splits) =
-    (4, 1, 4, 1), (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) with >= 160
-    workgroups; M >= 128 on longer rows of layers with N >= 4096: the 16x16
-    staged GEMM, 4 activation and 2 weight tiles per wavefront; else
-    gemm_w4a16."""
+    """M >= 64 on rows of up to 4096 weights, and M >= 512 on any rows: the
+    32x32 staged GEMM, the first of (rows, max_blocks, unroll = wavefronts
+    sharing the staging, splits) = (4, 2, 4, 1) (M >= 256), (4, 1, 4, 1),
+    (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) (rows of up to 4096 weights)
+    with >= 160 workgroups; M >= 128 on longer rows of layers with N >= 4096:
+    the 16x16 staged GEMM, 4 activation and 2 weight tiles per wavefront;
+    else gemm_w4a16."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
     assert plan["kernel"] == kernel

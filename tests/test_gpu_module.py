@@ -110,7 +110,7 @@ def test_module_noncontiguous_and_3d(gpu):
     assert_parity(out3.reshape(6, 16), expected(x, p, s), "3-D")
 
 
-@pytest.mark.parametrize("fused,m,k,n", [(True, 16, 128, 8), (True, 300, 128, 8), (False, 1, 128, 8),
+@pytest.mark.parametrize("fused,m,k,n", [(True, 16, 128, 8), (True, 300, 128, 8), (True, 600, 128, 8), (False, 1, 128, 8),
                                          (False, 4, 128, 8), (True, 64, 2048, 5632), (True, 256, 4096, 512),
                                          (True, 9, 5632, 300)])
 def test_module_prefill_paths_match_dequant_linear(gpu, fused, m, k, n):

@@ -407,7 +407,8 @@ def test_gemm_lds_variants(gpu, rows, blocks, sn, splits, m, k, n):
     assert_parity(got, expected(x, p, s), f"gemm_lds {rows}/{blocks}/{sn}/{splits} M={m} K={k} N={n}")
 
 
-GEMM32_SHAPES = [(4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2)]
+GEMM32_SHAPES = [(4, 2, 4, 1), (4, 1, 4, 1), (2, 1, 4, 2), (2, 2, 2, 2), (2, 2, 4, 1), (4, 1, 2, 2), (2, 1, 2, 4),
+                 (2, 1, 1, 4)]
 
 
 @pytest.mark.parametrize("rows,blocks,sn,splits", GEMM32_SHAPES)
@@ -425,14 +426,15 @@ def test_gemm32_variants(gpu, rows, blocks, sn, splits, m, k, n):
 def test_gemm32_rejects(gpu):
     x, p, s = make_case(64, 256, 64, seed=1)
     with pytest.raises(_lib.W4A16Error, match="32x32 GEMM kernel"):
-        _run_tuned(gpu, x, p, s, GEMM32, 4, 1, 4, max_blocks=2)
+        _run_tuned(gpu, x, p, s, GEMM32, 4, 2, 2, max_blocks=2)   # (4, 2, 2, 2): not instantiated
 
 
 @pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm32"), (130, 5632, 2048, "gemm"),
                                           (512, 2048, 256, "gemm"), (33, 8192, 1000, "gemm"),
                                           (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm32"),
                                           (256, 2048, 5632, "gemm32"), (128, 1024, 20480, "gemm32"),
-                                          (100, 2048, 6000, "gemm32"), (64, 2048, 2048, "gemm")])
+                                          (100, 2048, 6000, "gemm32"), (64, 2048, 2048, "gemm"),
+                                          (520, 1024, 8200, "gemm32"), (512, 4224, 4103, "gemm32")])
 def test_default_dispatch_gemm(gpu, m, k, n, kernel):
     x, p, s = make_case(m, k, n, seed=m + k + 3 * n)
     assert _lib.plan_linear(1 << 20, 1 << 20, m, n, k, 128)["kernel"] == kernel
