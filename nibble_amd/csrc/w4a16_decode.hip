@@ -224,69 +224,107 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
 
 // ---------------------------------------------------------------------------
 // Greedy argmax over fp16 logits (first index of the maximum, as
-// torch.argmax), one workgroup of 1024 threads reading 16-byte vectors when
-// the logits are 16-byte aligned; writes the token and, when given, advances
-// the position by one and gathers the token's embedding row into `emb_out`
-// (the next decode step's input), so the step needs no separate gather.
+// torch.argmax; NaN logits are skipped), one workgroup of 1024 threads
+// reading 16-byte vectors when the logits are 16-byte aligned; writes the
+// token and, when given, advances the position by one and gathers the
+// token's embedding row into `emb_out` (the next decode step's input), so the
+// step needs no separate gather. Two passes: the maximum (packed fp16 max
+// over each thread's vectors, then the workgroup), and the first index that
+// holds it, searched only by the threads whose own maximum it is (from the
+// registers of the first round, re-read past it). The position is read at
+// launch and the last steps (the winners' reduction, the token, the gather)
+// run in wavefront 0 alone.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
 argmax_kernel(const f16* __restrict__ logits, int n, int64_t* __restrict__ token, int64_t* __restrict__ position,
               const f16* __restrict__ table, int64_t vocab, int hidden, f16* __restrict__ emb_out) {
-    __shared__ float best_v[16];
-    __shared__ int best_i[16];
-    __shared__ int64_t chosen;
-    float bv = -__builtin_inff();
-    int bi = n;   // sentinel: larger than any index
+    constexpr int T = 1024;
+    __shared__ float wave_max[T / 64];
+    __shared__ int wave_first[T / 64];
+    // the position is requested first, so its round trip overlaps the logits'
+    const int64_t pos0 = (position != nullptr && threadIdx.x == 0) ? position[0] : 0;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const bool vec = (reinterpret_cast<uintptr_t>(logits) & 15u) == 0;
     const int nv = vec ? n >> 3 : 0;
     constexpr int kBatch = 4;   // vectors requested per thread before any is compared
-    for (int j0 = threadIdx.x; j0 < nv; j0 += kBatch * blockDim.x) {
-        u32x4 u[kBatch];
+    const f16 ninf = __builtin_bit_cast(f16, (uint16_t)0xFC00u);
+    f16x2 m2 = {ninf, ninf};
+    u32x4 u[kBatch];   // after the loop: the last round's vectors (the only round when nv <= kBatch T)
+    for (int j0 = tid; j0 < nv; j0 += kBatch * T) {
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int j = min(j0 + b * (int)blockDim.x, nv - 1);
-            u[b] = reinterpret_cast<const u32x4*>(logits)[j];
-        }
+        for (int b = 0; b < kBatch; ++b) u[b] = reinterpret_cast<const u32x4*>(logits)[min(j0 + b * T, nv - 1)];
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int j = j0 + b * (int)blockDim.x;
-            if (j >= nv) break;
+        for (int b = 0; b < kBatch; ++b)
+            if (j0 + b * T < nv)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const f16x2 h = as_f16x2(u[b][e]);
-                const int i = 8 * j + 2 * e;
-                const float a = (float)h.x, c = (float)h.y;
-                if (a > bv || (a == bv && i < bi)) { bv = a; bi = i; }
-                if (c > bv || (c == bv && i + 1 < bi)) { bv = c; bi = i + 1; }
-            }
-        }
+                for (int e = 0; e < 4; ++e) m2 = __builtin_elementwise_max(m2, as_f16x2(u[b][e]));
     }
-    for (int i = 8 * nv + threadIdx.x; i < n; i += blockDim.x) {
-        const float v = (float)logits[i];
-        if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { best_v[wave] = bv; best_i[wave] = bi; }
+    for (int i = 8 * nv + tid; i < n; i += T) m2.x = __builtin_elementwise_max(m2.x, logits[i]);
+    const float mine = fmaxf((float)m2.x, (float)m2.y);
+    float gm = mine;
+    for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+    if (lane == 0) wave_max[wave] = gm;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int waves = blockDim.x >> 6;
-        for (int w = 1; w < waves; ++w)
-            if (best_v[w] > bv || (best_v[w] == bv && best_i[w] < bi)) { bv = best_v[w]; bi = best_i[w]; }
-        const int64_t t = bi < n ? bi : 0;
+#pragma unroll
+    for (int w = 0; w < T / 64; ++w) gm = fmaxf(gm, wave_max[w]);
+
+    // the first index holding gm among this thread's elements, in index order
+    // (rounds, vectors of a round, elements of a vector, then the tail);
+    // gm = -inf (every logit -inf or NaN) gives token 0
+    int first = n;
+    if (mine == gm && gm != -__builtin_inff()) {
+        const bool one_round = nv <= kBatch * T;
+        for (int j0 = tid; j0 < nv; j0 += kBatch * T) {
+            if (!one_round)
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) u[b] = reinterpret_cast<const u32x4*>(logits)[min(j0 + b * T, nv - 1)];
+#pragma unroll
+            for (int b = 0; b < kBatch; ++b) {
+                const int j = j0 + b * T;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const f16x2 h = as_f16x2(u[b][e >> 1]);
+                    if (j < nv && (float)((e & 1) ? h.y : h.x) == gm) first = min(first, 8 * j + e);
+                }
+            }
+            if (first < n) break;
+        }
+        for (int i = 8 * nv + tid; i < n && first == n; i += T)
+            if ((float)logits[i] == gm) first = i;
+    }
+    for (int off = 32; off >= 1; off >>= 1) first = min(first, __shfl_xor(first, off));
+    if (lane == 0) wave_first[wave] = first;
+    __syncthreads();
+    if (wave != 0) return;
+    // wavefront 0: the smallest of the 16 wavefronts' first indices, the
+    // token, the position, the gather
+    first = lane < T / 64 ? wave_first[lane] : n;
+    for (int off = 8; off >= 1; off >>= 1) first = min(first, __shfl_xor(first, off));
+    first = __shfl(first, 0);
+    const int64_t t = first < n ? first : 0;
+    if (lane == 0) {
         token[0] = t;
-        chosen = t;
-        if (position != nullptr) position[0] += 1;
+        if (position != nullptr) position[0] = pos0 + 1;
     }
     if (emb_out == nullptr) return;
-    __syncthreads();
-    const int64_t t = chosen;
     const f16* row = table + t * hidden;
-    for (int i = threadIdx.x; i < hidden; i += blockDim.x) emb_out[i] = t < vocab ? row[i] : (f16)0.0f;
+    const bool in_range = t < vocab;
+    if ((hidden & 7) == 0 && ((reinterpret_cast<uintptr_t>(row) | reinterpret_cast<uintptr_t>(emb_out)) & 15u) == 0) {
+        const int nvec = hidden >> 3;
+        for (int i0 = lane; i0 < nvec; i0 += 4 * 64) {
+            u32x4 v[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int i = min(i0 + 64 * b, nvec - 1);
+                v[b] = in_range ? reinterpret_cast<const u32x4*>(row)[i] : (u32x4){0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                if (i0 + 64 * b < nvec) reinterpret_cast<u32x4*>(emb_out)[i0 + 64 * b] = v[b];
+        }
+    } else {
+        for (int i = lane; i < hidden; i += 64) emb_out[i] = in_range ? row[i] : (f16)0.0f;
+    }
 }
 
 // out[i] = table[token, i]; an out-of-range token gives zeros.

@@ -546,8 +546,47 @@ def test_argmax_first_maximum_and_position(gpu, n):
     assert int(token) == int(torch.argmax(logits))
 
 
-def test_argmax_embed_gathers_next_row(gpu):
-    vocab, hidden = 1000, 2048
+def test_argmax_special_values(gpu):
+    """The first maximum past the first round of vectors (n > 32768), in the
+    scalar tail, on misaligned logits; NaN logits are skipped; all -inf
+    gives token 0 (torch.argmax's answer there)."""
+    token = torch.zeros((1,), dtype=torch.int64, device=gpu)
+
+    def run(lg):
+        _lib.argmax_f16(lg, token)
+        torch.cuda.synchronize()
+        return int(token)
+
+    gen = torch.Generator().manual_seed(5)
+    lg = torch.randn((40000,), generator=gen).to(torch.float16)
+    lg[39000] = 9.0
+    lg[39001] = 9.0
+    lg[100] = float("nan")
+    lg[33000] = float("nan")
+    assert run(lg.to(gpu)) == 39000
+    lg[12345] = 9.0                       # the same maximum in the first round wins
+    assert run(lg.to(gpu)) == 12345
+    tail = torch.zeros((33,), dtype=torch.float16)
+    tail[32] = 5.0                        # index 32 is past the 4 vectors
+    assert run(tail.to(gpu)) == 32
+    tail[7] = 5.0
+    assert run(tail.to(gpu)) == 7
+    buf = torch.zeros((34,), dtype=torch.float16, device=gpu)
+    buf[1:] = tail.to(gpu)
+    assert run(buf[1:]) == 7              # misaligned: every element on the scalar path
+    assert run(torch.full((1000,), float("-inf"), dtype=torch.float16, device=gpu)) == 0
+    neg = torch.full((1000,), float("-inf"), dtype=torch.float16)
+    neg[600] = -60000.0
+    neg[10] = float("nan")
+    assert run(neg.to(gpu)) == 600
+
+
+@pytest.mark.parametrize("hidden", [2048, 8200, 4100, 24])
+def test_argmax_embed_gathers_next_row(gpu, hidden):
+    """The row is gathered by 16-byte vectors (several per lane past 512
+    halves) or, for a hidden size that is not a multiple of 8 or a
+    misaligned output, element by element."""
+    vocab = 1000
     table = torch.randn((vocab, hidden)).to(torch.float16).to(gpu)
     logits = torch.randn((vocab,)).to(torch.float16)
     logits[777] = 50.0
@@ -564,6 +603,11 @@ def test_argmax_embed_gathers_next_row(gpu):
     _lib.argmax_embed_f16(buf[1:], token, None, table, out)
     torch.cuda.synchronize()
     assert int(token) == 777
+    # misaligned output: element by element
+    obuf = torch.zeros((hidden + 1,), dtype=torch.float16, device=gpu)
+    _lib.argmax_embed_f16(logits.to(gpu), token, None, table, obuf[1:])
+    torch.cuda.synchronize()
+    assert torch.equal(obuf[1:], table[777]) and float(obuf[0]) == 0.0
 
 
 def test_embedding_gather(gpu):
