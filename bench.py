@@ -8,13 +8,18 @@ at M = 1 -- up/gate K=2048 N=5632 and down K=5632 N=2048 -- group size 128,
 fp16 activations ~N(0,1), weights ~N(0,0.02) fp32 quantized RTN absmax, each
 shape with 64 rotated weight copies (762 MB together) so no layer runs from
 the 256 MB Infinity Cache. One step = one call of each shape on its next
-copy. Steps are recorded in a HIP graph and replayed: 0.25 s of untimed
-replays of whole rotations bring the GPU out of its idle clock, then the
-pre-roll, the W warm-up steps and exactly K timed steps are enqueued back to
-back, the K steps bracketed by events on the replay stream (synchronised
-before and after). `value` = algorithmic bytes moved by
-the K steps / elapsed time (GB/s), with algorithmic bytes per call
-N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 (reference scripts/profile_kernel.py:310-323).
+copy. 0.25 s of untimed graph replays of whole rotations bring the GPU out of
+its idle clock; then untimed pre-roll replays (enough to keep the GPU busy
+while the host enqueues the timed calls), the W warm-up steps (a graph) and
+exactly K timed steps, enqueued as eager calls, go back to back, the K steps
+bracketed by events on the stream (synchronised before and after). The GPU
+must still be in the pre-roll when the last timed call is enqueued (checked:
+the start event has not fired), so the events hold the 2K kernels and no host
+launch gap; the same K steps replayed as one graph carry the graph launch's
+own 9-10 us of GPU time and are reported beside it (`value_graph_replay`).
+`value` = algorithmic bytes moved by the K steps / elapsed time (GB/s), with
+algorithmic bytes per call N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 (reference
+scripts/profile_kernel.py:310-323).
 
 Rotation: step g reads copy g mod 64 of one continuous sequence -- an untimed
 64-step pre-roll, the warm-up steps, the timed steps -- so every timed call
@@ -614,27 +619,72 @@ def main() -> int:
     preroll = capture(step, copies)
     warm = capture(lambda i: step(copies + i), warmup)
     timed = capture(lambda i: step(copies + warmup + i), args.steps)
-    # The GPU leaves its idle clock only under sustained load (a 20-step timed
-    # region alone runs ~0.15 ms, at whatever clock the idle GPU is in):
-    # ~0.25 s of pre-roll replays first (whole rotations, so the copy order
-    # is unchanged), then the pre-roll, warm-up and timed steps are enqueued
-    # back to back with no host wait between them.
-    settle_start = time.perf_counter()
-    while time.perf_counter() - settle_start < SETTLE_SECONDS:
-        for _ in range(20):
-            preroll.replay()
-        torch.cuda.synchronize()
+
+    def settle() -> None:
+        # The GPU leaves its idle clock only under sustained load (a 20-step
+        # timed region alone runs ~0.15 ms, at whatever clock the idle GPU is
+        # in): ~0.25 s of pre-roll replays (whole rotations, so the copy
+        # order is unchanged) before each timed sequence.
+        settle_start = time.perf_counter()
+        while time.perf_counter() - settle_start < SETTLE_SECONDS:
+            for _ in range(20):
+                preroll.replay()
+            torch.cuda.synchronize()
+
+    # The K timed steps are enqueued as eager calls, the way the op is called,
+    # while untimed pre-roll replays still keep the GPU busy, so every timed
+    # kernel is queued before the GPU reaches it and the events bracket the
+    # 2K kernels alone. (Replayed as one graph, the same steps carry the
+    # graph launch's own 9-10 us of GPU time per replay: reported beside it
+    # as value_graph_replay.) Enough pre-roll replays are queued to cover the
+    # host's enqueueing of the K steps; if the GPU nevertheless reached the
+    # start event before the last timed call was enqueued, the sequence runs
+    # again with twice the pre-roll (then falls back to the graph replay).
+    settle()
+    t0 = time.perf_counter()
+    for i in range(8):
+        step(copies + warmup + i)
+    host_step_s = (time.perf_counter() - t0) / 8
+    torch.cuda.synchronize()
+    preroll_s = time_graph(preroll)
+    rolls = 1 + int(1.5 * args.steps * host_step_s / preroll_s)
     start_ev = torch.cuda.Event(enable_timing=True)
     end_ev = torch.cuda.Event(enable_timing=True)
+    timed_launch = None
+    for _attempt in range(4):
+        settle()
+        for _ in range(rolls):
+            preroll.replay()
+        warm.replay()
+        start_ev.record()
+        for i in range(args.steps):
+            step(copies + warmup + i)
+        queued = not start_ev.query()
+        end_ev.record()
+        end_ev.synchronize()
+        if queued:
+            timed_launch = (f"eager calls, enqueued behind {rolls} untimed pre-roll replays and the warm-up "
+                            "(the GPU had not reached the timed region when the last timed call was enqueued)")
+            break
+        rolls *= 2
+    eager_elapsed = start_ev.elapsed_time(end_ev) / 1e3
+    # the same steps as one graph replay, queued behind the pre-roll and warm-up
+    settle()
     preroll.replay()
     warm.replay()
     start_ev.record()
     timed.replay()
     end_ev.record()
     end_ev.synchronize()
-    elapsed = start_ev.elapsed_time(end_ev) / 1e3
+    graph_elapsed = start_ev.elapsed_time(end_ev) / 1e3
+    if timed_launch is None:
+        timed_launch = "one graph replay queued behind the pre-roll and warm-up (the eager enqueue could not stay ahead)"
+        elapsed = graph_elapsed
+    else:
+        elapsed = eager_elapsed
     step_bytes = sum(payload_bytes(1, n, k) for k, n in shapes)
     value = step_bytes * args.steps / elapsed / 1e9
+    value_graph = step_bytes * args.steps / graph_elapsed / 1e9
 
     # ---- per-layer and the dominant kernel's roofline ----
     layer_rows = {}
@@ -679,13 +729,16 @@ def main() -> int:
         "data": "synthetic (weights ~N(0,0.02) fp32 RTN-quantized to INT4 g128, activations ~N(0,1) fp16)",
         "config": {
             "workload": "configs[1]: M=1 MLP layers K2048xN5632 + K5632xN2048, group 128, 64 rotated copies each",
-            "step": "one call of each shape, HIP-graph replay; step g reads copy g mod 64",
-            "rotation": f"{SETTLE_SECONDS} s of untimed pre-roll replays (GPU clock settle), then an untimed 64-step pre-roll, then the warm-up steps, then the timed steps, all one "
+            "step": "one call of each shape (the C-ABI entry point); step g reads copy g mod 64",
+            "timed_launch": timed_launch,
+            "rotation": f"{SETTLE_SECONDS} s of untimed pre-roll replays (GPU clock settle), then untimed 64-step pre-rolls, then the warm-up steps, then the timed steps, all one "
                         "sequence: every timed call reads a copy last read 64 steps (762 MB of weights) earlier; "
                         f"the timed steps read copies {(copies + warmup) % copies}.. of 64",
             "timed_copies": min(args.steps, copies),
             "parallelism": "single GPU",
         },
+        "value_graph_replay": round(value_graph, 1),
+        "ms_per_step_graph_replay": round(graph_elapsed / args.steps * 1e3, 5),
         "layers_us": layer_rows,
         "torch_op_us": op_us,
         "torch_op_eager_us": op_eager_us,
