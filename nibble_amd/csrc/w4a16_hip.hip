@@ -347,8 +347,12 @@ bool stream_fits(int64_t K) {
 // shape from the sweep over M 32..256 and the 1.1B / 8B layer shapes: the
 // first of (MT, RB) = (4, 4), (2, 4), (4, 2), (2, 2), (1, 4), (1, 2), (2, 1),
 // (1, 1) with MT <= ceil(M / 16) that leaves at least 160 workgroups (the
-// most workgroups otherwise); 2 wavefronts splitting K for tiles of 8 or 16
-// MFMA blocks, else 4 (2 on rows of fewer than 8 groups).
+// most workgroups otherwise); 4 wavefronts splitting K (2 on rows of fewer
+// than 8 groups). A later sweep of (MT, RB, SK) over M = 16..256 on 5632 x
+// 2048 / 2560, 14336 x 4096, 2048 x 2048 / 2560 and 4096 x 4096 found 4
+// wavefronts at least as fast as 2 for tiles of 8 and 16 MFMA blocks too
+// (M = 128, 5632 x 2560: 21.4 against 23.0 us; M = 128, 14336 x 4096: 54.6
+// against 56.6; M = 256, 5632 x 2048: 20.1 against 20.9).
 Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
     Plan p;
     p.kernel = W4A16_KERNEL_GEMM;
@@ -371,12 +375,12 @@ Plan plan_gemm(int64_t M, int64_t N, int64_t K) {
             p.max_blocks = rb;
         }
     }
-    p.splits = (K / 128 < 8 || p.rows * p.max_blocks >= 8) ? 2 : 4;
+    p.splits = K / 128 < 8 ? 2 : 4;
     p.unroll = 0;
     return p;
 }
 
-// LDS-staged GEMM (w4a16_gemm.h, gemm2_w4a16) for M >= 128 on rows longer
+// LDS-staged GEMM (w4a16_gemm.h, gemm2_w4a16) for M >= kGemmLdsMinM on rows longer
 // than 4096 weights with N >= 4096 (M = 256, 14336 x 4096: 68.5 against
 // 78.5 us for gemm_w4a16; shorter rows take the 32x32 kernel below or
 // gemm_w4a16). Plan fields: rows = MT, max_blocks = RB, unroll = SN
@@ -394,9 +398,17 @@ Plan plan_gemm_lds(int64_t M, int64_t N, int64_t K) {
     return p;
 }
 
+// Smallest M routed to gemm2_w4a16 (long rows): up to M = 128 gemm_w4a16
+// takes 32-row tiles with 4 wavefronts splitting K and wins (M = 128: 14336
+// x 4096 54.5 against 68.4 us, 11008 x 4096 39.8 against 58.1, 5632 x 4096
+// 22.2 against 30.1); above it gemm_w4a16 needs 64-row tiles and the staged
+// kernel wins or ties (M = 160: 68.3 against 78.3, 57.8 against 55.7, 29.9
+// against 31.4; M = 256: 68.9 against 80.4).
+constexpr int64_t kGemmLdsMinM = 129;
+
 bool gemm_lds_route(int64_t M, int64_t N, int64_t K) {
     const Plan p = plan_gemm_lds(M, N, K);
-    return M >= 128 && K > 4096 && N >= 4096 && w4a16_internal::gemm_fits(M, N, K) &&
+    return M >= kGemmLdsMinM && K > 4096 && N >= 4096 && w4a16_internal::gemm_fits(M, N, K) &&
            w4a16_internal::gemm2_instantiated(p.rows, p.max_blocks, p.unroll, p.splits);
 }
 

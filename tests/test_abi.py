@@ -171,15 +171,16 @@ def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
 
 @pytest.mark.parametrize("m,n,k,rows,blocks,splits", [
     # best shapes of the M = 32..256 sweep on the 1.1B / 8B layers
-    (32, 2560, 2048, 1, 2, 4), (32, 2048, 2048, 1, 1, 4), (32, 11264, 2048, 2, 4, 2), (32, 14336, 4096, 2, 4, 2),
-    (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (48, 11264, 2048, 2, 4, 2), (64, 4096, 14336, 2, 2, 4),
-    (100, 2048, 5632, 2, 2, 4), (256, 2048, 5632, 2, 4, 2),   # from M = 64 short rows mostly take the 32x32 GEMM
+    (32, 2560, 2048, 1, 2, 4), (32, 2048, 2048, 1, 1, 4), (32, 11264, 2048, 2, 4, 4), (32, 14336, 4096, 2, 4, 4),
+    (64, 2560, 2048, 2, 2, 4), (64, 2048, 5632, 1, 2, 4), (48, 11264, 2048, 2, 4, 4), (64, 4096, 14336, 2, 2, 4),
+    (100, 2048, 5632, 2, 2, 4), (256, 2048, 5632, 2, 4, 4),   # from M = 64 short rows mostly take the 32x32 GEMM
+    (128, 4096, 14336, 2, 4, 4),   # long rows up to M = 128: gemm_w4a16, not the staged kernel
     (17, 64, 256, 1, 1, 2),     # few workgroups whatever the shape: the most; short rows: 2 wavefronts
 ])
 def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
     """M > 16: the largest tile (activation tiles within ceil(M / 16)) that
-    leaves >= 160 workgroups; 2 wavefronts splitting K for 8+ MFMA blocks per
-    wavefront or rows of fewer than 8 groups, else 4."""
+    leaves >= 160 workgroups; 4 wavefronts splitting K, 2 on rows of fewer
+    than 8 groups."""
     monkeypatch.setenv("W4A16_DECODE", "valu")   # the selector covers M <= 8 only
     plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
     assert (plan["kernel"], plan["rows"], plan["max_blocks"], plan["splits"]) == ("gemm", rows, blocks, splits)
@@ -220,7 +221,8 @@ def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
     (511, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
     (128, 2048, 2048, "gemm", None),   # no 32x32 shape reaches 160 workgroups
     (64, 4096, 4096, "gemm", None), (32, 11264, 2048, "gemm", None), (63, 14336, 4096, "gemm", None),
-    (256, 4096, 14336, "gemm_lds", (4, 2, 2, 4)), (128, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
+    (256, 4096, 14336, "gemm_lds", (4, 2, 2, 4)), (129, 4096, 14336, "gemm_lds", (4, 2, 2, 4)),
+    (128, 4096, 14336, "gemm", None),
     (256, 2048, 5632, "gemm", None),   # long rows of a narrow layer: the per-round barriers lose
 ])
 def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
@@ -228,7 +230,7 @@ def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
     32x32 staged GEMM, the first of (rows, max_blocks, unroll = wavefronts
     sharing the staging, splits) = (4, 2, 4, 1) (M >= 256), (4, 1, 4, 1),
     (2, 1, 4, 2), (2, 1, 2, 4), (2, 1, 1, 4) (rows of up to 4096 weights)
-    with >= 160 workgroups; M >= 128 on longer rows of layers with N >= 4096:
+    with >= 160 workgroups; M > 128 on longer rows of layers with N >= 4096:
     the 16x16 staged GEMM, 4 activation and 2 weight tiles per wavefront;
     else gemm_w4a16."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)

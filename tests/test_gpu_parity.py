@@ -431,7 +431,7 @@ def test_gemm32_rejects(gpu):
 
 @pytest.mark.parametrize("m,k,n,kernel", [(17, 2048, 2048, "gemm"), (64, 2048, 5632, "gemm32"), (130, 5632, 2048, "gemm"),
                                           (512, 2048, 256, "gemm"), (33, 8192, 1000, "gemm"),
-                                          (128, 4224, 4103, "gemm_lds"), (200, 2048, 11300, "gemm32"),
+                                          (129, 4224, 4103, "gemm_lds"), (128, 4224, 4103, "gemm"), (200, 2048, 11300, "gemm32"),
                                           (256, 2048, 5632, "gemm32"), (128, 1024, 20480, "gemm32"),
                                           (100, 2048, 6000, "gemm32"), (64, 2048, 2048, "gemm"),
                                           (520, 1024, 8200, "gemm32"), (512, 4224, 4103, "gemm32")])
