@@ -967,6 +967,186 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
     }
 }
 
+
+// Prefill attention on the matrix cores, for the two-launch path (more than
+// kPrefillOneLaunch tokens; the rotary k and the v rows of the new tokens are
+// already in the caches) when the query heads per KV head, group, are a power
+// of two up to 64. Workgroup (hk, b) of 4 wavefronts takes KV head hk and the
+// 64 / group tokens t = b 64 / group .. of all its group query heads: 64 query
+// columns, column c = token offset * group + head offset, wavefront w owning
+// columns 16 w .. 16 w + 15. It stages the k and v rows of every slot its last
+// token sees once (shared by the 64 columns, where the one-query kernel above
+// restages them per head and per 4 queries), then each wavefront walks the
+// slots in chunks of 32 with an online softmax:
+//   S^T = K Q^T (v_mfma_f32_16x16x32_f16; A = k rows from LDS, lane (q4, j)
+//     holds slot 16 mt + j, dims 32 s + 8 q4 .. +8; B = the rotary q of column
+//     j, rounded to fp16), so lane (q4, j) receives column j's scores for
+//     slots c0 + 16 mt + 4 q4 + e, scaled by 1/8 and masked past the column's
+//     last slot (start + its token);
+//   the column's running maximum and sum across the four lanes that hold it
+//     by v_permlane16_swap / v_permlane32_swap;
+//   O^T += V^T P^T with P^T (fp16) straight from the score registers and V^T
+//     from the row-major LDS tile through ds_read_b64_tr_b16 (the lane mapping
+//     of attn_o_kernel), the accumulator rescaled by exp(old max - new max).
+// fp32 scores, softmax and accumulation; the probabilities enter the MFMA as
+// fp16. LDS: k and v [NK rounded up to 32][kPrefillRow] fp16, rows past NK
+// zero.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+prefill_attention_mfma_kernel(const f16* __restrict__ qkv, const f16* __restrict__ k_cache,
+                              const f16* __restrict__ v_cache, const float* __restrict__ cos_table,
+                              const float* __restrict__ sin_table, int start, int T, f16* __restrict__ out,
+                              int num_heads, int num_kv, int S, int glog) {
+    constexpr int D = 64;
+    constexpr int KR = kPrefillRow;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int group = 1 << glog;
+    const int tpw = 64 >> glog;   // tokens per workgroup
+    const int hk = blockIdx.x;
+    const int t0 = blockIdx.y * tpw;
+    const int NK = start + min(t0 + tpw, T);   // slots the workgroup's last token sees
+    const int NKP = (NK + 31) & ~31;
+    f16* ks = reinterpret_cast<f16*>(smem);   // [NKP][KR]
+    f16* vs = ks + (size_t)NKP * KR;          // [NKP][KR]
+    const int row_stride = (num_heads + 2 * num_kv) * D;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int q4 = lane >> 4, j = lane & 15;
+
+    // 1. this lane's query column (requested first) and the k / v rows
+    const int col = 16 * wave + j;
+    const int tq = t0 + (col >> glog);
+    const int tqc = min(tq, T - 1);
+    const int hq = hk * group + (col & (group - 1));
+    const f16* qrow = qkv + (size_t)tqc * row_stride + (size_t)hq * D;
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(qrow + 8 * q4);
+    const u32x4 qz = *reinterpret_cast<const u32x4*>(qrow + 32 + 8 * q4);
+    float cs[8], sn[8];
+    {
+        const size_t ti = (size_t)(start + tqc) * (D / 2) + 8 * q4;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            cs[i] = cos_table[ti + i];
+            sn[i] = sin_table[ti + i];
+        }
+    }
+    {
+        const u32x4* kc = reinterpret_cast<const u32x4*>(k_cache + (size_t)hk * S * D);
+        const u32x4* vc = reinterpret_cast<const u32x4*>(v_cache + (size_t)hk * S * D);
+        const int units = NK * 8, punits = NKP * 8;
+        for (int i0 = threadIdx.x; i0 < punits; i0 += 8 * 256) {
+            u32x4 kb[8], vb[8];
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const int i = min(i0 + 256 * b, units - 1);
+                kb[b] = kc[i];
+                vb[b] = vc[i];
+            }
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const int i = i0 + 256 * b;
+                if (i < punits) {
+                    const bool live = i < units;
+                    const int r = i >> 3, e = i & 7;
+                    reinterpret_cast<u32x4*>(ks + (size_t)r * KR)[e] = live ? kb[b] : (u32x4){0u, 0u, 0u, 0u};
+                    reinterpret_cast<u32x4*>(vs + (size_t)r * KR)[e] = live ? vb[b] : (u32x4){0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    }
+    // the rotary q (B operand): dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i (s = 1)
+    u32x4 qb[2];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        const f16x2 a = as_f16x2(qa[h]), z = as_f16x2(qz[h]);
+        const float c0 = cs[2 * h], c1 = cs[2 * h + 1], s0 = sn[2 * h], s1 = sn[2 * h + 1];
+        const f16x2 lo = {(f16)((float)a.x * c0 - (float)z.x * s0), (f16)((float)a.y * c1 - (float)z.y * s1)};
+        const f16x2 hi = {(f16)((float)z.x * c0 + (float)a.x * s0), (f16)((float)z.y * c1 + (float)a.y * s1)};
+        qb[0][h] = as_u32(lo);
+        qb[1][h] = as_u32(hi);
+    }
+    __syncthreads();
+    if (t0 + ((16 * wave) >> glog) >= T) return;   // no column of this wavefront is a token
+
+    // 2. chunks of 32 slots up to the wavefront's last visible slot
+    const int last = start + tqc;
+    const int lastw = start + min(t0 + ((16 * wave + 15) >> glog), T - 1);
+    const int tk = j >> 2, tm = j & 3;   // this lane's row / 4-dim block in the transposing read
+    float run_max = -__builtin_inff(), run_sum = 0.0f;
+    f32x4 o[4];
+#pragma unroll
+    for (int md = 0; md < 4; ++md) o[md] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 <= lastw; c0 += 32) {
+        f32x4 st[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            st[mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            const f16* krow = ks + (size_t)(c0 + 16 * mt + j) * KR + 8 * q4;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+                st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(krow + 32 * s2)),
+                    __builtin_bit_cast(f16x8, qb[s2]), st[mt], 0, 0, 0);
+        }
+        float mx = run_max;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int slot = c0 + 16 * mt + 4 * q4 + e;
+                st[mt][e] = slot <= last ? st[mt][e] * 0.125f : -__builtin_inff();
+                mx = fmaxf(mx, st[mt][e]);
+            }
+        mx = row_pair_max(mx);
+        const float rescale = __expf(run_max - mx);   // 0 on the first chunk
+        float psum = 0.0f;
+        float pe[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int slot = c0 + 16 * mt + 4 * q4 + e;
+                pe[mt][e] = slot <= last ? __expf(st[mt][e] - mx) : 0.0f;
+                psum += pe[mt][e];
+            }
+        const f16x2 p00 = {(f16)pe[0][0], (f16)pe[0][1]}, p01 = {(f16)pe[0][2], (f16)pe[0][3]};
+        const f16x2 p10 = {(f16)pe[1][0], (f16)pe[1][1]}, p11 = {(f16)pe[1][2], (f16)pe[1][3]};
+        const u32x4 pb = {as_u32(p00), as_u32(p01), as_u32(p10), as_u32(p11)};
+        psum = row_pair_sum(psum);
+        run_sum = run_sum * rescale + psum;
+        run_max = mx;
+#pragma unroll
+        for (int md = 0; md < 4; ++md) {
+            const f16* src = vs + (size_t)(c0 + 4 * q4 + tk) * KR + 16 * md + 4 * tm;
+            const uint2 lo = lds_read_tr16(src);
+            const uint2 hi = lds_read_tr16(src + 16 * KR);
+            const u32x4 a = {lo.x, lo.y, hi.x, hi.y};
+            o[md] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, pb),
+                                                           o[md] * rescale, 0, 0, 0);
+        }
+    }
+
+    // 3. lane (q4, j) holds column j's dims 16 md + 4 q4 .. + 3
+    if (tq >= T) return;
+    const float inv = 1.0f / run_sum;
+    f16* orow = out + (size_t)tq * num_heads * D + (size_t)hq * D;
+    const bool vec = (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        const f16x2 a = {(f16)(o[md][0] * inv), (f16)(o[md][1] * inv)};
+        const f16x2 b = {(f16)(o[md][2] * inv), (f16)(o[md][3] * inv)};
+        f16* dst = orow + 16 * md + 4 * q4;
+        if (vec) {
+            *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(a), as_u32(b));
+        } else {
+            dst[0] = a.x;
+            dst[1] = a.y;
+            dst[2] = b.x;
+            dst[3] = b.y;
+        }
+    }
+}
+
 }  // namespace w4a16
 
 namespace w4a16_internal {
@@ -1208,6 +1388,10 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     const int nk = (int)(start + tokens);   // slots the last query block sees
     const size_t lds = (size_t)w4a16::kPrefillQueries * 64 * 4 + (size_t)2 * nk * w4a16::kPrefillRow * 2;
     const bool fused = tokens <= w4a16::kPrefillOneLaunch;
+    const int64_t group = num_heads / num_kv_heads;
+    int glog = 0;
+    while ((int64_t)1 << glog < group) ++glog;
+    const bool mfma = !fused && ((int64_t)1 << glog) == group && group <= 64;
     const auto attend = fused ? w4a16::prefill_attention_kernel<true> : w4a16::prefill_attention_kernel<false>;
     const void* kern = reinterpret_cast<const void*>(attend);
     if (lds > 64 * 1024) {
@@ -1223,6 +1407,21 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
                            (int)start, (int)tokens, (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
         const int rc = check_launch();
         if (rc != W4A16_OK) return rc;
+    }
+    if (mfma) {
+        const void* mk = reinterpret_cast<const void*>(w4a16::prefill_attention_mfma_kernel);
+        const size_t mlds = (size_t)2 * ((nk + 31) & ~31) * w4a16::kPrefillRow * 2;
+        if (mlds > 64 * 1024) {
+            const hipError_t e = hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)mlds);
+            if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
+        }
+        const int tpw = 64 >> glog;
+        hipLaunchKernelGGL(w4a16::prefill_attention_mfma_kernel, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)),
+                           dim3(256), mlds, static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           static_cast<const w4a16::f16*>(k_cache), static_cast<const w4a16::f16*>(v_cache), cos_table,
+                           sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
+                           (int)num_kv_heads, (int)max_seq_len, glog);
+        return check_launch();
     }
     hipLaunchKernelGGL(attend, dim3((unsigned)num_heads, blocks), dim3(256), lds, static_cast<hipStream_t>(stream),
                        static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),
