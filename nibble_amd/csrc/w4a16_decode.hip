@@ -992,9 +992,10 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
 // fp16. LDS: k and v [NK rounded up to 32][kPrefillRow] fp16, rows past NK
 // zero.
 // ---------------------------------------------------------------------------
+template <bool FUSED>
 __global__ void __launch_bounds__(256)
-prefill_attention_mfma_kernel(const f16* __restrict__ qkv, const f16* __restrict__ k_cache,
-                              const f16* __restrict__ v_cache, const float* __restrict__ cos_table,
+prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
+                              f16* __restrict__ v_cache, const float* __restrict__ cos_table,
                               const float* __restrict__ sin_table, int start, int T, f16* __restrict__ out,
                               int num_heads, int num_kv, int S, int glog) {
     constexpr int D = 64;
@@ -1031,9 +1032,11 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, const f16* __restrict
         }
     }
     {
+        // rows from the caches: all NK (zeros past them up to NKP), or (FUSED)
+        // those below start
         const u32x4* kc = reinterpret_cast<const u32x4*>(k_cache + (size_t)hk * S * D);
         const u32x4* vc = reinterpret_cast<const u32x4*>(v_cache + (size_t)hk * S * D);
-        const int units = NK * 8, punits = NKP * 8;
+        const int units = (FUSED ? start : NK) * 8, punits = (FUSED ? start : NKP) * 8;
         for (int i0 = threadIdx.x; i0 < punits; i0 += 8 * 256) {
             u32x4 kb[8], vb[8];
 #pragma unroll
@@ -1052,6 +1055,81 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, const f16* __restrict
                     reinterpret_cast<u32x4*>(vs + (size_t)r * KR)[e] = live ? vb[b] : (u32x4){0u, 0u, 0u, 0u};
                 }
             }
+        }
+    }
+    if constexpr (FUSED) {
+        // the new rows this workgroup sees (tokens 0 .. nn - 1) from qkv: v
+        // as is, k rotated at its slot (fp32, rounded to fp16, as
+        // prefill_rope_append_kernel); the workgroup's own tokens t0 .. nn - 1
+        // are appended to the caches; rows NK .. NKP - 1 zero
+        const int nn = NK - start;
+        const f16* kq = qkv + (size_t)num_heads * D + (size_t)hk * D;
+        const f16* vq = qkv + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
+        for (int i0 = threadIdx.x; i0 < nn * 8; i0 += 4 * 256) {
+            u32x4 vb[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int i = min(i0 + 256 * b, nn * 8 - 1);
+                vb[b] = *reinterpret_cast<const u32x4*>(vq + (size_t)(i >> 3) * row_stride + 8 * (i & 7));
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int i = i0 + 256 * b;
+                if (i < nn * 8) {
+                    const int r = i >> 3, e = i & 7;
+                    reinterpret_cast<u32x4*>(vs + (size_t)(start + r) * KR)[e] = vb[b];
+                    if (r >= t0)
+                        reinterpret_cast<u32x4*>(v_cache + ((size_t)hk * S + start + r) * D)[e] = vb[b];
+                }
+            }
+        }
+        for (int i0 = threadIdx.x; i0 < nn * 4; i0 += 2 * 256) {
+            u32x4 ka[2], kz[2];
+            f32x4 cv[2][2], sv[2][2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int i = min(i0 + 256 * b, nn * 4 - 1);
+                const int r = i >> 2, db = i & 3;
+                const f16* kr = kq + (size_t)r * row_stride + 8 * db;
+                ka[b] = *reinterpret_cast<const u32x4*>(kr);
+                kz[b] = *reinterpret_cast<const u32x4*>(kr + 32);
+                const size_t ti = (size_t)(start + r) * (D / 2) + 8 * db;
+                cv[b][0] = *reinterpret_cast<const f32x4*>(cos_table + ti);
+                cv[b][1] = *reinterpret_cast<const f32x4*>(cos_table + ti + 4);
+                sv[b][0] = *reinterpret_cast<const f32x4*>(sin_table + ti);
+                sv[b][1] = *reinterpret_cast<const f32x4*>(sin_table + ti + 4);
+            }
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int i = i0 + 256 * b;
+                if (i < nn * 4) {
+                    const int r = i >> 2, db = i & 3;
+                    u32x4 lo, hi;
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        const f16x2 a = as_f16x2(ka[b][h]), z = as_f16x2(kz[b][h]);
+                        const float c0 = cv[b][h >> 1][2 * (h & 1)], c1 = cv[b][h >> 1][2 * (h & 1) + 1];
+                        const float s0 = sv[b][h >> 1][2 * (h & 1)], s1 = sv[b][h >> 1][2 * (h & 1) + 1];
+                        const f16x2 l2 = {(f16)((float)a.x * c0 - (float)z.x * s0), (f16)((float)a.y * c1 - (float)z.y * s1)};
+                        const f16x2 h2 = {(f16)((float)z.x * c0 + (float)a.x * s0), (f16)((float)z.y * c1 + (float)a.y * s1)};
+                        lo[h] = as_u32(l2);
+                        hi[h] = as_u32(h2);
+                    }
+                    f16* krow = ks + (size_t)(start + r) * KR;
+                    reinterpret_cast<u32x4*>(krow)[db] = lo;
+                    reinterpret_cast<u32x4*>(krow)[4 + db] = hi;
+                    if (r >= t0) {
+                        u32x4* dst = reinterpret_cast<u32x4*>(k_cache + ((size_t)hk * S + start + r) * D);
+                        dst[db] = lo;
+                        dst[4 + db] = hi;
+                    }
+                }
+            }
+        }
+        for (int i = threadIdx.x; i < (NKP - NK) * 8; i += 256) {
+            const int r = NK + (i >> 3), e = i & 7;
+            reinterpret_cast<u32x4*>(ks + (size_t)r * KR)[e] = (u32x4){0u, 0u, 0u, 0u};
+            reinterpret_cast<u32x4*>(vs + (size_t)r * KR)[e] = (u32x4){0u, 0u, 0u, 0u};
         }
     }
     // the rotary q (B operand): dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i (s = 1)
@@ -1391,7 +1469,24 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     const int64_t group = num_heads / num_kv_heads;
     int glog = 0;
     while ((int64_t)1 << glog < group) ++glog;
-    const bool mfma = !fused && ((int64_t)1 << glog) == group && group <= 64;
+    const bool mfma = ((int64_t)1 << glog) == group && group <= 64 && aligned(qkv, 16) && aligned(cos_table, 16) &&
+                      aligned(sin_table, 16);
+    if (mfma) {
+        const auto mkern = w4a16::prefill_attention_mfma_kernel<true>;
+        const void* mk = reinterpret_cast<const void*>(mkern);
+        const size_t mlds = (size_t)2 * ((nk + 31) & ~31) * w4a16::kPrefillRow * 2;
+        if (mlds > 64 * 1024) {
+            const hipError_t e = hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)mlds);
+            if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
+        }
+        const int tpw = 64 >> glog;
+        hipLaunchKernelGGL(mkern, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)),
+                           dim3(256), mlds, static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table,
+                           sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
+                           (int)num_kv_heads, (int)max_seq_len, glog);
+        return check_launch();
+    }
     const auto attend = fused ? w4a16::prefill_attention_kernel<true> : w4a16::prefill_attention_kernel<false>;
     const void* kern = reinterpret_cast<const void*>(attend);
     if (lds > 64 * 1024) {
@@ -1407,21 +1502,6 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
                            (int)start, (int)tokens, (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
         const int rc = check_launch();
         if (rc != W4A16_OK) return rc;
-    }
-    if (mfma) {
-        const void* mk = reinterpret_cast<const void*>(w4a16::prefill_attention_mfma_kernel);
-        const size_t mlds = (size_t)2 * ((nk + 31) & ~31) * w4a16::kPrefillRow * 2;
-        if (mlds > 64 * 1024) {
-            const hipError_t e = hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)mlds);
-            if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
-        }
-        const int tpw = 64 >> glog;
-        hipLaunchKernelGGL(w4a16::prefill_attention_mfma_kernel, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)),
-                           dim3(256), mlds, static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
-                           static_cast<const w4a16::f16*>(k_cache), static_cast<const w4a16::f16*>(v_cache), cos_table,
-                           sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
-                           (int)num_kv_heads, (int)max_seq_len, glog);
-        return check_launch();
     }
     hipLaunchKernelGGL(attend, dim3((unsigned)num_heads, blocks), dim3(256), lds, static_cast<hipStream_t>(stream),
                        static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),

@@ -177,12 +177,19 @@ def _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv):
     return out.transpose(0, 1).reshape(t, heads * 64), kc, vc, k_new, v_new
 
 
-@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
-@pytest.mark.parametrize("tokens,start", [(1, 0), (5, 0), (16, 0), (64, 0), (16, 7), (64, 192), (7, 3), (130, 0),
-                                          (256, 0), (100, 101)])
-def test_prefill_attention(gpu, heads, kv, tokens, start):
+_ATTN_CASES = [(1, 0), (5, 0), (16, 0), (64, 0), (16, 7), (64, 192), (7, 3), (130, 0), (256, 0), (100, 101)]
+
+
+@pytest.mark.parametrize("heads,kv,misaligned", [(32, 4, False), (8, 8, False), (4, 1, False), (32, 1, False),
+                                                 (64, 1, False), (12, 4, False), (32, 4, True)])
+@pytest.mark.parametrize("tokens,start", _ATTN_CASES)
+def test_prefill_attention(gpu, heads, kv, misaligned, tokens, start):
+    """Query heads per KV head a power of two up to 64 with 16-byte aligned
+    qkv and tables: the matrix-core kernel (64 query columns per workgroup);
+    otherwise (group 3, or qkv at a 2-byte offset) the one-query-per-wavefront
+    kernels."""
     S = 256
-    gen = torch.Generator().manual_seed(tokens * 13 + start + heads)
+    gen = torch.Generator().manual_seed(tokens * 13 + start + heads + kv)
     qkv = torch.randn((tokens, (heads + 2 * kv) * 64), generator=gen).to(torch.float16)
     k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
     v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
@@ -190,8 +197,15 @@ def test_prefill_attention(gpu, heads, kv, tokens, start):
     ref, kc_ref, vc_ref, k_new, v_new = _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv)
     kd, vd = k_cache.to(gpu), v_cache.to(gpu)
     out = torch.full((tokens, heads * 64), float("nan"), dtype=torch.float16, device=gpu)
-    print(f"[case] prefill attention heads={heads} kv={kv} tokens={tokens} start={start}", flush=True)
-    _lib.prefill_attention_f16(qkv.to(gpu), kd, vd, cos.to(gpu), sin.to(gpu), start, out, heads, kv)
+    print(f"[case] prefill attention heads={heads} kv={kv} tokens={tokens} start={start} misaligned={misaligned}",
+          flush=True)
+    if misaligned:
+        buf = torch.empty((qkv.numel() + 1,), dtype=torch.float16, device=gpu)
+        buf[1:] = qkv.to(gpu).view(-1)
+        qkv_d = buf[1:].view(qkv.shape)
+    else:
+        qkv_d = qkv.to(gpu)
+    _lib.prefill_attention_f16(qkv_d, kd, vd, cos.to(gpu), sin.to(gpu), start, out, heads, kv)
     torch.cuda.synchronize()
     got = out.double().cpu()
     assert torch.isfinite(got).all()
