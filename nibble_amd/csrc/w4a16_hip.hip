@@ -584,10 +584,35 @@ bool pair_split_route(int64_t M, int64_t N, int64_t K) {
 // M = 9..16 on the paired kernel: two launches, rows [0, m1) and [m1, M) with
 // m1 = ceil(M/2) (each half 4..8 rows), each with its own launch shape unless
 // the caller fixed one; the weights are streamed twice.
+// M = 9..16 in one paired launch (16 row slots, the dequantized weights in B)
+// where it beats the GEMM: measured at M = 9, 12, 16 against gemm_w4a16
+// (graph timing, one box), 5632 x 2048 7.3-7.9 against 7.9-9.0 us, 14336 x
+// 4096 14.4-18.0 against 16.8-21.0, 2048 x 11264 8.2-8.5 against 8.5-9.2;
+// the GEMM keeps rows of 2049..4096 weights and narrower layers of short
+// rows (4096 x 4096 7.3-7.8 against 6.7-7.7, 2048 x 2048 4.5-5.0 against
+// 4.1-4.7, 2048 x 2560 5.6-6.2 against 4.3-4.9, 4096 x 14336 a tie) and
+// grids of more than 256 workgroups.
+bool pair16_route(int64_t M, int64_t N, int64_t K) {
+    if (M < 9 || M > 16 || K < 128 || K % 128 != 0 || K > 32768) return false;
+    if (!(K > 4096 || (K <= 2048 && N >= 8192))) return false;
+    const Plan p = plan_mfma_pair(M, N, K);
+    const int64_t wgs = (N + 8 * p.max_blocks - 1) / (8 * p.max_blocks);
+    return wgs <= 256 && w4a16_internal::mfma_pair_instantiated(M, p.splits, p.max_blocks, p.rows, p.unroll) &&
+           w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
+}
+
 int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16* x, const uint8_t* w,
                           const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t st) {
     if (M <= 8)
         return w4a16_internal::launch_mfma_pair(p.splits, p.max_blocks, p.rows, p.unroll, M, x, w, s, o, N, K, st);
+    {   // M = 9..16 in one launch (16 row slots) where that shape is instantiated and fits in LDS
+        const Plan q = own_plans ? plan_mfma_pair(M, N, K) : p;
+        const int pairs = (K / 128 + 1) / 2;
+        const int gpw = q.unroll > 0 ? q.unroll : q.splits > 0 ? (pairs + q.splits - 1) / q.splits : 0;
+        if (gpw > 0 && w4a16_internal::mfma_pair_instantiated(M, q.splits, q.max_blocks, q.rows, gpw) &&
+            w4a16_internal::mfma_pair_lds_bytes(M, K, q.splits, q.max_blocks, q.rows, gpw) <= kMaxLdsBytes)
+            return w4a16_internal::launch_mfma_pair(q.splits, q.max_blocks, q.rows, gpw, M, x, w, s, o, N, K, st);
+    }
     const int m1 = (M + 1) / 2;
     const int ms[2] = {m1, M - m1};
     for (int h = 0; h < 2; ++h) {
@@ -651,6 +676,13 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     }
     if (aligned && M > 8 && M <= 16 && family == W4A16_KERNEL_MFMA_PAIR && mfma_pair_fits(M, N, K)) {
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
+        return W4A16_OK;
+    }
+    // M = 9..16 on long rows (and wide layers of short rows) whose paired
+    // plan keeps at most one workgroup per CU: the paired kernel in one
+    // launch (16 row slots)
+    if (aligned && family == 0 && pair16_route(M, N, K)) {
+        *out = plan_mfma_pair(M, N, K);
         return W4A16_OK;
     }
     // M > 8 (a prompt): the W4A16 GEMM; from M = 64 on rows of up to 4096

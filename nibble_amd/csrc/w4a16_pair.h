@@ -44,13 +44,24 @@ namespace w4a16 {
 // the constant -(1032, 1032, 1152, 1152, ...), shared by the RB blocks)
 // instead of staging dot products and an LDS table.
 //
+// 16 row slots (M = 9..16): the A rows are the activation rows of one group,
+// so a step runs two MFMAs against the same B (the pair's two groups); a
+// lane keeps the D of the MFMA whose group matches its B column, and the
+// halves of an output sit in lanes l and l + 8. These put the dequantized
+// weights in B (exact codes times the group scale, rounded to fp16 once, as
+// w4a16_dequantize_f16 writes them; activations staged unscaled, no bias)
+// and accumulate in the MFMA: the result is the reference's prefill path
+// (dequantize, fp16 GEMM with fp32 accumulation) up to summation order,
+// where an fp32 scale applied to per-group sums of codes, or the offset
+// decode's sums of ~1032 |x|, would miss its 1e-3 tolerance.
+//
 // Chunks (C pairs < SK * GPW): rows too long for LDS are staged C pairs at a
 // time into two alternating buffers, one barrier per chunk: chunk c + 1 is
 // written to the other buffer after chunk c's MFMAs. Loads are requested
 // chunk by chunk (activations, then that chunk's scales and weights), the
 // first LA chunks up front and chunk c + LA when chunk c starts.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr int pair_row_slots(int M) { return M <= 4 ? 4 : 8; }
+__host__ __device__ constexpr int pair_row_slots(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 // LDS of gemv_mfma_pair: one or two buffers (one when a single chunk of
 // `chunk` pairs covers the `pairs` a workgroup steps over) of staged units
@@ -72,6 +83,10 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     constexpr int P = SK * GPW;                // pairs the workgroup steps over
     static_assert(C % SK == 0 && C <= P, "a chunk is a whole number of steps");
     static_assert(LA >= 1, "at least the first chunk is requested up front");
+    static_assert(MS == 4 || MS == 8 || MS == 16, "4, 8 or 16 row slots");
+    static_assert(MS != 16 || !MB, "16 row slots take the bias from the staging");
+    constexpr bool W16 = MS == 16;   // M = 9..16: one activation group per MFMA, two MFMAs per step, exact decode
+    constexpr int H = W16 ? 2 : 1;   // A fragment sets per step
     constexpr int NC = (P + C - 1) / C;        // chunks
     constexpr int NB = NC > 1 ? 2 : 1;         // staging buffers
     constexpr int JPC = C / SK;                // steps per chunk
@@ -118,11 +133,13 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             const int gl = ul >> 4, qq = (ul >> 2) & 3, t = ul & 3;
             const bool zero = 2 * c * C + gl >= G;
             u32x4 pv = permute8(a[p]);
-            pv.y = as_u32(as_f16x2(pv.y) * sixteenth);
-            pv.w = as_u32(as_f16x2(pv.w) * sixteenth);
+            if (!W16) {
+                pv.y = as_u32(as_f16x2(pv.y) * sixteenth);
+                pv.w = as_u32(as_f16x2(pv.w) * sixteenth);
+            }
             if (zero) pv = (u32x4){0u, 0u, 0u, 0u};
             float cs = 0.0f;
-            if (!MB) {
+            if (!MB && !W16) {
                 cs = __builtin_amdgcn_fdot2(as_f16x2(pv.x), b0, cs, false);
                 cs = __builtin_amdgcn_fdot2(as_f16x2(pv.y), b1, cs, false);
                 cs = __builtin_amdgcn_fdot2(as_f16x2(pv.z), b0, cs, false);
@@ -135,7 +152,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             }
             if (m < M) {
                 xb[(((gl >> 1) * 4 + t) * 4 + qq) * LS + ((m + MS * (gl & 1) + 4 * qq + t) & (LS - 1))] = pv;
-                if (!MB && (ul & 15) == 0) bb[gl * 16 + m] = -cs;
+                if (!MB && !W16 && (ul & 15) == 0) bb[gl * 16 + m] = -cs;
             }
         }
     };
@@ -187,11 +204,19 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     // the MFMAs. A row `col` = activation row arow of group group(j, bhalf);
     // D rows 4 q .. 4 q + 3 = activation rows dm .. dm + 3 of group
     // group(j, q >> 1).
-    const int arow = brow % M;
-    int toff[4];
+    // M <= 8: A row `col` = activation row arow of group group(j, bhalf).
+    // M > 8 (16 row slots): A row `col` = activation row col of group
+    // group(j, h) in the step's h-th MFMA; B columns col < 8 hold group
+    // group(j, 0) and col >= 8 group group(j, 1), so a lane keeps the D of
+    // the MFMA whose group matches its B column.
+    const int arow = W16 ? col % M : brow % M;
+    int toff[H][4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) toff[t] = (kw * 16 + q) * LS + 4 * t * LS + ((arow + MS * bhalf + 4 * q + t) & (LS - 1));
-    const int boff = (2 * kw + (q >> 1)) * 16 + 4 * (q & 1);
+    for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            toff[h][t] = (kw * 16 + q) * LS + 4 * t * LS + ((arow + MS * (W16 ? h : bhalf) + 4 * q + t) & (LS - 1));
+    const int boff = W16 ? 2 * kw * 16 + 4 * q : (2 * kw + (q >> 1)) * 16 + 4 * (q & 1);
     f32x4 acc[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) acc[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -201,24 +226,31 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         const u32x4* xb = xs + buf * XS;
         const float* bb = base + buf * C * 32;
         if (c + LA < NC) issue(c + LA);
-        auto fetch = [&](u32x4 (&av)[4], f32x4& bv, int jl) {
+        auto fetch = [&](u32x4 (&av)[H][4], f32x4 (&bv)[H], int jl) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) av[t] = xb[jl * SK * 16 * LS + toff[t]];
-            if (!MB) bv = *reinterpret_cast<const f32x4*>(bb + jl * SK * 32 + boff);
+            for (int h = 0; h < H; ++h) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) av[h][t] = xb[jl * SK * 16 * LS + toff[h][t]];
+                if (!MB && !W16) bv[h] = *reinterpret_cast<const f32x4*>(bb + jl * SK * 32 + boff + 16 * h);
+            }
         };
         const int steps = (c + 1) * JPC <= GPW ? JPC : GPW - c * JPC;
-        u32x4 A0[4], A1[4];
-        f32x4 B0 = {0.0f, 0.0f, 0.0f, 0.0f}, B1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        u32x4 A0[H][4], A1[H][4];
+        f32x4 B0[H], B1[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) B0[h] = B1[h] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
         fetch(A0, B0, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jl = 0; jl < JPC; ++jl) {
             if (jl < steps) {
                 const int j = c * JPC + jl;
-                u32x4 (&cur)[4] = (jl & 1) ? A1 : A0;
-                u32x4 (&nxt)[4] = (jl & 1) ? A0 : A1;
-                f32x4& cb = (jl & 1) ? B1 : B0;
-                f32x4& nbv = (jl & 1) ? B0 : B1;
+                u32x4 (&curh)[H][4] = (jl & 1) ? A1 : A0;
+                u32x4 (&nxt)[H][4] = (jl & 1) ? A0 : A1;
+                f32x4 (&cbh)[H] = (jl & 1) ? B1 : B0;
+                f32x4 (&nbv)[H] = (jl & 1) ? B0 : B1;
+                u32x4 (&cur)[4] = curh[0];
+                f32x4& cb = cbh[0];
                 if (jl + 1 < steps) fetch(nxt, nbv, jl + 1);
                 __builtin_amdgcn_sched_barrier(0);
                 const bool in_range = group(j, bhalf) < G;
@@ -237,17 +269,33 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
                 }
 #pragma unroll
                 for (int b = 0; b < RB; ++b) {
-                    f32x4 d = cb;
+                    // 16 row slots: B = fp16_rn(code * scale), the dequantized
+                    // weights bit for bit (scale 0 past K), summed unscaled
+                    const f16 sc16 = in_range ? __builtin_bit_cast(f16, (uint16_t)sv[j][b]) : (f16)0.0f;
+                    const f16x2 sc2 = {sc16, sc16};
+                    f32x4 dh[H];
+#pragma unroll
+                    for (int h = 0; h < H; ++h) dh[h] = W16 ? acc[b] : cbh[h];
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const Codes8 cw = unpack8_offset(wv[j][b][t]);
+                        Codes8 cw = W16 ? unpack8(wv[j][b][t]) : unpack8_offset(wv[j][b][t]);
+                        if (W16) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) cw.p[e] = cw.p[e] * sc2;
+                        }
                         const f16x8 bt = __builtin_bit_cast(
                             f16x8, (u32x4){as_u32(cw.p[0]), as_u32(cw.p[1]), as_u32(cw.p[2]), as_u32(cw.p[3])});
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[t]), bt, d, 0, 0,
-                                                                   0);
+#pragma unroll
+                        for (int h = 0; h < H; ++h)
+                            dh[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, curh[h][t]), bt,
+                                                                           dh[h], 0, 0, 0);
                     }
-                    const float sc = in_range ? (float)__builtin_bit_cast(f16, (uint16_t)sv[j][b]) : 0.0f;
-                    acc[b] = d * sc + acc[b];
+                    if (W16) {
+                        acc[b] = bhalf ? dh[H - 1] : dh[0];
+                    } else {
+                        const float sc = in_range ? (float)sc16 : 0.0f;
+                        acc[b] = dh[0] * sc + acc[b];
+                    }
                 }
             }
         }
@@ -258,17 +306,19 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     }
 
     // 3. reduce the SK partial tiles and the two halves (lane l + 40 onto
-    // lane l, q < 2, c < 8), store rows m < M
+    // lane l, q < 2, c < 8; with 16 row slots lane l + 8 onto lane l, c < 8),
+    // store rows m < M
+    constexpr int HALF = W16 ? 8 : 40;
 #pragma unroll
     for (int b = 0; b < RB; ++b) red[(wave * RB + b) * 64 + lane] = acc[b];
     __syncthreads();
-    if (kw != 0 || q >= 2 || col >= 8) return;
+    if (kw != 0 || (!W16 && q >= 2) || col >= 8) return;
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-        f32x4 v = acc[b] + red[(wave * RB + b) * 64 + lane + 40];
+        f32x4 v = acc[b] + red[(wave * RB + b) * 64 + lane + HALF];
 #pragma unroll
         for (int s2 = 1; s2 < SK; ++s2)
-            v += red[((wave + s2) * RB + b) * 64 + lane] + red[((wave + s2) * RB + b) * 64 + lane + 40];
+            v += red[((wave + s2) * RB + b) * 64 + lane] + red[((wave + s2) * RB + b) * 64 + lane + HALF];
         const int nn = n0 + 8 * b + col;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {

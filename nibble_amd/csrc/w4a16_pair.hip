@@ -87,12 +87,18 @@ Kern pick_chunked(int sk, int sn, int gpw) {
             case 6: return gemv_mfma_pair<8, SN, 1, 6, MS, C, kLookahead>;                                                 \
             case 7: return gemv_mfma_pair<8, SN, 1, 7, MS, C, kLookahead>;                                                 \
             case 8: return gemv_mfma_pair<8, SN, 1, 8, MS, C, kLookahead>;                                                 \
-            case 10: return gemv_mfma_pair<8, SN, 1, 10, MS, C, kLookahead, true>;                                               \
-            case 12: return gemv_mfma_pair<8, SN, 1, 12, MS, C, kLookahead, true>;                                               \
-            case 14: return gemv_mfma_pair<8, SN, 1, 14, MS, C, kLookahead, true>;                                               \
-            case 16: return gemv_mfma_pair<8, SN, 1, 16, MS, C, kLookahead, true>;                                               \
-            default: return nullptr;                                                                           \
+            default: break;                                                                                    \
         }                                                                                                      \
+        if constexpr (MS != 16) {                                                                              \
+            switch (gpw) {                                                                                     \
+                case 10: return gemv_mfma_pair<8, SN, 1, 10, MS, C, kLookahead, true>;                         \
+                case 12: return gemv_mfma_pair<8, SN, 1, 12, MS, C, kLookahead, true>;                         \
+                case 14: return gemv_mfma_pair<8, SN, 1, 14, MS, C, kLookahead, true>;                         \
+                case 16: return gemv_mfma_pair<8, SN, 1, 16, MS, C, kLookahead, true>;                         \
+                default: break;                                                                                \
+            }                                                                                                  \
+        }                                                                                                      \
+        return nullptr;                                                                                        \
     }
     W4A16_G4(1) W4A16_G4(2) W4A16_G4(4) W4A16_G8(1) W4A16_G8(2)
 #undef W4A16_G4
@@ -120,8 +126,11 @@ namespace w4a16_internal {
 int mfma_pair_auto_chunk(int64_t M, int sk, int sn, int gpw) { return auto_chunk(M, sk, sn, gpw); }
 
 Kern pick(int64_t M, int sk, int sn, int chunk, int gpw) {
-    if (chunk == sk * gpw) return M <= 4 ? pick_whole<4>(sk, sn, gpw) : pick_whole<8>(sk, sn, gpw);
-    if (chunk == kChunkPairs) return M <= 4 ? pick_chunked<4>(sk, sn, gpw) : pick_chunked<8>(sk, sn, gpw);
+    if (chunk == sk * gpw)
+        return M <= 4 ? pick_whole<4>(sk, sn, gpw) : M <= 8 ? pick_whole<8>(sk, sn, gpw) : pick_whole<16>(sk, sn, gpw);
+    if (chunk == kChunkPairs)
+        return M <= 4 ? pick_chunked<4>(sk, sn, gpw) : M <= 8 ? pick_chunked<8>(sk, sn, gpw)
+                                                      : pick_chunked<16>(sk, sn, gpw);
     return nullptr;
 }
 
@@ -144,7 +153,7 @@ int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int
 // The caller has checked pointers, group size 128 and 16-byte alignment.
 int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream) {
-    if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel needs 2 <= M <= 8");
+    if (M < 2 || M > 16) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel needs 2 <= M <= 16");
     if (K < 128 || K % 128 != 0) return fail(W4A16_ERR_CONFIG, "paired MFMA kernel: K must be a positive multiple of 128");
     const int G = K / 128;
     const int pairs = (G + 1) / 2;

@@ -132,7 +132,8 @@ ALIGNED = 1 << 20
         (8, 5632, 128, ALIGNED, "mfma_pair"),
         (9, 2048, 128, ALIGNED, "gemm"),           # a short prompt: the GEMM at one activation tile
         (16, 4096, 128, ALIGNED, "gemm"),
-        (16, 5632, 128, ALIGNED, "gemm"),
+        (12, 5632, 128, ALIGNED, "mfma_pair"),     # M = 9..16 on long rows: one paired launch (16 row slots)
+        (9, 5632, 128, ALIGNED, "mfma_pair"),
         (9, 28672, 128, ALIGNED, "gemm"),
         (16, 34816, 128, ALIGNED, "gemm"),
         (17, 2048, 128, ALIGNED, "gemm"),          # prompts above one tile: the W4A16 GEMM
@@ -343,6 +344,7 @@ def test_reference_decode_versions(monkeypatch, value, kernel):
     # M > 1, misaligned operands, other group sizes: the default routing
     assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 2048, 128)["kernel"] == "mfma_pair"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 16, 64, 2048, 128)["kernel"] == "gemm"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 16, 64, 5632, 128)["kernel"] == "mfma_pair"   # 16 row slots
     assert _lib.plan_linear(ALIGNED + 2, ALIGNED, 1, 64, 2048, 128)["kernel"] == "generic"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 64)["kernel"] == "generic"
     # activations past LDS: the default routing

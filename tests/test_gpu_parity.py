@@ -159,23 +159,25 @@ def test_mfma_oneshot_variants(gpu, m, rows, splits, k, n):
 
 
 def _pair_lds(m, staged, chunk, splits, blocks):
-    slots = 4 if m <= 4 else 8
+    slots = 4 if m <= 4 else 8 if m <= 8 else 16
     buffers = 2 if chunk < staged else 1
     return buffers * (chunk * 16 * 2 * slots * 16 + chunk * 128) + splits * blocks * 1024
 
 
 # paired-group MFMA, whole rows staged (rows = splits * unroll): every
 # (splits, blocks) class, odd group counts (a half pair zero-filled), splits *
-# unroll past the last pair (padding pairs), ragged N, both row-slot widths
-# (M <= 4 and M > 4), K up to LDS
+# unroll past the last pair (padding pairs), ragged N, every row-slot width
+# (M <= 4, M <= 8 and M = 9..16: one activation group per MFMA), K up to LDS
 @pytest.mark.parametrize("splits,blocks", [(2, 1), (4, 2), (8, 1), (2, 8), (4, 4), (8, 2)])
 @pytest.mark.parametrize("k,n", [(128, 7), (384, 9), (1152, 33), (2048, 2048), (3968, 21), (5632, 100),
                                  (8192, 64), (16384, 24)])
-@pytest.mark.parametrize("m", [2, 3, 4, 6, 8])
+@pytest.mark.parametrize("m", [2, 3, 4, 6, 8, 9, 13, 16])
 def test_mfma_pair_whole(gpu, m, splits, blocks, k, n):
     pairs = (k // 128 + 1) // 2
     unroll = -(-pairs // splits)
     staged = splits * unroll
+    if m > 8 and (unroll > 8 or _pair_lds(m, staged, staged, splits, blocks) > 160 * 1024):
+        pytest.skip("no 16-slot kernel for this shape (test_mfma_pair_m9_16_tuned covers the row-halves path)")
     if unroll > 8 or _pair_lds(m, staged, staged, splits, blocks) > 160 * 1024:
         x, p, s = make_case(m, k, n, seed=1)
         with pytest.raises(_lib.W4A16Error, match="no instantiation|do not fit in LDS"):
@@ -192,7 +194,7 @@ def test_mfma_pair_whole(gpu, m, splits, blocks, k, n):
 @pytest.mark.parametrize("splits,blocks,k", [(4, 1, 7168), (4, 4, 8192), (4, 2, 6400), (8, 1, 5632), (8, 2, 5760),
                                              (8, 1, 8192), (8, 2, 14336), (8, 1, 16512), (8, 2, 28672),
                                              (8, 1, 32768)])
-@pytest.mark.parametrize("m", [2, 4, 5, 8])
+@pytest.mark.parametrize("m", [2, 4, 5, 8, 12, 16])
 def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
     n = 37
     pairs = (k // 128 + 1) // 2
@@ -201,6 +203,7 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
         unroll += unroll % 2
     assert _pair_lds(m, splits * unroll, 8, splits, blocks) <= 160 * 1024
     x, p, s = make_case(m, k, n, seed=m * 7 + k + blocks)
+    # (M > 8 past 8 pairs per wavefront: no 16-slot kernel, two launches over the row halves)
     out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 8, splits, unroll, blocks)
     assert_parity(out, expected(x, p, s), f"mfma_pair chunked M={m} splits={splits} blocks={blocks} K={k}")
 
@@ -208,8 +211,9 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
 @pytest.mark.parametrize("m,k,n", [(3, 2048, 5632), (5, 4096, 4096), (7, 5632, 2048), (8, 8192, 1000),
                                    (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
                                    (5, 8320, 77),
-                                   # M = 9..16 with the selector: two launches over the row halves
-                                   (16, 5632, 2048), (9, 28672, 100), (13, 8192, 77)])
+                                   # M = 9..16 with the selector: one launch with 16 row slots, or two
+                                   # over the row halves where that shape has no 16-slot kernel
+                                   (16, 5632, 2048), (9, 28672, 100), (13, 8192, 77), (12, 2048, 11264)])
 def test_default_dispatch_mfma_pair(gpu, m, k, n, monkeypatch):
     if m > 8:
         monkeypatch.setenv("W4A16_DECODE", "mfma_pair")   # M = 9..16 defaults to the GEMM
@@ -227,12 +231,13 @@ def test_mfma_pair_more_pairs_than_needed(gpu, rows):
     assert_parity(out, expected(x, p, s), f"mfma_pair padded rows={rows}")
 
 
-@pytest.mark.parametrize("m", [9, 11, 16])
-def test_mfma_pair_two_halves_tuned(gpu, m):
-    # one launch shape for both halves (rows [0, ceil(m/2)) and the rest)
-    x, p, s = make_case(m, 2048, 300, seed=m)
-    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4, 0, 2)
-    assert_parity(out, expected(x, p, s), f"mfma_pair two halves M={m}")
+@pytest.mark.parametrize("m,k,splits", [(9, 2048, 4), (11, 2048, 4), (16, 2048, 4), (16, 20480, 8)])
+def test_mfma_pair_m9_16_tuned(gpu, m, k, splits):
+    # one launch with 16 row slots; rows past the 16-slot kernels (K = 20480:
+    # 10 pairs per wavefront) run as two launches over the row halves
+    x, p, s = make_case(m, k, 300, seed=m)
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, splits, 0, 2)
+    assert_parity(out, expected(x, p, s), f"mfma_pair M={m} K={k}")
 
 
 def test_mfma_pair_rejects(gpu):
@@ -458,6 +463,21 @@ def test_gemm_uses_dequantized_weights(gpu, m, k, n):
         assert torch.all((got - ref).abs() <= ulp * ref.abs() + 1e-4), (kernel, float((got - ref).abs().max()))
 
 
+@pytest.mark.parametrize("m,k,n", [(16, 2048, 512), (12, 5632, 96)])
+def test_mfma_pair_16_slots_uses_dequantized_weights(gpu, m, k, n):
+    """16 row slots (M = 9..16): B is fp16_rn(code * scale), bit-identical to
+    w4a16_dequantize_f16's weights, so the output is within one fp16
+    rounding of a float64 product with them."""
+    x, p, s = make_case(m, k, n, seed=m + n + 1)
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    wdq = torch.empty((n, k), dtype=torch.float16, device=gpu)
+    _lib.dequantize_f16(pd, sd, wdq, 128)
+    ref = (xd.double() @ wdq.double().t()).cpu()
+    ulp = torch.finfo(torch.float16).eps / 2
+    got = _run_tuned(gpu, x, p, s, MFMA_PAIR, 0, 4 if k <= 4096 else 8, 0, 1).double().cpu()
+    assert torch.all((got - ref).abs() <= ulp * ref.abs() + 1e-4), float((got - ref).abs().max())
+
+
 def test_gemm_rejects(gpu):
     x, p, s = make_case(32, 2048, 16, seed=3)
     xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
@@ -524,15 +544,23 @@ def test_stream_rejects(gpu):
     assert not out.any() and not out1.any()
 
 
-@pytest.mark.parametrize("kernel", ["gemm", "mfma_oneshot"])
-@pytest.mark.parametrize("m,k,n", [(9, 2048, 300), (16, 2048, 2048), (16, 4096, 64), (12, 256, 7), (16, 5632, 2048)])
-def test_default_dispatch_short_prompt(gpu, m, k, n, kernel, monkeypatch):
-    """M = 9..16: the GEMM by default, the one-shot MFMA kernel with its
-    selector (where its activations fit in LDS)."""
+@pytest.mark.parametrize("kernel", ["default", "mfma_oneshot"])
+@pytest.mark.parametrize("m,k,n,default", [(9, 2048, 300, "gemm"), (16, 2048, 2048, "gemm"),
+                                           (16, 4096, 64, "gemm"), (12, 256, 7, "gemm"),
+                                           (16, 5632, 2048, "mfma_pair"), (16, 2048, 2560, "gemm"),
+                                           (11, 5632, 2048, "mfma_pair"), (16, 4096, 14336, "gemm"),
+                                           (12, 2048, 11264, "mfma_pair"), (9, 14336, 4096, "mfma_pair")])
+def test_default_dispatch_short_prompt(gpu, m, k, n, default, kernel, monkeypatch):
+    """M = 9..16: the paired kernel in one launch (16 row slots) on rows
+    longer than 4096 weights and on layers of N >= 8192 with rows of up to
+    2048 (at most 256 workgroups), else the GEMM; the one-shot MFMA kernel
+    with its selector (where its activations fit in LDS)."""
     if kernel == "mfma_oneshot":
         if m * k * 2 > 100 * 1024:
             pytest.skip("activations past the one-shot MFMA kernel's LDS")
         monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
+    else:
+        kernel = default
     x, p, s = make_case(m, k, n, seed=m + k)
     assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == kernel
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"prompt M={m} K={k} N={n} {kernel}")
