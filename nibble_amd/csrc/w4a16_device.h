@@ -78,6 +78,14 @@ __device__ __forceinline__ f16x2 unpack_byte_pair(uint32_t u_offset) {
     return __builtin_elementwise_fma(as_f16x2(t), mul, bias);
 }
 
+// out = fp16(fp16(silu(fp16(g))) * fp16(u)) for fp32 sums g, u: the
+// roundings of silu(gate) * up on a GEMM's fp16 outputs.
+__device__ __forceinline__ f16 gemm_silu_mul(float g, float u) {
+    const float gh = (float)(f16)g;
+    const f16 sg = (f16)(gh / (1.0f + __expf(-gh)));
+    return (f16)((float)sg * (float)(f16)u);
+}
+
 // Activation permutation matching unpack8: 8 consecutive halves x0..x7 held
 // as words a=(x0,x1) b=(x2,x3) c=(x4,x5) e=(x6,x7) become
 // (x0,x4) (x1,x5) (x2,x6) (x3,x7).

@@ -59,12 +59,8 @@ struct GemmGroup {
 // output width `inter`, the packed weights hold 2 inter rows (gate rows, then
 // up rows), and a wavefront's RB weight tiles are RB / 2 gate tiles and the
 // up tiles of the same columns; out[m][n] = fp16(fp16(silu(fp16(g))) *
-// fp16(u)), the roundings of silu(gate) * up on the op's fp16 outputs.
-__device__ __forceinline__ f16 gemm_silu_mul(float g, float u) {
-    const float gh = (float)(f16)g;
-    const f16 sg = (f16)(gh / (1.0f + __expf(-gh)));
-    return (f16)((float)sg * (float)(f16)u);
-}
+// fp16(u)), the roundings of silu(gate) * up on the op's fp16 outputs
+// (gemm_silu_mul, w4a16_device.h).
 
 template <int MT, int RB, int SK, bool PAIRED = false>
 __global__ void __launch_bounds__(64 * SK)

@@ -25,6 +25,11 @@ bool mfma_pair_instantiated(int64_t M, int sk, int sn, int chunk, int gpw);
 int64_t mfma_pair_lds_bytes(int64_t M, int64_t K, int sk, int sn, int chunk, int gpw);
 int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, const uint8_t* w, const void* s,
                      void* o, int N, int K, hipStream_t stream);
+// its SiLU-multiply form for M = 9..16 (16 row slots, whole rows staged)
+int64_t mfma_pair_silu_lds_bytes(int64_t K, int sk, int sn, int gpw);
+bool mfma_pair_silu_instantiated(int sk, int sn, int gpw);
+int launch_mfma_pair_silu(int sk, int sn, int gpw, int M, const void* x, const uint8_t* w, const void* s, void* o,
+                          int inter, int K, hipStream_t stream);
 int64_t pair_stream_lds(int64_t M, int64_t K);
 bool pair_stream_instantiated(int depth);
 int pair_stream_waves(int64_t M, int64_t N, int64_t K);
@@ -1393,6 +1398,17 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
     }
     if (!w4a16_internal::gemm_fits(M, 2 * inter, K))
         return fail(W4A16_ERR_TOO_LARGE, "linear + SiLU: every operand must be below 4 GiB");
+    // M = 9..16 where the op takes the 16-row-slot paired kernel: its SiLU
+    // form, a gate and an up block per wavefront (half the plain plan's
+    // row-block wavefronts, so the same rows per workgroup)
+    if (pair16_route(M, 2 * inter, K)) {
+        const Plan q = plan_mfma_pair(M, 2 * inter, K);
+        const int sn = q.max_blocks > 1 ? q.max_blocks / 2 : 1;
+        if (q.rows == q.splits * q.unroll && w4a16_internal::mfma_pair_silu_instantiated(q.splits, sn, q.unroll) &&
+            w4a16_internal::mfma_pair_silu_lds_bytes(K, q.splits, sn, q.unroll) <= kMaxLdsBytes)
+            return w4a16_internal::launch_mfma_pair_silu(q.splits, sn, q.unroll, (int)M, activations, packed_weights,
+                                                         scales, output, (int)inter, (int)K, st);
+    }
     // the GEMM the op would run over the 2 inter rows, with an even number of weight tiles per wavefront
     Plan q3;
     if (plan_gemm32_silu(M, inter, K, &q3) &&

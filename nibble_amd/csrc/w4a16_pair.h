@@ -73,7 +73,7 @@ __host__ __device__ constexpr int64_t pair_lds_bytes(int64_t M, int64_t pairs, i
            waves * rb * 64 * 16;
 }
 
-template <int SK, int SN, int RB, int GPW, int MS, int C, int LA = 64, bool MB = false>
+template <int SK, int SN, int RB, int GPW, int MS, int C, int LA = 64, bool MB = false, bool SILU = false>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
                f16* __restrict__ out, int M, int N, int K) {
@@ -85,6 +85,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     static_assert(LA >= 1, "at least the first chunk is requested up front");
     static_assert(MS == 4 || MS == 8 || MS == 16, "4, 8 or 16 row slots");
     static_assert(MS != 16 || !MB, "16 row slots take the bias from the staging");
+    static_assert(!SILU || (MS == 16 && RB == 2), "the SiLU-multiply form pairs a gate block and its up block");
     constexpr bool W16 = MS == 16;   // M = 9..16: one activation group per MFMA, two MFMAs per step, exact decode
     constexpr int H = W16 ? 2 : 1;   // A fragment sets per step
     constexpr int NC = (P + C - 1) / C;        // chunks
@@ -103,7 +104,14 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     const int col = lane & 15, q = lane >> 4;
     const int brow = col & 7, bhalf = col >> 3;
     const int kw = wave % SK, nb = wave / SK;
-    const int n0 = (blockIdx.x * SN + nb) * RB * 8;
+    constexpr int RO = SILU ? 1 : RB;   // output blocks of 8 rows per wavefront
+    const int n0 = (blockIdx.x * SN + nb) * RO * 8;
+    // weight row of block b for this lane: SILU (N = inter, 2 inter weight
+    // rows) takes gate row n and up row inter + n of the same output column
+    auto wrow = [&](int b) -> int {
+        if constexpr (SILU) return (b ? N : 0) + min(n0 + brow, N - 1);
+        else return min(n0 + 8 * b + brow, N - 1);
+    };
     const uint32_t row_bytes = (uint32_t)(K >> 1);
     const int upr = K >> 3;                    // 16-byte units per activation row
     auto group = [&](int j, int h) { return 2 * (kw + SK * j) + h; };
@@ -176,7 +184,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             if (j < GPW) {
 #pragma unroll
                 for (int b = 0; b < RB; ++b) {
-                    const int n = min(n0 + 8 * b + brow, N - 1);
+                    const int n = wrow(b);
                     sv[j][b] = sbase[(size_t)n * G + min(group(j, bhalf), G - 1)];
                 }
             }
@@ -187,7 +195,7 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
             if (j < GPW) {
 #pragma unroll
                 for (int b = 0; b < RB; ++b) {
-                    const int n = min(n0 + 8 * b + brow, N - 1);
+                    const int n = wrow(b);
                     wv[j][b] = load_stream(reinterpret_cast<const u32x4*>(
                         w + (size_t)n * row_bytes + (uint32_t)min(group(j, bhalf), G - 1) * 64u + q * 16));
                 }
@@ -313,17 +321,21 @@ gemv_mfma_pair(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     for (int b = 0; b < RB; ++b) red[(wave * RB + b) * 64 + lane] = acc[b];
     __syncthreads();
     if (kw != 0 || (!W16 && q >= 2) || col >= 8) return;
+    f32x4 v[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
-        f32x4 v = acc[b] + red[(wave * RB + b) * 64 + lane + HALF];
+        v[b] = acc[b] + red[(wave * RB + b) * 64 + lane + HALF];
 #pragma unroll
         for (int s2 = 1; s2 < SK; ++s2)
-            v += red[((wave + s2) * RB + b) * 64 + lane] + red[((wave + s2) * RB + b) * 64 + lane + HALF];
+            v[b] += red[((wave + s2) * RB + b) * 64 + lane] + red[((wave + s2) * RB + b) * 64 + lane + HALF];
+    }
+#pragma unroll
+    for (int b = 0; b < RO; ++b) {
         const int nn = n0 + 8 * b + col;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int m = q * 4 + e;
-            if (m < M && nn < N) out[(size_t)m * N + nn] = (f16)v[e];
+            if (m < M && nn < N) out[(size_t)m * N + nn] = SILU ? gemm_silu_mul(v[0][e], v[1][e]) : (f16)v[b][e];
         }
     }
 }

@@ -186,6 +186,70 @@ int launch_mfma_pair(int sk, int sn, int chunk, int gpw, int M, const void* x, c
     return W4A16_OK;
 }
 
+// SiLU-multiply form of the 16-row-slot paired kernel (M = 9..16): each
+// wavefront takes a block of 8 gate rows and the 8 up rows of the same
+// output columns (inter + n), whole rows staged; out[m][n] = fp16(fp16(
+// silu(fp16(g))) * fp16(u)). Instantiated: (sk, sn) in (2, 2), (2, 4),
+// (4, 1), (4, 2), (8, 1), (8, 2), 1..8 pairs per wavefront.
+namespace {
+Kern pick_silu(int sk, int sn, int gpw) {
+    using namespace w4a16;
+#define W4A16_S(SK, SN)                                                                                        \
+    if (sk == SK && sn == SN) {                                                                                \
+        switch (gpw) {                                                                                         \
+            case 1: return gemv_mfma_pair<SK, SN, 2, 1, 16, SK * 1, 64, false, true>;                          \
+            case 2: return gemv_mfma_pair<SK, SN, 2, 2, 16, SK * 2, 64, false, true>;                          \
+            case 3: return gemv_mfma_pair<SK, SN, 2, 3, 16, SK * 3, 64, false, true>;                          \
+            case 4: return gemv_mfma_pair<SK, SN, 2, 4, 16, SK * 4, 64, false, true>;                          \
+            case 5: return gemv_mfma_pair<SK, SN, 2, 5, 16, SK * 5, 64, false, true>;                          \
+            case 6: return gemv_mfma_pair<SK, SN, 2, 6, 16, SK * 6, 64, false, true>;                          \
+            case 7: return gemv_mfma_pair<SK, SN, 2, 7, 16, SK * 7, 64, false, true>;                          \
+            case 8: return gemv_mfma_pair<SK, SN, 2, 8, 16, SK * 8, 64, false, true>;                          \
+            default: return nullptr;                                                                           \
+        }                                                                                                      \
+    }
+    W4A16_S(2, 2) W4A16_S(2, 4) W4A16_S(4, 1) W4A16_S(4, 2) W4A16_S(8, 1) W4A16_S(8, 2)
+#undef W4A16_S
+    return nullptr;
+}
+}  // namespace
+
+int64_t mfma_pair_silu_lds_bytes(int64_t K, int sk, int sn, int gpw) {
+    (void)K;
+    const int64_t pairs = (int64_t)sk * gpw;
+    return w4a16::pair_lds_bytes(16, pairs, pairs, (int64_t)sk * sn, 2);
+}
+
+bool mfma_pair_silu_instantiated(int sk, int sn, int gpw) { return pick_silu(sk, sn, gpw) != nullptr; }
+
+// out [M, inter] = silu(x W_gate^T) * (x W_up^T) over the packed [gate; up]
+// rows; M = 9..16. The caller has checked pointers, group size 128 and
+// 16-byte alignment.
+int launch_mfma_pair_silu(int sk, int sn, int gpw, int M, const void* x, const uint8_t* w, const void* s, void* o,
+                          int inter, int K, hipStream_t stream) {
+    if (M < 9 || M > 16) return fail(W4A16_ERR_CONFIG, "paired SiLU kernel needs 9 <= M <= 16");
+    if (K < 128 || K % 128 != 0) return fail(W4A16_ERR_CONFIG, "paired SiLU kernel: K must be a positive multiple of 128");
+    const int pairs = (K / 128 + 1) / 2;
+    if (gpw < 1 || (int64_t)sk * gpw < pairs)
+        return fail(W4A16_ERR_CONFIG, "paired SiLU kernel: splits * unroll must cover the K / 256 group pairs");
+    const Kern kern = pick_silu(sk, sn, gpw);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "paired SiLU kernel: no instantiation for this shape");
+    const int64_t lds = mfma_pair_silu_lds_bytes(K, sk, sn, gpw);
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired SiLU kernel: activations do not fit in LDS");
+    const int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int cols = 8 * sn;   // output columns per workgroup
+    hipLaunchKernelGGL(kern, dim3((inter + cols - 1) / cols), dim3(64 * sk * sn), (size_t)lds, stream,
+                       static_cast<const w4a16::f16*>(x), w, static_cast<const w4a16::f16*>(s),
+                       static_cast<w4a16::f16*>(o), M, inter, K);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));
+        return W4A16_ERR_LAUNCH;
+    }
+    return W4A16_OK;
+}
+
 // Streaming paired kernel (gemv_pair_stream): whole rows staged once per
 // workgroup. depth = pairs in flight per wavefront (2, 3, 4 or 6); waves =
 // wavefronts per workgroup (0: the fewest that cover the 8-row blocks with

@@ -105,10 +105,11 @@ def test_silu_mul(gpu, rows, inter):
     assert torch.all((got - torch_ref).abs() <= 2 * ULP * torch_ref.abs() + 2 ** -20)
 
 
-@pytest.mark.parametrize("m,k,inter", [(1, 2048, 5632), (2, 2048, 5632), (16, 2048, 5632), (64, 2048, 5632),
+@pytest.mark.parametrize("m,k,inter", [(1, 2048, 5632), (2, 2048, 5632), (16, 2048, 5632), (9, 2048, 5000),
+                                       (13, 5632, 1000), (12, 2048, 4100), (64, 2048, 5632),
                                        (37, 1152, 100), (1, 20480, 64), (130, 4096, 257), (256, 2048, 5632),
                                        (128, 5632, 2100)])
-def test_linear_silu(gpu, m, k, inter):
+def test_linear_silu(gpu, m, k, inter, monkeypatch):
     """w4a16_linear_silu_f16 against the op over the 2 inter rows followed by
     SiLU * up: bit-identical to the same GEMM shape (or, at M = 1 with K <=
     16384, to the paired fused GEMV), and within the parity bar of the oracle's
@@ -128,6 +129,11 @@ def test_linear_silu(gpu, m, k, inter):
     else:
         # the same GEMM over the 2 inter rows (the op's shape), then SiLU * up
         plan = _lib.plan_linear(1 << 20, 1 << 20, m, 2 * inter, k, 128)
+        if plan["kernel"] == "mfma_pair" and m > 8 and plan["rows"] != plan["splits"] * plan["unroll"]:
+            # the SiLU form of the 16-slot kernel stages whole rows only; else the GEMM
+            monkeypatch.setenv("W4A16_DECODE", "valu")   # off the paired route (M <= 8 selector)
+            plan = _lib.plan_linear(1 << 20, 1 << 20, m, 2 * inter, k, 128)
+            monkeypatch.delenv("W4A16_DECODE")
         # the SiLU form of the 32x32 kernel: the first of 128, 64, 32 output
         # columns per workgroup (K split 1, 2, 4 ways) with >= 160 workgroups;
         # the plain 32x32 GEMM with the same K split sums in the same order
@@ -140,6 +146,10 @@ def test_linear_silu(gpu, m, k, inter):
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM_LDS, 4, plan["splits"], plan["unroll"], 2)
         elif plan["kernel"] == "gemm":
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM, plan["rows"], plan["splits"], 0, 2)
+        elif plan["kernel"] == "mfma_pair" and m > 8:
+            # M = 9..16: the 16-row-slot paired kernel; its SiLU form takes a gate
+            # and an up block per wavefront with the same K split, same sums
+            _lib.linear_f16(xd, pd, sd, gu)
         else:   # M = 1, K > 16384: the op runs a GEMV; compare with the GEMM at 1 activation tile
             _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_GEMM, 1, 4, 0, 2)
         ref = torch.empty_like(out)
