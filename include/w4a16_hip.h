@@ -58,8 +58,10 @@ extern "C" {
  * scales: fp16 [N, K/group_size]; output: fp16 [M, N].
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
  * takes the tuned kernels and M > 8 the W4A16 GEMM (operands below 4 GiB;
- * its LDS-staged form from M = 128; W4A16_DECODE = mfma_oneshot or mfma_pair
- * selects those kernels for M = 9..16); anything else takes the generic
+ * its LDS-staged forms from M = 64; M = 9..16 on rows longer than 4096
+ * weights, or N >= 8192 with rows of up to 2048, the paired kernel with 16
+ * row slots; W4A16_DECODE = mfma_oneshot or mfma_pair selects those kernels
+ * for M = 9..16); anything else takes the generic
  * kernel (the reference routes every M > 8 to its naive kernel).
  * Environment, read at every call, with the reference's semantics
  * (csrc/int4_linear_kernel.cu:459-491, :713-749):
@@ -185,9 +187,10 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     splitting K (4|8), unroll = groups per wavefront (0 = ceil(K / 128 /
  *     splits); else enough to cover K: 1..8, 10, 12, 14, 16 with 4 splits,
  *     1..8 with 8), max_blocks ignored.
- *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 16, K <= 32768; M > 8 runs as two
- *     launches over rows [0, ceil(M/2)) and the rest, each choosing its
- *     own staging chunk, rows ignored): splits = wavefronts
+ *   W4A16_KERNEL_MFMA_PAIR (2 <= M <= 16, K <= 32768; M > 8 runs in one
+ *     launch with 16 row slots where that shape is instantiated and fits in
+ *     LDS, else as two launches over rows [0, ceil(M/2)) and the rest, each
+ *     choosing its own staging chunk, rows ignored): splits = wavefronts
  *     splitting the K / 256 group pairs (2|4|8), max_blocks = 8-row-block
  *     wavefronts per workgroup (1|2|4|8, splits * max_blocks <= 16), unroll =
  *     group pairs per wavefront (0 = ceil(K / 256 / splits); else with
