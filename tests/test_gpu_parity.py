@@ -171,13 +171,11 @@ def _pair_lds(m, staged, chunk, splits, blocks):
 @pytest.mark.parametrize("splits,blocks", [(2, 1), (4, 2), (8, 1), (2, 8), (4, 4), (8, 2)])
 @pytest.mark.parametrize("k,n", [(128, 7), (384, 9), (1152, 33), (2048, 2048), (3968, 21), (5632, 100),
                                  (8192, 64), (16384, 24)])
-@pytest.mark.parametrize("m", [2, 3, 4, 6, 8, 9, 13, 16])
+@pytest.mark.parametrize("m", [2, 3, 4, 6, 8])
 def test_mfma_pair_whole(gpu, m, splits, blocks, k, n):
     pairs = (k // 128 + 1) // 2
     unroll = -(-pairs // splits)
     staged = splits * unroll
-    if m > 8 and (unroll > 8 or _pair_lds(m, staged, staged, splits, blocks) > 160 * 1024):
-        pytest.skip("no 16-slot kernel for this shape (test_mfma_pair_m9_16_tuned covers the row-halves path)")
     if unroll > 8 or _pair_lds(m, staged, staged, splits, blocks) > 160 * 1024:
         x, p, s = make_case(m, k, n, seed=1)
         with pytest.raises(_lib.W4A16Error, match="no instantiation|do not fit in LDS"):
@@ -186,6 +184,22 @@ def test_mfma_pair_whole(gpu, m, splits, blocks, k, n):
     x, p, s = make_case(m, k, n, seed=m * 17 + k + n)
     out = _run_tuned(gpu, x, p, s, MFMA_PAIR, staged, splits, unroll, blocks)
     assert_parity(out, expected(x, p, s), f"mfma_pair M={m} splits={splits} blocks={blocks} K={k} N={n}")
+
+
+# 16 row slots (M = 9..16), whole rows: every (splits, blocks) class on rows
+# up to 16 pairs (what LDS holds at 16 slots), odd group counts, padding
+# pairs, ragged N
+@pytest.mark.parametrize("splits,blocks", [(2, 1), (4, 2), (8, 1), (2, 8), (4, 4), (8, 2)])
+@pytest.mark.parametrize("k,n", [(128, 7), (384, 9), (1152, 33), (2048, 2048), (3968, 21)])
+@pytest.mark.parametrize("m", [9, 13, 16])
+def test_mfma_pair_whole_16_slots(gpu, m, splits, blocks, k, n):
+    pairs = (k // 128 + 1) // 2
+    unroll = -(-pairs // splits)
+    staged = splits * unroll
+    assert _pair_lds(m, staged, staged, splits, blocks) <= 160 * 1024
+    x, p, s = make_case(m, k, n, seed=m * 19 + k + n)
+    out = _run_tuned(gpu, x, p, s, MFMA_PAIR, staged, splits, unroll, blocks)
+    assert_parity(out, expected(x, p, s), f"mfma_pair 16 slots M={m} splits={splits} blocks={blocks} K={k} N={n}")
 
 
 # chunked staging (rows = 8 pairs per chunk, two buffers): every
