@@ -968,12 +968,16 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
 }
 
 
-// Prefill attention on the matrix cores, for the two-launch path (more than
-// kPrefillOneLaunch tokens; the rotary k and the v rows of the new tokens are
-// already in the caches) when the query heads per KV head, group, are a power
-// of two up to 64. Workgroup (hk, b) of 4 wavefronts takes KV head hk and the
-// 64 / group tokens t = b 64 / group .. of all its group query heads: 64 query
-// columns, column c = token offset * group + head offset, wavefront w owning
+// Prefill attention on the matrix cores, for any prompt length, when the
+// query heads per KV head, group, are a power of two up to 64 and qkv and the
+// rotary tables are 16-byte aligned. The launcher runs the FUSED form: slots
+// below start come from the caches, the new tokens' rotary k and v rows are
+// computed from qkv by every workgroup that sees them and appended to the
+// caches by the workgroup that owns the token (FUSED = false reads every slot
+// from the caches, for callers that appended them beforehand).
+// Workgroup (hk, b) of 4 wavefronts takes KV head hk and the 64 / group tokens
+// t = b 64 / group .. of all its group query heads: 64 query columns, column
+// c = token offset * group + head offset, wavefront w owning
 // columns 16 w .. 16 w + 15. It stages the k and v rows of every slot its last
 // token sees once (shared by the 64 columns, where the one-query kernel above
 // restages them per head and per 4 queries), then each wavefront walks the
