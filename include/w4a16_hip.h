@@ -178,7 +178,8 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *   W4A16_KERNEL_DIAG (M = 1 only): rows = output rows per wavefront task
  *     (1|2|4), splits = wavefronts per workgroup (1..4), unroll = 1 KiB spans
  *     in flight per row (1|2|4; 4 needs rows <= 2), max_blocks = grid cap.
- *   W4A16_KERNEL_ONESHOT (M <= 4): rows = output rows per wavefront (1|2),
+ *   W4A16_KERNEL_ONESHOT (M <= 4): rows = output rows per wavefront (1|2; 4
+ *     at M = 1 with splits 4 and unroll <= 8),
  *     splits = wavefronts per workgroup (4|8), unroll = 1 KiB loads per row
  *     per lane (0 = the smallest that covers K; else >= ceil(K / 2048) and
  *     one of 1..8, 10, 12, 14, 16), max_blocks ignored.

@@ -215,20 +215,50 @@ int oneshot_loads(int64_t K) {
 }
 
 // Launch shape of the one-shot kernel, from the M = 1..4 sweeps over the
-// benchmark shapes (offset decode): at M = 1, two rows per wavefront and 4
-// wavefronts per workgroup when a row is 2 or >= 12 loads (K 4096, 28672),
-// else one row and 8 wavefronts; M >= 2 always one row and 8 wavefronts
-// (more rows per workgroup share each staged copy of the activations).
-Plan plan_oneshot(int64_t M, int64_t K, int rows) {
+// benchmark shapes (offset decode) and an M = 1 sweep of wide layers
+// (graph timing, every shape timed twice in interleaved passes):
+//   M = 1, rows of one load (K <= 2048): one row and 8 wavefronts per
+//     workgroup up to N = 8192 (2048 x 8192: 3.85 against 3.98 us with 2
+//     rows), 2 rows and 4 wavefronts above (2048 x 11264: 4.54 against 4.78
+//     us; 2048 x 16384: 5.31 against 5.92), 4 rows and 4 wavefronts from
+//     N = 24576 (2048 x 32000, the lm_head of the 1.1B model: 7.78 against
+//     9.26 us; 2 rows 8.46);
+//   M = 1, rows of 2 loads (K 4096): 2 rows, 8 wavefronts up to N = 8192
+//     (4096 x 4096: 3.85 against 4.10 us with 4; 4096 x 8192: 5.14 against
+//     5.30), else 4 (4096 x 14336: 7.14 against 7.19);
+//   M = 1, rows of 12 or more loads (K 28672): 2 rows and 4 wavefronts;
+//   otherwise one row and 8 wavefronts (M >= 2: more rows per workgroup
+//   share each staged copy of the activations).
+// An explicit row count (W4A16_ROWS_PER_WARP) keeps the wavefront count,
+// except 4 rows, which run with 4 wavefronts at M = 1 on rows of up to 8
+// loads and as 2 rows elsewhere.
+Plan plan_oneshot(int64_t M, int64_t N, int64_t K, int rows) {
     Plan p;
     p.kernel = W4A16_KERNEL_ONESHOT;
     p.unroll = oneshot_loads(K);
-    const bool pair = M == 1 && (p.unroll == 2 || p.unroll >= 12);
-    if (rows > 0)
-        p.rows = rows >= 2 ? 2 : 1;   // W4A16_ROWS_PER_WARP=4 runs as 2 rows in this kernel
-    else
-        p.rows = pair ? 2 : 1;
-    p.splits = pair ? 4 : 8;
+    int r = 1, w = 8;
+    if (M == 1) {
+        if (p.unroll == 1 && N >= 24576) {
+            r = 4;
+            w = 4;
+        } else if (p.unroll == 1 && N > 8192) {
+            r = 2;
+            w = 4;
+        } else if (p.unroll == 2) {
+            r = 2;
+            w = N <= 8192 ? 8 : 4;
+        } else if (p.unroll >= 12) {
+            r = 2;
+            w = 4;
+        }
+    }
+    if (rows > 0) {
+        const bool four = rows >= 4 && M == 1 && p.unroll <= 8;
+        r = four ? 4 : rows >= 2 ? 2 : 1;
+        if (four) w = 4;
+    }
+    p.rows = r;
+    p.splits = w;
     return p;
 }
 
@@ -780,7 +810,7 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     if (family == W4A16_KERNEL_VALU_OFFSET && M != 1) family = W4A16_KERNEL_VALU;
     if (family == W4A16_KERNEL_ONESHOT) {
         if (oneshot_fits(M, K)) {
-            *out = plan_oneshot(M, K, rows);
+            *out = plan_oneshot(M, N, K, rows);
             return W4A16_OK;
         }
         family = M <= 8 ? W4A16_KERNEL_VALU : W4A16_KERNEL_MFMA;   // rows too long or M > 4
@@ -853,11 +883,18 @@ int launch_oneshot_m(const Plan& p, const w4a16::f16* x, const uint8_t* w, const
     W4A16_PICK_L(R, 5, W) W4A16_PICK_L(R, 6, W) W4A16_PICK_L(R, 7, W) W4A16_PICK_L(R, 8, W)             \
     W4A16_PICK_L(R, 10, W) W4A16_PICK_L(R, 12, W) W4A16_PICK_L(R, 14, W) W4A16_PICK_L(R, 16, W)
     W4A16_PICK(1, 4) W4A16_PICK(1, 8) W4A16_PICK(2, 4) W4A16_PICK(2, 8)
+    if constexpr (M == 1) {
+        // 4 rows per wavefront (wide layers of short rows): 4 wavefronts,
+        // rows of up to 8 loads
+        W4A16_PICK_L(4, 1, 4) W4A16_PICK_L(4, 2, 4) W4A16_PICK_L(4, 3, 4) W4A16_PICK_L(4, 4, 4)
+        W4A16_PICK_L(4, 5, 4) W4A16_PICK_L(4, 6, 4) W4A16_PICK_L(4, 7, 4) W4A16_PICK_L(4, 8, 4)
+    }
 #undef W4A16_PICK
 #undef W4A16_PICK_L
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
-                    "one-shot kernel: rows 1 or 2, splits 4 or 8, unroll one of 1..8, 10, 12, 14, 16");
+                    "one-shot kernel: rows 1 or 2 (or 4 with splits 4 at M = 1 and unroll <= 8), splits 4 or 8, "
+                    "unroll one of 1..8, 10, 12, 14, 16");
     const int lds = (int)oneshot_lds_bytes(M, K, false);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "one-shot kernel: M*K activations do not fit in LDS");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), lds);

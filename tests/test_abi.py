@@ -297,12 +297,23 @@ def test_mfma_oneshot_plan_shapes(monkeypatch):
 def test_oneshot_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
-    # (K, rows, waves per workgroup, loads per row)
-    for k, rows, splits, loads in [(2048, 1, 8, 1), (4096, 2, 4, 2), (5632, 1, 8, 3), (8192, 1, 8, 4),
+    # (K, rows, waves per workgroup, loads per row) on a narrow layer
+    for k, rows, splits, loads in [(2048, 1, 8, 1), (4096, 2, 8, 2), (5632, 1, 8, 3), (8192, 1, 8, 4),
                                    (14336, 1, 8, 7), (18432, 1, 8, 10), (28672, 2, 4, 14), (32768, 2, 4, 16),
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
+    # wide layers: more rows per wavefront on short rows above N = 8192; rows
+    # of 2 loads take 4 wavefronts above N = 8192
+    for k, n, rows, splits, loads in [(2048, 5632, 1, 8, 1), (2048, 8192, 1, 8, 1), (2048, 8193, 2, 4, 1),
+                                      (2048, 16384, 2, 4, 1), (2048, 24575, 2, 4, 1), (2048, 24576, 4, 4, 1),
+                                      (2048, 32000, 4, 4, 1), (1024, 32000, 4, 4, 1), (4096, 4096, 2, 8, 2),
+                                      (4096, 8192, 2, 8, 2), (4096, 8193, 2, 4, 2), (4096, 14336, 2, 4, 2),
+                                      (4096, 32000, 2, 4, 2), (8192, 32000, 1, 8, 4)]:
+        plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
+        assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
+            ("oneshot", rows, splits, loads), (k, n)
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 32000, 2048, 128)["rows"] == 1   # M = 2: one row per wavefront
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 34816, 128)["kernel"] == "mfma"     # M > 2, long rows
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")
@@ -310,7 +321,13 @@ def test_oneshot_plan_shapes(monkeypatch):
     assert _lib.plan_linear(ALIGNED, ALIGNED, 5, 64, 2048, 128)["kernel"] == "valu"     # M > 4
     assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 64, 32768, 128)["kernel"] == "mfma"    # no LDS room: MFMA
     monkeypatch.setenv("W4A16_ROWS_PER_WARP", "4")
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["rows"] == 2
+    # 4 rows (with 4 wavefronts) on rows of up to 8 loads, else 2
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    assert (plan["rows"], plan["splits"]) == (4, 4)
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 18432, 128)["rows"] == 2
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)
+    assert (plan["rows"], plan["splits"]) == (2, 8)
 
 
 def test_env_selectors(monkeypatch):

@@ -141,6 +141,37 @@ def test_oneshot_variants(gpu, m, rows, splits, k, n):
     assert_parity(out, expected(x, p, s), f"oneshot M={m} rows={rows} splits={splits} K={k} N={n}")
 
 
+# 4 rows per wavefront (M = 1, 4 wavefronts): rows of one partial load up to
+# 8 loads (16384), N not a multiple of 4 (the last wavefront's rows clamp)
+@pytest.mark.parametrize("k,n", [(256, 7), (2048, 13), (2048, 2050), (5632, 41), (14336, 22), (16384, 9)])
+def test_oneshot_four_rows(gpu, k, n):
+    x, p, s = make_case(1, k, n, seed=k + n)
+    out = _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
+    assert_parity(out, expected(x, p, s), f"oneshot rows=4 K={k} N={n}")
+
+
+def test_oneshot_four_rows_all_nibbles_and_rejects(gpu):
+    x, p, s = make_case(1, 1024, 66, seed=12, all_nibbles=True)
+    assert_parity(_run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0), expected(x, p, s), "oneshot rows=4 all nibbles")
+    x, p, s = make_case(1, 18432, 8, seed=13)   # 10 loads per row
+    with pytest.raises(_lib.W4A16Error, match="rows 1 or 2"):
+        _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
+    x, p, s = make_case(2, 2048, 8, seed=14)    # M = 2
+    with pytest.raises(_lib.W4A16Error, match="rows 1 or 2"):
+        _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
+
+
+# the M = 1 default on wide layers of short rows (2 and 4 rows per
+# wavefront) and on 4096 x 4096 (2 rows, 8 wavefronts), at full size
+@pytest.mark.parametrize("k,n,rows,splits", [(2048, 32000, 4, 4), (2048, 16384, 2, 4), (2048, 11264, 2, 4),
+                                             (4096, 4096, 2, 8), (1024, 24577, 4, 4)])
+def test_default_dispatch_wide_m1(gpu, k, n, rows, splits):
+    x, p, s = make_case(1, k, n, seed=k ^ n)
+    plan = _lib.plan_linear(16, 16, 1, n, k)
+    assert (plan["kernel"], plan["rows"], plan["splits"]) == ("oneshot", rows, splits)
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default")
+
+
 # one-shot MFMA: every (rows, splits) shape, K from one group to 32 groups
 # (partial last step when splits do not divide K / 128), ragged N
 @pytest.mark.parametrize("rows,splits", [(1, 4), (2, 4), (1, 8), (2, 8)])
@@ -604,7 +635,7 @@ def test_oneshot_rejects_short_unroll_and_long_rows(gpu):
     with pytest.raises(_lib.W4A16Error, match="too small"):
         _run_tuned(gpu, x, p, s, ONESHOT, 1, 4, 1)
     with pytest.raises(_lib.W4A16Error, match="rows 1 or 2"):
-        _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
+        _run_tuned(gpu, x, p, s, ONESHOT, 4, 8, 0)   # 4 rows run with 4 wavefronts only
     x, p, s = make_case(1, 34816, 3, seed=4)
     with pytest.raises(_lib.W4A16Error, match="K > 32768"):
         _run_tuned(gpu, x, p, s, ONESHOT, 1, 8, 0)
