@@ -744,7 +744,18 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
     // keeps auto on the looped VALU kernel whose rows it sets.
     // Measured routing (M = 1..8 sweeps over the benchmark shapes):
     //   M = 1: streaming VALU for long rows of wide layers (K >= 14336,
-    //   N >= 4096), else one-shot VALU;  M = 2: one-shot VALU up to K = 5632;
+    //   N >= 4096), else one-shot VALU;
+    //   M = 2 (a K x N grid of 2048..28672 x 2048..28672, graph timing, two
+    //   interleaved passes): the streaming paired kernel on wide layers of
+    //   rows above 4096 weights (N >= 14336; 11008 x 28672 38.8 against 55.4
+    //   us on the looped VALU kernel, 5632 x 14336 11.2 against 13.6 on the
+    //   one-shot), the paired kernel on rows above 6144 weights (28672 x 2048
+    //   11.4 against 24.4 on the looped MFMA kernel, 8192 x 8192 9.9 against
+    //   13.0, 7168 x 4096 6.2 against 7.5 on the one-shot) and on wide layers
+    //   of rows up to 4096 (N >= 8192; 2048 x 32000 9.5 against 11.8, 4096 x
+    //   14336 9.5 against 10.2), else the one-shot VALU kernel (rows of up to
+    //   three 1 KiB loads, 6144 weights; the paired kernel lost there, 5632 x
+    //   8192 10.5 against 8.7, 6144 x 8192 10.5 against 8.9);
     //   M >= 3: the streaming paired kernel on wide layers (N >= 14336,
     //   K >= 4096) whose M*K activations fit in LDS, else the paired-group
     //   MFMA kernel up to K = 32768 (activations staged whole or in chunks);
@@ -763,7 +774,11 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         const bool small = K <= 5632 && N <= 5632;
         if (rows == 0 && M == 1 && K >= kStreamMinK && N >= kStreamMinN && stream_fits(K))
             family = W4A16_KERNEL_STREAM;
-        else if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 5632)))
+        else if (M == 2 && K > 4096 && N >= kPairStreamMinN && pair_stream_fits(M, K))
+            family = W4A16_KERNEL_PAIR_STREAM;
+        else if (M == 2 && ((K <= 4096 && N >= 8192) || K > 6144) && mfma_pair_fits(M, N, K))
+            family = W4A16_KERNEL_MFMA_PAIR;
+        else if (rows == 0 && oneshot_fits(M, K) && (M == 1 || (M == 2 && K <= 6144)))
             family = W4A16_KERNEL_ONESHOT;
         else if (rows == 0 && M >= 3 && N >= kPairStreamMinN && K >= kPairStreamMinK && pair_stream_fits(M, K))
             family = W4A16_KERNEL_PAIR_STREAM;

@@ -117,8 +117,8 @@ ALIGNED = 1 << 20
         (3, 2048, 128, ALIGNED, "mfma_pair"),  # M >= 3: paired-group MFMA wherever M*K fits in LDS
         (4, 2048, 128, ALIGNED, "mfma_pair"),
         (4, 5632, 128, ALIGNED, "mfma_pair"),
-        (2, 8192, 128, ALIGNED, "valu"),       # small batch, VALU side of the crossover
-        (2, 28672, 128, ALIGNED, "mfma"),      # very long rows
+        (2, 8192, 128, ALIGNED, "mfma_pair"),  # M = 2, rows above 6144 weights: the paired kernel
+        (2, 28672, 128, ALIGNED, "mfma_pair"),
         (4, 8192, 128, ALIGNED, "mfma_pair"),
         (8, 8192, 128, ALIGNED, "mfma_pair"),
         (8, 8320, 128, ALIGNED, "mfma_pair"),      # rows past LDS: staged in chunks
@@ -191,7 +191,8 @@ def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
     (8, 28672, 8192, "pair_stream", 16), (4, 28672, 8192, "pair_stream", 16), (8, 14336, 4096, "pair_stream", 8),
     (3, 14336, 4096, "pair_stream", 8), (4, 14336, 14336, "pair_stream", 8),
     (8, 14336, 14336, "mfma_pair", 0),    # 8 x 14336 activations do not fit in LDS
-    (8, 8192, 8192, "mfma_pair", 0), (8, 14336, 2048, "mfma_pair", 0), (2, 28672, 8192, "valu", 0),
+    (8, 8192, 8192, "mfma_pair", 0), (8, 14336, 2048, "mfma_pair", 0), (2, 28672, 8192, "pair_stream", 16),
+    (2, 14336, 4096, "mfma_pair", 0),     # M = 2 streams only rows above 4096 weights
 ])
 def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
     """M >= 3 on wide layers (N >= 14336, K >= 4096) whose activations fit
@@ -294,6 +295,25 @@ def test_mfma_oneshot_plan_shapes(monkeypatch):
     assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 64, 8320, 128)["kernel"] == "mfma"   # rows too long
 
 
+def test_m2_routing(monkeypatch):
+    """M = 2: the paired kernel on wide layers of rows up to 4096 weights and
+    on rows above 6144, the streaming paired kernel on wide layers of rows
+    above 4096, else the one-shot kernel."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    for k, n, kernel in [(2048, 2048, "oneshot"), (2048, 5632, "oneshot"), (5632, 2048, "oneshot"),
+                         (2048, 8191, "oneshot"), (2048, 8192, "mfma_pair"), (2048, 32000, "mfma_pair"),
+                         (4096, 4096, "oneshot"), (4096, 14336, "mfma_pair"), (4096, 28672, "mfma_pair"),
+                         (5632, 8192, "oneshot"), (6144, 8192, "oneshot"), (6272, 4096, "mfma_pair"),
+                         (5632, 14336, "pair_stream"), (8192, 8192, "mfma_pair"),
+                         (8192, 14336, "pair_stream"), (14336, 4096, "mfma_pair"), (28672, 2048, "mfma_pair"),
+                         (28672, 28672, "mfma_pair"),   # 2 x 28672 activations past the streaming kernel's LDS
+                         (34816, 64, "mfma")]:
+        assert _lib.plan_linear(ALIGNED, ALIGNED, 2, n, k, 128)["kernel"] == kernel, (k, n)
+    monkeypatch.setenv("W4A16_DECODE", "oneshot")   # an explicit family keeps its kernel
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 32000, 2048, 128)["kernel"] == "oneshot"
+
+
 def test_oneshot_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
@@ -313,7 +333,8 @@ def test_oneshot_plan_shapes(monkeypatch):
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
             ("oneshot", rows, splits, loads), (k, n)
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 32000, 2048, 128)["rows"] == 1   # M = 2: one row per wavefront
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 2, 5632, 2048, 128)   # M = 2: one row per wavefront
+    assert (plan["kernel"], plan["rows"], plan["splits"]) == ("oneshot", 1, 8)
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 34816, 128)["kernel"] == "mfma"     # M > 2, long rows
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")

@@ -172,6 +172,19 @@ def test_default_dispatch_wide_m1(gpu, k, n, rows, splits):
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default")
 
 
+# M = 2 through the default route on the paired kernel (wide layers of short
+# rows, rows above 6144 weights), the streaming paired kernel (wide layers of
+# longer rows) and the one-shot kernel (rows of up to 6144), at full size
+@pytest.mark.parametrize("k,n,kernel", [(2048, 32000, "mfma_pair"), (4096, 14336, "mfma_pair"),
+                                        (5632, 14336, "pair_stream"), (8192, 8192, "mfma_pair"),
+                                        (7168, 4096, "mfma_pair"), (6144, 4096, "oneshot"),
+                                        (28672, 2048, "mfma_pair"), (11008, 28672, "pair_stream")])
+def test_default_dispatch_m2(gpu, k, n, kernel):
+    x, p, s = make_case(2, k, n, seed=k + 3 * n)
+    assert _lib.plan_linear(16, 16, 2, n, k)["kernel"] == kernel
+    assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=2 K={k} N={n} default")
+
+
 # one-shot MFMA: every (rows, splits) shape, K from one group to 32 groups
 # (partial last step when splits do not divide K / 128), ragged N
 @pytest.mark.parametrize("rows,splits", [(1, 4), (2, 4), (1, 8), (2, 8)])
