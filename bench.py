@@ -395,9 +395,10 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
         "prefill_ms": round(prefill * 1e3, 3),
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),
         "prefill": "16-token prompt, one HIP graph: RMSNorm of the embeddings, then per layer W4A16 op for "
-                   "q|k|v (the W4A16 GEMM, M=16), rotary+KV append+causal attention, W4A16 op for o, "
-                   "residual add+RMSNorm, W4A16 GEMM for gate|up with the SiLU*up epilogue, W4A16 op for down, "
-                   "residual add+next RMSNorm; then lm_head GEMV and argmax; "
+                   "q|k|v (the W4A16 GEMM, M=16), rotary+KV append+causal attention (matrix cores), W4A16 op for "
+                   "o (GEMM), residual add+RMSNorm, gate|up with the SiLU*up epilogue (paired kernel, 16 row "
+                   "slots), W4A16 op for down (paired kernel, 16 row slots), residual add+next RMSNorm; then "
+                   "lm_head GEMV and argmax; "
                    "prefill_eager_ms: the same prompt as eager torch ops around QuantizedLinear",
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),
