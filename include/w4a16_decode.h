@@ -214,8 +214,9 @@ int w4a16_silu_mul_f16(const void* gate_up, void* output, int64_t rows, int64_t 
  * holding the gate rows then the up rows. The same values as
  * w4a16_linear_f16 over the 2 inter rows followed by w4a16_silu_mul_f16, in
  * one launch: the W4A16 GEMM with the multiply in its epilogue (M >= 2, or
- * K > 16384; M = 9..16 where the op takes the 16-row-slot paired kernel
- * with whole rows staged: that kernel's SiLU form), or the decode step's
+ * K > 16384; M = 9..16 on rows longer than 4096 weights, or on 2 inter >=
+ * 8192 rows of up to 2048, where the 16-row-slot paired plan stages whole
+ * rows: that kernel's SiLU form), or the decode step's
  * paired fused GEMV (M = 1). Replaces the
  * gate_proj / up_proj QuantizedLinear calls and act_fn(gate) * up of HF's
  * LlamaMLP (w4a16/linear.py:154-200 for each projection). Needs group_size

@@ -59,9 +59,10 @@ extern "C" {
  * group_size == 128 with 16-byte aligned activations and weights and M <= 8
  * takes the tuned kernels and M > 8 the W4A16 GEMM (operands below 4 GiB;
  * its LDS-staged forms from M = 64; M = 9..16 on rows longer than 4096
- * weights, or N >= 8192 with rows of up to 2048, the paired kernel with 16
- * row slots; W4A16_DECODE = mfma_oneshot or mfma_pair selects those kernels
- * for M = 9..16); anything else takes the generic
+ * weights the paired kernel with 16 row slots where its plan keeps at most 2
+ * wavefronts on weight blocks, and N >= 8192 with rows of up to 2048 the
+ * one-shot MFMA kernel; W4A16_DECODE = mfma_oneshot or mfma_pair selects
+ * those kernels for M = 9..16); anything else takes the generic
  * kernel (the reference routes every M > 8 to its naive kernel).
  * Environment, read at every call, with the reference's semantics
  * (csrc/int4_linear_kernel.cu:459-491, :713-749):

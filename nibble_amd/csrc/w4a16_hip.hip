@@ -620,20 +620,34 @@ bool pair_split_route(int64_t M, int64_t N, int64_t K) {
 // m1 = ceil(M/2) (each half 4..8 rows), each with its own launch shape unless
 // the caller fixed one; the weights are streamed twice.
 // M = 9..16 in one paired launch (16 row slots, the dequantized weights in B)
-// where it beats the GEMM: measured at M = 9, 12, 16 against gemm_w4a16
-// (graph timing, one box), 5632 x 2048 7.3-7.9 against 7.9-9.0 us, 14336 x
-// 4096 14.4-18.0 against 16.8-21.0, 2048 x 11264 8.2-8.5 against 8.5-9.2;
-// the GEMM keeps rows of 2049..4096 weights and narrower layers of short
-// rows (4096 x 4096 7.3-7.8 against 6.7-7.7, 2048 x 2048 4.5-5.0 against
-// 4.1-4.7, 2048 x 2560 5.6-6.2 against 4.3-4.9, 4096 x 14336 a tie) and
-// grids of more than 256 workgroups.
-bool pair16_route(int64_t M, int64_t N, int64_t K) {
+// on rows longer than 4096 weights where it beats the GEMM: measured at M =
+// 9, 12, 16 against gemm_w4a16 (graph timing), 5632 x 2048 7.3-7.9 against
+// 7.9-9.0 us, 14336 x 4096 14.4-18.0 against 16.8-21.0, 8192 x 2048 10.3
+// against 11.6, 14336 x 2048 12.9 against 18.7; the GEMM keeps rows of up
+// to 4096 weights (4096 x 4096 7.3-7.8 against 6.7-7.7, 4096 x 14336 a tie)
+// and grids of more than 256 workgroups. Plans with more than 2 wavefronts
+// on weight blocks stay on the GEMM too: with 16 row slots their 1024-thread
+// workgroups spill registers (8192 x 8192: 37.3 against 15.9 us).
+// The 16-row-slot paired plan fits: instantiated, within LDS, at most 256
+// workgroups.
+bool pair16_fits(int64_t M, int64_t N, int64_t K, int max_blocks_cap) {
     if (M < 9 || M > 16 || K < 128 || K % 128 != 0 || K > 32768) return false;
-    if (!(K > 4096 || (K <= 2048 && N >= 8192))) return false;
     const Plan p = plan_mfma_pair(M, N, K);
     const int64_t wgs = (N + 8 * p.max_blocks - 1) / (8 * p.max_blocks);
-    return wgs <= 256 && w4a16_internal::mfma_pair_instantiated(M, p.splits, p.max_blocks, p.rows, p.unroll) &&
+    return wgs <= 256 && p.max_blocks <= max_blocks_cap &&
+           w4a16_internal::mfma_pair_instantiated(M, p.splits, p.max_blocks, p.rows, p.unroll) &&
            w4a16_internal::mfma_pair_lds_bytes(M, K, p.splits, p.max_blocks, p.rows, p.unroll) <= kMaxLdsBytes;
+}
+
+bool pair16_route(int64_t M, int64_t N, int64_t K) { return K > 4096 && pair16_fits(M, N, K, 2); }
+
+// M = 9..16 on wide layers of short rows (K <= 2048, N >= 8192): the one-shot
+// MFMA kernel (a K x N grid at M = 12 and 16, graph timing, two interleaved
+// passes: 2048 x 8192 5.50 against 5.90 us on the GEMM, 2048 x 14336 8.14
+// against 9.05, 2048 x 32000 14.13 against 14.80; the GEMM keeps N <= 4096,
+// 4.54 against 5.22 at 2048 x 2048).
+bool mfma_oneshot16_route(int64_t M, int64_t N, int64_t K) {
+    return M >= 9 && M <= 16 && K <= 2048 && N >= 8192 && mfma_oneshot_fits(M, K);
 }
 
 int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16* x, const uint8_t* w,
@@ -713,9 +727,14 @@ int make_plan(const void* act, const void* packed, int64_t M, int64_t N, int64_t
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
-    // M = 9..16 on long rows (and wide layers of short rows) whose paired
-    // plan keeps at most one workgroup per CU: the paired kernel in one
-    // launch (16 row slots)
+    // M = 9..16 on wide layers of short rows: the one-shot MFMA kernel; on
+    // long rows whose paired plan keeps at most one workgroup per CU and 2
+    // wavefronts on weight blocks: the paired kernel in one launch (16 row
+    // slots)
+    if (aligned && family == 0 && mfma_oneshot16_route(M, N, K)) {
+        *out = plan_mfma_oneshot(M, N, K);
+        return W4A16_OK;
+    }
     if (aligned && family == 0 && pair16_route(M, N, K)) {
         *out = plan_mfma_pair(M, N, K);
         return W4A16_OK;
@@ -1450,10 +1469,12 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
     }
     if (!w4a16_internal::gemm_fits(M, 2 * inter, K))
         return fail(W4A16_ERR_TOO_LARGE, "linear + SiLU: every operand must be below 4 GiB");
-    // M = 9..16 where the op takes the 16-row-slot paired kernel: its SiLU
-    // form, a gate and an up block per wavefront (half the plain plan's
-    // row-block wavefronts, so the same rows per workgroup)
-    if (pair16_route(M, 2 * inter, K)) {
+    // M = 9..16 on rows longer than 4096 weights and on wide layers of rows
+    // up to 2048 (the 1.1B model's gate|up: 8.9 against 9.6 us on the GEMM's
+    // SiLU form): the 16-row-slot paired kernel's SiLU form, a gate and an up
+    // block per wavefront (half the plain plan's row-block wavefronts, so the
+    // same rows per workgroup and half the registers of the plain plan)
+    if ((K > 4096 || (K <= 2048 && 2 * inter >= 8192)) && pair16_fits(M, 2 * inter, K, 8)) {
         const Plan q = plan_mfma_pair(M, 2 * inter, K);
         const int sn = q.max_blocks > 1 ? q.max_blocks / 2 : 1;
         if (q.rows == q.splits * q.unroll && w4a16_internal::mfma_pair_silu_instantiated(q.splits, sn, q.unroll) &&

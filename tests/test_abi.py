@@ -314,6 +314,20 @@ def test_m2_routing(monkeypatch):
     assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 32000, 2048, 128)["kernel"] == "oneshot"
 
 
+def test_short_prompt_routing(monkeypatch):
+    """M = 9..16: the one-shot MFMA kernel on wide layers of rows up to 2048
+    weights, the 16-row-slot paired kernel on longer rows whose plan keeps 2
+    wavefronts or fewer on weight blocks (8192 x 8192 would take 4 and spill),
+    else the GEMM."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    for m, k, n, kernel in [(12, 2048, 8192, "mfma_oneshot"), (16, 2048, 32000, "mfma_oneshot"),
+                            (9, 1024, 16384, "mfma_oneshot"), (12, 2048, 4096, "gemm"), (16, 2048, 2560, "gemm"),
+                            (16, 4096, 14336, "gemm"), (16, 8192, 8192, "gemm"), (12, 8192, 4096, "mfma_pair"),
+                            (9, 14336, 4096, "mfma_pair"), (12, 5632, 2048, "mfma_pair"), (17, 2048, 8192, "gemm")]:
+        assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] == kernel, (m, k, n)
+
+
 def test_oneshot_plan_shapes(monkeypatch):
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
