@@ -658,6 +658,47 @@ def test_fused_step_matches_torch_step(gpu):
     assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
 
 
+def test_decoder_matches_cpu_reference_path(gpu):
+    """The GPU decoder (fused prefill, fused decode step with attention + o)
+    against the same weights on the CPU, where every projection runs the
+    product's torch restatement of the reference's path (dequantize, fp32
+    matmul: nibble_amd.reference, pinned against the C oracle in
+    tests/test_api_cpu.py) and attention, RMSNorm and SiLU are torch ops: the
+    prefill's last-position logits and one decode step's logits within
+    5e-3 (1 + |ref|) (measured: 1.5e-3 at |ref| <= 1.65). No HIP code on the
+    reference side."""
+    from nibble_amd.llama import LlamaDecoder
+
+    cfg = _small_cfg()
+    model = LlamaDecoder(cfg, device=gpu, seed=0)
+    ref = LlamaDecoder(cfg, device="cpu", init="empty")
+    ref.load_state_dict({k: v.detach().cpu() for k, v in model.state_dict().items()})
+    assert model.fused and model.attn_o and not ref.fused
+    prompt = torch.randint(0, cfg.vocab_size, (12,), generator=torch.Generator().manual_seed(5))
+    with torch.inference_mode():
+        print("[case] decoder vs CPU reference path: prefill", flush=True)
+        model.prefill(prompt.to(gpu))
+        torch.cuda.synchronize()
+        got = model.logits.float().cpu()
+        ref.k_cache.zero_()
+        ref.v_cache.zero_()
+        want = ref._forward(prompt, torch.arange(prompt.numel())).float()
+        assert torch.isfinite(got).all()
+        assert torch.all((got - want).abs() <= 5e-3 * (1 + want.abs())), float((got - want).abs().max())
+        # the CPU model's state for the step, and the same next token on the
+        # GPU (a near-tie in the argmax must not change the comparison)
+        ref.prefill(prompt)
+        model.token.copy_(ref.token.to(gpu))
+        model.x_buf.copy_(model.embed[model.token[0]])
+        print("[case] decoder vs CPU reference path: one step", flush=True)
+        model.step()
+        ref.step()
+        torch.cuda.synchronize()
+        got, want = model.logits.float().cpu(), ref.logits.float()
+        assert torch.all((got - want).abs() <= 5e-3 * (1 + want.abs())), float((got - want).abs().max())
+        assert int(model.position) == int(ref.position) == prompt.numel() + 1
+
+
 def test_attention_o_step_matches_two_launch_step(gpu):
     """From the same state, the step with attention + o as one launch and the
     step with separate attention and o GEMV launches agree (logits
