@@ -658,23 +658,27 @@ def test_fused_step_matches_torch_step(gpu):
     assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
 
 
-def test_decoder_matches_cpu_reference_path(gpu):
+@pytest.mark.parametrize("size,bound", [("small", 5e-3), ("full", 2e-2)])
+def test_decoder_matches_cpu_reference_path(gpu, size, bound):
     """The GPU decoder (fused prefill, fused decode step with attention + o)
     against the same weights on the CPU, where every projection runs the
     product's torch restatement of the reference's path (dequantize, fp32
     matmul: nibble_amd.reference, pinned against the C oracle in
     tests/test_api_cpu.py) and attention, RMSNorm and SiLU are torch ops: the
     prefill's last-position logits and one decode step's logits within
-    5e-3 (1 + |ref|) (measured: 1.5e-3 at |ref| <= 1.65). No HIP code on the
+    bound * (1 + |ref|) (small model: measured 1.5e-3 at |ref| <= 1.65), on
+    the 2-layer test model and on configs[4] at full size (22 layers,
+    hidden 2048, 155 INT4 linears, 16-token prompt). No HIP code on the
     reference side."""
-    from nibble_amd.llama import LlamaDecoder
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
 
-    cfg = _small_cfg()
+    cfg = _small_cfg() if size == "small" else LlamaConfig(max_seq_len=48)
     model = LlamaDecoder(cfg, device=gpu, seed=0)
     ref = LlamaDecoder(cfg, device="cpu", init="empty")
     ref.load_state_dict({k: v.detach().cpu() for k, v in model.state_dict().items()})
     assert model.fused and model.attn_o and not ref.fused
-    prompt = torch.randint(0, cfg.vocab_size, (12,), generator=torch.Generator().manual_seed(5))
+    prompt = torch.randint(0, cfg.vocab_size, (12 if size == "small" else 16,),
+                           generator=torch.Generator().manual_seed(5))
     with torch.inference_mode():
         print("[case] decoder vs CPU reference path: prefill", flush=True)
         model.prefill(prompt.to(gpu))
@@ -684,7 +688,8 @@ def test_decoder_matches_cpu_reference_path(gpu):
         ref.v_cache.zero_()
         want = ref._forward(prompt, torch.arange(prompt.numel())).float()
         assert torch.isfinite(got).all()
-        assert torch.all((got - want).abs() <= 5e-3 * (1 + want.abs())), float((got - want).abs().max())
+        print(f"[case] {size}: prefill logits max |err| {float((got - want).abs().max()):.3e}", flush=True)
+        assert torch.all((got - want).abs() <= bound * (1 + want.abs())), float((got - want).abs().max())
         # the CPU model's state for the step, and the same next token on the
         # GPU (a near-tie in the argmax must not change the comparison)
         ref.prefill(prompt)
@@ -695,7 +700,8 @@ def test_decoder_matches_cpu_reference_path(gpu):
         ref.step()
         torch.cuda.synchronize()
         got, want = model.logits.float().cpu(), ref.logits.float()
-        assert torch.all((got - want).abs() <= 5e-3 * (1 + want.abs())), float((got - want).abs().max())
+        print(f"[case] {size}: step logits max |err| {float((got - want).abs().max()):.3e}", flush=True)
+        assert torch.all((got - want).abs() <= bound * (1 + want.abs())), float((got - want).abs().max())
         assert int(model.position) == int(ref.position) == prompt.numel() + 1
 
 
