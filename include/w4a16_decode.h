@@ -243,14 +243,17 @@ int w4a16_add_rmsnorm_f16(const void* x, const void* delta, const void* weight, 
  * 32] fp32) on q and k rounded to fp16; k and v appended to the caches; query t
  * attends to slots 0 .. start + t (slots below start read from the caches):
  * output[t] = softmax(q k^T / 8) v, [tokens, num_heads * 64] fp16.
- * Needs head_dim 64, start + tokens <= min(max_seq_len, 256), 16-byte
- * aligned caches. When num_heads / num_kv_heads is a power of two up to 64
- * and qkv and the tables are 16-byte aligned: one launch on the matrix cores,
- * a workgroup per KV head and 64 / group tokens (fp32 scores and softmax, the
- * probabilities rounded to fp16 for the value product), which also appends
- * its own tokens' rows to the caches. Otherwise one workgroup per query head
- * and block of 4 tokens (fp32 throughout); above 16 tokens a launch before it
- * writes the new rotary k and v rows to the caches.
+ * Needs head_dim 64, start + tokens <= max_seq_len, 16-byte aligned caches.
+ * When num_heads / num_kv_heads is a power of two up to 64 and qkv and the
+ * tables are 16-byte aligned: the matrix cores, a workgroup per KV head and
+ * 64 / group tokens (fp32 scores and an online softmax, the probabilities
+ * rounded to fp16 for the value product). Up to 256 slots one launch, which
+ * also appends its own tokens' rows to the caches; past 256 slots a launch
+ * before it writes the new rotary k and v rows to the caches and the
+ * attention streams the slots through LDS in blocks of 256. Otherwise (only
+ * up to 256 slots; more return W4A16_ERR_SHAPE) one workgroup per query head
+ * and block of 4 tokens (fp32 throughout); above 16 tokens a launch before
+ * it writes the new rotary k and v rows to the caches.
  */
 int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
                                 const float* sin_table, int64_t start, int64_t tokens, void* output,

@@ -838,6 +838,7 @@ silu_mul_vec_kernel(const f16* __restrict__ gate_up, f16* __restrict__ out, int 
 constexpr int kPrefillRow = 72;
 constexpr int kPrefillOneLaunch = 16;
 constexpr int kPrefillMaxSlots = 256;   // start + tokens: 73 KiB of LDS at 256 slots
+constexpr int kPrefillBlock = 256;      // slots per streamed block past kPrefillMaxSlots
 constexpr int kPrefillQueries = 4;      // queries per workgroup, one per wavefront
 
 __global__ void __launch_bounds__(256)
@@ -1011,8 +1012,11 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     const int t0 = blockIdx.y * tpw;
     const int NK = start + min(t0 + tpw, T);   // slots the workgroup's last token sees
     const int NKP = (NK + 31) & ~31;
-    f16* ks = reinterpret_cast<f16*>(smem);   // [NKP][KR]
-    f16* vs = ks + (size_t)NKP * KR;          // [NKP][KR]
+    // LDS rows: every slot the workgroup sees (FUSED), or one block of up to
+    // kPrefillBlock slots at a time, streamed from the caches (FUSED = false)
+    const int LR = FUSED ? NKP : min(NKP, kPrefillBlock);
+    f16* ks = reinterpret_cast<f16*>(smem);   // [LR][KR]
+    f16* vs = ks + (size_t)LR * KR;           // [LR][KR]
     const int row_stride = (num_heads + 2 * num_kv) * D;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -1035,17 +1039,17 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             sn[i] = sin_table[ti + i];
         }
     }
-    {
-        // rows from the caches: all NK (zeros past them up to NKP), or (FUSED)
-        // those below start
-        const u32x4* kc = reinterpret_cast<const u32x4*>(k_cache + (size_t)hk * S * D);
-        const u32x4* vc = reinterpret_cast<const u32x4*>(v_cache + (size_t)hk * S * D);
-        const int units = (FUSED ? start : NK) * 8, punits = (FUSED ? start : NKP) * 8;
+    // cache rows r0 .. r0 + n - 1 into LDS rows 0 .. n - 1, rows n .. np - 1
+    // zero (16-byte units; loads clamped into the rows being copied)
+    const u32x4* kc = reinterpret_cast<const u32x4*>(k_cache + (size_t)hk * S * D);
+    const u32x4* vc = reinterpret_cast<const u32x4*>(v_cache + (size_t)hk * S * D);
+    auto stage_rows = [&](int r0, int n, int np) {
+        const int units = n * 8, punits = np * 8;
         for (int i0 = threadIdx.x; i0 < punits; i0 += 8 * 256) {
             u32x4 kb[8], vb[8];
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const int i = min(i0 + 256 * b, units - 1);
+                const int i = r0 * 8 + max(min(i0 + 256 * b, units - 1), 0);
                 kb[b] = kc[i];
                 vb[b] = vc[i];
             }
@@ -1060,8 +1064,9 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
                 }
             }
         }
-    }
+    };
     if constexpr (FUSED) {
+        stage_rows(0, start, start);   // the slots below start
         // the new rows this workgroup sees (tokens 0 .. nn - 1) from qkv: v
         // as is, k rotated at its slot (fp32, rounded to fp16, as
         // prefill_rope_append_kernel); the workgroup's own tokens t0 .. nn - 1
@@ -1148,17 +1153,22 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         qb[1][h] = as_u32(hi);
     }
     __syncthreads();
-    if (t0 + ((16 * wave) >> glog) >= T) return;   // no column of this wavefront is a token
+    // a wavefront none of whose columns is a token only helps stage the
+    // streamed blocks (FUSED = false)
+    const bool active = t0 + ((16 * wave) >> glog) < T;
+    if (FUSED && !active) return;
 
     // 2. chunks of 32 slots up to the wavefront's last visible slot
     const int last = start + tqc;
-    const int lastw = start + min(t0 + ((16 * wave + 15) >> glog), T - 1);
+    const int lastw = active ? start + min(t0 + ((16 * wave + 15) >> glog), T - 1) : -1;
     const int tk = j >> 2, tm = j & 3;   // this lane's row / 4-dim block in the transposing read
     float run_max = -__builtin_inff(), run_sum = 0.0f;
     f32x4 o[4];
 #pragma unroll
     for (int md = 0; md < 4; ++md) o[md] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c0 = 0; c0 <= lastw; c0 += 32) {
+    // LDS rows 0 .. rows - 1 hold slots b0 .. b0 + rows - 1
+    auto attend = [&](int b0, int rows) {
+    for (int c0 = 0; c0 < rows && b0 + c0 <= lastw; c0 += 32) {
         f32x4 st[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1175,7 +1185,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int slot = c0 + 16 * mt + 4 * q4 + e;
+                const int slot = b0 + c0 + 16 * mt + 4 * q4 + e;
                 st[mt][e] = slot <= last ? st[mt][e] * 0.125f : -__builtin_inff();
                 mx = fmaxf(mx, st[mt][e]);
             }
@@ -1187,7 +1197,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int slot = c0 + 16 * mt + 4 * q4 + e;
+                const int slot = b0 + c0 + 16 * mt + 4 * q4 + e;
                 pe[mt][e] = slot <= last ? __expf(st[mt][e] - mx) : 0.0f;
                 psum += pe[mt][e];
             }
@@ -1206,6 +1216,21 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             o[md] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, pb),
                                                            o[md] * rescale, 0, 0, 0);
         }
+    }
+    };
+    if constexpr (FUSED) {
+        attend(0, NKP);
+    } else {
+        // blocks of kPrefillBlock slots: every wavefront stages, the active
+        // ones attend; the softmax state carries over from block to block
+        for (int b0 = 0; b0 < NK; b0 += kPrefillBlock) {
+            const int nb = min(kPrefillBlock, NK - b0), nbp = (nb + 31) & ~31;
+            if (b0 > 0) __syncthreads();   // every wavefront done with the previous block
+            stage_rows(b0, nb, nbp);
+            __syncthreads();
+            attend(b0, nbp);
+        }
+        if (!active) return;
     }
 
     // 3. lane (q4, j) holds column j's dims 16 md + 4 q4 .. + 3
@@ -1463,8 +1488,8 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "prefill attention: head_dim must be 64");
     if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
         return fail(W4A16_ERR_SHAPE, "prefill attention: num_heads must be a positive multiple of num_kv_heads");
-    if (tokens < 0 || start < 0 || start + tokens > w4a16::kPrefillMaxSlots || start + tokens > max_seq_len)
-        return fail(W4A16_ERR_SHAPE, "prefill attention: needs 0 <= tokens and start + tokens <= min(max_seq_len, 256)");
+    if (tokens < 0 || start < 0 || start + tokens > max_seq_len || max_seq_len > INT32_MAX / 64)
+        return fail(W4A16_ERR_SHAPE, "prefill attention: needs 0 <= tokens and start + tokens <= max_seq_len");
     if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(qkv, 2) || !aligned(output, 2))
         return fail(W4A16_ERR_ALIGNMENT, "prefill attention: caches must be 16-byte aligned, qkv and output 2-byte");
     const int nk = (int)(start + tokens);   // slots the last query block sees
@@ -1475,6 +1500,35 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     while ((int64_t)1 << glog < group) ++glog;
     const bool mfma = ((int64_t)1 << glog) == group && group <= 64 && aligned(qkv, 16) && aligned(cos_table, 16) &&
                       aligned(sin_table, 16);
+    if (nk > w4a16::kPrefillMaxSlots) {
+        // past the slots LDS holds at once: the new rows appended by a launch
+        // of their own, then the matrix-core kernel streaming the caches
+        // through LDS in blocks of kPrefillBlock slots
+        if (!mfma)
+            return fail(W4A16_ERR_SHAPE, "prefill attention past 256 slots needs query heads per KV head a power of "
+                                         "two up to 64 and 16-byte aligned qkv and rotary tables");
+        if ((tokens + (64 >> glog) - 1) / (64 >> glog) > 65535)
+            return fail(W4A16_ERR_SHAPE, "prefill attention: tokens / (64 / query heads per KV head) above 65535");
+        const int64_t appends = tokens * num_kv_heads * 64;
+        hipLaunchKernelGGL(w4a16::prefill_rope_append_kernel, dim3((unsigned)((appends + 255) / 256)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table, sin_table,
+                           (int)start, (int)tokens, (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
+        int rc = check_launch();
+        if (rc != W4A16_OK) return rc;
+        const auto skern = w4a16::prefill_attention_mfma_kernel<false>;
+        const size_t slds = (size_t)2 * w4a16::kPrefillBlock * w4a16::kPrefillRow * 2;
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(skern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)slds);
+        if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
+        const int tpw = 64 >> glog;
+        hipLaunchKernelGGL(skern, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)), dim3(256), slds,
+                           static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table,
+                           sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
+                           (int)num_kv_heads, (int)max_seq_len, glog);
+        return check_launch();
+    }
     if (mfma) {
         const auto mkern = w4a16::prefill_attention_mfma_kernel<true>;
         const void* mk = reinterpret_cast<const void*>(mkern);

@@ -30,13 +30,15 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill of a prompt of up to 256 tokens runs the W4A16 op itself for every
-projection (q|k|v as one op; the op's W4A16 GEMM from 9 rows, its LDS-staged
+Prefill of a prompt runs the W4A16 op itself for every projection up to 512
+tokens (q|k|v as one op; the op's W4A16 GEMM from 9 rows, its LDS-staged
 form from 128; up to 8 rows its small-batch kernels), gate|up as one GEMM
 with the SiLU-multiply in its epilogue, and one launch each for the residual
-add + RMSNorm and the rotary + KV append + causal attention; longer prompts
-run torch ops around the same op (the GEMM up to 256 rows, dequantize +
-hipBLASLt beyond). ``capture_prefill(T)`` records
+add + RMSNorm and the rotary + KV append + causal attention; from 513 tokens
+the projections take dequantize + hipBLASLt. The attention launch holds up
+to 256 cache slots in LDS and streams longer prompts through it in 256-slot
+blocks where query heads per KV head are a power of two up to 64; other
+head layouts run prompts past 256 tokens as torch ops around the same op. ``capture_prefill(T)`` records
 a T-token prefill in a HIP graph. ``Decoder.capture()`` records one decode step -- embedding, 22 blocks,
 lm_head, greedy argmax, KV-cache write and position increment -- in a HIP
 graph, so generating a token is one ``graph.replay()``.
@@ -51,11 +53,14 @@ import torch
 import torch.nn.functional as F
 
 from nibble_amd import _lib
-from nibble_amd.linear import QuantizedLinear
+from nibble_amd.cuda import dequantize_cuda
+from nibble_amd.linear import NATIVE_GEMM_MAX_ROWS, QuantizedLinear
 from nibble_amd.quantization import quantize_and_pack_weights
 
-# Longest prompt the fused prefill takes (w4a16_prefill_attention_f16 holds
-# at most 256 cache slots in LDS).
+# Longest prompt the fused prefill takes where the prefill attention cannot
+# stream the caches (query heads per KV head not a power of two up to 64:
+# w4a16_prefill_attention_f16 then holds at most 256 cache slots in LDS);
+# elsewhere it takes any prompt that fits the cache.
 FUSED_PREFILL_MAX_TOKENS = 256
 # Most rows a prefill projection sends to the W4A16 op in the torch-op
 # prefill; more rows take dequantize + hipBLASLt. Measured on the 1.1B and 8B
@@ -259,7 +264,7 @@ class LlamaDecoder(torch.nn.Module):
         self.qkv_rope = True
         self.host_position = 0   # host copy of `position` (set by prefill, +1 per step)
         self.prefill_graph: torch.cuda.CUDAGraph | None = None
-        self.fuse_prefill = True   # prompts of <= 256 tokens: fused prefill (see fused_prefill)
+        self.fuse_prefill = True   # fused prefill (see fused_prefill)
         self.prefill_tokens: torch.Tensor | None = None
         self.prefill_positions: torch.Tensor | None = None
         # fused-step weights (views keep the per-module state-dict entries) and work buffers
@@ -293,10 +298,13 @@ class LlamaDecoder(torch.nn.Module):
     def fused_prefill(self, tokens: int) -> bool:
         """Whether a prompt of `tokens` tokens takes the fused prefill: the W4A16
         op for every projection and one launch for each RMSNorm, attention and
-        SiLU-multiply (1 <= tokens <= FUSED_PREFILL_MAX_TOKENS, within the
-        cache and the attention launch's 256 slots)."""
-        return (self.fused and self.fuse_prefill and 1 <= tokens <= FUSED_PREFILL_MAX_TOKENS
-                and tokens <= min(self.cfg.max_seq_len, 256))
+        SiLU-multiply (1 <= tokens <= max_seq_len; past FUSED_PREFILL_MAX_TOKENS
+        only where the attention streams the caches through LDS, query heads
+        per KV head a power of two up to 64)."""
+        group = self.cfg.num_heads // self.cfg.num_kv_heads
+        streams = group & (group - 1) == 0 and group <= 64
+        limit = self.cfg.max_seq_len if streams else min(self.cfg.max_seq_len, FUSED_PREFILL_MAX_TOKENS)
+        return self.fused and self.fuse_prefill and 1 <= tokens <= limit
 
     def _prefill(self, prompt: torch.Tensor, positions: torch.Tensor) -> None:
         self.k_cache.zero_()
@@ -331,18 +339,29 @@ class LlamaDecoder(torch.nn.Module):
         for i, b in enumerate(self.layers):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
-            qkv = torch.ops.w4a16.linear(h, qkv_w, qkv_s, g)
+            qkv = self._prefill_linear(h, qkv_w, qkv_s)
             _lib.prefill_attention_f16(qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, attn,
                                        cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
-            o = torch.ops.w4a16.linear(attn, b.o_proj.packed_weights, b.o_proj.scales, g)
+            o = self._prefill_linear(attn, b.o_proj.packed_weights, b.o_proj.scales)
             _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
-            _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
-            d = torch.ops.w4a16.linear(mlp, b.down_proj.packed_weights, b.down_proj.scales, g)
+            if t <= NATIVE_GEMM_MAX_ROWS:
+                _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
+            else:
+                gu = self._prefill_linear(h, gu_w, gu_s)
+                torch.mul(F.silu(gu[:, :cfg.intermediate_size]), gu[:, cfg.intermediate_size:], out=mlp)
+            d = self._prefill_linear(mlp, b.down_proj.packed_weights, b.down_proj.scales)
             nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.norm
             _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
         _lib.gemv_fused_f16(h[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits)
         _lib.argmax_embed_f16(self.logits, self.token, None, self.embed, self.x_buf)
         self.position.fill_(t)
+
+    def _prefill_linear(self, x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+        """A prefill projection: the W4A16 op up to NATIVE_GEMM_MAX_ROWS rows,
+        dequantize + hipBLASLt beyond (faster there on the wide layers)."""
+        if x.shape[0] <= NATIVE_GEMM_MAX_ROWS:
+            return torch.ops.w4a16.linear(x, packed, scales, self.cfg.group_size)
+        return F.linear(x, dequantize_cuda(packed, scales, self.cfg.group_size))
 
     @torch.inference_mode()
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:

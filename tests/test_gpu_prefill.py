@@ -239,6 +239,36 @@ def test_prefill_attention(gpu, heads, kv, misaligned, tokens, start):
     assert torch.allclose(kg[:, new].float(), k_new.transpose(0, 1).float(), rtol=ULP, atol=2 ** -14)
 
 
+# past the 256 slots LDS holds at once: the new rows appended by their own
+# launch, the caches streamed through LDS in blocks of 256 slots (1 to 3
+# blocks, a partial last block, a start past the first block)
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (64, 1)])
+@pytest.mark.parametrize("tokens,start,S", [(257, 0, 320), (300, 0, 512), (100, 300, 512), (520, 0, 1024),
+                                            (64, 700, 1024)])
+def test_prefill_attention_streamed(gpu, heads, kv, tokens, start, S):
+    gen = torch.Generator().manual_seed(tokens * 7 + start + heads)
+    qkv = torch.randn((tokens, (heads + 2 * kv) * 64), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    cos, sin = _tables(S)
+    ref, kc_ref, vc_ref, k_new, v_new = _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv)
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = torch.full((tokens, heads * 64), float("nan"), dtype=torch.float16, device=gpu)
+    print(f"[case] streamed prefill attention heads={heads} kv={kv} tokens={tokens} start={start} S={S}", flush=True)
+    _lib.prefill_attention_f16(qkv.to(gpu), kd, vd, cos.to(gpu), sin.to(gpu), start, out, heads, kv)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs()), float(err.max())
+    kg, vg = kd.cpu(), vd.cpu()
+    new = slice(start, start + tokens)
+    others = [s for s in range(S) if not start <= s < start + tokens]
+    assert torch.equal(kg[:, others], k_cache[:, others]) and torch.equal(vg[:, others], v_cache[:, others])
+    assert torch.equal(vg[:, new], v_new.transpose(0, 1))
+    assert torch.allclose(kg[:, new].float(), k_new.transpose(0, 1).float(), rtol=ULP, atol=2 ** -14)
+
+
 def test_prefill_attention_rejects(gpu):
     heads, kv, S = 8, 2, 300
     kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
@@ -246,12 +276,19 @@ def test_prefill_attention_rejects(gpu):
     cos, sin = _tables(S)
     cos, sin = cos.to(gpu), sin.to(gpu)
     short_k = torch.zeros((kv, 64, 64), dtype=torch.float16, device=gpu)
-    for tokens, start, kc, vc in [(257, 0, kd, vd), (10, 250, kd, vd), (10, 60, short_k, short_k)]:
-        # past the 256 slots the launch holds in LDS, or past the caches' 64 slots
+    for tokens, start, kc, vc in [(301, 0, kd, vd), (10, 295, kd, vd), (10, 60, short_k, short_k)]:
+        # past the caches' 300 (or 64) slots
         qkv = torch.zeros((tokens, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
         out = torch.zeros((tokens, heads * 64), dtype=torch.float16, device=gpu)
         with pytest.raises(_lib.W4A16Error, match="tokens"):
             _lib.prefill_attention_f16(qkv, kc, vc, cos, sin, start, out, heads, kv)
+    # past 256 slots only the matrix-core layout streams: not group 3, not qkv at a 2-byte offset
+    for h, misaligned in [(6, False), (8, True)]:
+        buf = torch.zeros((257 * (h + 2 * kv) * 64 + 1,), dtype=torch.float16, device=gpu)
+        qkv = (buf[1:] if misaligned else buf[:-1]).view(257, (h + 2 * kv) * 64)
+        out = torch.zeros((257, h * 64), dtype=torch.float16, device=gpu)
+        with pytest.raises(_lib.W4A16Error, match="256 slots"):
+            _lib.prefill_attention_f16(qkv, kd, vd, cos, sin, 0, out, h, kv)
     qkv = torch.zeros((4, (heads + 2 * kv) * 64), dtype=torch.float16, device=gpu)
     out = torch.zeros((4, heads * 64), dtype=torch.float16, device=gpu)
     with pytest.raises(_lib.W4A16Error, match="head_dim"):
@@ -268,17 +305,19 @@ def _small_cfg():
                        num_kv_heads=2, head_dim=64, max_seq_len=32)
 
 
-@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64, 130])
+@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64, 130, 300, 600])
 def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     """The fused prefill (up to 16 tokens the one-shot / paired MFMA kernels,
-    beyond that the GEMM) against the torch-op prefill of the same model and
-    prompt: logits of the last token within 2e-2 (1 + |ref|), KV caches within
-    fp16 roundings; the graphed fused prefill reproduces the eager one exactly."""
+    beyond that the GEMM; 300 and 600 tokens stream the attention through
+    256-slot blocks, 600 also takes dequantize + hipBLASLt projections)
+    against the torch-op prefill of the same model and prompt: logits of the
+    last token within 2e-2 (1 + |ref|), KV caches within fp16 roundings; the
+    graphed fused prefill reproduces the eager one exactly."""
     from dataclasses import replace
 
     from nibble_amd.llama import LlamaDecoder
 
-    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=160), device=gpu, seed=11)
+    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=max(160, tokens + 16)), device=gpu, seed=11)
     prompt = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(tokens)).to(gpu)
     assert model.fused_prefill(tokens)
     with torch.inference_mode():
