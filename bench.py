@@ -408,12 +408,13 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
-def prefill_long(device, lengths=(64, 256), runs: int = 5) -> dict:
-    """Prompts of 64 and 256 tokens on the random-init 1.1B Llama, each path
-    recorded in a HIP graph: the fused prefill (every projection on the W4A16
-    op: its GEMM at M = 64, the LDS-staged GEMM at M = 256) against the
-    reference's prefill path (every projection as dequantize + hipBLASLt
-    inside QuantizedLinear, torch ops around them)."""
+def prefill_long(device, lengths=(64, 256, 1024), runs: int = 5) -> dict:
+    """Prompts of 64, 256 and 1024 tokens on the random-init 1.1B Llama, each
+    path recorded in a HIP graph: the fused prefill (every projection on the
+    W4A16 op: its GEMM at M = 64, the LDS-staged and 32x32 GEMMs above; the
+    1024-token attention streams the caches through LDS in 256-slot blocks)
+    against the reference's prefill path (every projection as dequantize +
+    hipBLASLt inside QuantizedLinear, torch ops around them)."""
     import torch
 
     from nibble_amd.linear import FUSED_MAX_ROWS, NATIVE_GEMM_MAX_ROWS

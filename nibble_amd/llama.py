@@ -30,11 +30,11 @@ a contiguous view of its rows, so state-dict keys and layouts are those of
 the per-layer modules. ``fused=False`` runs the same step as separate torch
 ops around ``QuantizedLinear`` (the reference-shaped decoder).
 
-Prefill of a prompt runs the W4A16 op itself for every projection up to 512
+Prefill of a prompt runs the W4A16 op itself for every projection up to 1024
 tokens (q|k|v as one op; the op's W4A16 GEMM from 9 rows, its LDS-staged
 form from 128; up to 8 rows its small-batch kernels), gate|up as one GEMM
 with the SiLU-multiply in its epilogue, and one launch each for the residual
-add + RMSNorm and the rotary + KV append + causal attention; from 513 tokens
+add + RMSNorm and the rotary + KV append + causal attention; from 1025 tokens
 the projections take dequantize + hipBLASLt. The attention launch holds up
 to 256 cache slots in LDS and streams longer prompts through it in 256-slot
 blocks where query heads per KV head are a power of two up to 64; other
@@ -54,7 +54,7 @@ import torch.nn.functional as F
 
 from nibble_amd import _lib
 from nibble_amd.cuda import dequantize_cuda
-from nibble_amd.linear import NATIVE_GEMM_MAX_ROWS, QuantizedLinear
+from nibble_amd.linear import QuantizedLinear
 from nibble_amd.quantization import quantize_and_pack_weights
 
 # Longest prompt the fused prefill takes where the prefill attention cannot
@@ -67,6 +67,11 @@ FUSED_PREFILL_MAX_TOKENS = 256
 # layer shapes: the op's GEMM is 1.2-3x faster than dequantize + hipBLASLt
 # from 32 to 256 rows, except 4096 x 14336 at 256 rows (90.7 against 80.7 us).
 NATIVE_PREFILL_MAX_ROWS = 256
+# Most rows a fused-prefill projection sends to the W4A16 op (the GEMM and its
+# SiLU form); longer prompts take dequantize + hipBLASLt. Measured on the whole
+# 1.1B prefill (one HIP graph): 1024 tokens 4.31 ms with the op against 4.88
+# with dequantize + hipBLASLt from 513 rows; 2048 tokens 7.65 against 7.53.
+FUSED_PREFILL_NATIVE_MAX_ROWS = 1024
 
 
 @dataclass
@@ -344,7 +349,7 @@ class LlamaDecoder(torch.nn.Module):
                                        cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
             o = self._prefill_linear(attn, b.o_proj.packed_weights, b.o_proj.scales)
             _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
-            if t <= NATIVE_GEMM_MAX_ROWS:
+            if t <= FUSED_PREFILL_NATIVE_MAX_ROWS:
                 _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
             else:
                 gu = self._prefill_linear(h, gu_w, gu_s)
@@ -357,9 +362,9 @@ class LlamaDecoder(torch.nn.Module):
         self.position.fill_(t)
 
     def _prefill_linear(self, x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
-        """A prefill projection: the W4A16 op up to NATIVE_GEMM_MAX_ROWS rows,
-        dequantize + hipBLASLt beyond (faster there on the wide layers)."""
-        if x.shape[0] <= NATIVE_GEMM_MAX_ROWS:
+        """A fused-prefill projection: the W4A16 op up to
+        FUSED_PREFILL_NATIVE_MAX_ROWS rows, dequantize + hipBLASLt beyond."""
+        if x.shape[0] <= FUSED_PREFILL_NATIVE_MAX_ROWS:
             return torch.ops.w4a16.linear(x, packed, scales, self.cfg.group_size)
         return F.linear(x, dequantize_cuda(packed, scales, self.cfg.group_size))
 

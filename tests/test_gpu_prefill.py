@@ -305,11 +305,11 @@ def _small_cfg():
                        num_kv_heads=2, head_dim=64, max_seq_len=32)
 
 
-@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64, 130, 300, 600])
+@pytest.mark.parametrize("tokens", [1, 9, 16, 17, 33, 64, 130, 300, 600, 1100])
 def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     """The fused prefill (up to 16 tokens the one-shot / paired MFMA kernels,
-    beyond that the GEMM; 300 and 600 tokens stream the attention through
-    256-slot blocks, 600 also takes dequantize + hipBLASLt projections)
+    beyond that the GEMM; from 300 tokens the attention streams through
+    256-slot blocks, and 1100 tokens take dequantize + hipBLASLt projections)
     against the torch-op prefill of the same model and prompt: logits of the
     last token within 2e-2 (1 + |ref|), KV caches within fp16 roundings; the
     graphed fused prefill reproduces the eager one exactly."""
