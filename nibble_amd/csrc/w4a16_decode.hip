@@ -839,6 +839,8 @@ constexpr int kPrefillRow = 72;
 constexpr int kPrefillOneLaunch = 16;
 constexpr int kPrefillMaxSlots = 256;   // start + tokens: 73 KiB of LDS at 256 slots
 constexpr int kPrefillBlock = 256;      // slots per streamed block past kPrefillMaxSlots
+constexpr int kPrefillThreads = 512;    // matrix-core prefill attention: 8 wavefronts per workgroup
+constexpr int kPrefillMergeBytes = 4 * 18 * 64 * 4;   // its merge of the two wavefronts per column block
 constexpr int kPrefillQueries = 4;      // queries per workgroup, one per wavefront
 
 __global__ void __launch_bounds__(256)
@@ -976,13 +978,15 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
 // computed from qkv by every workgroup that sees them and appended to the
 // caches by the workgroup that owns the token (FUSED = false reads every slot
 // from the caches, for callers that appended them beforehand).
-// Workgroup (hk, b) of 4 wavefronts takes KV head hk and the 64 / group tokens
-// t = b 64 / group .. of all its group query heads: 64 query columns, column
-// c = token offset * group + head offset, wavefront w owning
-// columns 16 w .. 16 w + 15. It stages the k and v rows of every slot its last
-// token sees once (shared by the 64 columns, where the one-query kernel above
-// restages them per head and per 4 queries), then each wavefront walks the
-// slots in chunks of 32 with an online softmax:
+// Workgroup (hk, y) of 8 wavefronts takes KV head hk and the 64 / group tokens
+// t = b 64 / group .., b = gridDim.y - 1 - y (the workgroups with the most
+// slots to attend dispatched first), of all its group query heads: 64 query
+// columns, column c = token offset * group + head offset, wavefronts w and
+// w + 4 owning columns 16 w .. 16 w + 15. It stages the k and v rows of every
+// slot its last token sees once (shared by the 64 columns, where the one-query
+// kernel above restages them per head and per 4 queries); wavefront w walks
+// the even chunks of 32 slots and w + 4 the odd ones, each with an online
+// softmax, and w merges the two states at the end:
 //   S^T = K Q^T (v_mfma_f32_16x16x32_f16; A = k rows from LDS, lane (q4, j)
 //     holds slot 16 mt + j, dims 32 s + 8 q4 .. +8; B = the rotary q of column
 //     j, rounded to fp16), so lane (q4, j) receives column j's scores for
@@ -998,18 +1002,20 @@ prefill_attention_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
 // zero.
 // ---------------------------------------------------------------------------
 template <bool FUSED>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kPrefillThreads)
 prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache,
                               f16* __restrict__ v_cache, const float* __restrict__ cos_table,
                               const float* __restrict__ sin_table, int start, int T, f16* __restrict__ out,
                               int num_heads, int num_kv, int S, int glog) {
     constexpr int D = 64;
     constexpr int KR = kPrefillRow;
+    constexpr int NT = kPrefillThreads;
     extern __shared__ __align__(16) uint8_t smem[];
     const int group = 1 << glog;
     const int tpw = 64 >> glog;   // tokens per workgroup
     const int hk = blockIdx.x;
-    const int t0 = blockIdx.y * tpw;
+    // the last tokens (most slots to attend) in the first workgroups dispatched
+    const int t0 = (gridDim.y - 1 - blockIdx.y) * tpw;
     const int NK = start + min(t0 + tpw, T);   // slots the workgroup's last token sees
     const int NKP = (NK + 31) & ~31;
     // LDS rows: every slot the workgroup sees (FUSED), or one block of up to
@@ -1018,7 +1024,10 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     f16* ks = reinterpret_cast<f16*>(smem);   // [LR][KR]
     f16* vs = ks + (size_t)LR * KR;           // [LR][KR]
     const int row_stride = (num_heads + 2 * num_kv) * D;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // wavefronts w and w + 4 own columns 16 w .. 16 w + 15: w the even
+    // 32-slot chunks, w + 4 the odd ones (half = 0 / 1)
+    const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & 3);
+    const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4, j = lane & 15;
 
@@ -1045,17 +1054,17 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     const u32x4* vc = reinterpret_cast<const u32x4*>(v_cache + (size_t)hk * S * D);
     auto stage_rows = [&](int r0, int n, int np) {
         const int units = n * 8, punits = np * 8;
-        for (int i0 = threadIdx.x; i0 < punits; i0 += 8 * 256) {
+        for (int i0 = threadIdx.x; i0 < punits; i0 += 8 * NT) {
             u32x4 kb[8], vb[8];
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const int i = r0 * 8 + max(min(i0 + 256 * b, units - 1), 0);
+                const int i = r0 * 8 + max(min(i0 + NT * b, units - 1), 0);
                 kb[b] = kc[i];
                 vb[b] = vc[i];
             }
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const int i = i0 + 256 * b;
+                const int i = i0 + NT * b;
                 if (i < punits) {
                     const bool live = i < units;
                     const int r = i >> 3, e = i & 7;
@@ -1074,16 +1083,16 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         const int nn = NK - start;
         const f16* kq = qkv + (size_t)num_heads * D + (size_t)hk * D;
         const f16* vq = qkv + (size_t)(num_heads + num_kv) * D + (size_t)hk * D;
-        for (int i0 = threadIdx.x; i0 < nn * 8; i0 += 4 * 256) {
+        for (int i0 = threadIdx.x; i0 < nn * 8; i0 += 4 * NT) {
             u32x4 vb[4];
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const int i = min(i0 + 256 * b, nn * 8 - 1);
+                const int i = min(i0 + NT * b, nn * 8 - 1);
                 vb[b] = *reinterpret_cast<const u32x4*>(vq + (size_t)(i >> 3) * row_stride + 8 * (i & 7));
             }
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const int i = i0 + 256 * b;
+                const int i = i0 + NT * b;
                 if (i < nn * 8) {
                     const int r = i >> 3, e = i & 7;
                     reinterpret_cast<u32x4*>(vs + (size_t)(start + r) * KR)[e] = vb[b];
@@ -1092,12 +1101,12 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
                 }
             }
         }
-        for (int i0 = threadIdx.x; i0 < nn * 4; i0 += 2 * 256) {
+        for (int i0 = threadIdx.x; i0 < nn * 4; i0 += 2 * NT) {
             u32x4 ka[2], kz[2];
             f32x4 cv[2][2], sv[2][2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int i = min(i0 + 256 * b, nn * 4 - 1);
+                const int i = min(i0 + NT * b, nn * 4 - 1);
                 const int r = i >> 2, db = i & 3;
                 const f16* kr = kq + (size_t)r * row_stride + 8 * db;
                 ka[b] = *reinterpret_cast<const u32x4*>(kr);
@@ -1110,7 +1119,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int i = i0 + 256 * b;
+                const int i = i0 + NT * b;
                 if (i < nn * 4) {
                     const int r = i >> 2, db = i & 3;
                     u32x4 lo, hi;
@@ -1135,7 +1144,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
                 }
             }
         }
-        for (int i = threadIdx.x; i < (NKP - NK) * 8; i += 256) {
+        for (int i = threadIdx.x; i < (NKP - NK) * 8; i += NT) {
             const int r = NK + (i >> 3), e = i & 7;
             reinterpret_cast<u32x4*>(ks + (size_t)r * KR)[e] = (u32x4){0u, 0u, 0u, 0u};
             reinterpret_cast<u32x4*>(vs + (size_t)r * KR)[e] = (u32x4){0u, 0u, 0u, 0u};
@@ -1153,10 +1162,9 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         qb[1][h] = as_u32(hi);
     }
     __syncthreads();
-    // a wavefront none of whose columns is a token only helps stage the
-    // streamed blocks (FUSED = false)
+    // a wavefront none of whose columns is a token only stages and takes part
+    // in the barriers
     const bool active = t0 + ((16 * wave) >> glog) < T;
-    if (FUSED && !active) return;
 
     // 2. chunks of 32 slots up to the wavefront's last visible slot
     const int last = start + tqc;
@@ -1168,7 +1176,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     for (int md = 0; md < 4; ++md) o[md] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     // LDS rows 0 .. rows - 1 hold slots b0 .. b0 + rows - 1
     auto attend = [&](int b0, int rows) {
-    for (int c0 = 0; c0 < rows && b0 + c0 <= lastw; c0 += 32) {
+    for (int c0 = 32 * half; c0 < rows && b0 + c0 <= lastw; c0 += 64) {
         f32x4 st[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1190,7 +1198,9 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
                 mx = fmaxf(mx, st[mt][e]);
             }
         mx = row_pair_max(mx);
-        const float rescale = __expf(run_max - mx);   // 0 on the first chunk
+        // -inf while no slot of the column has been seen (odd chunks only)
+        const float mb = mx == -__builtin_inff() ? 0.0f : mx;
+        const float rescale = __expf(run_max - mb);   // 0 on the column's first chunk
         float psum = 0.0f;
         float pe[2][4];
 #pragma unroll
@@ -1198,7 +1208,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int slot = b0 + c0 + 16 * mt + 4 * q4 + e;
-                pe[mt][e] = slot <= last ? __expf(st[mt][e] - mx) : 0.0f;
+                pe[mt][e] = slot <= last ? __expf(st[mt][e] - mb) : 0.0f;
                 psum += pe[mt][e];
             }
         const f16x2 p00 = {(f16)pe[0][0], (f16)pe[0][1]}, p01 = {(f16)pe[0][2], (f16)pe[0][3]};
@@ -1230,11 +1240,35 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             __syncthreads();
             attend(b0, nbp);
         }
-        if (!active) return;
     }
 
-    // 3. lane (q4, j) holds column j's dims 16 md + 4 q4 .. + 3
-    if (tq >= T) return;
+    // 3. the odd-chunk wavefront's state merged into the even one's through
+    // LDS (the k / v rows are no longer read): [wave][18 values][64 lanes]
+    __syncthreads();
+    float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * 18 * 64 + lane;
+    if (half == 1) {
+        xs[0] = run_max;
+        xs[64] = run_sum;
+#pragma unroll
+        for (int md = 0; md < 4; ++md)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xs[(2 + 4 * md + e) * 64] = o[md][e];
+    }
+    __syncthreads();
+    if (half == 1 || !active || tq >= T) return;
+    {
+        // run_max is finite here: the even chunks start at slot 0
+        const float m1 = xs[0];
+        const float m = fmaxf(run_max, m1);
+        const float a0 = __expf(run_max - m), a1 = __expf(m1 - m);
+        run_sum = run_sum * a0 + xs[64] * a1;
+#pragma unroll
+        for (int md = 0; md < 4; ++md)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[md][e] = o[md][e] * a0 + xs[(2 + 4 * md + e) * 64] * a1;
+    }
+
+    // 4. lane (q4, j) holds column j's dims 16 md + 4 q4 .. + 3
     const float inv = 1.0f / run_sum;
     f16* orow = out + (size_t)tq * num_heads * D + (size_t)hq * D;
     const bool vec = (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
@@ -1517,12 +1551,14 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
         int rc = check_launch();
         if (rc != W4A16_OK) return rc;
         const auto skern = w4a16::prefill_attention_mfma_kernel<false>;
-        const size_t slds = (size_t)2 * w4a16::kPrefillBlock * w4a16::kPrefillRow * 2;
+        const size_t slds = std::max((size_t)2 * w4a16::kPrefillBlock * w4a16::kPrefillRow * 2,
+                                     (size_t)w4a16::kPrefillMergeBytes);
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(skern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)slds);
         if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
         const int tpw = 64 >> glog;
-        hipLaunchKernelGGL(skern, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)), dim3(256), slds,
+        hipLaunchKernelGGL(skern, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)),
+                           dim3(w4a16::kPrefillThreads), slds,
                            static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
                            static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table,
                            sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
@@ -1532,14 +1568,15 @@ int w4a16_prefill_attention_f16(const void* qkv, void* k_cache, void* v_cache, c
     if (mfma) {
         const auto mkern = w4a16::prefill_attention_mfma_kernel<true>;
         const void* mk = reinterpret_cast<const void*>(mkern);
-        const size_t mlds = (size_t)2 * ((nk + 31) & ~31) * w4a16::kPrefillRow * 2;
+        const size_t mlds = std::max((size_t)2 * ((nk + 31) & ~31) * w4a16::kPrefillRow * 2,
+                                     (size_t)w4a16::kPrefillMergeBytes);
         if (mlds > 64 * 1024) {
             const hipError_t e = hipFuncSetAttribute(mk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)mlds);
             if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "prefill attention: LDS request refused");
         }
         const int tpw = 64 >> glog;
         hipLaunchKernelGGL(mkern, dim3((unsigned)num_kv_heads, (unsigned)((tokens + tpw - 1) / tpw)),
-                           dim3(256), mlds, static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
+                           dim3(w4a16::kPrefillThreads), mlds, static_cast<hipStream_t>(stream), static_cast<const w4a16::f16*>(qkv),
                            static_cast<w4a16::f16*>(k_cache), static_cast<w4a16::f16*>(v_cache), cos_table,
                            sin_table, (int)start, (int)tokens, static_cast<w4a16::f16*>(output), (int)num_heads,
                            (int)num_kv_heads, (int)max_seq_len, glog);
