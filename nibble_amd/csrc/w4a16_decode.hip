@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <string>
+#include <type_traits>
 
 #include "w4a16_device.h"
 
@@ -1150,14 +1151,18 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             reinterpret_cast<u32x4*>(vs + (size_t)r * KR)[e] = (u32x4){0u, 0u, 0u, 0u};
         }
     }
-    // the rotary q (B operand): dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i (s = 1)
+    // the rotary q (B operand): dims 8 q4 + i (s = 0) pair with 32 + 8 q4 + i
+    // (s = 1), times the score scale 1/8 (a power of two: the fp16 rounding of
+    // the scaled value is the scaled rounding)
     u32x4 qb[2];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
         const f16x2 a = as_f16x2(qa[h]), z = as_f16x2(qz[h]);
         const float c0 = cs[2 * h], c1 = cs[2 * h + 1], s0 = sn[2 * h], s1 = sn[2 * h + 1];
-        const f16x2 lo = {(f16)((float)a.x * c0 - (float)z.x * s0), (f16)((float)a.y * c1 - (float)z.y * s1)};
-        const f16x2 hi = {(f16)((float)z.x * c0 + (float)a.x * s0), (f16)((float)z.y * c1 + (float)a.y * s1)};
+        const f16x2 lo = {(f16)(0.125f * ((float)a.x * c0 - (float)z.x * s0)),
+                          (f16)(0.125f * ((float)a.y * c1 - (float)z.y * s1))};
+        const f16x2 hi = {(f16)(0.125f * ((float)z.x * c0 + (float)a.x * s0)),
+                          (f16)(0.125f * ((float)z.y * c1 + (float)a.y * s1))};
         qb[0][h] = as_u32(lo);
         qb[1][h] = as_u32(hi);
     }
@@ -1174,9 +1179,13 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     f32x4 o[4];
 #pragma unroll
     for (int md = 0; md < 4; ++md) o[md] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    // LDS rows 0 .. rows - 1 hold slots b0 .. b0 + rows - 1
-    auto attend = [&](int b0, int rows) {
-    for (int c0 = 32 * half; c0 < rows && b0 + c0 <= lastw; c0 += 64) {
+    // the smallest last slot among the wavefront's columns: chunks wholly at or
+    // below it need no mask
+    const int firstlast = start + min(t0 + ((16 * wave) >> glog), T - 1);
+    constexpr float kLog2e = 1.4426950408889634f;
+    // one chunk: LDS rows c0 .. c0 + 31 holding slots base .. base + 31
+    auto chunk = [&](int c0, int base, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
         f32x4 st[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1193,22 +1202,24 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int slot = b0 + c0 + 16 * mt + 4 * q4 + e;
-                st[mt][e] = slot <= last ? st[mt][e] * 0.125f : -__builtin_inff();
+                if constexpr (MASK) {
+                    const int slot = base + 16 * mt + 4 * q4 + e;
+                    st[mt][e] = slot <= last ? st[mt][e] : -__builtin_inff();
+                }
                 mx = fmaxf(mx, st[mt][e]);
             }
         mx = row_pair_max(mx);
-        // -inf while no slot of the column has been seen (odd chunks only)
-        const float mb = mx == -__builtin_inff() ? 0.0f : mx;
-        const float rescale = __expf(run_max - mb);   // 0 on the column's first chunk
+        // -inf while no slot of the column has been seen (odd chunks only);
+        // exp(x - m) as 2^(x log2 e - m log2 e), masked scores giving 2^-inf = 0
+        const float mbl = (mx == -__builtin_inff() ? 0.0f : mx) * kLog2e;
+        const float rescale = __builtin_amdgcn_exp2f(run_max * kLog2e - mbl);   // 0 on the column's first chunk
         float psum = 0.0f;
         float pe[2][4];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int slot = b0 + c0 + 16 * mt + 4 * q4 + e;
-                pe[mt][e] = slot <= last ? __expf(st[mt][e] - mb) : 0.0f;
+                pe[mt][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][e], kLog2e, -mbl));
                 psum += pe[mt][e];
             }
         const f16x2 p00 = {(f16)pe[0][0], (f16)pe[0][1]}, p01 = {(f16)pe[0][2], (f16)pe[0][3]};
@@ -1226,7 +1237,15 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
             o[md] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, pb),
                                                            o[md] * rescale, 0, 0, 0);
         }
-    }
+    };
+    // LDS rows 0 .. rows - 1 hold slots b0 .. b0 + rows - 1
+    auto attend = [&](int b0, int rows) {
+        for (int c0 = 32 * half; c0 < rows && b0 + c0 <= lastw; c0 += 64) {
+            if (b0 + c0 + 31 <= firstlast)
+                chunk(c0, b0 + c0, std::false_type{});
+            else
+                chunk(c0, b0 + c0, std::true_type{});
+        }
     };
     if constexpr (FUSED) {
         attend(0, NKP);
@@ -1260,7 +1279,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
         // run_max is finite here: the even chunks start at slot 0
         const float m1 = xs[0];
         const float m = fmaxf(run_max, m1);
-        const float a0 = __expf(run_max - m), a1 = __expf(m1 - m);
+        const float a0 = __builtin_amdgcn_exp2f((run_max - m) * kLog2e), a1 = __builtin_amdgcn_exp2f((m1 - m) * kLog2e);
         run_sum = run_sum * a0 + xs[64] * a1;
 #pragma unroll
         for (int md = 0; md < 4; ++md)
