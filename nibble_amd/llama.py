@@ -352,8 +352,7 @@ class LlamaDecoder(torch.nn.Module):
             if t <= FUSED_PREFILL_NATIVE_MAX_ROWS:
                 _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
             else:
-                gu = self._prefill_linear(h, gu_w, gu_s)
-                torch.mul(F.silu(gu[:, :cfg.intermediate_size]), gu[:, cfg.intermediate_size:], out=mlp)
+                _lib.silu_mul_f16(self._prefill_linear(h, gu_w, gu_s), mlp)
             d = self._prefill_linear(mlp, b.down_proj.packed_weights, b.down_proj.scales)
             nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.norm
             _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
