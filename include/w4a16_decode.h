@@ -97,6 +97,24 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache,
                                int64_t head_dim, int64_t max_seq_len, void* stream);
 
 /*
+ * w4a16_decode_attention_f16 with each head's slots 0 .. position split into
+ * `splits` shares of whole 64-slot chunks, one workgroup per head and share
+ * (num_heads x splits workgroups, where the unsplit form has num_heads), then
+ * a second launch that merges the shares' softmax states per head. workspace:
+ * num_heads * splits * 66 fp32 (264 bytes per head and share, 4-byte
+ * aligned), overwritten by every call; calls that share one must not run
+ * concurrently. 1 <= splits <= 64; other arguments, output and NaN rows as
+ * w4a16_decode_attention_f16 (the new k / v rows are appended once).
+ * Replaces (reference): the same attention as w4a16_decode_attention_f16.
+ */
+int w4a16_decode_attention_split_f16(const void* qkv, void* k_cache, void* v_cache,
+                                     const float* cos_table, const float* sin_table,
+                                     const int64_t* position, void* output,
+                                     int64_t num_heads, int64_t num_kv_heads,
+                                     int64_t head_dim, int64_t max_seq_len, int64_t splits,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Attention of one new token fused with the o projection and the residual
  * add, for positions below 64 (one chunk of cache slots):
  *   attn = softmax(q k^T / 8) v as w4a16_decode_attention_f16 (same qkv

@@ -76,6 +76,7 @@ DECODE_SIGNATURES = {
         [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp],
     ),
     "w4a16_decode_attention_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 4 + [_vp]),
+    "w4a16_decode_attention_split_f16": (ctypes.c_int, [_vp] * 7 + [_i64] * 5 + [_vp, _i64, _vp]),
     "w4a16_attention_o_f16": (ctypes.c_int, [_vp] * 8 + [_i64] * 6 + [_vp]),
     "w4a16_gemv_qkv_rope_f16": (
         ctypes.c_int,
@@ -279,6 +280,20 @@ def decode_attention_f16(qkv, k_cache, v_cache, cos_table, sin_table, position, 
             qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
             position.data_ptr(), output.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2],
             _stream_ptr(stream),
+        )
+    )
+
+
+def decode_attention_split_f16(qkv, k_cache, v_cache, cos_table, sin_table, position, output, num_heads: int,
+                               num_kv_heads: int, splits: int, workspace, head_dim: int = 64, stream=None) -> None:
+    """``w4a16_decode_attention_split_f16``: the slots split into `splits` shares
+    (one workgroup per head and share), merged per head; `workspace` holds at
+    least num_heads * splits * 66 fp32."""
+    _raise_on(
+        lib().w4a16_decode_attention_split_f16(
+            qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(),
+            position.data_ptr(), output.data_ptr(), num_heads, num_kv_heads, head_dim, k_cache.shape[-2], splits,
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_ptr(stream),
         )
     )
 

@@ -68,11 +68,17 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int WA>
+// SPLIT: workgroup (hq, s) of gridDim.y attends a share of the slots 0 .. p
+// (64-slot aligned, the shares in slot order) and writes its unnormalised
+// state to partial[hq][s] = {max, sum, acc[64]} for decode_attention_merge;
+// only share 0 appends the new k / v rows.
+template <int WA, bool SPLIT>
 __global__ void __launch_bounds__(64 * WA)
 decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
                  const float* __restrict__ cos_table, const float* __restrict__ sin_table,
-                 const int64_t* __restrict__ position, f16* __restrict__ out, int num_heads, int num_kv, int S) {
+                 const int64_t* __restrict__ position, f16* __restrict__ out, int num_heads, int num_kv, int S,
+                 float* __restrict__ partial) {
+    static_assert(!SPLIT || WA > 1, "the split form merges its wavefronts through LDS");
     constexpr int D = 64;
     __shared__ __align__(16) float qs_all[WA][D];
     __shared__ __align__(16) f16 knew_all[WA][D];
@@ -107,6 +113,14 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
     };
     u32x4 kr[8], vr[8];
     int c0 = 64 * wave;
+    int end = 0;   // slots c0 .. end - 1 (set below for the unsplit form)
+    if constexpr (SPLIT) {
+        const int pe = (p64 >= 0 && p64 < S) ? (int)p64 : 0;
+        const int per = ((pe + (int)gridDim.y) / (int)gridDim.y + 63) & ~63;
+        const int lo = min((int)blockIdx.y * per, pe + 1);
+        c0 += lo;
+        end = min(lo + per, pe + 1);
+    }
     load_k(kr, c0);
     load_v(vr, c0);
     const f16* q = qkv + (size_t)hq * D;
@@ -131,20 +145,21 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
     qs[lane] = (float)q16;
     knew[lane] = k16;
     vnew[lane] = v16;
-    if (valid && wave == 0 && hq % group == 0) {
+    if (valid && wave == 0 && hq % group == 0 && (!SPLIT || blockIdx.y == 0)) {
         k_cache[((size_t)hk * S + p) * D + lane] = k16;
         v_cache[((size_t)hk * S + p) * D + lane] = v16;
     }
     wave_lds_sync();
-    if (!valid) {
-        if (wave == 0) out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
+    if (!valid) {   // (the split form's merge writes the NaN rows)
+        if (!SPLIT && wave == 0) out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
         return;
     }
+    if constexpr (!SPLIT) end = p + 1;
 
     float run_max = -__builtin_inff(), run_sum = 0.0f, acc = 0.0f;
     f16* my_vt = vt[wave];
     float* my_probs = probs[wave];
-    for (; c0 <= p; c0 += 64 * WA) {
+    for (; c0 < end; c0 += 64 * WA) {
         const int t = c0 + lane;
         float dot = 0.0f;
         if (t == p) {
@@ -161,7 +176,7 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
                 }
             }
         }
-        const float score = t <= p ? dot * 0.125f : -__builtin_inff();
+        const float score = t < end ? dot * 0.125f : -__builtin_inff();
         // value rows of the chunk to LDS: rows past p zeroed, slot p from vnew
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -169,18 +184,18 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
             const int slot = c0 + row;
             u32x4 val = vr[i];
             if (slot == p) val = reinterpret_cast<const u32x4*>(vnew)[lane & 7];
-            if (slot > p) val = (u32x4){0u, 0u, 0u, 0u};
+            if (slot >= end) val = (u32x4){0u, 0u, 0u, 0u};
             reinterpret_cast<u32x4*>(my_vt + row * D)[lane & 7] = val;
         }
         // next chunk's rows requested before this chunk's reductions
         const int next = c0 + 64 * WA;
-        if (next <= p) {
+        if (next < end) {
             load_k(kr, next);
             load_v(vr, next);
         }
         const float cmax = wave_max(score);
         const float new_max = fmaxf(run_max, cmax);
-        const float pr = t <= p ? expf(score - new_max) : 0.0f;
+        const float pr = t < end ? expf(score - new_max) : 0.0f;
         const float psum = wave_sum(pr);
         const float rescale = expf(run_max - new_max);   // 0 on the first chunk
         my_probs[lane] = pr;
@@ -199,7 +214,7 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
         run_sum = run_sum * rescale + psum;
         run_max = new_max;
     }
-    if (WA == 1) {
+    if constexpr (WA == 1) {
         out[(size_t)hq * D + lane] = (f16)(acc / run_sum);
         return;
     }
@@ -219,6 +234,45 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
         const float f = wsum[w] > 0.0f ? expf(wmax[w] - m) : 0.0f;
         num = __builtin_fmaf(wacc[w][lane], f, num);
         den = __builtin_fmaf(wsum[w], f, den);
+    }
+    if constexpr (SPLIT) {
+        // a share past p (no slots) leaves max -inf and sum 0
+        float* pp = partial + ((size_t)hq * gridDim.y + blockIdx.y) * (D + 2);
+        if (lane == 0) {
+            pp[0] = m;
+            pp[1] = den;
+        }
+        pp[2 + lane] = num;
+    } else {
+        out[(size_t)hq * D + lane] = (f16)(num / den);
+    }
+}
+
+// The split form's states of head blockIdx.x merged: out = sum_s acc_s e^(m_s - m)
+// / sum_s sum_s e^(m_s - m), m the largest share maximum (shares with no slots
+// skipped); NaN rows for a position outside [0, S).
+__global__ void __launch_bounds__(64)
+decode_attention_merge(const float* __restrict__ partial, const int64_t* __restrict__ position,
+                       f16* __restrict__ out, int splits, int S) {
+    constexpr int D = 64;
+    const int hq = blockIdx.x, lane = threadIdx.x;
+    const int64_t p64 = position[0];
+    if (!(p64 >= 0 && p64 < S)) {
+        out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
+        return;
+    }
+    const float* pp = partial + (size_t)hq * splits * (D + 2);
+    float m = -__builtin_inff();
+    for (int s = 0; s < splits; ++s) m = fmaxf(m, pp[(size_t)s * (D + 2)]);
+    float num = 0.0f, den = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float* ps = pp + (size_t)s * (D + 2);
+        const float l = ps[1];
+        if (l > 0.0f) {
+            const float f = expf(ps[0] - m);
+            num = __builtin_fmaf(ps[2 + lane], f, num);
+            den = __builtin_fmaf(l, f, den);
+        }
     }
     out[(size_t)hq * D + lane] = (f16)(num / den);
 }
@@ -1404,13 +1458,48 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache, co
     // keep one wavefront (a second would only re-read the same chunk)
     const int WA = max_seq_len <= 64 ? 1 : max_seq_len <= 256 ? 4 : 8;
     void (*kern)(const w4a16::f16*, w4a16::f16*, w4a16::f16*, const float*, const float*, const int64_t*,
-                 w4a16::f16*, int, int, int) = WA == 1   ? w4a16::decode_attention<1>
-                                                : WA == 4 ? w4a16::decode_attention<4>
-                                                          : w4a16::decode_attention<8>;
+                 w4a16::f16*, int, int, int, float*) = WA == 1   ? w4a16::decode_attention<1, false>
+                                                       : WA == 4 ? w4a16::decode_attention<4, false>
+                                                                 : w4a16::decode_attention<8, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)num_heads), dim3(64 * WA), 0, static_cast<hipStream_t>(stream),
                        static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),
                        static_cast<w4a16::f16*>(v_cache), cos_table, sin_table, position,
-                       static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads, (int)max_seq_len);
+                       static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads, (int)max_seq_len,
+                       nullptr);
+    return check_launch();
+}
+
+int w4a16_decode_attention_split_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
+                                     const float* sin_table, const int64_t* position, void* output,
+                                     int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                     int64_t max_seq_len, int64_t splits, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    if (!qkv || !k_cache || !v_cache || !cos_table || !sin_table || !position || !output || !workspace)
+        return fail(W4A16_ERR_NULL, "split attention: every pointer must be non-NULL");
+    if (head_dim != 64) return fail(W4A16_ERR_CONFIG, "split attention: head_dim must be 64");
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || num_heads > 65535)
+        return fail(W4A16_ERR_SHAPE, "split attention: num_heads must be a positive multiple of num_kv_heads");
+    if (max_seq_len <= 0 || max_seq_len > 16384)
+        return fail(W4A16_ERR_SHAPE, "split attention: max_seq_len must be in 1..16384");
+    if (splits < 1 || splits > 64) return fail(W4A16_ERR_CONFIG, "split attention: splits must be in 1..64");
+    if (workspace_bytes < num_heads * splits * 66 * 4)
+        return fail(W4A16_ERR_TOO_LARGE, "split attention: workspace below num_heads * splits * 264 bytes");
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(qkv, 2) || !aligned(output, 2) ||
+        !aligned(workspace, 4))
+        return fail(W4A16_ERR_ALIGNMENT,
+                    "split attention: caches 16-byte aligned, fp16 buffers 2-byte, workspace 4-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const auto skern = w4a16::decode_attention<4, true>;
+    hipLaunchKernelGGL(skern, dim3((unsigned)num_heads, (unsigned)splits), dim3(256), 0,
+                       st, static_cast<const w4a16::f16*>(qkv), static_cast<w4a16::f16*>(k_cache),
+                       static_cast<w4a16::f16*>(v_cache), cos_table, sin_table, position,
+                       static_cast<w4a16::f16*>(output), (int)num_heads, (int)num_kv_heads, (int)max_seq_len,
+                       static_cast<float*>(workspace));
+    const int rc = check_launch();
+    if (rc != W4A16_OK) return rc;
+    hipLaunchKernelGGL(w4a16::decode_attention_merge, dim3((unsigned)num_heads), dim3(64), 0, st,
+                       static_cast<const float*>(workspace), position, static_cast<w4a16::f16*>(output), (int)splits,
+                       (int)max_seq_len);
     return check_launch();
 }
 

@@ -146,6 +146,81 @@ def test_decode_attention(gpu, heads, kv, pos):
     assert torch.allclose(kg[:, pos].float(), k_new.float(), rtol=2 ** -10, atol=2 ** -14)
 
 
+def _decode_case(heads, kv, pos, S, seed):
+    """Inputs and the float64 reference of one decode-attention call (as
+    test_decode_attention builds them)."""
+    gen = torch.Generator().manual_seed(seed)
+    qkv = torch.randn(((heads + 2 * kv) * 64,), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    cos, sin = _tables(S)
+    c, s_ = cos[pos].double(), sin[pos].double()
+    q = _rope64(qkv[: heads * 64].view(heads, 64), c, s_).to(torch.float16).double()
+    k_new = _rope64(qkv[heads * 64: (heads + kv) * 64].view(kv, 64), c, s_).to(torch.float16)
+    v_new = qkv[(heads + kv) * 64:].view(kv, 64)
+    kc, vc = k_cache.clone(), v_cache.clone()
+    kc[:, pos], vc[:, pos] = k_new, v_new
+    group = heads // kv
+    kf = kc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    vf = vc.double().repeat_interleave(group, 0)[:, : pos + 1]
+    scores = torch.einsum("hd,hsd->hs", q, kf) / math.sqrt(64)
+    ref = torch.einsum("hs,hsd->hd", torch.softmax(scores, dim=-1), vf).reshape(-1)
+    return qkv, k_cache, v_cache, cos, sin, ref, k_new, v_new
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8, 64])
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8), (4, 1)])
+@pytest.mark.parametrize("pos", [0, 63, 64, 200, 511, 1500, 2047])
+def test_decode_attention_split(gpu, heads, kv, pos, splits):
+    """The split form (a workgroup per head and share of the slots, merged per
+    head) against the float64 reference, within the unsplit form's bound;
+    shares past the position (no slots) included; the new k / v rows
+    appended once, every other slot untouched."""
+    S = 2048
+    qkv, k_cache, v_cache, cos, sin, ref, k_new, v_new = _decode_case(heads, kv, pos, S, pos * 7 + heads + splits)
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    out = torch.full((heads * 64,), float("nan"), dtype=torch.float16, device=gpu)
+    ws = torch.full((heads * splits * 66,), float("nan"), dtype=torch.float32, device=gpu)
+    position = torch.tensor([pos], dtype=torch.int64, device=gpu)
+    print(f"[case] split attention heads={heads} kv={kv} pos={pos} splits={splits}", flush=True)
+    _lib.decode_attention_split_f16(qkv.to(gpu), kd, vd, cos.to(gpu), sin.to(gpu), position, out, heads, kv,
+                                    splits, ws)
+    torch.cuda.synchronize()
+    got = out.double().cpu()
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs()
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs()), float(err.max())
+    kg, vg = kd.cpu(), vd.cpu()
+    others = [t for t in range(S) if t != pos]
+    assert torch.equal(kg[:, others], k_cache[:, others]) and torch.equal(vg[:, others], v_cache[:, others])
+    assert torch.equal(vg[:, pos], v_new)
+    assert torch.allclose(kg[:, pos].float(), k_new.float(), rtol=2 ** -10, atol=2 ** -14)
+
+
+def test_decode_attention_split_out_of_range_and_rejects(gpu):
+    S, heads, kv = 256, 8, 2
+    qkv = torch.randn(((heads + 2 * kv) * 64,)).to(torch.float16).to(gpu)
+    kd = torch.zeros((kv, S, 64), dtype=torch.float16, device=gpu)
+    vd = torch.zeros_like(kd)
+    cos, sin = _tables(S)
+    cos, sin = cos.to(gpu), sin.to(gpu)
+    out = torch.zeros((heads * 64,), dtype=torch.float16, device=gpu)
+    ws = torch.zeros((heads * 4 * 66,), dtype=torch.float32, device=gpu)
+    for bad in (S, -1):
+        position = torch.tensor([bad], dtype=torch.int64, device=gpu)
+        _lib.decode_attention_split_f16(qkv, kd, vd, cos, sin, position, out, heads, kv, 4, ws)
+        torch.cuda.synchronize()
+        assert torch.isnan(out).all()
+        assert not kd.any() and not vd.any()
+    position = torch.tensor([3], dtype=torch.int64, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="workspace"):
+        _lib.decode_attention_split_f16(qkv, kd, vd, cos, sin, position, out, heads, kv, 5, ws)
+    for bad_splits in (0, 65):
+        with pytest.raises(_lib.W4A16Error, match="splits"):
+            _lib.decode_attention_split_f16(qkv, kd, vd, cos, sin, position, out, heads, kv, bad_splits, ws)
+    assert not kd.any() and not vd.any()
+
+
 def test_decode_attention_position_out_of_range(gpu):
     S, heads, kv = 16, 8, 2
     qkv = torch.randn(((heads + 2 * kv) * 64,)).to(torch.float16).to(gpu)
@@ -730,6 +805,44 @@ def test_attention_o_step_matches_two_launch_step(gpu):
     assert torch.equal(model.token, ref_tok)
     p = int(state[3])
     assert torch.allclose(model.k_cache[:, :, p].float(), ref_k[:, :, p].float(), rtol=1e-2, atol=1e-2)
+
+
+def test_split_attention_step(gpu):
+    """A 640-slot cache takes the split decode attention (5 shares per head):
+    from the same state after a 600-token prompt, the fused step against the
+    torch-op step and against the fused step with one workgroup per head
+    (logits |err| <= 2e-2 (1 + |ref|)); graphed tokens equal eager ones."""
+    from dataclasses import replace
+
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=640), device=gpu, seed=5)
+    assert model.attn_splits == 5
+    prompt = torch.randint(0, 512, (600,), generator=torch.Generator().manual_seed(6)).to(gpu)
+    model.prefill(prompt)
+    state = (model.k_cache.clone(), model.v_cache.clone(), model.token.clone(), model.position.clone(),
+             model.x_buf.clone())
+
+    def step(fused: bool, splits: int):
+        for t, s_ in zip((model.k_cache, model.v_cache, model.token, model.position, model.x_buf), state):
+            t.copy_(s_)
+        model.fused, model.attn_splits = fused, splits
+        with torch.inference_mode():
+            model.step()
+        torch.cuda.synchronize()
+        return model.logits.float().cpu(), model.k_cache.clone()
+
+    ref, ref_k = step(False, 5)
+    got, got_k = step(True, 5)
+    one, _ = step(True, 0)
+    for other in (ref, one):
+        assert torch.all((got - other).abs() <= 2e-2 * (1 + other.abs())), float((got - other).abs().max())
+    assert torch.allclose(got_k[:, :, 600].float(), ref_k[:, :, 600].float(), rtol=1e-2, atol=1e-2)
+    model.attn_splits = 5
+    eager = model.generate(prompt, 6, use_graph=False)
+    model.prefill(prompt)
+    model.capture()
+    assert torch.equal(model.generate(prompt, 6, use_graph=True), eager)
 
 
 def test_decode_graphs_across_position_64(gpu):
