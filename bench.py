@@ -408,6 +408,49 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
+def decode_long_context(device, prompt_len: int = 1500, max_seq_len: int = 2048, new_tokens: int = 64,
+                        runs: int = 3) -> dict:
+    """Graph-replayed decode (8 steps per replay) after a 1500-token prompt
+    in a 2048-slot cache on the random-init 1.1B Llama: the decode attention
+    split over the slots (the decoder's default past 512 slots) against one
+    workgroup per head."""
+    import torch
+
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    model = LlamaDecoder(LlamaConfig(max_seq_len=max_seq_len), device=device, seed=0)
+    prompt = torch.randint(0, model.cfg.vocab_size, (prompt_len,), generator=torch.Generator().manual_seed(2))
+    prompt = prompt.to(device)
+    splits = model.attn_splits
+
+    def timed() -> float:
+        model.prefill(prompt)
+        model.capture(tokens_per_replay=TOKENS_PER_REPLAY)
+        ts = []
+        for _ in range(runs + 1):
+            model.prefill(prompt)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            left = new_tokens
+            while left > 0:
+                left -= model.replay_tokens(limit=left).numel()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        ts = sorted(ts[1:])
+        return new_tokens / ts[len(ts) // 2]
+
+    split_rate = timed()
+    model.attn_splits = 0
+    single_rate = timed()
+    del model
+    torch.cuda.empty_cache()
+    return {f"decode_ctx{prompt_len}_tok_s": round(split_rate, 1),
+            f"decode_ctx{prompt_len}_one_wg_per_head_tok_s": round(single_rate, 1),
+            "decode_long_context": f"{new_tokens} tokens after a {prompt_len}-token prompt, {max_seq_len}-slot "
+                                   f"cache, {TOKENS_PER_REPLAY} steps per graph replay: decode attention split "
+                                   f"into {splits} shares per head, against one workgroup per head"}
+
+
 def prefill_long(device, lengths=(64, 256, 1024), runs: int = 5) -> dict:
     """Prompts of 64, 256 and 1024 tokens on the random-init 1.1B Llama, each
     path recorded in a HIP graph: the fused prefill (every projection on the
@@ -755,6 +798,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["decode"] = decode_tok_s(device)
         line["decode"].update(prefill_long(device))
+        line["decode"].update(decode_long_context(device))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(shapes)
     print(json.dumps(line), flush=True)
