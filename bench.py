@@ -579,6 +579,11 @@ def main() -> int:
     ap.add_argument("--prefill-pass", type=int, metavar="TOKENS",
                     help="for rocprofv3 --kernel-trace: capture the fused prefill of a TOKENS-token prompt on the "
                          "random-init 1.1B Llama and replay it 10 times; no JSON")
+    ap.add_argument("--decode-pass", type=int, nargs=2, metavar=("CONTEXT", "SPLITS"),
+                    help="for rocprofv3 --kernel-trace: on the random-init 1.1B Llama with a 2048-slot cache, "
+                         "prefill a CONTEXT-token prompt, then decode 64 tokens by graph replay (8 steps per "
+                         "replay) with the decode attention split into SPLITS shares per head (0: one workgroup "
+                         "per head, -1: the decoder's default); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -610,6 +615,25 @@ def main() -> int:
             model.prefill(prompt)
         torch.cuda.synchronize()
         print("prefill pass done", flush=True)
+        return 0
+
+    if args.decode_pass:
+        from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+        ctx, splits = args.decode_pass
+        model = LlamaDecoder(LlamaConfig(max_seq_len=2048), device=device, seed=0)
+        if splits >= 0:
+            model.attn_splits = splits
+            model.attn_ws = torch.empty((max(1, model.cfg.num_heads * splits * 66),), dtype=torch.float32,
+                                        device=device)
+        prompt = torch.randint(0, model.cfg.vocab_size, (ctx,), generator=torch.Generator().manual_seed(0))
+        model.prefill(prompt.to(device))
+        model.capture(tokens_per_replay=TOKENS_PER_REPLAY)
+        left = 64
+        while left > 0:
+            left -= model.replay_tokens(limit=left).numel()
+        torch.cuda.synchronize()
+        print("decode pass done", flush=True)
         return 0
 
     if args.layer_pass:

@@ -257,24 +257,23 @@ decode_attention_merge(const float* __restrict__ partial, const int64_t* __restr
     constexpr int D = 64;
     const int hq = blockIdx.x, lane = threadIdx.x;
     const int64_t p64 = position[0];
-    if (!(p64 >= 0 && p64 < S)) {
-        out[(size_t)hq * D + lane] = (f16)__builtin_nanf("");
-        return;
-    }
+    // every share's values requested together (the workspace is read in
+    // bounds whatever the position; an invalid one only selects NaN at the end)
     const float* pp = partial + (size_t)hq * splits * (D + 2);
     float m = -__builtin_inff();
+#pragma unroll 8
     for (int s = 0; s < splits; ++s) m = fmaxf(m, pp[(size_t)s * (D + 2)]);
     float num = 0.0f, den = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < splits; ++s) {
         const float* ps = pp + (size_t)s * (D + 2);
-        const float l = ps[1];
-        if (l > 0.0f) {
-            const float f = expf(ps[0] - m);
-            num = __builtin_fmaf(ps[2 + lane], f, num);
-            den = __builtin_fmaf(l, f, den);
-        }
+        const float l = ps[1], a = ps[2 + lane];
+        const float f = l > 0.0f ? expf(ps[0] - m) : 0.0f;
+        num = __builtin_fmaf(a, f, num);
+        den = __builtin_fmaf(l, f, den);
     }
-    out[(size_t)hq * D + lane] = (f16)(num / den);
+    const bool valid = p64 >= 0 && p64 < S;
+    out[(size_t)hq * D + lane] = valid ? (f16)(num / den) : (f16)__builtin_nanf("");
 }
 
 // ---------------------------------------------------------------------------
