@@ -98,7 +98,7 @@ int w4a16_decode_attention_f16(const void* qkv, void* k_cache, void* v_cache,
 
 /*
  * w4a16_decode_attention_f16 with each head's slots 0 .. position split into
- * `splits` shares of whole 64-slot chunks, one workgroup per head and share
+ * up to `splits` shares of whole 64-slot chunks (at least 192 slots each), one workgroup per head and share
  * (num_heads x splits workgroups, where the unsplit form has num_heads), then
  * a second launch that merges the shares' softmax states per head. workspace:
  * num_heads * splits * 66 fp32 (264 bytes per head and share, 4-byte

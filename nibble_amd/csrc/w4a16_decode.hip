@@ -116,7 +116,8 @@ decode_attention(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __
     int end = 0;   // slots c0 .. end - 1 (set below for the unsplit form)
     if constexpr (SPLIT) {
         const int pe = (p64 >= 0 && p64 < S) ? (int)p64 : 0;
-        const int per = ((pe + (int)gridDim.y) / (int)gridDim.y + 63) & ~63;
+        // at least 3 chunks per share: shorter contexts use fewer shares
+        const int per = max(((pe + (int)gridDim.y) / (int)gridDim.y + 63) & ~63, 192);
         const int lo = min((int)blockIdx.y * per, pe + 1);
         c0 += lo;
         end = min(lo + per, pe + 1);
