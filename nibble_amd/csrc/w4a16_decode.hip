@@ -1316,20 +1316,24 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     }
 
     // 3. the odd-chunk wavefront's state merged into the even one's through
-    // LDS (the k / v rows are no longer read): [wave][18 values][64 lanes]
-    __syncthreads();
-    float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * 18 * 64 + lane;
-    if (half == 1) {
-        xs[0] = run_max;
-        xs[64] = run_sum;
+    // LDS (the k / v rows are no longer read): [wave][18 values][64 lanes];
+    // with one chunk of slots (NKP = 32, the same for the whole workgroup)
+    // the odd-chunk wavefronts attended nothing and there is nothing to merge
+    if (NKP == 32) {
+        if (half == 1 || !active || tq >= T) return;
+    } else {
+        __syncthreads();
+        float* xs = reinterpret_cast<float*>(smem) + (size_t)wave * 18 * 64 + lane;
+        if (half == 1) {
+            xs[0] = run_max;
+            xs[64] = run_sum;
 #pragma unroll
-        for (int md = 0; md < 4; ++md)
+            for (int md = 0; md < 4; ++md)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xs[(2 + 4 * md + e) * 64] = o[md][e];
-    }
-    __syncthreads();
-    if (half == 1 || !active || tq >= T) return;
-    {
+                for (int e = 0; e < 4; ++e) xs[(2 + 4 * md + e) * 64] = o[md][e];
+        }
+        __syncthreads();
+        if (half == 1 || !active || tq >= T) return;
         // run_max is finite here: the even chunks start at slot 0
         const float m1 = xs[0];
         const float m = fmaxf(run_max, m1);
