@@ -55,3 +55,28 @@ def test_fused_weight_buffers_keep_state_dict_layout():
         assert b.up_proj.packed_weights.data_ptr() == gu_w[cfg.intermediate_size:].data_ptr()
         assert torch.equal(torch.cat([b.gate_proj.packed_weights, b.up_proj.packed_weights]), gu_w)
     assert not m.fused   # the fused step runs on GPUs only
+
+
+def test_prefill_length_and_split_attention_rules():
+    """Host-side routing of the decoder: the fused prefill takes any prompt
+    that fits the cache when query heads per KV head are a power of two up to
+    64 (the attention streams the caches), else prompts up to 256 tokens; the
+    decode attention splits over the slots only past 512 cache slots, into
+    256 / heads shares, with a workspace of heads * shares * 66 fp32."""
+    from dataclasses import replace
+
+    from nibble_amd.llama import FUSED_PREFILL_MAX_TOKENS
+
+    streamed = LlamaDecoder(replace(_tiny(), max_seq_len=600), device="cpu")
+    streamed.fused = True   # the fused path's host rules, without a GPU
+    assert streamed.fused_prefill(1) and streamed.fused_prefill(300) and streamed.fused_prefill(600)
+    assert not streamed.fused_prefill(0) and not streamed.fused_prefill(601)
+    streamed.fuse_prefill = False
+    assert not streamed.fused_prefill(16)
+    odd = LlamaDecoder(replace(_tiny(), num_heads=12, num_kv_heads=4, hidden_size=12 * 32, max_seq_len=600),
+                       device="cpu")
+    odd.fused = True
+    assert odd.fused_prefill(FUSED_PREFILL_MAX_TOKENS) and not odd.fused_prefill(FUSED_PREFILL_MAX_TOKENS + 1)
+    assert streamed.attn_splits == min(256 // 4, 600 // 128) == 4
+    assert streamed.attn_ws.numel() == 4 * 4 * 66
+    assert LlamaDecoder(replace(_tiny(), max_seq_len=512), device="cpu").attn_splits == 0
