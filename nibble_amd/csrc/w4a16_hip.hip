@@ -1563,12 +1563,13 @@ int w4a16_dequantize_f16(const uint8_t* packed_weights, const void* scales, void
         return fail(W4A16_ERR_NULL, "packed_weights, scales and output must be non-NULL");
     if (reinterpret_cast<uintptr_t>(output) & 15u) return fail(W4A16_ERR_ALIGNMENT, "output must be 16-byte aligned");
     if (reinterpret_cast<uintptr_t>(scales) & 1u) return fail(W4A16_ERR_ALIGNMENT, "scales must be 2-byte aligned");
-    if (K / 32 > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "K too large");
-    const int64_t blocks = (chunks + 255) / 256;
+    if (K / 8 > INT32_MAX - 64) return fail(W4A16_ERR_TOO_LARGE, "K too large");
+    const int64_t words = chunks * 4;   // 32-bit words of codes, 8 weights each
+    const int64_t blocks = (words + 1023) / 1024;
     if (blocks > INT32_MAX) return fail(W4A16_ERR_TOO_LARGE, "too many chunks for one launch");
     hipLaunchKernelGGL(w4a16::dequantize_kernel, dim3((unsigned)blocks), dim3(256), 0,
                        static_cast<hipStream_t>(stream), packed_weights, static_cast<const w4a16::f16*>(scales),
-                       static_cast<w4a16::f16*>(output), chunks, (int)(K / 32), (int)(group_size / 32),
+                       static_cast<w4a16::f16*>(output), words, (int)(K / 8), (int)(group_size / 8),
                        (int)(K / group_size));
     return check_launch();
 }

@@ -1170,34 +1170,50 @@ linear_generic(const f16* __restrict__ x, const uint8_t* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------
-// Dequantize: out[n][k] = fp16_rn(code * scale), one thread per 16-byte chunk
-// (32 weights, inside one group since G % 32 == 0), 64 bytes written per
-// thread in natural k order. Codes are exact in f16, and an IEEE binary16
-// multiply of exact operands rounds the exact product once (round to nearest
-// even, subnormals kept), which is the value of reference
-// w4a16/reference.py:38-46 followed by .to(torch.float16).
+// Dequantize: out[n][k] = fp16_rn(code * scale). The packed codes are read
+// as 32-bit words (8 weights each, inside one group since G % 32 == 0): a
+// wavefront takes 256 consecutive words, lane l words q 64 + l (q < 4), so
+// every load instruction reads 256 contiguous bytes and every store writes
+// 1 KiB. Codes are exact in f16, and an IEEE binary16 multiply of exact
+// operands rounds the exact product once (round to nearest even, subnormals
+// kept), which is the value of reference w4a16/reference.py:38-46 followed by
+// .to(torch.float16).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
 dequantize_kernel(const uint8_t* __restrict__ w, const f16* __restrict__ scales,
-                  f16* __restrict__ out, int64_t chunks, int chunks_per_row,
-                  int chunks_per_group, int groups_per_row) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= chunks) return;
-    const int64_t n = i / chunks_per_row;
-    const int c = (int)(i - n * chunks_per_row);
-    const u32x4 d = load_stream(reinterpret_cast<const u32x4*>(w) + i);
-    const f16 s = scales[n * groups_per_row + c / chunks_per_group];
-    const f16x2 ss = {s, s};
-    u32x4* o = reinterpret_cast<u32x4*>(out) + i * 4;
+                  f16* __restrict__ out, int64_t words, int words_per_row,
+                  int words_per_group, int groups_per_row) {
+    const int lane = threadIdx.x & 63;
+    const int64_t base = ((int64_t)blockIdx.x * 256 + (threadIdx.x & ~63)) * 4;   // the wavefront's first word
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(w);
+    uint32_t d[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t u = d[q] ^ 0x88888888u;
-        u32x4 v;
-        v.x = as_u32(unpack_byte_pair<0>(u) * ss);
-        v.y = as_u32(unpack_byte_pair<1>(u) * ss);
-        v.z = as_u32(unpack_byte_pair<2>(u) * ss);
-        v.w = as_u32(unpack_byte_pair<3>(u) * ss);
-        o[q] = v;
+        const int64_t j = base + 64 * q + lane;
+        d[q] = j < words ? __builtin_nontemporal_load(wp + j) : 0u;
+    }
+    // row and word-in-row of word base + lane, then steps of 64 words
+    int64_t n = (base + lane) / words_per_row;
+    int c = (int)(base + lane - n * words_per_row);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t j = base + 64 * q + lane;
+        if (j < words) {
+            const f16 s = scales[n * groups_per_row + c / words_per_group];
+            const f16x2 ss = {s, s};
+            const uint32_t u = d[q] ^ 0x88888888u;
+            u32x4 v;
+            v.x = as_u32(unpack_byte_pair<0>(u) * ss);
+            v.y = as_u32(unpack_byte_pair<1>(u) * ss);
+            v.z = as_u32(unpack_byte_pair<2>(u) * ss);
+            v.w = as_u32(unpack_byte_pair<3>(u) * ss);
+            reinterpret_cast<u32x4*>(out)[j] = v;
+        }
+        c += 64;
+        while (c >= words_per_row) {   // 64 words may cross several short rows
+            c -= words_per_row;
+            ++n;
+        }
     }
 }
 
