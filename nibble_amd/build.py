@@ -50,7 +50,8 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print("\n".join(lines), flush=True)
 
 
-HIP_SOURCES = ["w4a16_hip.hip", "w4a16_decode.hip", "w4a16_pair.hip", "w4a16_stream.hip", "w4a16_gemm.hip"]
+HIP_SOURCES = ["w4a16_hip.hip", "w4a16_decode.hip", "w4a16_pair.hip", "w4a16_stream.hip", "w4a16_gemm.hip",
+               "w4a16_pair_m1.hip"]
 
 
 def build_hip(verbose: bool = False) -> str:

@@ -152,14 +152,15 @@ def test_plan_routing(monkeypatch, m, k, g, act, kernel):
 
 
 @pytest.mark.parametrize("n,k,kernel,rows,splits,unroll", [
-    (8192, 28672, "stream", 4, 4, 2), (4096, 14336, "stream", 2, 8, 3), (8192, 16384, "stream", 2, 8, 3),
+    (8192, 28672, "pair_m1", 4, 2, 6), (4096, 14336, "pair_m1", 2, 2, 10), (8192, 16384, "stream", 2, 8, 3),
     (4096, 32768, "stream", 4, 4, 2), (4096, 16512, "stream", 4, 4, 2),
-    (4096, 11008, "oneshot", 1, 8, 6), (2048, 16384, "oneshot", 1, 8, 8), (28672, 8192, "oneshot", 1, 8, 4),
+    (4096, 11008, "oneshot", 1, 8, 6), (2048, 16384, "oneshot", 1, 8, 8), (28672, 8192, "pair_m1", 7, 1, 6),
     (4096, 34816, "valu", 2, 4, 8),
 ])
 def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
-    """M = 1: long rows of wide layers stream; shorter rows, narrow layers
-    and rows past 32768 keep their kernels."""
+    """M = 1: the paired M = 1 kernel where a launch shape is instantiated
+    for the row length; other long rows of wide layers stream; shorter rows,
+    narrow layers and rows past 32768 keep their kernels."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
@@ -240,6 +241,46 @@ def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
     assert plan["kernel"] == kernel
     if shape:
         assert (plan["rows"], plan["max_blocks"], plan["unroll"], plan["splits"]) == shape
+
+
+@pytest.mark.parametrize("k,n,shape", [
+    (2048, 4096, (3, 1, 8)), (2048, 5632, (3, 1, 8)), (2048, 16383, (3, 1, 8)), (2048, 16384, (8, 1, 4)),
+    (2048, 32000, (8, 1, 4)), (4096, 4096, (2, 2, 8)), (4096, 8191, (2, 2, 8)), (4096, 8192, (8, 1, 6)),
+    (4096, 14336, (8, 1, 6)), (3840, 14336, (2, 2, 8)),   # 15 pairs: 8 per wavefront over 2 slices
+    (5632, 2048, (1, 4, 6)), (6144, 4096, (1, 4, 6)), (5376, 2048, (1, 4, 6)), (8192, 8192, (4, 2, 4)),
+    (8192, 4096, (4, 2, 4)), (8192, 28672, (7, 1, 6)), (7936, 8192, (4, 2, 4)), (14336, 4096, (2, 2, 10)),
+    (14080, 8192, (2, 2, 10)), (28672, 8192, (4, 2, 6)), (28416, 4096, (4, 2, 6)),
+])
+def test_pair_m1_plan_shapes(monkeypatch, k, n, shape):
+    """M = 1, group 128, aligned operands: the paired M = 1 kernel with the
+    launch shape (rows = 8-row-block wavefronts, splits = K slices, unroll =
+    pairs in flight) of its row-length class."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
+    assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("pair_m1", *shape), (k, n)
+
+
+def test_pair_m1_plan_exclusions(monkeypatch):
+    """Shapes the paired M = 1 kernel leaves alone: narrow layers of short
+    rows, K not a multiple of 256 or with no instantiated pairs per
+    wavefront, M > 1, other group sizes, W4A16_ROWS_PER_WARP and v1..v3;
+    W4A16_DECODE=pair_m1 selects it where a shape exists."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    for m, k, n in [(1, 2048, 2048), (1, 2048, 2560), (1, 4096, 2048), (1, 5632, 1024), (1, 14336, 2048),
+                    (1, 2176, 8192), (1, 11008, 4096), (1, 16384, 8192), (2, 4096, 14336), (8, 14336, 4096)]:
+        assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] != "pair_m1", (m, k, n)
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 64)["kernel"] == "generic"
+    monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "valu"
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP")
+    monkeypatch.setenv("W4A16_DECODE", "v3")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "valu_offset"
+    monkeypatch.setenv("W4A16_DECODE", "pair_m1")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "pair_m1"
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "oneshot"   # no shape for N = 64
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 14336, 4096, 128)["kernel"] == "pair_stream"   # M > 1
 
 
 def test_stream_env_selector(monkeypatch):
@@ -337,13 +378,10 @@ def test_oneshot_plan_shapes(monkeypatch):
                                    (256, 1, 8, 1)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("oneshot", rows, splits, loads), k
-    # wide layers: more rows per wavefront on short rows above N = 8192; rows
-    # of 2 loads take 4 wavefronts above N = 8192
-    for k, n, rows, splits, loads in [(2048, 5632, 1, 8, 1), (2048, 8192, 1, 8, 1), (2048, 8193, 2, 4, 1),
-                                      (2048, 16384, 2, 4, 1), (2048, 24575, 2, 4, 1), (2048, 24576, 4, 4, 1),
-                                      (2048, 32000, 4, 4, 1), (1024, 32000, 4, 4, 1), (4096, 4096, 2, 8, 2),
-                                      (4096, 8192, 2, 8, 2), (4096, 8193, 2, 4, 2), (4096, 14336, 2, 4, 2),
-                                      (4096, 32000, 2, 4, 2), (8192, 32000, 1, 8, 4)]:
+    # wide layers the paired M = 1 kernel does not take: more rows per
+    # wavefront on short rows above N = 8192
+    for k, n, rows, splits, loads in [(2048, 2560, 1, 8, 1), (2048, 4095, 1, 8, 1), (1024, 32000, 4, 4, 1),
+                                      (1024, 24576, 4, 4, 1), (4096, 4095, 2, 8, 2), (11008, 8192, 1, 8, 6)]:
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
             ("oneshot", rows, splits, loads), (k, n)

@@ -1,0 +1,104 @@
+"""GPU parity of the paired-layout M = 1 kernel (w4a16_pair_m1.h) against the
+CPU oracle, through the C ABI: every instantiated launch shape (tuned entry
+point), ragged N, K with a shorter last slice, all sixteen nibble codes, the
+default route at full size on every configs shape it takes, the fallback
+for 4-byte misaligned scales, and its rejects. Bar: |err| <= 1e-2 (1 + |ref|)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nibble_amd import _lib
+from tests._cases import assert_parity, expected, make_case
+
+pytestmark = pytest.mark.gpu
+
+PAIR_M1 = _lib.KERNEL_PAIR_M1
+
+# (splits = wavefronts splitting K, rows = 8-row-block wavefronts, unroll =
+# pairs in flight, K values whose pairs per wavefront match the instantiation)
+SHAPES = [
+    (1, 3, 8, (2048,)),
+    (1, 8, 4, (2048,)),
+    (2, 2, 8, (4096, 3840)),            # 3840: 15 pairs, the second slice one short
+    (1, 8, 6, (4096,)),
+    (4, 1, 6, (6144, 5632, 5376)),      # 5632: 22 pairs over 4 slices of 6
+    (2, 4, 4, (8192, 7936)),
+    (1, 7, 6, (8192,)),
+    (2, 2, 10, (14336, 14080)),
+    (2, 4, 6, (28672, 28416)),
+]
+VARIANTS = [(sk, sn, d, k) for sk, sn, d, ks in SHAPES for k in ks]
+
+
+def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0):
+    xd, pd, sd = x.to(dev), p.to(dev), s.to(dev)
+    out = torch.full((x.shape[0], p.shape[0]), float("nan"), dtype=torch.float16, device=dev)
+    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} M={x.shape[0]} K={x.shape[1]} "
+          f"N={p.shape[0]}", flush=True)
+    if kernel is None:
+        _lib.linear_f16(xd, pd, sd, out)
+    else:
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, kernel, rows, splits, unroll)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("splits,rows,unroll,k", VARIANTS)
+@pytest.mark.parametrize("n", [7, 65, 300])
+def test_pair_m1_variants(gpu, splits, rows, unroll, k, n):
+    """Every instantiated shape on ragged N (partial 8-row blocks, a partial
+    last workgroup), against the oracle."""
+    x, p, s = make_case(1, k, n, seed=k + 7 * n + splits)
+    out = _run(gpu, x, p, s, PAIR_M1, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"pair_m1 ({splits},{rows},{unroll}) K={k} N={n}")
+
+
+@pytest.mark.parametrize("splits,rows,unroll,k", [(2, 2, 8, 4096), (4, 1, 6, 5632), (2, 2, 10, 14336)])
+def test_pair_m1_all_nibbles(gpu, splits, rows, unroll, k):
+    """Uniform random bytes (code -8 included) with scales in [0.01, 1.01)."""
+    x, p, s = make_case(1, k, 97, seed=5, all_nibbles=True)
+    out = _run(gpu, x, p, s, PAIR_M1, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"pair_m1 all nibbles K={k}")
+
+
+# every configs shape the default M = 1 route sends to this kernel, at full
+# size (configs[1], [2] at M = 1, [3], and the 1.1B model's lm_head)
+@pytest.mark.parametrize("k,n", [(2048, 5632), (5632, 2048), (4096, 4096), (4096, 14336), (14336, 4096),
+                                 (8192, 8192), (8192, 28672), (28672, 8192), (2048, 32000)])
+def test_pair_m1_default_route_full_size(gpu, k, n):
+    x, p, s = make_case(1, k, n, seed=k ^ (3 * n), device="cuda")
+    assert _lib.plan_linear(16, 16, 1, n, k)["kernel"] == "pair_m1"
+    assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default (pair_m1)")
+
+
+def test_pair_m1_misaligned_scales_fall_back(gpu):
+    """Scales 2-byte but not 4-byte aligned: the default route takes another
+    kernel (this one reads scale pairs as 32-bit words), the tuned entry
+    point rejects it."""
+    k, n = 4096, 14336
+    x, p, s = make_case(1, k, n, seed=21, device="cuda")
+    xd, pd = x.to(gpu), p.to(gpu)
+    buf = torch.empty(s.numel() + 1, dtype=torch.float16, device=gpu)
+    sd = buf[1:].view(n, k // 128)
+    sd.copy_(s.to(gpu))
+    assert sd.data_ptr() % 4 == 2
+    out = torch.full((1, n), float("nan"), dtype=torch.float16, device=gpu)
+    _lib.linear_f16(xd, pd, sd, out)
+    torch.cuda.synchronize()
+    assert_parity(out, expected(x, p, s), "misaligned scales, default route")
+    with pytest.raises(_lib.W4A16Error, match="4-byte aligned"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, PAIR_M1, 8, 1, 6)
+
+
+def test_pair_m1_rejects(gpu):
+    x, p, s = make_case(1, 2176, 16, seed=3)   # 17 groups: K not a multiple of 256
+    with pytest.raises(_lib.W4A16Error, match="multiple of 256"):
+        _run(gpu, x, p, s, PAIR_M1, 3, 1, 8)
+    x, p, s = make_case(1, 4096, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="not instantiated"):
+        _run(gpu, x, p, s, PAIR_M1, 3, 1, 8)     # 16 pairs per wavefront with 3 row wavefronts: no such shape
+    x, p, s = make_case(2, 4096, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="M == 1"):
+        _run(gpu, x, p, s, PAIR_M1, 8, 1, 6)

@@ -161,14 +161,16 @@ def test_oneshot_four_rows_all_nibbles_and_rejects(gpu):
         _run_tuned(gpu, x, p, s, ONESHOT, 4, 4, 0)
 
 
-# the M = 1 default on wide layers of short rows (2 and 4 rows per
-# wavefront) and on 4096 x 4096 (2 rows, 8 wavefronts), at full size
-@pytest.mark.parametrize("k,n,rows,splits", [(2048, 32000, 4, 4), (2048, 16384, 2, 4), (2048, 11264, 2, 4),
-                                             (4096, 4096, 2, 8), (1024, 24577, 4, 4)])
-def test_default_dispatch_wide_m1(gpu, k, n, rows, splits):
+# the M = 1 default on wide layers of short rows (the paired M = 1 kernel;
+# 4 rows per wavefront of the one-shot kernel where K has no paired shape)
+# and on 4096 x 4096, at full size
+@pytest.mark.parametrize("k,n,kernel,rows,splits", [(2048, 32000, "pair_m1", 8, 1), (2048, 16384, "pair_m1", 8, 1),
+                                                    (2048, 11264, "pair_m1", 3, 1), (4096, 4096, "pair_m1", 2, 2),
+                                                    (1024, 24577, "oneshot", 4, 4), (2048, 2560, "oneshot", 1, 8)])
+def test_default_dispatch_wide_m1(gpu, k, n, kernel, rows, splits):
     x, p, s = make_case(1, k, n, seed=k ^ n)
     plan = _lib.plan_linear(16, 16, 1, n, k)
-    assert (plan["kernel"], plan["rows"], plan["splits"]) == ("oneshot", rows, splits)
+    assert (plan["kernel"], plan["rows"], plan["splits"]) == (kernel, rows, splits)
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default")
 
 
