@@ -49,7 +49,7 @@ extern "C" {
 #define W4A16_KERNEL_GEMM_LDS 12     /* GEMM with the activation block staged in LDS per round of groups (large M) */
 #define W4A16_KERNEL_PAIR_SPLIT 13   /* PAIR_STREAM over K slices, fp32 partials in a workspace + reduce (2 <= M <= 8) */
 #define W4A16_KERNEL_GEMM32 14       /* GEMM_LDS on 32x32x16 MFMA tiles (large M, rows of up to 4096 weights) */
-#define W4A16_KERNEL_PAIR_M1 15      /* fp16 MFMA on 8 rows x 2 groups, a ring of loads in flight per wavefront (M = 1) */
+#define W4A16_KERNEL_PAIR_RING 15    /* fp16 MFMA on 8 rows x 2 groups, a ring of loads in flight per wavefront (M <= 8) */
 
 /*
  * Fused W4A16 linear layer.
@@ -208,12 +208,12 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
  *     (the ring runs on into the next rows when a row has fewer steps),
  *     max_blocks = grid (0 = the workgroups resident on the device at once).
- *   W4A16_KERNEL_PAIR_M1 (M = 1, K a multiple of 256, scales 4-byte
- *     aligned): splits = wavefronts splitting K, rows = wavefronts on 8-row
- *     blocks per workgroup, unroll = group pairs in flight per wavefront;
- *     (splits, rows, ceil(K / 256 / splits), unroll) one of (1,3,8,8)
- *     (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6) (2,4,16,4) (1,7,32,6)
- *     (2,2,28,10) (2,4,56,6); max_blocks ignored.
+ *   W4A16_KERNEL_PAIR_RING (1 <= M <= 8, K a multiple of 256, scales
+ *     4-byte aligned): splits = wavefronts splitting K, rows = wavefronts
+ *     on 8-row blocks per workgroup, unroll = group pairs in flight per
+ *     wavefront; at M = 1 (splits, rows, ceil(K / 256 / splits), unroll)
+ *     one of (1,3,8,8) (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6) (2,4,16,4)
+ *     (1,7,32,6) (2,2,28,10) (2,4,56,6); max_blocks ignored.
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
  *     row blocks with the workgroups resident at once; else 1..16), unroll =

@@ -40,14 +40,14 @@ KERNEL_PAIR_STREAM = 11
 KERNEL_GEMM_LDS = 12
 KERNEL_PAIR_SPLIT = 13
 KERNEL_GEMM32 = 14
-KERNEL_PAIR_M1 = 15
+KERNEL_PAIR_RING = 15
 KERNEL_NAMES = {KERNEL_NONE: "none", KERNEL_VALU: "valu", KERNEL_MFMA: "mfma", KERNEL_GENERIC: "generic",
                 KERNEL_DIAG: "diag", KERNEL_VALU_OFFSET: "valu_offset",
                 KERNEL_ONESHOT: "oneshot", KERNEL_MFMA_ONESHOT: "mfma_oneshot",
                 KERNEL_MFMA_PAIR: "mfma_pair", KERNEL_STREAM: "stream",
                 KERNEL_GEMM: "gemm", KERNEL_PAIR_STREAM: "pair_stream",
                 KERNEL_GEMM_LDS: "gemm_lds", KERNEL_PAIR_SPLIT: "pair_split", KERNEL_GEMM32: "gemm32",
-                KERNEL_PAIR_M1: "pair_m1"}
+                KERNEL_PAIR_RING: "pair_ring"}
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

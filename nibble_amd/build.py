@@ -51,7 +51,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 HIP_SOURCES = ["w4a16_hip.hip", "w4a16_decode.hip", "w4a16_pair.hip", "w4a16_stream.hip", "w4a16_gemm.hip",
-               "w4a16_pair_m1.hip"]
+               "w4a16_pair_ring.hip"]
 
 
 def build_hip(verbose: bool = False) -> str:

@@ -40,11 +40,11 @@ int64_t pair_split_workspace_bytes(int64_t M, int64_t N, int slices);
 bool pair_split_valid(int64_t K, int slices);
 int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, const void* x, const uint8_t* w,
                       const void* s, void* o, int N, int K, void* part, int64_t part_bytes, hipStream_t stream);
-// w4a16_pair_m1.hip: the paired-layout MFMA kernel for M = 1
-int pair_m1_ppw(int64_t K, int sk);
-bool pair_m1_instantiated(int64_t K, int sk, int sn, int depth);
-int launch_pair_m1(int sk, int sn, int depth, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
-                   w4a16::f16* o, int N, int K, hipStream_t stream);
+// w4a16_pair_ring.hip: the paired-layout ring MFMA kernel for M = 1..8
+int pair_ring_ppw(int64_t K, int sk);
+bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth);
+int launch_pair_ring(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
+                     w4a16::f16* o, int N, int K, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -152,7 +152,7 @@ int read_decode_env() {
         {"mfma_pair", W4A16_KERNEL_MFMA_PAIR},
         {"stream", W4A16_KERNEL_STREAM},
         {"pair_stream", W4A16_KERNEL_PAIR_STREAM},
-        {"pair_m1", W4A16_KERNEL_PAIR_M1},
+        {"pair_ring", W4A16_KERNEL_PAIR_RING},
     };
     for (const auto& e : kNames)
         if (std::strcmp(d, e.name) == 0) return e.family;
@@ -530,24 +530,36 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
            w4a16_internal::gemm_instantiated(p.rows, p.max_blocks, p.splits);
 }
 
-// M = 1 on the paired-layout MFMA kernel (w4a16_pair_m1.h). Plan fields:
-// splits = wavefronts splitting K, rows = wavefronts on 8-row blocks per
-// workgroup, unroll = pairs in flight per wavefront. Launch shapes from a
-// sweep of (splits, rows, pairs in flight) per layer shape (graph timing
-// over rotated copies, one box), against the kernels these layers took
-// before (one-shot VALU, or the streaming VALU kernel on rows of 14336 and
-// more), us per call:
-//   4096 x 14336: (1, 8, 6) 6.34 against 7.88; 14336 x 4096: (2, 2, 10)
-//   6.56 against 7.78; 8192 x 8192: (2, 4, 4) 6.96 against 8.56; 8192 x
-//   28672: (1, 7, 6) 21.1 against 21.5; 28672 x 8192: (2, 4, 6) 20.2
-//   against 21.5; 2048 x 32000: (1, 8, 4) 7.13 against 7.91; 4096 x 4096:
-//   (2, 2, 8) 3.54 against 3.73; 5632 x 2048: (4, 1, 6) 3.27 against 3.46;
-//   2048 x 5632: (1, 3, 8) 3.19 against 3.25.
-// Layers of 2048 x N with N < 4096 keep the one-shot kernel (2048 x 2048:
-// 2.64 against 2.55; 2048 x 2560: 2.86 against 2.71). Only the instantiated
-// shapes are taken (K a multiple of 256 whose pairs per wavefront match).
-bool plan_pair_m1(int64_t N, int64_t K, Plan* out) {
-    if (K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
+// M = 1..8 on the paired-layout ring MFMA kernel (w4a16_pair_ring.h). Plan
+// fields: splits = wavefronts splitting K, rows = wavefronts on 8-row blocks
+// per workgroup, unroll = pairs in flight per wavefront. Launch shapes from
+// sweeps of (splits, rows, pairs in flight) per layer shape and M (graph
+// timing over rotated copies, one box), against the kernels these layers
+// took before (one-shot VALU, streaming VALU on rows of 14336 and more,
+// paired / streaming paired MFMA at M >= 2), us per call:
+//   M = 1: 4096 x 14336 (1, 8, 6) 6.34 against 7.88; 14336 x 4096 (2, 2,
+//   10) 6.56 against 7.78; 8192 x 8192 (2, 4, 4) 6.96 against 8.56; 8192 x
+//   28672 (1, 7, 6) 21.1 against 21.5; 28672 x 8192 (2, 4, 6) 20.2 against
+//   21.5; 2048 x 32000 (1, 8, 4) 7.13 against 7.91; 4096 x 4096 (2, 2, 8)
+//   3.54 against 3.73; 5632 x 2048 (4, 1, 6) 3.27 against 3.46; 2048 x
+//   5632 (1, 3, 8) 3.19 against 3.25; 2048 x N < 4096 keeps the one-shot
+//   kernel (2048 x 2048 2.64 against 2.55, 2048 x 2560 2.86 against 2.71).
+//   M = 8: 4096 x 14336 (1, 8, 6) 7.76 against 10.80; 8192 x 8192 (2, 4, 4)
+//   9.83 against 11.82; 4096 x 4096 (4, 2, 4) 4.59 against 5.19; 2048 x
+//   5632 (1, 4, 6) 3.71 against 4.35; 2048 x 2048 (4, 1, 2) 3.09 against
+//   3.23. M = 4: 4096 x 14336 7.19 against 10.12; 8192 x 8192 8.34 against
+//   10.28; 14336 x 4096 (4, 2, 6) 9.03 against 9.87; 5632 x 2048 (8, 1, 3)
+//   4.25 against 4.70; 4096 x 4096 (2, 2, 4) 4.17 against 4.71. M = 2: 4096
+//   x 14336 7.03 against 9.66; 8192 x 8192 7.99 against 10.03; 14336 x 4096
+//   8.52 against 9.17.
+// Kept on their kernels: M = 2 and 5..8 on 5632 x 2048 (tied: 3.90 / 5.45
+// against 3.88 / 5.40; every CU stages all M K activations for one 8-row
+// block), M = 5..8 on rows longer than 8192 (M K activations past LDS) and
+// M >= 2 on wider layers of long rows (N > 8192 with K >= 8192). Only
+// instantiated shapes are taken (K a multiple of 256 whose pairs per
+// wavefront match).
+bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out) {
+    if (M < 1 || M > 8 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
     const int64_t P = K / 256;
     struct Shape {
         int sk, sn, d;
@@ -555,26 +567,43 @@ bool plan_pair_m1(int64_t N, int64_t K, Plan* out) {
     // candidates in order of preference for the row-length class; the first
     // whose pairs per wavefront are instantiated is taken
     Shape c[2] = {{0, 0, 0}, {0, 0, 0}};
-    if (P <= 8) {
-        if (N >= 16384) c[0] = {1, 8, 4};
-        else if (N >= 4096) c[0] = {1, 3, 8};
-    } else if (P <= 16) {
-        if (N >= 8192) c[0] = {1, 8, 6}, c[1] = {2, 2, 8};
-        else if (N >= 4096) c[0] = {2, 2, 8};
-    } else if (P <= 24) {
-        if (N >= 2048) c[0] = {4, 1, 6};
-    } else if (P <= 32) {
-        if (N >= 16384) c[0] = {1, 7, 6}, c[1] = {2, 4, 4};
-        else if (N >= 4096) c[0] = {2, 4, 4};
-    } else if (P <= 56) {
-        if (N >= 4096) c[0] = {2, 2, 10};
-    } else if (P <= 112) {
-        if (N >= 4096) c[0] = {2, 4, 6};
+    if (M == 1) {
+        if (P <= 8) {
+            if (N >= 16384) c[0] = {1, 8, 4};
+            else if (N >= 4096) c[0] = {1, 3, 8};
+        } else if (P <= 16) {
+            if (N >= 8192) c[0] = {1, 8, 6}, c[1] = {2, 2, 8};
+            else if (N >= 4096) c[0] = {2, 2, 8};
+        } else if (P <= 24) {
+            if (N >= 2048) c[0] = {4, 1, 6};
+        } else if (P <= 32) {
+            if (N >= 16384) c[0] = {1, 7, 6}, c[1] = {2, 4, 4};
+            else if (N >= 4096) c[0] = {2, 4, 4};
+        } else if (P <= 56) {
+            if (N >= 4096) c[0] = {2, 2, 10};
+        } else if (P <= 112) {
+            if (N >= 4096) c[0] = {2, 4, 6};
+        }
+    } else {
+        const bool wide = M > 4;
+        if (P <= 8) {
+            if (N >= 1024 && N <= 2048) c[0] = {4, 1, 2};
+            else if (N > 2048 && N <= 8192) c[0] = {1, 4, 6};
+        } else if (P <= 16) {
+            if (N >= 8192) c[0] = {1, 8, 6};
+            else if (N >= 4096) c[0] = wide ? Shape{4, 2, 4} : Shape{2, 2, 4};
+        } else if (P <= 24) {
+            if (M >= 3 && M <= 4 && N >= 2048 && N <= 4096) c[0] = {8, 1, 3};
+        } else if (P <= 32) {
+            if (N >= 6144 && N <= 8192) c[0] = {2, 4, 4};
+        } else if (P <= 56) {
+            if (!wide && N >= 4096 && N <= 8192) c[0] = {4, 2, 6};
+        }
     }
     for (const Shape& e : c) {
-        if (e.sk == 0 || !w4a16_internal::pair_m1_instantiated(K, e.sk, e.sn, e.d)) continue;
+        if (e.sk == 0 || !w4a16_internal::pair_ring_instantiated(M, K, e.sk, e.sn, e.d)) continue;
         Plan p;
-        p.kernel = W4A16_KERNEL_PAIR_M1;
+        p.kernel = W4A16_KERNEL_PAIR_RING;
         p.splits = e.sk;
         p.rows = e.sn;
         p.unroll = e.d;
@@ -849,9 +878,9 @@ int make_plan(const void* act, const void* packed, const void* scales, int64_t M
     //   otherwise the looped VALU kernel for M = 1, M = 2 (K <= 16384) or
     //   M <= 4 (K <= 4096), else the looped MFMA kernel.
     const bool scales4 = (reinterpret_cast<uintptr_t>(scales) & 3u) == 0;
-    if ((family == 0 || family == W4A16_KERNEL_PAIR_M1) && rows == 0 && M == 1 && scales4 && plan_pair_m1(N, K, out))
+    if ((family == 0 || family == W4A16_KERNEL_PAIR_RING) && rows == 0 && scales4 && plan_pair_ring(M, N, K, out))
         return W4A16_OK;
-    if (family == W4A16_KERNEL_PAIR_M1) family = 0;   // M > 1 or a shape without an instantiation
+    if (family == W4A16_KERNEL_PAIR_RING) family = 0;   // a shape without an instantiation
     if (family == 0 && rows == 0 && workspace && pair_split_route(M, N, K)) {
         *out = plan_pair_split(M, N, K);
         return W4A16_OK;
@@ -1196,8 +1225,9 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_MFMA_ONESHOT: return launch_mfma_oneshot(p, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_MFMA_PAIR:
             return launch_mfma_pair_rows(p, own_plans, (int)M, x, packed, s, o, (int)N, (int)K, st);
-        case W4A16_KERNEL_PAIR_M1:
-            return w4a16_internal::launch_pair_m1(p.splits, p.rows, p.unroll, x, packed, s, o, (int)N, (int)K, st);
+        case W4A16_KERNEL_PAIR_RING:
+            return w4a16_internal::launch_pair_ring(p.splits, p.rows, p.unroll, (int)M, x, packed, s, o, (int)N, (int)K,
+                                                    st);
         case W4A16_KERNEL_STREAM:
             return w4a16_internal::launch_stream(p.rows, p.splits, p.unroll, p.max_blocks, x, packed, s, o, (int)N,
                                                  (int)K, st);
@@ -1400,11 +1430,11 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
             return fail(W4A16_ERR_CONFIG,
                         "the streaming kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
                         "weights");
-    } else if (kernel == W4A16_KERNEL_PAIR_M1) {
-        if (group_size != 128 || M != 1 || !aligned16(activations) || !aligned16(packed_weights))
+    } else if (kernel == W4A16_KERNEL_PAIR_RING) {
+        if (group_size != 128 || M < 1 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
-                        "the paired M = 1 kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
-                        "weights");
+                        "the paired ring kernel needs group_size 128, 1 <= M <= 8 and 16-byte aligned activations "
+                        "and weights");
     } else if (kernel == W4A16_KERNEL_PAIR_STREAM) {
         if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
@@ -1432,7 +1462,7 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
     } else if (kernel != W4A16_KERNEL_GENERIC) {
         return fail(W4A16_ERR_CONFIG,
                     "kernel must be W4A16_KERNEL_VALU, _VALU_OFFSET, _ONESHOT, _MFMA, _MFMA_ONESHOT, _MFMA_PAIR, "
-                    "_PAIR_STREAM, _PAIR_SPLIT, _PAIR_M1, _STREAM, _GEMM, _GEMM_LDS, _GEMM32, _DIAG or _GENERIC");
+                    "_PAIR_STREAM, _PAIR_SPLIT, _PAIR_RING, _STREAM, _GEMM, _GEMM_LDS, _GEMM32, _DIAG or _GENERIC");
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, false, workspace,
                     workspace_bytes);

@@ -1,0 +1,301 @@
+// Small-batch GEMV (M = 1..8) on the matrix cores in the paired layout, with
+// a ring of weight loads in flight per wavefront, for gfx950. Kept apart
+// from w4a16_kernels.h so its instantiations build in their own
+// translation unit.
+#pragma once
+
+#include "w4a16_device.h"
+
+namespace w4a16 {
+
+// ---------------------------------------------------------------------------
+// Paired-layout ring GEMV, G = 128, G even, runtime M <= MS (MS = 1, 4 or 8
+// row slots).
+//
+// Operand layout of v_mfma_f32_16x16x32_f16 (lane l = 16 q + c): lane l
+// supplies A row c, k = 8q .. 8q + 7 and B column c, k = 8q .. 8q + 7, and
+// receives D rows 4q .. 4q + 3 of column c. Column c of B is weight row
+// c & 7 of an 8-row block, group 2p + (c >> 3) of group pair p: the lane
+// loads bytes 16q .. 16q + 15 of that group, so one load instruction reads
+// 8 rows x 128 contiguous bytes, and its four 32-bit words are the B
+// operands of the pair's four MFMAs (word t: k = 32q + 8t .. + 7 of the
+// group). A row c holds activation row c & 7 (M = 1: row 0 in every A row)
+// of the group of half c >> 3, so D[i][c] is a wanted product when i and c
+// lie in the same half: D rows 0..7 x columns 0..7 (lanes 0..7 and 16..23,
+// group 2p) and D rows 8..15 x columns 8..15 (lanes 40..47 and 56..63,
+// group 2p + 1). The halves of an output are added at the end (lane l + 40
+// onto lane l); the cross-half blocks are dropped. The MFMA count per byte of
+// weights does not depend on M.
+//
+// Offset decode: B holds the codes without fix-ups (even k as 1024 + v, odd
+// k as 1024 + 16 v with v = s + 8, one shift and four v_bitop3 per word); A
+// holds the activations permuted to the same pair order with the odd-k
+// halves scaled by 1/16 (exact for normal fp16), so the chain's sum is
+// sum(x s) + 1032 sum(x_even) + 1152 sum(x_odd / 16). The activation term is
+// computed once per (group, activation row) while staging and each chain
+// starts from its negative, loaded into the accumulator straight from LDS.
+// The group scale then multiplies the chain's result in fp32 FMAs (one at M =
+// 1, four otherwise). VALU work per 8 rows x 128 weights: 20 decode
+// instructions and 1 or 4 FMAs.
+//
+// Workgroup = SK x SN wavefronts; wavefront (kw, nb) owns RB blocks of 8 rows
+// and pairs kw PPW .. kw PPW + PPW - 1. Order of requests: the workgroup's
+// activation units, its scale words, then the wavefront's first D pairs of
+// weights (a wavefront's loads return in issue order). Staging writes the
+// permuted units, the per-(group, row) bias and the workgroup's scales as
+// fp32 split by half (s[row][h][p] = scale of group 2p + h), one barrier,
+// then pair j is decoded as its load arrives, pair j + D is requested into
+// the registers it freed, and pair j goes through the MFMAs. Requesting every
+// pair up front (D = PPW) measured slower: the memory pipeline accepts
+// requests at its own pace, so a wavefront that issues all of them sits at
+// the issue of its later loads while its first pairs have long arrived, the
+// staging and every multiply wait until the last request is out (about
+// 3.5 us into a 4096 x 14336 call, from in-kernel timestamps) and the
+// arithmetic then runs as a burst after the stream (7.05 against 6.34 us at
+// that shape and M = 1). Pairs past K (SK PPW > G/2) re-read the last pair
+// with zero activations, zero bias and zero scale. SK > 1: the K slices'
+// partial sums are added in slice order through LDS.
+//
+// Staged activations: unit (m, g, u) (row m, k = 128 g + 8 u .. + 7) at byte
+// m RS + 272 g + 16 u. The group stride of 272 bytes and a row stride RS
+// = 32 mod 256 put the 16 units one A-fragment read takes from a DPP row of
+// lanes (8 rows x 2 groups) on distinct 16-byte bank slots; staging writes
+// 16 consecutive units per DPP row.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int pair_ring_group_bytes() { return 272; }
+
+__host__ __device__ constexpr int64_t pair_ring_row_bytes(int SK, int PPW) {
+    // 2 SK PPW groups of 272 bytes, padded to 32 mod 256
+    return ((int64_t)2 * SK * PPW * 272 + 224 + 255) / 256 * 256 - 224;
+}
+
+__host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN, int RB, int PPW) {
+    return (MS == 1 ? (int64_t)2 * SK * PPW * 272 : MS * pair_ring_row_bytes(SK, PPW))   // staged units
+           + (int64_t)2 * SK * PPW * (MS == 1 ? 1 : 8) * 4                              // per-(group, row) bias
+           + (int64_t)8 * RB * SN * 2 * SK * PPW * 4                                    // fp32 scales
+           + (SK > 1 ? (int64_t)SN * RB * SK * (MS == 1 ? 8 : 64) * 4 : 0);            // K-slice partials
+}
+
+template <int MS, int SK, int SN, int RB, int PPW, int D>
+__global__ void __launch_bounds__(64 * SK * SN)
+gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
+               f16* __restrict__ out, int M, int N, int K) {
+    static_assert(MS == 1 || MS == 4 || MS == 8, "1, 4 or 8 activation row slots");
+    static_assert(D >= 1 && D <= PPW, "ring depth 1 .. PPW");
+    constexpr int W = SK * SN;
+    constexpr int T = 64 * W;
+    constexpr int PS = SK * PPW;              // pairs staged
+    constexpr int GS = 2 * PS;                // groups staged
+    constexpr int US = GS * 16;               // activation units staged per row
+    constexpr int XU = (MS * US + T - 1) / T; // staging units per thread
+    constexpr int R = 8 * RB * SN;            // rows per workgroup
+    constexpr int SD = R * PS;                // scale words (pairs) per workgroup
+    constexpr int SU = (SD + T - 1) / T;      // scale words per thread
+    constexpr int RS = MS == 1 ? 0 : (int)pair_ring_row_bytes(SK, PPW);
+    constexpr int XB = MS == 1 ? GS * 272 : MS * RS;
+    constexpr int BS = MS == 1 ? 1 : 8;       // bias slots per group
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* bias = reinterpret_cast<float*>(smem + XB);   // [GS][BS]
+    float* sc = bias + GS * BS;                            // [R][2][PS]
+    float* red = sc + R * 2 * PS;                          // [SN RB][SK][8 or 64]
+
+    const int G = K >> 7;
+    const int P = G >> 1;
+    const int units = K >> 3;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15, q = lane >> 4;
+    const int brow = col & 7, h = col >> 3;
+    const int kw = wave % SK, nb = wave / SK;
+    const int n0 = blockIdx.x * R;
+    const int nw = n0 + nb * RB * 8;
+    const uint32_t row_bytes = (uint32_t)(K >> 1);
+
+    // 1. requests: activation units (clamped; units past K or M are not
+    // staged), the workgroup's scale words, then the wavefront's first D
+    // pairs of weights
+    u32x4 a[XU];
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+        const int i = threadIdx.x + u * T;
+        const int m = MS == 1 ? 0 : min(i / US, M - 1);
+        const int uu = min(MS == 1 ? i : i % US, units - 1);
+        a[u] = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + (size_t)uu * 8);
+    }
+    const uint32_t* s32 = reinterpret_cast<const uint32_t*>(scales);
+    uint32_t sw[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+        const int d = threadIdx.x + u * T;
+        const int r = d / PS, p = d - r * PS;
+        const int n = min(n0 + r, N - 1);
+        sw[u] = s32[(size_t)n * P + min(p, P - 1)];
+    }
+    // weights of pair j go to ring slot j % D
+    u32x4 wv[D][RB];
+    auto issue = [&](int j) {
+        const uint32_t pg = (uint32_t)min(kw * PPW + j, P - 1);
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            const int n = min(nw + 8 * b + brow, N - 1);
+            wv[j % D][b] = load_stream(reinterpret_cast<const u32x4*>(w + (size_t)n * row_bytes + pg * 128u +
+                                                                     (uint32_t)(h * 64 + q * 16)));
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < D; ++j) issue(j);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. staging: unit i = m US + uu covers x[m][8 uu .. 8 uu + 7] (group
+    // uu / 16); the 16 units of a (row, group) sit in one DPP row, whose sum
+    // is that row's bias for the group
+    const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 c_even = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 c_odd = {(f16)1152.0f, (f16)1152.0f};
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+        const int i = threadIdx.x + u * T;
+        const int m = MS == 1 ? 0 : i / US;
+        const int uu = MS == 1 ? i : i % US;
+        u32x4 v = permute8(a[u]);
+        v.y = as_u32(as_f16x2(v.y) * sixteenth);
+        v.w = as_u32(as_f16x2(v.w) * sixteenth);
+        if (uu >= units) v = (u32x4){0u, 0u, 0u, 0u};
+        float cs = __builtin_amdgcn_fdot2(as_f16x2(v.x), c_even, 0.0f, false);
+        cs = __builtin_amdgcn_fdot2(as_f16x2(v.y), c_odd, cs, false);
+        cs = __builtin_amdgcn_fdot2(as_f16x2(v.z), c_even, cs, false);
+        cs = __builtin_amdgcn_fdot2(as_f16x2(v.w), c_odd, cs, false);
+        cs += dpp<0xB1>(cs);
+        cs += dpp<0x4E>(cs);
+        cs += dpp<0x141>(cs);
+        cs += dpp<0x140>(cs);
+        if ((MS == 1 ? i < US : m < M) && i < MS * US) {
+            const int g = uu >> 4;
+            *reinterpret_cast<u32x4*>(smem + (MS == 1 ? 0 : m * RS) + g * 272 + (uu & 15) * 16) = v;
+            if ((uu & 15) == 0) bias[g * BS + (MS == 1 ? 0 : m)] = -cs;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+        const int d = threadIdx.x + u * T;
+        const int r = d / PS, p = d - r * PS;
+        if (d < SD) {
+            const bool ok = p < P;
+            const f16x2 sv = as_f16x2(sw[u]);
+            sc[(2 * r) * PS + p] = ok ? (float)sv.x : 0.0f;
+            sc[(2 * r + 1) * PS + p] = ok ? (float)sv.y : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // 3. pairs in arrival order; A fragments of pair j + 1 read during pair j.
+    // A row c = activation row c & 7 (clamped to M - 1) of group 2p + h; D
+    // rows 4q .. 4q + 3 = activation rows 4 (q & 1) .. + 3 of group
+    // 2p + (q >> 1)
+    const int arow = MS == 1 ? 0 : min(brow, M - 1);
+    const uint8_t* xl = smem + (MS == 1 ? 0 : arow * RS) + (2 * kw * PPW + h) * 272 + q * 64;
+    const float* bl = MS == 1 ? bias + 2 * kw * PPW + h : bias + (2 * kw * PPW + (q >> 1)) * 8 + 4 * (q & 1);
+    const float* scl[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) scl[b] = sc + (2 * (8 * (nb * RB + b) + brow) + h) * PS + kw * PPW;
+    constexpr int NA = MS == 1 ? 1 : 4;   // accumulators per lane
+    float acc[RB][NA];
+    f32x4 d[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+#pragma unroll
+        for (int e = 0; e < NA; ++e) acc[b][e] = 0.0f;
+        d[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    u32x4 A0[4], A1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) A0[t] = *reinterpret_cast<const u32x4*>(xl + t * 16);
+#pragma unroll
+    for (int j = 0; j < PPW; ++j) {
+        u32x4 (&cur)[4] = (j & 1) ? A1 : A0;
+        u32x4 (&nxt)[4] = (j & 1) ? A0 : A1;
+        if (j + 1 < PPW) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) nxt[t] = *reinterpret_cast<const u32x4*>(xl + (j + 1) * 544 + t * 16);
+        }
+        f32x4 bj;
+        if constexpr (MS == 1) bj.x = bl[2 * j];
+        else bj = *reinterpret_cast<const f32x4*>(bl + 16 * j);
+        Codes8 cw[RB][4];
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cw[b][t] = unpack8_offset(wv[j % D][b][t]);
+        if (j + D < PPW) {
+            // the slot is free once decoded: request pair j + D
+            __builtin_amdgcn_sched_barrier(0);
+            issue(j + D);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            f32x4 dd = d[b];
+            if constexpr (MS == 1) dd.x = bj.x;   // registers 1..3 carry unused values
+            else dd = bj;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const f16x8 bt = __builtin_bit_cast(f16x8, (u32x4){as_u32(cw[b][t].p[0]), as_u32(cw[b][t].p[1]),
+                                                                   as_u32(cw[b][t].p[2]), as_u32(cw[b][t].p[3])});
+                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[t]), bt, dd, 0, 0, 0);
+            }
+            const float s = scl[b][j];
+#pragma unroll
+            for (int e = 0; e < NA; ++e) acc[b][e] = __builtin_fmaf(dd[e], s, acc[b][e]);
+            d[b] = dd;
+        }
+    }
+
+    // 4. halves (lane l + 40 onto lane l), then the K slices in order. M = 1:
+    // lane c < 8 holds row c; else lane 16 q + c (q < 2, c < 8) holds
+    // activation rows 4q .. 4q + 3 of weight row c.
+    constexpr int RED = MS == 1 ? 8 : 64;
+    const bool keep = MS == 1 ? lane < 8 : (q < 2 && col < 8);
+    const int rl = MS == 1 ? lane : (q * 8 + col) * 4;   // slot in a block's partials
+    float v[RB][NA];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int e = 0; e < NA; ++e) v[b][e] = acc[b][e] + __shfl(acc[b][e], lane + 40);
+    auto store = [&](int b, const float (&vb)[NA]) {
+        const int n = nw + 8 * b + brow;
+        if (n >= N) return;
+#pragma unroll
+        for (int e = 0; e < NA; ++e) {
+            const int m = MS == 1 ? 0 : 4 * q + e;
+            if (MS == 1 || m < M) out[(size_t)m * N + n] = (f16)vb[e];
+        }
+    };
+    if constexpr (SK == 1) {
+        if (keep) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b) store(b, v[b]);
+        }
+    } else {
+        if (keep) {
+#pragma unroll
+            for (int b = 0; b < RB; ++b)
+#pragma unroll
+                for (int e = 0; e < NA; ++e) red[((nb * RB + b) * SK + kw) * RED + rl + e] = v[b][e];
+        }
+        __syncthreads();
+        if (kw != 0 || !keep) return;
+#pragma unroll
+        for (int b = 0; b < RB; ++b) {
+            float t[NA];
+#pragma unroll
+            for (int e = 0; e < NA; ++e) {
+                t[e] = red[((nb * RB + b) * SK) * RED + rl + e];
+#pragma unroll
+                for (int s = 1; s < SK; ++s) t[e] += red[((nb * RB + b) * SK + s) * RED + rl + e];
+            }
+            store(b, t);
+        }
+    }
+}
+
+}  // namespace w4a16

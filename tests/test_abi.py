@@ -152,9 +152,9 @@ def test_plan_routing(monkeypatch, m, k, g, act, kernel):
 
 
 @pytest.mark.parametrize("n,k,kernel,rows,splits,unroll", [
-    (8192, 28672, "pair_m1", 4, 2, 6), (4096, 14336, "pair_m1", 2, 2, 10), (8192, 16384, "stream", 2, 8, 3),
+    (8192, 28672, "pair_ring", 4, 2, 6), (4096, 14336, "pair_ring", 2, 2, 10), (8192, 16384, "stream", 2, 8, 3),
     (4096, 32768, "stream", 4, 4, 2), (4096, 16512, "stream", 4, 4, 2),
-    (4096, 11008, "oneshot", 1, 8, 6), (2048, 16384, "oneshot", 1, 8, 8), (28672, 8192, "pair_m1", 7, 1, 6),
+    (4096, 11008, "oneshot", 1, 8, 6), (2048, 16384, "oneshot", 1, 8, 8), (28672, 8192, "pair_ring", 7, 1, 6),
     (4096, 34816, "valu", 2, 4, 8),
 ])
 def test_stream_plan_shapes(monkeypatch, n, k, kernel, rows, splits, unroll):
@@ -189,16 +189,17 @@ def test_gemm_plan_shapes(monkeypatch, m, n, k, rows, blocks, splits):
 
 
 @pytest.mark.parametrize("m,n,k,kernel,waves", [
-    (8, 28672, 8192, "pair_stream", 16), (4, 28672, 8192, "pair_stream", 16), (8, 14336, 4096, "pair_stream", 8),
-    (3, 14336, 4096, "pair_stream", 8), (4, 14336, 14336, "pair_stream", 8),
+    (8, 28672, 8192, "pair_stream", 16), (4, 28672, 8192, "pair_stream", 16), (8, 14336, 4096, "pair_ring", 0),
+    (3, 14336, 4096, "pair_ring", 0), (4, 14336, 14336, "pair_stream", 8),
     (8, 14336, 14336, "mfma_pair", 0),    # 8 x 14336 activations do not fit in LDS
-    (8, 8192, 8192, "mfma_pair", 0), (8, 14336, 2048, "mfma_pair", 0), (2, 28672, 8192, "pair_stream", 16),
-    (2, 14336, 4096, "mfma_pair", 0),     # M = 2 streams only rows above 4096 weights
+    (8, 8192, 8192, "pair_ring", 0), (8, 14336, 2048, "mfma_pair", 0), (2, 28672, 8192, "pair_stream", 16),
+    (2, 14336, 4096, "pair_ring", 0), (5, 14336, 8192, "pair_stream", 8),
 ])
 def test_pair_stream_routing(monkeypatch, m, n, k, kernel, waves):
     """M >= 3 on wide layers (N >= 14336, K >= 4096) whose activations fit
-    in LDS: the streaming paired kernel, 4 pairs in flight, 16 wavefronts
-    from 3072 row blocks of 8, else 8."""
+    in LDS and that the ring kernel does not take: the streaming paired
+    kernel, 4 pairs in flight, 16 wavefronts from 3072 row blocks of 8, else
+    8."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
@@ -251,36 +252,52 @@ def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
     (8192, 4096, (4, 2, 4)), (8192, 28672, (7, 1, 6)), (7936, 8192, (4, 2, 4)), (14336, 4096, (2, 2, 10)),
     (14080, 8192, (2, 2, 10)), (28672, 8192, (4, 2, 6)), (28416, 4096, (4, 2, 6)),
 ])
-def test_pair_m1_plan_shapes(monkeypatch, k, n, shape):
+def test_pair_ring_m1_plan_shapes(monkeypatch, k, n, shape):
     """M = 1, group 128, aligned operands: the paired M = 1 kernel with the
     launch shape (rows = 8-row-block wavefronts, splits = K slices, unroll =
     pairs in flight) of its row-length class."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
-    assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("pair_m1", *shape), (k, n)
+    assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("pair_ring", *shape), (k, n)
 
 
-def test_pair_m1_plan_exclusions(monkeypatch):
-    """Shapes the paired M = 1 kernel leaves alone: narrow layers of short
-    rows, K not a multiple of 256 or with no instantiated pairs per
-    wavefront, M > 1, other group sizes, W4A16_ROWS_PER_WARP and v1..v3;
-    W4A16_DECODE=pair_m1 selects it where a shape exists."""
+@pytest.mark.parametrize("m,k,n,shape", [
+    (2, 2048, 2048, (1, 4, 2)), (8, 2048, 1024, (1, 4, 2)), (4, 2048, 5632, (4, 1, 6)), (8, 2048, 8192, (4, 1, 6)),
+    (2, 4096, 4096, (2, 2, 4)), (8, 4096, 4096, (2, 4, 4)), (5, 4096, 6000, (2, 4, 4)), (3, 4096, 14336, (8, 1, 6)),
+    (8, 4096, 28672, (8, 1, 6)), (3, 5632, 2048, (1, 8, 3)), (4, 6144, 4096, (1, 8, 3)), (2, 8192, 8192, (4, 2, 4)),
+    (8, 8192, 6144, (4, 2, 4)), (2, 14336, 4096, (2, 4, 6)), (4, 14336, 8192, (2, 4, 6)),
+])
+def test_pair_ring_small_batch_plan_shapes(monkeypatch, m, k, n, shape):
+    """M = 2..8: the ring kernel's (rows, splits, unroll) per row-length
+    class and row slots (4 up to M = 4, 8 beyond)."""
+    monkeypatch.delenv("W4A16_DECODE", raising=False)
+    monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+    assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == ("pair_ring", *shape), (m, k, n)
+
+
+def test_pair_ring_m1_plan_exclusions(monkeypatch):
+    """Shapes the ring kernel leaves alone: narrow layers of short rows,
+    K not a multiple of 256 or with no instantiated pairs per wavefront,
+    narrow layers at M = 2, long rows at M > 4, other group sizes,
+    W4A16_ROWS_PER_WARP and v1..v3; W4A16_DECODE=pair_ring selects it where
+    a shape exists."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
     for m, k, n in [(1, 2048, 2048), (1, 2048, 2560), (1, 4096, 2048), (1, 5632, 1024), (1, 14336, 2048),
-                    (1, 2176, 8192), (1, 11008, 4096), (1, 16384, 8192), (2, 4096, 14336), (8, 14336, 4096)]:
-        assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] != "pair_m1", (m, k, n)
+                    (1, 2176, 8192), (1, 11008, 4096), (1, 16384, 8192), (2, 5632, 2048), (8, 14336, 4096)]:
+        assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] != "pair_ring", (m, k, n)
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 64)["kernel"] == "generic"
     monkeypatch.setenv("W4A16_ROWS_PER_WARP", "2")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "valu"
     monkeypatch.delenv("W4A16_ROWS_PER_WARP")
     monkeypatch.setenv("W4A16_DECODE", "v3")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "valu_offset"
-    monkeypatch.setenv("W4A16_DECODE", "pair_m1")
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "pair_m1"
+    monkeypatch.setenv("W4A16_DECODE", "pair_ring")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 14336, 4096, 128)["kernel"] == "pair_ring"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 1, 64, 2048, 128)["kernel"] == "oneshot"   # no shape for N = 64
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 4, 14336, 4096, 128)["kernel"] == "pair_stream"   # M > 1
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 8, 14336, 14336, 128)["kernel"] == "mfma_pair"   # no shape
 
 
 def test_stream_env_selector(monkeypatch):
@@ -337,17 +354,18 @@ def test_mfma_oneshot_plan_shapes(monkeypatch):
 
 
 def test_m2_routing(monkeypatch):
-    """M = 2: the paired kernel on wide layers of rows up to 4096 weights and
-    on rows above 6144, the streaming paired kernel on wide layers of rows
-    above 4096, else the one-shot kernel."""
+    """M = 2: the ring kernel where it has a shape; the paired kernel on
+    wide layers of rows up to 4096 weights and on rows above 6144, the
+    streaming paired kernel on wide layers of rows above 4096, else the
+    one-shot kernel."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
-    for k, n, kernel in [(2048, 2048, "oneshot"), (2048, 5632, "oneshot"), (5632, 2048, "oneshot"),
-                         (2048, 8191, "oneshot"), (2048, 8192, "mfma_pair"), (2048, 32000, "mfma_pair"),
-                         (4096, 4096, "oneshot"), (4096, 14336, "mfma_pair"), (4096, 28672, "mfma_pair"),
+    for k, n, kernel in [(2048, 2048, "pair_ring"), (2048, 5632, "pair_ring"), (5632, 2048, "oneshot"),
+                         (2048, 8191, "pair_ring"), (2048, 8193, "mfma_pair"), (2048, 32000, "mfma_pair"),
+                         (4096, 4096, "pair_ring"), (4096, 14336, "pair_ring"), (4096, 28672, "pair_ring"),
                          (5632, 8192, "oneshot"), (6144, 8192, "oneshot"), (6272, 4096, "mfma_pair"),
-                         (5632, 14336, "pair_stream"), (8192, 8192, "mfma_pair"),
-                         (8192, 14336, "pair_stream"), (14336, 4096, "mfma_pair"), (28672, 2048, "mfma_pair"),
+                         (5632, 14336, "pair_stream"), (8192, 8192, "pair_ring"), (2048, 512, "oneshot"),
+                         (8192, 14336, "pair_stream"), (14336, 4096, "pair_ring"), (28672, 2048, "mfma_pair"),
                          (28672, 28672, "mfma_pair"),   # 2 x 28672 activations past the streaming kernel's LDS
                          (34816, 64, "mfma")]:
         assert _lib.plan_linear(ALIGNED, ALIGNED, 2, n, k, 128)["kernel"] == kernel, (k, n)
@@ -385,10 +403,10 @@ def test_oneshot_plan_shapes(monkeypatch):
         plan = _lib.plan_linear(ALIGNED, ALIGNED, 1, n, k, 128)
         assert (plan["kernel"], plan["rows"], plan["splits"], plan["unroll"]) == \
             ("oneshot", rows, splits, loads), (k, n)
-    plan = _lib.plan_linear(ALIGNED, ALIGNED, 2, 5632, 2048, 128)   # M = 2: one row per wavefront
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, 2, 2048, 5632, 128)   # M = 2: one row per wavefront
     assert (plan["kernel"], plan["rows"], plan["splits"]) == ("oneshot", 1, 8)
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 34816, 128)["kernel"] == "mfma"     # M > 2, long rows
-    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 4096, 128)["kernel"] == "oneshot"   # M = 2, any N
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 2, 6000, 5632, 128)["kernel"] == "oneshot"   # M = 2, any N
     monkeypatch.setenv("W4A16_DECODE", "oneshot")
     assert _lib.plan_linear(ALIGNED, ALIGNED, 3, 6000, 2048, 128)["kernel"] == "oneshot"
     assert _lib.plan_linear(ALIGNED, ALIGNED, 5, 64, 2048, 128)["kernel"] == "valu"     # M > 4

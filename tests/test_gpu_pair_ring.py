@@ -14,7 +14,7 @@ from tests._cases import assert_parity, expected, make_case
 
 pytestmark = pytest.mark.gpu
 
-PAIR_M1 = _lib.KERNEL_PAIR_M1
+RING = _lib.KERNEL_PAIR_RING
 
 # (splits = wavefronts splitting K, rows = 8-row-block wavefronts, unroll =
 # pairs in flight, K values whose pairs per wavefront match the instantiation)
@@ -30,6 +30,13 @@ SHAPES = [
     (2, 4, 6, (28672, 28416)),
 ]
 VARIANTS = [(sk, sn, d, k) for sk, sn, d, ks in SHAPES for k in ks]
+
+# M = 2..4 (4 row slots) and M = 5..8 (8 row slots)
+SHAPES4 = [(4, 1, 2, (2048, 1792)), (1, 4, 6, (2048,)), (2, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)),
+           (8, 1, 3, (5632, 6144)), (2, 4, 4, (8192,)), (4, 2, 6, (14336, 14080))]
+SHAPES8 = [(4, 1, 2, (2048,)), (1, 4, 6, (2048,)), (4, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)), (2, 4, 4, (8192, 7936))]
+SMALL = ([(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES4 for k in ks for m in (2, 3, 4)] +
+         [(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES8 for k in ks for m in (5, 8)])
 
 
 def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0):
@@ -47,19 +54,30 @@ def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0):
 
 @pytest.mark.parametrize("splits,rows,unroll,k", VARIANTS)
 @pytest.mark.parametrize("n", [7, 65, 300])
-def test_pair_m1_variants(gpu, splits, rows, unroll, k, n):
+def test_pair_ring_m1_variants(gpu, splits, rows, unroll, k, n):
     """Every instantiated shape on ragged N (partial 8-row blocks, a partial
     last workgroup), against the oracle."""
     x, p, s = make_case(1, k, n, seed=k + 7 * n + splits)
-    out = _run(gpu, x, p, s, PAIR_M1, rows, splits, unroll)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll)
     assert_parity(out, expected(x, p, s), f"pair_m1 ({splits},{rows},{unroll}) K={k} N={n}")
 
 
-@pytest.mark.parametrize("splits,rows,unroll,k", [(2, 2, 8, 4096), (4, 1, 6, 5632), (2, 2, 10, 14336)])
-def test_pair_m1_all_nibbles(gpu, splits, rows, unroll, k):
+@pytest.mark.parametrize("m,splits,rows,unroll,k", SMALL)
+@pytest.mark.parametrize("n", [13, 300])
+def test_pair_ring_small_batch_variants(gpu, m, splits, rows, unroll, k, n):
+    """Every M = 2..8 shape at every M of its row slots (rows past M in the
+    A operand and in the stores), ragged N, against the oracle."""
+    x, p, s = make_case(m, k, n, seed=k + 5 * n + 11 * m + splits)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll)
+    assert_parity(out, expected(x, p, s), f"pair_ring M={m} ({splits},{rows},{unroll}) K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,splits,rows,unroll,k", [(1, 2, 2, 8, 4096), (1, 4, 1, 6, 5632), (1, 2, 2, 10, 14336),
+                                                    (3, 8, 1, 3, 5632), (8, 4, 2, 4, 4096), (8, 2, 4, 4, 8192)])
+def test_pair_ring_m1_all_nibbles(gpu, m, splits, rows, unroll, k):
     """Uniform random bytes (code -8 included) with scales in [0.01, 1.01)."""
-    x, p, s = make_case(1, k, 97, seed=5, all_nibbles=True)
-    out = _run(gpu, x, p, s, PAIR_M1, rows, splits, unroll)
+    x, p, s = make_case(m, k, 97, seed=5, all_nibbles=True)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll)
     assert_parity(out, expected(x, p, s), f"pair_m1 all nibbles K={k}")
 
 
@@ -67,13 +85,25 @@ def test_pair_m1_all_nibbles(gpu, splits, rows, unroll, k):
 # size (configs[1], [2] at M = 1, [3], and the 1.1B model's lm_head)
 @pytest.mark.parametrize("k,n", [(2048, 5632), (5632, 2048), (4096, 4096), (4096, 14336), (14336, 4096),
                                  (8192, 8192), (8192, 28672), (28672, 8192), (2048, 32000)])
-def test_pair_m1_default_route_full_size(gpu, k, n):
+def test_pair_ring_m1_default_route_full_size(gpu, k, n):
+    """M = 1 through the default route (the plan the benchmark times)."""
     x, p, s = make_case(1, k, n, seed=k ^ (3 * n), device="cuda")
-    assert _lib.plan_linear(16, 16, 1, n, k)["kernel"] == "pair_m1"
+    assert _lib.plan_linear(16, 16, 1, n, k)["kernel"] == "pair_ring"
     assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default (pair_m1)")
 
 
-def test_pair_m1_misaligned_scales_fall_back(gpu):
+# the M = 2..8 configs[2] / configs[3] shapes the default route sends here
+@pytest.mark.parametrize("m,k,n", [(2, 2048, 2048), (4, 2048, 5632), (8, 2048, 5632), (8, 2048, 2048),
+                                   (2, 4096, 4096), (8, 4096, 4096), (2, 4096, 14336), (4, 4096, 14336),
+                                   (8, 4096, 14336), (4, 8192, 8192), (8, 8192, 8192), (2, 14336, 4096),
+                                   (4, 14336, 4096), (4, 5632, 2048)])
+def test_pair_ring_default_route_small_batch_full_size(gpu, m, k, n):
+    x, p, s = make_case(m, k, n, seed=m + k ^ (5 * n), device="cuda")
+    assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "pair_ring"
+    assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (pair_ring)")
+
+
+def test_pair_ring_m1_misaligned_scales_fall_back(gpu):
     """Scales 2-byte but not 4-byte aligned: the default route takes another
     kernel (this one reads scale pairs as 32-bit words), the tuned entry
     point rejects it."""
@@ -89,16 +119,19 @@ def test_pair_m1_misaligned_scales_fall_back(gpu):
     torch.cuda.synchronize()
     assert_parity(out, expected(x, p, s), "misaligned scales, default route")
     with pytest.raises(_lib.W4A16Error, match="4-byte aligned"):
-        _lib.linear_f16_tuned(xd, pd, sd, out, 128, PAIR_M1, 8, 1, 6)
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, RING, 8, 1, 6)
 
 
-def test_pair_m1_rejects(gpu):
+def test_pair_ring_m1_rejects(gpu):
     x, p, s = make_case(1, 2176, 16, seed=3)   # 17 groups: K not a multiple of 256
     with pytest.raises(_lib.W4A16Error, match="multiple of 256"):
-        _run(gpu, x, p, s, PAIR_M1, 3, 1, 8)
+        _run(gpu, x, p, s, RING, 3, 1, 8)
     x, p, s = make_case(1, 4096, 16, seed=3)
     with pytest.raises(_lib.W4A16Error, match="not instantiated"):
-        _run(gpu, x, p, s, PAIR_M1, 3, 1, 8)     # 16 pairs per wavefront with 3 row wavefronts: no such shape
-    x, p, s = make_case(2, 4096, 16, seed=3)
-    with pytest.raises(_lib.W4A16Error, match="M == 1"):
-        _run(gpu, x, p, s, PAIR_M1, 8, 1, 6)
+        _run(gpu, x, p, s, RING, 3, 1, 8)     # 16 pairs per wavefront with 3 row wavefronts: no such shape
+    x, p, s = make_case(2, 2048, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="not instantiated for this M"):
+        _run(gpu, x, p, s, RING, 3, 1, 8)     # an M = 1 shape
+    x, p, s = make_case(9, 4096, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="1 <= M <= 8"):
+        _run(gpu, x, p, s, RING, 8, 1, 6)

@@ -164,8 +164,8 @@ def test_oneshot_four_rows_all_nibbles_and_rejects(gpu):
 # the M = 1 default on wide layers of short rows (the paired M = 1 kernel;
 # 4 rows per wavefront of the one-shot kernel where K has no paired shape)
 # and on 4096 x 4096, at full size
-@pytest.mark.parametrize("k,n,kernel,rows,splits", [(2048, 32000, "pair_m1", 8, 1), (2048, 16384, "pair_m1", 8, 1),
-                                                    (2048, 11264, "pair_m1", 3, 1), (4096, 4096, "pair_m1", 2, 2),
+@pytest.mark.parametrize("k,n,kernel,rows,splits", [(2048, 32000, "pair_ring", 8, 1), (2048, 16384, "pair_ring", 8, 1),
+                                                    (2048, 11264, "pair_ring", 3, 1), (4096, 4096, "pair_ring", 2, 2),
                                                     (1024, 24577, "oneshot", 4, 4), (2048, 2560, "oneshot", 1, 8)])
 def test_default_dispatch_wide_m1(gpu, k, n, kernel, rows, splits):
     x, p, s = make_case(1, k, n, seed=k ^ n)
@@ -174,11 +174,12 @@ def test_default_dispatch_wide_m1(gpu, k, n, kernel, rows, splits):
     assert_parity(_run_default(gpu, x, p, s), expected(x, p, s), f"M=1 K={k} N={n} default")
 
 
-# M = 2 through the default route on the paired kernel (wide layers of short
-# rows, rows above 6144 weights), the streaming paired kernel (wide layers of
-# longer rows) and the one-shot kernel (rows of up to 6144), at full size
-@pytest.mark.parametrize("k,n,kernel", [(2048, 32000, "mfma_pair"), (4096, 14336, "mfma_pair"),
-                                        (5632, 14336, "pair_stream"), (8192, 8192, "mfma_pair"),
+# M = 2 through the default route on the ring kernel, the paired kernel (wide
+# layers of short rows, rows above 6144 weights), the streaming paired kernel
+# (wide layers of longer rows) and the one-shot kernel (rows of up to 6144),
+# at full size
+@pytest.mark.parametrize("k,n,kernel", [(2048, 32000, "mfma_pair"), (4096, 14336, "pair_ring"),
+                                        (5632, 14336, "pair_stream"), (8192, 8192, "pair_ring"),
                                         (7168, 4096, "mfma_pair"), (6144, 4096, "oneshot"),
                                         (28672, 2048, "mfma_pair"), (11008, 28672, "pair_stream")])
 def test_default_dispatch_m2(gpu, k, n, kernel):
@@ -268,7 +269,7 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
     assert_parity(out, expected(x, p, s), f"mfma_pair chunked M={m} splits={splits} blocks={blocks} K={k}")
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 2048, 5632), (5, 4096, 4096), (7, 5632, 2048), (8, 8192, 1000),
+@pytest.mark.parametrize("m,k,n", [(3, 2048, 9000), (5, 4352, 4096), (7, 5632, 2048), (8, 8192, 1000),
                                    (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
                                    (5, 8320, 77),
                                    # M = 9..16 with the selector: one launch with 16 row slots, or two
@@ -343,7 +344,7 @@ def test_pair_stream_many_tasks(gpu, waves, cap, m, k, n):
     assert_parity(got, expected(x, p, s), f"pair_stream waves={waves} cap={cap} M={m} K={k} N={n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 4096, 14343), (8, 8192, 28672), (5, 4224, 16384)])
+@pytest.mark.parametrize("m,k,n", [(3, 5632, 14343), (8, 8192, 28672), (5, 4224, 16384)])
 def test_default_dispatch_pair_stream(gpu, m, k, n):
     """Wide layers route to the streaming paired kernel (ragged N, an odd
     group count at K = 4224)."""
