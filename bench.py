@@ -37,8 +37,8 @@ CPU oracle's time for the same layers on the host cores (`cpu_baseline`; a
 reported baseline, not a target), with configs[0] (M = 1, 2048 x 2048) timed
 on the product's torch CPU path beside the oracle, and the CPU model.
 
-usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables]
-       python bench.py --layer-pass M K N COPIES CALLS | --prefill-pass TOKENS   (profiler passes)
+usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables] [--long]
+       python bench.py --headline-pass | --layer-pass M K N COPIES CALLS | --prefill-pass TOKENS   (profiler passes)
 """
 
 from __future__ import annotations
@@ -65,12 +65,24 @@ TOKENS_PER_REPLAY = 8
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
 # reads half the bytes on this part, WRITE_SIZE is exact).
-MEASURED_TRAFFIC_BYTES = 6070301
-TRAFFIC_SOURCE = "profiles/gemv_oneshot_m1_mlp_traffic.md"
+MEASURED_TRAFFIC_BYTES = 6130746
+TRAFFIC_SOURCE = "profiles/gemv_pair_ring_m1_mlp_traffic.md"
+# Mean kernel duration of the same two kernels in a rocprofv3 kernel trace of
+# `bench.py --headline-pass` (the headline sequence alone), per launch: the
+# profiler's timestamps run above the event-timed launches, so the line
+# reports both.
+TRACE_US_PER_LAUNCH = 3.459
+TRACE_SOURCE = "profiles/gemv_pair_ring_m1_mlp_kernel_trace.md"
 
 
-def _kernel_name(plan: dict) -> str:
-    """Template instance the C ABI launches for a plan (w4a16_kernels.h)."""
+def _kernel_name(plan: dict, m: int = 1, k: int = 0) -> str:
+    """Template instance the C ABI launches for a plan (w4a16_kernels.h,
+    w4a16_pair_ring.h)."""
+    if plan["kernel"] == "pair_ring":
+        slots = 1 if m <= 1 else 4 if m <= 4 else 8
+        pairs = -(-(k // 256) // max(1, plan["splits"]))
+        return (f"w4a16::gemv_pair_ring<{slots},{plan['splits']},{plan['rows']},1,{pairs},"
+                f"{plan['unroll']}>")
     if plan["kernel"] == "oneshot":
         return f"w4a16::gemv_oneshot<1,{plan['rows']},{plan['unroll']},{plan['splits']}>"
     if plan["kernel"] == "valu":
@@ -269,13 +281,14 @@ def _median_call_us(fn, budget_s: float) -> tuple[float, int]:
     return times[len(times) // 2] * 1e6, len(times)
 
 
-def cpu_baseline(shapes, budget_s: float = 12.0, configs0_budget_s: float = 3.0) -> dict:
-    """The CPU oracle (C restatement of reference w4a16/reference.py:49-80:
-    full fp32 dequantize + fp32 matmul + fp16 cast) on the host cores, on a
-    bounded sample of the same layers (M = 1, one weight copy per shape); and
-    configs[0] (M = 1, 2048 x 2048), the reference's own CPU path, timed both
-    as the product's torch restatement (nibble_amd.reference.linear_reference,
-    which QuantizedLinear runs for CPU tensors) and as the C oracle."""
+def cpu_baseline(shapes, budget_s: float = 12.0, port_budget_s: float = 6.0, configs0_budget_s: float = 3.0) -> dict:
+    """The reference's CPU path (w4a16/reference.py:49-80: fp32 dequantize of
+    the whole matrix, fp32 matmul, fp16 cast), as the product's torch
+    restatement nibble_amd.reference.linear_reference (which QuantizedLinear
+    runs for CPU tensors), timed on the host cores on a bounded sample of the
+    same layers (M = 1, one weight copy per shape): `value`. Beside it the C
+    oracle (the same arithmetic with float64 sums, OpenMP) on the same layers,
+    and configs[0] (M = 1, 2048 x 2048) on both."""
     import numpy as np
     import torch
 
@@ -294,12 +307,30 @@ def cpu_baseline(shapes, budget_s: float = 12.0, configs0_budget_s: float = 3.0)
         oracle.linear(x, p, s, 128, threads=threads)
     calls, total_bytes = 0, 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
+    while time.perf_counter() - t0 < port_budget_s:
         for x, p, s, nbytes in layers:
             oracle.linear(x, p, s, 128, threads=threads)
             calls += 1
             total_bytes += nbytes
-    elapsed = time.perf_counter() - t0
+    port_elapsed = time.perf_counter() - t0
+
+    # the reference's path in torch on the same layers and threads
+    tlayers = [(torch.from_numpy(x), torch.from_numpy(p), torch.from_numpy(s), nbytes) for x, p, s, nbytes in layers]
+    torch_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        for x, p, s, _ in tlayers:  # warm-up
+            linear_reference(x, p, s, 128)
+        ref_calls, ref_bytes = 0, 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            for x, p, s, nbytes in tlayers:
+                linear_reference(x, p, s, 128)
+                ref_calls += 1
+                ref_bytes += nbytes
+        ref_elapsed = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(torch_threads)
 
     # seed 0, weights randn(N, K) * 0.02 fp32 -> RTN group 128,
     # activations randn(1, K) -> fp16, as BASELINE.json states it
@@ -310,7 +341,6 @@ def cpu_baseline(shapes, budget_s: float = 12.0, configs0_budget_s: float = 3.0)
 
     p0, s0 = quantize_and_pack_weights(w0, 128)
     x0 = torch.randn((1, k0), generator=gen).to(torch.float16)
-    torch_threads = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
         torch_us, torch_calls = _median_call_us(lambda: linear_reference(x0, p0, s0, 128), configs0_budget_s)
@@ -321,13 +351,19 @@ def cpu_baseline(shapes, budget_s: float = 12.0, configs0_budget_s: float = 3.0)
                                           configs0_budget_s)
     b0 = payload_bytes(1, n0, k0)
     return {
-        "value": round(total_bytes / elapsed / 1e9, 3),
+        "value": round(ref_bytes / ref_elapsed / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
-        "kind": "port",
-        "sample": f"{calls} single-token calls alternating up (2048x5632) and down (5632x2048) "
-                  f"in {elapsed:.1f} s, 1 weight copy per shape",
-        "us_per_call": round(elapsed / calls * 1e6, 1),
+        "kind": "reference",
+        "sample": f"{ref_calls} single-token calls alternating up (2048x5632) and down (5632x2048) "
+                  f"in {ref_elapsed:.1f} s, 1 weight copy per shape, through the reference's CPU path "
+                  f"(reference w4a16/reference.py:49-80 as nibble_amd.reference.linear_reference, torch CPU, "
+                  f"{threads} threads)",
+        "us_per_call": round(ref_elapsed / ref_calls * 1e6, 1),
+        "port_value": round(total_bytes / port_elapsed / 1e9, 3),
+        "port_us_per_call": round(port_elapsed / calls * 1e6, 1),
+        "port": f"oracle.linear (C restatement, OpenMP, {threads} threads) on the same layers: {calls} calls in "
+                f"{port_elapsed:.1f} s",
         "cpu_model": _cpu_model(),
         "logical_cpus": os.cpu_count(),
         "configs0": {
@@ -510,7 +546,19 @@ def _copies(nbytes: int, floor_bytes: int = 512 << 20) -> int:
     return max(2, -(-floor_bytes // nbytes))
 
 
-def layer_tables(device) -> dict:
+def row_metrics(m: int, n: int, k: int, us: float, copy_gbps: float | None) -> dict:
+    """us, GB/s, % of the 8 TB/s peak, % of the measured copy bandwidth and
+    arithmetic intensity (FLOP per algorithmic byte) of one layer call, as the
+    reference reports them per row (scripts/profile_kernel.py:622-628)."""
+    gbs = payload_bytes(m, n, k) / us / 1e3
+    row = {"us": round(us, 3), "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2)}
+    if copy_gbps:
+        row["pct_copy"] = round(100 * gbs / copy_gbps, 2)
+    row["flop_per_byte"] = round(2 * m * n * k / payload_bytes(m, n, k), 2)
+    return row
+
+
+def layer_tables(device, copy_gbps: float | None = None) -> dict:
     """M in {1, 2, 4, 8} on the three small-batch shapes, each next
     to an fp16 hipBLASLt GEMM (F.linear) on the dequantized weights; configs[3]:
     the 8B- and 70B-class shapes at M in {1, 8}. Per-layer time = median of
@@ -538,9 +586,7 @@ def layer_tables(device) -> dict:
                 # plan uses one (the split-K kernel), as the torch op does
                 plan = _lib.plan_linear(x.data_ptr(), packed[0].data_ptr(), m, n, k)
                 kernel = "pair_split" if _lib.linear_workspace_bytes(m, n, k) > 0 else plan["kernel"]
-                gbs = payload_bytes(m, n, k) / us / 1e3
-                row = {"K": k, "N": n, "M": m, "us": round(us, 3), "GBps": round(gbs, 1),
-                       "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": kernel,
+                row = {"K": k, "N": n, "M": m, **row_metrics(m, n, k, us, copy_gbps), "kernel": kernel,
                        "eager_us": round(eager_us(lambda i: torch.ops.w4a16.linear(x, packed[i], scales[i], 128),
                                                   copies), 3)}
                 if m == 1:
@@ -569,6 +615,12 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-tables", action="store_true", help="skip the configs[2] / configs[3] per-layer tables")
+    ap.add_argument("--long", action="store_true",
+                    help="also time prompts of 64 / 256 / 1024 tokens and decode after a 1500-token prompt (no "
+                         "BASELINE config covers them)")
+    ap.add_argument("--headline-pass", action="store_true",
+                    help="for rocprofv3 --kernel-trace: the headline sequence alone (clock settle, pre-roll, "
+                         "warm-up, the K timed eager steps); prints the event-timed ms per step; no JSON")
     ap.add_argument("--counter-pass", action="store_true",
                     help="eager launches only, for rocprofv3 --pmc: 50 calls of each MLP shape on rotated "
                          "copies, then 5 elementwise negations of a 256 MiB fp32 buffer into another "
@@ -737,6 +789,15 @@ def main() -> int:
             break
         rolls *= 2
     eager_elapsed = start_ev.elapsed_time(end_ev) / 1e3
+    if args.headline_pass:
+        torch.cuda.synchronize()
+        print(json.dumps({"headline_pass": True, "steps": args.steps, "queued": timed_launch is not None,
+                          "ms_per_step": round(eager_elapsed / args.steps * 1e3, 5),
+                          "us_per_launch": round(eager_elapsed / args.steps / 2 * 1e6, 3),
+                          "kernels": [_kernel_name(_lib.plan_linear(xs[j].data_ptr(), layers[j][0][0].data_ptr(),
+                                                                    1, n, k), 1, k)
+                                      for j, (k, n) in enumerate(shapes)]}), flush=True)
+        return 0
     # the same steps as one graph replay, queued behind the pre-roll and warm-up
     settle()
     preroll.replay()
@@ -756,13 +817,13 @@ def main() -> int:
     value_graph = step_bytes * args.steps / graph_elapsed / 1e9
 
     # ---- per-layer and the dominant kernel's roofline ----
+    copy_gbps = round(copy_bandwidth(device), 1)
     layer_rows = {}
     for j, (k, n) in enumerate(shapes):
         us = per_layer(lambda i, j=j: call_raw(j, i), copies)
-        gbs = payload_bytes(1, n, k) / us / 1e3
         plan = _lib.plan_linear(xs[j].data_ptr(), layers[j][0][0].data_ptr(), 1, n, k)
-        layer_rows[f"K{k}xN{n}"] = {"us": round(us, 3), "GBps": round(gbs, 1),
-                                    "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBPS, 2), "kernel": plan}
+        layer_rows[f"K{k}xN{n}"] = {**row_metrics(1, n, k, us, copy_gbps), "kernel": plan,
+                                    "kernel_name": _kernel_name(plan, 1, k)}
     # torch-op path (drop-in API) for the same shapes, graph-timed, and its
     # single-call eager latency (launch and Python dispatch included)
     op_us = {f"K{k}xN{n}": round(per_layer(lambda i, j=j: call(j, i), copies), 3) for j, (k, n) in enumerate(shapes)}
@@ -778,9 +839,13 @@ def main() -> int:
         "frac": round(achieved / HBM_PEAK_GBPS, 4),
         "traffic": MEASURED_TRAFFIC_BYTES,
         "traffic_source": TRAFFIC_SOURCE,
-        "kernel": " + ".join(_kernel_name(r["kernel"]) for r in layer_rows.values()),
+        "kernel": " + ".join(r["kernel_name"] for r in layer_rows.values()),
         "bytes_per_launch": step_bytes // 2,
         "us_per_launch": round(elapsed / args.steps / 2 * 1e6, 3),
+        "frac_trace": round(step_bytes / 2 / (TRACE_US_PER_LAUNCH * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "trace_us_per_launch": TRACE_US_PER_LAUNCH,
+        "trace_source": TRACE_SOURCE,
+        "profiler_offset_us": round(TRACE_US_PER_LAUNCH - elapsed / args.steps / 2 * 1e6, 3),
     }
 
     line = {
@@ -814,15 +879,16 @@ def main() -> int:
         "roofline": roofline,
     }
     line["gpu_state"] = gpu_state_under_load(preroll)
-    line["copy_GBps"] = round(copy_bandwidth(device), 1)
+    line["copy_GBps"] = copy_gbps
     if not args.no_tables:
-        line["layers"] = layer_tables(device)
+        line["layers"] = layer_tables(device, copy_gbps)
     if not args.no_decode:
         del layers
         torch.cuda.empty_cache()
         line["decode"] = decode_tok_s(device)
-        line["decode"].update(prefill_long(device))
-        line["decode"].update(decode_long_context(device))
+        if args.long:
+            line["decode"].update(prefill_long(device))
+            line["decode"].update(decode_long_context(device))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(shapes)
     print(json.dumps(line), flush=True)
