@@ -118,8 +118,10 @@ int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights,
  * keep no partial sums): it is for callers that cannot allocate, such as
  * code under HIP graph capture, tight serving loops or harnesses that
  * forbid allocation. Results are bit-identical to w4a16_linear_ws_f16 with
- * a caller workspace. A layer whose split-K partials need more than the
- * scratch (slices * M * N * 4 bytes) is W4A16_ERR_TOO_LARGE. Every call on
+ * a caller workspace, except for a layer whose split-K partials would need
+ * more than the scratch (slices * M * N * 4 bytes): it takes the route of
+ * w4a16_linear_f16 (no workspace, no split-K), bit-identical to that entry
+ * point instead. Every call on
  * one GPU shares that GPU's scratch: calls that overlap on one GPU (two
  * streams, two threads) race and must be serialised by the caller. The
  * first call on a device that needs the scratch looks up its address

@@ -731,15 +731,6 @@ bool pair16_fits(int64_t M, int64_t N, int64_t K, int max_blocks_cap) {
 
 bool pair16_route(int64_t M, int64_t N, int64_t K) { return K > 4096 && pair16_fits(M, N, K, 2); }
 
-// M = 9..16 on wide layers of short rows (K <= 2048, N >= 8192): the one-shot
-// MFMA kernel (a K x N grid at M = 12 and 16, graph timing, two interleaved
-// passes: 2048 x 8192 5.50 against 5.90 us on the GEMM, 2048 x 14336 8.14
-// against 9.05, 2048 x 32000 14.13 against 14.80; the GEMM keeps N <= 4096,
-// 4.54 against 5.22 at 2048 x 2048).
-bool mfma_oneshot16_route(int64_t M, int64_t N, int64_t K) {
-    return M >= 9 && M <= 16 && K <= 2048 && N >= 8192 && mfma_oneshot_fits(M, K);
-}
-
 int launch_mfma_pair_rows(const Plan& p, bool own_plans, int M, const w4a16::f16* x, const uint8_t* w,
                           const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t st) {
     if (M <= 8)
@@ -819,14 +810,14 @@ int make_plan(const void* act, const void* packed, const void* scales, int64_t M
         *out = plan_mfma_pair((M + 1) / 2, N, K);   // the first half's shape; each half plans its own
         return W4A16_OK;
     }
-    // M = 9..16 on wide layers of short rows: the one-shot MFMA kernel; on
-    // long rows whose paired plan keeps at most one workgroup per CU and 2
-    // wavefronts on weight blocks: the paired kernel in one launch (16 row
-    // slots)
-    if (aligned && family == 0 && mfma_oneshot16_route(M, N, K)) {
-        *out = plan_mfma_oneshot(M, N, K);
-        return W4A16_OK;
-    }
+    // M = 9..16 on long rows whose paired plan keeps at most one workgroup
+    // per CU and 2 wavefronts on weight blocks: the paired kernel in one
+    // launch (16 row slots). Prompt rows take only kernels whose B operand is
+    // the dequantized fp16 weights (these two and the GEMM), so the op's
+    // prefill agrees with dequantize + fp16 GEMM at the reference's 1e-3
+    // tolerance; the one-shot MFMA kernel (offset decode, faster on wide
+    // layers of short rows: 2048 x 8192 at M = 12 5.50 against 5.90 us)
+    // stays behind W4A16_DECODE=mfma_oneshot.
     if (aligned && family == 0 && pair16_route(M, N, K)) {
         *out = plan_mfma_pair(M, N, K);
         return W4A16_OK;
@@ -1382,13 +1373,15 @@ int w4a16_linear_noalloc_f16(const void* activations, const uint8_t* packed_weig
     if (p.kernel == W4A16_KERNEL_NONE) return W4A16_OK;
     rc = check_pointers(activations, packed_weights, scales, output);
     if (rc != W4A16_OK) return rc;
-    const int64_t need =
+    int64_t need =
         p.kernel == W4A16_KERNEL_PAIR_SPLIT ? w4a16_internal::pair_split_workspace_bytes(M, N, p.splits) : 0;
-    if (need > kNoAllocScratchBytes)
-        return fail(W4A16_ERR_TOO_LARGE, "w4a16_linear_noalloc_f16: this layer needs " + std::to_string(need) +
-                                             " bytes of split-K scratch, more than the library's " +
-                                             std::to_string(kNoAllocScratchBytes) +
-                                             "; use w4a16_linear_ws_f16 with a caller workspace");
+    if (need > kNoAllocScratchBytes) {
+        // partial sums past the scratch: the route without a workspace (the
+        // kernels w4a16_linear_f16 runs), which needs none
+        rc = make_plan(activations, packed_weights, scales, M, N, K, group_size, &p, false);
+        if (rc != W4A16_OK) return rc;
+        need = 0;
+    }
     void* ws = nullptr;
     if (need > 0) {
         rc = scratch_address(&ws);

@@ -9,11 +9,12 @@ Mirrors reference ``w4a16/linear.py`` (constructor checks, buffers
 * GPU tensors, ``fused`` and M <= ``FUSED_MAX_ROWS``: ``w4a16::linear``
   (the gfx950 GEMV / small-batch kernels);
 * GPU tensors, ``fused``, group_size 128 and M <= ``NATIVE_GEMM_MAX_ROWS``
-  (prompts): ``w4a16::linear`` as well, which runs the W4A16 MFMA GEMM on
-  weights decoded in registers, bit-identical to the dequantized fp16 weights,
-  with fp32 accumulation; the reference sends these rows to dequantize +
-  cuBLAS, and the result agrees with that path within its own prefill
-  tolerance (reference tests/test_linear.py:207-225, rtol = atol = 1e-3);
+  (prompts): ``w4a16::linear`` as well, which runs the W4A16 MFMA GEMM (at
+  9..16 rows of long rows, its 16-row paired form) on weights decoded in
+  registers, bit-identical to the dequantized fp16 weights, with fp32
+  accumulation; the reference sends these rows to dequantize + cuBLAS, and
+  the result agrees with that path within its own prefill tolerance
+  (reference tests/test_linear.py:207-225, rtol = atol = 1e-3);
 * GPU tensors otherwise (longer prompts, ``fused=False``):
   ``w4a16::dequantize`` then ``F.linear`` (hipBLASLt) when group_size is a
   multiple of 32, else ``w4a16::linear``'s generic kernel (any M, any even

@@ -286,8 +286,9 @@ class LlamaDecoder(torch.nn.Module):
         # allow) and merged per head; 0 keeps one workgroup per head. 1.1B
         # model, graph-replayed decode: 2048 slots at position 1500 1837
         # against 1597 tok/s, 1024 at 900 1907 against 1830, 512 at 300 1970
-        # against 2030 (so 512 slots keep the single launch)
-        self.attn_splits = (min(max(1, 256 // cfg.num_heads), max(1, cfg.max_seq_len // 128))
+        # against 2030 (so 512 slots keep the single launch); at most 64
+        # shares, the split launch's limit
+        self.attn_splits = (min(max(1, 256 // cfg.num_heads), max(1, cfg.max_seq_len // 128), 64)
                             if cfg.max_seq_len > 512 else 0)
         self.attn_ws = torch.empty((max(1, cfg.num_heads * self.attn_splits * 66),), dtype=torch.float32,
                                    device=device)

@@ -75,7 +75,12 @@ def quantize_groupwise(
     rows, cols = weights.shape
     groups = weights.to(torch.float32).reshape(rows, cols // group_size, group_size)
     amax = groups.abs().amax(dim=2, keepdim=True)
-    scale = torch.where(amax == 0, torch.ones_like(amax), amax / 7.0)
+    # amax / 7 as a correctly rounded fp32 quotient on every device: torch's
+    # GPU kernels divide by a Python scalar as a product with its rounded
+    # reciprocal (an ulp off for about half of the quotients, which moves ~5e-5
+    # of the fp16 scales), so the divisor is a tensor and GPU quantization
+    # writes the same bytes as the CPU path
+    scale = torch.where(amax == 0, torch.ones_like(amax), amax / torch.full_like(amax, 7.0))
     codes = torch.round(groups / scale).clamp_(-7, 7).to(torch.int8).reshape(rows, cols)
     return codes, scale.squeeze(2).to(torch.float16)
 

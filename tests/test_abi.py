@@ -374,17 +374,20 @@ def test_m2_routing(monkeypatch):
 
 
 def test_short_prompt_routing(monkeypatch):
-    """M = 9..16: the one-shot MFMA kernel on wide layers of rows up to 2048
-    weights, the 16-row-slot paired kernel on longer rows whose plan keeps 2
-    wavefronts or fewer on weight blocks (8192 x 8192 would take 4 and spill),
-    else the GEMM."""
+    """M = 9..16: the 16-row-slot paired kernel on rows longer than 4096
+    weights whose plan keeps 2 wavefronts or fewer on weight blocks (8192 x
+    8192 would take 4 and spill), else the GEMM; both put the dequantized
+    fp16 weights in B. The offset-decode one-shot MFMA kernel only with its
+    selector."""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
-    for m, k, n, kernel in [(12, 2048, 8192, "mfma_oneshot"), (16, 2048, 32000, "mfma_oneshot"),
-                            (9, 1024, 16384, "mfma_oneshot"), (12, 2048, 4096, "gemm"), (16, 2048, 2560, "gemm"),
+    for m, k, n, kernel in [(12, 2048, 8192, "gemm"), (16, 2048, 32000, "gemm"),
+                            (9, 1024, 16384, "gemm"), (12, 2048, 4096, "gemm"), (16, 2048, 2560, "gemm"),
                             (16, 4096, 14336, "gemm"), (16, 8192, 8192, "gemm"), (12, 8192, 4096, "mfma_pair"),
                             (9, 14336, 4096, "mfma_pair"), (12, 5632, 2048, "mfma_pair"), (17, 2048, 8192, "gemm")]:
         assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] == kernel, (m, k, n)
+    monkeypatch.setenv("W4A16_DECODE", "mfma_oneshot")
+    assert _lib.plan_linear(ALIGNED, ALIGNED, 12, 8192, 2048, 128)["kernel"] == "mfma_oneshot"
 
 
 def test_oneshot_plan_shapes(monkeypatch):
@@ -501,19 +504,16 @@ def test_valu_falls_back_to_mfma_when_activations_exceed_lds(monkeypatch):
 
 
 def test_noalloc_rejects_before_launch():
-    """w4a16_linear_noalloc_f16 checks its arguments and the scratch size on
-    the host: a layer whose split-K partials exceed the 8 MiB scratch is
-    W4A16_ERR_TOO_LARGE (nothing launched, so stand-in addresses are safe)."""
+    """w4a16_linear_noalloc_f16 checks its arguments on the host (nothing
+    launched, so stand-in addresses are safe). The scratch holds the split-K
+    partials of M = 8, K = 20480 up to N = 65536; wider layers take the route
+    without a workspace (tested on the GPU)."""
     lib = _lib.lib()
     assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 1, 8, 256, 0, None) == _lib.W4A16_ERR_GROUP_SIZE
     assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 1, 8, 256, 128, None) == _lib.W4A16_ERR_NULL
     assert lib.w4a16_linear_noalloc_f16(None, None, None, None, 0, 8, 256, 128, None) == _lib.W4A16_OK
-    m, k, n = 8, 20480, 65544
-    need = _lib.linear_workspace_bytes(m, n, k)
-    assert need > _lib.NOALLOC_SCRATCH_BYTES
-    a = ALIGNED
-    assert lib.w4a16_linear_noalloc_f16(a, a, a, a, m, n, k, 128, None) == _lib.W4A16_ERR_TOO_LARGE
-    assert str(need) in _lib.last_error() and "w4a16_linear_ws_f16" in _lib.last_error()
+    m, k = 8, 20480
+    assert _lib.linear_workspace_bytes(m, 65544, k) > _lib.NOALLOC_SCRATCH_BYTES
     assert _lib.linear_workspace_bytes(m, 65536, k) == _lib.NOALLOC_SCRATCH_BYTES   # the largest that fits
 
 

@@ -16,6 +16,7 @@ import w4a16
 from w4a16.cuda import dequantize_cuda, linear_cuda
 from w4a16.linear import QuantizedLinear
 from w4a16.quantization import quantize_and_pack_weights
+from nibble_amd import _lib
 from tests._cases import assert_parity, expected, make_case
 
 pytestmark = pytest.mark.gpu
@@ -129,6 +130,24 @@ def test_module_prefill_paths_match_dequant_linear(gpu, fused, m, k, n):
     if fused and 8 < m <= NATIVE_GEMM_MAX_ROWS:
         # the module's prompt rows are the op's, bit for bit
         assert torch.equal(out, linear_cuda(x.to(gpu), *_on(gpu, p, s), 128))
+
+
+@pytest.mark.parametrize("m,k,n", [(16, 2048, 8192), (12, 2048, 32000), (9, 2048, 11264), (16, 5632, 2048),
+                                   (13, 4096, 14336), (64, 2048, 5632)])
+def test_module_prompt_rows_randn_weights(gpu, m, k, n):
+    """Prompt rows of a fused layer with randn (not 0.02-scaled) weights, as
+    reference tests/test_linear.py:207-225 makes them: every kernel the op
+    routes 9..512 rows to must agree with F.linear on the dequantized fp16
+    weights at rtol = atol = 1e-3 (the offset-decode kernels, whose sums run at
+    ~1032 |x| per group, would not at these scales)."""
+    torch.manual_seed(m + k + n)
+    x = torch.randn((m, k), dtype=torch.float16, device=gpu)
+    w = torch.randn((n, k), dtype=torch.float16, device=gpu)
+    packed, scales = quantize_and_pack_weights(w, group_size=128)
+    layer = QuantizedLinear(packed, scales, group_size=128, fused=True)
+    print(f"[case] module prompt M={m} K={k} N={n} plan={_lib.plan_linear(x.data_ptr(), packed.data_ptr(), m, n, k)}",
+          flush=True)
+    torch.testing.assert_close(layer(x), F.linear(x, dequantize_cuda(packed, scales, 128)), rtol=1e-3, atol=1e-3)
 
 
 def test_module_prefill_matches_dequant_linear_reference_case(gpu):

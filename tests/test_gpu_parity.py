@@ -610,11 +610,10 @@ def test_stream_rejects(gpu):
                                            (16, 4096, 64, "gemm"), (12, 256, 7, "gemm"),
                                            (16, 5632, 2048, "mfma_pair"), (16, 2048, 2560, "gemm"),
                                            (11, 5632, 2048, "mfma_pair"), (16, 4096, 14336, "gemm"),
-                                           (12, 2048, 11264, "mfma_oneshot"), (9, 14336, 4096, "mfma_pair"),
-                                           (16, 8192, 8192, "gemm"), (12, 2048, 32000, "mfma_oneshot")])
+                                           (12, 2048, 11264, "gemm"), (9, 14336, 4096, "mfma_pair"),
+                                           (16, 8192, 8192, "gemm"), (12, 2048, 32000, "gemm")])
 def test_default_dispatch_short_prompt(gpu, m, k, n, default, kernel, monkeypatch):
-    """M = 9..16: the one-shot MFMA kernel on layers of N >= 8192 with rows
-    of up to 2048, the paired kernel in one launch (16 row slots) on rows
+    """M = 9..16: the paired kernel in one launch (16 row slots) on rows
     longer than 4096 weights (at most 256 workgroups and 2 wavefronts on
     weight blocks), else the GEMM; the one-shot MFMA kernel with its
     selector (where its activations fit in LDS)."""

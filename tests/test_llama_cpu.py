@@ -80,3 +80,6 @@ def test_prefill_length_and_split_attention_rules():
     assert streamed.attn_splits == min(256 // 4, 600 // 128) == 4
     assert streamed.attn_ws.numel() == 4 * 4 * 66
     assert LlamaDecoder(replace(_tiny(), max_seq_len=512), device="cpu").attn_splits == 0
+    # few query heads and a long cache: capped at the split launch's 64 shares
+    few = replace(_tiny(), num_heads=2, num_kv_heads=2, max_seq_len=16384)
+    assert LlamaDecoder(few, device="cpu").attn_splits == 64
