@@ -57,6 +57,9 @@ HBM_PEAK_GBPS = 8000.0
 # Untimed back-to-back replays before the headline's timed steps: the GPU's
 # clock rises from idle only under sustained load.
 SETTLE_SECONDS = 0.25
+# The same before each per-layer timing (whose weights the host has just
+# built while the GPU idled).
+LAYER_SETTLE_SECONDS = 0.15
 # Decode steps per graph replay in the decode measurement (the generation
 # loop replays a graph of this many steps while the position allows it, one
 # step otherwise); the one-step-per-replay rate is reported beside it.
@@ -140,13 +143,21 @@ def time_graph(graph, reps: int = 1) -> float:
 
 def per_layer(op, copies: int, calls: int = 100, samples: int = 20) -> float:
     """Median microseconds per call over `samples` replays of a graph of at
-    least `calls` calls over the rotated copies. The graph holds whole
-    rotations (a multiple of `copies` calls), so across replays as within one
-    every copy is read again only after all the other copies were."""
+    least `calls` calls over the rotated copies, after LAYER_SETTLE_SECONDS of
+    untimed replays. The graph holds whole rotations (a multiple of `copies`
+    calls), so across replays as within one every copy is read again only
+    after all the other copies were."""
+    import torch
+
     calls = copies * -(-calls // copies)
     graph = capture(lambda i: op(i % copies), calls)
-    for _ in range(3):
-        graph.replay()
+    # untimed replays until the GPU has left the clock it idled at while the
+    # host built the weights (as the headline's settle does)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < LAYER_SETTLE_SECONDS:
+        for _ in range(5):
+            graph.replay()
+        torch.cuda.synchronize()
     times = sorted(time_graph(graph) / calls * 1e6 for _ in range(samples))
     return times[len(times) // 2]
 

@@ -49,7 +49,7 @@ extern "C" {
 #define W4A16_KERNEL_GEMM_LDS 12     /* GEMM with the activation block staged in LDS per round of groups (large M) */
 #define W4A16_KERNEL_PAIR_SPLIT 13   /* PAIR_STREAM over K slices, fp32 partials in a workspace + reduce (2 <= M <= 8) */
 #define W4A16_KERNEL_GEMM32 14       /* GEMM_LDS on 32x32x16 MFMA tiles (large M, rows of up to 4096 weights) */
-#define W4A16_KERNEL_PAIR_RING 15    /* fp16 MFMA on 8 rows x 2 groups, a ring of loads in flight per wavefront (M <= 8) */
+#define W4A16_KERNEL_PAIR_RING 15    /* fp16 MFMA on 8 rows x 2 groups, a ring of loads in flight per wavefront (M <= 16) */
 
 /*
  * Fused W4A16 linear layer.
@@ -95,8 +95,10 @@ int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gr
  * w4a16_linear_f16 with a caller workspace (device memory, 16-byte aligned,
  * contents ignored; workspace_bytes >= w4a16_linear_workspace_bytes): with
  * it, M = 3..8 layers with K > 16384 and N >= 8192 take
- * W4A16_KERNEL_PAIR_SPLIT, the streaming paired kernel over K slices whose
- * fp32 partial sums are added in slice order by a second launch. workspace == NULL routes exactly as w4a16_linear_f16;
+ * W4A16_KERNEL_PAIR_SPLIT, the streaming paired kernel over K slices, and
+ * M = 12..16 layers of K = 5632 (N <= 4096), 8192 or 14336 (N <= 8192) the
+ * paired ring kernel over K slices; the fp32 partial sums are added in slice
+ * order by a second launch. workspace == NULL routes exactly as w4a16_linear_f16;
  * a smaller non-NULL workspace is W4A16_ERR_CONFIG. The torch op
  * w4a16::linear (reference csrc/int4_linear.cpp:16-28) calls this entry
  * point with a workspace from the caching allocator.
@@ -210,12 +212,20 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     wavefronts per workgroup (4|8), unroll = 1 KiB loads per row in flight
  *     (the ring runs on into the next rows when a row has fewer steps),
  *     max_blocks = grid (0 = the workgroups resident on the device at once).
- *   W4A16_KERNEL_PAIR_RING (1 <= M <= 8, K a multiple of 256, scales
+ *   W4A16_KERNEL_PAIR_RING (1 <= M <= 16, K a multiple of 256, scales
  *     4-byte aligned): splits = wavefronts splitting K, rows = wavefronts
  *     on 8-row blocks per workgroup, unroll = group pairs in flight per
- *     wavefront; at M = 1 (splits, rows, ceil(K / 256 / splits), unroll)
- *     one of (1,3,8,8) (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6) (2,4,16,4)
- *     (1,7,32,6) (2,2,28,10) (2,4,56,6); max_blocks ignored.
+ *     wavefront, max_blocks = K slices (0 or 1 = none; 2..16 store fp32
+ *     partial sums in a workspace of max_blocks * M * N * 4 bytes, then a
+ *     reduce launch adds them in slice order); with P = ceil(K / 256 /
+ *     slices) pairs per slice, (splits, rows, ceil(P / splits), unroll) at
+ *     M = 1 one of (1,3,8,8) (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6)
+ *     (2,4,16,4) (1,7,32,6) (2,2,28,10) (2,4,56,6); at M = 2..4 (4,1,2,2)
+ *     (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) (2,4,16,4) (4,2,14,6); at
+ *     M = 5..8 (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); at M =
+ *     9..16 (exact decode: the dequantized fp16 weights in the B operand)
+ *     (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3)
+ *     (1,8,14,4) (1,8,16,4).
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
  *     row blocks with the workgroups resident at once; else 1..16), unroll =
@@ -243,8 +253,8 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  * The VALU and MFMA families need group_size 128, M <= 8 (16 for
  * W4A16_KERNEL_MFMA_ONESHOT, 2..16 for W4A16_KERNEL_MFMA_PAIR) and 16-byte
  * aligned activations and weights. workspace / workspace_bytes: as for
- * w4a16_linear_ws_f16 (only W4A16_KERNEL_PAIR_SPLIT uses them; NULL / 0
- * otherwise). No reference counterpart (the reference's W4A16_DECODE /
+ * w4a16_linear_ws_f16 (only W4A16_KERNEL_PAIR_SPLIT and W4A16_KERNEL_PAIR_RING
+ * with K slices use them; NULL / 0 otherwise). No reference counterpart (the reference's W4A16_DECODE /
  * W4A16_ROWS_PER_WARP selectors play this role).
  */
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights,

@@ -204,12 +204,15 @@ def linear_noalloc_f16(activations, packed_weights, scales, output, group_size: 
 
 def linear_f16_tuned(activations, packed_weights, scales, output, group_size, kernel, rows, splits, unroll,
                      max_blocks=0, stream=None, workspace=None) -> None:
-    """``w4a16_linear_f16_tuned``; the split-K family gets a workspace of
-    splits * M * N fp32 from the caching allocator unless one is given."""
+    """``w4a16_linear_f16_tuned``; the split-K paired kernel gets a workspace
+    of splits * M * N fp32 (the ring kernel over max_blocks > 1 K slices one
+    of max_blocks * M * N) from the caching allocator unless one is given."""
     m, k = activations.shape
     n = packed_weights.shape[0]
     if workspace is None and kernel == KERNEL_PAIR_SPLIT:
         workspace = _workspace(max(1, splits) * m * n * 4, output.device, stream)
+    if workspace is None and kernel == KERNEL_PAIR_RING and max_blocks > 1:
+        workspace = _workspace(max_blocks * m * n * 4, output.device, stream)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _raise_on(

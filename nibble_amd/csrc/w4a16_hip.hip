@@ -40,11 +40,16 @@ int64_t pair_split_workspace_bytes(int64_t M, int64_t N, int slices);
 bool pair_split_valid(int64_t K, int slices);
 int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, const void* x, const uint8_t* w,
                       const void* s, void* o, int N, int K, void* part, int64_t part_bytes, hipStream_t stream);
-// w4a16_pair_ring.hip: the paired-layout ring MFMA kernel for M = 1..8
+// w4a16_pair_ring.hip: the paired-layout ring MFMA kernel for M = 1..16
 int pair_ring_ppw(int64_t K, int sk);
-bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth);
-int launch_pair_ring(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
-                     w4a16::f16* o, int N, int K, hipStream_t stream);
+int64_t pair_ring_workspace_bytes(int64_t M, int64_t N, int slices);
+bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth, int slices);
+bool pair_ring_silu_instantiated(int64_t M, int64_t K, int sk, int sn, int depth);
+int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::f16* x, const uint8_t* w,
+                     const w4a16::f16* s, w4a16::f16* o, int N, int K, void* part, int64_t part_bytes,
+                     hipStream_t stream);
+int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w,
+                          const w4a16::f16* s, w4a16::f16* o, int inter, int K, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -558,16 +563,35 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 // M >= 2 on wider layers of long rows (N > 8192 with K >= 8192). Only
 // instantiated shapes are taken (K a multiple of 256 whose pairs per
 // wavefront match).
-bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out) {
-    if (M < 1 || M > 8 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
+//   M = 9..16 (16 row slots, exact decode; M = 16 / 9, graph timing,
+//   against the routes they replace; rows of 2048 weights on layers of
+//   1024 .. 16384 rows): 2048 x 2048 (8, 1, 1) 4.39 / 3.97
+//   against 4.70 / 4.04 us; 2048 x 2560 (4, 2, 2) 4.75 / 4.37 against 4.99
+//   / 4.48; 2048 x 11264 (2, 4, 4) 7.70 / 7.12 against 9.20 / 8.48. With a
+//   workspace, K slices on long rows from M = 12 (the reduce launch costs
+//   about 2 us; at M = 9 the slices tie or lose): 5632 x 2048 8 slices of
+//   (1, 8, 3) 7.24 against 7.81; 14336 x 4096 4 slices of (1, 8, 4) 15.08
+//   against 17.86; 8192 x 8192 2 slices of (1, 8, 4) 15.33 against 16.89.
+bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace = false) {
+    if (M < 1 || M > 16 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
     const int64_t P = K / 256;
     struct Shape {
-        int sk, sn, d;
+        int sk, sn, d, slices;
     };
     // candidates in order of preference for the row-length class; the first
     // whose pairs per wavefront are instantiated is taken
-    Shape c[2] = {{0, 0, 0}, {0, 0, 0}};
-    if (M == 1) {
+    Shape c[2] = {{0, 0, 0, 1}, {0, 0, 0, 1}};
+    if (M > 8) {
+        if (P == 8 && N >= 1024 && N <= 16384) {
+            if (N <= 2048) c[0] = {8, 1, 1, 1};
+            else if (N <= 4096) c[0] = {4, 2, 2, 1};
+            else c[0] = {2, 4, 4, 1};
+        } else if (workspace && M >= 12) {
+            if (P == 22 && N <= 4096) c[0] = {1, 8, 3, 8};
+            else if (P == 56 && N <= 8192) c[0] = {1, 8, 4, 4};
+            else if (P == 32 && N <= 8192) c[0] = {1, 8, 4, 2};
+        }
+    } else if (M == 1) {
         if (P <= 8) {
             if (N >= 16384) c[0] = {1, 8, 4};
             else if (N >= 4096) c[0] = {1, 3, 8};
@@ -601,13 +625,13 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out) {
         }
     }
     for (const Shape& e : c) {
-        if (e.sk == 0 || !w4a16_internal::pair_ring_instantiated(M, K, e.sk, e.sn, e.d)) continue;
+        if (e.sk == 0 || !w4a16_internal::pair_ring_instantiated(M, K, e.sk, e.sn, e.d, e.slices)) continue;
         Plan p;
         p.kernel = W4A16_KERNEL_PAIR_RING;
         p.splits = e.sk;
         p.rows = e.sn;
         p.unroll = e.d;
-        p.max_blocks = 0;
+        p.max_blocks = e.slices > 1 ? e.slices : 0;   // K slices
         *out = p;
         return true;
     }
@@ -818,6 +842,12 @@ int make_plan(const void* act, const void* packed, const void* scales, int64_t M
     // tolerance; the one-shot MFMA kernel (offset decode, faster on wide
     // layers of short rows: 2048 x 8192 at M = 12 5.50 against 5.90 us)
     // stays behind W4A16_DECODE=mfma_oneshot.
+    const bool scales4 = (reinterpret_cast<uintptr_t>(scales) & 3u) == 0;
+    // M = 9..16 on the paired ring kernel's 16-row-slot form (exact decode)
+    // where a shape is measured and instantiated
+    if (aligned && M > 8 && M <= 16 && (family == 0 || family == W4A16_KERNEL_PAIR_RING) && scales4 &&
+        plan_pair_ring(M, N, K, out, workspace))
+        return W4A16_OK;
     if (aligned && family == 0 && pair16_route(M, N, K)) {
         *out = plan_mfma_pair(M, N, K);
         return W4A16_OK;
@@ -868,7 +898,6 @@ int make_plan(const void* act, const void* packed, const void* scales, int64_t M
     //   MFMA up to K = 8192 when N >= 4096 gives it enough row blocks;
     //   otherwise the looped VALU kernel for M = 1, M = 2 (K <= 16384) or
     //   M <= 4 (K <= 4096), else the looped MFMA kernel.
-    const bool scales4 = (reinterpret_cast<uintptr_t>(scales) & 3u) == 0;
     if ((family == 0 || family == W4A16_KERNEL_PAIR_RING) && rows == 0 && scales4 && plan_pair_ring(M, N, K, out))
         return W4A16_OK;
     if (family == W4A16_KERNEL_PAIR_RING) family = 0;   // a shape without an instantiation
@@ -1198,6 +1227,13 @@ int check_scalar_args(int64_t M, int64_t N, int64_t K, int64_t G) {
     return W4A16_OK;
 }
 
+// Workspace a plan's kernels take (fp32 partial sums of split-K routes).
+int64_t plan_workspace_bytes(const Plan& p, int64_t M, int64_t N) {
+    if (p.kernel == W4A16_KERNEL_PAIR_SPLIT) return w4a16_internal::pair_split_workspace_bytes(M, N, p.splits);
+    if (p.kernel == W4A16_KERNEL_PAIR_RING) return w4a16_internal::pair_ring_workspace_bytes(M, N, p.max_blocks);
+    return 0;
+}
+
 int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* scales, void* out,
              int64_t M, int64_t N, int64_t K, int64_t G, void* stream, bool own_plans = true,
              void* workspace = nullptr, int64_t workspace_bytes = 0) {
@@ -1217,8 +1253,8 @@ int run_plan(const Plan& p, const void* act, const uint8_t* packed, const void* 
         case W4A16_KERNEL_MFMA_PAIR:
             return launch_mfma_pair_rows(p, own_plans, (int)M, x, packed, s, o, (int)N, (int)K, st);
         case W4A16_KERNEL_PAIR_RING:
-            return w4a16_internal::launch_pair_ring(p.splits, p.rows, p.unroll, (int)M, x, packed, s, o, (int)N, (int)K,
-                                                    st);
+            return w4a16_internal::launch_pair_ring(p.splits, p.rows, p.unroll, p.max_blocks, (int)M, x, packed, s, o,
+                                                    (int)N, (int)K, workspace, workspace_bytes, st);
         case W4A16_KERNEL_STREAM:
             return w4a16_internal::launch_stream(p.rows, p.splits, p.unroll, p.max_blocks, x, packed, s, o, (int)N,
                                                  (int)K, st);
@@ -1373,8 +1409,7 @@ int w4a16_linear_noalloc_f16(const void* activations, const uint8_t* packed_weig
     if (p.kernel == W4A16_KERNEL_NONE) return W4A16_OK;
     rc = check_pointers(activations, packed_weights, scales, output);
     if (rc != W4A16_OK) return rc;
-    int64_t need =
-        p.kernel == W4A16_KERNEL_PAIR_SPLIT ? w4a16_internal::pair_split_workspace_bytes(M, N, p.splits) : 0;
+    int64_t need = plan_workspace_bytes(p, M, N);
     if (need > kNoAllocScratchBytes) {
         // partial sums past the scratch: the route without a workspace (the
         // kernels w4a16_linear_f16 runs), which needs none
@@ -1396,7 +1431,7 @@ int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gr
     Plan p;
     alignas(16) static const uint8_t probe[16] = {};   // stands for 16-byte aligned operands
     if (make_plan(probe, probe, nullptr, M, N, K, group_size, &p, true) != W4A16_OK) return 0;
-    return p.kernel == W4A16_KERNEL_PAIR_SPLIT ? w4a16_internal::pair_split_workspace_bytes(M, N, p.splits) : 0;
+    return plan_workspace_bytes(p, M, N);
 }
 
 int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weights, const void* scales,
@@ -1424,9 +1459,9 @@ int w4a16_linear_f16_tuned(const void* activations, const uint8_t* packed_weight
                         "the streaming kernel needs group_size 128, M == 1 and 16-byte aligned activations and "
                         "weights");
     } else if (kernel == W4A16_KERNEL_PAIR_RING) {
-        if (group_size != 128 || M < 1 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
+        if (group_size != 128 || M < 1 || M > 16 || !aligned16(activations) || !aligned16(packed_weights))
             return fail(W4A16_ERR_CONFIG,
-                        "the paired ring kernel needs group_size 128, 1 <= M <= 8 and 16-byte aligned activations "
+                        "the paired ring kernel needs group_size 128, 1 <= M <= 16 and 16-byte aligned activations "
                         "and weights");
     } else if (kernel == W4A16_KERNEL_PAIR_STREAM) {
         if (group_size != 128 || M < 2 || M > 8 || !aligned16(activations) || !aligned16(packed_weights))
@@ -1544,6 +1579,12 @@ int w4a16_gemv_qkv_rope_f16(const void* activations, const void* norm_weight, fl
                        : launch_fused_t<false, false, false, true>(L, 2, 8, x, fz, packed_weights, sc, o, N, (int)K, st);
 }
 
+// Launch shape of the ring kernel's SiLU form at K = 2048 (wavefronts
+// splitting K, wavefronts on output blocks, pairs in flight): at M = 16,
+// 2048 x 2 x 5632, 7.78 us against 8.72 on (2, 2, 4) and 10.1 on the
+// 16-row-slot paired kernel's SiLU form.
+constexpr int kRingSiluShape[3] = {1, 4, 4};
+
 int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,
                           int64_t M, int64_t inter, int64_t K, int64_t group_size, void* stream) {
     int rc = check_scalar_args(M, 2 * inter, K, group_size);
@@ -1571,6 +1612,16 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
     // SiLU form): the 16-row-slot paired kernel's SiLU form, a gate and an up
     // block per wavefront (half the plain plan's row-block wavefronts, so the
     // same rows per workgroup and half the registers of the plain plan)
+    // M = 9..16 on rows of 2048 weights of wide layers: the paired ring
+    // kernel's SiLU form (16 row slots, exact decode, a gate and an up block
+    // per wavefront)
+    if (M > 8 && K == 2048 && 2 * inter >= 8192 && (reinterpret_cast<uintptr_t>(scales) & 3u) == 0 &&
+        inter <= INT32_MAX && w4a16_internal::pair_ring_silu_instantiated(M, K, kRingSiluShape[0], kRingSiluShape[1],
+                                                                          kRingSiluShape[2]))
+        return w4a16_internal::launch_pair_ring_silu(kRingSiluShape[0], kRingSiluShape[1], kRingSiluShape[2], (int)M,
+                                                     static_cast<const f16*>(activations), packed_weights,
+                                                     static_cast<const f16*>(scales), static_cast<f16*>(output),
+                                                     (int)inter, (int)K, st);
     if ((K > 4096 || (K <= 2048 && 2 * inter >= 8192)) && pair16_fits(M, 2 * inter, K, 8)) {
         const Plan q = plan_mfma_pair(M, 2 * inter, K);
         const int sn = q.max_blocks > 1 ? q.max_blocks / 2 : 1;

@@ -353,6 +353,16 @@ int pair_split_waves(int64_t M, int64_t N, int64_t K, int slices) {
     return (int)std::min<int64_t>(16, std::max<int64_t>(1, (blocks + resident - 1) / resident));
 }
 
+// o = fp16(part[0] + .. + part[slices - 1]) over mn outputs, slices 2..16
+// (the paired ring kernel's K slices).
+int launch_split_reduce(int slices, const float* part, w4a16::f16* o, int64_t mn, hipStream_t stream) {
+    if (slices < 2 || slices > 16) return fail(W4A16_ERR_CONFIG, "split-K reduce: 2..16 slices");
+    hipLaunchKernelGGL(pick_reduce(slices), dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, stream, part, o, (int)mn);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    return W4A16_OK;
+}
+
 int launch_pair_split(int depth, int waves, int slices, int max_blocks, int M, const void* x, const uint8_t* w,
                       const void* s, void* o, int N, int K, void* part, int64_t part_bytes, hipStream_t stream) {
     if (M < 2 || M > 8) return fail(W4A16_ERR_CONFIG, "split-K paired kernel needs 2 <= M <= 8");

@@ -64,40 +64,69 @@ namespace w4a16 {
 // ---------------------------------------------------------------------------
 __host__ __device__ constexpr int pair_ring_group_bytes() { return 272; }
 
-__host__ __device__ constexpr int64_t pair_ring_row_bytes(int SK, int PPW) {
-    // 2 SK PPW groups of 272 bytes, padded to 32 mod 256
-    return ((int64_t)2 * SK * PPW * 272 + 224 + 255) / 256 * 256 - 224;
+__host__ __device__ constexpr int64_t pair_ring_row_bytes(int SK, int PPW, int MS = 8) {
+    // 2 SK PPW groups of 272 bytes, padded to 32 mod 256 (16 mod 256 with 16
+    // row slots, whose A-fragment reads take 16 rows of one group)
+    return ((int64_t)2 * SK * PPW * 272 + (MS == 16 ? 240 : 224) + 255) / 256 * 256 - (MS == 16 ? 240 : 224);
 }
 
 __host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN, int RB, int PPW) {
-    return (MS == 1 ? (int64_t)2 * SK * PPW * 272 : MS * pair_ring_row_bytes(SK, PPW))   // staged units
-           + (int64_t)2 * SK * PPW * (MS == 1 ? 1 : 8) * 4                              // per-(group, row) bias
-           + (int64_t)8 * RB * SN * 2 * SK * PPW * 4                                    // fp32 scales
-           + (SK > 1 ? (int64_t)SN * RB * SK * (MS == 1 ? 8 : 64) * 4 : 0);            // K-slice partials
+    return (MS == 1 ? (int64_t)2 * SK * PPW * 272 : MS * pair_ring_row_bytes(SK, PPW, MS))   // staged units
+           + (MS == 16 ? 0 : (int64_t)2 * SK * PPW * (MS == 1 ? 1 : 8) * 4)                 // per-(group, row) bias
+           + (int64_t)8 * RB * SN * 2 * SK * PPW * 4                                         // fp32 scales
+           + (SK > 1 ? (int64_t)SN * RB * SK * (MS == 1 ? 8 : MS == 16 ? 128 : 64) * 4 : 0); // K-slice partials
 }
 
-template <int MS, int SK, int SN, int RB, int PPW, int D>
+// SPLIT (narrow layers of long rows): the K / 256 pairs are cut into S
+// slices of SK PPW pairs; workgroup b takes slice b mod S of rows (b / S) R
+// .., stages only that slice's activations, and stores fp32 partial sums to
+// part[slice][m][n] instead of fp16 outputs (pair_split_reduce adds the
+// slices in slice order). Every CU then stages M K / S activations instead
+// of M K, which on such layers outweighs the CU's weights.
+//
+// MS = 16 (M = 9..16, a short prompt): the dequantized weights in B, exact
+// codes times the group scale rounded to fp16 once (as w4a16_dequantize_f16
+// writes them), the activations staged unscaled and no bias, summed in the
+// MFMA's fp32 accumulators across pairs: the reference's prefill (dequantize,
+// fp16 GEMM with fp32 accumulation) up to summation order. A rows are the 16
+// activation rows of one group, so each pair runs two MFMAs per word against
+// the same B (group 2p in A for B columns 0..7, group 2p + 1 for columns
+// 8..15) and a lane keeps both; the halves of an output sit in lanes l and
+// l + 8. The staged row stride is 16 mod 256 so the 16 rows of a fragment
+// read fall on distinct bank slots.
+//
+// SILU (MS = 16, RB = 2): N is the intermediate width, the weights hold 2 N
+// rows (gate rows, then up rows); block 0 of a wavefront is gate rows n ..
+// n + 7 and block 1 the up rows N + n .., and the output is
+// fp16(fp16(silu(fp16(g))) * fp16(u)), the roundings of silu(gate) * up on
+// the op's fp16 outputs.
+template <int MS, int SK, int SN, int RB, int PPW, int D, bool SPLIT = false, bool SILU = false>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
-               f16* __restrict__ out, int M, int N, int K) {
-    static_assert(MS == 1 || MS == 4 || MS == 8, "1, 4 or 8 activation row slots");
+               f16* __restrict__ out, int M, int N, int K, float* __restrict__ part, int S) {
+    static_assert(MS == 1 || MS == 4 || MS == 8 || MS == 16, "1, 4, 8 or 16 activation row slots");
     static_assert(D >= 1 && D <= PPW, "ring depth 1 .. PPW");
+    static_assert(!SILU || (MS == 16 && RB == 2 && !SPLIT), "the SiLU form pairs a gate block and its up block");
+    constexpr bool W16 = MS == 16;            // exact decode, two MFMAs per word
     constexpr int W = SK * SN;
     constexpr int T = 64 * W;
     constexpr int PS = SK * PPW;              // pairs staged
     constexpr int GS = 2 * PS;                // groups staged
     constexpr int US = GS * 16;               // activation units staged per row
     constexpr int XU = (MS * US + T - 1) / T; // staging units per thread
-    constexpr int R = 8 * RB * SN;            // rows per workgroup
-    constexpr int SD = R * PS;                // scale words (pairs) per workgroup
+    constexpr int RO = SILU ? 1 : RB;         // output blocks of 8 rows per wavefront
+    constexpr int R = 8 * RO * SN;            // output rows per workgroup
+    constexpr int SR = 8 * RB * SN;           // weight rows per workgroup
+    constexpr int SD = SR * PS;               // scale words (pairs) per workgroup
     constexpr int SU = (SD + T - 1) / T;      // scale words per thread
-    constexpr int RS = MS == 1 ? 0 : (int)pair_ring_row_bytes(SK, PPW);
+    constexpr int RS = MS == 1 ? 0 : (int)pair_ring_row_bytes(SK, PPW, MS);
     constexpr int XB = MS == 1 ? GS * 272 : MS * RS;
     constexpr int BS = MS == 1 ? 1 : 8;       // bias slots per group
+    constexpr int NB = W16 ? 0 : GS * BS;     // bias words
     extern __shared__ __align__(16) uint8_t smem[];
     float* bias = reinterpret_cast<float*>(smem + XB);   // [GS][BS]
-    float* sc = bias + GS * BS;                            // [R][2][PS]
-    float* red = sc + R * 2 * PS;                          // [SN RB][SK][8 or 64]
+    float* sc = bias + NB;                                 // [SR][2][PS]
+    float* red = sc + SR * 2 * PS;                         // [SN RB][SK][8, 64 or 128]
 
     const int G = K >> 7;
     const int P = G >> 1;
@@ -107,9 +136,16 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     const int col = lane & 15, q = lane >> 4;
     const int brow = col & 7, h = col >> 3;
     const int kw = wave % SK, nb = wave / SK;
-    const int n0 = blockIdx.x * R;
-    const int nw = n0 + nb * RB * 8;
+    const int sl = SPLIT ? (int)blockIdx.x % S : 0;   // K slice
+    const int n0 = (SPLIT ? (int)blockIdx.x / S : (int)blockIdx.x) * R;
+    const int nw = n0 + nb * RO * 8;                  // first output row of the wavefront
+    const int pb = sl * PS;                           // first pair of the slice
     const uint32_t row_bytes = (uint32_t)(K >> 1);
+    // weight row of block b, row r (clamped to the layer)
+    auto wrow = [&](int base, int b, int r) {
+        if constexpr (SILU) return (b ? N : 0) + min(base + r, N - 1);
+        else return min(base + 8 * b + r, N - 1);
+    };
 
     // 1. requests: activation units (clamped; units past K or M are not
     // staged), the workgroup's scale words, then the wavefront's first D
@@ -119,7 +155,7 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     for (int u = 0; u < XU; ++u) {
         const int i = threadIdx.x + u * T;
         const int m = MS == 1 ? 0 : min(i / US, M - 1);
-        const int uu = min(MS == 1 ? i : i % US, units - 1);
+        const int uu = min(pb * 32 + (MS == 1 ? i : i % US), units - 1);
         a[u] = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + (size_t)uu * 8);
     }
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(scales);
@@ -127,17 +163,18 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
 #pragma unroll
     for (int u = 0; u < SU; ++u) {
         const int d = threadIdx.x + u * T;
-        const int r = d / PS, p = d - r * PS;
-        const int n = min(n0 + r, N - 1);
-        sw[u] = s32[(size_t)n * P + min(p, P - 1)];
+        const int r = d / PS, p = d - r * PS;   // staged row r = (wavefront, block, row)
+        const int blk = r >> 3;
+        const int n = wrow(n0 + (blk / RB) * RO * 8, blk % RB, r & 7);
+        sw[u] = s32[(size_t)n * P + min(pb + p, P - 1)];
     }
     // weights of pair j go to ring slot j % D
     u32x4 wv[D][RB];
     auto issue = [&](int j) {
-        const uint32_t pg = (uint32_t)min(kw * PPW + j, P - 1);
+        const uint32_t pg = (uint32_t)min(pb + kw * PPW + j, P - 1);
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
-            const int n = min(nw + 8 * b + brow, N - 1);
+            const int n = wrow(nw, b, brow);
             wv[j % D][b] = load_stream(reinterpret_cast<const u32x4*>(w + (size_t)n * row_bytes + pg * 128u +
                                                                      (uint32_t)(h * 64 + q * 16)));
         }
@@ -148,7 +185,7 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
 
     // 2. staging: unit i = m US + uu covers x[m][8 uu .. 8 uu + 7] (group
     // uu / 16); the 16 units of a (row, group) sit in one DPP row, whose sum
-    // is that row's bias for the group
+    // is that row's bias for the group (offset decode only)
     const f16x2 sixteenth = {(f16)0.0625f, (f16)0.0625f};
     const f16x2 c_even = {(f16)1032.0f, (f16)1032.0f};
     const f16x2 c_odd = {(f16)1152.0f, (f16)1152.0f};
@@ -158,21 +195,26 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         const int m = MS == 1 ? 0 : i / US;
         const int uu = MS == 1 ? i : i % US;
         u32x4 v = permute8(a[u]);
-        v.y = as_u32(as_f16x2(v.y) * sixteenth);
-        v.w = as_u32(as_f16x2(v.w) * sixteenth);
-        if (uu >= units) v = (u32x4){0u, 0u, 0u, 0u};
-        float cs = __builtin_amdgcn_fdot2(as_f16x2(v.x), c_even, 0.0f, false);
-        cs = __builtin_amdgcn_fdot2(as_f16x2(v.y), c_odd, cs, false);
-        cs = __builtin_amdgcn_fdot2(as_f16x2(v.z), c_even, cs, false);
-        cs = __builtin_amdgcn_fdot2(as_f16x2(v.w), c_odd, cs, false);
-        cs += dpp<0xB1>(cs);
-        cs += dpp<0x4E>(cs);
-        cs += dpp<0x141>(cs);
-        cs += dpp<0x140>(cs);
+        if constexpr (!W16) {
+            v.y = as_u32(as_f16x2(v.y) * sixteenth);
+            v.w = as_u32(as_f16x2(v.w) * sixteenth);
+        }
+        if (pb * 32 + uu >= units) v = (u32x4){0u, 0u, 0u, 0u};
+        float cs = 0.0f;
+        if constexpr (!W16) {
+            cs = __builtin_amdgcn_fdot2(as_f16x2(v.x), c_even, 0.0f, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(v.y), c_odd, cs, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(v.z), c_even, cs, false);
+            cs = __builtin_amdgcn_fdot2(as_f16x2(v.w), c_odd, cs, false);
+            cs += dpp<0xB1>(cs);
+            cs += dpp<0x4E>(cs);
+            cs += dpp<0x141>(cs);
+            cs += dpp<0x140>(cs);
+        }
         if ((MS == 1 ? i < US : m < M) && i < MS * US) {
             const int g = uu >> 4;
             *reinterpret_cast<u32x4*>(smem + (MS == 1 ? 0 : m * RS) + g * 272 + (uu & 15) * 16) = v;
-            if ((uu & 15) == 0) bias[g * BS + (MS == 1 ? 0 : m)] = -cs;
+            if (!W16 && (uu & 15) == 0) bias[g * BS + (MS == 1 ? 0 : m)] = -cs;
         }
     }
 #pragma unroll
@@ -180,7 +222,7 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         const int d = threadIdx.x + u * T;
         const int r = d / PS, p = d - r * PS;
         if (d < SD) {
-            const bool ok = p < P;
+            const bool ok = pb + p < P;
             const f16x2 sv = as_f16x2(sw[u]);
             sc[(2 * r) * PS + p] = ok ? (float)sv.x : 0.0f;
             sc[(2 * r + 1) * PS + p] = ok ? (float)sv.y : 0.0f;
@@ -189,43 +231,66 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     __syncthreads();
 
     // 3. pairs in arrival order; A fragments of pair j + 1 read during pair j.
-    // A row c = activation row c & 7 (clamped to M - 1) of group 2p + h; D
-    // rows 4q .. 4q + 3 = activation rows 4 (q & 1) .. + 3 of group
-    // 2p + (q >> 1)
-    const int arow = MS == 1 ? 0 : min(brow, M - 1);
-    const uint8_t* xl = smem + (MS == 1 ? 0 : arow * RS) + (2 * kw * PPW + h) * 272 + q * 64;
+    // MS <= 8: A row c = activation row c & 7 (clamped to M - 1) of group
+    // 2p + h; D rows 4q .. 4q + 3 = activation rows 4 (q & 1) .. + 3 of group
+    // 2p + (q >> 1). MS = 16: A row c = activation row c (clamped) of group
+    // 2p (first MFMA) or 2p + 1 (second); D rows 4q .. 4q + 3 = activation
+    // rows 4q .. 4q + 3.
+    constexpr int H = W16 ? 2 : 1;   // MFMAs per word
+    const int arow = MS == 1 ? 0 : min(W16 ? col : brow, M - 1);
+    const uint8_t* xl = smem + (MS == 1 ? 0 : arow * RS) + (2 * kw * PPW + (W16 ? 0 : h)) * 272 + q * 64;
     const float* bl = MS == 1 ? bias + 2 * kw * PPW + h : bias + (2 * kw * PPW + (q >> 1)) * 8 + 4 * (q & 1);
     const float* scl[RB];
 #pragma unroll
     for (int b = 0; b < RB; ++b) scl[b] = sc + (2 * (8 * (nb * RB + b) + brow) + h) * PS + kw * PPW;
     constexpr int NA = MS == 1 ? 1 : 4;   // accumulators per lane
     float acc[RB][NA];
-    f32x4 d[RB];
+    f32x4 d[RB][H];
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
 #pragma unroll
         for (int e = 0; e < NA; ++e) acc[b][e] = 0.0f;
-        d[b] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    u32x4 A0[4], A1[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) A0[t] = *reinterpret_cast<const u32x4*>(xl + t * 16);
+        for (int hh = 0; hh < H; ++hh) d[b][hh] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    u32x4 A0[H][4], A1[H][4];
+#pragma unroll
+    for (int hh = 0; hh < H; ++hh)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) A0[hh][t] = *reinterpret_cast<const u32x4*>(xl + hh * 272 + t * 16);
 #pragma unroll
     for (int j = 0; j < PPW; ++j) {
-        u32x4 (&cur)[4] = (j & 1) ? A1 : A0;
-        u32x4 (&nxt)[4] = (j & 1) ? A0 : A1;
+        u32x4 (&cur)[H][4] = (j & 1) ? A1 : A0;
+        u32x4 (&nxt)[H][4] = (j & 1) ? A0 : A1;
         if (j + 1 < PPW) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) nxt[t] = *reinterpret_cast<const u32x4*>(xl + (j + 1) * 544 + t * 16);
+            for (int hh = 0; hh < H; ++hh)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    nxt[hh][t] = *reinterpret_cast<const u32x4*>(xl + (j + 1) * 544 + hh * 272 + t * 16);
         }
-        f32x4 bj;
+        f32x4 bj = {0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (MS == 1) bj.x = bl[2 * j];
-        else bj = *reinterpret_cast<const f32x4*>(bl + 16 * j);
+        else if constexpr (!W16) bj = *reinterpret_cast<const f32x4*>(bl + 16 * j);
         Codes8 cw[RB][4];
 #pragma unroll
-        for (int b = 0; b < RB; ++b)
+        for (int b = 0; b < RB; ++b) {
+            if constexpr (W16) {
+                // B = fp16_rn(code * scale): the staged fp32 scale is an fp16
+                // value, so the conversion back is exact (0 past K)
+                const f16 s16 = (f16)scl[b][j];
+                const f16x2 s2 = {s16, s16};
 #pragma unroll
-            for (int t = 0; t < 4; ++t) cw[b][t] = unpack8_offset(wv[j % D][b][t]);
+                for (int t = 0; t < 4; ++t) {
+                    cw[b][t] = unpack8(wv[j % D][b][t]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) cw[b][t].p[e] = cw[b][t].p[e] * s2;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) cw[b][t] = unpack8_offset(wv[j % D][b][t]);
+            }
+        }
         if (j + D < PPW) {
             // the slot is free once decoded: request pair j + D
             __builtin_amdgcn_sched_barrier(0);
@@ -234,47 +299,63 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         }
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
-            f32x4 dd = d[b];
-            if constexpr (MS == 1) dd.x = bj.x;   // registers 1..3 carry unused values
-            else dd = bj;
+            f32x4 dd[H];
+#pragma unroll
+            for (int hh = 0; hh < H; ++hh) dd[hh] = d[b][hh];
+            if constexpr (MS == 1) dd[0].x = bj.x;   // registers 1..3 carry unused values
+            else if constexpr (!W16) dd[0] = bj;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const f16x8 bt = __builtin_bit_cast(f16x8, (u32x4){as_u32(cw[b][t].p[0]), as_u32(cw[b][t].p[1]),
                                                                    as_u32(cw[b][t].p[2]), as_u32(cw[b][t].p[3])});
-                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[t]), bt, dd, 0, 0, 0);
-            }
-            const float s = scl[b][j];
 #pragma unroll
-            for (int e = 0; e < NA; ++e) acc[b][e] = __builtin_fmaf(dd[e], s, acc[b][e]);
-            d[b] = dd;
+                for (int hh = 0; hh < H; ++hh)
+                    dd[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur[hh][t]), bt, dd[hh],
+                                                                    0, 0, 0);
+            }
+            if constexpr (!W16) {
+                const float s = scl[b][j];
+#pragma unroll
+                for (int e = 0; e < NA; ++e) acc[b][e] = __builtin_fmaf(dd[0][e], s, acc[b][e]);
+            }
+#pragma unroll
+            for (int hh = 0; hh < H; ++hh) d[b][hh] = dd[hh];
         }
     }
 
-    // 4. halves (lane l + 40 onto lane l), then the K slices in order. M = 1:
-    // lane c < 8 holds row c; else lane 16 q + c (q < 2, c < 8) holds
-    // activation rows 4q .. 4q + 3 of weight row c.
-    constexpr int RED = MS == 1 ? 8 : 64;
-    const bool keep = MS == 1 ? lane < 8 : (q < 2 && col < 8);
+    // 4. halves (MS <= 8: lane l + 40 onto lane l; MS = 16: lane l + 8 onto
+    // lane l), then the K slices in order. M = 1: lane c < 8 holds row c;
+    // else lane 16 q + c (c < 8; q < 2 for MS <= 8) holds activation rows
+    // 4q .. 4q + 3 of weight row c.
+    constexpr int RED = MS == 1 ? 8 : W16 ? 128 : 64;
+    const bool keep = MS == 1 ? lane < 8 : ((W16 || q < 2) && col < 8);
     const int rl = MS == 1 ? lane : (q * 8 + col) * 4;   // slot in a block's partials
     float v[RB][NA];
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int e = 0; e < NA; ++e) v[b][e] = acc[b][e] + __shfl(acc[b][e], lane + 40);
-    auto store = [&](int b, const float (&vb)[NA]) {
-        const int n = nw + 8 * b + brow;
-        if (n >= N) return;
-#pragma unroll
         for (int e = 0; e < NA; ++e) {
-            const int m = MS == 1 ? 0 : 4 * q + e;
-            if (MS == 1 || m < M) out[(size_t)m * N + n] = (f16)vb[e];
+            if constexpr (W16) v[b][e] = d[b][0][e] + __shfl(d[b][1][e], lane + 8);
+            else v[b][e] = acc[b][e] + __shfl(acc[b][e], lane + 40);
+        }
+    auto store = [&](const float (&vv)[RB][NA]) {
+#pragma unroll
+        for (int b = 0; b < RO; ++b) {
+            const int n = nw + 8 * b + brow;
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < NA; ++e) {
+                const int m = MS == 1 ? 0 : 4 * q + e;
+                if (MS == 1 || m < M) {
+                    if constexpr (SPLIT) part[((size_t)sl * M + m) * N + n] = vv[b][e];
+                    else if constexpr (SILU) out[(size_t)m * N + n] = gemm_silu_mul(vv[0][e], vv[1][e]);
+                    else out[(size_t)m * N + n] = (f16)vv[b][e];
+                }
+            }
         }
     };
     if constexpr (SK == 1) {
-        if (keep) {
-#pragma unroll
-            for (int b = 0; b < RB; ++b) store(b, v[b]);
-        }
+        if (keep) store(v);
     } else {
         if (keep) {
 #pragma unroll
@@ -284,17 +365,16 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         }
         __syncthreads();
         if (kw != 0 || !keep) return;
+        float t[RB][NA];
 #pragma unroll
-        for (int b = 0; b < RB; ++b) {
-            float t[NA];
+        for (int b = 0; b < RB; ++b)
 #pragma unroll
             for (int e = 0; e < NA; ++e) {
-                t[e] = red[((nb * RB + b) * SK) * RED + rl + e];
+                t[b][e] = red[((nb * RB + b) * SK) * RED + rl + e];
 #pragma unroll
-                for (int s = 1; s < SK; ++s) t[e] += red[((nb * RB + b) * SK + s) * RED + rl + e];
+                for (int s = 1; s < SK; ++s) t[b][e] += red[((nb * RB + b) * SK + s) * RED + rl + e];
             }
-            store(b, t);
-        }
+        store(t);
     }
 }
 

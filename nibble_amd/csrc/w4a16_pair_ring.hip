@@ -1,4 +1,4 @@
-// Launcher of the paired-layout ring GEMV (w4a16_pair_ring.h, M = 1..8) and
+// Launcher of the paired-layout ring GEMV (w4a16_pair_ring.h, M = 1..16) and
 // its instantiations, in a translation unit of their own. Called by the
 // dispatcher in w4a16_hip.hip.
 #include "w4a16_hip.h"
@@ -12,6 +12,7 @@
 namespace w4a16_internal {
 void set_last_error(const std::string& message);   // w4a16_hip.hip
 int ensure_lds(const void* kernel, int bytes);     // w4a16_hip.hip: raise the dynamic-LDS limit once
+int launch_split_reduce(int slices, const float* part, w4a16::f16* o, int64_t mn, hipStream_t stream);   // w4a16_pair.hip
 }  // namespace w4a16_internal
 
 namespace {
@@ -23,9 +24,9 @@ int fail(int code, const std::string& message) {
     return code;
 }
 
-using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int);
+using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int, float*, int);
 
-int row_slots(int M) { return M <= 1 ? 1 : M <= 4 ? 4 : 8; }
+int row_slots(int M) { return M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 // Instantiated (row slots, wavefronts splitting K, wavefronts on 8-row
 // blocks, pairs per wavefront, pairs in flight): the launch shapes the M = 1
@@ -57,8 +58,47 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
     W4A16_P(8, 4, 2, 4, 4)    // K = 4096, N < 8192
     W4A16_P(8, 1, 8, 16, 6)   // K = 4096, N >= 8192
     W4A16_P(8, 2, 4, 16, 4)   // K = 8192, N <= 8192
+    // M = 9..16 (exact decode)
+    W4A16_P(16, 8, 1, 1, 1)   // K = 2048, N <= 2048
+    W4A16_P(16, 4, 2, 2, 2)   // K = 2048, N <= 4096
+    W4A16_P(16, 2, 4, 4, 4)   // K = 2048, N > 4096
+    W4A16_P(16, 1, 4, 8, 4)   // K = 2048: the SiLU form's K split over plain rows
 #undef W4A16_P
     return nullptr;
+}
+
+// Split-K instantiations (slices > 1; row slots, wavefronts, pairs per
+// wavefront per slice, pairs in flight): M = 9..16 on 5632 x 2048 (8 slices
+// of 3 pairs), 14336 x 4096 (4 of 14) and 8192 x 8192 (2 of 16).
+Kern pick_split(int ms, int sk, int sn, int ppw, int depth) {
+#define W4A16_P(MS, SK, SN, PPW, D) \
+    if (ms == MS && sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<MS, SK, SN, 1, PPW, D, true>;
+    W4A16_P(16, 1, 8, 3, 3)
+    W4A16_P(16, 1, 8, 14, 4)
+    W4A16_P(16, 1, 8, 16, 4)
+#undef W4A16_P
+    return nullptr;
+}
+
+// SiLU form (16 row slots, a gate and an up block per wavefront):
+// (wavefronts splitting K, wavefronts on output blocks, pairs per
+// wavefront, pairs in flight). Measured at M = 16 / 9, 2048 x 2 x 5632
+// (graph timing): (1, 4, 8, 4) 7.78 / 7.51 us, (4, 2, 2, 2) 8.26 / 7.61,
+// (2, 4, 4, 4) 8.41 / 7.99, (2, 2, 4, 4) 8.73 / 8.30, (8, 1, 1, 1) 9.57 /
+// 8.64, (1, 8, 8, 4) 10.09 / 9.70.
+Kern pick_silu(int sk, int sn, int ppw, int depth) {
+#define W4A16_P(SK, SN, PPW, D) \
+    if (sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<16, SK, SN, 2, PPW, D, false, true>;
+    W4A16_P(1, 4, 8, 4)   // K = 2048
+#undef W4A16_P
+    return nullptr;
+}
+
+// Pairs per wavefront for `slices` K slices of `sk` wavefronts each.
+int ppw_of(int64_t K, int sk, int slices) {
+    const int64_t P = K / 256;
+    const int64_t per_slice = (P + slices - 1) / slices;
+    return (int)((per_slice + sk - 1) / sk);
 }
 
 }  // namespace
@@ -68,36 +108,92 @@ namespace w4a16_internal {
 // Pairs per wavefront for K split over `sk` wavefronts (G = K / 128 even).
 int pair_ring_ppw(int64_t K, int sk) { return sk > 0 ? (int)((K / 256 + sk - 1) / sk) : 0; }
 
-bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth) {
-    if (M < 1 || M > 8 || K < 256 || K % 256 != 0) return false;
-    const int ppw = pair_ring_ppw(K, sk);
-    const int ms = row_slots((int)M);
-    return pick(ms, sk, sn, ppw, depth) != nullptr && w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw) <= kMaxLdsBytes;
+int64_t pair_ring_workspace_bytes(int64_t M, int64_t N, int slices) {
+    return slices > 1 ? (int64_t)slices * M * N * 4 : 0;
 }
 
-int launch_pair_ring(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w, const w4a16::f16* s,
-                     w4a16::f16* o, int N, int K, hipStream_t stream) {
-    if (M < 1 || M > 8) return fail(W4A16_ERR_CONFIG, "paired ring kernel: 1 <= M <= 8");
+// Slices > 1 must leave none empty: (slices - 1) ceil(P / slices) < P.
+bool pair_ring_slices_valid(int64_t K, int slices) {
+    const int64_t P = K / 256;
+    return slices == 1 || (slices >= 2 && slices <= 16 && (int64_t)(slices - 1) * ((P + slices - 1) / slices) < P);
+}
+
+bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth, int slices) {
+    if (M < 1 || M > 16 || K < 256 || K % 256 != 0 || sk < 1) return false;
+    if (slices < 1) slices = 1;
+    if (!pair_ring_slices_valid(K, slices)) return false;
+    const int ppw = ppw_of(K, sk, slices);
+    const int ms = row_slots((int)M);
+    const Kern k = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : pick(ms, sk, sn, ppw, depth);
+    return k != nullptr && w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw) <= kMaxLdsBytes;
+}
+
+bool pair_ring_silu_instantiated(int64_t M, int64_t K, int sk, int sn, int depth) {
+    if (M < 9 || M > 16 || K < 256 || K % 256 != 0 || sk < 1) return false;
+    const int ppw = ppw_of(K, sk, 1);
+    return pick_silu(sk, sn, ppw, depth) != nullptr && w4a16::pair_ring_lds_bytes(16, sk, sn, 2, ppw) <= kMaxLdsBytes;
+}
+
+int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::f16* x, const uint8_t* w,
+                     const w4a16::f16* s, w4a16::f16* o, int N, int K, void* part, int64_t part_bytes,
+                     hipStream_t stream) {
+    if (M < 1 || M > 16) return fail(W4A16_ERR_CONFIG, "paired ring kernel: 1 <= M <= 16");
     if (K < 256 || K % 256 != 0)
         return fail(W4A16_ERR_CONFIG, "paired ring kernel: K must be a multiple of 256 (an even group count)");
     if (reinterpret_cast<uintptr_t>(s) & 3u)
         return fail(W4A16_ERR_CONFIG, "paired ring kernel: scales must be 4-byte aligned");
-    const int ppw = pair_ring_ppw(K, sk);
+    if (slices < 1) slices = 1;
+    if (!pair_ring_slices_valid(K, slices))
+        return fail(W4A16_ERR_CONFIG, "paired ring kernel: max_blocks (K slices) 1..16, each slice non-empty");
+    if (sk < 1) return fail(W4A16_ERR_CONFIG, "paired ring kernel: splits (wavefronts splitting K) must be positive");
+    const int ppw = ppw_of(K, sk, slices);
     const int ms = row_slots(M);
-    Kern kern = pick(ms, sk, sn, ppw, depth);
+    Kern kern = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : pick(ms, sk, sn, ppw, depth);
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
                     "paired ring kernel: (splits, rows, pairs per wavefront, unroll) not instantiated for this M; "
                     "M = 1: (1,3,8,8) (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6) (2,4,16,4) (1,7,32,6) "
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
-                    "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4)");
+                    "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); "
+                    "M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3) (1,8,14,4) "
+                    "(1,8,16,4)");
     const int64_t lds = w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired ring kernel: staging exceeds LDS");
+    const int64_t need = pair_ring_workspace_bytes(M, N, slices);
+    if (slices > 1 && (part == nullptr || part_bytes < need || (reinterpret_cast<uintptr_t>(part) & 15u)))
+        return fail(W4A16_ERR_CONFIG, "paired ring kernel: K slices need a 16-byte aligned workspace of " +
+                                          std::to_string(need) + " bytes (w4a16_linear_workspace_bytes)");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
     if (rc != W4A16_OK) return rc;
     const int rows = 8 * sn;
-    const int blocks = (N + rows - 1) / rows;
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, N, K);
+    const int blocks = (N + rows - 1) / rows * slices;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, N, K,
+                       static_cast<float*>(part), slices);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
+    if (slices > 1) return launch_split_reduce(slices, static_cast<const float*>(part), o, (int64_t)M * N, stream);
+    return W4A16_OK;
+}
+
+int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w,
+                          const w4a16::f16* s, w4a16::f16* o, int inter, int K, hipStream_t stream) {
+    if (M < 9 || M > 16) return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: 9 <= M <= 16");
+    if (K < 256 || K % 256 != 0)
+        return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: K must be a multiple of 256 (an even group count)");
+    if (reinterpret_cast<uintptr_t>(s) & 3u)
+        return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: scales must be 4-byte aligned");
+    if (sk < 1) return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: splits must be positive");
+    const int ppw = ppw_of(K, sk, 1);
+    Kern kern = pick_silu(sk, sn, ppw, depth);
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: shape not instantiated");
+    const int64_t lds = w4a16::pair_ring_lds_bytes(16, sk, sn, 2, ppw);
+    if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired ring SiLU kernel: staging exceeds LDS");
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int rows = 8 * sn;
+    const int blocks = (inter + rows - 1) / rows;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, inter, K,
+                       (float*)nullptr, 1);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
     return W4A16_OK;

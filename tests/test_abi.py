@@ -374,15 +374,18 @@ def test_m2_routing(monkeypatch):
 
 
 def test_short_prompt_routing(monkeypatch):
-    """M = 9..16: the 16-row-slot paired kernel on rows longer than 4096
-    weights whose plan keeps 2 wavefronts or fewer on weight blocks (8192 x
-    8192 would take 4 and spill), else the GEMM; both put the dequantized
-    fp16 weights in B. The offset-decode one-shot MFMA kernel only with its
-    selector."""
+    """M = 9..16: the paired ring kernel's 16-row-slot form on rows of 2048
+    weights of 1024 .. 16384-row layers; the 16-row-slot paired kernel on
+    rows longer than 4096 weights whose plan keeps 2 wavefronts or fewer on
+    weight blocks (8192 x 8192 would take 4 and spill), else the GEMM; all
+    three put the dequantized fp16 weights in B. The offset-decode one-shot
+    MFMA kernel only with its selector. (Without a workspace: the ring
+    kernel's K-slice plans need one.)"""
     monkeypatch.delenv("W4A16_DECODE", raising=False)
     monkeypatch.delenv("W4A16_ROWS_PER_WARP", raising=False)
-    for m, k, n, kernel in [(12, 2048, 8192, "gemm"), (16, 2048, 32000, "gemm"),
-                            (9, 1024, 16384, "gemm"), (12, 2048, 4096, "gemm"), (16, 2048, 2560, "gemm"),
+    for m, k, n, kernel in [(12, 2048, 8192, "pair_ring"), (16, 2048, 32000, "gemm"), (16, 2048, 512, "gemm"),
+                            (9, 1024, 16384, "gemm"), (12, 2048, 4096, "pair_ring"), (16, 2048, 2560, "pair_ring"),
+                            (16, 2048, 2048, "pair_ring"), (16, 2048, 11264, "pair_ring"),
                             (16, 4096, 14336, "gemm"), (16, 8192, 8192, "gemm"), (12, 8192, 4096, "mfma_pair"),
                             (9, 14336, 4096, "mfma_pair"), (12, 5632, 2048, "mfma_pair"), (17, 2048, 8192, "gemm")]:
         assert _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)["kernel"] == kernel, (m, k, n)

@@ -9,6 +9,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+import oracle
 from nibble_amd import _lib
 from tests._cases import assert_parity, expected, make_case
 
@@ -39,15 +40,24 @@ SMALL = ([(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES4 for k in ks for m in (2
          [(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES8 for k in ks for m in (5, 8)])
 
 
-def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0):
+# M = 9..16 (16 row slots, exact decode): (splits, rows, unroll, K slices,
+# K values whose pairs per wavefront per slice match the instantiation)
+SHAPES16 = [(8, 1, 1, 1, (2048, 1792)), (4, 2, 2, 1, (2048, 1536)), (2, 4, 4, 1, (2048, 1792)),
+            (1, 4, 4, 1, (2048,)),
+            (1, 8, 3, 8, (5632, 6144)),      # 5632: 22 pairs in 8 slices of 3, the last holding 1
+            (1, 8, 4, 4, (14336, 14080)), (1, 8, 4, 2, (8192, 7936))]   # 14 / 16 pairs per wavefront
+PROMPT = [(m, sk, sn, d, sl, k) for sk, sn, d, sl, ks in SHAPES16 for k in ks for m in (9, 13, 16)]
+
+
+def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0, slices=0):
     xd, pd, sd = x.to(dev), p.to(dev), s.to(dev)
     out = torch.full((x.shape[0], p.shape[0]), float("nan"), dtype=torch.float16, device=dev)
-    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} M={x.shape[0]} K={x.shape[1]} "
-          f"N={p.shape[0]}", flush=True)
+    print(f"[case] kernel={kernel} rows={rows} splits={splits} unroll={unroll} slices={slices} M={x.shape[0]} "
+          f"K={x.shape[1]} N={p.shape[0]}", flush=True)
     if kernel is None:
         _lib.linear_f16(xd, pd, sd, out)
     else:
-        _lib.linear_f16_tuned(xd, pd, sd, out, 128, kernel, rows, splits, unroll)
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, kernel, rows, splits, unroll, slices)
     torch.cuda.synchronize()
     return out
 
@@ -133,5 +143,70 @@ def test_pair_ring_m1_rejects(gpu):
     with pytest.raises(_lib.W4A16Error, match="not instantiated for this M"):
         _run(gpu, x, p, s, RING, 3, 1, 8)     # an M = 1 shape
     x, p, s = make_case(9, 4096, 16, seed=3)
-    with pytest.raises(_lib.W4A16Error, match="1 <= M <= 8"):
-        _run(gpu, x, p, s, RING, 8, 1, 6)
+    with pytest.raises(_lib.W4A16Error, match="not instantiated for this M"):
+        _run(gpu, x, p, s, RING, 8, 1, 6)     # an M = 1..8 shape at M = 9
+    x, p, s = make_case(17, 2048, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="1 <= M <= 16"):
+        _run(gpu, x, p, s, RING, 1, 8, 1)
+    x, p, s = make_case(16, 5632, 16, seed=3)
+    with pytest.raises(_lib.W4A16Error, match="each slice non-empty"):
+        _run(gpu, x, p, s, RING, 8, 1, 3, slices=12)   # 22 pairs in 12 slices of 2: the last empty
+    xd, pd, sd = x.to(gpu), p.to(gpu), s.to(gpu)
+    out = torch.empty((16, 16), dtype=torch.float16, device=gpu)
+    small = torch.empty((16 * 16 * 8 - 1,), dtype=torch.float32, device=gpu)
+    with pytest.raises(_lib.W4A16Error, match="workspace"):
+        _lib.linear_f16_tuned(xd, pd, sd, out, 128, RING, 8, 1, 3, 8, workspace=small)
+
+
+@pytest.mark.parametrize("m,splits,rows,unroll,slices,k", PROMPT)
+@pytest.mark.parametrize("n", [13, 300])
+def test_pair_ring_prompt_variants(gpu, m, splits, rows, unroll, slices, k, n):
+    """Every M = 9..16 shape (16 row slots, K slices included) at M = 9, 13
+    and 16, ragged N, K with a short or padded last slice, against the
+    oracle."""
+    x, p, s = make_case(m, k, n, seed=k + 3 * n + 13 * m + splits)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll, slices)
+    assert_parity(out, expected(x, p, s), f"pair_ring M={m} ({splits},{rows},{unroll}) x{slices} K={k} N={n}")
+
+
+@pytest.mark.parametrize("splits,rows,unroll,slices,k", [(sk, sn, d, sl, ks[0]) for sk, sn, d, sl, ks in SHAPES16])
+def test_pair_ring_prompt_uses_dequantized_weights(gpu, splits, rows, unroll, slices, k):
+    """16 row slots: B is fp16_rn(code * scale), w4a16_dequantize_f16's
+    weights, summed in fp32: the reference's prefill path (dequantize, fp16
+    GEMM). With four nonzero activations per row (small integers and halves)
+    every product and partial sum is exact in fp32, so the output must equal
+    the float64 product with the dequantized weights rounded to fp16, bit for
+    bit; scaling exact codes in fp32 instead (the M <= 8 decode) would miss it
+    wherever code * scale is not an fp16 value."""
+    m, n = 16, 96
+    x, p, s = make_case(m, k, n, seed=k + splits, all_nibbles=True)
+    gen = torch.Generator().manual_seed(k)
+    x = torch.zeros((m, k), dtype=torch.float16)
+    vals = torch.tensor([-3.0, -2.0, -1.0, -0.5, 0.5, 1.0, 2.0, 3.0], dtype=torch.float16)
+    for r in range(m):
+        cols = torch.randperm(k, generator=gen)[:4]
+        x[r, cols] = vals[torch.randint(0, 8, (4,), generator=gen)]
+    pd, sd = p.to(gpu), s.to(gpu)
+    wdq = torch.empty((n, k), dtype=torch.float16, device=gpu)
+    _lib.dequantize_f16(pd, sd, wdq, 128)
+    ref = (x.to(gpu).double() @ wdq.double().t()).to(torch.float16).cpu()
+    got = _run(gpu, x, p, s, RING, rows, splits, unroll, slices).cpu()
+    assert torch.equal(got, ref), int((got != ref).sum())
+    # the check discriminates: exact codes times the scale, unrounded (the
+    # M <= 8 decode's sums), land on other fp16 values for some outputs
+    q = torch.from_numpy(oracle.unpack_int4(p.numpy())).double()
+    alt = (x.double() @ (q * s.double().repeat_interleave(128, dim=1)).t()).to(torch.float16)
+    assert not torch.equal(alt, ref)
+
+
+# the 1.1B model's prompt projections (M = 16, and M = 9 / 12 at the slice
+# threshold) through the default route with a workspace, as the op runs them
+@pytest.mark.parametrize("m,k,n,slices", [(16, 2048, 2048, 0), (16, 2048, 2560, 0), (16, 2048, 11264, 0),
+                                          (9, 2048, 2560, 0), (16, 5632, 2048, 8), (12, 5632, 2048, 8),
+                                          (16, 14336, 4096, 4), (16, 8192, 8192, 2)])
+def test_pair_ring_prompt_default_route(gpu, m, k, n, slices):
+    x, p, s = make_case(m, k, n, seed=m + k ^ (7 * n), device="cuda")
+    if slices == 0:
+        assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "pair_ring"
+    assert _lib.linear_workspace_bytes(m, n, k) == slices * m * n * 4
+    assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (pair_ring, {slices} slices)")

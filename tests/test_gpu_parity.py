@@ -606,17 +606,21 @@ def test_stream_rejects(gpu):
 
 
 @pytest.mark.parametrize("kernel", ["default", "mfma_oneshot"])
-@pytest.mark.parametrize("m,k,n,default", [(9, 2048, 300, "gemm"), (16, 2048, 2048, "gemm"),
+@pytest.mark.parametrize("m,k,n,default", [(9, 2048, 300, "gemm"), (16, 2048, 2048, "pair_ring"),
                                            (16, 4096, 64, "gemm"), (12, 256, 7, "gemm"),
-                                           (16, 5632, 2048, "mfma_pair"), (16, 2048, 2560, "gemm"),
+                                           (16, 5632, 2048, "mfma_pair"), (16, 2048, 2560, "pair_ring"),
                                            (11, 5632, 2048, "mfma_pair"), (16, 4096, 14336, "gemm"),
-                                           (12, 2048, 11264, "gemm"), (9, 14336, 4096, "mfma_pair"),
+                                           (12, 2048, 11264, "pair_ring"), (9, 14336, 4096, "mfma_pair"),
                                            (16, 8192, 8192, "gemm"), (12, 2048, 32000, "gemm")])
 def test_default_dispatch_short_prompt(gpu, m, k, n, default, kernel, monkeypatch):
-    """M = 9..16: the paired kernel in one launch (16 row slots) on rows
-    longer than 4096 weights (at most 256 workgroups and 2 wavefronts on
-    weight blocks), else the GEMM; the one-shot MFMA kernel with its
-    selector (where its activations fit in LDS)."""
+    """M = 9..16 without a workspace: the paired ring kernel's 16-row-slot
+    form on rows of 2048 weights of 1024 .. 16384-row layers, the paired
+    kernel in one launch (16 row slots) on rows longer than 4096 weights (at
+    most 256 workgroups and 2 wavefronts on weight blocks), else the GEMM;
+    the one-shot MFMA kernel with its selector (where its activations fit in
+    LDS). The run itself goes through the op's route with a workspace (K
+    slices of the ring kernel at M >= 12 on 5632 x 2048, 14336 x 4096 and
+    8192 x 8192)."""
     if kernel == "mfma_oneshot":
         if m * k * 2 > 100 * 1024:
             pytest.skip("activations past the one-shot MFMA kernel's LDS")

@@ -133,8 +133,16 @@ def test_linear_silu(gpu, m, k, inter, monkeypatch):
         # stages whole rows (else the GEMM's); its sibling is the plain 16-slot
         # kernel over the 2 inter rows (selector mfma_pair), same K split,
         # same sums
+        # M = 9..16 on rows of 2048 weights of wide layers: the paired ring
+        # kernel's SiLU form, whose sibling is its plain 16-slot form with
+        # the same K split (one wavefront, all 8 pairs) over the 2 inter rows
+        ring16 = 9 <= m <= 16 and k == 2048 and 2 * inter >= 8192
         silu16 = 9 <= m <= 16 and (k > 4096 or (k <= 2048 and 2 * inter >= 8192))
-        if silu16:
+        if ring16:
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_PAIR_RING, 4, 1, 4)
+            ref16 = torch.empty_like(out)
+            _lib.silu_mul_f16(gu, ref16)
+        elif silu16:
             monkeypatch.setenv("W4A16_DECODE", "mfma_pair")
             _lib.linear_f16(xd, pd, sd, gu)
             monkeypatch.delenv("W4A16_DECODE")
@@ -162,7 +170,7 @@ def test_linear_silu(gpu, m, k, inter, monkeypatch):
         _lib.silu_mul_f16(gu, ref)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    if m == 16 and k == 2048 and inter == 5632:   # the 1.1B decoder's gate|up takes the 16-slot SiLU form
+    if 9 <= m <= 16 and k == 2048 and 2 * inter >= 8192:   # the 1.1B decoder's gate|up: the ring SiLU form
         assert torch.equal(out, ref16)
     elif ref16 is None or not torch.equal(out, ref16):
         assert torch.equal(out, ref)
