@@ -647,6 +647,10 @@ def main() -> int:
                          "prefill a CONTEXT-token prompt, then decode 64 tokens by graph replay (8 steps per "
                          "replay) with the decode attention split into SPLITS shares per head (0: one workgroup "
                          "per head, -1: the decoder's default); no JSON")
+    ap.add_argument("--decode-step-pass", action="store_true",
+                    help="for rocprofv3 --kernel-trace: the decode leg's fused measurement alone (configs[4]: "
+                         "random-init 1.1B Llama, 48-slot cache, 16-token prompt, 31 tokens by graph replay of "
+                         f"{TOKENS_PER_REPLAY} steps, 6 times); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -678,6 +682,24 @@ def main() -> int:
             model.prefill(prompt)
         torch.cuda.synchronize()
         print("prefill pass done", flush=True)
+        return 0
+
+    if args.decode_step_pass:
+        from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+        prompt_len, new_tokens = 16, 32
+        model = LlamaDecoder(LlamaConfig(max_seq_len=prompt_len + new_tokens), device=device, seed=0)
+        prompt = torch.randint(0, model.cfg.vocab_size, (prompt_len,), generator=torch.Generator().manual_seed(0))
+        prompt = prompt.to(device)
+        model.prefill(prompt)
+        model.capture(tokens_per_replay=TOKENS_PER_REPLAY)
+        for _ in range(6):
+            model.prefill(prompt)
+            left = new_tokens - 1
+            while left > 0:
+                left -= model.replay_tokens(limit=left).numel()
+        torch.cuda.synchronize()
+        print("decode step pass done", flush=True)
         return 0
 
     if args.decode_pass:

@@ -16,6 +16,7 @@
 #include <string>
 
 #include "w4a16_kernels.h"
+#include "w4a16_pair_ring.h"
 
 namespace w4a16_internal {
 // w4a16_pair.hip: the paired-group MFMA kernel for M = 2..8 (chunk = staged
@@ -50,6 +51,8 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                      hipStream_t stream);
 int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w,
                           const w4a16::f16* s, w4a16::f16* o, int inter, int K, hipStream_t stream);
+int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusion& fz, const uint8_t* w,
+                           const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -1523,6 +1526,17 @@ int w4a16_gemv_fused_f16(const void* activations, const void* norm_weight, float
     f16* o = static_cast<f16*>(output);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int n = (int)N, k = (int)K;
+    // the ring kernel where a fused shape is instantiated (4-byte aligned
+    // scales): the decode step's gate|up, down and lm_head
+    if ((reinterpret_cast<uintptr_t>(scales) & 3u) == 0 && N <= INT32_MAX / 2) {
+        w4a16::RingFusion rz{nw, eps, static_cast<const f16*>(residual)};
+        const int kind = paired ? 0 : residual ? 1 : (nw && N >= 16384) ? 2 : -1;
+        if (kind >= 0 && (kind != 0 || N >= 48)) {
+            const int rc2 = w4a16_internal::launch_pair_ring_fused(kind, x, rz, packed_weights, sc, o,
+                                                                   paired ? n / 2 : n, k, st);
+            if (rc2 != W4A16_ERR_CONFIG) return rc2;
+        }
+    }
     w4a16::GemvFusion fz{};
     fz.norm_weight = nw;
     fz.eps = eps;
@@ -1597,6 +1611,14 @@ int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights
         return fail(W4A16_ERR_ALIGNMENT, "linear + SiLU needs 16-byte aligned activations and weights");
     hipStream_t st = static_cast<hipStream_t>(stream);
     using w4a16::f16;
+    if (M == 1 && K == 2048 && inter >= 24 && (reinterpret_cast<uintptr_t>(scales) & 3u) == 0) {
+        // one row of 2048: the ring kernel's SiLU form, as the decode step's gate|up
+        const int rc2 = w4a16_internal::launch_pair_ring_fused(0, static_cast<const f16*>(activations),
+                                                               w4a16::RingFusion{}, packed_weights,
+                                                               static_cast<const f16*>(scales),
+                                                               static_cast<f16*>(output), (int)inter, (int)K, st);
+        if (rc2 != W4A16_ERR_CONFIG) return rc2;
+    }
     if (M == 1 && K <= 16384) {   // one row: the paired fused GEMV of the decode step
         int R, W;
         fused_shape(true, false, 2 * inter, R, W);

@@ -74,8 +74,17 @@ __host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN
     return (MS == 1 ? (int64_t)2 * SK * PPW * 272 : MS * pair_ring_row_bytes(SK, PPW, MS))   // staged units
            + (MS == 16 ? 0 : (int64_t)2 * SK * PPW * (MS == 1 ? 1 : 8) * 4)                 // per-(group, row) bias
            + (int64_t)8 * RB * SN * 2 * SK * PPW * 4                                         // fp32 scales
-           + (SK > 1 ? (int64_t)SN * RB * SK * (MS == 1 ? 8 : MS == 16 ? 128 : 64) * 4 : 0); // K-slice partials
+           + (SK > 1 ? (int64_t)SN * RB * SK * (MS == 1 ? 8 : MS == 16 ? 128 : 64) * 4 : 0) // K-slice partials
+           + (MS == 1 ? (int64_t)SK * SN * 4 : 0);                                           // RMSNorm partials
 }
+
+// Fused decode-step work (M = 1): an RMSNorm of the activation row while it
+// is staged (norm_weight), a residual add in the epilogue (residual).
+struct RingFusion {
+    const f16* norm_weight;   // null: no RMSNorm
+    float eps;
+    const f16* residual;      // null: no residual add
+};
 
 // SPLIT (narrow layers of long rows): the K / 256 pairs are cut into S
 // slices of SK PPW pairs; workgroup b takes slice b mod S of rows (b / S) R
@@ -95,18 +104,30 @@ __host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN
 // l + 8. The staged row stride is 16 mod 256 so the 16 rows of a fragment
 // read fall on distinct bank slots.
 //
-// SILU (MS = 16, RB = 2): N is the intermediate width, the weights hold 2 N
-// rows (gate rows, then up rows); block 0 of a wavefront is gate rows n ..
-// n + 7 and block 1 the up rows N + n .., and the output is
+// SILU (MS = 16 or 1, RB = 2): N is the intermediate width, the weights hold
+// 2 N rows (gate rows, then up rows); block 0 of a wavefront is gate rows n
+// .. n + 7 and block 1 the up rows N + n .., and the output is
 // fp16(fp16(silu(fp16(g))) * fp16(u)), the roundings of silu(gate) * up on
-// the op's fp16 outputs.
-template <int MS, int SK, int SN, int RB, int PPW, int D, bool SPLIT = false, bool SILU = false>
+// fp16 tensors.
+//
+// NORM (MS = 1): the staged row is y = fp16((fp32(x) * rsqrt(mean(x^2) + eps))
+// * fp32(norm_weight)), the fp32 operation order of an RMSNorm that returns
+// fp16 (the squares summed per thread, per wavefront by DPP, then the
+// wavefronts in order; one more barrier). RESID (MS = 1): out[n] =
+// fp16(fp32(residual[n]) + fp32(fp16(dot))), a residual stream's x +
+// linear(a); residual may alias out (each row is read and written by the
+// same lane, the read requested with the first weights).
+template <int MS, int SK, int SN, int RB, int PPW, int D, bool SPLIT = false, bool SILU = false, bool NORM = false,
+          bool RESID = false>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
-               f16* __restrict__ out, int M, int N, int K, float* __restrict__ part, int S) {
+               f16* out, int M, int N, int K, float* __restrict__ part, int S, RingFusion fz) {
     static_assert(MS == 1 || MS == 4 || MS == 8 || MS == 16, "1, 4, 8 or 16 activation row slots");
     static_assert(D >= 1 && D <= PPW, "ring depth 1 .. PPW");
-    static_assert(!SILU || (MS == 16 && RB == 2 && !SPLIT), "the SiLU form pairs a gate block and its up block");
+    static_assert(!SILU || ((MS == 16 || MS == 1) && RB == 2 && !SPLIT),
+                  "the SiLU form pairs a gate block and its up block");
+    static_assert(!NORM || (MS == 1 && !SPLIT), "the RMSNorm prologue normalises one whole activation row");
+    static_assert(!RESID || (MS == 1 && !SPLIT && !SILU), "the residual epilogue adds to one output row");
     constexpr bool W16 = MS == 16;            // exact decode, two MFMAs per word
     constexpr int W = SK * SN;
     constexpr int T = 64 * W;
@@ -127,6 +148,7 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     float* bias = reinterpret_cast<float*>(smem + XB);   // [GS][BS]
     float* sc = bias + NB;                                 // [SR][2][PS]
     float* red = sc + SR * 2 * PS;                         // [SN RB][SK][8, 64 or 128]
+    float* np = red + (SK > 1 ? SN * RB * SK * (MS == 1 ? 8 : MS == 16 ? 128 : 64) : 0);   // [W] (MS = 1)
 
     const int G = K >> 7;
     const int P = G >> 1;
@@ -158,6 +180,14 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
         const int uu = min(pb * 32 + (MS == 1 ? i : i % US), units - 1);
         a[u] = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + (size_t)uu * 8);
     }
+    u32x4 gw[NORM ? XU : 1];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int uu = min(pb * 32 + (int)threadIdx.x + u * T, units - 1);
+            gw[u] = *reinterpret_cast<const u32x4*>(fz.norm_weight + (size_t)uu * 8);
+        }
+    }
     const uint32_t* s32 = reinterpret_cast<const uint32_t*>(scales);
     uint32_t sw[SU];
 #pragma unroll
@@ -181,7 +211,46 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     };
 #pragma unroll
     for (int j = 0; j < D; ++j) issue(j);
+    // the residual values of this lane's output rows (lanes 0..7)
+    f16 resv[RB];
+    if constexpr (RESID) {
+#pragma unroll
+        for (int b = 0; b < RB; ++b) resv[b] = fz.residual[min(nw + 8 * b + (lane & 7), N - 1)];
+    }
     __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (NORM) {
+        // mean of squares of the row (units past K are not staged)
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = threadIdx.x + u * T;
+            if (i < US && pb * 32 + i < units) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f16x2 p = as_f16x2(a[u][e]);
+                    ss = __builtin_fmaf((float)p.x, (float)p.x, ss);
+                    ss = __builtin_fmaf((float)p.y, (float)p.y, ss);
+                }
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) np[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int v = 0; v < W; ++v) total += np[v];
+        const float inv = 1.0f / __builtin_sqrtf(total / (float)K + fz.eps);
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 p = as_f16x2(a[u][e]), g = as_f16x2(gw[u][e]);
+                const f16x2 y = {(f16)(((float)p.x * inv) * (float)g.x), (f16)(((float)p.y * inv) * (float)g.y)};
+                a[u][e] = as_u32(y);
+            }
+        }
+    }
 
     // 2. staging: unit i = m US + uu covers x[m][8 uu .. 8 uu + 7] (group
     // uu / 16); the 16 units of a (row, group) sit in one DPP row, whose sum
@@ -349,6 +418,7 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
                 if (MS == 1 || m < M) {
                     if constexpr (SPLIT) part[((size_t)sl * M + m) * N + n] = vv[b][e];
                     else if constexpr (SILU) out[(size_t)m * N + n] = gemm_silu_mul(vv[0][e], vv[1][e]);
+                    else if constexpr (RESID) out[n] = (f16)((float)resv[b] + (float)(f16)vv[b][e]);
                     else out[(size_t)m * N + n] = (f16)vv[b][e];
                 }
             }

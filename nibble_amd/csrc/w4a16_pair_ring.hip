@@ -24,7 +24,8 @@ int fail(int code, const std::string& message) {
     return code;
 }
 
-using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int, float*, int);
+using Kern = void (*)(const w4a16::f16*, const uint8_t*, const w4a16::f16*, w4a16::f16*, int, int, int, float*, int,
+                      w4a16::RingFusion);
 
 int row_slots(int M) { return M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
@@ -168,10 +169,49 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
     const int rows = 8 * sn;
     const int blocks = (N + rows - 1) / rows * slices;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, N, K,
-                       static_cast<float*>(part), slices);
+                       static_cast<float*>(part), slices, w4a16::RingFusion{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
     if (slices > 1) return launch_split_reduce(slices, static_cast<const float*>(part), o, (int64_t)M * N, stream);
+    return W4A16_OK;
+}
+
+// Fused decode-step GEMVs at M = 1 (the caller checks pointers and
+// alignment; scales 4-byte aligned). kind 0: the SiLU form (N = inter, 2 N
+// weight rows), RMSNorm when fz.norm_weight is set, K = 2048; kind 1: the
+// residual add, K = 5632; kind 2: RMSNorm, K = 2048 (wide layers). Shapes
+// from graph timing against the one-shot fused GEMVs (decode step of the
+// 1.1B model): gate|up 2048 x 2 x 5632 with RMSNorm (1, 3, 8 pairs, 4 in
+// flight, 2 blocks per wavefront) 4.13 against 4.85 us; down 5632 x 2048
+// with the residual (8 wavefronts on K, 3 pairs each) 3.31 against 3.45;
+// lm_head 2048 x 32000 with RMSNorm (1, 8, 8 pairs all in flight) 7.08
+// against 8.18. Returns W4A16_ERR_CONFIG for other shapes.
+int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusion& fz, const uint8_t* w,
+                           const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream) {
+    using namespace w4a16;
+    Kern kern = nullptr;
+    int sk = 1, sn = 1, rb = 1, ppw = 1;
+    if (kind == 0 && K == 2048) {
+        kern = fz.norm_weight ? gemv_pair_ring<1, 1, 3, 2, 8, 4, false, true, true>
+                              : gemv_pair_ring<1, 1, 3, 2, 8, 4, false, true, false>;
+        sk = 1, sn = 3, rb = 2, ppw = 8;
+    } else if (kind == 1 && K == 5632 && fz.norm_weight == nullptr) {
+        kern = gemv_pair_ring<1, 8, 1, 1, 3, 3, false, false, false, true>;
+        sk = 8, sn = 1, rb = 1, ppw = 3;
+    } else if (kind == 2 && K == 2048 && fz.norm_weight != nullptr) {
+        kern = gemv_pair_ring<1, 1, 8, 1, 8, 8, false, false, true>;
+        sk = 1, sn = 8, rb = 1, ppw = 8;
+    }
+    if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "fused ring GEMV: shape not instantiated");
+    const int64_t lds = pair_ring_lds_bytes(1, sk, sn, rb, ppw);
+    int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
+    if (rc != W4A16_OK) return rc;
+    const int rows = 8 * sn;
+    const int blocks = (N + rows - 1) / rows;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, 1, N, K,
+                       (float*)nullptr, 1, fz);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
     return W4A16_OK;
 }
 
@@ -193,7 +233,7 @@ int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x,
     const int rows = 8 * sn;
     const int blocks = (inter + rows - 1) / rows;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, inter, K,
-                       (float*)nullptr, 1);
+                       (float*)nullptr, 1, w4a16::RingFusion{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
     return W4A16_OK;

@@ -37,9 +37,13 @@ def _f16(a) -> np.ndarray:
     return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
-@pytest.mark.parametrize("k,n", [(256, 7), (2048, 64), (2048, 2560), (5632, 300), (16384, 33)])
+@pytest.mark.parametrize("k,n", [(256, 7), (2048, 64), (2048, 2560), (5632, 300), (16384, 33), (2048, 32000),
+                                 (2048, 20004)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_gemv_fused_plain_and_norm(gpu, k, n, norm):
+    """One row (the decode step's q|k|v and lm_head): the one-shot kernel, or
+    with RMSNorm on rows of 2048 of wide layers the ring kernel's RMSNorm
+    prologue; against the oracle on the fp16 RMSNorm of the row."""
     x, p, s = make_case(1, k, n, seed=k + n)
     gen = torch.Generator().manual_seed(k)
     w = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16)
@@ -53,8 +57,10 @@ def test_gemv_fused_plain_and_norm(gpu, k, n, norm):
 
 
 @pytest.mark.parametrize("alias", [False, True])
-@pytest.mark.parametrize("k,n", [(2048, 2048), (5632, 2048), (256, 9)])
+@pytest.mark.parametrize("k,n", [(2048, 2048), (5632, 2048), (256, 9), (5632, 2003)])
 def test_gemv_fused_residual(gpu, k, n, alias):
+    """The residual add (in place or not): rows of 5632 on the ring kernel's
+    residual epilogue (ragged N too), others on the one-shot kernel."""
     x, p, s = make_case(1, k, n, seed=3 * k + n)
     resid = torch.randn((n,), generator=torch.Generator().manual_seed(n)).to(torch.float16)
     ref = _f16(resid.float().numpy() + _f16(_linear_ref(x, p, s)))
@@ -67,8 +73,11 @@ def test_gemv_fused_residual(gpu, k, n, alias):
 
 
 @pytest.mark.parametrize("norm", [False, True])
-@pytest.mark.parametrize("k,half", [(2048, 5632), (256, 5), (4096, 64)])
+@pytest.mark.parametrize("k,half", [(2048, 5632), (256, 5), (4096, 64), (2048, 5000), (2048, 24)])
 def test_gemv_fused_paired_silu(gpu, k, half, norm):
+    """gate|up with SiLU * up: rows of 2048 on the ring kernel's SiLU form
+    (a gate and an up block per wavefront; ragged and tiny layers), others on
+    the one-shot kernel's paired rows."""
     x, p, s = make_case(1, k, 2 * half, seed=k + half)
     w = (1.0 + 0.25 * torch.randn((k,), generator=torch.Generator().manual_seed(7))).to(torch.float16)
     xin = _rms_norm_f16(x, w, 1e-6) if norm else x
@@ -538,9 +547,11 @@ def test_qkv_rope_pair_matches_attention_o(gpu, heads, kv, hidden, pos):
 @pytest.mark.parametrize("k,n", [(256, 1), (256, 7), (2048, 1000), (2048, 32000), (1024, 50257)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_gemv_argmax(gpu, k, n, norm):
-    """Logits bit-identical to the fused GEMV's (same arithmetic), token =
-    torch.argmax of them, position + 1, embedding row gathered; three calls in
-    a row (the workspace counters must return to zero)."""
+    """Logits bit-identical to the one-shot fused GEMV's (same arithmetic; with
+    RMSNorm on 2048 x 32000 the fused GEMV takes the ring kernel, and the
+    logits are checked against the oracle instead), token = torch.argmax of
+    them, position + 1, embedding row gathered; three calls in a row (the
+    workspace counters must return to zero)."""
     x, p, s = make_case(1, k, n, seed=k + 7 * n)
     gen = torch.Generator().manual_seed(n)
     w = (1.0 + 0.5 * torch.randn((k,), generator=gen)).to(torch.float16).to(gpu)
@@ -558,6 +569,10 @@ def test_gemv_argmax(gpu, k, n, norm):
         _lib.gemv_argmax_f16(xg, pg, sg, token, ws, logits=logits, norm_weight=w if norm else None, eps=1e-5,
                              position=position, table=table, emb_out=emb)
         torch.cuda.synchronize()
+        if norm and k == 2048 and n >= 16384:
+            xin = _rms_norm_f16(x, w.cpu(), 1e-5)
+            assert_parity(logits.view(1, n), _linear_ref(xin, p, s).reshape(1, n), "argmax logits")
+            ref_logits = logits.clone()
         assert torch.equal(logits, ref_logits)
         t = int(torch.argmax(ref_logits.float()))
         assert int(token) == t and int(position) == 11 + call
