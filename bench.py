@@ -74,7 +74,7 @@ TRAFFIC_SOURCE = "profiles/gemv_pair_ring_m1_mlp_traffic.md"
 # `bench.py --headline-pass` (the headline sequence alone), per launch: the
 # profiler's timestamps run above the event-timed launches, so the line
 # reports both.
-TRACE_US_PER_LAUNCH = 3.459
+TRACE_US_PER_LAUNCH = 3.407
 TRACE_SOURCE = "profiles/gemv_pair_ring_m1_mlp_kernel_trace.md"
 
 

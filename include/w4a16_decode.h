@@ -255,6 +255,26 @@ int w4a16_add_rmsnorm_f16(const void* x, const void* delta, const void* weight, 
                           void* output, int64_t rows, int64_t hidden, void* stream);
 
 /*
+ * A linear layer followed by the residual add + RMSNorm of its output rows
+ * (the down projection of a prompt and the next layer's input norm):
+ * x_out = fp16(x + linear(activations)) and output = RMSNorm(x_out) *
+ * norm_weight, bit-identical to w4a16_linear_ws_f16 followed by
+ * w4a16_add_rmsnorm_f16. Where the op takes the ring kernel's K slices on
+ * rows of at most 2048 outputs, the slices' sum runs in the norm's launch
+ * (two launches instead of three). workspace (16-byte aligned) holds
+ * w4a16_linear_add_rmsnorm_workspace_bytes(M, N, K, group_size) bytes:
+ * split-K partial sums, then an fp16 copy of the linear's output. x_out may
+ * be x. The decoder's fused prefill (reference w4a16/linear.py:154-200 for
+ * the projection, the norms of its Llama blocks) calls it; no other
+ * reference counterpart.
+ */
+int w4a16_linear_add_rmsnorm_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
+                                 const void* x, const void* norm_weight, float eps, void* x_out, void* output,
+                                 int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+int64_t w4a16_linear_add_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size);
+
+/*
  * Attention of `tokens` new tokens at cache slots start .. start + tokens - 1:
  * qkv rows [q (num_heads x 64) | k (num_kv_heads x 64) | v] fp16 as for
  * w4a16_decode_attention_f16; rotary embedding (cos / sin tables [max_seq_len,

@@ -96,6 +96,9 @@ DECODE_SIGNATURES = {
     "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
     "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
     "w4a16_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _vp]),
+    "w4a16_linear_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64,
+                                                    _i64, _i64, _vp, _i64, _vp]),
+    "w4a16_linear_add_rmsnorm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "w4a16_linear_silu_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "w4a16_prefill_attention_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                                    _i64, _vp]),
@@ -412,6 +415,22 @@ def linear_silu_f16(activations, packed_weights, scales, output, group_size: int
     inter = packed_weights.shape[0] // 2
     _raise_on(lib().w4a16_linear_silu_f16(activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(),
                                           output.data_ptr(), m, inter, k, group_size, _stream_ptr(stream)))
+
+
+def linear_add_rmsnorm_f16(activations, packed_weights, scales, x, norm_weight, eps: float, x_out, output,
+                           group_size: int = 128, stream=None, workspace=None) -> None:
+    """``w4a16_linear_add_rmsnorm_f16``: x_out <- x + linear(activations),
+    output <- RMSNorm(x_out) * norm_weight, with a workspace from the caching
+    allocator unless one is given."""
+    m, k = activations.shape
+    n = packed_weights.shape[0]
+    if workspace is None:
+        nbytes = int(lib().w4a16_linear_add_rmsnorm_workspace_bytes(m, n, k, group_size))
+        workspace = _workspace(max(nbytes, 16), output.device, stream)
+    _raise_on(lib().w4a16_linear_add_rmsnorm_f16(
+        activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), x.data_ptr(), norm_weight.data_ptr(),
+        float(eps), x_out.data_ptr(), output.data_ptr(), m, n, k, group_size, workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream_ptr(stream)))
 
 
 def silu_mul_f16(gate_up, output, stream=None) -> None:

@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <type_traits>
 
 #include "w4a16_device.h"
@@ -1365,10 +1366,104 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     }
 }
 
+// The K slices of a split-K linear layer, added and rounded, then the
+// residual add + RMSNorm of norm_rows_vec_kernel<true>, one workgroup per
+// row of at most 2048 elements (one 8-element unit per thread): d =
+// fp16(part[0] + part[1] + .. + part[S - 1]) in slice order in fp32 (the
+// arithmetic of pair_split_reduce), s = fp16(fp32(x) + fp32(d)) to x_out, and
+// out = fp16((fp32(s) * inv) * fp32(w)) with inv = 1 / sqrt(mean(s^2) + eps),
+// the squares summed per thread, per wavefront by DPP and over the four
+// wavefronts as (0 + 1) + (2 + 3) (those of norm_rows_vec_kernel): the
+// outputs equal the reduce launch followed by that kernel, bit for bit.
+template <int S>
+__global__ void __launch_bounds__(256)
+split_add_rmsnorm_kernel(const float* __restrict__ part, const f16* x, const f16* __restrict__ w, float eps,
+                         f16* x_out, f16* __restrict__ out, int rows, int hidden) {
+    __shared__ float partial[4];
+    const size_t row = (size_t)blockIdx.x * hidden;
+    const size_t mn = (size_t)rows * hidden;
+    const int units = hidden >> 3;
+    const int i = min((int)threadIdx.x, units - 1);
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + row + (size_t)i * 8);
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + (size_t)i * 8);
+    f32x4 pv[S][2];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            pv[sl][h] = *reinterpret_cast<const f32x4*>(part + sl * mn + row + (size_t)i * 8 + 4 * h);
+    u32x4 sv;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float d[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float acc = pv[0][e >> 1][2 * (e & 1) + j];
+#pragma unroll
+            for (int sl = 1; sl < S; ++sl) acc += pv[sl][e >> 1][2 * (e & 1) + j];
+            d[j] = (float)(f16)acc;
+        }
+        const f16x2 a = as_f16x2(xv[e]);
+        const f16x2 sum = {(f16)((float)a.x + d[0]), (f16)((float)a.y + d[1])};
+        sv[e] = as_u32(sum);
+    }
+    if ((int)threadIdx.x < units) {
+        *reinterpret_cast<u32x4*>(x_out + row + (size_t)threadIdx.x * 8) = sv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f16x2 a = as_f16x2(sv[e]);
+            ss = __builtin_fmaf((float)a.x, (float)a.x, ss);
+            ss = __builtin_fmaf((float)a.y, (float)a.y, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)hidden + eps);
+    if ((int)threadIdx.x < units) {
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const f16x2 a = as_f16x2(sv[e]), g = as_f16x2(wv[e]);
+            const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
+            o[e] = as_u32(y);
+        }
+        *reinterpret_cast<u32x4*>(out + row + (size_t)threadIdx.x * 8) = o;
+    }
+}
+
 }  // namespace w4a16
 
 namespace w4a16_internal {
 void set_last_error(const std::string& message);   // w4a16_hip.hip: the message w4a16_last_error() returns
+
+using SplitNormKern = void (*)(const float*, const w4a16::f16*, const w4a16::f16*, float, w4a16::f16*, w4a16::f16*,
+                               int, int);
+template <int... S>
+SplitNormKern split_norm_table(int slices, std::integer_sequence<int, S...>) {
+    static constexpr SplitNormKern table[] = {w4a16::split_add_rmsnorm_kernel<S + 2>...};
+    return table[slices - 2];
+}
+
+// split_add_rmsnorm_kernel over `rows` rows of `hidden` (8 | hidden <= 2048,
+// every buffer 16-byte aligned; the caller checks), slices 2..16.
+int launch_split_add_rmsnorm(int slices, const float* part, const w4a16::f16* x, const w4a16::f16* w, float eps,
+                             w4a16::f16* x_out, w4a16::f16* out, int rows, int hidden, hipStream_t stream) {
+    if (slices < 2 || slices > 16 || hidden <= 0 || hidden > 2048 || hidden % 8 != 0) {
+        set_last_error("split-K reduce + RMSNorm: 2..16 slices, rows of 8..2048 elements (a multiple of 8)");
+        return W4A16_ERR_CONFIG;
+    }
+    hipLaunchKernelGGL(split_norm_table(slices, std::make_integer_sequence<int, 15>{}), dim3((unsigned)rows),
+                       dim3(256), 0, stream, part, x, w, eps, x_out, out, rows, hidden);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_last_error(std::string("kernel launch failed: ") + hipGetErrorString(e));
+        return W4A16_ERR_LAUNCH;
+    }
+    return W4A16_OK;
+}
 }
 
 namespace {

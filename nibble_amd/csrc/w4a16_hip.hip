@@ -48,7 +48,10 @@ bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth, int
 bool pair_ring_silu_instantiated(int64_t M, int64_t K, int sk, int sn, int depth);
 int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::f16* x, const uint8_t* w,
                      const w4a16::f16* s, w4a16::f16* o, int N, int K, void* part, int64_t part_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, bool reduce = true);
+// w4a16_decode.hip: the K slices' sum + residual add + RMSNorm
+int launch_split_add_rmsnorm(int slices, const float* part, const w4a16::f16* x, const w4a16::f16* w, float eps,
+                             w4a16::f16* x_out, w4a16::f16* out, int rows, int hidden, hipStream_t stream);
 int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x, const uint8_t* w,
                           const w4a16::f16* s, w4a16::f16* o, int inter, int K, hipStream_t stream);
 int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusion& fz, const uint8_t* w,
@@ -1427,6 +1430,72 @@ int w4a16_linear_noalloc_f16(const void* activations, const uint8_t* packed_weig
     }
     return run_plan(p, activations, packed_weights, scales, output, M, N, K, group_size, stream, true, ws,
                     need > 0 ? kNoAllocScratchBytes : 0);
+}
+
+// The linear layer followed by the residual add + RMSNorm of its output
+// rows. The workspace holds the op's split-K partial sums (at offset 0) and
+// an fp16 copy of the linear's output (after them, 256-byte aligned). With
+// the ring kernel's K slices (the route w4a16_linear_ws_f16 takes with a
+// workspace) on rows of at most 2048 outputs, the slices' sum goes into the
+// norm's launch (two launches instead of three); otherwise the op writes its
+// output to the workspace and w4a16_add_rmsnorm_f16 reads it from there.
+// Bit-identical to w4a16_linear_ws_f16 followed by w4a16_add_rmsnorm_f16
+// either way.
+static int64_t linear_add_rmsnorm_ws(const Plan& p, int64_t M, int64_t N, int64_t* tail) {
+    const int64_t need = plan_workspace_bytes(p, M, N);
+    *tail = (need + 255) / 256 * 256;
+    return *tail + M * N * 2;
+}
+
+int64_t w4a16_linear_add_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {
+    if (check_scalar_args(M, N, K, group_size) != W4A16_OK || M * N == 0) return 0;
+    Plan p;
+    alignas(16) static const uint8_t probe[16] = {};   // stands for 16-byte aligned operands
+    if (make_plan(probe, probe, nullptr, M, N, K, group_size, &p, true) != W4A16_OK) return 0;
+    int64_t tail;
+    return linear_add_rmsnorm_ws(p, M, N, &tail);
+}
+
+int w4a16_linear_add_rmsnorm_f16(const void* activations, const uint8_t* packed_weights, const void* scales,
+                                 const void* x, const void* norm_weight, float eps, void* x_out, void* output,
+                                 int64_t M, int64_t N, int64_t K, int64_t group_size, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+    int rc = check_scalar_args(M, N, K, group_size);
+    if (rc != W4A16_OK) return rc;
+    if (M * N == 0) return W4A16_OK;
+    if (!x || !norm_weight || !x_out || !workspace)
+        return fail(W4A16_ERR_NULL, "linear + add_rmsnorm: x, norm_weight, x_out and workspace must be non-NULL");
+    rc = check_pointers(activations, packed_weights, scales, output);
+    if (rc != W4A16_OK) return rc;
+    if (!aligned16(workspace)) return fail(W4A16_ERR_ALIGNMENT, "linear + add_rmsnorm: workspace must be 16-byte aligned");
+    Plan p;
+    rc = make_plan(activations, packed_weights, scales, M, N, K, group_size, &p, true);
+    if (rc != W4A16_OK) return rc;
+    int64_t tail;
+    const int64_t total = linear_add_rmsnorm_ws(p, M, N, &tail);
+    if (workspace_bytes < total)
+        return fail(W4A16_ERR_CONFIG, "linear + add_rmsnorm: needs a workspace of " + std::to_string(total) +
+                                          " bytes (w4a16_linear_add_rmsnorm_workspace_bytes)");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    using w4a16::f16;
+    const bool fused = p.kernel == W4A16_KERNEL_PAIR_RING && p.max_blocks >= 2 && N <= 2048 && N % 8 == 0 &&
+                       eps >= 0.0f && aligned16(x) && aligned16(norm_weight) && aligned16(x_out) && aligned16(output);
+    if (fused) {
+        rc = w4a16_internal::launch_pair_ring(p.splits, p.rows, p.unroll, p.max_blocks, (int)M,
+                                              static_cast<const f16*>(activations), packed_weights,
+                                              static_cast<const f16*>(scales), static_cast<f16*>(output), (int)N,
+                                              (int)K, workspace, tail, st, false);
+        if (rc != W4A16_OK) return rc;
+        return w4a16_internal::launch_split_add_rmsnorm(p.max_blocks, static_cast<const float*>(workspace),
+                                                        static_cast<const f16*>(x),
+                                                        static_cast<const f16*>(norm_weight), eps,
+                                                        static_cast<f16*>(x_out), static_cast<f16*>(output), (int)M,
+                                                        (int)N, st);
+    }
+    void* d = static_cast<uint8_t*>(workspace) + tail;
+    rc = run_plan(p, activations, packed_weights, scales, d, M, N, K, group_size, stream, true, workspace, tail);
+    if (rc != W4A16_OK) return rc;
+    return w4a16_add_rmsnorm_f16(x, d, norm_weight, eps, x_out, output, M, N, stream);
 }
 
 int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {

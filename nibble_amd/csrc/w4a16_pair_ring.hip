@@ -137,7 +137,7 @@ bool pair_ring_silu_instantiated(int64_t M, int64_t K, int sk, int sn, int depth
 
 int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::f16* x, const uint8_t* w,
                      const w4a16::f16* s, w4a16::f16* o, int N, int K, void* part, int64_t part_bytes,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool reduce) {
     if (M < 1 || M > 16) return fail(W4A16_ERR_CONFIG, "paired ring kernel: 1 <= M <= 16");
     if (K < 256 || K % 256 != 0)
         return fail(W4A16_ERR_CONFIG, "paired ring kernel: K must be a multiple of 256 (an even group count)");
@@ -172,7 +172,8 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                        static_cast<float*>(part), slices, w4a16::RingFusion{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, std::string("kernel launch failed: ") + hipGetErrorString(e));
-    if (slices > 1) return launch_split_reduce(slices, static_cast<const float*>(part), o, (int64_t)M * N, stream);
+    if (slices > 1 && reduce)
+        return launch_split_reduce(slices, static_cast<const float*>(part), o, (int64_t)M * N, stream);
     return W4A16_OK;
 }
 

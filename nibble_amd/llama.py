@@ -338,11 +338,12 @@ class LlamaDecoder(torch.nn.Module):
         """The prompt (cache slots 0 .. T-1) with the decode step's roundings:
         RMSNorm of the embeddings, then per layer the q|k|v op, rotary + KV
         append + causal attention, the o op, residual add + RMSNorm, the
-        gate|up projection with its SiLU * up epilogue, the down op and
+        gate|up projection with its SiLU * up epilogue, the down op with the
         residual add + the next RMSNorm (the next layer's input norm, or the
-        final norm after the last layer); then the lm_head GEMV on the last
-        normed row and the greedy argmax, which also gathers the first decode
-        step's input row. 7 launches per layer."""
+        final norm after the last layer; w4a16_linear_add_rmsnorm_f16 sums
+        the op's K slices in the norm's launch); then the lm_head GEMV on the
+        last normed row and the greedy argmax, which also gathers the first
+        decode step's input row. 7 launches per layer."""
         cfg = self.cfg
         t = prompt.numel()
         g = cfg.group_size
@@ -364,9 +365,14 @@ class LlamaDecoder(torch.nn.Module):
                 _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
             else:
                 _lib.silu_mul_f16(self._prefill_linear(h, gu_w, gu_s), mlp)
-            d = self._prefill_linear(mlp, b.down_proj.packed_weights, b.down_proj.scales)
             nxt = self.layers[i + 1].input_norm if i + 1 < len(self.layers) else self.norm
-            _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
+            if t <= FUSED_PREFILL_NATIVE_MAX_ROWS:
+                # down + residual add + the next norm (the op's K slices summed in the norm's launch)
+                _lib.linear_add_rmsnorm_f16(mlp, b.down_proj.packed_weights, b.down_proj.scales, x, nxt.weight,
+                                            nxt.eps, x, h, g)
+            else:
+                d = self._prefill_linear(mlp, b.down_proj.packed_weights, b.down_proj.scales)
+                _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
         _lib.gemv_fused_f16(h[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits)
         _lib.argmax_embed_f16(self.logits, self.token, None, self.embed, self.x_buf)
         self.position.fill_(t)

@@ -62,6 +62,19 @@ def test_decode_entry_points_validate_before_launch():
     assert lib.w4a16_add_rmsnorm_f16(a, 0, a, 1e-5, a, a, 4, 2048, 0) == _lib.W4A16_ERR_NULL
     assert lib.w4a16_add_rmsnorm_f16(a, a, a, -1.0, a, a, 4, 2048, 0) == _lib.W4A16_ERR_CONFIG
     assert lib.w4a16_add_rmsnorm_f16(a, a, a, 1e-5, a, a, 0, 2048, 0) == _lib.W4A16_OK   # no rows: nothing
+    # linear + residual add + RMSNorm: the workspace and the norm's pointers are required
+    assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 16, 2048, 5632, 128, 0, 0, 0) == \
+        _lib.W4A16_ERR_NULL
+    assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, 0, a, 1e-5, a, a, 16, 2048, 5632, 128, a, 1 << 30, 0) == \
+        _lib.W4A16_ERR_NULL
+    assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 16, 2048, 5632, 128, a + 8, 1 << 30, 0) == \
+        _lib.W4A16_ERR_ALIGNMENT
+    need = lib.w4a16_linear_add_rmsnorm_workspace_bytes(16, 2048, 5632, 128)
+    assert need == 8 * 16 * 2048 * 4 + 16 * 2048 * 2   # 8 K slices of partial sums, then the fp16 output
+    assert lib.w4a16_linear_add_rmsnorm_workspace_bytes(4, 2048, 2048, 128) == 4 * 2048 * 2   # no K slices
+    assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 16, 2048, 5632, 128, a, need - 1, 0) == \
+        _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 0, 2048, 5632, 128, 0, 0, 0) == _lib.W4A16_OK
     # linear + SiLU: group size, shapes, NULL pointers, alignment, empty
     assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 256, 64, 0) == _lib.W4A16_ERR_GROUP_SIZE
     assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 200, 128, 0) == _lib.W4A16_ERR_SHAPE

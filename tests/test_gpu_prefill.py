@@ -345,3 +345,37 @@ def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     model.prefill(other)
     assert torch.equal(model.prefill(prompt), tok)
     assert torch.equal(model.logits, logits_eager) and torch.equal(model.k_cache, k_eager)
+
+
+@pytest.mark.parametrize("m,k,n,alias", [(16, 5632, 2048, True), (12, 5632, 2048, False), (9, 5632, 2048, True),
+                                         (16, 14336, 4096, False), (4, 5632, 2048, False), (16, 8192, 2048, True),
+                                         (16, 5632, 2044, False), (13, 5632, 1000, True)])
+def test_linear_add_rmsnorm_matches_separate_launches(gpu, m, k, n, alias):
+    """w4a16_linear_add_rmsnorm_f16 against the op with a workspace followed
+    by w4a16_add_rmsnorm_f16, bit for bit: where the op takes the ring
+    kernel's K slices on rows of at most 2048 outputs (M >= 12 on 5632 and
+    8192, N a multiple of 8) the slices are summed in the norm's launch,
+    elsewhere (other M, 4096 outputs, N not a multiple of 8) the two launches
+    run as they are; x_out in place or apart."""
+    from tests._cases import assert_parity, expected, make_case
+
+    x16, p, s = make_case(m, k, n, seed=m + k + n)
+    a, pd, sd = x16.to(gpu), p.to(gpu), s.to(gpu)
+    gen = torch.Generator().manual_seed(n)
+    resid = torch.randn((m, n), generator=gen).to(torch.float16).to(gpu)
+    w = (1 + 0.1 * torch.randn((n,), generator=gen)).to(torch.float16).to(gpu)
+    print(f"[case] linear_add_rmsnorm M={m} K={k} N={n} alias={alias}", flush=True)
+    xin = resid.clone()
+    x_out = xin if alias else torch.full_like(resid, float("nan"))
+    h = torch.full((m, n), float("nan"), dtype=torch.float16, device=gpu)
+    _lib.linear_add_rmsnorm_f16(a, pd, sd, xin, w, 1e-5, x_out, h)
+    # the separate launches
+    d = torch.empty((m, n), dtype=torch.float16, device=gpu)
+    _lib.linear_f16(a, pd, sd, d)
+    xs = torch.empty_like(resid)
+    hs = torch.empty_like(h)
+    _lib.add_rmsnorm_f16(resid, d, w, 1e-5, xs, hs)
+    torch.cuda.synchronize()
+    assert torch.equal(x_out, xs)
+    assert torch.equal(h, hs)
+    assert_parity(d, expected(x16, p, s), f"linear M={m} K={k} N={n}")
