@@ -578,6 +578,9 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   about 2 us; at M = 9 the slices tie or lose): 5632 x 2048 8 slices of
 //   (1, 8, 3) 7.24 against 7.81; 14336 x 4096 4 slices of (1, 8, 4) 15.08
 //   against 17.86; 8192 x 8192 2 slices of (1, 8, 4) 15.33 against 16.89.
+//   M = 3..4 with a workspace, 28672 x 8192: 4 slices of (1, 8, 4) 24.1 /
+//   24.5 against 28.7 / 28.6 us on the split-K streaming kernel (M = 5..8
+//   tie or lose: M = 6 28.8-30.2 against 29.7, M = 8 29.2-30.2 against 30.0).
 bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace = false) {
     if (M < 1 || M > 16 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
     const int64_t P = K / 256;
@@ -628,6 +631,8 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
             if (N >= 6144 && N <= 8192) c[0] = {2, 4, 4};
         } else if (P <= 56) {
             if (!wide && N >= 4096 && N <= 8192) c[0] = {4, 2, 6};
+        } else if (P == 112) {
+            if (workspace && M >= 3 && !wide && N >= 4096 && N <= 8192) c[0] = {1, 8, 4, 4};
         }
     }
     for (const Shape& e : c) {
@@ -904,7 +909,8 @@ int make_plan(const void* act, const void* packed, const void* scales, int64_t M
     //   MFMA up to K = 8192 when N >= 4096 gives it enough row blocks;
     //   otherwise the looped VALU kernel for M = 1, M = 2 (K <= 16384) or
     //   M <= 4 (K <= 4096), else the looped MFMA kernel.
-    if ((family == 0 || family == W4A16_KERNEL_PAIR_RING) && rows == 0 && scales4 && plan_pair_ring(M, N, K, out))
+    if ((family == 0 || family == W4A16_KERNEL_PAIR_RING) && rows == 0 && scales4 &&
+        plan_pair_ring(M, N, K, out, workspace))
         return W4A16_OK;
     if (family == W4A16_KERNEL_PAIR_RING) family = 0;   // a shape without an instantiation
     if (family == 0 && rows == 0 && workspace && pair_split_route(M, N, K)) {

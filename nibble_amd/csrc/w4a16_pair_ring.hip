@@ -70,10 +70,12 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
 
 // Split-K instantiations (slices > 1; row slots, wavefronts, pairs per
 // wavefront per slice, pairs in flight): M = 9..16 on 5632 x 2048 (8 slices
-// of 3 pairs), 14336 x 4096 (4 of 14) and 8192 x 8192 (2 of 16).
+// of 3 pairs), 14336 x 4096 (4 of 14) and 8192 x 8192 (2 of 16); M = 3..4
+// on 28672 x 8192 (4 of 28).
 Kern pick_split(int ms, int sk, int sn, int ppw, int depth) {
 #define W4A16_P(MS, SK, SN, PPW, D) \
     if (ms == MS && sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<MS, SK, SN, 1, PPW, D, true>;
+    W4A16_P(4, 1, 8, 28, 4)
     W4A16_P(16, 1, 8, 3, 3)
     W4A16_P(16, 1, 8, 14, 4)
     W4A16_P(16, 1, 8, 16, 4)
@@ -157,7 +159,7 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
                     "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); "
                     "M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3) (1,8,14,4) "
-                    "(1,8,16,4)");
+                    "(1,8,16,4); M = 2..4 with K slices (1,8,28,4)");
     const int64_t lds = w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired ring kernel: staging exceeds LDS");
     const int64_t need = pair_ring_workspace_bytes(M, N, slices);

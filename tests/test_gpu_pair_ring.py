@@ -47,6 +47,8 @@ SHAPES16 = [(8, 1, 1, 1, (2048, 1792)), (4, 2, 2, 1, (2048, 1536)), (2, 4, 4, 1,
             (1, 8, 3, 8, (5632, 6144)),      # 5632: 22 pairs in 8 slices of 3, the last holding 1
             (1, 8, 4, 4, (14336, 14080)), (1, 8, 4, 2, (8192, 7936))]   # 14 / 16 pairs per wavefront
 PROMPT = [(m, sk, sn, d, sl, k) for sk, sn, d, sl, ks in SHAPES16 for k in ks for m in (9, 13, 16)]
+# M = 2..4 with K slices: 28672 (112 pairs) and 28416 (111: the last slice one short) in 4 slices of 28
+SLICED4 = [(m, 1, 8, 4, 4, k) for k in (28672, 28416) for m in (2, 3, 4)]
 
 
 def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0, slices=0):
@@ -210,3 +212,24 @@ def test_pair_ring_prompt_default_route(gpu, m, k, n, slices):
         assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "pair_ring"
     assert _lib.linear_workspace_bytes(m, n, k) == slices * m * n * 4
     assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (pair_ring, {slices} slices)")
+
+
+@pytest.mark.parametrize("m,splits,rows,unroll,slices,k", SLICED4)
+@pytest.mark.parametrize("n", [13, 300])
+def test_pair_ring_sliced_small_batch_variants(gpu, m, splits, rows, unroll, slices, k, n):
+    """4 row slots over K slices (the workspace route of M = 3..4 on rows of
+    28672), every M of the slots, ragged N, a short last slice, against the
+    oracle."""
+    x, p, s = make_case(m, k, n, seed=k + 3 * n + 17 * m)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll, slices)
+    assert_parity(out, expected(x, p, s), f"pair_ring M={m} x{slices} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m", [3, 4])
+def test_pair_ring_sliced_default_route_full_size(gpu, m):
+    """28672 x 8192 at M = 3..4 through the default route with a workspace
+    (4 K slices of the ring kernel), as the op runs it."""
+    k, n = 28672, 8192
+    x, p, s = make_case(m, k, n, seed=m + 5, device="cuda")
+    assert _lib.linear_workspace_bytes(m, n, k) == 4 * m * n * 4
+    assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (ring, 4 K slices)")
