@@ -594,9 +594,10 @@ def layer_tables(device, copy_gbps: float | None = None) -> dict:
                 out = torch.empty((m, n), device=device, dtype=torch.float16)
                 us = per_layer(lambda i: _lib.linear_f16(x, packed[i], scales[i], out), copies, samples=samples)
                 # the calls take a workspace from the caching allocator where the
-                # plan uses one (the split-K kernel), as the torch op does
-                plan = _lib.plan_linear(x.data_ptr(), packed[0].data_ptr(), m, n, k)
-                kernel = "pair_split" if _lib.linear_workspace_bytes(m, n, k) > 0 else plan["kernel"]
+                # plan uses one (the split-K routes), as the torch op does
+                plan = _lib.plan_linear(x.data_ptr(), packed[0].data_ptr(), m, n, k, workspace=True)
+                kernel = plan["kernel"] + (f" x{plan['max_blocks']} K slices"
+                                           if plan["kernel"] == "pair_ring" and plan["max_blocks"] > 1 else "")
                 row = {"K": k, "N": n, "M": m, **row_metrics(m, n, k, us, copy_gbps), "kernel": kernel,
                        "eager_us": round(eager_us(lambda i: torch.ops.w4a16.linear(x, packed[i], scales[i], 128),
                                                   copies), 3)}

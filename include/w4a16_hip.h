@@ -97,8 +97,9 @@ int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t gr
  * it, M = 3..8 layers with K > 16384 and N >= 8192 take
  * W4A16_KERNEL_PAIR_SPLIT, the streaming paired kernel over K slices, and
  * M = 12..16 layers of K = 5632 (N <= 4096), 8192 or 14336 (N <= 8192) and
- * M = 3..4 layers of K = 28672 (N = 4096..8192) the paired ring kernel over
- * K slices; the fp32 partial sums are added in slice
+ * M = 3..8 layers of K = 28672 (N = 4096..8192) and M = 5..8 layers of
+ * K = 8192 with N >= 16384 the paired ring kernel over K slices; the fp32
+ * partial sums are added in slice
  * order by a second launch. workspace == NULL routes exactly as w4a16_linear_f16;
  * a smaller non-NULL workspace is W4A16_ERR_CONFIG. The torch op
  * w4a16::linear (reference csrc/int4_linear.cpp:16-28) calls this entry
@@ -173,6 +174,12 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
                       int* kernel, int* rows, int* splits, int* unroll,
                       int* max_blocks);
 
+/* The same for w4a16_linear_ws_f16 with a workspace (the split-K routes). */
+int w4a16_plan_linear_ws(const void* activations, const uint8_t* packed_weights,
+                         int64_t M, int64_t N, int64_t K, int64_t group_size,
+                         int* kernel, int* rows, int* splits, int* unroll,
+                         int* max_blocks);
+
 /*
  * w4a16_linear_f16 with an explicit kernel family and launch shape, for
  * tuning sweeps.
@@ -226,7 +233,9 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights,
  *     M = 5..8 (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); at M =
  *     9..16 (exact decode: the dequantized fp16 weights in the B operand)
  *     (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3)
- *     (1,8,14,4) (1,8,16,4); at M = 2..4 with K slices (1,8,28,4).
+ *     (1,8,14,4) (1,8,16,4); at M = 2..4 with K slices (1,8,28,4); at M =
+ *     5..8 with K slices (1,8,14,2) (1,8,16,3), whose wavefronts each take
+ *     two 8-row blocks (a workgroup covers 16 * rows rows).
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
  *     row blocks with the workgroups resident at once; else 1..16), unroll =

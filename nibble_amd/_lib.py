@@ -60,6 +60,7 @@ SIGNATURES = {
     "w4a16_check_linear_shapes": (ctypes.c_int, [_i64] * 7),
     "w4a16_check_dequantize_shapes": (ctypes.c_int, [_i64] * 5 + [ctypes.c_uint64]),
     "w4a16_plan_linear": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip, _ip]),
+    "w4a16_plan_linear_ws": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _ip, _ip, _ip, _ip, _ip]),
     "w4a16_linear_workspace_bytes": (_i64, [_i64] * 4),
     "w4a16_linear_ws_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w4a16_linear_noalloc_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
@@ -236,12 +237,13 @@ def dequantize_f16(packed_weights, scales, output, group_size: int = 128, stream
     )
 
 
-def plan_linear(act_ptr: int, packed_ptr: int, m: int, n: int, k: int, group_size: int = 128) -> dict:
-    """The dispatcher's choice for these sizes/alignments (host-only, no GPU needed)."""
+def plan_linear(act_ptr: int, packed_ptr: int, m: int, n: int, k: int, group_size: int = 128,
+                workspace: bool = False) -> dict:
+    """The dispatcher's choice for these sizes/alignments (host-only, no GPU
+    needed); with workspace, the choice of w4a16_linear_ws_f16 with one."""
     out = [ctypes.c_int(0) for _ in range(5)]
-    _raise_on(
-        lib().w4a16_plan_linear(act_ptr, packed_ptr, m, n, k, group_size, *[ctypes.byref(v) for v in out])
-    )
+    fn = lib().w4a16_plan_linear_ws if workspace else lib().w4a16_plan_linear
+    _raise_on(fn(act_ptr, packed_ptr, m, n, k, group_size, *[ctypes.byref(v) for v in out]))
     kernel, rows, splits, unroll, max_blocks = (v.value for v in out)
     return {"kernel": KERNEL_NAMES[kernel], "rows": rows, "splits": splits, "unroll": unroll,
             "max_blocks": max_blocks}

@@ -579,8 +579,12 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   (1, 8, 3) 7.24 against 7.81; 14336 x 4096 4 slices of (1, 8, 4) 15.08
 //   against 17.86; 8192 x 8192 2 slices of (1, 8, 4) 15.33 against 16.89.
 //   M = 3..4 with a workspace, 28672 x 8192: 4 slices of (1, 8, 4) 24.1 /
-//   24.5 against 28.7 / 28.6 us on the split-K streaming kernel (M = 5..8
-//   tie or lose: M = 6 28.8-30.2 against 29.7, M = 8 29.2-30.2 against 30.0).
+//   24.5 against 28.7 / 28.6 us on the split-K streaming kernel. M = 5..8
+//   with a workspace and two 8-row blocks per wavefront (half the staging
+//   per row): 28672 x 8192 8 slices of (1, 8, 2) 25.0 / 25.0 / 25.1 at M =
+//   5 / 6 / 8 against 29.6 / 29.7 / 30.2 (one block per wavefront: 27.2 /
+//   27.3 / 27.8); 8192 x 28672 2 slices of (1, 8, 3) 27.0 / 27.3 / 27.8
+//   against 28.4 / 28.6 / 29.1 on the streaming paired kernel.
 bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace = false) {
     if (M < 1 || M > 16 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
     const int64_t P = K / 256;
@@ -629,10 +633,12 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
             if (M >= 3 && M <= 4 && N >= 2048 && N <= 4096) c[0] = {8, 1, 3};
         } else if (P <= 32) {
             if (N >= 6144 && N <= 8192) c[0] = {2, 4, 4};
+            else if (workspace && wide && P == 32 && N >= 16384) c[0] = {1, 8, 3, 2};
         } else if (P <= 56) {
             if (!wide && N >= 4096 && N <= 8192) c[0] = {4, 2, 6};
         } else if (P == 112) {
             if (workspace && M >= 3 && !wide && N >= 4096 && N <= 8192) c[0] = {1, 8, 4, 4};
+            else if (workspace && wide && N >= 4096 && N <= 8192) c[0] = {1, 8, 2, 8};
         }
     }
     for (const Shape& e : c) {
@@ -1375,13 +1381,13 @@ int w4a16_check_dequantize_shapes(int64_t packed_rows, int64_t packed_cols, int6
     return W4A16_OK;
 }
 
-int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N,
-                      int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll,
+static int plan_query(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N, int64_t K,
+                      int64_t group_size, bool workspace, int* kernel, int* rows, int* splits, int* unroll,
                       int* max_blocks) {
     int rc = check_scalar_args(M, N, K, group_size);
     if (rc != W4A16_OK) return rc;
     Plan p;
-    rc = make_plan(activations, packed_weights, nullptr, M, N, K, group_size, &p);
+    rc = make_plan(activations, packed_weights, nullptr, M, N, K, group_size, &p, workspace);
     if (rc != W4A16_OK) return rc;
     if (kernel) *kernel = p.kernel;
     if (rows) *rows = p.rows;
@@ -1389,6 +1395,20 @@ int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, in
     if (unroll) *unroll = p.unroll;
     if (max_blocks) *max_blocks = p.max_blocks;
     return W4A16_OK;
+}
+
+int w4a16_plan_linear(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N,
+                      int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll,
+                      int* max_blocks) {
+    return plan_query(activations, packed_weights, M, N, K, group_size, false, kernel, rows, splits, unroll,
+                      max_blocks);
+}
+
+int w4a16_plan_linear_ws(const void* activations, const uint8_t* packed_weights, int64_t M, int64_t N,
+                         int64_t K, int64_t group_size, int* kernel, int* rows, int* splits, int* unroll,
+                         int* max_blocks) {
+    return plan_query(activations, packed_weights, M, N, K, group_size, true, kernel, rows, splits, unroll,
+                      max_blocks);
 }
 
 int w4a16_linear_ws_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,

@@ -69,18 +69,27 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
 }
 
 // Split-K instantiations (slices > 1; row slots, wavefronts, pairs per
-// wavefront per slice, pairs in flight): M = 9..16 on 5632 x 2048 (8 slices
-// of 3 pairs), 14336 x 4096 (4 of 14) and 8192 x 8192 (2 of 16); M = 3..4
-// on 28672 x 8192 (4 of 28).
-Kern pick_split(int ms, int sk, int sn, int ppw, int depth) {
-#define W4A16_P(MS, SK, SN, PPW, D) \
-    if (ms == MS && sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<MS, SK, SN, 1, PPW, D, true>;
-    W4A16_P(4, 1, 8, 28, 4)
-    W4A16_P(16, 1, 8, 3, 3)
-    W4A16_P(16, 1, 8, 14, 4)
-    W4A16_P(16, 1, 8, 16, 4)
+// wavefront per slice, pairs in flight) and their 8-row blocks per
+// wavefront: M = 9..16 on 5632 x 2048 (8 slices of 3 pairs), 14336 x 4096
+// (4 of 14) and 8192 x 8192 (2 of 16); M = 3..4 on 28672 x 8192 (4 of 28);
+// M = 5..8 with two blocks per wavefront (half the activation staging per
+// row) on 28672 x 8192 (8 of 14) and 8192 x 28672 (2 of 16).
+struct SplitPick {
+    Kern kern;
+    int rb;
+};
+SplitPick pick_split(int ms, int sk, int sn, int ppw, int depth) {
+#define W4A16_P(MS, SK, SN, RB, PPW, D)                               \
+    if (ms == MS && sk == SK && sn == SN && ppw == PPW && depth == D) \
+        return SplitPick{w4a16::gemv_pair_ring<MS, SK, SN, RB, PPW, D, true>, RB};
+    W4A16_P(4, 1, 8, 1, 28, 4)
+    W4A16_P(8, 1, 8, 2, 14, 2)
+    W4A16_P(8, 1, 8, 2, 16, 3)
+    W4A16_P(16, 1, 8, 1, 3, 3)
+    W4A16_P(16, 1, 8, 1, 14, 4)
+    W4A16_P(16, 1, 8, 1, 16, 4)
 #undef W4A16_P
-    return nullptr;
+    return SplitPick{nullptr, 1};
 }
 
 // SiLU form (16 row slots, a gate and an up block per wavefront):
@@ -127,8 +136,8 @@ bool pair_ring_instantiated(int64_t M, int64_t K, int sk, int sn, int depth, int
     if (!pair_ring_slices_valid(K, slices)) return false;
     const int ppw = ppw_of(K, sk, slices);
     const int ms = row_slots((int)M);
-    const Kern k = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : pick(ms, sk, sn, ppw, depth);
-    return k != nullptr && w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw) <= kMaxLdsBytes;
+    const SplitPick k = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : SplitPick{pick(ms, sk, sn, ppw, depth), 1};
+    return k.kern != nullptr && w4a16::pair_ring_lds_bytes(ms, sk, sn, k.rb, ppw) <= kMaxLdsBytes;
 }
 
 bool pair_ring_silu_instantiated(int64_t M, int64_t K, int sk, int sn, int depth) {
@@ -151,7 +160,8 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
     if (sk < 1) return fail(W4A16_ERR_CONFIG, "paired ring kernel: splits (wavefronts splitting K) must be positive");
     const int ppw = ppw_of(K, sk, slices);
     const int ms = row_slots(M);
-    Kern kern = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : pick(ms, sk, sn, ppw, depth);
+    const SplitPick pk = slices > 1 ? pick_split(ms, sk, sn, ppw, depth) : SplitPick{pick(ms, sk, sn, ppw, depth), 1};
+    const Kern kern = pk.kern;
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
                     "paired ring kernel: (splits, rows, pairs per wavefront, unroll) not instantiated for this M; "
@@ -159,8 +169,9 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
                     "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); "
                     "M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3) (1,8,14,4) "
-                    "(1,8,16,4); M = 2..4 with K slices (1,8,28,4)");
-    const int64_t lds = w4a16::pair_ring_lds_bytes(ms, sk, sn, 1, ppw);
+                    "(1,8,16,4); M = 2..4 with K slices (1,8,28,4); M = 5..8 with K slices and two 8-row blocks "
+                    "per wavefront (1,8,14,2) (1,8,16,3)");
+    const int64_t lds = w4a16::pair_ring_lds_bytes(ms, sk, sn, pk.rb, ppw);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired ring kernel: staging exceeds LDS");
     const int64_t need = pair_ring_workspace_bytes(M, N, slices);
     if (slices > 1 && (part == nullptr || part_bytes < need || (reinterpret_cast<uintptr_t>(part) & 15u)))
@@ -168,7 +179,7 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                                           std::to_string(need) + " bytes (w4a16_linear_workspace_bytes)");
     int rc = ensure_lds(reinterpret_cast<const void*>(kern), (int)lds);
     if (rc != W4A16_OK) return rc;
-    const int rows = 8 * sn;
+    const int rows = 8 * sn * pk.rb;
     const int blocks = (N + rows - 1) / rows * slices;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * sk * sn), (size_t)lds, stream, x, w, s, o, M, N, K,
                        static_cast<float*>(part), slices, w4a16::RingFusion{});

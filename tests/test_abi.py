@@ -567,20 +567,27 @@ def test_scalar_argument_errors():
 
 
 @pytest.mark.parametrize("m,n,k,splits", [
-    (8, 8192, 28672, None), (8, 4096, 14336, 0), (4, 8192, 28672, None), (3, 8192, 28672, None),
-    (3, 4096, 14336, 0), (5, 8192, 20480, None), (5, 4096, 20480, 0), (8, 8191, 28672, 0), (8, 8192, 16384, 0),
-    (8, 2048, 5632, 0), (8, 28672, 8192, 0), (1, 8192, 28672, 0), (2, 8192, 28672, 0), (16, 8192, 28672, 0),
-    (8, 4096, 4096, 0), (4, 4096, 8192, 0)])
+    (8, 8192, 28672, 8), (8, 4096, 14336, 0), (4, 8192, 28672, 4), (3, 8192, 28672, 4),
+    (3, 4096, 14336, 0), (5, 8192, 20480, None), (5, 4096, 20480, 0), (8, 8191, 28672, 8), (8, 8192, 16384, 0),
+    (8, 2048, 5632, 0), (8, 28672, 8192, 2), (5, 16384, 8192, 2), (4, 28672, 8192, 0), (1, 8192, 28672, 0),
+    (2, 8192, 28672, 0), (16, 8192, 28672, 0), (8, 4096, 4096, 0), (4, 4096, 8192, 0), (16, 2048, 5632, 8),
+    (12, 4096, 14336, 4), (16, 8192, 8192, 2), (9, 2048, 5632, 0)])
 def test_linear_workspace_bytes(m, n, k, splits):
-    """M = 3..8 layers with K > 16384 and N >= 8192 use splits * M * N fp32
-    of workspace (the split-K kernel); everything else none."""
+    """Layers whose route keeps fp32 partial sums use slices * M * N * 4
+    bytes of workspace: the paired ring kernel's K slices (M = 3..8 on rows
+    of 28672 with N = 4096..8192, M = 5..8 on rows of 8192 with N >= 16384,
+    M = 12..16 on 5632 x 2048, 14336 x 4096 and 8192 x 8192) and the split-K
+    streaming kernel (other M = 3..8 layers with K > 16384 and N >= 8192;
+    None: any slice count); everything else none."""
     got = _lib.linear_workspace_bytes(m, n, k)
     if splits == 0:
         assert got == 0
-    else:
+    elif splits is None:
         assert got > 0 and got % (m * n * 4) == 0
         s = got // (m * n * 4)
         assert 2 <= s <= 16
+    else:
+        assert got == splits * m * n * 4
     assert _lib.linear_workspace_bytes(m, n, k, 64) == 0   # other group sizes: the generic kernel
 
 
@@ -638,3 +645,17 @@ def test_split_plans_are_launchable():
             per_slice = -(-pairs // s)
             assert 2 <= s <= 16 and (s - 1) * per_slice < pairs, (m, k, s)
             assert per_slice * 16 * (2 * slots) * 16 + per_slice * 128 <= 160 * 1024, (m, k, s)
+
+
+@pytest.mark.parametrize("m,k,n,sk,sn,depth,slices", [
+    (8, 28672, 8192, 1, 8, 2, 8), (5, 28672, 8192, 1, 8, 2, 8), (3, 28672, 8192, 1, 8, 4, 4),
+    (8, 8192, 28672, 1, 8, 3, 2), (16, 5632, 2048, 1, 8, 3, 8), (12, 14336, 4096, 1, 8, 4, 4),
+    (16, 8192, 8192, 1, 8, 4, 2)])
+def test_workspace_plan_ring_slices(m, k, n, sk, sn, depth, slices):
+    """w4a16_plan_linear_ws: the route w4a16_linear_ws_f16 takes with a
+    workspace, here the ring kernel over K slices (max_blocks = slices);
+    without one the same layers plan no K slices."""
+    plan = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128, workspace=True)
+    assert plan == {"kernel": "pair_ring", "rows": sn, "splits": sk, "unroll": depth, "max_blocks": slices}
+    plain = _lib.plan_linear(ALIGNED, ALIGNED, m, n, k, 128)
+    assert not (plain["kernel"] == "pair_ring" and plain["max_blocks"] > 1)

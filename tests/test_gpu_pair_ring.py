@@ -49,6 +49,10 @@ SHAPES16 = [(8, 1, 1, 1, (2048, 1792)), (4, 2, 2, 1, (2048, 1536)), (2, 4, 4, 1,
 PROMPT = [(m, sk, sn, d, sl, k) for sk, sn, d, sl, ks in SHAPES16 for k in ks for m in (9, 13, 16)]
 # M = 2..4 with K slices: 28672 (112 pairs) and 28416 (111: the last slice one short) in 4 slices of 28
 SLICED4 = [(m, 1, 8, 4, 4, k) for k in (28672, 28416) for m in (2, 3, 4)]
+# M = 5..8 with K slices and two 8-row blocks per wavefront: 8 slices of 14 pairs (28672, 28416) and 2 of 16
+# (8192, 7936)
+SLICED8 = ([(m, 1, 8, 2, 8, k) for k in (28672, 28416) for m in (5, 8)] +
+           [(m, 1, 8, 3, 2, k) for k in (8192, 7936) for m in (5, 8)])
 
 
 def _run(dev, x, p, s, kernel=None, rows=0, splits=0, unroll=0, slices=0):
@@ -233,3 +237,24 @@ def test_pair_ring_sliced_default_route_full_size(gpu, m):
     x, p, s = make_case(m, k, n, seed=m + 5, device="cuda")
     assert _lib.linear_workspace_bytes(m, n, k) == 4 * m * n * 4
     assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (ring, 4 K slices)")
+
+
+@pytest.mark.parametrize("m,splits,rows,unroll,slices,k", SLICED8)
+@pytest.mark.parametrize("n", [13, 300])
+def test_pair_ring_sliced_two_blocks_variants(gpu, m, splits, rows, unroll, slices, k, n):
+    """8 row slots over K slices with two 8-row blocks per wavefront (a
+    workgroup covers 128 rows: ragged N leaves most of it past N), against
+    the oracle."""
+    x, p, s = make_case(m, k, n, seed=k + 7 * n + 19 * m)
+    out = _run(gpu, x, p, s, RING, rows, splits, unroll, slices)
+    assert_parity(out, expected(x, p, s), f"pair_ring RB2 M={m} x{slices} K={k} N={n}")
+
+
+@pytest.mark.parametrize("m,k,n,slices", [(5, 28672, 8192, 8), (8, 28672, 8192, 8), (6, 8192, 28672, 2),
+                                          (8, 8192, 28672, 2)])
+def test_pair_ring_sliced_two_blocks_default_route(gpu, m, k, n, slices):
+    """The 70B-class layers at M = 5..8 through the default route with a
+    workspace, as the op runs them."""
+    x, p, s = make_case(m, k, n, seed=m + k + n, device="cuda")
+    assert _lib.linear_workspace_bytes(m, n, k) == slices * m * n * 4
+    assert_parity(_run(gpu, x, p, s), expected(x, p, s), f"M={m} K={k} N={n} default (ring RB2, {slices} slices)")
