@@ -275,6 +275,39 @@ int w4a16_linear_add_rmsnorm_f16(const void* activations, const uint8_t* packed_
 int64_t w4a16_linear_add_rmsnorm_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size);
 
 /*
+ * One layer's attention half of a prompt after its q|k|v projection: attn =
+ * w4a16_prefill_attention_f16(qkv, caches, start, tokens) (which appends the
+ * tokens' rotary k and v rows to the caches), then x_out = fp16(x +
+ * linear(attn, o_packed, o_scales)) and output = RMSNorm(x_out) *
+ * norm_weight as w4a16_linear_add_rmsnorm_f16 (K = num_heads * head_dim, N =
+ * hidden). Where the o op runs one group
+ * pair per wavefront on 16 row slots (9..16 tokens, K = 2048; start +
+ * tokens <= 32, query heads per KV head a power of two, hidden <= 2048,
+ * 16-byte aligned buffers, 4-byte aligned o_scales) the attention runs
+ * inside the o projection's launch: each
+ * workgroup attends the four query heads of its K slice and the norm's
+ * launch sums the slices (two launches instead of three), with the
+ * separate launches' arithmetic (the same MFMA chains per group pair, added
+ * in the same order) up to the fp16 rounding of the fp32 rotary k and q,
+ * which may differ by one unit; otherwise the separate launches. workspace
+ * (16-byte aligned) holds
+ * w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(tokens, num_heads,
+ * hidden, group_size) bytes. x_out may be x. The decoder's fused prefill
+ * calls it (reference w4a16/linear.py:154-200 for the o projection, HF
+ * LlamaAttention and the post-attention norm around it,
+ * scripts/generate.py:260-305); no other reference counterpart.
+ */
+int w4a16_prefill_attention_o_add_rmsnorm_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
+                                              const float* sin_table, int64_t start, int64_t tokens,
+                                              int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                              int64_t max_seq_len, const uint8_t* o_packed, const void* o_scales,
+                                              int64_t hidden, int64_t group_size, const void* x,
+                                              const void* norm_weight, float eps, void* x_out, void* output,
+                                              void* workspace, int64_t workspace_bytes, void* stream);
+int64_t w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(int64_t tokens, int64_t num_heads, int64_t hidden,
+                                                              int64_t group_size);
+
+/*
  * Attention of `tokens` new tokens at cache slots start .. start + tokens - 1:
  * qkv rows [q (num_heads x 64) | k (num_kv_heads x 64) | v] fp16 as for
  * w4a16_decode_attention_f16; rotary embedding (cos / sin tables [max_seq_len,

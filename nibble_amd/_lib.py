@@ -100,6 +100,10 @@ DECODE_SIGNATURES = {
     "w4a16_linear_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64,
                                                     _i64, _i64, _vp, _i64, _vp]),
     "w4a16_linear_add_rmsnorm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "w4a16_prefill_attention_o_add_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                                                  _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
+                                                                  ctypes.c_float, _vp, _vp, _vp, _i64, _vp]),
+    "w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "w4a16_linear_silu_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "w4a16_prefill_attention_f16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
                                                    _i64, _vp]),
@@ -433,6 +437,28 @@ def linear_add_rmsnorm_f16(activations, packed_weights, scales, x, norm_weight, 
         activations.data_ptr(), packed_weights.data_ptr(), scales.data_ptr(), x.data_ptr(), norm_weight.data_ptr(),
         float(eps), x_out.data_ptr(), output.data_ptr(), m, n, k, group_size, workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream_ptr(stream)))
+
+
+def prefill_attention_o_add_rmsnorm_f16(qkv, k_cache, v_cache, cos_table, sin_table, start: int, o_packed,
+                                        o_scales, x, norm_weight, eps: float, x_out, output, num_heads: int,
+                                        num_kv_heads: int, head_dim: int = 64, group_size: int = 128, stream=None,
+                                        workspace=None) -> None:
+    """``w4a16_prefill_attention_o_add_rmsnorm_f16``: the attention of the
+    qkv rows [tokens, ...] at slots start .. start + tokens - 1 of one
+    layer's caches (appending their k / v rows), x_out <- x + linear(attn, o),
+    output <- RMSNorm(x_out) * norm_weight; a workspace from the caching
+    allocator unless one is given."""
+    tokens = qkv.shape[0]
+    hidden = o_packed.shape[0]
+    if workspace is None:
+        nbytes = int(lib().w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(tokens, num_heads, hidden,
+                                                                                 group_size))
+        workspace = _workspace(max(nbytes, 16), output.device, stream)
+    _raise_on(lib().w4a16_prefill_attention_o_add_rmsnorm_f16(
+        qkv.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), start,
+        tokens, num_heads, num_kv_heads, head_dim, k_cache.shape[-2], o_packed.data_ptr(), o_scales.data_ptr(),
+        hidden, group_size, x.data_ptr(), norm_weight.data_ptr(), float(eps), x_out.data_ptr(), output.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream_ptr(stream)))
 
 
 def silu_mul_f16(gate_up, output, stream=None) -> None:

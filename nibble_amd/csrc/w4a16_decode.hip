@@ -16,6 +16,7 @@
 #include <utility>
 #include <type_traits>
 
+#include "w4a16_attn_device.h"
 #include "w4a16_device.h"
 
 namespace w4a16 {
@@ -49,26 +50,6 @@ namespace w4a16 {
 // depend on the position (cache rows of each wavefront's first chunk, q, k,
 // v) is requested before the position arrives.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp<0xB1>(v));
-    v = fmaxf(v, dpp<0x4E>(v));
-    v = fmaxf(v, dpp<0x141>(v));
-    v = fmaxf(v, dpp<0x140>(v));
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-
-__device__ __forceinline__ void wave_lds_sync() {
-    // LDS operations of one wavefront complete in order; this only keeps the
-    // compiler from moving LDS accesses across the point
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // SPLIT: workgroup (hq, s) of gridDim.y attends a share of the slots 0 .. p
 // (64-slot aligned, the shares in slot order) and writes its unnormalised
 // state to partial[hq][s] = {max, sum, acc[64]} for decode_attention_merge;
@@ -432,37 +413,6 @@ embedding_kernel(const f16* __restrict__ table, int64_t vocab, int hidden, const
 // ---------------------------------------------------------------------------
 constexpr int kAttnOSlots = 64;
 constexpr int kVStride = 72;   // V tile row stride in halves (144 bytes: conflict-free 16-byte stores)
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-
-// Max / sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 (the four 16-lane
-// rows), in every lane: v_permlane16_swap / v_permlane32_swap hand each lane
-// its partner's value without LDS. Sums pair the rows as (r0 + r1) + (r2 + r3)
-// in every lane, so all lanes hold the same bits.
-__device__ __forceinline__ float row_pair_max(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                    false, false);
-    v = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                    false, false);
-    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
-}
-
-__device__ __forceinline__ float row_pair_sum(float v) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                    false, false);
-    v = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v), __builtin_bit_cast(uint32_t, v),
-                                                    false, false);
-    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
-}
-
-// ds_read_b64_tr_b16 at an LDS address (see attn_o_kernel for the lane mapping)
-__device__ __forceinline__ uint2 lds_read_tr16(const f16* p) {
-    const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4i16*)(reinterpret_cast<uintptr_t>(p)));
-    return __builtin_bit_cast(uint2, v);
-}
 
 template <int KV, int R, int L, bool CACHED>
 __global__ void __launch_bounds__(64 * KV)
@@ -1178,17 +1128,14 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
                 const int i = i0 + NT * b;
                 if (i < nn * 4) {
                     const int r = i >> 2, db = i & 3;
-                    u32x4 lo, hi;
+                    float c8[8], s8[8];
 #pragma unroll
-                    for (int h = 0; h < 4; ++h) {
-                        const f16x2 a = as_f16x2(ka[b][h]), z = as_f16x2(kz[b][h]);
-                        const float c0 = cv[b][h >> 1][2 * (h & 1)], c1 = cv[b][h >> 1][2 * (h & 1) + 1];
-                        const float s0 = sv[b][h >> 1][2 * (h & 1)], s1 = sv[b][h >> 1][2 * (h & 1) + 1];
-                        const f16x2 l2 = {(f16)((float)a.x * c0 - (float)z.x * s0), (f16)((float)a.y * c1 - (float)z.y * s1)};
-                        const f16x2 h2 = {(f16)((float)z.x * c0 + (float)a.x * s0), (f16)((float)z.y * c1 + (float)a.y * s1)};
-                        lo[h] = as_u32(l2);
-                        hi[h] = as_u32(h2);
+                    for (int e = 0; e < 8; ++e) {
+                        c8[e] = cv[b][e >> 2][e & 3];
+                        s8[e] = sv[b][e >> 2][e & 3];
                     }
+                    u32x4 lo, hi;
+                    rope8(ka[b], kz[b], c8, s8, 1.0f, lo, hi);
                     f16* krow = ks + (size_t)(start + r) * KR;
                     reinterpret_cast<u32x4*>(krow)[db] = lo;
                     reinterpret_cast<u32x4*>(krow)[4 + db] = hi;
@@ -1210,17 +1157,7 @@ prefill_attention_mfma_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_c
     // (s = 1), times the score scale 1/8 (a power of two: the fp16 rounding of
     // the scaled value is the scaled rounding)
     u32x4 qb[2];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        const f16x2 a = as_f16x2(qa[h]), z = as_f16x2(qz[h]);
-        const float c0 = cs[2 * h], c1 = cs[2 * h + 1], s0 = sn[2 * h], s1 = sn[2 * h + 1];
-        const f16x2 lo = {(f16)(0.125f * ((float)a.x * c0 - (float)z.x * s0)),
-                          (f16)(0.125f * ((float)a.y * c1 - (float)z.y * s1))};
-        const f16x2 hi = {(f16)(0.125f * ((float)z.x * c0 + (float)a.x * s0)),
-                          (f16)(0.125f * ((float)z.y * c1 + (float)a.y * s1))};
-        qb[0][h] = as_u32(lo);
-        qb[1][h] = as_u32(hi);
-    }
+    rope8(qa, qz, cs, sn, 0.125f, qb[0], qb[1]);
     __syncthreads();
     // a wavefront none of whose columns is a token only stages and takes part
     // in the barriers

@@ -56,6 +56,8 @@ int launch_pair_ring_silu(int sk, int sn, int depth, int M, const w4a16::f16* x,
                           const w4a16::f16* s, w4a16::f16* o, int inter, int K, hipStream_t stream);
 int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusion& fz, const uint8_t* w,
                            const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream);
+int launch_pair_ring_attn(int sn, int rb, const w4a16::RingFusion& fz, int T, const uint8_t* w,
+                          const w4a16::f16* s, int N, int K, float* part, hipStream_t stream);
 // w4a16_stream.hip: the streaming M = 1 kernel for long rows
 int64_t stream_lds_bytes(int64_t K);
 bool stream_instantiated(int rows, int waves, int depth, int64_t K);
@@ -1522,6 +1524,96 @@ int w4a16_linear_add_rmsnorm_f16(const void* activations, const uint8_t* packed_
     rc = run_plan(p, activations, packed_weights, scales, d, M, N, K, group_size, stream, true, workspace, tail);
     if (rc != W4A16_OK) return rc;
     return w4a16_add_rmsnorm_f16(x, d, norm_weight, eps, x_out, output, M, N, stream);
+}
+
+// The attention rows' bytes at the start of the separate launches' workspace.
+static int64_t attention_rows_bytes(int64_t tokens, int64_t K) { return (tokens * K * 2 + 255) / 256 * 256; }
+
+int64_t w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(int64_t tokens, int64_t num_heads, int64_t hidden,
+                                                              int64_t group_size) {
+    if (tokens <= 0 || num_heads <= 0 || hidden <= 0 || num_heads > INT32_MAX / 64) return 0;
+    const int64_t K = num_heads * 64;
+    const int64_t separate =
+        attention_rows_bytes(tokens, K) + w4a16_linear_add_rmsnorm_workspace_bytes(tokens, hidden, K, group_size);
+    // the fused route's K slices of partial sums (9..16 tokens only)
+    const bool slices = tokens >= 9 && tokens <= 16 && K % 256 == 0 && K / 256 >= 2 && K / 256 <= 16 && hidden <= 2048;
+    const int64_t fused = slices ? K / 256 * tokens * hidden * 4 : 0;
+    return separate > fused ? separate : fused;
+}
+
+int w4a16_prefill_attention_o_add_rmsnorm_f16(const void* qkv, void* k_cache, void* v_cache, const float* cos_table,
+                                              const float* sin_table, int64_t start, int64_t tokens,
+                                              int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                              int64_t max_seq_len, const uint8_t* o_packed, const void* o_scales,
+                                              int64_t hidden, int64_t group_size, const void* x,
+                                              const void* norm_weight, float eps, void* x_out, void* output,
+                                              void* workspace, int64_t workspace_bytes, void* stream) {
+    if (tokens == 0) return W4A16_OK;
+    if (!qkv || !k_cache || !v_cache || !cos_table || !sin_table || !o_packed || !o_scales || !x || !norm_weight ||
+        !x_out || !output || !workspace)
+        return fail(W4A16_ERR_NULL, "prefill attention + o + add_rmsnorm: every pointer must be non-NULL");
+    if (!aligned16(workspace))
+        return fail(W4A16_ERR_ALIGNMENT, "prefill attention + o + add_rmsnorm: workspace must be 16-byte aligned");
+    if (tokens < 0 || num_heads <= 0 || num_heads > INT32_MAX / 64 || hidden <= 0)
+        return fail(W4A16_ERR_SHAPE, "prefill attention + o + add_rmsnorm: tokens >= 0, num_heads and hidden positive");
+    const int64_t need =
+        w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(tokens, num_heads, hidden, group_size);
+    if (workspace_bytes < need)
+        return fail(W4A16_ERR_CONFIG, "prefill attention + o + add_rmsnorm: needs a workspace of " +
+                                          std::to_string(need) +
+                                          " bytes (w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes)");
+    const int64_t K = num_heads * 64;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    using w4a16::f16;
+    // One launch for attention + o (the ring kernel's ATTN form) where the
+    // separate attention runs its matrix-core kernel over one chunk of 32
+    // slots (query heads per KV head a power of two) and the o op runs one
+    // group pair per wavefront on 16 row slots: the attention rows are then
+    // the same arithmetic (up to the fp16 rounding of the rotary q and k),
+    // and the per-pair partial sums the same MFMA chains, added in the same
+    // order by the norm's launch
+    bool fused = head_dim == 64 && group_size == 128 && tokens >= 9 && tokens <= 16 && start >= 0 &&
+                 start + tokens <= 32 && start + tokens <= max_seq_len && max_seq_len <= INT32_MAX / 64 &&
+                 num_kv_heads > 0 && num_heads % num_kv_heads == 0 && num_heads / num_kv_heads <= 64 &&
+                 ((num_heads / num_kv_heads) & (num_heads / num_kv_heads - 1)) == 0 && K % 256 == 0 && K / 256 >= 2 &&
+                 K / 256 <= 16 && hidden <= 2048 && hidden % 8 == 0 && eps >= 0.0f && aligned16(qkv) &&
+                 aligned16(k_cache) && aligned16(v_cache) && aligned16(cos_table) && aligned16(sin_table) &&
+                 aligned16(o_packed) && (reinterpret_cast<uintptr_t>(o_scales) & 3u) == 0 && aligned16(x) &&
+                 aligned16(norm_weight) && aligned16(x_out) && aligned16(output);
+    if (fused) {
+        Plan p;
+        fused = make_plan(workspace, o_packed, o_scales, tokens, hidden, K, group_size, &p, true) == W4A16_OK &&
+                p.kernel == W4A16_KERNEL_PAIR_RING && p.max_blocks <= 1 && p.splits == K / 256;
+    }
+    if (fused) {
+        w4a16::RingFusion fz{};
+        fz.qkv = static_cast<const f16*>(qkv);
+        fz.k_cache = static_cast<f16*>(k_cache);
+        fz.v_cache = static_cast<f16*>(v_cache);
+        fz.cos_table = cos_table;
+        fz.sin_table = sin_table;
+        fz.start = (int)start;
+        fz.group = (int)(num_heads / num_kv_heads);
+        fz.num_kv = (int)num_kv_heads;
+        fz.max_seq = (int)max_seq_len;
+        int rc = w4a16_internal::launch_pair_ring_attn(8, 1, fz, (int)tokens, o_packed,
+                                                       static_cast<const f16*>(o_scales), (int)hidden, (int)K,
+                                                       static_cast<float*>(workspace), st);
+        if (rc != W4A16_OK) return rc;
+        return w4a16_internal::launch_split_add_rmsnorm((int)(K / 256), static_cast<const float*>(workspace),
+                                                        static_cast<const f16*>(x),
+                                                        static_cast<const f16*>(norm_weight), eps,
+                                                        static_cast<f16*>(x_out), static_cast<f16*>(output),
+                                                        (int)tokens, (int)hidden, st);
+    }
+    // the separate launches: attention rows at the start of the workspace
+    int rc = w4a16_prefill_attention_f16(qkv, k_cache, v_cache, cos_table, sin_table, start, tokens, workspace,
+                                         num_heads, num_kv_heads, head_dim, max_seq_len, stream);
+    if (rc != W4A16_OK) return rc;
+    const int64_t off = attention_rows_bytes(tokens, K);
+    return w4a16_linear_add_rmsnorm_f16(workspace, o_packed, o_scales, x, norm_weight, eps, x_out, output, tokens,
+                                        hidden, K, group_size, static_cast<uint8_t*>(workspace) + off,
+                                        workspace_bytes - off, stream);
 }
 
 int64_t w4a16_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t group_size) {

@@ -4,6 +4,7 @@
 // translation unit.
 #pragma once
 
+#include "w4a16_attn_device.h"
 #include "w4a16_device.h"
 
 namespace w4a16 {
@@ -78,13 +79,190 @@ __host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN
            + (MS == 1 ? (int64_t)SK * SN * 4 : 0);                                           // RMSNorm partials
 }
 
-// Fused decode-step work (M = 1): an RMSNorm of the activation row while it
-// is staged (norm_weight), a residual add in the epilogue (residual).
+// LDS of the ATTN prologue beyond the GEMV's: the slice's attention output
+// in natural order [16 rows][256] fp16, then one V tile [32 slots][72] fp16
+// per attending wavefront (rows padded to 144 bytes, as the prompt attention
+// kernel's).
+__host__ __device__ constexpr int64_t pair_ring_attn_lds_bytes() { return 16 * 256 * 2 + 4 * 32 * 72 * 2; }
+
+// Fused work around the GEMV: an RMSNorm of the activation row while it is
+// staged (norm_weight, M = 1), a residual add in the epilogue (residual, M =
+// 1), and the prompt attention that produces the activations (ATTN: qkv ..
+// max_seq).
 struct RingFusion {
     const f16* norm_weight;   // null: no RMSNorm
     float eps;
     const f16* residual;      // null: no residual add
+    const f16* qkv;           // [T][(H + 2 num_kv) 64]: q heads, k heads, v heads
+    f16* k_cache;             // [num_kv][max_seq][64]
+    f16* v_cache;
+    const float* cos_table;   // [max_seq][32]
+    const float* sin_table;
+    int start;                // the prompt's first cache slot
+    int group;                // query heads per KV head
+    int num_kv;
+    int max_seq;
 };
+
+// The ATTN prologue of one wavefront (see gemv_pair_ring): query head hq's
+// causal attention over the prompt's T tokens at slots fz.start ..
+// fz.start + T - 1 (at most slot 31), row t < T of the output written to
+// out[256 t .. 256 t + 63] (fp16); vt is the wavefront's V tile [32][72].
+// append: this wavefront writes the new k / v rows of its KV head to the
+// caches (the caller picks one per KV head). Every lane must be active.
+__device__ __forceinline__ void attend_slice(const RingFusion& fz, int T, int K, int hq, bool append, int lane,
+                                             f16* out, f16* vt) {
+    constexpr int VR = 72;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const int H = K >> 6;
+    const int start = fz.start, nk = start + T;
+    const int kv = hq / fz.group;
+    const size_t rs = (size_t)(H + 2 * fz.num_kv) * 64;   // qkv row stride
+    const f16* kq = fz.qkv + (size_t)(H + kv) * 64;
+    const f16* vq = fz.qkv + (size_t)(H + fz.num_kv + kv) * 64;
+    f16* kc = fz.k_cache + (size_t)kv * fz.max_seq * 64;
+    f16* vc = fz.v_cache + (size_t)kv * fz.max_seq * 64;
+    const int j = lane & 15, q4 = lane >> 4;
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+
+    // 1. loads: query column j (token min(j, T - 1)), key rows 16 mt + j
+    // (dims 8 q4 .. + 7 and 32 + 8 q4 .. + 7), V units lane + 64 b (slot i
+    // >> 3, dims 8 (i & 7) ..), slots below start from the caches and the
+    // new ones from qkv, then the rotary values of the query's and the keys'
+    // slots
+    const int tq = min(j, T - 1);
+    const f16* qrow = fz.qkv + (size_t)tq * rs + (size_t)hq * 64;
+    const u32x4 qa = *reinterpret_cast<const u32x4*>(qrow + 8 * q4);
+    const u32x4 qz = *reinterpret_cast<const u32x4*>(qrow + 32 + 8 * q4);
+    u32x4 kl[2], kh[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int r = 16 * mt + j;
+        const f16* src = r < start ? kc + (size_t)r * 64 : kq + (size_t)min(max(r - start, 0), T - 1) * rs;
+        kl[mt] = *reinterpret_cast<const u32x4*>(src + 8 * q4);
+        kh[mt] = *reinterpret_cast<const u32x4*>(src + 32 + 8 * q4);
+    }
+    u32x4 vv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int i = lane + 64 * b, r = i >> 3;
+        const f16* src = r < start ? vc + (size_t)r * 64 : vq + (size_t)min(max(r - start, 0), T - 1) * rs;
+        vv[b] = *reinterpret_cast<const u32x4*>(src + 8 * (i & 7));
+    }
+    auto trig = [&](int pos, float (&c)[8], float (&sn)[8]) {
+        const size_t ti = (size_t)pos * 32 + 8 * q4;
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(fz.cos_table + ti);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(fz.cos_table + ti + 4);
+        const f32x4 s0 = *reinterpret_cast<const f32x4*>(fz.sin_table + ti);
+        const f32x4 s1 = *reinterpret_cast<const f32x4*>(fz.sin_table + ti + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            c[e] = c0[e];
+            c[4 + e] = c1[e];
+            sn[e] = s0[e];
+            sn[4 + e] = s1[e];
+        }
+    };
+    float qc[8], qs[8], kcs[2][8], ksn[2][8];
+    trig(start + tq, qc, qs);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) trig(min(16 * mt + j, nk - 1), kcs[mt], ksn[mt]);
+
+    // 2. the rotary q (B operand, times 1/8) and the key rows (A operand):
+    // cached rows as they are, new rows rotated at their slot, rows past the
+    // prompt zero; then the append
+    u32x4 qb[2];
+    rope8(qa, qz, qc, qs, 0.125f, qb[0], qb[1]);
+    u32x4 ka[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const int r = 16 * mt + j;
+        u32x4 lo, hi;
+        rope8(kl[mt], kh[mt], kcs[mt], ksn[mt], 1.0f, lo, hi);
+        ka[mt][0] = r < start ? kl[mt] : r < nk ? lo : zero;
+        ka[mt][1] = r < start ? kh[mt] : r < nk ? hi : zero;
+    }
+    if (append) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const int r = 16 * mt + j;
+            if (r >= start && r < nk) {
+                *reinterpret_cast<u32x4*>(kc + (size_t)r * 64 + 8 * q4) = ka[mt][0];
+                *reinterpret_cast<u32x4*>(kc + (size_t)r * 64 + 32 + 8 * q4) = ka[mt][1];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int i = lane + 64 * b, r = i >> 3;
+            if (r >= start && r < nk) *reinterpret_cast<u32x4*>(vc + (size_t)r * 64 + 8 * (i & 7)) = vv[b];
+        }
+    }
+
+    // 3. the V tile, slot rows (zero past the prompt)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int i = lane + 64 * b, r = i >> 3;
+        *reinterpret_cast<u32x4*>(vt + r * VR + 8 * (i & 7)) = r < nk ? vv[b] : zero;
+    }
+    wave_lds_sync();
+
+    // 4. S^T = K Q^T: lane (q4, j) holds column j's scores of slots 16 mt +
+    // 4 q4 + e, masked past the column's slot; softmax over the 32 slots
+    f32x4 st[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        st[mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+            st[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ka[mt][s2]),
+                                                            __builtin_bit_cast(f16x8, qb[s2]), st[mt], 0, 0, 0);
+    }
+    const int last = start + tq;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int slot = 16 * mt + 4 * q4 + e;
+            st[mt][e] = slot <= last ? st[mt][e] : -__builtin_inff();
+            mx = fmaxf(mx, st[mt][e]);
+        }
+    mx = row_pair_max(mx);
+    const float mbl = mx * kLog2e;   // finite: slot 0 is visible to every column
+    float psum = 0.0f;
+    float pe[2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            pe[mt][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][e], kLog2e, -mbl));
+            psum += pe[mt][e];
+        }
+    const f16x2 p00 = {(f16)pe[0][0], (f16)pe[0][1]}, p01 = {(f16)pe[0][2], (f16)pe[0][3]};
+    const f16x2 p10 = {(f16)pe[1][0], (f16)pe[1][1]}, p11 = {(f16)pe[1][2], (f16)pe[1][3]};
+    const u32x4 pb = {as_u32(p00), as_u32(p01), as_u32(p10), as_u32(p11)};
+    psum = row_pair_sum(psum);
+
+    // 5. O^T = V^T P^T (V^T through the transposing LDS read): lane (q4, j)
+    // receives token j's dims 16 md + 4 q4 .. + 3
+    const float inv = 1.0f / psum;
+    const int tk = j >> 2, tm = j & 3;
+#pragma unroll
+    for (int md = 0; md < 4; ++md) {
+        const f16* src = vt + (4 * q4 + tk) * VR + 16 * md + 4 * tm;
+        const uint2 lo = lds_read_tr16(src);
+        const uint2 hi = lds_read_tr16(src + 16 * VR);
+        const u32x4 av = {lo.x, lo.y, hi.x, hi.y};
+        const f32x4 o = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                               __builtin_bit_cast(f16x8, pb),
+                                                               (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        if (j < T) {
+            const f16x2 a = {(f16)(o[0] * inv), (f16)(o[1] * inv)};
+            const f16x2 b = {(f16)(o[2] * inv), (f16)(o[3] * inv)};
+            *reinterpret_cast<uint2*>(out + j * 256 + 16 * md + 4 * q4) = make_uint2(as_u32(a), as_u32(b));
+        }
+    }
+}
 
 // SPLIT (narrow layers of long rows): the K / 256 pairs are cut into S
 // slices of SK PPW pairs; workgroup b takes slice b mod S of rows (b / S) R
@@ -117,8 +295,26 @@ struct RingFusion {
 // fp16(fp32(residual[n]) + fp32(fp16(dot))), a residual stream's x +
 // linear(a); residual may alias out (each row is read and written by the
 // same lane, the read requested with the first weights).
+//
+// ATTN (MS = 16, SPLIT, one pair per slice, SK = 1, SN >= 4): x is not read;
+// the activations are the causal attention of a prompt's M tokens at cache
+// slots start .. start + M - 1 (start + M <= 32, head_dim 64, K = 64 H for
+// H query heads), the o projection's input. Slice sl holds query heads 4 sl
+// .. 4 sl + 3; wavefront w < 4 attends head 4 sl + w for every token (MFMA
+// column j = token j) and writes its output rows to LDS, the other
+// wavefronts wait at the barrier, and staging reads the units from there.
+// The arithmetic is prefill_attention_mfma_kernel's for one chunk of 32
+// slots (rotary q scaled by 1/8 and k in fp32 rounded to fp16, S^T = K Q^T
+// and O^T = V^T P^T on the matrix cores, the softmax's max and sum across
+// the column's four lanes, exp as exp2 of the log2 e scaled score, P in
+// fp16); the compiler may round a rotary value to fp16 in one step (fused
+// multiply-add with an fp16 result) in one kernel and through fp32 in the
+// other, so a rotary q or k can differ from that kernel's by one fp16 unit.
+// Slots below start come from the caches; the new tokens' k (rotated at
+// their slots) and v come from qkv, and the first query head of each KV
+// head in row block 0 appends them to the caches.
 template <int MS, int SK, int SN, int RB, int PPW, int D, bool SPLIT = false, bool SILU = false, bool NORM = false,
-          bool RESID = false>
+          bool RESID = false, bool ATTN = false>
 __global__ void __launch_bounds__(64 * SK * SN)
 gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f16* __restrict__ scales,
                f16* out, int M, int N, int K, float* __restrict__ part, int S, RingFusion fz) {
@@ -128,6 +324,8 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
                   "the SiLU form pairs a gate block and its up block");
     static_assert(!NORM || (MS == 1 && !SPLIT), "the RMSNorm prologue normalises one whole activation row");
     static_assert(!RESID || (MS == 1 && !SPLIT && !SILU), "the residual epilogue adds to one output row");
+    static_assert(!ATTN || (MS == 16 && SPLIT && SK == 1 && PPW == 1 && SN >= 4 && !SILU),
+                  "the attention prologue fills one pair (four heads) per K slice");
     constexpr bool W16 = MS == 16;            // exact decode, two MFMAs per word
     constexpr int W = SK * SN;
     constexpr int T = 64 * W;
@@ -149,6 +347,8 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     float* sc = bias + NB;                                 // [SR][2][PS]
     float* red = sc + SR * 2 * PS;                         // [SN RB][SK][8, 64 or 128]
     float* np = red + (SK > 1 ? SN * RB * SK * (MS == 1 ? 8 : MS == 16 ? 128 : 64) : 0);   // [W] (MS = 1)
+    // ATTN: the slice's attention rows [16][256] fp16, then the V tiles
+    f16* xa = reinterpret_cast<f16*>(smem + (pair_ring_lds_bytes(MS, SK, SN, RB, PPW) + 15) / 16 * 16);
 
     const int G = K >> 7;
     const int P = G >> 1;
@@ -173,12 +373,14 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
     // staged), the workgroup's scale words, then the wavefront's first D
     // pairs of weights
     u32x4 a[XU];
+    if constexpr (!ATTN) {
 #pragma unroll
-    for (int u = 0; u < XU; ++u) {
-        const int i = threadIdx.x + u * T;
-        const int m = MS == 1 ? 0 : min(i / US, M - 1);
-        const int uu = min(pb * 32 + (MS == 1 ? i : i % US), units - 1);
-        a[u] = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + (size_t)uu * 8);
+        for (int u = 0; u < XU; ++u) {
+            const int i = threadIdx.x + u * T;
+            const int m = MS == 1 ? 0 : min(i / US, M - 1);
+            const int uu = min(pb * 32 + (MS == 1 ? i : i % US), units - 1);
+            a[u] = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + (size_t)uu * 8);
+        }
     }
     u32x4 gw[NORM ? XU : 1];
     if constexpr (NORM) {
@@ -249,6 +451,21 @@ gemv_pair_ring(const f16* __restrict__ x, const uint8_t* __restrict__ w, const f
                 const f16x2 y = {(f16)(((float)p.x * inv) * (float)g.x), (f16)(((float)p.y * inv) * (float)g.y)};
                 a[u][e] = as_u32(y);
             }
+        }
+    }
+
+    if constexpr (ATTN) {
+        // the first query head of each KV head in row block 0 appends
+        const int hq = 4 * sl + wave;
+        if (wave < 4)
+            attend_slice(fz, M, K, hq, blockIdx.x < (unsigned)S && hq % fz.group == 0, lane, xa + wave * 64,
+                         xa + 16 * 256 + wave * 32 * 72);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = threadIdx.x + u * T;
+            const int m = min(i / US, M - 1);
+            a[u] = *reinterpret_cast<const u32x4*>(xa + m * 256 + (i % US) * 8);
         }
     }
 

@@ -337,19 +337,23 @@ class LlamaDecoder(torch.nn.Module):
     def _prefill_fused(self, prompt: torch.Tensor) -> None:
         """The prompt (cache slots 0 .. T-1) with the decode step's roundings:
         RMSNorm of the embeddings, then per layer the q|k|v op, rotary + KV
-        append + causal attention, the o op, residual add + RMSNorm, the
-        gate|up projection with its SiLU * up epilogue, the down op with the
-        residual add + the next RMSNorm (the next layer's input norm, or the
-        final norm after the last layer; w4a16_linear_add_rmsnorm_f16 sums
-        the op's K slices in the norm's launch); then the lm_head GEMV on the
-        last normed row and the greedy argmax, which also gathers the first
-        decode step's input row. 7 launches per layer."""
+        append + causal attention, the o op, residual add + RMSNorm
+        (w4a16_prefill_attention_o_add_rmsnorm_f16: at 9..16 tokens the
+        attention runs inside the o op's launch and the norm's launch sums
+        its K slices), the gate|up projection with its SiLU * up epilogue,
+        the down op with the residual add + the next RMSNorm (the next
+        layer's input norm, or the final norm after the last layer;
+        w4a16_linear_add_rmsnorm_f16 sums the op's K slices in the norm's
+        launch); then the lm_head GEMV on the last normed row and the greedy
+        argmax, which also gathers the first decode step's input row. 6
+        launches per layer at 9..16 tokens, 7 otherwise."""
         cfg = self.cfg
         t = prompt.numel()
         g = cfg.group_size
         x = self.embed[prompt]
         h = torch.empty_like(x)
-        attn = torch.empty((t, cfg.num_heads * cfg.head_dim), dtype=torch.float16, device=x.device)
+        attn = (torch.empty((t, cfg.num_heads * cfg.head_dim), dtype=torch.float16, device=x.device)
+                if t > FUSED_PREFILL_NATIVE_MAX_ROWS else None)
         mlp = torch.empty((t, cfg.intermediate_size), dtype=torch.float16, device=x.device)
         first = self.layers[0].input_norm
         _lib.rmsnorm_f16(x, first.weight, first.eps, h)
@@ -357,10 +361,17 @@ class LlamaDecoder(torch.nn.Module):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
             qkv = self._prefill_linear(h, qkv_w, qkv_s)
-            _lib.prefill_attention_f16(qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, attn,
-                                       cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
-            o = self._prefill_linear(attn, b.o_proj.packed_weights, b.o_proj.scales)
-            _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
+            if t <= FUSED_PREFILL_NATIVE_MAX_ROWS:
+                # attention + o + residual add + norm (9..16 tokens: the attention inside the o op's launch)
+                _lib.prefill_attention_o_add_rmsnorm_f16(
+                    qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, b.o_proj.packed_weights,
+                    b.o_proj.scales, x, b.post_norm.weight, b.post_norm.eps, x, h, cfg.num_heads, cfg.num_kv_heads,
+                    cfg.head_dim, g)
+            else:
+                _lib.prefill_attention_f16(qkv, self.k_cache[i], self.v_cache[i], self.cos, self.sin, 0, attn,
+                                           cfg.num_heads, cfg.num_kv_heads, cfg.head_dim)
+                o = self._prefill_linear(attn, b.o_proj.packed_weights, b.o_proj.scales)
+                _lib.add_rmsnorm_f16(x, o, b.post_norm.weight, b.post_norm.eps, x, h)
             if t <= FUSED_PREFILL_NATIVE_MAX_ROWS:
                 _lib.linear_silu_f16(h, gu_w, gu_s, mlp, g)   # gate|up projection with the SiLU * up epilogue
             else:

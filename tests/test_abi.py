@@ -75,6 +75,24 @@ def test_decode_entry_points_validate_before_launch():
     assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 16, 2048, 5632, 128, a, need - 1, 0) == \
         _lib.W4A16_ERR_CONFIG
     assert lib.w4a16_linear_add_rmsnorm_f16(a, a, a, a, a, 1e-5, a, a, 0, 2048, 5632, 128, 0, 0, 0) == _lib.W4A16_OK
+    # prefill attention + o + residual add + RMSNorm: the workspace (the fused route's K slices of partial
+    # sums, or the attention rows then the separate launches' workspace), pointers, alignment, empty
+    need = lib.w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(16, 32, 2048, 128)
+    assert need == 8 * 16 * 2048 * 4
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(300, 32, 2048, 128) == \
+        300 * 2048 * 2 + lib.w4a16_linear_add_rmsnorm_workspace_bytes(300, 2048, 2048, 128)
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes(16, 0, 2048, 128) == 0
+    attn_args = [a] * 5 + [0, 16, 32, 4, 64, 48, a, a, 2048, 128, a, a, 1e-5, a, a]
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args, 0, 0, 0) == _lib.W4A16_ERR_NULL
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args[:11], 0, *attn_args[12:], a, need, 0) == \
+        _lib.W4A16_ERR_NULL
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args, a + 8, need, 0) == _lib.W4A16_ERR_ALIGNMENT
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args, a, need - 1, 0) == _lib.W4A16_ERR_CONFIG
+    assert "w4a16_prefill_attention_o_add_rmsnorm_workspace_bytes" in _lib.last_error()
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args[:6], -1, *attn_args[7:], a, need, 0) == \
+        _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_prefill_attention_o_add_rmsnorm_f16(*attn_args[:6], 0, *attn_args[7:], 0, 0, 0) == \
+        _lib.W4A16_OK   # no tokens: nothing
     # linear + SiLU: group size, shapes, NULL pointers, alignment, empty
     assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 256, 64, 0) == _lib.W4A16_ERR_GROUP_SIZE
     assert lib.w4a16_linear_silu_f16(a, a, a, a, 4, 64, 200, 128, 0) == _lib.W4A16_ERR_SHAPE

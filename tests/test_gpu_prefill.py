@@ -347,6 +347,66 @@ def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     assert torch.equal(model.logits, logits_eager) and torch.equal(model.k_cache, k_eager)
 
 
+# (query heads, KV heads, tokens, start, hidden): 9..16 tokens at slots up to
+# 31 with K = 2048 and a power-of-two group take the attention inside the o
+# op's launch (configs[4]'s prompt first; slots below start from the caches;
+# group 4, 8 and 32; hidden 1024); past slot 31, at 8 tokens, on K = 1024,
+# group 3 and hidden 2000 the separate launches
+_ATTN_O_CASES = [(32, 4, 16, 0, 2048), (32, 4, 9, 0, 2048), (32, 4, 12, 7, 2048), (32, 4, 16, 16, 2048),
+                 (32, 8, 16, 0, 1024), (32, 1, 13, 3, 2048), (32, 4, 16, 17, 2048), (32, 4, 8, 0, 2048),
+                 (16, 4, 16, 0, 2048), (12, 4, 16, 0, 1024), (32, 4, 16, 0, 2000)]
+
+
+@pytest.mark.parametrize("heads,kv,tokens,start,hidden", _ATTN_O_CASES)
+def test_prefill_attention_o_add_rmsnorm_matches_separate_launches(gpu, heads, kv, tokens, start, hidden):
+    """w4a16_prefill_attention_o_add_rmsnorm_f16 against the prefill
+    attention, the op and the residual add + RMSNorm as three launches: the
+    v cache bit for bit, the rotary k rows within an fp16 ulp (each kernel
+    rounds its fp32 rotation to fp16, the compiler choosing a single fused
+    rounding or fp32 then fp16 per instruction), x_out (in place) and the
+    normed rows within a few fp16 ulps; the separate launches' attention rows
+    are held to the float64 restatement and their o op to the oracle."""
+    from tests._cases import assert_parity, expected, make_case
+
+    S = 64
+    k = heads * 64
+    gen = torch.Generator().manual_seed(heads * 100 + kv * 10 + tokens + start + hidden)
+    qkv = torch.randn((tokens, (heads + 2 * kv) * 64), generator=gen).to(torch.float16)
+    k_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    v_cache = torch.randn((kv, S, 64), generator=gen).to(torch.float16)
+    cos, sin = _tables(S)
+    _, p, s = make_case(tokens, k, hidden, seed=hidden + tokens)
+    resid = torch.randn((tokens, hidden), generator=gen).to(torch.float16)
+    w = (1 + 0.1 * torch.randn((hidden,), generator=gen)).to(torch.float16)
+    qkv_d, cos_d, sin_d = qkv.to(gpu), cos.to(gpu), sin.to(gpu)
+    pd, sd, wd, resid_d = p.to(gpu), s.to(gpu), w.to(gpu), resid.to(gpu)
+    print(f"[case] prefill attention + o + add_rmsnorm heads={heads} kv={kv} tokens={tokens} start={start} "
+          f"hidden={hidden}", flush=True)
+    kd, vd = k_cache.to(gpu), v_cache.to(gpu)
+    x = resid_d.clone()
+    h = torch.full((tokens, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    _lib.prefill_attention_o_add_rmsnorm_f16(qkv_d, kd, vd, cos_d, sin_d, start, pd, sd, x, wd, 1e-5, x, h, heads,
+                                             kv)
+    # the separate launches
+    ks, vs = k_cache.to(gpu), v_cache.to(gpu)
+    attn = torch.empty((tokens, k), dtype=torch.float16, device=gpu)
+    _lib.prefill_attention_f16(qkv_d, ks, vs, cos_d, sin_d, start, attn, heads, kv)
+    d = torch.empty((tokens, hidden), dtype=torch.float16, device=gpu)
+    _lib.linear_f16(attn, pd, sd, d)
+    xs, hs = torch.empty_like(resid_d), torch.empty_like(h)
+    _lib.add_rmsnorm_f16(resid_d, d, wd, 1e-5, xs, hs)
+    torch.cuda.synchronize()
+    assert torch.equal(vd, vs)
+    assert torch.allclose(kd.float(), ks.float(), rtol=ULP, atol=2 ** -14)
+    for got, want, name in ((x, xs, "x_out"), (h, hs, "normed rows")):
+        err = (got.float() - want.float()).abs()
+        assert torch.all(err <= 4e-3 + 4 * ULP * want.float().abs()), (name, float(err.max()))
+    ref = _prefill_attention_ref(qkv, k_cache, v_cache, cos, sin, start, heads, kv)[0]
+    err = (attn.double().cpu() - ref).abs()
+    assert torch.all(err <= 2e-3 + 1e-2 * ref.abs()), float(err.max())
+    assert_parity(d, expected(attn.cpu(), p, s), f"o op tokens={tokens} K={k} N={hidden}")
+
+
 @pytest.mark.parametrize("m,k,n,alias", [(16, 5632, 2048, True), (12, 5632, 2048, False), (9, 5632, 2048, True),
                                          (16, 14336, 4096, False), (4, 5632, 2048, False), (16, 8192, 2048, True),
                                          (16, 5632, 2044, False), (13, 5632, 1000, True)])
