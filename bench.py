@@ -37,7 +37,12 @@ CPU oracle's time for the same layers on the host cores (`cpu_baseline`; a
 reported baseline, not a target), with configs[0] (M = 1, 2048 x 2048) timed
 on the product's torch CPU path beside the oracle, and the CPU model.
 
+Every leg runs inside a named roctx range (torch.cuda.nvtx on ROCm;
+`rocprofv3 --marker-trace` records them), and `--profiler torch` writes a
+Chrome trace of the configs[1] calls, as the reference's profiler script does.
+
 usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-decode] [--no-cpu] [--no-tables] [--long]
+                       [--profiler none|torch] [--trace-dir DIR]
        python bench.py --headline-pass | --layer-pass M K N COPIES CALLS | --prefill-pass TOKENS   (profiler passes)
 """
 
@@ -91,6 +96,42 @@ def _kernel_name(plan: dict, m: int = 1, k: int = 0) -> str:
     if plan["kernel"] == "valu":
         return f"w4a16::gemv_valu<1,{plan['rows']},{plan['unroll']},false>"
     return f"w4a16 {plan['kernel']} kernel"
+
+
+class trace_range:
+    """A named range around one leg of the bench (reference
+    scripts/profile_kernel.py:346-352 wraps each baseline in an NVTX range):
+    torch.cuda.nvtx is roctx on ROCm, so `rocprofv3 --marker-trace` records
+    it and the kernels inside the range's span belong to that leg."""
+
+    def __init__(self, name: str):
+        self.name = name
+
+    def __enter__(self):
+        import torch
+
+        torch.cuda.nvtx.range_push(self.name)
+        return self
+
+    def __exit__(self, *exc):
+        import torch
+
+        torch.cuda.nvtx.range_pop()
+        return False
+
+
+def torch_trace(op, iters: int, path: str) -> None:
+    """Chrome trace of `iters` eager calls of `op` (reference
+    scripts/profile_kernel.py:576-591, its --profiler torch)."""
+    import torch
+
+    os.makedirs(os.path.dirname(path) or ".", exist_ok=True)
+    activities = [torch.profiler.ProfilerActivity.CPU, torch.profiler.ProfilerActivity.CUDA]
+    with torch.profiler.profile(activities=activities, record_shapes=True) as prof:
+        for i in range(iters):
+            op(i)
+        torch.cuda.synchronize()
+    prof.export_chrome_trace(path)
 
 
 def payload_bytes(m: int, n: int, k: int, group: int = 128) -> int:
@@ -592,7 +633,8 @@ def layer_tables(device, copy_gbps: float | None = None) -> dict:
             for m in ms:
                 x = torch.randn((m, k), device=device).to(torch.float16)
                 out = torch.empty((m, n), device=device, dtype=torch.float16)
-                us = per_layer(lambda i: _lib.linear_f16(x, packed[i], scales[i], out), copies, samples=samples)
+                with trace_range(f"w4a16_fused M={m} K{k}xN{n}"):
+                    us = per_layer(lambda i: _lib.linear_f16(x, packed[i], scales[i], out), copies, samples=samples)
                 # the calls take a workspace from the caching allocator where the
                 # plan uses one (the split-K routes), as the torch op does
                 plan = _lib.plan_linear(x.data_ptr(), packed[0].data_ptr(), m, n, k, workspace=True)
@@ -606,8 +648,16 @@ def layer_tables(device, copy_gbps: float | None = None) -> dict:
                 else:
                     row["vs_M1"] = round(us / base_us, 3)
                 if w16:
-                    row["fp16_hipblaslt_us"] = round(
-                        per_layer(lambda i: F.linear(x, w16[i]), len(w16), samples=samples), 3)
+                    with trace_range(f"w4a16_fp16 M={m} K{k}xN{n}"):
+                        row["fp16_hipblaslt_us"] = round(
+                            per_layer(lambda i: F.linear(x, w16[i]), len(w16), samples=samples), 3)
+                    # the reference's dequant_every_call baseline: the weights
+                    # dequantized on every call (here by the dequantize op),
+                    # then the fp16 GEMM
+                    with trace_range(f"w4a16_dequant M={m} K{k}xN{n}"):
+                        row["dequant_every_call_us"] = round(per_layer(
+                            lambda i: F.linear(x, torch.ops.w4a16.dequantize(packed[i], scales[i], 128)), copies,
+                            samples=samples), 3)
                 rows.append(row)
             del packed, scales, w16
             torch.cuda.empty_cache()
@@ -630,6 +680,10 @@ def main() -> int:
     ap.add_argument("--long", action="store_true",
                     help="also time prompts of 64 / 256 / 1024 tokens and decode after a 1500-token prompt (no "
                          "BASELINE config covers them)")
+    ap.add_argument("--profiler", choices=("none", "torch"), default="none",
+                    help="torch: also write a Chrome trace of 20 torch-op calls of each configs[1] shape to "
+                         "--trace-dir (reference scripts/profile_kernel.py --profiler torch)")
+    ap.add_argument("--trace-dir", default="profile_results", help="directory of the --profiler torch traces")
     ap.add_argument("--headline-pass", action="store_true",
                     help="for rocprofv3 --kernel-trace: the headline sequence alone (clock settle, pre-roll, "
                          "warm-up, the K timed eager steps); prints the event-timed ms per step; no JSON")
@@ -811,12 +865,13 @@ def main() -> int:
         for _ in range(rolls):
             preroll.replay()
         warm.replay()
-        start_ev.record()
-        for i in range(args.steps):
-            step(copies + warmup + i)
-        queued = not start_ev.query()
-        end_ev.record()
-        end_ev.synchronize()
+        with trace_range("w4a16_fused headline timed steps"):
+            start_ev.record()
+            for i in range(args.steps):
+                step(copies + warmup + i)
+            queued = not start_ev.query()
+            end_ev.record()
+            end_ev.synchronize()
         if queued:
             timed_launch = (f"eager calls, enqueued behind {rolls} untimed pre-roll replays and the warm-up "
                             "(the GPU had not reached the timed region when the last timed call was enqueued)")
@@ -914,17 +969,28 @@ def main() -> int:
     }
     line["gpu_state"] = gpu_state_under_load(preroll)
     line["copy_GBps"] = copy_gbps
+    if args.profiler == "torch":
+        traces = []
+        for j, (k, n) in enumerate(shapes):
+            path = os.path.join(args.trace_dir, f"torch_fused_M1_K{k}xN{n}.json")
+            with trace_range(f"w4a16_fused torch trace K{k}xN{n}"):
+                torch_trace(lambda i, j=j: call(j, i), 20, path)
+            traces.append(path)
+        line["torch_traces"] = traces
     if not args.no_tables:
         line["layers"] = layer_tables(device, copy_gbps)
     if not args.no_decode:
         del layers
         torch.cuda.empty_cache()
-        line["decode"] = decode_tok_s(device)
+        with trace_range("decode configs[4]"):
+            line["decode"] = decode_tok_s(device)
         if args.long:
-            line["decode"].update(prefill_long(device))
-            line["decode"].update(decode_long_context(device))
+            with trace_range("long prompts and long-context decode"):
+                line["decode"].update(prefill_long(device))
+                line["decode"].update(decode_long_context(device))
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(shapes)
+        with trace_range("cpu baseline"):
+            line["cpu_baseline"] = cpu_baseline(shapes)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -107,8 +107,13 @@ int ensure_lds(const void* kernel, int bytes) {
     if (done.count({kernel, device})) return W4A16_OK;
     const hipError_t e =
         hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes);
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        // the runtime also keeps the error as the thread's last error: take
+        // it back, so the next launch check (ours or the caller's) does not
+        // report it as its own
+        (void)hipGetLastError();
         return fail(W4A16_ERR_LAUNCH, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+    }
     done.insert({kernel, device});
     return W4A16_OK;
 }
