@@ -65,10 +65,12 @@ SETTLE_SECONDS = 0.25
 # The same before each per-layer timing (whose weights the host has just
 # built while the GPU idled).
 LAYER_SETTLE_SECONDS = 0.15
-# Decode steps per graph replay in the decode measurement (the generation
-# loop replays a graph of this many steps while the position allows it, one
-# step otherwise); the one-step-per-replay rate is reported beside it.
-TOKENS_PER_REPLAY = 8
+# Most decode steps per graph replay in the decode measurement: the decoder
+# captures graphs of 16, 8, 4 and 2 steps and the generation loop replays the
+# largest that fits the tokens left while the position allows it, one step
+# otherwise (31 tokens: 5 replays); the one-step-per-replay rate is reported
+# beside it.
+TOKENS_PER_REPLAY = 16
 # HBM bytes per launch of the M=1 GEMV on the two configs[1] shapes (mean),
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
@@ -96,6 +98,18 @@ def _kernel_name(plan: dict, m: int = 1, k: int = 0) -> str:
     if plan["kernel"] == "valu":
         return f"w4a16::gemv_valu<1,{plan['rows']},{plan['unroll']},false>"
     return f"w4a16 {plan['kernel']} kernel"
+
+
+def torch_inference(fn):
+    """fn under torch.inference_mode (the decoder's buffers are inference
+    tensors; graph captures of launches on them must run in that mode)."""
+    def wrapped(*args, **kwargs):
+        import torch
+
+        with torch.inference_mode():
+            return fn(*args, **kwargs)
+
+    return wrapped
 
 
 class trace_range:
@@ -478,7 +492,8 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
         "weight_GBps": round(model.packed_bytes() * (new_tokens - 1) / med / 1e9, 1),
         "step": "fused, positions < 64: RMSNorm+qkv GEMV+rotary+KV append, attention+o GEMV+residual, "
                 "RMSNorm+gate|up GEMV+SiLU*up, down GEMV+residual per layer; RMSNorm+lm_head GEMV, argmax; "
-                f"{TOKENS_PER_REPLAY} steps per graph replay while the position allows, else one",
+                f"graphs of {TOKENS_PER_REPLAY}, {TOKENS_PER_REPLAY // 2}, .. 2 steps (the largest that fits the "
+                "tokens left) while the position allows, else one step per replay",
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),
@@ -496,9 +511,99 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     }
 
 
+@torch_inference
+def launch_times(device, prompt_len: int = 16) -> dict:
+    """Per-launch GPU time of the configs[4] decoder's fused prefill (16
+    tokens) and fused decode step: each launch kind captured 22 times (layer
+    i's weights and caches in call i) in one graph, median replay time / 22,
+    after untimed replays; the whole prefill graph timed with events around
+    its replay. Inputs are the decoder's own buffers after a prefill (the
+    values only set the data the launches read)."""
+    import torch
+
+    from nibble_amd import _lib
+    from nibble_amd.llama import LlamaConfig, LlamaDecoder
+
+    model = LlamaDecoder(LlamaConfig(max_seq_len=48), device=device, seed=0)
+    cfg, g = model.cfg, model.cfg.group_size
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=torch.Generator().manual_seed(0)).to(device)
+    model.capture_prefill(prompt_len)
+    model.prefill(prompt)
+    torch.cuda.synchronize()
+
+    def graph_us(fn, count: int) -> float:
+        graph = capture(lambda i: fn(i), count)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < LAYER_SETTLE_SECONDS:
+            graph.replay()
+            torch.cuda.synchronize()
+        times = sorted(time_graph(graph) for _ in range(15))
+        return times[len(times) // 2] / count * 1e6
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    whole = []
+    for _ in range(15):
+        torch.cuda.synchronize()
+        start.record()
+        model.prefill_graph.replay()
+        end.record()
+        end.synchronize()
+        whole.append(start.elapsed_time(end) * 1e3)
+    whole.sort()
+    layers = len(model.layers)
+    x = model.embed[prompt].contiguous()
+    h = torch.empty_like(x)
+    qkv = torch.empty((prompt_len, model.qkv[0][0].shape[0]), dtype=torch.float16, device=device)
+    mlp = torch.empty((prompt_len, cfg.intermediate_size), dtype=torch.float16, device=device)
+    blk = model.layers
+    prefill = {
+        "rmsnorm (embeddings, once)": lambda i: _lib.rmsnorm_f16(x, blk[0].input_norm.weight, 1e-5, h),
+        "q|k|v op": lambda i: _lib.linear_f16(h, model.qkv[i][0], model.qkv[i][1], qkv),
+        "attention + o op, then slice sum + residual + RMSNorm (2 launches)":
+            lambda i: _lib.prefill_attention_o_add_rmsnorm_f16(
+                qkv, model.k_cache[i], model.v_cache[i], model.cos, model.sin, 0, blk[i].o_proj.packed_weights,
+                blk[i].o_proj.scales, x, blk[i].post_norm.weight, 1e-5, x, h, cfg.num_heads, cfg.num_kv_heads,
+                cfg.head_dim, g),
+        "gate|up op + SiLU * up": lambda i: _lib.linear_silu_f16(h, model.gate_up[i][0], model.gate_up[i][1], mlp, g),
+        "down op, then slice sum + residual + RMSNorm (2 launches)":
+            lambda i: _lib.linear_add_rmsnorm_f16(mlp, blk[i].down_proj.packed_weights, blk[i].down_proj.scales, x,
+                                                  blk[i].post_norm.weight, 1e-5, x, h, g),
+        "lm_head GEMV (once)": lambda i: _lib.gemv_fused_f16(h[-1], model.lm_head.packed_weights,
+                                                             model.lm_head.scales, model.logits),
+        "argmax + next embedding (once)": lambda i: _lib.argmax_embed_f16(model.logits, model.token, None,
+                                                                          model.embed, model.x_buf),
+    }
+    out = {"prefill_tokens": prompt_len,
+           "prefill_graph_us": round(whole[len(whole) // 2], 2),
+           "prefill_us_per_launch": {k: round(graph_us(f, layers), 2) for k, f in prefill.items()}}
+    # the decode step's launches at position 16 (below 64: the short step)
+    model.position.fill_(prompt_len)
+    xb = model.x_buf
+    step = {
+        "RMSNorm + q|k|v GEMV + rotary + KV append": lambda i: _lib.gemv_qkv_rope_f16(
+            xb, model.qkv[i][0], model.qkv[i][1], model.qkv_buf, model.k_cache[i], model.v_cache[i], model.inv_freq,
+            model.position, cfg.num_heads, cfg.num_kv_heads, norm_weight=blk[i].input_norm.weight, eps=1e-5),
+        "attention + o GEMV + residual": lambda i: _lib.attention_o_cached_f16(
+            model.qkv_buf, model.k_cache[i], model.v_cache[i], model.position, blk[i].o_proj.packed_weights,
+            blk[i].o_proj.scales, xb, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, g),
+        "RMSNorm + gate|up GEMV + SiLU * up": lambda i: _lib.gemv_fused_f16(
+            xb, model.gate_up[i][0], model.gate_up[i][1], model.mlp_buf, norm_weight=blk[i].post_norm.weight,
+            eps=1e-5, paired=True),
+        "down GEMV + residual": lambda i: _lib.gemv_fused_f16(model.mlp_buf, blk[i].down_proj.packed_weights,
+                                                              blk[i].down_proj.scales, xb, residual=xb),
+        "RMSNorm + lm_head GEMV (once)": lambda i: _lib.gemv_fused_f16(
+            xb, model.lm_head.packed_weights, model.lm_head.scales, model.logits, norm_weight=model.norm.weight,
+            eps=1e-5),
+        "argmax + next embedding (once)": lambda i: _lib.argmax_embed_f16(model.logits, model.token, None,
+                                                                          model.embed, xb),
+    }
+    out["decode_us_per_launch"] = {k: round(graph_us(f, layers), 2) for k, f in step.items()}
+    return out
+
+
 def decode_long_context(device, prompt_len: int = 1500, max_seq_len: int = 2048, new_tokens: int = 64,
                         runs: int = 3) -> dict:
-    """Graph-replayed decode (8 steps per replay) after a 1500-token prompt
+    """Graph-replayed decode (one step per replay: positions past 63) after a 1500-token prompt
     in a 2048-slot cache on the random-init 1.1B Llama: the decode attention
     split over the slots (the decoder's default past 512 slots) against one
     workgroup per head."""
@@ -535,7 +640,7 @@ def decode_long_context(device, prompt_len: int = 1500, max_seq_len: int = 2048,
     return {f"decode_ctx{prompt_len}_tok_s": round(split_rate, 1),
             f"decode_ctx{prompt_len}_one_wg_per_head_tok_s": round(single_rate, 1),
             "decode_long_context": f"{new_tokens} tokens after a {prompt_len}-token prompt, {max_seq_len}-slot "
-                                   f"cache, {TOKENS_PER_REPLAY} steps per graph replay: decode attention split "
+                                   f"cache, one step per graph replay: decode attention split "
                                    f"into {splits} shares per head, against one workgroup per head"}
 
 
@@ -697,15 +802,20 @@ def main() -> int:
     ap.add_argument("--prefill-pass", type=int, metavar="TOKENS",
                     help="for rocprofv3 --kernel-trace: capture the fused prefill of a TOKENS-token prompt on the "
                          "random-init 1.1B Llama and replay it 10 times; no JSON")
+    ap.add_argument("--launch-pass", action="store_true",
+                    help="graph timing of each launch of the configs[4] decoder alone (the 16-token prefill's "
+                         "and the decode step's), 22 launches per graph over the layers' weights, the "
+                         "whole prefill graph beside them (rocprofv3 durations of graph-replayed kernels run "
+                         "above these); prints one JSON line")
     ap.add_argument("--decode-pass", type=int, nargs=2, metavar=("CONTEXT", "SPLITS"),
                     help="for rocprofv3 --kernel-trace: on the random-init 1.1B Llama with a 2048-slot cache, "
-                         "prefill a CONTEXT-token prompt, then decode 64 tokens by graph replay (8 steps per "
+                         "prefill a CONTEXT-token prompt, then decode 64 tokens by graph replay (one step per "
                          "replay) with the decode attention split into SPLITS shares per head (0: one workgroup "
                          "per head, -1: the decoder's default); no JSON")
     ap.add_argument("--decode-step-pass", action="store_true",
                     help="for rocprofv3 --kernel-trace: the decode leg's fused measurement alone (configs[4]: "
-                         "random-init 1.1B Llama, 48-slot cache, 16-token prompt, 31 tokens by graph replay of "
-                         f"{TOKENS_PER_REPLAY} steps, 6 times); no JSON")
+                         "random-init 1.1B Llama, 48-slot cache, 16-token prompt, 31 tokens by replays of the "
+                         f"{TOKENS_PER_REPLAY}, 8, 4, 2 and 1-step graphs, 6 times); no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -737,6 +847,10 @@ def main() -> int:
             model.prefill(prompt)
         torch.cuda.synchronize()
         print("prefill pass done", flush=True)
+        return 0
+
+    if args.launch_pass:
+        print(json.dumps(launch_times(device)), flush=True)
         return 0
 
     if args.decode_step_pass:

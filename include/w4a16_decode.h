@@ -189,13 +189,16 @@ int w4a16_argmax_f16(const void* logits, int64_t n, int64_t* token, int64_t* pos
 /*
  * w4a16_argmax_f16, then output[0..hidden) = table[*token, :] (fp16 [vocab,
  * hidden], vocab >= n): the next step's embedding gathered by the same
- * launch, so a decode step needs no separate gather.
+ * launch, so a decode step needs no separate gather. token_copy (may be
+ * NULL) receives the token too: a slot of a caller's token history (a graph
+ * of several decode steps gives each step's launch its own slot, so no copy
+ * launch follows the step).
  * Replaces (reference): the greedy pick plus the next step's embedding
  * lookup (scripts/generate.py:286-293).
  */
 int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_t* position,
                            const void* table, int64_t vocab, int64_t hidden, void* output,
-                           void* stream);
+                           int64_t* token_copy, void* stream);
 
 /*
  * output[0..hidden) = table[*token, :] (fp16 [vocab, hidden]); a token

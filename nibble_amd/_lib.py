@@ -92,7 +92,7 @@ DECODE_SIGNATURES = {
         [_vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64, _vp],
     ),
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
-    "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
     "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
@@ -384,12 +384,14 @@ def argmax_f16(logits, token, position=None, stream=None) -> None:
                                      _stream_ptr(stream)))
 
 
-def argmax_embed_f16(logits, token, position, table, output, stream=None) -> None:
+def argmax_embed_f16(logits, token, position, table, output, stream=None, token_copy=None) -> None:
     """``w4a16_argmax_embed_f16``: token <- argmax(logits); position += 1;
-    output <- table[token] (the next step's input row)."""
+    output <- table[token] (the next step's input row); token_copy (an int64
+    element, e.g. a slot of a token history) <- the token as well."""
     vocab, hidden = table.shape
     _raise_on(lib().w4a16_argmax_embed_f16(logits.data_ptr(), logits.numel(), token.data_ptr(), _ptr(position),
-                                           table.data_ptr(), vocab, hidden, output.data_ptr(), _stream_ptr(stream)))
+                                           table.data_ptr(), vocab, hidden, output.data_ptr(), _ptr(token_copy),
+                                           _stream_ptr(stream)))
 
 
 def embedding_f16(table, token, output, stream=None) -> None:

@@ -263,7 +263,8 @@ decode_attention_merge(const float* __restrict__ partial, const int64_t* __restr
 // Greedy argmax over fp16 logits (first index of the maximum, as
 // torch.argmax; NaN logits are skipped), one workgroup of 1024 threads
 // reading 16-byte vectors when the logits are 16-byte aligned; writes the
-// token and, when given, advances the position by one and gathers the
+// token (and, when given, the same to token_copy, a slot of a token
+// history) and, when given, advances the position by one and gathers the
 // token's embedding row into `emb_out` (the next decode step's input), so the
 // step needs no separate gather. Two passes: the maximum (packed fp16 max
 // over each thread's vectors, then the workgroup), and the first index that
@@ -274,7 +275,8 @@ decode_attention_merge(const float* __restrict__ partial, const int64_t* __restr
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
 argmax_kernel(const f16* __restrict__ logits, int n, int64_t* __restrict__ token, int64_t* __restrict__ position,
-              const f16* __restrict__ table, int64_t vocab, int hidden, f16* __restrict__ emb_out) {
+              const f16* __restrict__ table, int64_t vocab, int hidden, f16* __restrict__ emb_out,
+              int64_t* __restrict__ token_copy) {
     constexpr int T = 1024;
     __shared__ float wave_max[T / 64];
     __shared__ int wave_first[T / 64];
@@ -341,6 +343,7 @@ argmax_kernel(const f16* __restrict__ logits, int n, int64_t* __restrict__ token
     const int64_t t = first < n ? first : 0;
     if (lane == 0) {
         token[0] = t;
+        if (token_copy != nullptr) token_copy[0] = t;
         if (position != nullptr) position[0] = pos0 + 1;
     }
     if (emb_out == nullptr) return;
@@ -1557,11 +1560,11 @@ int w4a16_attention_o_cached_f16(const void* qkv, const void* k_cache, const voi
 }
 
 int w4a16_argmax_f16(const void* logits, int64_t n, int64_t* token, int64_t* position, void* stream) {
-    return w4a16_argmax_embed_f16(logits, n, token, position, nullptr, 0, 0, nullptr, stream);
+    return w4a16_argmax_embed_f16(logits, n, token, position, nullptr, 0, 0, nullptr, nullptr, stream);
 }
 
 int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_t* position, const void* table,
-                           int64_t vocab, int64_t hidden, void* output, void* stream) {
+                           int64_t vocab, int64_t hidden, void* output, int64_t* token_copy, void* stream) {
     if (!logits || !token) return fail(W4A16_ERR_NULL, "argmax: logits and token must be non-NULL");
     if (n <= 0 || n > INT32_MAX - 1024) return fail(W4A16_ERR_SHAPE, "argmax: n must be in 1..2^31-1025");
     if ((table == nullptr) != (output == nullptr))
@@ -1570,7 +1573,8 @@ int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_
         return fail(W4A16_ERR_SHAPE, "argmax: the embedding table needs vocab >= n and a positive hidden size");
     hipLaunchKernelGGL(w4a16::argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
                        static_cast<const w4a16::f16*>(logits), (int)n, token, position,
-                       static_cast<const w4a16::f16*>(table), vocab, (int)hidden, static_cast<w4a16::f16*>(output));
+                       static_cast<const w4a16::f16*>(table), vocab, (int)hidden, static_cast<w4a16::f16*>(output),
+                       token_copy);
     return check_launch();
 }
 

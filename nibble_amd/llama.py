@@ -262,8 +262,10 @@ class LlamaDecoder(torch.nn.Module):
         self.position = torch.zeros((1,), dtype=torch.int64, device=device)
         self.graph: torch.cuda.CUDAGraph | None = None
         self.graph_short: torch.cuda.CUDAGraph | None = None   # attention + o fused (position < 64)
-        # several short steps in one graph (capture(tokens_per_replay=T)); step j's token goes to multi_tokens[j]
+        # several short steps in one graph (capture(tokens_per_replay=T)): graphs of T, T // 2, .. (> 1)
+        # steps; step j's token goes to multi_tokens[j]. graph_multi is the T-step one.
         self.graph_multi: torch.cuda.CUDAGraph | None = None
+        self.graphs_multi: dict[int, torch.cuda.CUDAGraph] = {}
         self.multi_tokens: torch.Tensor | None = None
         # position < 64: rotary + KV append in the q|k|v GEMV's epilogue (else in the attention + o launch)
         self.qkv_rope = True
@@ -434,21 +436,25 @@ class LlamaDecoder(torch.nn.Module):
         launch, which covers positions below 64."""
         return self.attn_o and self.host_position < min(64, self.cfg.max_seq_len)
 
-    def _step(self, short: bool | None = None) -> None:
+    def _step(self, short: bool | None = None, token_copy: torch.Tensor | None = None) -> None:
+        """One decode step; token_copy (an int64 element) also receives the
+        new token."""
         if self.fused:
-            self._step_fused(self.short_step() if short is None else short)
+            self._step_fused(self.short_step() if short is None else short, token_copy)
             return
         logits = self._forward(self.token, self.position)
         self.logits.copy_(logits)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.add_(1)
+        if token_copy is not None:
+            token_copy.copy_(self.token[0])
 
-    def _step_fused(self, short: bool = False) -> None:
+    def _step_fused(self, short: bool = False, token_copy: torch.Tensor | None = None) -> None:
         """One decode step as 5 launches per layer plus 2 (include/w4a16_decode.h),
         4 per layer when `short` (attention + o projection in one launch; the
         position must then be below 64). x_buf holds the current token's
         embedding on entry (prefill gathers the first one); the final argmax
-        gathers the next token's."""
+        gathers the next token's and writes the token to token_copy as well."""
         cfg = self.cfg
         x = self.x_buf
         for i, b in enumerate(self.layers):
@@ -487,7 +493,7 @@ class LlamaDecoder(torch.nn.Module):
         # (w4a16_gemv_argmax_f16) pays one device-scope fence per workgroup.
         _lib.gemv_fused_f16(x, self.lm_head.packed_weights, self.lm_head.scales, self.logits,
                             norm_weight=self.norm.weight, eps=self.norm.eps)
-        _lib.argmax_embed_f16(self.logits, self.token, self.position, self.embed, x)
+        _lib.argmax_embed_f16(self.logits, self.token, self.position, self.embed, x, token_copy=token_copy)
 
     @torch.inference_mode()
     def step(self) -> torch.Tensor:
@@ -511,12 +517,11 @@ class LlamaDecoder(torch.nn.Module):
         return graph
 
     def _capture_steps(self, count: int) -> torch.cuda.CUDAGraph:
-        """`count` short steps in one HIP graph, each followed by a copy of its
-        token into multi_tokens[j] (a warm-up run on a side stream first)."""
+        """`count` short steps in one HIP graph, step j writing its token to
+        multi_tokens[j] as well (a warm-up run on a side stream first)."""
         def steps():
             for j in range(count):
-                self._step(True)
-                self.multi_tokens[j].copy_(self.token[0])
+                self._step(True, self.multi_tokens[j:j + 1])
 
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
@@ -533,10 +538,11 @@ class LlamaDecoder(torch.nn.Module):
     def capture(self, tokens_per_replay: int = 1) -> None:
         """Record the decode step in HIP graphs: the general one and, when the
         attention + o launch applies, the step for positions below 64; with
-        tokens_per_replay = T > 1 also T of those short steps in one graph,
-        which `replay_tokens` uses while the position stays below 64 (every
-        graph replay costs a fixed 12-16 us of GPU time, so T steps per replay
-        pay it once). The KV cache, position and the fused step's input row are
+        tokens_per_replay = T > 1 also graphs of T, T // 2, T // 4, .. (more
+        than one) of those short steps, which `replay_tokens` uses while the
+        position stays below 64, the largest that fits first (every graph
+        replay costs a fixed 12-16 us of GPU time: 31 tokens at T = 16 take 5
+        replays). The KV cache, position and the fused step's input row are
         restored afterwards (capturing runs steps)."""
         saved = (self.k_cache.clone(), self.v_cache.clone(), self.token.clone(), self.position.clone(),
                  self.x_buf.clone())
@@ -551,6 +557,7 @@ class LlamaDecoder(torch.nn.Module):
         self.graph = self._capture_step(False)
         restore()
         self.graph_multi = None
+        self.graphs_multi = {}
         if self.attn_o:
             # the warm-up step must see a position the short step accepts
             short_end = min(64, self.cfg.max_seq_len)
@@ -559,10 +566,14 @@ class LlamaDecoder(torch.nn.Module):
             restore()
             if tokens_per_replay > 1 and tokens_per_replay <= short_end:
                 self.multi_tokens = torch.zeros((tokens_per_replay,), dtype=torch.int64, device=self.position.device)
-                # the capture runs 2 T steps (warm-up and recording) from a position they all accept
-                self.position.fill_(max(0, min(self.host_position, short_end - tokens_per_replay)))
-                self.graph_multi = self._capture_steps(tokens_per_replay)
-                restore()
+                count = tokens_per_replay
+                while count > 1:
+                    # the capture runs 2 count steps (warm-up and recording) from a position they all accept
+                    self.position.fill_(max(0, min(self.host_position, short_end - count)))
+                    self.graphs_multi[count] = self._capture_steps(count)
+                    restore()
+                    count //= 2
+                self.graph_multi = self.graphs_multi[tokens_per_replay]
         torch.cuda.synchronize()
 
     def replay(self) -> None:
@@ -574,23 +585,22 @@ class LlamaDecoder(torch.nn.Module):
             self.graph.replay()
         self.host_position += 1
 
-    def multi_steps(self) -> int:
-        """Steps the multi-step graph would take now (0 when it does not apply:
-        not captured, or the position would pass 63 within it)."""
-        if self.graph_multi is None:
-            return 0
-        t = self.multi_tokens.numel()
-        return t if self.host_position + t <= min(64, self.cfg.max_seq_len) else 0
+    def multi_steps(self, limit: int | None = None) -> int:
+        """Steps of the largest multi-step graph that applies now: at most
+        `limit` steps and none past position 63 (0 when none does)."""
+        end = min(64, self.cfg.max_seq_len)
+        fits = [c for c in self.graphs_multi if self.host_position + c <= end and (limit is None or c <= limit)]
+        return max(fits, default=0)
 
     def replay_tokens(self, limit: int | None = None) -> torch.Tensor:
-        """Replay decode graphs for the next tokens: the multi-step graph when it
-        applies and at most `limit` tokens are wanted, else one step. Returns the
-        new tokens (int64 [n], on the device)."""
-        t = self.multi_steps()
-        if t and (limit is None or t <= limit):
-            self.graph_multi.replay()
+        """Replay decode graphs for the next tokens: the largest multi-step
+        graph that applies with at most `limit` tokens, else one step. Returns
+        the new tokens (int64 [n], on the device)."""
+        t = self.multi_steps(limit)
+        if t:
+            self.graphs_multi[t].replay()
             self.host_position += t
-            return self.multi_tokens.clone()
+            return self.multi_tokens[:t].clone()
         self.replay()
         return self.token.clone()
 

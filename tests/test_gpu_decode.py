@@ -698,6 +698,11 @@ def test_argmax_embed_gathers_next_row(gpu, hidden):
     _lib.argmax_embed_f16(logits.to(gpu), token, None, table, obuf[1:])
     torch.cuda.synchronize()
     assert torch.equal(obuf[1:], table[777]) and float(obuf[0]) == 0.0
+    # the token history slot: only that element is written
+    history = torch.full((4,), -1, dtype=torch.int64, device=gpu)
+    _lib.argmax_embed_f16(logits.to(gpu), token, position, table, out, token_copy=history[2:3])
+    torch.cuda.synchronize()
+    assert history.tolist() == [-1, -1, 777, -1] and int(token) == 777 and int(position) == 5
 
 
 def test_embedding_gather(gpu):
