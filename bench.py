@@ -459,6 +459,10 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
     prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=gen).to(device)
 
     def timed(fused: bool, per_replay: int = 1):
+        # as the reference's benchmark_prompt (scripts/generate.py:331-352):
+        # the prefill timed on its own runs back to back (its
+        # generate(max_new_tokens=1) samples), then the decode of the
+        # new_tokens - 1 further tokens after an untimed prefill
         model.fused = fused
         model.prefill(prompt)
         model.capture(tokens_per_replay=per_replay)
@@ -468,14 +472,16 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
             t0 = time.perf_counter()
             model.prefill(prompt)
             torch.cuda.synchronize()
+            prefill_s.append(time.perf_counter() - t0)
+        for _ in range(runs + 1):
+            model.prefill(prompt)
+            torch.cuda.synchronize()
             t1 = time.perf_counter()
             left = new_tokens - 1
             while left > 0:
                 left -= model.replay_tokens(limit=left).numel()
             torch.cuda.synchronize()
-            t2 = time.perf_counter()
-            prefill_s.append(t1 - t0)
-            decode_s.append(t2 - t1)
+            decode_s.append(time.perf_counter() - t1)
         decode_s, prefill_s = sorted(decode_s[1:]), sorted(prefill_s[1:])
         return decode_s[len(decode_s) // 2], prefill_s[len(prefill_s) // 2]
 
@@ -496,12 +502,15 @@ def decode_tok_s(device, runs: int = 5, new_tokens: int = 32, prompt_len: int = 
                 "tokens left) while the position allows, else one step per replay",
         "unfused_decode_tok_s": round((new_tokens - 1) / unfused_s, 1),
         "prefill_ms": round(prefill * 1e3, 3),
+        "prefill_timing": "host wall time of prefill() (the prompt copy, the graph replay, the token read-back) "
+                          "and a synchronize, median of back-to-back runs, as the reference times its "
+                          "generate(max_new_tokens=1) samples",
         "prefill_eager_ms": round(prefill_eager * 1e3, 3),
-        "prefill": "16-token prompt, one HIP graph: RMSNorm of the embeddings, then per layer W4A16 op for "
-                   "q|k|v (the W4A16 GEMM, M=16), rotary+KV append+causal attention (matrix cores), W4A16 op for "
-                   "o (GEMM), residual add+RMSNorm, gate|up with the SiLU*up epilogue (paired kernel, 16 row "
-                   "slots), W4A16 op for down (paired kernel, 16 row slots), residual add+next RMSNorm; then "
-                   "lm_head GEMV and argmax; "
+        "prefill": "16-token prompt, one HIP graph: the embeddings and their RMSNorm, then per layer the W4A16 op "
+                   "for q|k|v (the ring kernel's 16-row-slot form), rotary + KV append + causal attention inside "
+                   "the o projection's launch (8 K slices of 4 heads), the slices' sum + residual add + RMSNorm, "
+                   "gate|up with the SiLU*up epilogue, down (8 K slices), the slices' sum + residual add + next "
+                   "RMSNorm; then the lm_head GEMV on the last row and the argmax + next embedding; "
                    "prefill_eager_ms: the same prompt as eager torch ops around QuantizedLinear",
         "linear_layers": len(model.linear_layers()),
         "packed_weight_bytes_per_token": model.packed_bytes(),

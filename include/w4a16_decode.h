@@ -201,6 +201,21 @@ int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_
                            int64_t* token_copy, void* stream);
 
 /*
+ * x_out[r, :] = table[tokens[r], :] (fp16 [vocab, hidden]; zeros for a token
+ * outside [0, vocab)) and output[r, :] = RMSNorm(x_out[r, :]) * weight for
+ * r < rows, one launch: the prompt's embedding rows and the first layer's
+ * input RMSNorm (the arithmetic of w4a16_rmsnorm_f16, bit for bit); position
+ * (int64[1], may be NULL) <- rows, the decode position after the prompt.
+ * hidden a multiple of 8 up to 8192; table, weight, x_out and output 16-byte
+ * aligned; tokens int64 [rows].
+ * Replaces (reference): the prompt's embedding lookup and the first input
+ * RMSNorm of HF's Llama forward (scripts/generate.py:260-305).
+ */
+int w4a16_embed_rmsnorm_f16(const void* table, int64_t vocab, int64_t hidden, const int64_t* tokens,
+                            int64_t rows, const void* weight, float eps, void* x_out, void* output,
+                            int64_t* position, void* stream);
+
+/*
  * output[0..hidden) = table[*token, :] (fp16 [vocab, hidden]); a token
  * outside [0, vocab) gives zeros.
  * Replaces (reference): the embedding lookup of the decode step.

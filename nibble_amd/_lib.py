@@ -93,6 +93,8 @@ DECODE_SIGNATURES = {
     ),
     "w4a16_argmax_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "w4a16_argmax_embed_f16": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "w4a16_embed_rmsnorm_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _vp, _vp,
+                                               _vp]),
     "w4a16_embedding_f16": (ctypes.c_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "w4a16_rmsnorm_f16": (ctypes.c_int, [_vp, _vp, ctypes.c_float, _vp, _i64, _i64, _vp]),
     "w4a16_silu_mul_f16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
@@ -392,6 +394,15 @@ def argmax_embed_f16(logits, token, position, table, output, stream=None, token_
     _raise_on(lib().w4a16_argmax_embed_f16(logits.data_ptr(), logits.numel(), token.data_ptr(), _ptr(position),
                                            table.data_ptr(), vocab, hidden, output.data_ptr(), _ptr(token_copy),
                                            _stream_ptr(stream)))
+
+
+def embed_rmsnorm_f16(table, tokens, weight, eps: float, x_out, output, position=None, stream=None) -> None:
+    """``w4a16_embed_rmsnorm_f16``: x_out <- table[tokens] ([rows, hidden]);
+    output <- RMSNorm(x_out) * weight; position (int64[1]) <- rows when given."""
+    vocab, hidden = table.shape
+    _raise_on(lib().w4a16_embed_rmsnorm_f16(table.data_ptr(), vocab, hidden, tokens.data_ptr(), tokens.numel(),
+                                            weight.data_ptr(), float(eps), x_out.data_ptr(), output.data_ptr(),
+                                            _ptr(position), _stream_ptr(stream)))
 
 
 def embedding_f16(table, token, output, stream=None) -> None:

@@ -789,6 +789,65 @@ norm_rows_vec_kernel(const f16* x, const f16* __restrict__ delta, const f16* __r
     }
 }
 
+// A prompt's embedding rows and their RMSNorm in one launch (the vectorised
+// layout of norm_rows_vec_kernel): row r is table[tokens[r]] (zeros for a
+// token outside [0, vocab)), written to x_out[r] as the residual stream, and
+// out[r] = its RMSNorm with the arithmetic of norm_rows_vec_kernel<false>, so
+// both equal the gather followed by that kernel, bit for bit. position (may
+// be NULL) <- rows: the decode position after the prompt.
+__global__ void __launch_bounds__(256)
+embed_norm_rows_kernel(const f16* __restrict__ table, int64_t vocab, const int64_t* __restrict__ tokens,
+                       const f16* __restrict__ w, float eps, f16* __restrict__ x_out, f16* __restrict__ out,
+                       int hidden, int64_t* __restrict__ position) {
+    __shared__ float partial[4];
+    const int64_t t = tokens[blockIdx.x];
+    const bool in_range = t >= 0 && t < vocab;
+    const f16* src = table + (in_range ? t : 0) * (int64_t)hidden;
+    const size_t row = (size_t)blockIdx.x * hidden;
+    const int units = hidden >> 3;
+    u32x4 xv[kNormUnits], wv[kNormUnits];
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = min((int)threadIdx.x + 256 * u, units - 1);
+        xv[u] = in_range ? *reinterpret_cast<const u32x4*>(src + (size_t)i * 8) : (u32x4){0u, 0u, 0u, 0u};
+        wv[u] = *reinterpret_cast<const u32x4*>(w + (size_t)i * 8);
+    }
+    if (position != nullptr && blockIdx.x == 0 && threadIdx.x == 0) position[0] = (int64_t)gridDim.x;
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < units) {
+            *reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8) = xv[u];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 a = as_f16x2(xv[u][e]);
+                ss = __builtin_fmaf((float)a.x, (float)a.x, ss);
+                ss = __builtin_fmaf((float)a.y, (float)a.y, ss);
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
+    const float inv = 1.0f / __builtin_sqrtf(total / (float)hidden + eps);
+#pragma unroll
+    for (int u = 0; u < kNormUnits; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        if (i < units) {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const f16x2 a = as_f16x2(xv[u][e]), g = as_f16x2(wv[u][e]);
+                const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
+                o[e] = as_u32(y);
+            }
+            *reinterpret_cast<u32x4*>(out + row + (size_t)i * 8) = o;
+        }
+    }
+}
+
 // out[r, i] = fp16(fp16(silu(g)) * u), g = gate_up[r, i], u = gate_up[r, inter + i]:
 // the roundings of torch's silu(g) * u on fp16 tensors.
 __device__ __forceinline__ f16 silu_mul_one(f16 gh, f16 uh) {
@@ -1610,6 +1669,29 @@ int w4a16_rmsnorm_f16(const void* x, const void* weight, float eps, void* output
     hipLaunchKernelGGL(w4a16::rmsnorm_rows_kernel, dim3((unsigned)rows), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const f16*>(x), static_cast<const f16*>(weight),
                        eps, static_cast<f16*>(output), (int)hidden);
+    return check_launch();
+}
+
+int w4a16_embed_rmsnorm_f16(const void* table, int64_t vocab, int64_t hidden, const int64_t* tokens, int64_t rows,
+                            const void* weight, float eps, void* x_out, void* output, int64_t* position,
+                            void* stream) {
+    if (rows == 0) return W4A16_OK;
+    if (!table || !tokens || !weight || !x_out || !output)
+        return fail(W4A16_ERR_NULL, "embed + rmsnorm: table, tokens, weight, x_out and output must be non-NULL");
+    if (rows < 0 || rows > INT32_MAX || vocab <= 0)
+        return fail(W4A16_ERR_SHAPE, "embed + rmsnorm: rows must be non-negative and vocab positive");
+    if (hidden <= 0 || hidden % 8 != 0 || hidden > w4a16::kAddNormMax)
+        return fail(W4A16_ERR_SHAPE, "embed + rmsnorm: hidden must be a positive multiple of 8 up to 8192");
+    if (!(eps >= 0.0f)) return fail(W4A16_ERR_CONFIG, "embed + rmsnorm: eps must be non-negative");
+    if (!aligned(table, 16) || !aligned(weight, 16) || !aligned(x_out, 16) || !aligned(output, 16) ||
+        !aligned(tokens, 8) || (position != nullptr && !aligned(position, 8)))
+        return fail(W4A16_ERR_ALIGNMENT, "embed + rmsnorm: fp16 buffers must be 16-byte aligned, tokens and "
+                                         "position 8-byte aligned");
+    using w4a16::f16;
+    hipLaunchKernelGGL(w4a16::embed_norm_rows_kernel, dim3((unsigned)rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f16*>(table), vocab, tokens,
+                       static_cast<const f16*>(weight), eps, static_cast<f16*>(x_out), static_cast<f16*>(output),
+                       (int)hidden, position);
     return check_launch();
 }
 

@@ -348,17 +348,27 @@ class LlamaDecoder(torch.nn.Module):
         w4a16_linear_add_rmsnorm_f16 sums the op's K slices in the norm's
         launch); then the lm_head GEMV on the last normed row and the greedy
         argmax, which also gathers the first decode step's input row. 6
-        launches per layer at 9..16 tokens, 7 otherwise."""
+        launches per layer at 9..16 tokens, 7 otherwise. The embedding
+        gather, the first RMSNorm and the position after the prompt are one
+        launch (w4a16_embed_rmsnorm_f16)."""
         cfg = self.cfg
         t = prompt.numel()
         g = cfg.group_size
-        x = self.embed[prompt]
-        h = torch.empty_like(x)
+        first = self.layers[0].input_norm
+        one_launch = cfg.hidden_size % 8 == 0 and cfg.hidden_size <= 8192 and self.embed.is_contiguous()
+        if one_launch:
+            # the embedding rows, their RMSNorm and the position after the prompt in one launch
+            x = torch.empty((t, cfg.hidden_size), dtype=torch.float16, device=prompt.device)
+            h = torch.empty_like(x)
+            _lib.embed_rmsnorm_f16(self.embed, prompt.contiguous(), first.weight, first.eps, x, h,
+                                   position=self.position)
+        else:
+            x = self.embed[prompt]
+            h = torch.empty_like(x)
+            _lib.rmsnorm_f16(x, first.weight, first.eps, h)
         attn = (torch.empty((t, cfg.num_heads * cfg.head_dim), dtype=torch.float16, device=x.device)
                 if t > FUSED_PREFILL_NATIVE_MAX_ROWS else None)
         mlp = torch.empty((t, cfg.intermediate_size), dtype=torch.float16, device=x.device)
-        first = self.layers[0].input_norm
-        _lib.rmsnorm_f16(x, first.weight, first.eps, h)
         for i, b in enumerate(self.layers):
             qkv_w, qkv_s = self.qkv[i]
             gu_w, gu_s = self.gate_up[i]
@@ -388,7 +398,8 @@ class LlamaDecoder(torch.nn.Module):
                 _lib.add_rmsnorm_f16(x, d, nxt.weight, nxt.eps, x, h)
         _lib.gemv_fused_f16(h[-1], self.lm_head.packed_weights, self.lm_head.scales, self.logits)
         _lib.argmax_embed_f16(self.logits, self.token, None, self.embed, self.x_buf)
-        self.position.fill_(t)
+        if not one_launch:
+            self.position.fill_(t)
 
     def _prefill_linear(self, x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
         """A fused-prefill projection: the W4A16 op up to

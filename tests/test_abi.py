@@ -56,6 +56,13 @@ def test_decode_entry_points_validate_before_launch():
     assert lib.w4a16_argmax_f16(a, 0, a, 0, 0) == _lib.W4A16_ERR_SHAPE
     assert lib.w4a16_argmax_f16(0, 10, a, 0, 0) == _lib.W4A16_ERR_NULL
     assert lib.w4a16_embedding_f16(a, 0, 64, a, a, 0) == _lib.W4A16_ERR_SHAPE
+    # embedding rows + RMSNorm: rejects before any launch
+    assert lib.w4a16_embed_rmsnorm_f16(0, 10, 64, a, 2, a, 1e-5, a, a, 0, 0) == _lib.W4A16_ERR_NULL
+    assert lib.w4a16_embed_rmsnorm_f16(a, 10, 60, a, 2, a, 1e-5, a, a, 0, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_embed_rmsnorm_f16(a, 10, 16384, a, 2, a, 1e-5, a, a, 0, 0) == _lib.W4A16_ERR_SHAPE
+    assert lib.w4a16_embed_rmsnorm_f16(a, 10, 64, a, 2, a, -1.0, a, a, 0, 0) == _lib.W4A16_ERR_CONFIG
+    assert lib.w4a16_embed_rmsnorm_f16(a + 2, 10, 64, a, 2, a, 1e-5, a, a, 0, 0) == _lib.W4A16_ERR_ALIGNMENT
+    assert lib.w4a16_embed_rmsnorm_f16(a, 10, 64, a, 0, a, 1e-5, a, a, 0, 0) == _lib.W4A16_OK
     assert lib.w4a16_embedding_f16(a, 10, 64, 0, a, 0) == _lib.W4A16_ERR_NULL
     # residual add + RMSNorm: row length, NULL pointers, eps
     assert lib.w4a16_add_rmsnorm_f16(a, a, a, 1e-5, a, a, 4, 8193, 0) == _lib.W4A16_ERR_SHAPE

@@ -45,6 +45,41 @@ def test_rmsnorm_rows(gpu, rows, hidden):
     assert torch.all((got - ref).abs() <= ULP * ref.abs() + 2 ** -24), float((got - ref).abs().max())
 
 
+@pytest.mark.parametrize("rows,hidden", [(16, 2048), (1, 2048), (5, 8192), (3, 24)])
+def test_embed_rmsnorm_rows(gpu, rows, hidden):
+    """w4a16_embed_rmsnorm_f16: the gathered rows exactly, the norm bit-identical
+    to w4a16_rmsnorm_f16 on the gathered rows (and within one fp16 rounding of
+    float64), zeros for a token outside the table, position <- rows."""
+    vocab = 300
+    gen = torch.Generator().manual_seed(rows + hidden)
+    table = (2.0 * torch.randn((vocab, hidden), generator=gen)).to(torch.float16).to(gpu)
+    w = (1.0 + 0.5 * torch.randn((hidden,), generator=gen)).to(torch.float16).to(gpu)
+    tokens = torch.randint(0, vocab, (rows,), generator=gen)
+    if rows > 2:
+        tokens[1] = vocab + 5   # out of range: a zero row
+        tokens[2] = tokens[0]   # a repeated token
+    tokens = tokens.to(gpu)
+    eps = 1e-5
+    x = torch.full((rows, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    out = torch.full((rows, hidden), float("nan"), dtype=torch.float16, device=gpu)
+    position = torch.tensor([-7], dtype=torch.int64, device=gpu)
+    print(f"[case] embed + rmsnorm rows={rows} hidden={hidden}", flush=True)
+    _lib.embed_rmsnorm_f16(table, tokens, w, eps, x, out, position=position)
+    gathered = torch.zeros((rows, hidden), dtype=torch.float16, device=gpu)
+    ok = (tokens >= 0) & (tokens < vocab)
+    gathered[ok] = table[tokens[ok]]
+    ref = torch.empty_like(out)
+    _lib.rmsnorm_f16(gathered, w, eps, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(x, gathered)
+    assert torch.equal(out, ref)
+    assert int(position) == rows
+    gd = gathered.double().cpu()
+    exact = (gd * torch.rsqrt(gd.pow(2).mean(dim=-1, keepdim=True) + eps)) * w.double().cpu()
+    got = out.double().cpu()
+    assert torch.all((got - exact).abs() <= ULP * exact.abs() + 2 ** -24), float((got - exact).abs().max())
+
+
 @pytest.mark.parametrize("rows,hidden,alias", [(1, 2048, True), (64, 2048, True), (7, 5632, False), (3, 100, False),
                                               (2, 8192, True)])
 def test_add_rmsnorm_rows(gpu, rows, hidden, alias):
