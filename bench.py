@@ -566,7 +566,8 @@ def launch_times(device, prompt_len: int = 16) -> dict:
     mlp = torch.empty((prompt_len, cfg.intermediate_size), dtype=torch.float16, device=device)
     blk = model.layers
     prefill = {
-        "rmsnorm (embeddings, once)": lambda i: _lib.rmsnorm_f16(x, blk[0].input_norm.weight, 1e-5, h),
+        "embedding rows + RMSNorm + position (once)": lambda i: _lib.embed_rmsnorm_f16(
+            model.embed, model.prefill_tokens, blk[0].input_norm.weight, 1e-5, x, h),
         "q|k|v op": lambda i: _lib.linear_f16(h, model.qkv[i][0], model.qkv[i][1], qkv),
         "attention + o op, then slice sum + residual + RMSNorm (2 launches)":
             lambda i: _lib.prefill_attention_o_add_rmsnorm_f16(
