@@ -757,7 +757,7 @@ norm_rows_vec_kernel(const f16* x, const f16* __restrict__ delta, const f16* __r
                 const f16x2 sum = {(f16)((float)a.x + (float)b.x), (f16)((float)a.y + (float)b.y)};
                 xv[u][e] = as_u32(sum);
             }
-            if (i < units) *reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8) = xv[u];
+            if (i < units) store_through(reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8), xv[u]);
         }
         if (i < units) {
 #pragma unroll
@@ -784,7 +784,7 @@ norm_rows_vec_kernel(const f16* x, const f16* __restrict__ delta, const f16* __r
                 const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
                 o[e] = as_u32(y);
             }
-            *reinterpret_cast<u32x4*>(out + row + (size_t)i * 8) = o;
+            store_through(reinterpret_cast<u32x4*>(out + row + (size_t)i * 8), o);
         }
     }
 }
@@ -818,7 +818,7 @@ embed_norm_rows_kernel(const f16* __restrict__ table, int64_t vocab, const int64
     for (int u = 0; u < kNormUnits; ++u) {
         const int i = threadIdx.x + 256 * u;
         if (i < units) {
-            *reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8) = xv[u];
+            store_through(reinterpret_cast<u32x4*>(x_out + row + (size_t)i * 8), xv[u]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const f16x2 a = as_f16x2(xv[u][e]);
@@ -843,7 +843,7 @@ embed_norm_rows_kernel(const f16* __restrict__ table, int64_t vocab, const int64
                 const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
                 o[e] = as_u32(y);
             }
-            *reinterpret_cast<u32x4*>(out + row + (size_t)i * 8) = o;
+            store_through(reinterpret_cast<u32x4*>(out + row + (size_t)i * 8), o);
         }
     }
 }
@@ -1408,7 +1408,7 @@ split_add_rmsnorm_kernel(const float* __restrict__ part, const f16* x, const f16
         sv[e] = as_u32(sum);
     }
     if ((int)threadIdx.x < units) {
-        *reinterpret_cast<u32x4*>(x_out + row + (size_t)threadIdx.x * 8) = sv;
+        store_through(reinterpret_cast<u32x4*>(x_out + row + (size_t)threadIdx.x * 8), sv);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const f16x2 a = as_f16x2(sv[e]);
@@ -1429,7 +1429,7 @@ split_add_rmsnorm_kernel(const float* __restrict__ part, const f16* x, const f16
             const f16x2 y = {(f16)(((float)a.x * inv) * (float)g.x), (f16)(((float)a.y * inv) * (float)g.y)};
             o[e] = as_u32(y);
         }
-        *reinterpret_cast<u32x4*>(out + row + (size_t)threadIdx.x * 8) = o;
+        store_through(reinterpret_cast<u32x4*>(out + row + (size_t)threadIdx.x * 8), o);
     }
 }
 

@@ -17,6 +17,37 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
+// Stores of results a later launch reads, written through to memory:
+// system-scope stores (vector stores with the sc0 sc1 bits), which the L2
+// does not keep dirty, so the release at the end of the launch has none of
+// them left to write back. 16-byte values go out as two 8-byte stores (there
+// is no 16-byte atomic store). Used where a wavefront stores contiguous runs
+// (the ring kernel's 8-row outputs, whole normalised rows); where one lane
+// of each wavefront stores two scattered fp16 values (the one-shot GEMV's
+// q|k|v + rotary + KV append, attention + o's residual rows), ordinary stores
+// measured faster: each scattered write-through store is its own partial-line
+// write, which the L2 otherwise merges (decode 2779 tok/s with them plain,
+// 2662 / 2669 with either written through, 2563 with both).
+__device__ __forceinline__ void store_through(f16* p, f16 v) {
+    __hip_atomic_store(reinterpret_cast<short*>(p), __builtin_bit_cast(short, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_through(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_through(int64_t* p, int64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_through(uint2* p, uint2 v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(p), (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_through(u32x4* p, u32x4 v) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // v_perm_b32: byte i of the result is byte sel[i] of the 8-byte value {hi:lo}
 // (selector 0-3 = lo bytes, 4-7 = hi bytes, 0x0c = zero byte).
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {

@@ -79,23 +79,14 @@ __host__ __device__ constexpr int64_t pair_ring_lds_bytes(int MS, int SK, int SN
            + (MS == 1 ? (int64_t)SK * SN * 4 : 0);                                           // RMSNorm partials
 }
 
-// Stores of results the next launch reads, written through to memory
-// (system-scope stores, which the L2 does not keep dirty): the release at the
-// end of the launch then has none of them left to write back. Graph timing at
-// M = 1: 2048 x 5632 3.21-3.28 -> 3.16-3.18 us, 5632 x 2048 3.17 -> 3.14,
-// 4096 x 14336 6.44-6.48 -> 6.43-6.44 (non-temporal stores instead: +0.5 us
-// on the first two). Used for the fp16 outputs of every form and for the fp32
-// K-slice partial sums of the 16-row-slot forms (5632 x 2048 at M = 16, 8
-// slices: 7.34 -> 7.14 us); the partial sums at M <= 8 keep ordinary stores
-// (28672 x 8192 at M = 8, 2 MB of partials beside the weight stream: 24.95
-// against 25.9 us written through).
-__device__ __forceinline__ void store_through(f16* p, f16 v) {
-    __hip_atomic_store(reinterpret_cast<short*>(p), __builtin_bit_cast(short, v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ void store_through(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
+// The outputs of every form, and the fp32 K-slice partial sums of the
+// 16-row-slot forms, go out through store_through (w4a16_device.h). Graph
+// timing at M = 1: 2048 x 5632 3.21-3.28 -> 3.16-3.18 us, 5632 x 2048 3.17 ->
+// 3.14, 4096 x 14336 6.44-6.48 -> 6.43-6.44 (non-temporal stores instead: +0.5
+// us on the first two); 5632 x 2048 at M = 16 with 8 K slices 7.34 -> 7.14.
+// The partial sums at M <= 8 keep ordinary stores (28672 x 8192 at M = 8, 2 MB
+// of partials beside the weight stream: 24.95 against 25.9 us written
+// through).
 
 // LDS of the ATTN prologue beyond the GEMV's: the slice's attention output
 // in natural order [16 rows][256] fp16, then one V tile [32 slots][72] fp16
