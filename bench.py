@@ -75,13 +75,13 @@ TOKENS_PER_REPLAY = 16
 # from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over `bench.py --counter-pass`,
 # each scaled by the counter's reading on a kernel of known traffic (FETCH_SIZE
 # reads half the bytes on this part, WRITE_SIZE is exact).
-MEASURED_TRAFFIC_BYTES = 6130746
+MEASURED_TRAFFIC_BYTES = 6141114
 TRAFFIC_SOURCE = "profiles/gemv_pair_ring_m1_mlp_traffic.md"
 # Mean kernel duration of the same two kernels in a rocprofv3 kernel trace of
 # `bench.py --headline-pass` (the headline sequence alone), per launch: the
 # profiler's timestamps run above the event-timed launches, so the line
 # reports both.
-TRACE_US_PER_LAUNCH = 3.407
+TRACE_US_PER_LAUNCH = 3.481
 TRACE_SOURCE = "profiles/gemv_pair_ring_m1_mlp_kernel_trace.md"
 
 
