@@ -570,9 +570,12 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   4.25 against 4.70; 4096 x 4096 (2, 2, 4) 4.17 against 4.71. M = 2: 4096
 //   x 14336 7.03 against 9.66; 8192 x 8192 7.99 against 10.03; 14336 x 4096
 //   8.52 against 9.17.
-// Kept on their kernels: M = 2 and 5..8 on 5632 x 2048 (tied: 3.90 / 5.45
-// against 3.88 / 5.40; every CU stages all M K activations for one 8-row
-// block), M = 5..8 on rows longer than 8192 (M K activations past LDS) and
+// M = 6..8 on 5632 x 2048 (22 pairs): 11 wavefronts of 2 pairs each (more
+// wavefronts requesting the 90 KB of staging at once) 5.05-5.10 us at M = 8
+// against 5.22 on the paired kernel, 4.88-4.93 against 4.95 at M = 6 (the
+// 8-wavefront ring shape 5.44 at M = 8, 16 wavefronts 5.83). Kept on their
+// kernels: M = 2 and 5 on 5632 x 2048 (tied: 3.90 / 5.45 against 3.88 /
+// 5.40; every CU stages all M K activations for one 8-row block), M = 5..8 on rows longer than 8192 (M K activations past LDS) and
 // M >= 2 on wider layers of long rows (N > 8192 with K >= 8192). Only
 // instantiated shapes are taken (K a multiple of 256 whose pairs per
 // wavefront match).
@@ -638,6 +641,7 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
             else if (N >= 4096) c[0] = wide ? Shape{4, 2, 4} : Shape{2, 2, 4};
         } else if (P <= 24) {
             if (M >= 3 && M <= 4 && N >= 2048 && N <= 4096) c[0] = {8, 1, 3};
+            else if (M >= 6 && N >= 1024 && N <= 2048) c[0] = {11, 1, 2};
         } else if (P <= 32) {
             if (N >= 6144 && N <= 8192) c[0] = {2, 4, 4};
             else if (workspace && wide && P == 32 && N >= 16384) c[0] = {1, 8, 3, 2};

@@ -35,7 +35,8 @@ VARIANTS = [(sk, sn, d, k) for sk, sn, d, ks in SHAPES for k in ks]
 # M = 2..4 (4 row slots) and M = 5..8 (8 row slots)
 SHAPES4 = [(4, 1, 2, (2048, 1792)), (1, 4, 6, (2048,)), (2, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)),
            (8, 1, 3, (5632, 6144)), (2, 4, 4, (8192,)), (4, 2, 6, (14336, 14080))]
-SHAPES8 = [(4, 1, 2, (2048,)), (1, 4, 6, (2048,)), (4, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)), (2, 4, 4, (8192, 7936))]
+SHAPES8 = [(4, 1, 2, (2048,)), (1, 4, 6, (2048,)), (4, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)), (2, 4, 4, (8192, 7936)),
+           (11, 1, 2, (5632, 5376))]   # 5376: 21 pairs, the last wavefront one short
 SMALL = ([(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES4 for k in ks for m in (2, 3, 4)] +
          [(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES8 for k in ks for m in (5, 8)])
 
@@ -112,7 +113,7 @@ def test_pair_ring_m1_default_route_full_size(gpu, k, n):
 @pytest.mark.parametrize("m,k,n", [(2, 2048, 2048), (4, 2048, 5632), (8, 2048, 5632), (8, 2048, 2048),
                                    (2, 4096, 4096), (8, 4096, 4096), (2, 4096, 14336), (4, 4096, 14336),
                                    (8, 4096, 14336), (4, 8192, 8192), (8, 8192, 8192), (2, 14336, 4096),
-                                   (4, 14336, 4096), (4, 5632, 2048)])
+                                   (4, 14336, 4096), (4, 5632, 2048), (6, 5632, 2048), (8, 5632, 2048)])
 def test_pair_ring_default_route_small_batch_full_size(gpu, m, k, n):
     x, p, s = make_case(m, k, n, seed=m + k ^ (5 * n), device="cuda")
     assert _lib.plan_linear(16, 16, m, n, k)["kernel"] == "pair_ring"

@@ -269,7 +269,7 @@ def test_mfma_pair_chunked(gpu, m, splits, blocks, k):
     assert_parity(out, expected(x, p, s), f"mfma_pair chunked M={m} splits={splits} blocks={blocks} K={k}")
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 2048, 9000), (5, 4352, 4096), (7, 5632, 2048), (8, 8192, 1000),
+@pytest.mark.parametrize("m,k,n", [(3, 2048, 9000), (5, 4352, 4096), (5, 5632, 2048), (7, 5632, 2560), (8, 8192, 1000),
                                    (4, 14336, 300), (6, 14336, 300), (8, 28672, 64), (3, 20480, 100),
                                    (5, 8320, 77),
                                    # M = 9..16 with the selector: one launch with 16 row slots, or two
