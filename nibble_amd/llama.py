@@ -325,11 +325,13 @@ class LlamaDecoder(torch.nn.Module):
         return self.fused and self.fuse_prefill and 1 <= tokens <= limit
 
     def _prefill(self, prompt: torch.Tensor, positions: torch.Tensor) -> None:
-        self.k_cache.zero_()
-        self.v_cache.zero_()
         if self.fused_prefill(prompt.numel()):
+            # no cache reset: every fused attention kernel selects away the
+            # slots past the position it attends to, whatever they hold
             self._prefill_fused(prompt)
             return
+        self.k_cache.zero_()
+        self.v_cache.zero_()
         logits = self._forward(prompt, positions)
         self.token.copy_(torch.argmax(logits).view(1))
         self.position.fill_(prompt.numel())
@@ -423,8 +425,9 @@ class LlamaDecoder(torch.nn.Module):
     @torch.inference_mode()
     def capture_prefill(self, prompt_len: int) -> None:
         """Record prefill of a prompt_len-token prompt in a HIP graph (the
-        prompt is copied into a static buffer before each replay). Resets the
-        KV cache, token and position like a prefill does."""
+        prompt is copied into a static buffer before each replay). Sets the
+        token and position like a prefill does; the torch-op prefill also
+        resets the KV caches."""
         device = self.token.device
         # Every tensor the graph reads must outlive it: the token and position
         # buffers are attributes (a local allocated before the capture would be

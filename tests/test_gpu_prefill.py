@@ -382,6 +382,40 @@ def test_fused_prefill_matches_torch_prefill(gpu, tokens):
     assert torch.equal(model.logits, logits_eager) and torch.equal(model.k_cache, k_eager)
 
 
+@pytest.mark.parametrize("tokens", [16, 33, 70])
+def test_fused_prefill_ignores_stale_cache_slots(gpu, tokens):
+    """The fused prefill does not reset the KV caches: slots past the prompt
+    keep what they held, and every fused attention kernel (the prompt's, the
+    short step's attention + o launch, the split attention past 64) selects
+    them away. With NaN in every slot beforehand, the greedy tokens of the
+    prefill and 6 decode steps and the caches' prompt slots equal those of a
+    run on zeroed caches, eager and with the prefill graph."""
+    from dataclasses import replace
+
+    from nibble_amd.llama import LlamaDecoder
+
+    model = LlamaDecoder(replace(_small_cfg(), max_seq_len=tokens + 8), device=gpu, seed=5)
+    prompt = torch.randint(0, 512, (tokens,), generator=torch.Generator().manual_seed(tokens + 1)).to(gpu)
+    assert model.fused_prefill(tokens)
+    print(f"[case] stale cache slots, {tokens}-token prompt", flush=True)
+    with torch.inference_mode():
+        model.k_cache.zero_(); model.v_cache.zero_()
+    ref = model.generate(prompt, 7, use_graph=False)
+    k_ref, v_ref = model.k_cache[:, :, :tokens].clone(), model.v_cache[:, :, :tokens].clone()
+    assert not bool(torch.isnan(model.logits).any())
+    for graphed in (False, True):
+        with torch.inference_mode():
+            model.k_cache.fill_(float("nan")); model.v_cache.fill_(float("nan"))
+        if graphed:
+            model.capture_prefill(tokens)
+            with torch.inference_mode():
+                model.k_cache.fill_(float("nan")); model.v_cache.fill_(float("nan"))
+        got = model.generate(prompt, 7, use_graph=False)
+        assert torch.equal(got, ref), (graphed, got.tolist(), ref.tolist())
+        assert torch.equal(model.k_cache[:, :, :tokens], k_ref) and torch.equal(model.v_cache[:, :, :tokens], v_ref)
+        assert bool(torch.isnan(model.k_cache[:, :, tokens + 6:]).all())
+
+
 # (query heads, KV heads, tokens, start, hidden): 9..16 tokens at slots up to
 # 31 with K = 2048 and a power-of-two group take the attention inside the o
 # op's launch (configs[4]'s prompt first; slots below start from the caches;
