@@ -207,7 +207,8 @@ int w4a16_argmax_embed_f16(const void* logits, int64_t n, int64_t* token, int64_
  * input RMSNorm (the arithmetic of w4a16_rmsnorm_f16, bit for bit); position
  * (int64[1], may be NULL) <- rows, the decode position after the prompt.
  * hidden a multiple of 8 up to 8192; table, weight, x_out and output 16-byte
- * aligned; tokens int64 [rows].
+ * aligned; tokens int64 [rows]. rows = 0 launches nothing (the position is
+ * left as it was).
  * Replaces (reference): the prompt's embedding lookup and the first input
  * RMSNorm of HF's Llama forward (scripts/generate.py:260-305).
  */

@@ -261,15 +261,18 @@ decode_attention_merge(const float* __restrict__ partial, const int64_t* __restr
 
 // ---------------------------------------------------------------------------
 // Greedy argmax over fp16 logits (first index of the maximum, as
-// torch.argmax; NaN logits are skipped), one workgroup of 1024 threads
+// torch.argmax: any NaN counts as the largest value, so the first NaN wins,
+// and -0 equals +0), one workgroup of 1024 threads
 // reading 16-byte vectors when the logits are 16-byte aligned; writes the
 // token (and, when given, the same to token_copy, a slot of a token
 // history) and, when given, advances the position by one and gathers the
 // token's embedding row into `emb_out` (the next decode step's input), so the
-// step needs no separate gather. Two passes: the maximum (packed fp16 max
-// over each thread's vectors, then the workgroup), and the first index that
-// holds it, searched only by the threads whose own maximum it is (from the
-// registers of the first round, re-read past it). The position is read at
+// step needs no separate gather. Two passes: the maximum (IEEE 754-2019
+// maximum, which propagates NaN: v_pk_maximum3_f16 over each thread's
+// vectors, v_maximum3_f32 across the workgroup), and the first index that
+// holds it (the first NaN when the maximum is NaN), searched only by the
+// threads whose own maximum it is (from the registers of the first round,
+// re-read past it). The position is read at
 // launch and the last steps (the winners' reduction, the token, the gather)
 // run in wavefront 0 alone.
 // ---------------------------------------------------------------------------
@@ -296,22 +299,41 @@ argmax_kernel(const f16* __restrict__ logits, int n, int64_t* __restrict__ token
         for (int b = 0; b < kBatch; ++b)
             if (j0 + b * T < nv)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) m2 = __builtin_elementwise_max(m2, as_f16x2(u[b][e]));
+                for (int e = 0; e < 4; ++e) m2 = __builtin_elementwise_maximum(m2, as_f16x2(u[b][e]));
     }
-    for (int i = 8 * nv + tid; i < n; i += T) m2.x = __builtin_elementwise_max(m2.x, logits[i]);
-    const float mine = fmaxf((float)m2.x, (float)m2.y);
+    for (int i = 8 * nv + tid; i < n; i += T) m2.x = __builtin_elementwise_maximum(m2.x, logits[i]);
+    const float mine = __builtin_elementwise_maximum((float)m2.x, (float)m2.y);
     float gm = mine;
-    for (int off = 32; off >= 1; off >>= 1) gm = fmaxf(gm, __shfl_xor(gm, off));
+    for (int off = 32; off >= 1; off >>= 1) gm = __builtin_elementwise_maximum(gm, __shfl_xor(gm, off));
     if (lane == 0) wave_max[wave] = gm;
     __syncthreads();
 #pragma unroll
-    for (int w = 0; w < T / 64; ++w) gm = fmaxf(gm, wave_max[w]);
+    for (int w = 0; w < T / 64; ++w) gm = __builtin_elementwise_maximum(gm, wave_max[w]);
+    const bool any_nan = gm != gm;
 
-    // the first index holding gm among this thread's elements, in index order
-    // (rounds, vectors of a round, elements of a vector, then the tail);
-    // gm = -inf (every logit -inf or NaN) gives token 0
+    // the first index holding the target among this thread's elements, in
+    // index order (rounds, vectors of a round, elements of a vector, then the
+    // tail): gm, or the first NaN when any logit is one (a compact loop of its
+    // own, re-reading the thread's logits: the common path keeps its code
+    // size); every logit -inf gives token 0
     int first = n;
-    if (mine == gm && gm != -__builtin_inff()) {
+    if (__builtin_expect(any_nan, false)) {
+        if (mine != mine) {
+#pragma unroll 1
+            for (int j = tid; j < nv && first == n; j += T) {
+                const u32x4 v = reinterpret_cast<const u32x4*>(logits)[j];
+#pragma unroll 1
+                for (int e = 0; e < 8; ++e)
+                    if (((v[e >> 1] >> (16 * (e & 1))) & 0x7fffu) > 0x7c00u) {
+                        first = 8 * j + e;
+                        break;
+                    }
+            }
+#pragma unroll 1
+            for (int i = 8 * nv + tid; i < n && first == n; i += T)
+                if ((__builtin_bit_cast(uint16_t, logits[i]) & 0x7fffu) > 0x7c00u) first = i;
+        }
+    } else if (mine == gm && gm != -__builtin_inff()) {
         const bool one_round = nv <= kBatch * T;
         for (int j0 = tid; j0 < nv; j0 += kBatch * T) {
             if (!one_round)

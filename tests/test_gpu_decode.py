@@ -638,24 +638,30 @@ def test_argmax_first_maximum_and_position(gpu, n):
 
 def test_argmax_special_values(gpu):
     """The first maximum past the first round of vectors (n > 32768), in the
-    scalar tail, on misaligned logits; NaN logits are skipped; all -inf
-    gives token 0 (torch.argmax's answer there)."""
+    scalar tail, on misaligned logits; any NaN counts as the largest value
+    (the first NaN wins, in the vectors or the scalar tail, whatever its
+    sign), -0 equals +0, all -inf gives token 0: each answer is torch.argmax's
+    on the same logits."""
     token = torch.zeros((1,), dtype=torch.int64, device=gpu)
 
     def run(lg):
         _lib.argmax_f16(lg, token)
         torch.cuda.synchronize()
-        return int(token)
+        got = int(token)
+        assert got == int(torch.argmax(lg.float().cpu())), (got, int(torch.argmax(lg.float().cpu())))
+        return got
 
     gen = torch.Generator().manual_seed(5)
     lg = torch.randn((40000,), generator=gen).to(torch.float16)
     lg[39000] = 9.0
     lg[39001] = 9.0
-    lg[100] = float("nan")
-    lg[33000] = float("nan")
     assert run(lg.to(gpu)) == 39000
     lg[12345] = 9.0                       # the same maximum in the first round wins
     assert run(lg.to(gpu)) == 12345
+    lg[33000] = float("nan")              # a NaN beats every number
+    assert run(lg.to(gpu)) == 33000
+    lg[100] = -float("nan")               # the first NaN wins, whatever its sign
+    assert run(lg.to(gpu)) == 100
     tail = torch.zeros((33,), dtype=torch.float16)
     tail[32] = 5.0                        # index 32 is past the 4 vectors
     assert run(tail.to(gpu)) == 32
@@ -664,11 +670,20 @@ def test_argmax_special_values(gpu):
     buf = torch.zeros((34,), dtype=torch.float16, device=gpu)
     buf[1:] = tail.to(gpu)
     assert run(buf[1:]) == 7              # misaligned: every element on the scalar path
+    buf[30] = float("nan")
+    assert run(buf[1:]) == 29             # a NaN on the scalar path
+    tail[32] = float("nan")
+    tail[7] = 5.0
+    assert run(tail.to(gpu)) == 32        # a NaN in the vectors' scalar tail
+    zeros = torch.zeros((100,), dtype=torch.float16)
+    zeros[:50] = -0.0
+    assert run(zeros.to(gpu)) == 0        # -0 equals +0: the first index
     assert run(torch.full((1000,), float("-inf"), dtype=torch.float16, device=gpu)) == 0
     neg = torch.full((1000,), float("-inf"), dtype=torch.float16)
     neg[600] = -60000.0
-    neg[10] = float("nan")
     assert run(neg.to(gpu)) == 600
+    neg[10] = float("nan")
+    assert run(neg.to(gpu)) == 10
 
 
 @pytest.mark.parametrize("hidden", [2048, 8200, 4100, 24])
