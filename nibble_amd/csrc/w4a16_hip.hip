@@ -1790,10 +1790,10 @@ int w4a16_gemv_qkv_rope_f16(const void* activations, const void* norm_weight, fl
 }
 
 // Launch shape of the ring kernel's SiLU form at K = 2048 (wavefronts
-// splitting K, wavefronts on output blocks, pairs in flight): at M = 16,
-// 2048 x 2 x 5632, 7.78 us against 8.72 on (2, 2, 4) and 10.1 on the
-// 16-row-slot paired kernel's SiLU form.
-constexpr int kRingSiluShape[3] = {1, 4, 4};
+// splitting K, wavefronts on output blocks, pairs in flight): at M = 16 / 9,
+// 2048 x 2 x 5632, 7.35-7.47 / 7.11-7.20 us against 8.20-8.50 / 7.93-7.98 on
+// (1, 4, 4) and 10.1 (M = 16) on the 16-row-slot paired kernel's SiLU form.
+constexpr int kRingSiluShape[3] = {4, 3, 1};
 
 int w4a16_linear_silu_f16(const void* activations, const uint8_t* packed_weights, const void* scales, void* output,
                           int64_t M, int64_t inter, int64_t K, int64_t group_size, void* stream) {

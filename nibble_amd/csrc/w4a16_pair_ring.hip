@@ -95,14 +95,19 @@ SplitPick pick_split(int ms, int sk, int sn, int ppw, int depth) {
 
 // SiLU form (16 row slots, a gate and an up block per wavefront):
 // (wavefronts splitting K, wavefronts on output blocks, pairs per
-// wavefront, pairs in flight). Measured at M = 16 / 9, 2048 x 2 x 5632
-// (graph timing): (1, 4, 8, 4) 7.78 / 7.51 us, (4, 2, 2, 2) 8.26 / 7.61,
-// (2, 4, 4, 4) 8.41 / 7.99, (2, 2, 4, 4) 8.73 / 8.30, (8, 1, 1, 1) 9.57 /
-// 8.64, (1, 8, 8, 4) 10.09 / 9.70.
+// wavefront, pairs in flight). Measured at M = 16 / 9, 2048 x 2 x 5632,
+// graph timing of 22 calls over 24 weight copies (one box, two passes):
+// (4, 3, 2, 1) 7.35-7.47 / 7.11-7.20 us; (4, 3, 2, 2) 7.75-7.88 / 7.40;
+// (2, 3, 4, 2) 7.82-8.03 / 7.50-7.57; (2, 4, 4, 2) 7.88 / 7.57; (3, 3, 3, 1)
+// 8.07-8.19 / 7.77; (1, 4, 8, 4) 8.20-8.50 / 7.93-7.98; (4, 4, 2, 1) 8.45 /
+// 8.24-8.37; (1, 3, 8, 4) 8.66-8.73 / 8.16-8.19; (4, 2, 2, 1) 8.74 / 8.27;
+// (2, 2, 4, 2) 8.96 / 8.53; (3, 5, 3, 1) 11.1 / 10.8. Three wavefronts on
+// output blocks give 235 workgroups (one per CU; four give 176), and four
+// on K give each CU 12 wavefronts requesting its 64 KB of activations.
 Kern pick_silu(int sk, int sn, int ppw, int depth) {
 #define W4A16_P(SK, SN, PPW, D) \
     if (sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<16, SK, SN, 2, PPW, D, false, true>;
-    W4A16_P(1, 4, 8, 4)   // K = 2048
+    W4A16_P(4, 3, 2, 1)   // K = 2048
 #undef W4A16_P
     return nullptr;
 }

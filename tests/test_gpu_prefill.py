@@ -170,11 +170,12 @@ def test_linear_silu(gpu, m, k, inter, monkeypatch):
         # same sums
         # M = 9..16 on rows of 2048 weights of wide layers: the paired ring
         # kernel's SiLU form, whose sibling is its plain 16-slot form with
-        # the same K split (one wavefront, all 8 pairs) over the 2 inter rows
+        # the same K split (four wavefronts of 2 pairs each, their sums added
+        # in order) over the 2 inter rows
         ring16 = 9 <= m <= 16 and k == 2048 and 2 * inter >= 8192
         silu16 = 9 <= m <= 16 and (k > 4096 or (k <= 2048 and 2 * inter >= 8192))
         if ring16:
-            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_PAIR_RING, 4, 1, 4)
+            _lib.linear_f16_tuned(xd, pd, sd, gu, 128, _lib.KERNEL_PAIR_RING, 2, 4, 2)
             ref16 = torch.empty_like(out)
             _lib.silu_mul_f16(gu, ref16)
         elif silu16:
