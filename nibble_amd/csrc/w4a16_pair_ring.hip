@@ -205,8 +205,13 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
 // 1.1B model): gate|up 2048 x 2 x 5632 with RMSNorm (1, 3, 8 pairs, 4 in
 // flight, 2 blocks per wavefront) 4.13 against 4.85 us; down 5632 x 2048
 // with the residual (8 wavefronts on K, 3 pairs each) 3.31 against 3.45;
-// lm_head 2048 x 32000 with RMSNorm (1, 8, 8 pairs all in flight) 7.08
-// against 8.18. Returns W4A16_ERR_CONFIG for other shapes.
+// lm_head 2048 x 32000 with RMSNorm (1, 4, 8 pairs all in flight) 7.70
+// against 7.92-8.17 on (1, 8, 8) and 8.18 on the one-shot form (12 rotated
+// weight copies). Other shapes measured with 22-call graphs over 24 copies
+// (wavefronts on K, on blocks, pairs, in flight): gate|up (2, 3, 4, 4)
+// 4.80-4.86 and (4, 3, 2, 1) 5.22-5.26 against 4.46-4.52; down (4, 1, 6, 6)
+// 3.67 and (11, 1, 2, 1) 3.75 against 3.56-3.58; lm_head (2, 4, 4, 4)
+// 8.17-8.64. Returns W4A16_ERR_CONFIG for other shapes.
 int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusion& fz, const uint8_t* w,
                            const w4a16::f16* s, w4a16::f16* o, int N, int K, hipStream_t stream) {
     using namespace w4a16;
@@ -220,8 +225,8 @@ int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusio
         kern = gemv_pair_ring<1, 8, 1, 1, 3, 3, false, false, false, true>;
         sk = 8, sn = 1, rb = 1, ppw = 3;
     } else if (kind == 2 && K == 2048 && fz.norm_weight != nullptr) {
-        kern = gemv_pair_ring<1, 1, 8, 1, 8, 8, false, false, true>;
-        sk = 1, sn = 8, rb = 1, ppw = 8;
+        kern = gemv_pair_ring<1, 1, 4, 1, 8, 8, false, false, true>;
+        sk = 1, sn = 4, rb = 1, ppw = 8;
     }
     if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "fused ring GEMV: shape not instantiated");
     const int64_t lds = pair_ring_lds_bytes(1, sk, sn, rb, ppw);
