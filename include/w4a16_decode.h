@@ -178,8 +178,10 @@ int w4a16_attention_o_cached_f16(const void* qkv, const void* k_cache, const voi
                                  int64_t hidden, int64_t group_size, void* stream);
 
 /*
- * Greedy token: *token = first index of the maximum of logits[0..n) (fp16);
- * if position != NULL, *position += 1.
+ * Greedy token: *token = first index of the maximum of logits[0..n) (fp16),
+ * with torch.argmax's special values: any NaN counts as the largest value
+ * (the first NaN wins), -0 equals +0, all -inf gives 0; if position != NULL,
+ * *position += 1.
  * Replaces (reference): the greedy pick of HF generate(do_sample=False),
  * scripts/generate.py:286-293.
  */
