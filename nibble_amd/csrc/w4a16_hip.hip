@@ -1115,7 +1115,9 @@ int launch_fused_t(int L, int R, int W, const w4a16::f16* x, const w4a16::GemvFu
 #define W4A16_PICK(RR, WW)                                                                               \
     W4A16_PICK_L(RR, 1, WW) W4A16_PICK_L(RR, 2, WW) W4A16_PICK_L(RR, 3, WW) W4A16_PICK_L(RR, 4, WW)   \
     W4A16_PICK_L(RR, 5, WW) W4A16_PICK_L(RR, 6, WW) W4A16_PICK_L(RR, 7, WW) W4A16_PICK_L(RR, 8, WW)
-    if constexpr (PAIRED || ROPE) {
+    if constexpr (ROPE) {
+        W4A16_PICK(2, 6)
+    } else if constexpr (PAIRED) {
         W4A16_PICK(2, 8)
     } else {
         W4A16_PICK(1, 8) W4A16_PICK(2, 8) W4A16_PICK(4, 4)
@@ -1785,8 +1787,12 @@ int w4a16_gemv_qkv_rope_f16(const void* activations, const void* norm_weight, fl
     f16* o = static_cast<f16*>(qkv);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int L = oneshot_loads(K);
-    return norm_weight ? launch_fused_t<true, false, false, true>(L, 2, 8, x, fz, packed_weights, sc, o, N, (int)K, st)
-                       : launch_fused_t<false, false, false, true>(L, 2, 8, x, fz, packed_weights, sc, o, N, (int)K, st);
+    // 6 wavefronts (row pairs) per workgroup: 1.1B model's q|k|v (2048 x
+    // 2560, 214 workgroups) 3.44-3.45 us against 3.49-3.51 on 8 (160
+    // workgroups), 3.48 on 5 (256), 3.90 on 4 (graph timing over 24 weight
+    // copies; the same outputs bit for bit)
+    return norm_weight ? launch_fused_t<true, false, false, true>(L, 2, 6, x, fz, packed_weights, sc, o, N, (int)K, st)
+                       : launch_fused_t<false, false, false, true>(L, 2, 6, x, fz, packed_weights, sc, o, N, (int)K, st);
 }
 
 // Launch shape of the ring kernel's SiLU form at K = 2048 (wavefronts
