@@ -404,16 +404,20 @@ embedding_kernel(const f16* __restrict__ table, int64_t vocab, int hidden, const
 // Attention of one new token fused with the o projection and the residual
 // add, for positions p < 64 (one chunk of cache slots), head_dim 64.
 //
-// Grid: ceil(N / (R * KV)) workgroups of KV wavefronts, N = hidden size.
+// Grid: ceil(N / (R * W)) workgroups of W wavefronts, N = hidden size, W =
+// KV, or 2 KV with HV (the cached form): wavefronts KV .. 2 KV - 1 then only
+// load the V rows of KV head w - KV into the V tile (a workgroup barrier
+// before O^T), so each CU's 64 KB of cache rows are requested by twice the
+// wavefronts (the per-CU request rate, not the bytes, bounds this staging).
 // Every workgroup recomputes the whole attention output (all H = KV * group
 // query heads over slots 0..p) from the caches, keeps it in LDS as the o
 // GEMV's activation row (unit-major: 16-byte unit q of 32-weight chunk c at
-// slot q C + c, natural order) and then runs the GEMV for its R * KV output
-// rows with the exact decode (unpack8 against permute8 of the unit), so no
-// staging pass or second barrier follows the attention; the o weights and
-// the rows' residual values are requested at launch, so they stream in
-// while the attention runs. Wavefront g handles KV head g and its `group`
-// query heads (group <= 16) on the matrix cores:
+// slot q C + c, natural order) and then runs the GEMV for its R * W output
+// rows (every wavefront, helpers included) with the exact decode (unpack8
+// against permute8 of the unit), so no staging pass follows the attention;
+// the o weights and the rows' residual values are requested at launch, so
+// they stream in while the attention runs. Wavefront g < KV handles KV head
+// g and its `group` query heads (group <= 16) on the matrix cores:
 //   S^T = K Q^T (v_mfma_f32_16x16x32_f16; A = cache rows, lane (q4, j) holds
 //     slot 16 mt + j, dims 32 s + 8 q4 .. +8; B = rotated q of head j), so
 //     lane (q4, j) receives head j's scores for slots 16 mt + 4 q4 + e;
@@ -439,13 +443,15 @@ embedding_kernel(const f16* __restrict__ table, int64_t vocab, int hidden, const
 constexpr int kAttnOSlots = 64;
 constexpr int kVStride = 72;   // V tile row stride in halves (144 bytes: conflict-free 16-byte stores)
 
-template <int KV, int R, int L, bool CACHED>
-__global__ void __launch_bounds__(64 * KV)
+template <int KV, int R, int L, bool CACHED, bool HV = false>
+__global__ void __launch_bounds__(64 * KV * (HV ? 2 : 1))
 attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
               const float* __restrict__ inv_freq, const int64_t* __restrict__ position,
               const uint8_t* __restrict__ w, const f16* __restrict__ scales, f16* resid, int group, int S,
               int N) {
+    static_assert(!HV || CACHED, "V helper wavefronts serve the cached form (slot p already in the caches)");
     constexpr int D = 64;
+    constexpr int NW = KV * (HV ? 2 : 1);   // wavefronts per workgroup
     const int64_t p64 = position[0];
     const float freq = CACHED ? 0.0f : inv_freq[threadIdx.x & 31];
     __builtin_amdgcn_sched_barrier(0);
@@ -460,34 +466,42 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int q4 = lane >> 4, j = lane & 15;
-    const int g = wave;
+    // HV: wavefronts KV .. 2 KV - 1 load the V rows of KV head wave - KV into
+    // the V tile while wavefronts 0 .. KV - 1 load K and q and attend
+    const bool helper = HV && wave >= KV;
+    const int g = HV ? (wave & (KV - 1)) : wave;
     const f16* kc = k_cache + (size_t)g * S * D;
     const f16* vc = v_cache + (size_t)g * S * D;
     const int hq = g * group + min(j, group - 1);
 
     // 1. every load that does not need the position
-    u32x4 ka[4][2];
+    u32x4 ka[4][2] = {};
+    if (!helper) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int row = min(16 * mt + j, S - 1);
+        for (int mt = 0; mt < 4; ++mt) {
+            const int row = min(16 * mt + j, S - 1);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) ka[mt][s] = *reinterpret_cast<const u32x4*>(kc + (size_t)row * D + 32 * s + 8 * q4);
+            for (int s = 0; s < 2; ++s)
+                ka[mt][s] = *reinterpret_cast<const u32x4*>(kc + (size_t)row * D + 32 * s + 8 * q4);
+        }
     }
-    u32x4 vr[8];
-    {
+    u32x4 vr[8] = {};
+    if (!HV || helper) {
         const int row = min(lane, S - 1);
 #pragma unroll
         for (int e = 0; e < 8; ++e) vr[e] = reinterpret_cast<const u32x4*>(vc + (size_t)row * D)[e];
     }
-    u32x4 qb[2], kn[2];
+    u32x4 qb[2] = {}, kn[2];
+    if (!helper) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        qb[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)hq * D + 32 * s + 8 * q4);
-        if (!CACHED) kn[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)(H + g) * D + 32 * s + 8 * q4);
+        for (int s = 0; s < 2; ++s) {
+            qb[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)hq * D + 32 * s + 8 * q4);
+            if (!CACHED) kn[s] = *reinterpret_cast<const u32x4*>(qkv + (size_t)(H + g) * D + 32 * s + 8 * q4);
+        }
     }
     const f16 vn = CACHED ? (f16)0.0f : qkv[(size_t)(H + KV + g) * D + lane];
     // o weights and scales of this wavefront's R rows (one-shot layout)
-    const int row0 = (blockIdx.x * KV + wave) * R;
+    const int row0 = (blockIdx.x * NW + wave) * R;
     const uint32_t row_bytes = (uint32_t)(K >> 1);
     uint32_t sv[R][L];
     u32x4 wv[R][L];
@@ -568,8 +582,8 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
 
     // 3. V tile into LDS, row-major: lane l stores slot l (zero past p), then
     // slot p from qkv
-    f16* vt = vt_all + wave * kAttnOSlots * kVStride;
-    {
+    f16* vt = vt_all + g * kAttnOSlots * kVStride;
+    if (!HV || helper) {
         const bool live = lane <= p;
         u32x4* row = reinterpret_cast<u32x4*>(vt + lane * kVStride);
 #pragma unroll
@@ -582,6 +596,9 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
 
     // 4. S^T = K Q^T, softmax over the head's 64 slots
     f32x4 st[4];
+    float sum = 0.0f;
+    u32x4 pb[2];   // P^T as the B operand of the two k-steps
+    if (!helper) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
         st[mt] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
@@ -600,8 +617,6 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
             mx = fmaxf(mx, st[mt][e]);
         }
     mx = row_pair_max(mx);
-    float sum = 0.0f;
-    u32x4 pb[2];   // P^T as the B operand of the two k-steps
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
         float pe[4];
@@ -616,9 +631,13 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
         pb[mt >> 1][2 * (mt & 1) + 1] = as_u32(b);
     }
     sum = row_pair_sum(sum);
-    wave_lds_sync();
+    }
+    // the V tile complete (HV: written by the helper wavefronts)
+    if constexpr (HV) __syncthreads();
+    else wave_lds_sync();
 
     // 5. O^T = V^T P^T; lane (q4, j) receives head j, dims 16 md + 4 q4 + e
+    if (!helper) {
     const float inv_sum = valid ? 1.0f / sum : __builtin_nanf("");
     const int tk = j >> 2, tm = j & 3;   // this lane's row / 4-dim block in the transposing read
 #pragma unroll
@@ -641,6 +660,7 @@ attn_o_kernel(const f16* __restrict__ qkv, f16* __restrict__ k_cache, f16* __res
             uint8_t* dst = reinterpret_cast<uint8_t*>(xs + ((k >> 3) & 3) * C + (k >> 5)) + (k & 7) * 2;
             *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(a), as_u32(b));
         }
+    }
     }
     __syncthreads();
 
@@ -1534,24 +1554,31 @@ int launch_attention_o(const void* qkv, void* k_cache, void* v_cache, const floa
     const int KV = (int)num_kv_heads, group = (int)(num_heads / num_kv_heads);
     const int K = (int)num_heads * 64;
     const int L = (K / 32 + 63) / 64;   // 1 KiB loads per o row: 1 or 2
-    constexpr int R = 2;                // o rows per wavefront
+    // the cached form: 2 KV wavefronts (V rows loaded by helper wavefronts),
+    // one o row each; the rotating form: KV wavefronts of 2 o rows. Graph
+    // timing, 1.1B model (KV = 4, positions 16..47): 4.92-4.94 us against
+    // 5.10 for the cached form on KV wavefronts of 2 rows (decode 2775 ->
+    // 2809 tok/s on one box)
+    constexpr int R = CACHED ? 1 : 2;   // o rows per wavefront
+    constexpr bool HV = CACHED;
     void (*kern)(const f16*, f16*, f16*, const float*, const int64_t*, const uint8_t*, const f16*, f16*, int, int,
                  int) = nullptr;
     switch (KV) {
-        case 1: kern = L == 1 ? attn_o_kernel<1, R, 1, CACHED> : attn_o_kernel<1, R, 2, CACHED>; break;
-        case 2: kern = L == 1 ? attn_o_kernel<2, R, 1, CACHED> : attn_o_kernel<2, R, 2, CACHED>; break;
-        case 4: kern = L == 1 ? attn_o_kernel<4, R, 1, CACHED> : attn_o_kernel<4, R, 2, CACHED>; break;
-        default: kern = L == 1 ? attn_o_kernel<8, R, 1, CACHED> : attn_o_kernel<8, R, 2, CACHED>; break;
+        case 1: kern = L == 1 ? attn_o_kernel<1, R, 1, CACHED, HV> : attn_o_kernel<1, R, 2, CACHED, HV>; break;
+        case 2: kern = L == 1 ? attn_o_kernel<2, R, 1, CACHED, HV> : attn_o_kernel<2, R, 2, CACHED, HV>; break;
+        case 4: kern = L == 1 ? attn_o_kernel<4, R, 1, CACHED, HV> : attn_o_kernel<4, R, 2, CACHED, HV>; break;
+        default: kern = L == 1 ? attn_o_kernel<8, R, 1, CACHED, HV> : attn_o_kernel<8, R, 2, CACHED, HV>; break;
     }
+    const int nw = HV ? 2 * KV : KV, rpw = R;
     const int lds = KV * kAttnOSlots * kVStride * 2 + K * 2 + KV * 64 * 4;
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         if (e != hipSuccess) return fail(W4A16_ERR_LAUNCH, "attention_o: LDS request refused");
     }
-    const int rows_per_block = R * KV;
+    const int rows_per_block = rpw * nw;
     const int blocks = (int)((hidden + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * KV), lds, static_cast<hipStream_t>(stream),
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64 * nw), lds, static_cast<hipStream_t>(stream),
                        static_cast<const f16*>(qkv), static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), inv_freq,
                        position, o_packed, static_cast<const f16*>(o_scales), static_cast<f16*>(residual), group,
                        (int)max_seq_len, (int)hidden);
