@@ -594,7 +594,11 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   per row): 28672 x 8192 8 slices of (1, 8, 2) 25.0 / 25.0 / 25.1 at M =
 //   5 / 6 / 8 against 29.6 / 29.7 / 30.2 (one block per wavefront: 27.2 /
 //   27.3 / 27.8); 8192 x 28672 2 slices of (1, 8, 3) 27.0 / 27.3 / 27.8
-//   against 28.4 / 28.6 / 29.1 on the streaming paired kernel.
+//   against 28.4 / 28.6 / 29.1 on the streaming paired kernel; 14336 x
+//   4096 8 slices of (1, 4, 2) with two blocks per wavefront 10.9-11.0 /
+//   10.6 at M = 8 / 6 against 11.5-12.3 / 11.2 on the paired kernel (its
+//   whole rows staged in chunks), reduce launch included (4 slices of (1,
+//   8, 2) 13.1-13.3, (2, 4, 3) 10.9-11.0, 8 slices of (1, 8, 2) 11.2-11.4).
 bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace = false) {
     if (M < 1 || M > 16 || K < 256 || K % 256 != 0 || N > INT32_MAX) return false;
     const int64_t P = K / 256;
@@ -647,6 +651,7 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
             else if (workspace && wide && P == 32 && N >= 16384) c[0] = {1, 8, 3, 2};
         } else if (P <= 56) {
             if (!wide && N >= 4096 && N <= 8192) c[0] = {4, 2, 6};
+            else if (workspace && wide && P == 56 && N >= 2048 && N <= 4096) c[0] = {1, 4, 2, 8};
         } else if (P == 112) {
             if (workspace && M >= 3 && !wide && N >= 4096 && N <= 8192) c[0] = {1, 8, 4, 4};
             else if (workspace && wide && N >= 4096 && N <= 8192) c[0] = {1, 8, 2, 8};

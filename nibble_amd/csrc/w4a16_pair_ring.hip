@@ -74,7 +74,8 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
 // wavefront: M = 9..16 on 5632 x 2048 (8 slices of 3 pairs), 14336 x 4096
 // (4 of 14) and 8192 x 8192 (2 of 16); M = 3..4 on 28672 x 8192 (4 of 28);
 // M = 5..8 with two blocks per wavefront (half the activation staging per
-// row) on 28672 x 8192 (8 of 14) and 8192 x 28672 (2 of 16).
+// row) on 28672 x 8192 (8 of 14), 8192 x 28672 (2 of 16) and, on 4
+// wavefronts, 14336 x 4096 (8 of 7).
 struct SplitPick {
     Kern kern;
     int rb;
@@ -89,6 +90,7 @@ SplitPick pick_split(int ms, int sk, int sn, int ppw, int depth) {
     W4A16_P(16, 1, 8, 1, 3, 3)
     W4A16_P(16, 1, 8, 1, 14, 4)
     W4A16_P(16, 1, 8, 1, 16, 4)
+    W4A16_P(8, 1, 4, 2, 7, 2)
 #undef W4A16_P
     return SplitPick{nullptr, 1};
 }
