@@ -234,8 +234,8 @@ int w4a16_plan_linear_ws(const void* activations, const uint8_t* packed_weights,
  *     9..16 (exact decode: the dequantized fp16 weights in the B operand)
  *     (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3)
  *     (1,8,14,4) (1,8,16,4); at M = 2..4 with K slices (1,8,28,4); at M =
- *     5..8 with K slices (1,8,14,2) (1,8,16,3), whose wavefronts each take
- *     two 8-row blocks (a workgroup covers 16 * rows rows).
+ *     5..8 with K slices (1,8,14,2) (1,8,16,3) (1,4,7,2), whose wavefronts
+ *     each take two 8-row blocks (a workgroup covers 16 * rows rows).
  *   W4A16_KERNEL_PAIR_STREAM (2 <= M <= 8, whole rows of activations in
  *     LDS): rows = wavefronts per workgroup (0 = the fewest that cover N / 8
  *     row blocks with the workgroups resident at once; else 1..16), unroll =

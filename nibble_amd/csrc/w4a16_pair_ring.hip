@@ -179,7 +179,7 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                     "M = 5..8 also (11,1,2,2); M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices "
                     "(1,8,3,3) (1,8,14,4) "
                     "(1,8,16,4); M = 2..4 with K slices (1,8,28,4); M = 5..8 with K slices and two 8-row blocks "
-                    "per wavefront (1,8,14,2) (1,8,16,3)");
+                    "per wavefront (1,8,14,2) (1,8,16,3) (1,4,7,2)");
     const int64_t lds = w4a16::pair_ring_lds_bytes(ms, sk, sn, pk.rb, ppw);
     if (lds > kMaxLdsBytes) return fail(W4A16_ERR_CONFIG, "paired ring kernel: staging exceeds LDS");
     const int64_t need = pair_ring_workspace_bytes(M, N, slices);
