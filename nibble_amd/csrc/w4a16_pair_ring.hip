@@ -204,11 +204,13 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
 // weight rows), RMSNorm when fz.norm_weight is set, K = 2048; kind 1: the
 // residual add, K = 5632; kind 2: RMSNorm, K = 2048 (wide layers). Shapes
 // from graph timing against the one-shot fused GEMVs (decode step of the
-// 1.1B model): gate|up 2048 x 2 x 5632 with RMSNorm (1, 3, 8 pairs, 4 in
-// flight, 2 blocks per wavefront) 4.13 against 4.85 us; down 5632 x 2048
-// with the residual (8 wavefronts on K, 3 pairs each) 3.31 against 3.45;
-// lm_head 2048 x 32000 with RMSNorm (1, 4, 8 pairs all in flight) 7.70
-// against 7.92-8.17 on (1, 8, 8) and 8.18 on the one-shot form (12 rotated
+// 1.1B model): gate|up 2048 x 2 x 5632 with RMSNorm (1, 3, 8 pairs, 6 in
+// flight, 2 blocks per wavefront) 4.39-4.41 us against 4.48-4.52 with 4 in
+// flight (3: 4.82-4.87, 5: 4.72-4.75, 8: 4.87) and 4.85 on the one-shot
+// form; down 5632 x 2048 with the residual (8 wavefronts on K, 3 pairs each)
+// 3.31 against 3.45; lm_head 2048 x 32000 with RMSNorm (1, 4, 8 pairs, 6 in
+// flight) 7.47-7.53 against 7.88-7.95 with all 8 in flight, 7.53-7.71 with
+// 4, 7.92-8.17 on (1, 8, 8) and 8.18 on the one-shot form (12 rotated
 // weight copies). Other shapes measured with 22-call graphs over 24 copies
 // (wavefronts on K, on blocks, pairs, in flight): gate|up (2, 3, 4, 4)
 // 4.80-4.86 and (4, 3, 2, 1) 5.22-5.26 against 4.46-4.52; down (4, 1, 6, 6)
@@ -220,14 +222,14 @@ int launch_pair_ring_fused(int kind, const w4a16::f16* x, const w4a16::RingFusio
     Kern kern = nullptr;
     int sk = 1, sn = 1, rb = 1, ppw = 1;
     if (kind == 0 && K == 2048) {
-        kern = fz.norm_weight ? gemv_pair_ring<1, 1, 3, 2, 8, 4, false, true, true>
-                              : gemv_pair_ring<1, 1, 3, 2, 8, 4, false, true, false>;
+        kern = fz.norm_weight ? gemv_pair_ring<1, 1, 3, 2, 8, 6, false, true, true>
+                              : gemv_pair_ring<1, 1, 3, 2, 8, 6, false, true, false>;
         sk = 1, sn = 3, rb = 2, ppw = 8;
     } else if (kind == 1 && K == 5632 && fz.norm_weight == nullptr) {
         kern = gemv_pair_ring<1, 8, 1, 1, 3, 3, false, false, false, true>;
         sk = 8, sn = 1, rb = 1, ppw = 3;
     } else if (kind == 2 && K == 2048 && fz.norm_weight != nullptr) {
-        kern = gemv_pair_ring<1, 1, 4, 1, 8, 8, false, false, true>;
+        kern = gemv_pair_ring<1, 1, 4, 1, 8, 6, false, false, true>;
         sk = 1, sn = 4, rb = 1, ppw = 8;
     }
     if (kern == nullptr) return fail(W4A16_ERR_CONFIG, "fused ring GEMV: shape not instantiated");
