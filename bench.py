@@ -78,10 +78,10 @@ TOKENS_PER_REPLAY = 16
 MEASURED_TRAFFIC_BYTES = 6141114
 TRAFFIC_SOURCE = "profiles/gemv_pair_ring_m1_mlp_traffic.md"
 # Mean kernel duration of the same two kernels in a rocprofv3 kernel trace of
-# `bench.py --headline-pass` (the headline sequence alone), per launch: the
-# profiler's timestamps run above the event-timed launches, so the line
-# reports both.
-TRACE_US_PER_LAUNCH = 3.481
+# `bench.py --headline-pass` (the headline sequence alone, outside its timed
+# steps), per launch; the line reports the trace's fraction beside the
+# event-timed one.
+TRACE_US_PER_LAUNCH = 3.064
 TRACE_SOURCE = "profiles/gemv_pair_ring_m1_mlp_kernel_trace.md"
 
 

@@ -562,6 +562,12 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   3.54 against 3.73; 5632 x 2048 (4, 1, 6) 3.27 against 3.46; 2048 x
 //   5632 (1, 3, 8) 3.19 against 3.25; 2048 x N < 4096 keeps the one-shot
 //   kernel (2048 x 2048 2.64 against 2.55, 2048 x 2560 2.86 against 2.71).
+//   Pairs in flight, swept later on each shape (64-call graphs, one box,
+//   three passes): 2048 x 5632 7 of 8 3.17-3.20 against 3.29-3.30 with all
+//   8; 2048 x 8192 6 of 8 3.95-3.98 against 4.11-4.14; 4096 x 4096 7 of 8
+//   3.57-3.58 against 3.64-3.67; 8192 x 8192 6 of 16 7.08-7.10 against
+//   7.15-7.22 with 4; 4096 x 14336 (6) and 14336 x 4096 (10) unchanged
+//   (the alternatives within noise).
 //   M = 8: 4096 x 14336 (1, 8, 6) 7.76 against 10.80; 8192 x 8192 (2, 4, 4)
 //   9.83 against 11.82; 4096 x 4096 (4, 2, 4) 4.59 against 5.19; 2048 x
 //   5632 (1, 4, 6) 3.71 against 4.35; 2048 x 2048 (4, 1, 2) 3.09 against
@@ -621,15 +627,16 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
     } else if (M == 1) {
         if (P <= 8) {
             if (N >= 16384) c[0] = {1, 8, 4};
-            else if (N >= 4096) c[0] = {1, 3, 8};
+            else if (N >= 8192) c[0] = {1, 3, 6};
+            else if (N >= 4096) c[0] = {1, 3, 7};
         } else if (P <= 16) {
-            if (N >= 8192) c[0] = {1, 8, 6}, c[1] = {2, 2, 8};
-            else if (N >= 4096) c[0] = {2, 2, 8};
+            if (N >= 8192) c[0] = {1, 8, 6}, c[1] = {2, 2, 7};
+            else if (N >= 4096) c[0] = {2, 2, 7};
         } else if (P <= 24) {
             if (N >= 2048) c[0] = {4, 1, 6};
         } else if (P <= 32) {
-            if (N >= 16384) c[0] = {1, 7, 6}, c[1] = {2, 4, 4};
-            else if (N >= 4096) c[0] = {2, 4, 4};
+            if (N >= 16384) c[0] = {1, 7, 6}, c[1] = {2, 4, 6};
+            else if (N >= 4096) c[0] = {2, 4, 6};
         } else if (P <= 56) {
             if (N >= 4096) c[0] = {2, 2, 10};
         } else if (P <= 112) {

@@ -36,12 +36,16 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
 #define W4A16_P(MS, SK, SN, PPW, D) \
     if (ms == MS && sk == SK && sn == SN && ppw == PPW && depth == D) return w4a16::gemv_pair_ring<MS, SK, SN, 1, PPW, D>;
     // M = 1
-    W4A16_P(1, 1, 3, 8, 8)    // K = 2048, N < 16384
+    W4A16_P(1, 1, 3, 8, 8)    // K = 2048 (tuned entry)
+    W4A16_P(1, 1, 3, 8, 7)    // K = 2048, N < 8192
+    W4A16_P(1, 1, 3, 8, 6)    // K = 2048, 8192 <= N < 16384
     W4A16_P(1, 1, 8, 8, 4)    // K = 2048, N >= 16384
-    W4A16_P(1, 2, 2, 8, 8)    // K = 4096, N < 8192
+    W4A16_P(1, 2, 2, 8, 8)    // K = 4096 (tuned entry)
+    W4A16_P(1, 2, 2, 8, 7)    // K = 4096, N < 8192
     W4A16_P(1, 1, 8, 16, 6)   // K = 4096, N >= 8192
     W4A16_P(1, 4, 1, 6, 6)    // K = 5376 .. 6144
-    W4A16_P(1, 2, 4, 16, 4)   // K = 8192, N < 16384
+    W4A16_P(1, 2, 4, 16, 4)   // K = 8192 (tuned entry)
+    W4A16_P(1, 2, 4, 16, 6)   // K = 8192, N < 16384
     W4A16_P(1, 1, 7, 32, 6)   // K = 8192, N >= 16384
     W4A16_P(1, 2, 2, 28, 10)  // K = 14080 .. 14336
     W4A16_P(1, 2, 4, 56, 6)   // K = 28416 .. 28672
@@ -173,7 +177,8 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
     if (kern == nullptr)
         return fail(W4A16_ERR_CONFIG,
                     "paired ring kernel: (splits, rows, pairs per wavefront, unroll) not instantiated for this M; "
-                    "M = 1: (1,3,8,8) (1,8,8,4) (2,2,8,8) (1,8,16,6) (4,1,6,6) (2,4,16,4) (1,7,32,6) "
+                    "M = 1: (1,3,8,8) (1,3,8,7) (1,3,8,6) (1,8,8,4) (2,2,8,8) (2,2,8,7) (1,8,16,6) (4,1,6,6) "
+                    "(2,4,16,4) (2,4,16,6) (1,7,32,6) "
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
                     "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); "
                     "M = 5..8 also (11,1,2,2); M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices "

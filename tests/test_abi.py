@@ -283,11 +283,12 @@ def test_gemm_lds_routing(monkeypatch, m, n, k, kernel, shape):
 
 
 @pytest.mark.parametrize("k,n,shape", [
-    (2048, 4096, (3, 1, 8)), (2048, 5632, (3, 1, 8)), (2048, 16383, (3, 1, 8)), (2048, 16384, (8, 1, 4)),
-    (2048, 32000, (8, 1, 4)), (4096, 4096, (2, 2, 8)), (4096, 8191, (2, 2, 8)), (4096, 8192, (8, 1, 6)),
-    (4096, 14336, (8, 1, 6)), (3840, 14336, (2, 2, 8)),   # 15 pairs: 8 per wavefront over 2 slices
-    (5632, 2048, (1, 4, 6)), (6144, 4096, (1, 4, 6)), (5376, 2048, (1, 4, 6)), (8192, 8192, (4, 2, 4)),
-    (8192, 4096, (4, 2, 4)), (8192, 28672, (7, 1, 6)), (7936, 8192, (4, 2, 4)), (14336, 4096, (2, 2, 10)),
+    (2048, 4096, (3, 1, 7)), (2048, 5632, (3, 1, 7)), (2048, 8191, (3, 1, 7)), (2048, 8192, (3, 1, 6)),
+    (2048, 16383, (3, 1, 6)), (2048, 16384, (8, 1, 4)),
+    (2048, 32000, (8, 1, 4)), (4096, 4096, (2, 2, 7)), (4096, 8191, (2, 2, 7)), (4096, 8192, (8, 1, 6)),
+    (4096, 14336, (8, 1, 6)), (3840, 14336, (2, 2, 7)),   # 15 pairs: 8 per wavefront over 2 slices
+    (5632, 2048, (1, 4, 6)), (6144, 4096, (1, 4, 6)), (5376, 2048, (1, 4, 6)), (8192, 8192, (4, 2, 6)),
+    (8192, 4096, (4, 2, 6)), (8192, 28672, (7, 1, 6)), (7936, 8192, (4, 2, 6)), (14336, 4096, (2, 2, 10)),
     (14080, 8192, (2, 2, 10)), (28672, 8192, (4, 2, 6)), (28416, 4096, (4, 2, 6)),
 ])
 def test_pair_ring_m1_plan_shapes(monkeypatch, k, n, shape):
@@ -592,7 +593,8 @@ def test_scalar_argument_errors():
 
 
 @pytest.mark.parametrize("m,n,k,splits", [
-    (8, 8192, 28672, 8), (8, 4096, 14336, 0), (4, 8192, 28672, 4), (3, 8192, 28672, 4),
+    (8, 8192, 28672, 8), (8, 4096, 14336, 8), (5, 2048, 14336, 8), (8, 8192, 14336, 0), (4, 8192, 28672, 4),
+    (3, 8192, 28672, 4),
     (3, 4096, 14336, 0), (5, 8192, 20480, None), (5, 4096, 20480, 0), (8, 8191, 28672, 8), (8, 8192, 16384, 0),
     (8, 2048, 5632, 0), (8, 28672, 8192, 2), (5, 16384, 8192, 2), (4, 28672, 8192, 0), (1, 8192, 28672, 0),
     (2, 8192, 28672, 0), (16, 8192, 28672, 0), (8, 4096, 4096, 0), (4, 4096, 8192, 0), (16, 2048, 5632, 8),
@@ -600,8 +602,9 @@ def test_scalar_argument_errors():
 def test_linear_workspace_bytes(m, n, k, splits):
     """Layers whose route keeps fp32 partial sums use slices * M * N * 4
     bytes of workspace: the paired ring kernel's K slices (M = 3..8 on rows
-    of 28672 with N = 4096..8192, M = 5..8 on rows of 8192 with N >= 16384,
-    M = 12..16 on 5632 x 2048, 14336 x 4096 and 8192 x 8192) and the split-K
+    of 28672 with N = 4096..8192, M = 5..8 on rows of 8192 with N >= 16384
+    and on rows of 14336 with N = 2048..4096, M = 12..16 on 5632 x 2048,
+    14336 x 4096 and 8192 x 8192) and the split-K
     streaming kernel (other M = 3..8 layers with K > 16384 and N >= 8192;
     None: any slice count); everything else none."""
     got = _lib.linear_workspace_bytes(m, n, k)

@@ -21,11 +21,15 @@ RING = _lib.KERNEL_PAIR_RING
 # pairs in flight, K values whose pairs per wavefront match the instantiation)
 SHAPES = [
     (1, 3, 8, (2048,)),
+    (1, 3, 7, (2048,)),
+    (1, 3, 6, (2048,)),
     (1, 8, 4, (2048,)),
     (2, 2, 8, (4096, 3840)),            # 3840: 15 pairs, the second slice one short
+    (2, 2, 7, (4096, 3840)),
     (1, 8, 6, (4096,)),
     (4, 1, 6, (6144, 5632, 5376)),      # 5632: 22 pairs over 4 slices of 6
     (2, 4, 4, (8192, 7936)),
+    (2, 4, 6, (8192, 7936)),
     (1, 7, 6, (8192,)),
     (2, 2, 10, (14336, 14080)),
     (2, 4, 6, (28672, 28416)),
