@@ -62,7 +62,8 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
     W4A16_P(8, 1, 4, 8, 6)    // K = 2048, N <= 8192
     W4A16_P(8, 4, 2, 4, 4)    // K = 4096, N < 8192
     W4A16_P(8, 1, 8, 16, 6)   // K = 4096, N >= 8192
-    W4A16_P(8, 2, 4, 16, 4)   // K = 8192, N <= 8192
+    W4A16_P(8, 2, 4, 16, 4)   // K = 8192 (tuned entry)
+    W4A16_P(8, 2, 4, 16, 5)   // K = 8192, N <= 8192
     W4A16_P(8, 11, 1, 2, 2)   // K = 5376 .. 5632, N <= 2048 (M = 6..8)
     // M = 9..16 (exact decode)
     W4A16_P(16, 8, 1, 1, 1)   // K = 2048, N <= 2048
@@ -180,7 +181,8 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                     "M = 1: (1,3,8,8) (1,3,8,7) (1,3,8,6) (1,8,8,4) (2,2,8,8) (2,2,8,7) (1,8,16,6) (4,1,6,6) "
                     "(2,4,16,4) (2,4,16,6) (1,7,32,6) "
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
-                    "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4); "
+                    "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4) "
+                    "(2,4,16,5); "
                     "M = 5..8 also (11,1,2,2); M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices "
                     "(1,8,3,3) (1,8,14,4) "
                     "(1,8,16,4); M = 2..4 with K slices (1,8,28,4); M = 5..8 with K slices and two 8-row blocks "

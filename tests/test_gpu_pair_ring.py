@@ -40,6 +40,7 @@ VARIANTS = [(sk, sn, d, k) for sk, sn, d, ks in SHAPES for k in ks]
 SHAPES4 = [(4, 1, 2, (2048, 1792)), (1, 4, 6, (2048,)), (2, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)),
            (8, 1, 3, (5632, 6144)), (2, 4, 4, (8192,)), (4, 2, 6, (14336, 14080))]
 SHAPES8 = [(4, 1, 2, (2048,)), (1, 4, 6, (2048,)), (4, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)), (2, 4, 4, (8192, 7936)),
+           (2, 4, 5, (8192, 7936)),
            (11, 1, 2, (5632, 5376))]   # 5376: 21 pairs, the last wavefront one short
 SMALL = ([(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES4 for k in ks for m in (2, 3, 4)] +
          [(m, sk, sn, d, k) for sk, sn, d, ks in SHAPES8 for k in ks for m in (5, 8)])
