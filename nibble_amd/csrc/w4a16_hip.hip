@@ -567,7 +567,8 @@ bool gemm_fits(int64_t M, int64_t N, int64_t K) {
 //   8; 2048 x 8192 6 of 8 3.95-3.98 against 4.11-4.14; 4096 x 4096 7 of 8
 //   3.57-3.58 against 3.64-3.67; 8192 x 8192 6 of 16 7.08-7.10 against
 //   7.15-7.22 with 4; 4096 x 14336 (6) and 14336 x 4096 (10) unchanged
-//   (the alternatives within noise).
+//   (the alternatives within noise), as the 70B class (8192 x 28672 and
+//   28672 x 8192: 5, 7 or 8 in flight against 6, no faster).
 //   M = 8: 4096 x 14336 (1, 8, 6) 7.76 against 10.80; 8192 x 8192 (2, 4, 4)
 //   9.83 against 11.82; 4096 x 4096 (4, 2, 4) 4.59 against 5.19; 2048 x
 //   5632 (1, 4, 6) 3.71 against 4.35; 2048 x 2048 (4, 1, 2) 3.09 against
