@@ -230,7 +230,8 @@ int w4a16_plan_linear_ws(const void* activations, const uint8_t* packed_weights,
  *     M = 1 one of (1,3,8,8) (1,3,8,7) (1,3,8,6) (1,8,8,4) (2,2,8,8)
  *     (2,2,8,7) (1,8,16,6) (4,1,6,6) (2,4,16,4) (2,4,16,6) (1,7,32,6)
  *     (2,2,28,10) (2,4,56,6); at M = 2..4 (4,1,2,2)
- *     (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) (2,4,16,4) (4,2,14,6); at
+ *     (1,4,8,6) (1,4,8,7) (2,2,8,4) (2,2,8,6) (1,8,16,6) (8,1,3,3) (2,4,16,4)
+ *     (4,2,14,6); at
  *     M = 5..8 (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4) (2,4,16,5) (11,1,2,2); at M =
  *     9..16 (exact decode: the dequantized fp16 weights in the B operand)
  *     (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices (1,8,3,3)

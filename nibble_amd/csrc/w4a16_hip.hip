@@ -645,12 +645,17 @@ bool plan_pair_ring(int64_t M, int64_t N, int64_t K, Plan* out, bool workspace =
         }
     } else {
         const bool wide = M > 4;
+        // pairs in flight at M = 2..4 (graph timing, M = 2 / 4): 2048 x 5632
+        // 7 of 8 3.46-3.50 / 3.55-3.56 against 3.49-3.53 / 3.58-3.61 us
+        // with 6; 4096 x 4096 6 of 8 4.10-4.17 / 4.31-4.35 against 4.30-4.37
+        // / 4.42-4.48 with 4 (M = 5..8 keep 6 and 4: 7 and 3 measured no
+        // faster there)
         if (P <= 8) {
             if (N >= 1024 && N <= 2048) c[0] = {4, 1, 2};
-            else if (N > 2048 && N <= 8192) c[0] = {1, 4, 6};
+            else if (N > 2048 && N <= 8192) c[0] = wide ? Shape{1, 4, 6} : Shape{1, 4, 7};
         } else if (P <= 16) {
             if (N >= 8192) c[0] = {1, 8, 6};
-            else if (N >= 4096) c[0] = wide ? Shape{4, 2, 4} : Shape{2, 2, 4};
+            else if (N >= 4096) c[0] = wide ? Shape{4, 2, 4} : Shape{2, 2, 6};
         } else if (P <= 24) {
             if (M >= 3 && M <= 4 && N >= 2048 && N <= 4096) c[0] = {8, 1, 3};
             else if (M >= 6 && N >= 1024 && N <= 2048) c[0] = {11, 1, 2};

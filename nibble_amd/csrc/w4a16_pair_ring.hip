@@ -51,8 +51,10 @@ Kern pick(int ms, int sk, int sn, int ppw, int depth) {
     W4A16_P(1, 2, 4, 56, 6)   // K = 28416 .. 28672
     // M = 2..4
     W4A16_P(4, 4, 1, 2, 2)    // K = 2048, N <= 2048
-    W4A16_P(4, 1, 4, 8, 6)    // K = 2048, N <= 8192
-    W4A16_P(4, 2, 2, 8, 4)    // K = 4096, N < 8192
+    W4A16_P(4, 1, 4, 8, 6)    // K = 2048 (tuned entry)
+    W4A16_P(4, 1, 4, 8, 7)    // K = 2048, N <= 8192
+    W4A16_P(4, 2, 2, 8, 4)    // K = 4096 (tuned entry)
+    W4A16_P(4, 2, 2, 8, 6)    // K = 4096, N < 8192
     W4A16_P(4, 1, 8, 16, 6)   // K = 4096, N >= 8192
     W4A16_P(4, 8, 1, 3, 3)    // K = 5376 .. 6144 (M = 3, 4)
     W4A16_P(4, 2, 4, 16, 4)   // K = 8192, N <= 8192
@@ -181,7 +183,7 @@ int launch_pair_ring(int sk, int sn, int depth, int slices, int M, const w4a16::
                     "M = 1: (1,3,8,8) (1,3,8,7) (1,3,8,6) (1,8,8,4) (2,2,8,8) (2,2,8,7) (1,8,16,6) (4,1,6,6) "
                     "(2,4,16,4) (2,4,16,6) (1,7,32,6) "
                     "(2,2,28,10) (2,4,56,6); M = 2..4: (4,1,2,2) (1,4,8,6) (2,2,8,4) (1,8,16,6) (8,1,3,3) "
-                    "(2,4,16,4) (4,2,14,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4) "
+                    "(2,4,16,4) (4,2,14,6) (1,4,8,7) (2,2,8,6); M = 5..8: (4,1,2,2) (1,4,8,6) (4,2,4,4) (1,8,16,6) (2,4,16,4) "
                     "(2,4,16,5); "
                     "M = 5..8 also (11,1,2,2); M = 9..16: (8,1,1,1) (4,2,2,2) (2,4,4,4) (1,4,8,4), and with K slices "
                     "(1,8,3,3) (1,8,14,4) "

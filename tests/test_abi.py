@@ -302,8 +302,8 @@ def test_pair_ring_m1_plan_shapes(monkeypatch, k, n, shape):
 
 
 @pytest.mark.parametrize("m,k,n,shape", [
-    (2, 2048, 2048, (1, 4, 2)), (8, 2048, 1024, (1, 4, 2)), (4, 2048, 5632, (4, 1, 6)), (8, 2048, 8192, (4, 1, 6)),
-    (2, 4096, 4096, (2, 2, 4)), (8, 4096, 4096, (2, 4, 4)), (5, 4096, 6000, (2, 4, 4)), (3, 4096, 14336, (8, 1, 6)),
+    (2, 2048, 2048, (1, 4, 2)), (8, 2048, 1024, (1, 4, 2)), (4, 2048, 5632, (4, 1, 7)), (8, 2048, 8192, (4, 1, 6)),
+    (5, 2048, 5632, (4, 1, 6)), (2, 4096, 4096, (2, 2, 6)), (8, 4096, 4096, (2, 4, 4)), (5, 4096, 6000, (2, 4, 4)), (3, 4096, 14336, (8, 1, 6)),
     (8, 4096, 28672, (8, 1, 6)), (3, 5632, 2048, (1, 8, 3)), (4, 6144, 4096, (1, 8, 3)), (2, 8192, 8192, (4, 2, 4)),
     (8, 8192, 6144, (4, 2, 5)), (5, 8192, 8192, (4, 2, 5)), (4, 8192, 8192, (4, 2, 4)), (2, 14336, 4096, (2, 4, 6)),
     (4, 14336, 8192, (2, 4, 6)),

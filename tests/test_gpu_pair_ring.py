@@ -37,7 +37,8 @@ SHAPES = [
 VARIANTS = [(sk, sn, d, k) for sk, sn, d, ks in SHAPES for k in ks]
 
 # M = 2..4 (4 row slots) and M = 5..8 (8 row slots)
-SHAPES4 = [(4, 1, 2, (2048, 1792)), (1, 4, 6, (2048,)), (2, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)),
+SHAPES4 = [(4, 1, 2, (2048, 1792)), (1, 4, 6, (2048,)), (1, 4, 7, (2048,)), (2, 2, 4, (4096, 3840)),
+           (2, 2, 6, (4096, 3840)), (1, 8, 6, (4096,)),
            (8, 1, 3, (5632, 6144)), (2, 4, 4, (8192,)), (4, 2, 6, (14336, 14080))]
 SHAPES8 = [(4, 1, 2, (2048,)), (1, 4, 6, (2048,)), (4, 2, 4, (4096, 3840)), (1, 8, 6, (4096,)), (2, 4, 4, (8192, 7936)),
            (2, 4, 5, (8192, 7936)),
